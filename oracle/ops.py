@@ -1,0 +1,320 @@
+"""CPU restatement of the reference's per-operator arithmetic (test infrastructure only).
+
+Every function cites the reference lines it follows. Floating-point work is eager torch on the CPU
+in fp32 with the reference's casts: each product and sum is its own rounded op (no FMA), which is
+also what the gfx950 kernels do, so the only differences left are reduction orders.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import torch
+
+# NF4 levels in code order, as in solution/kernels.py:76-83 (the QLoRA NF4 table, README.md:53).
+NF4_LEVELS = np.array(
+    [
+        -1.0, -0.6961928009986877, -0.5250730514526367, -0.39491748809814453,
+        -0.28444138169288635, -0.18477343022823334, -0.09105003625154495, 0.0,
+        0.07958029955625534, 0.16093020141124725, 0.24611230194568634, 0.33791524171829224,
+        0.44070982933044434, 0.5626170039176941, 0.7229568362236023, 1.0,
+    ],
+    dtype=np.float32,
+)
+
+PRESCALE_GRAD = 65536.0  # solution/ops.py:171
+
+
+def _up(x: torch.Tensor) -> torch.Tensor:
+    """fp32 compute type (float64 inputs stay float64, for the float64 invariant checks)."""
+    return x if x.dtype == torch.float64 else x.float()
+
+
+# ---------------------------------------------------------------------------------------------
+# NF4 double-quant dequant — solution/kernels.py:27-118 and launcher kernels.py:572-619
+# ---------------------------------------------------------------------------------------------
+
+
+def nf4_dequant(
+    packed: np.ndarray,
+    absmax: np.ndarray,
+    code2: np.ndarray,
+    absmax2: np.ndarray,
+    offset,
+    out_shape: tuple[int, int],
+    split_bytes: tuple[int, int] | None = None,
+    blocksize: int = 64,
+    super_blocksize: int = 256,
+    absmax2_bases: tuple[int, int] | None = None,
+) -> np.ndarray:
+    """fp16 weights from packed NF4 codes.
+
+    byte b holds elements 2b (high nibble, kernels.py:66-68) and 2b+1 (low nibble); segment s of
+    byte b is (b >= split1) + (b >= split2) (kernels.py:59-63); scale = fp32(fp32(code2[absmax[blk]]
+    * absmax2[sup]) + off_s) with two roundings (kernels.py:64 without contraction, as
+    bitsandbytes' dequantize_blockwise followed by ``absmax += offset``); value =
+    fp16_rne(fp32(NF4[nib] * scale)) (kernels.py:90, 115). sup is the super-block index relative
+    to the segment's first block plus the segment's absmax2 base; with the default bases this is
+    the reference's global ``block // super_blocksize`` (kernels.py:53-57) whenever each segment
+    holds a multiple of super_blocksize blocks.
+
+    Pinned by: hand-computed known answers, a float64 brute force, segment-vs-separate equality
+    and the quantise->dequantise error bound (tests/test_oracle.py).
+    """
+    packed = np.asarray(packed, dtype=np.uint8).reshape(-1)
+    absmax = np.asarray(absmax, dtype=np.uint8).reshape(-1)
+    code2 = np.asarray(code2, dtype=np.float32).reshape(-1)
+    absmax2 = np.asarray(absmax2, dtype=np.float32).reshape(-1)
+    n = int(out_shape[0]) * int(out_shape[1])
+    nb = n // 2
+    hb = blocksize // 2
+    if isinstance(offset, (tuple, list)):
+        offs = np.array([offset[0], offset[1], offset[2]], dtype=np.float32)
+    else:
+        offs = np.full(3, offset, dtype=np.float32)
+    s1, s2 = (nb, nb) if split_bytes is None else (int(split_bytes[0]), int(split_bytes[1]))
+    if absmax2_bases is None:
+        n0 = -(-(s1 // hb) // super_blocksize) if s1 > 0 else 0
+        n1 = -(-((s2 - s1) // hb) // super_blocksize) if s2 > s1 else 0
+        absmax2_bases = (n0, n0 + n1)
+    bases = np.array([0, absmax2_bases[0], absmax2_bases[1]], dtype=np.int64)
+    first_blk = np.array([0, s1 // hb, s2 // hb], dtype=np.int64)
+
+    b = np.arange(nb, dtype=np.int64)
+    seg = (b >= s1).astype(np.int64) + (b >= s2).astype(np.int64)
+    blk = b // hb
+    sup = bases[seg] + (blk - first_blk[seg]) // super_blocksize
+    scale = code2[absmax[blk]] * absmax2[sup]  # float32 * float32 -> float32
+    scale = (scale + offs[seg]).astype(np.float32)
+    byte = packed[:nb]
+    out = np.empty(n, dtype=np.float32)
+    out[0::2] = NF4_LEVELS[byte >> 4] * scale
+    out[1::2] = NF4_LEVELS[byte & 15] * scale
+    return out.astype(np.float16).reshape(out_shape)
+
+
+# ---------------------------------------------------------------------------------------------
+# Residual + RMSNorm — solution/kernels.py:125-199, wrapper ops.py:30-54
+# ---------------------------------------------------------------------------------------------
+
+
+def rms_norm_fwd(x: torch.Tensor, w: torch.Tensor, eps: float = 1e-6, residual: torch.Tensor | None = None):
+    """(y, h, rstd): h = T(x + res) (kernels.py:149), rstd = 1/sqrt(mean(h^2) + eps) in fp32
+    (kernels.py:154-156), y = T(fp32(T(h*rstd)) * fp32(w)) (kernels.py:161-162; Qwen2RMSNorm's
+    cast order). Pinned against transformers' Qwen2RMSNorm."""
+    dt = x.dtype
+    h = (_up(x) + _up(residual)).to(dt) if residual is not None else x
+    hf = _up(h)
+    var = (hf * hf).sum(-1, keepdim=True) / hf.shape[-1]
+    rstd = 1.0 / torch.sqrt(var + eps)
+    y = ((hf * rstd).to(dt).to(hf.dtype) * _up(w)).to(dt)
+    return y, h, rstd.squeeze(-1)
+
+
+def rms_norm_bwd(dy: torch.Tensor, h: torch.Tensor, w: torch.Tensor, rstd: torch.Tensor,
+                 dresidual: torch.Tensor | None = None) -> torch.Tensor:
+    """dx = T((w*dy - xhat*mean(xhat*w*dy)) * rstd + dres), xhat = h*rstd (kernels.py:190-197).
+    Pinned against torch autograd of the forward formula in float64."""
+    xh = _up(h) * _up(rstd).unsqueeze(-1)
+    g = _up(w) * _up(dy)
+    c = (xh * g).sum(-1, keepdim=True) / h.shape[-1]
+    dx = (g - xh * c) * _up(rstd).unsqueeze(-1)
+    if dresidual is not None:
+        dx = dx + _up(dresidual)
+    return dx.to(h.dtype)
+
+
+# ---------------------------------------------------------------------------------------------
+# LoRA delta + NeoX RoPE — solution/kernels.py:206-348, wrapper ops.py:88-164
+# ---------------------------------------------------------------------------------------------
+
+
+def rope_tables(max_pos: int, head_dim: int, theta: float, dtype=torch.float16):
+    """cos/sin [max_pos, head_dim] as Qwen2RotaryEmbedding builds them (default rope type): inv
+    = 1/theta^(2i/d) in fp32, freqs = pos*inv, emb = [freqs, freqs], cast to ``dtype``
+    (the engine takes its cache from the model's rotary module, ops.py:655-666). Pinned against
+    transformers' Qwen2RotaryEmbedding."""
+    inv = 1.0 / (theta ** (torch.arange(0, head_dim, 2, dtype=torch.int64).float() / head_dim))
+    pos = torch.arange(max_pos, dtype=torch.float32)
+    freqs = pos[:, None] * inv[None, :]
+    emb = torch.cat([freqs, freqs], dim=-1)
+    return emb.cos().to(dtype), emb.sin().to(dtype)
+
+
+def _rot(x: torch.Tensor, c: torch.Tensor, s: torch.Tensor) -> torch.Tensor:
+    half = x.shape[-1] // 2
+    lo, hi = x[..., :half], x[..., half:]
+    out_lo = lo * c[..., :half] - hi * s[..., :half]
+    out_hi = hi * c[..., half:] + lo * s[..., half:]
+    return torch.cat([out_lo, out_hi], dim=-1)
+
+
+def _rot_t(dy: torch.Tensor, c: torch.Tensor, s: torch.Tensor) -> torch.Tensor:
+    half = dy.shape[-1] // 2
+    lo, hi = dy[..., :half], dy[..., half:]
+    dx_lo = lo * c[..., :half] + hi * s[..., half:]
+    dx_hi = hi * c[..., half:] - lo * s[..., :half]
+    return torch.cat([dx_lo, dx_hi], dim=-1)
+
+
+def qkv_rope_fwd(qkv, cos, sin, pos_ids, q_lora=None, v_lora=None, scale_q=2.0, scale_v=2.0,
+                 h_q=12, h_kv=2, head_dim=128):
+    """(q, k, v) [n, h, d]: q = T(R(p)(q + s_q*ql)), k = T(R(p)k), v = T(v + s_v*vl), fp32 math,
+    out_lo = a*cos_lo - b*sin_lo, out_hi = b*cos_hi + a*sin_hi (kernels.py:242-283). Pinned against
+    transformers' apply_rotary_pos_emb and the reference test formula (test_kernels.py:111-124)."""
+    dt = qkv.dtype
+    n = qkv.shape[0]
+    qd, kd = h_q * head_dim, h_kv * head_dim
+    q = _up(qkv[:, :qd])
+    k = _up(qkv[:, qd:qd + kd])
+    v = _up(qkv[:, qd + kd:qd + 2 * kd])
+    if q_lora is not None and v_lora is not None:
+        q = q + _up(q_lora) * scale_q
+        v = v + _up(v_lora) * scale_v
+    c = _up(cos[pos_ids]).unsqueeze(1)
+    s = _up(sin[pos_ids]).unsqueeze(1)
+    qo = _rot(q.view(n, h_q, head_dim), c, s).to(dt)
+    ko = _rot(k.view(n, h_kv, head_dim), c, s).to(dt)
+    return qo, ko, v.view(n, h_kv, head_dim).to(dt)
+
+
+def qkv_rope_bwd(dq, dk, dv, cos, sin, pos_ids, h_q=12, h_kv=2, head_dim=128,
+                 scale_q: float | None = None, scale_v: float | None = None):
+    """dqkv [n, (h_q+2h_kv)*d] = [R^T dQ | R^T dK | dV] (kernels.py:315-348); with scales also
+    (dq_lora, dv_lora) = T(fp32(dQ_T)*s) from the rounded values (ops.py:144-147). Pinned by
+    R^T R = I and against autograd of the forward."""
+    dt = dq.dtype
+    n = dq.shape[0]
+    c = _up(cos[pos_ids]).unsqueeze(1)
+    s = _up(sin[pos_ids]).unsqueeze(1)
+    gq = _rot_t(_up(dq).view(n, h_q, head_dim), c, s).to(dt).view(n, -1)
+    gk = _rot_t(_up(dk).view(n, h_kv, head_dim), c, s).to(dt).view(n, -1)
+    gv = dv.reshape(n, -1).to(dt)
+    dqkv = torch.cat([gq, gk, gv], dim=1)
+    if scale_q is None:
+        return dqkv
+    return dqkv, (_up(gq) * scale_q).to(dt), (_up(gv) * scale_v).to(dt)
+
+
+# ---------------------------------------------------------------------------------------------
+# SwiGLU — solution/kernels.py:355-446, wrapper ops.py:57-85
+# ---------------------------------------------------------------------------------------------
+
+
+def swiglu_fwd(g: torch.Tensor, u: torch.Tensor) -> torch.Tensor:
+    """T(g*sigmoid(g)*u), sigmoid = 1/(1+exp(-g)) in fp32 (kernels.py:388-391). Pinned against
+    F.silu."""
+    gf = _up(g)
+    sg = 1.0 / (1.0 + torch.exp(-gf))
+    return ((gf * sg) * _up(u)).to(g.dtype)
+
+
+def swiglu_bwd(dout: torch.Tensor, g: torch.Tensor, u: torch.Tensor):
+    """(dg, du): du = T(dout*silu), dg = T((dout*u)*(s + silu*(1-s))) (kernels.py:435-439).
+    Pinned against autograd of F.silu(g)*u."""
+    gf, uf, df = _up(g), _up(u), _up(dout)
+    sg = 1.0 / (1.0 + torch.exp(-gf))
+    silu = gf * sg
+    du = df * silu
+    dg = (df * uf) * (sg + silu * (1.0 - sg))
+    return dg.to(g.dtype), du.to(g.dtype)
+
+
+# ---------------------------------------------------------------------------------------------
+# Chunked lm_head cross-entropy — solution/kernels.py:453-565, ops.py:174-349
+# ---------------------------------------------------------------------------------------------
+
+
+def lm_head_logits(h16: torch.Tensor, w16: torch.Tensor) -> torch.Tensor:
+    """z16 = fp16(H·W^T) with fp32 accumulation (the fp16 torch.mm of ops.py:231), as fp32."""
+    return (h16.float() @ w16.float().t()).to(torch.float16).float()
+
+
+def lm_head_ce(h16: torch.Tensor, w16: torch.Tensor, labels: torch.Tensor,
+               num_items_in_batch: float | None = None, v_chunk: int = 8192,
+               need_grad: bool = True, grad_loss: float = 1.0) -> dict:
+    """Per-token statistics and the hidden-state gradient of the vocab-chunked lm_head CE.
+
+    Over fp16-rounded logits z: m = max z, s = sum e^{z-m}, w = sum e^{z-m} z; lse = m + ln s,
+    entropy = lse - w/s, nll = lse - z[y] (0 for y = -100), argmax = first index of max
+    (kernels.py:480-565); loss = sum(nll)/denom with denom = num_items_in_batch or #valid, >= 1
+    (ops.py:268-277). Gradient: G = fp16((e^{z-lse} - 1[v=y]) * 2^16/denom), 0 on masked rows
+    (kernels.py:517-531); dH = fp16((sum_v G W) * grad_loss/2^16) with the sum accumulated in fp32
+    (the reference accumulates in fp16 across chunks, ops.py:283, 320, 337-338).
+    Pinned against F.cross_entropy / logsumexp / softmax entropy / argmax and autograd on the
+    full logits.
+    """
+    n, d = h16.shape
+    V = w16.shape[0]
+    labels = labels.reshape(-1).long()
+    hf = h16.float()
+    m = torch.full((n,), -float("inf"))
+    s = torch.zeros(n)
+    wsum = torch.zeros(n)
+    best = torch.full((n,), -float("inf"))
+    best_idx = torch.zeros(n, dtype=torch.long)
+    target = torch.zeros(n)
+    for start in range(0, V, v_chunk):
+        end = min(start + v_chunk, V)
+        z = (hf @ w16[start:end].float().t()).to(torch.float16).float()
+        cmax, carg = z.max(dim=1)
+        upd = cmax > best
+        best_idx = torch.where(upd, carg + start, best_idx)
+        best = torch.where(upd, cmax, best)
+        m_new = torch.maximum(m, cmax)
+        alpha = torch.exp(m - m_new)
+        e = torch.exp(z - m_new[:, None])
+        s = s * alpha + e.sum(1)
+        wsum = wsum * alpha + (e * z).sum(1)
+        m = m_new
+        inr = (labels >= start) & (labels < end)
+        if inr.any():
+            idx = torch.nonzero(inr).squeeze(1)
+            target[idx] = z[idx, labels[idx] - start]
+    lse = m + torch.log(s)
+    entropy = lse - wsum / s
+    valid = labels != -100
+    nll = torch.where(valid, lse - target, torch.zeros_like(lse))
+    denom = float(num_items_in_batch) if num_items_in_batch is not None else float(valid.sum())
+    denom = max(denom, 1.0)
+    out = {"loss": nll.sum() / denom, "nll": nll, "lse": lse, "entropy": entropy,
+           "argmax": best_idx, "denom": denom}
+    if need_grad:
+        scale = torch.where(valid, torch.full((n,), PRESCALE_GRAD / denom), torch.zeros(n))
+        dh = torch.zeros(n, d)
+        for start in range(0, V, v_chunk):
+            end = min(start + v_chunk, V)
+            wf = w16[start:end].float()
+            z = (hf @ wf.t()).to(torch.float16).float()
+            p = torch.exp(z - lse[:, None])
+            onehot = torch.zeros_like(p)
+            inr = (labels >= start) & (labels < end)
+            if inr.any():
+                idx = torch.nonzero(inr).squeeze(1)
+                onehot[idx, labels[idx] - start] = 1.0
+            g16 = ((p - onehot) * scale[:, None]).to(torch.float16).float()
+            dh += g16 @ wf
+        out["dh"] = (dh * (grad_loss / PRESCALE_GRAD)).to(torch.float16)
+    return out
+
+
+def softmax_stats_reference(z: torch.Tensor, labels: torch.Tensor) -> dict:
+    """Library-routine statistics of full fp32 logits (the pin for ``lm_head_ce``)."""
+    labels = labels.reshape(-1).long()
+    lse = torch.logsumexp(z, dim=-1)
+    p = torch.softmax(z, dim=-1)
+    ent = lse - (p * z).sum(-1)
+    nll = torch.nn.functional.cross_entropy(z, labels.clamp(min=0), reduction="none")
+    nll = torch.where(labels != -100, nll, torch.zeros_like(nll))
+    return {"lse": lse, "entropy": ent, "nll": nll, "argmax": z.argmax(-1)}
+
+
+def fp16_ulp(x: torch.Tensor) -> torch.Tensor:
+    """Spacing of fp16 numbers at |x| (subnormal spacing below 2^-14)."""
+    a = x.abs().float().clamp(min=2.0**-14)
+    e = torch.floor(torch.log2(a))
+    return torch.pow(2.0, e - 10)
+
+
+__all__ = [name for name in dir() if not name.startswith("_") and name not in ("math", "np", "torch")]

@@ -1,0 +1,80 @@
+"""Loader for the gfx950 kernel library (``librus_amd.so``) and its C ABI (``include/rus_amd.h``).
+
+The library must be built (``python -m rus_amd.build``) before any kernel is called; there is no
+CPU or Python fallback, so a missing library or a non-HIP tensor raises immediately.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "librus_amd.so"
+ABI_VERSION = 1
+
+DTYPE_F16 = 0
+DTYPE_F32 = 1
+
+_vp = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_i32 = ctypes.c_int32
+_f32 = ctypes.c_float
+
+# name -> argtypes, in the order of include/rus_amd.h. Every entry point returns int.
+SIGNATURES: dict[str, list] = {
+    "rus_nf4_dequant": [_vp, _vp, _vp, _vp, _f32, _f32, _f32, _i64, _i64, _i64, _i64, _i64, _i64,
+                        _i64, _i32, _i32, _vp, _vp],
+    "rus_rmsnorm_fwd": [_vp, _vp, _vp, _i32, _vp, _vp, _vp, _i64, _i64, _i64, _f32, _i32, _vp],
+    "rus_rmsnorm_bwd": [_vp, _vp, _vp, _i32, _vp, _vp, _vp, _i64, _i64, _i64, _i32, _vp],
+    "rus_qkv_lora_rope_fwd": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64,
+                              _i64, _i64, _f32, _f32, _i32, _i32, _i32, _vp, _i32, _vp],
+    "rus_qkv_rope_bwd": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _f32,
+                         _f32, _i32, _i32, _i32, _vp, _i32, _vp],
+    "rus_swiglu_fwd": [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i32, _vp],
+    "rus_swiglu_bwd": [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i32,
+                       _vp],
+}
+
+_lock = threading.Lock()
+_lib: ctypes.CDLL | None = None
+
+
+def load() -> ctypes.CDLL:
+    """Returns the loaded library, loading it on first use (after torch, to share its HIP runtime)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        import torch  # noqa: F401  (torch's libamdhip64.so.7 must be the one this library binds)
+
+        if not LIB_PATH.exists():
+            raise RuntimeError(
+                f"rus_amd: {LIB_PATH.name} is not built; run `python -m rus_amd.build` "
+                "(there is no fallback path)"
+            )
+        lib = ctypes.CDLL(str(LIB_PATH))
+        lib.rus_last_error.restype = ctypes.c_char_p
+        lib.rus_last_error.argtypes = []
+        lib.rus_abi_version.restype = ctypes.c_int
+        lib.rus_abi_version.argtypes = []
+        for name, argtypes in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = ctypes.c_int
+            fn.argtypes = argtypes
+        got = lib.rus_abi_version()
+        if got != ABI_VERSION:
+            raise RuntimeError(f"rus_amd: library ABI {got} != expected {ABI_VERSION}; rebuild it")
+        _lib = lib
+    return _lib
+
+
+def call(name: str, *args) -> None:
+    """Calls one C entry point and raises RuntimeError with the library's message on failure."""
+    lib = load()
+    rc = getattr(lib, name)(*args)
+    if rc != 0:
+        msg = lib.rus_last_error().decode(errors="replace")
+        raise RuntimeError(f"{name} failed (code {rc}): {msg}")

@@ -1,0 +1,252 @@
+// NF4 double-quant dequantisation for gfx950.
+//
+// Behaviour follows solution/kernels.py:27-118 (nf4_dequant_turing_kernel) and the launcher
+// solution/kernels.py:572-619: one packed byte holds two NF4 codes (high nibble = even element),
+// the per-block scale is code2[absmax[blk]] * absmax2[super] + segment offset, and the output is
+// fp16 stored as fp16x2 words. Layout and design (CDNA4, wave64):
+//   * one thread decodes one 4-byte unit of packed codes = 8 fp16 = one 16-byte store, so a wave
+//     reads 256 contiguous bytes and writes 1 KiB contiguous per access (coalesced 128-bit stores);
+//     UNROLL units per thread are loaded before any is decoded to keep several loads in flight;
+//   * the NF4 codebook (16 floats) and the 256-entry code2 table live in LDS: the codebook index
+//     differs per lane, and a 16-entry table hits 16 distinct banks (broadcast, conflict free),
+//     which costs ~1 LDS read per element instead of a 15-select mux tree per element;
+//   * the file is built with -ffp-contract=off so scale = (code2*absmax2) + off keeps two
+//     roundings, matching an eager mul-then-add (bitsandbytes dequantize_blockwise + offset);
+//   * the super-block (absmax2) index is taken relative to each segment's first block, so fused
+//     segments whose block counts are not multiples of super_blocksize stay correct.
+#include "common.h"
+
+namespace rus {
+namespace {
+
+// NF4 code points in nibble order (QLoRA normal-float-4 table; solution/kernels.py:76-83).
+__constant__ float kNF4[16] = {
+    -1.0f,
+    -0.6961928009986877f,
+    -0.5250730514526367f,
+    -0.39491748809814453f,
+    -0.28444138169288635f,
+    -0.18477343022823334f,
+    -0.09105003625154495f,
+    0.0f,
+    0.07958029955625534f,
+    0.16093020141124725f,
+    0.24611230194568634f,
+    0.33791524171829224f,
+    0.44070982933044434f,
+    0.5626170039176941f,
+    0.7229568362236023f,
+    1.0f,
+};
+
+constexpr int kThreads = 256;
+
+struct Nf4Args {
+  const uint32_t* packed;  // packed codes viewed as 32-bit units
+  const uint8_t* packed_bytes;
+  const uint8_t* absmax;
+  const float* code2;
+  const float* absmax2;
+  uint32_t* out;  // one fp16x2 word per packed byte
+  float off0, off1, off2;
+  uint32_t split1, split2;  // first byte of segment 1 / 2
+  uint32_t blk0_1, blk0_2;  // first absmax block of segment 1 / 2
+  uint32_t sbase1, sbase2;  // first absmax2 entry of segment 1 / 2
+  uint32_t n_units;         // complete 4-byte units
+  uint32_t n_bytes;
+  int hb_shift;  // log2(blocksize / 2): bytes per absmax block
+  int sb_shift;  // log2(super_blocksize): absmax blocks per absmax2 entry
+};
+
+// Per-block scale for the block holding `byte` (all bytes of a 4-byte unit share one block
+// because blocksize/2 >= 4 and segment starts are block aligned).
+__device__ __forceinline__ float block_scale(const Nf4Args& a, uint32_t byte,
+                                             const float* __restrict__ s_code2) {
+  const uint32_t blk = byte >> a.hb_shift;
+  uint32_t sup;
+  float off;
+  if (byte >= a.split2) {
+    sup = a.sbase2 + ((blk - a.blk0_2) >> a.sb_shift);
+    off = a.off2;
+  } else if (byte >= a.split1) {
+    sup = a.sbase1 + ((blk - a.blk0_1) >> a.sb_shift);
+    off = a.off1;
+  } else {
+    sup = blk >> a.sb_shift;
+    off = a.off0;
+  }
+  const float c = s_code2[a.absmax[blk]];
+  const float s = c * a.absmax2[sup];  // rounded product (no contraction in this file)
+  return s + off;
+}
+
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+
+// Decode one packed byte into the fp16x2 word (even element in the low half).
+__device__ __forceinline__ uint32_t decode_byte(uint32_t b, float scale,
+                                                const float* __restrict__ s_nf4) {
+  const float vh = s_nf4[(b >> 4) & 15u] * scale;
+  const float vl = s_nf4[b & 15u] * scale;
+  h2 r;
+  r.x = static_cast<_Float16>(vh);
+  r.y = static_cast<_Float16>(vl);
+  return __builtin_bit_cast(uint32_t, r);
+}
+
+template <int UNROLL>
+__global__ __launch_bounds__(kThreads) void nf4_dequant_kernel(Nf4Args a) {
+  __shared__ float s_code2[256];
+  __shared__ float s_nf4[16];
+  const uint32_t t = threadIdx.x;
+  s_code2[t] = a.code2[t];
+  if (t < 16) s_nf4[t] = kNF4[t];
+  __syncthreads();
+
+  const uint32_t base = blockIdx.x * (kThreads * UNROLL) + t;
+  uint32_t p[UNROLL];
+  float sc[UNROLL];
+  if ((blockIdx.x + 1) * (kThreads * UNROLL) <= a.n_units) {
+    // Whole block in range (all but the last block): no per-unit checks, all loads issued first.
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u) p[u] = a.packed[base + u * kThreads];
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u) sc[u] = block_scale(a, (base + u * kThreads) * 4u, s_code2);
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u) {
+      uint4 w;
+      w.x = decode_byte(p[u] & 0xffu, sc[u], s_nf4);
+      w.y = decode_byte((p[u] >> 8) & 0xffu, sc[u], s_nf4);
+      w.z = decode_byte((p[u] >> 16) & 0xffu, sc[u], s_nf4);
+      w.w = decode_byte(p[u] >> 24, sc[u], s_nf4);
+      reinterpret_cast<uint4*>(a.out)[base + u * kThreads] = w;
+    }
+  } else {
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u) {
+      const uint32_t idx = base + u * kThreads;
+      p[u] = idx < a.n_units ? a.packed[idx] : 0u;
+    }
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u) {
+      const uint32_t idx = base + u * kThreads;
+      sc[u] = idx < a.n_units ? block_scale(a, idx * 4u, s_code2) : 0.0f;
+    }
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u) {
+      const uint32_t idx = base + u * kThreads;
+      if (idx < a.n_units) {
+        uint4 w;
+        w.x = decode_byte(p[u] & 0xffu, sc[u], s_nf4);
+        w.y = decode_byte((p[u] >> 8) & 0xffu, sc[u], s_nf4);
+        w.z = decode_byte((p[u] >> 16) & 0xffu, sc[u], s_nf4);
+        w.w = decode_byte(p[u] >> 24, sc[u], s_nf4);
+        reinterpret_cast<uint4*>(a.out)[idx] = w;
+      }
+    }
+  }
+
+  // Trailing bytes that do not fill a 4-byte unit (n_bytes % 4 != 0): the last block does them.
+  if (blockIdx.x == gridDim.x - 1) {
+    const uint32_t byte = a.n_units * 4u + t;
+    if (byte < a.n_bytes) {
+      const float s = block_scale(a, byte, s_code2);
+      a.out[byte] = decode_byte(a.packed_bytes[byte], s, s_nf4);
+    }
+  }
+}
+
+bool is_pow2(int64_t v) { return v > 0 && (v & (v - 1)) == 0; }
+
+int ilog2(int64_t v) {
+  int r = 0;
+  while ((int64_t(1) << r) < v) ++r;
+  return r;
+}
+
+}  // namespace
+}  // namespace rus
+
+extern "C" int rus_nf4_dequant(const uint8_t* packed, const uint8_t* absmax, const float* code2,
+                               const float* absmax2, float off0, float off1, float off2,
+                               int64_t split_byte_1, int64_t split_byte_2, int64_t absmax2_base_1,
+                               int64_t absmax2_base_2, int64_t n_bytes, int64_t n_absmax,
+                               int64_t n_absmax2, int32_t blocksize, int32_t super_blocksize,
+                               uint32_t* out_u32, void* stream) {
+  using namespace rus;
+  if (n_bytes < 0 || n_bytes >= (int64_t(1) << 31))
+    return fail(RUS_ERR_UNSUPPORTED, "rus_nf4_dequant: n_bytes=%lld outside [0, 2^31)",
+                (long long)n_bytes);
+  if (n_bytes == 0) return RUS_OK;
+  if (!packed || !absmax || !code2 || !absmax2 || !out_u32)
+    return fail(RUS_ERR_INVALID, "rus_nf4_dequant: null pointer argument");
+  if (!is_pow2(blocksize) || blocksize < 8 || !is_pow2(super_blocksize))
+    return fail(RUS_ERR_INVALID,
+                "rus_nf4_dequant: blocksize=%d (power of two >= 8) / super_blocksize=%d "
+                "(power of two) invalid",
+                blocksize, super_blocksize);
+  if (!aligned(packed, 4) || !aligned(out_u32, 16))
+    return fail(RUS_ERR_INVALID,
+                "rus_nf4_dequant: packed must be 4-byte and out 16-byte aligned");
+  const int64_t half_block = blocksize / 2;
+  if (split_byte_1 < 0 || split_byte_2 < split_byte_1 || split_byte_2 > n_bytes)
+    return fail(RUS_ERR_INVALID, "rus_nf4_dequant: splits (%lld, %lld) not ordered in [0, %lld]",
+                (long long)split_byte_1, (long long)split_byte_2, (long long)n_bytes);
+  if ((split_byte_1 < n_bytes && split_byte_1 % half_block) ||
+      (split_byte_2 < n_bytes && split_byte_2 % half_block))
+    return fail(RUS_ERR_INVALID,
+                "rus_nf4_dequant: segment starts (%lld, %lld) must be multiples of blocksize/2=%lld",
+                (long long)split_byte_1, (long long)split_byte_2, (long long)half_block);
+  if (absmax2_base_1 < 0 || absmax2_base_2 < absmax2_base_1)
+    return fail(RUS_ERR_INVALID, "rus_nf4_dequant: absmax2 bases must be non-negative, ordered");
+
+  // Every absmax / absmax2 index the kernel can form must be in range.
+  {
+    const int hb = ilog2(half_block), sb = ilog2(super_blocksize);
+    const int64_t last_blk = (n_bytes - 1) >> hb;
+    if (last_blk >= n_absmax)
+      return fail(RUS_ERR_INVALID, "rus_nf4_dequant: absmax has %lld entries, needs %lld",
+                  (long long)n_absmax, (long long)(last_blk + 1));
+    const int64_t starts[3] = {0, split_byte_1, split_byte_2};
+    const int64_t ends[3] = {split_byte_1, split_byte_2, n_bytes};
+    const int64_t bases[3] = {0, absmax2_base_1, absmax2_base_2};
+    for (int s = 0; s < 3; ++s) {
+      if (ends[s] <= starts[s]) continue;
+      const int64_t blk_first = starts[s] >> hb, blk_last = (ends[s] - 1) >> hb;
+      const int64_t sup_last = bases[s] + ((blk_last - blk_first) >> sb);
+      if (sup_last >= n_absmax2)
+        return fail(RUS_ERR_INVALID,
+                    "rus_nf4_dequant: absmax2 has %lld entries, segment %d needs index %lld",
+                    (long long)n_absmax2, s, (long long)sup_last);
+    }
+  }
+
+  Nf4Args a;
+  a.packed = reinterpret_cast<const uint32_t*>(packed);
+  a.packed_bytes = packed;
+  a.absmax = absmax;
+  a.code2 = code2;
+  a.absmax2 = absmax2;
+  a.out = out_u32;
+  a.off0 = off0;
+  a.off1 = off1;
+  a.off2 = off2;
+  // A split equal to n_bytes means "segment absent"; keep it unreachable.
+  a.split1 = static_cast<uint32_t>(split_byte_1);
+  a.split2 = static_cast<uint32_t>(split_byte_2);
+  a.hb_shift = ilog2(half_block);
+  a.sb_shift = ilog2(super_blocksize);
+  a.blk0_1 = static_cast<uint32_t>(split_byte_1 >> a.hb_shift);
+  a.blk0_2 = static_cast<uint32_t>(split_byte_2 >> a.hb_shift);
+  a.sbase1 = static_cast<uint32_t>(absmax2_base_1);
+  a.sbase2 = static_cast<uint32_t>(absmax2_base_2);
+  a.n_bytes = static_cast<uint32_t>(n_bytes);
+  a.n_units = static_cast<uint32_t>(n_bytes / 4);
+
+  constexpr int kUnroll = 4;
+  const uint32_t per_block = kThreads * kUnroll;
+  uint32_t grid = (a.n_units + per_block - 1) / per_block;
+  if (grid == 0) grid = 1;  // tail-only input
+  hipLaunchKernelGGL(nf4_dequant_kernel<kUnroll>, dim3(grid), dim3(kThreads), 0,
+                     static_cast<hipStream_t>(stream), a);
+  return check_launch("rus_nf4_dequant");
+}

@@ -1,0 +1,373 @@
+// Residual + RMSNorm forward and its one-pass backward for gfx950.
+//
+// Behaviour follows solution/kernels.py:125-199 (rms_norm_residual_fwd_kernel,
+// rms_norm_bwd_kernel) with the cast order of Qwen2RMSNorm: h = T(x + res), fp32 statistics,
+// y = T(fp32(T(h * rstd)) * w). Design (CDNA4, wave64):
+//   * one wavefront owns one row; each lane moves 16-byte packs (8 x fp16 or 4 x fp32), so a
+//     1536-wide fp16 row is 3 fully coalesced 1 KiB wave accesses per tensor; the packs stay in
+//     registers between the sum-of-squares reduction and the normalisation, so every input byte
+//     is read from HBM once and each output byte written once;
+//   * the row reduction is a 64-lane butterfly (no LDS, no block barrier);
+//   * rows narrower than NIT*64*pack or with a width that is not a multiple of the pack fall back
+//     to a scalar two-pass kernel (the second pass re-reads the row from L1/L2, not HBM);
+//   * built with -ffp-contract=off so every product and sum is rounded as in an eager fp32
+//     restatement (only the reduction order differs).
+#include "common.h"
+
+namespace rus {
+namespace {
+
+// Loads a pack of N weights as 16-byte chunks (fp32 weights for 8 fp16 activations: two 16-byte
+// loads) or as one narrower access (fp16 weights for 4 fp32 activations: one 8-byte load).
+template <typename T, int N>
+__device__ __forceinline__ void load16(const T* __restrict__ p, float (&out)[N]) {
+  constexpr int per = 16 / sizeof(T);
+  if constexpr (N >= per) {
+    static_assert(N % per == 0, "pack must be whole 16-byte chunks");
+#pragma unroll
+    for (int k = 0; k < N / per; ++k) {
+      float tmp[per];
+      load_f32<T, per>(p + k * per, tmp);
+#pragma unroll
+      for (int i = 0; i < per; ++i) out[k * per + i] = tmp[i];
+    }
+  } else {
+    load_f32<T, N>(p, out);
+  }
+}
+
+template <typename T, typename W, int NIT, bool HAS_RES>
+__global__ __launch_bounds__(256) void rmsnorm_fwd_vec(const T* __restrict__ x,
+                                                      const T* __restrict__ res,
+                                                      const W* __restrict__ w,
+                                                      T* __restrict__ sum_out, T* __restrict__ y,
+                                                      float* __restrict__ rstd, int n_rows,
+                                                      int n_cols, int64_t stride, float eps) {
+  constexpr int V = 16 / sizeof(T);
+  const int lane = threadIdx.x & (kWave - 1);
+  const int row = blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave;
+  if (row >= n_rows) return;
+  const int64_t off = static_cast<int64_t>(row) * stride;
+
+  float h[NIT][V];
+  float ss = 0.0f;
+#pragma unroll
+  for (int it = 0; it < NIT; ++it) {
+    const int c = (it * kWave + lane) * V;
+    if (c < n_cols) {
+      load_f32<T, V>(x + off + c, h[it]);
+      if (HAS_RES) {
+        float r[V];
+        load_f32<T, V>(res + off + c, r);
+#pragma unroll
+        for (int i = 0; i < V; ++i) h[it][i] = round_to<T>(h[it][i] + r[i]);
+        store_from_f32<T, V>(sum_out + off + c, h[it]);
+      }
+#pragma unroll
+      for (int i = 0; i < V; ++i) ss += h[it][i] * h[it][i];
+    }
+  }
+  ss = wave_sum(ss);
+  const float r = 1.0f / sqrtf(ss / static_cast<float>(n_cols) + eps);
+  if (lane == 0) rstd[row] = r;
+#pragma unroll
+  for (int it = 0; it < NIT; ++it) {
+    const int c = (it * kWave + lane) * V;
+    if (c < n_cols) {
+      float wv[V], o[V];
+      load16<W, V>(w + c, wv);
+#pragma unroll
+      for (int i = 0; i < V; ++i) o[i] = round_to<T>(h[it][i] * r) * wv[i];
+      store_from_f32<T, V>(y + off + c, o);
+    }
+  }
+}
+
+// Scalar two-pass fallback for any width.
+template <typename T, typename W, bool HAS_RES>
+__global__ __launch_bounds__(256) void rmsnorm_fwd_any(const T* __restrict__ x,
+                                                      const T* __restrict__ res,
+                                                      const W* __restrict__ w, T* sum_out,
+                                                      T* __restrict__ y, float* __restrict__ rstd,
+                                                      int n_rows, int n_cols, int64_t stride,
+                                                      float eps) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int row = blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave;
+  if (row >= n_rows) return;
+  const int64_t off = static_cast<int64_t>(row) * stride;
+  float ss = 0.0f;
+  for (int c = lane; c < n_cols; c += kWave) {
+    float h = static_cast<float>(x[off + c]);
+    if (HAS_RES) {
+      h = round_to<T>(h + static_cast<float>(res[off + c]));
+      sum_out[off + c] = static_cast<T>(h);
+    }
+    ss += h * h;
+  }
+  ss = wave_sum(ss);
+  const float r = 1.0f / sqrtf(ss / static_cast<float>(n_cols) + eps);
+  if (lane == 0) rstd[row] = r;
+  const T* hsrc = HAS_RES ? sum_out : x;  // this lane wrote these sum_out elements itself
+  for (int c = lane; c < n_cols; c += kWave) {
+    const float h = static_cast<float>(hsrc[off + c]);
+    y[off + c] = static_cast<T>(round_to<T>(h * r) * static_cast<float>(w[c]));
+  }
+}
+
+template <typename T, typename W, int NIT, bool HAS_DRES>
+__global__ __launch_bounds__(256) void rmsnorm_bwd_vec(const T* __restrict__ dy,
+                                                      const T* __restrict__ h,
+                                                      const W* __restrict__ w,
+                                                      const float* __restrict__ rstd,
+                                                      const T* __restrict__ dres,
+                                                      T* __restrict__ dx, int n_rows, int n_cols,
+                                                      int64_t stride) {
+  constexpr int V = 16 / sizeof(T);
+  const int lane = threadIdx.x & (kWave - 1);
+  const int row = blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave;
+  if (row >= n_rows) return;
+  const int64_t off = static_cast<int64_t>(row) * stride;
+  const float r = rstd[row];
+
+  float xh[NIT][V], g[NIT][V];
+  float acc = 0.0f;
+#pragma unroll
+  for (int it = 0; it < NIT; ++it) {
+    const int c = (it * kWave + lane) * V;
+    if (c < n_cols) {
+      float dv[V], wv[V];
+      load_f32<T, V>(h + off + c, xh[it]);
+      load_f32<T, V>(dy + off + c, dv);
+      load16<W, V>(w + c, wv);
+#pragma unroll
+      for (int i = 0; i < V; ++i) {
+        xh[it][i] = xh[it][i] * r;
+        g[it][i] = wv[i] * dv[i];
+        acc += xh[it][i] * g[it][i];
+      }
+    }
+  }
+  const float cm = wave_sum(acc) / static_cast<float>(n_cols);
+#pragma unroll
+  for (int it = 0; it < NIT; ++it) {
+    const int c = (it * kWave + lane) * V;
+    if (c < n_cols) {
+      float o[V];
+#pragma unroll
+      for (int i = 0; i < V; ++i) o[i] = (g[it][i] - xh[it][i] * cm) * r;
+      if (HAS_DRES) {
+        float d[V];
+        load_f32<T, V>(dres + off + c, d);
+#pragma unroll
+        for (int i = 0; i < V; ++i) o[i] = o[i] + d[i];
+      }
+      store_from_f32<T, V>(dx + off + c, o);
+    }
+  }
+}
+
+template <typename T, typename W, bool HAS_DRES>
+__global__ __launch_bounds__(256) void rmsnorm_bwd_any(const T* __restrict__ dy,
+                                                      const T* __restrict__ h,
+                                                      const W* __restrict__ w,
+                                                      const float* __restrict__ rstd,
+                                                      const T* __restrict__ dres,
+                                                      T* __restrict__ dx, int n_rows, int n_cols,
+                                                      int64_t stride) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int row = blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave;
+  if (row >= n_rows) return;
+  const int64_t off = static_cast<int64_t>(row) * stride;
+  const float r = rstd[row];
+  float acc = 0.0f;
+  for (int c = lane; c < n_cols; c += kWave) {
+    const float xh = static_cast<float>(h[off + c]) * r;
+    const float g = static_cast<float>(w[c]) * static_cast<float>(dy[off + c]);
+    acc += xh * g;
+  }
+  const float cm = wave_sum(acc) / static_cast<float>(n_cols);
+  for (int c = lane; c < n_cols; c += kWave) {
+    const float xh = static_cast<float>(h[off + c]) * r;
+    const float g = static_cast<float>(w[c]) * static_cast<float>(dy[off + c]);
+    float o = (g - xh * cm) * r;
+    if (HAS_DRES) o = o + static_cast<float>(dres[off + c]);
+    dx[off + c] = static_cast<T>(o);
+  }
+}
+
+// Iteration counts instantiated for the register-resident path (row width <= NIT*64*pack).
+constexpr int kNitChoices[] = {1, 2, 3, 4, 6, 8, 12, 16};
+
+int pick_nit(int64_t n_cols, int pack, int max_nit) {
+  for (int nit : kNitChoices) {
+    if (nit > max_nit) break;
+    if (n_cols <= static_cast<int64_t>(nit) * kWave * pack) return nit;
+  }
+  return 0;
+}
+
+struct Launch {
+  dim3 grid, block;
+};
+
+Launch row_launch(int64_t n_rows) {
+  // Four rows (waves) per workgroup once there are enough rows to fill every CU several times;
+  // otherwise one row per workgroup so that small batches still spread over all 256 CUs.
+  const int rows_per_block = n_rows >= 4096 ? 4 : 1;
+  Launch l;
+  l.block = dim3(kWave * rows_per_block);
+  l.grid = dim3(static_cast<unsigned>((n_rows + rows_per_block - 1) / rows_per_block));
+  return l;
+}
+
+template <typename T, typename W>
+int fwd_typed(const void* x, const void* res, const void* w, void* sum_out, void* y, float* rstd,
+              int64_t n_rows, int64_t n_cols, int64_t stride, float eps, hipStream_t st) {
+  constexpr int V = 16 / sizeof(T);
+  const T* xp = static_cast<const T*>(x);
+  const T* rp = static_cast<const T*>(res);
+  const W* wp = static_cast<const W*>(w);
+  T* sp = static_cast<T*>(sum_out);
+  T* yp = static_cast<T*>(y);
+  const Launch l = row_launch(n_rows);
+  const bool vec_ok = n_cols % V == 0 && stride % V == 0 && aligned(x, 16) && aligned(y, 16) &&
+                      aligned(w, 16) && (!res || (aligned(res, 16) && aligned(sum_out, 16)));
+  const int nit = vec_ok ? pick_nit(n_cols, V, 16) : 0;
+  const int nr = static_cast<int>(n_rows), nc = static_cast<int>(n_cols);
+#define RUS_FWD_VEC(NIT)                                                                      \
+  case NIT:                                                                                   \
+    if (res)                                                                                  \
+      hipLaunchKernelGGL((rmsnorm_fwd_vec<T, W, NIT, true>), l.grid, l.block, 0, st, xp, rp,  \
+                         wp, sp, yp, rstd, nr, nc, stride, eps);                              \
+    else                                                                                      \
+      hipLaunchKernelGGL((rmsnorm_fwd_vec<T, W, NIT, false>), l.grid, l.block, 0, st, xp, rp, \
+                         wp, sp, yp, rstd, nr, nc, stride, eps);                              \
+    break;
+  switch (nit) {
+    RUS_FWD_VEC(1)
+    RUS_FWD_VEC(2)
+    RUS_FWD_VEC(3)
+    RUS_FWD_VEC(4)
+    RUS_FWD_VEC(6)
+    RUS_FWD_VEC(8)
+    RUS_FWD_VEC(12)
+    RUS_FWD_VEC(16)
+    default:
+      if (res)
+        hipLaunchKernelGGL((rmsnorm_fwd_any<T, W, true>), l.grid, l.block, 0, st, xp, rp, wp, sp,
+                           yp, rstd, nr, nc, stride, eps);
+      else
+        hipLaunchKernelGGL((rmsnorm_fwd_any<T, W, false>), l.grid, l.block, 0, st, xp, rp, wp,
+                           sp, yp, rstd, nr, nc, stride, eps);
+  }
+#undef RUS_FWD_VEC
+  return check_launch("rus_rmsnorm_fwd");
+}
+
+template <typename T, typename W>
+int bwd_typed(const void* dy, const void* h, const void* w, const float* rstd, const void* dres,
+              void* dx, int64_t n_rows, int64_t n_cols, int64_t stride, hipStream_t st) {
+  constexpr int V = 16 / sizeof(T);
+  const T* dyp = static_cast<const T*>(dy);
+  const T* hp = static_cast<const T*>(h);
+  const W* wp = static_cast<const W*>(w);
+  const T* dp = static_cast<const T*>(dres);
+  T* dxp = static_cast<T*>(dx);
+  const Launch l = row_launch(n_rows);
+  const bool vec_ok = n_cols % V == 0 && stride % V == 0 && aligned(dy, 16) && aligned(h, 16) &&
+                      aligned(w, 16) && aligned(dx, 16) && (!dres || aligned(dres, 16));
+  // Two register-resident arrays per lane: cap the width so they stay within the VGPR budget.
+  const int nit = vec_ok ? pick_nit(n_cols, V, 8) : 0;
+  const int nr = static_cast<int>(n_rows), nc = static_cast<int>(n_cols);
+#define RUS_BWD_VEC(NIT)                                                                      \
+  case NIT:                                                                                   \
+    if (dres)                                                                                 \
+      hipLaunchKernelGGL((rmsnorm_bwd_vec<T, W, NIT, true>), l.grid, l.block, 0, st, dyp, hp, \
+                         wp, rstd, dp, dxp, nr, nc, stride);                                  \
+    else                                                                                      \
+      hipLaunchKernelGGL((rmsnorm_bwd_vec<T, W, NIT, false>), l.grid, l.block, 0, st, dyp,    \
+                         hp, wp, rstd, dp, dxp, nr, nc, stride);                              \
+    break;
+  switch (nit) {
+    RUS_BWD_VEC(1)
+    RUS_BWD_VEC(2)
+    RUS_BWD_VEC(3)
+    RUS_BWD_VEC(4)
+    RUS_BWD_VEC(6)
+    RUS_BWD_VEC(8)
+    default:
+      if (dres)
+        hipLaunchKernelGGL((rmsnorm_bwd_any<T, W, true>), l.grid, l.block, 0, st, dyp, hp, wp,
+                           rstd, dp, dxp, nr, nc, stride);
+      else
+        hipLaunchKernelGGL((rmsnorm_bwd_any<T, W, false>), l.grid, l.block, 0, st, dyp, hp, wp,
+                           rstd, dp, dxp, nr, nc, stride);
+  }
+#undef RUS_BWD_VEC
+  return check_launch("rus_rmsnorm_bwd");
+}
+
+int check_common(const char* fn, int64_t n_rows, int64_t n_cols, int64_t stride, int32_t dtype,
+                 int32_t w_dtype) {
+  if (n_rows < 0 || n_cols <= 0 || n_rows >= (int64_t(1) << 31) || n_cols >= (int64_t(1) << 30))
+    return fail(RUS_ERR_INVALID, "%s: bad shape [%lld, %lld]", fn, (long long)n_rows,
+                (long long)n_cols);
+  if (stride < n_cols)
+    return fail(RUS_ERR_INVALID, "%s: stride_row %lld < n_cols %lld", fn, (long long)stride,
+                (long long)n_cols);
+  if ((dtype != RUS_DTYPE_F16 && dtype != RUS_DTYPE_F32) ||
+      (w_dtype != RUS_DTYPE_F16 && w_dtype != RUS_DTYPE_F32))
+    return fail(RUS_ERR_INVALID, "%s: dtype %d / w_dtype %d not fp16(0)/fp32(1)", fn, dtype,
+                w_dtype);
+  return RUS_OK;
+}
+
+}  // namespace
+}  // namespace rus
+
+extern "C" int rus_rmsnorm_fwd(const void* x, const void* residual, const void* weight,
+                               int32_t w_dtype, void* sum_out, void* y, float* rstd,
+                               int64_t n_rows, int64_t n_cols, int64_t stride_row, float eps,
+                               int32_t dtype, void* stream) {
+  using namespace rus;
+  if (int e = check_common("rus_rmsnorm_fwd", n_rows, n_cols, stride_row, dtype, w_dtype)) return e;
+  if (n_rows == 0) return RUS_OK;
+  if (!x || !weight || !y || !rstd || (residual && !sum_out))
+    return fail(RUS_ERR_INVALID, "rus_rmsnorm_fwd: null pointer argument");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (dtype == RUS_DTYPE_F16) {
+    if (w_dtype == RUS_DTYPE_F16)
+      return fwd_typed<f16, f16>(x, residual, weight, sum_out, y, rstd, n_rows, n_cols,
+                                 stride_row, eps, st);
+    return fwd_typed<f16, float>(x, residual, weight, sum_out, y, rstd, n_rows, n_cols,
+                                 stride_row, eps, st);
+  }
+  if (w_dtype == RUS_DTYPE_F16)
+    return fwd_typed<float, f16>(x, residual, weight, sum_out, y, rstd, n_rows, n_cols,
+                                 stride_row, eps, st);
+  return fwd_typed<float, float>(x, residual, weight, sum_out, y, rstd, n_rows, n_cols,
+                                 stride_row, eps, st);
+}
+
+extern "C" int rus_rmsnorm_bwd(const void* dy, const void* h, const void* weight, int32_t w_dtype,
+                               const float* rstd, const void* dresidual, void* dx, int64_t n_rows,
+                               int64_t n_cols, int64_t stride_row, int32_t dtype, void* stream) {
+  using namespace rus;
+  if (int e = check_common("rus_rmsnorm_bwd", n_rows, n_cols, stride_row, dtype, w_dtype)) return e;
+  if (n_rows == 0) return RUS_OK;
+  if (!dy || !h || !weight || !rstd || !dx)
+    return fail(RUS_ERR_INVALID, "rus_rmsnorm_bwd: null pointer argument");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (dtype == RUS_DTYPE_F16) {
+    if (w_dtype == RUS_DTYPE_F16)
+      return bwd_typed<f16, f16>(dy, h, weight, rstd, dresidual, dx, n_rows, n_cols, stride_row,
+                                 st);
+    return bwd_typed<f16, float>(dy, h, weight, rstd, dresidual, dx, n_rows, n_cols, stride_row,
+                                 st);
+  }
+  if (w_dtype == RUS_DTYPE_F16)
+    return bwd_typed<float, f16>(dy, h, weight, rstd, dresidual, dx, n_rows, n_cols, stride_row,
+                                 st);
+  return bwd_typed<float, float>(dy, h, weight, rstd, dresidual, dx, n_rows, n_cols, stride_row,
+                                 st);
+}

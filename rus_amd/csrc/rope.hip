@@ -1,0 +1,335 @@
+// LoRA-delta add + NeoX rotary embedding (forward) and its adjoint with [dQ | dK | dV] packing
+// (backward) for gfx950.
+//
+// Behaviour follows solution/kernels.py:206-348 (qkv_lora_rope_fwd_kernel,
+// qkv_lora_rope_bwd_kernel) and the LoRA-gradient scaling of solution/ops.py:144-147: NeoX pairs
+// element j with j + head_dim/2 of the same head, cos/sin rows are indexed by each token's
+// position, and outputs are token-major [n_tokens, heads, head_dim]. Design (CDNA4, wave64):
+//   * one thread owns 8 consecutive elements of the low half of one head and the matching 8 of
+//     the high half (two 16-byte fp16 accesses each way); threads are numbered token-major, then
+//     head, then column, so each wave access covers whole 128-byte lines of consecutive heads;
+//   * Q, K and V heads of a token are all handled in the same launch (one pass over qkv, q_lora,
+//     v_lora), and the backward also emits the scaled LoRA gradients from the rounded packed
+//     values, which the reference computes with two extra elementwise launches;
+//   * positions are clamped into the cos/sin table, so a bad position can never read out of
+//     bounds; an optional device flag records that it happened;
+//   * built with -ffp-contract=off: products and sums round exactly as an eager fp32 restatement.
+#include "common.h"
+
+namespace rus {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kSpan = 8;  // elements per thread in each half of a head
+
+__device__ __forceinline__ int64_t clamp_pos(const int64_t* __restrict__ pos, int64_t t,
+                                             int64_t n_pos, int32_t* err_flag) {
+  int64_t p = pos[t];
+  if (p < 0 || p >= n_pos) {
+    if (err_flag) *err_flag = 1;
+    p = p < 0 ? 0 : n_pos - 1;
+  }
+  return p;
+}
+
+template <typename T>
+struct RopeFwdArgs {
+  const T* qkv;
+  const T* q_lora;
+  const T* v_lora;
+  const T* cos;
+  const T* sin;
+  const int64_t* pos;
+  T* q_out;
+  T* k_out;
+  T* v_out;
+  int64_t n_tokens, stride_qkv, stride_ql, stride_vl, stride_cos, n_pos;
+  float scale_q, scale_v;
+  int h_q, h_kv, head_dim;
+  int32_t* err_flag;
+};
+
+template <typename T, bool HAS_LORA>
+__global__ __launch_bounds__(kThreads) void rope_fwd_kernel(RopeFwdArgs<T> a) {
+  const int half = a.head_dim / 2;
+  const int per_head = half / kSpan;
+  const int heads = a.h_q + 2 * a.h_kv;
+  const int slots = heads * per_head;
+  const int64_t gid = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  const int64_t t = gid / slots;
+  if (t >= a.n_tokens) return;
+  const int slot = static_cast<int>(gid - t * slots);
+  const int hd = slot / per_head;
+  const int j = (slot - hd * per_head) * kSpan;
+
+  float lo[kSpan], hi[kSpan];
+  const T* row = a.qkv + t * a.stride_qkv + static_cast<int64_t>(hd) * a.head_dim;
+  load_f32<T, kSpan>(row + j, lo);
+  load_f32<T, kSpan>(row + j + half, hi);
+
+  if (hd >= a.h_q + a.h_kv) {  // V head: LoRA delta only
+    const int kv = hd - a.h_q - a.h_kv;
+    if (HAS_LORA) {
+      float dl[kSpan], dh[kSpan];
+      const T* vl = a.v_lora + t * a.stride_vl + static_cast<int64_t>(kv) * a.head_dim;
+      load_f32<T, kSpan>(vl + j, dl);
+      load_f32<T, kSpan>(vl + j + half, dh);
+#pragma unroll
+      for (int i = 0; i < kSpan; ++i) {
+        lo[i] = lo[i] + dl[i] * a.scale_v;
+        hi[i] = hi[i] + dh[i] * a.scale_v;
+      }
+    }
+    T* o = a.v_out + (t * a.h_kv + kv) * a.head_dim;
+    store_from_f32<T, kSpan>(o + j, lo);
+    store_from_f32<T, kSpan>(o + j + half, hi);
+    return;
+  }
+
+  if (HAS_LORA && hd < a.h_q) {
+    float dl[kSpan], dh[kSpan];
+    const T* ql = a.q_lora + t * a.stride_ql + static_cast<int64_t>(hd) * a.head_dim;
+    load_f32<T, kSpan>(ql + j, dl);
+    load_f32<T, kSpan>(ql + j + half, dh);
+#pragma unroll
+    for (int i = 0; i < kSpan; ++i) {
+      lo[i] = lo[i] + dl[i] * a.scale_q;
+      hi[i] = hi[i] + dh[i] * a.scale_q;
+    }
+  }
+  const int64_t p = clamp_pos(a.pos, t, a.n_pos, a.err_flag);
+  float cl[kSpan], ch[kSpan], sl[kSpan], sh[kSpan];
+  const T* cr = a.cos + p * a.stride_cos;
+  const T* sr = a.sin + p * a.stride_cos;
+  load_f32<T, kSpan>(cr + j, cl);
+  load_f32<T, kSpan>(cr + j + half, ch);
+  load_f32<T, kSpan>(sr + j, sl);
+  load_f32<T, kSpan>(sr + j + half, sh);
+  float ol[kSpan], oh[kSpan];
+#pragma unroll
+  for (int i = 0; i < kSpan; ++i) {
+    ol[i] = lo[i] * cl[i] - hi[i] * sl[i];
+    oh[i] = hi[i] * ch[i] + lo[i] * sh[i];
+  }
+  T* o = hd < a.h_q ? a.q_out + (t * a.h_q + hd) * a.head_dim
+                    : a.k_out + (t * a.h_kv + (hd - a.h_q)) * a.head_dim;
+  store_from_f32<T, kSpan>(o + j, ol);
+  store_from_f32<T, kSpan>(o + j + half, oh);
+}
+
+template <typename T>
+struct RopeBwdArgs {
+  const T* dq;
+  const T* dk;
+  const T* dv;
+  const T* cos;
+  const T* sin;
+  const int64_t* pos;
+  T* dqkv;
+  T* dq_lora;
+  T* dv_lora;
+  int64_t n_tokens, stride_dqkv, stride_cos, n_pos;
+  float scale_q, scale_v;
+  int h_q, h_kv, head_dim;
+  int32_t* err_flag;
+};
+
+template <typename T, bool LORA_OUT>
+__global__ __launch_bounds__(kThreads) void rope_bwd_kernel(RopeBwdArgs<T> a) {
+  const int half = a.head_dim / 2;
+  const int per_head = half / kSpan;
+  const int heads = a.h_q + 2 * a.h_kv;
+  const int slots = heads * per_head;
+  const int64_t gid = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  const int64_t t = gid / slots;
+  if (t >= a.n_tokens) return;
+  const int slot = static_cast<int>(gid - t * slots);
+  const int hd = slot / per_head;
+  const int j = (slot - hd * per_head) * kSpan;
+  T* out = a.dqkv + t * a.stride_dqkv + static_cast<int64_t>(hd) * a.head_dim;
+
+  float lo[kSpan], hi[kSpan];
+  if (hd >= a.h_q + a.h_kv) {  // dV: copy (and scale into dv_lora)
+    const int kv = hd - a.h_q - a.h_kv;
+    const T* src = a.dv + (t * a.h_kv + kv) * a.head_dim;
+    load_f32<T, kSpan>(src + j, lo);
+    load_f32<T, kSpan>(src + j + half, hi);
+    store_from_f32<T, kSpan>(out + j, lo);
+    store_from_f32<T, kSpan>(out + j + half, hi);
+    if (LORA_OUT) {
+#pragma unroll
+      for (int i = 0; i < kSpan; ++i) {
+        lo[i] = lo[i] * a.scale_v;
+        hi[i] = hi[i] * a.scale_v;
+      }
+      T* l = a.dv_lora + (t * a.h_kv + kv) * a.head_dim;
+      store_from_f32<T, kSpan>(l + j, lo);
+      store_from_f32<T, kSpan>(l + j + half, hi);
+    }
+    return;
+  }
+
+  const T* src = hd < a.h_q ? a.dq + (t * a.h_q + hd) * a.head_dim
+                            : a.dk + (t * a.h_kv + (hd - a.h_q)) * a.head_dim;
+  load_f32<T, kSpan>(src + j, lo);
+  load_f32<T, kSpan>(src + j + half, hi);
+  const int64_t p = clamp_pos(a.pos, t, a.n_pos, a.err_flag);
+  float cl[kSpan], ch[kSpan], sl[kSpan], sh[kSpan];
+  const T* cr = a.cos + p * a.stride_cos;
+  const T* sr = a.sin + p * a.stride_cos;
+  load_f32<T, kSpan>(cr + j, cl);
+  load_f32<T, kSpan>(cr + j + half, ch);
+  load_f32<T, kSpan>(sr + j, sl);
+  load_f32<T, kSpan>(sr + j + half, sh);
+  float ol[kSpan], oh[kSpan];
+#pragma unroll
+  for (int i = 0; i < kSpan; ++i) {
+    ol[i] = round_to<T>(lo[i] * cl[i] + hi[i] * sh[i]);
+    oh[i] = round_to<T>(hi[i] * ch[i] - lo[i] * sl[i]);
+  }
+  store_from_f32<T, kSpan>(out + j, ol);
+  store_from_f32<T, kSpan>(out + j + half, oh);
+  if (LORA_OUT && hd < a.h_q) {
+#pragma unroll
+    for (int i = 0; i < kSpan; ++i) {
+      ol[i] = ol[i] * a.scale_q;
+      oh[i] = oh[i] * a.scale_q;
+    }
+    T* l = a.dq_lora + (t * a.h_q + hd) * a.head_dim;
+    store_from_f32<T, kSpan>(l + j, ol);
+    store_from_f32<T, kSpan>(l + j + half, oh);
+  }
+}
+
+int check_heads(const char* fn, int64_t n_tokens, int32_t h_q, int32_t h_kv, int32_t head_dim,
+                int64_t n_pos, int64_t stride_cos, int32_t dtype) {
+  if (dtype != RUS_DTYPE_F16 && dtype != RUS_DTYPE_F32)
+    return fail(RUS_ERR_INVALID, "%s: dtype %d not fp16(0)/fp32(1)", fn, dtype);
+  if (n_tokens < 0 || n_tokens >= (int64_t(1) << 31))
+    return fail(RUS_ERR_INVALID, "%s: n_tokens=%lld", fn, (long long)n_tokens);
+  if (h_q <= 0 || h_kv <= 0 || head_dim <= 0 || head_dim % (2 * kSpan))
+    return fail(RUS_ERR_INVALID, "%s: h_q=%d h_kv=%d head_dim=%d (multiple of 16 required)", fn,
+                h_q, h_kv, head_dim);
+  if (n_pos <= 0 || stride_cos < head_dim)
+    return fail(RUS_ERR_INVALID, "%s: cos/sin table [%lld, stride %lld] too small", fn,
+                (long long)n_pos, (long long)stride_cos);
+  return RUS_OK;
+}
+
+// Every pointer and row stride must allow 16-byte (fp16: 8 elements) accesses at element offsets
+// that are multiples of 8.
+template <typename T>
+bool aligned8(const void* p, int64_t stride) {
+  return p == nullptr || (aligned(p, 16) && (stride * static_cast<int64_t>(sizeof(T))) % 16 == 0);
+}
+
+template <typename T>
+int fwd_typed(const RopeFwdArgs<T>& a, hipStream_t st) {
+  if (!aligned8<T>(a.qkv, a.stride_qkv) || !aligned8<T>(a.q_lora, a.stride_ql) ||
+      !aligned8<T>(a.v_lora, a.stride_vl) || !aligned8<T>(a.cos, a.stride_cos) ||
+      !aligned8<T>(a.sin, a.stride_cos) || !aligned(a.q_out, 16) || !aligned(a.k_out, 16) ||
+      !aligned(a.v_out, 16))
+    return fail(RUS_ERR_INVALID, "rus_qkv_lora_rope_fwd: pointers/strides must be 16-byte aligned");
+  const int64_t slots = static_cast<int64_t>(a.h_q + 2 * a.h_kv) * (a.head_dim / 2 / kSpan);
+  const int64_t threads = a.n_tokens * slots;
+  const dim3 grid(static_cast<unsigned>((threads + kThreads - 1) / kThreads));
+  if (a.q_lora)
+    hipLaunchKernelGGL((rope_fwd_kernel<T, true>), grid, dim3(kThreads), 0, st, a);
+  else
+    hipLaunchKernelGGL((rope_fwd_kernel<T, false>), grid, dim3(kThreads), 0, st, a);
+  return check_launch("rus_qkv_lora_rope_fwd");
+}
+
+template <typename T>
+int bwd_typed(const RopeBwdArgs<T>& a, hipStream_t st) {
+  if (!aligned(a.dq, 16) || !aligned(a.dk, 16) || !aligned(a.dv, 16) ||
+      !aligned8<T>(a.cos, a.stride_cos) || !aligned8<T>(a.sin, a.stride_cos) ||
+      !aligned8<T>(a.dqkv, a.stride_dqkv) || (a.dq_lora && !aligned(a.dq_lora, 16)) ||
+      (a.dv_lora && !aligned(a.dv_lora, 16)))
+    return fail(RUS_ERR_INVALID, "rus_qkv_rope_bwd: pointers/strides must be 16-byte aligned");
+  const int64_t slots = static_cast<int64_t>(a.h_q + 2 * a.h_kv) * (a.head_dim / 2 / kSpan);
+  const int64_t threads = a.n_tokens * slots;
+  const dim3 grid(static_cast<unsigned>((threads + kThreads - 1) / kThreads));
+  if (a.dq_lora)
+    hipLaunchKernelGGL((rope_bwd_kernel<T, true>), grid, dim3(kThreads), 0, st, a);
+  else
+    hipLaunchKernelGGL((rope_bwd_kernel<T, false>), grid, dim3(kThreads), 0, st, a);
+  return check_launch("rus_qkv_rope_bwd");
+}
+
+}  // namespace
+}  // namespace rus
+
+extern "C" int rus_qkv_lora_rope_fwd(const void* qkv, const void* q_lora, const void* v_lora,
+                                     const void* cos, const void* sin, const int64_t* pos_ids,
+                                     void* q_out, void* k_out, void* v_out, int64_t n_tokens,
+                                     int64_t stride_qkv, int64_t stride_ql, int64_t stride_vl,
+                                     int64_t stride_cos, int64_t n_pos, float scale_q,
+                                     float scale_v, int32_t h_q, int32_t h_kv, int32_t head_dim,
+                                     int32_t* err_flag, int32_t dtype, void* stream) {
+  using namespace rus;
+  if (int e = check_heads("rus_qkv_lora_rope_fwd", n_tokens, h_q, h_kv, head_dim, n_pos,
+                          stride_cos, dtype))
+    return e;
+  if (n_tokens == 0) return RUS_OK;
+  if (!qkv || !cos || !sin || !pos_ids || !q_out || !k_out || !v_out)
+    return fail(RUS_ERR_INVALID, "rus_qkv_lora_rope_fwd: null pointer argument");
+  if ((q_lora == nullptr) != (v_lora == nullptr))
+    return fail(RUS_ERR_INVALID, "rus_qkv_lora_rope_fwd: q_lora and v_lora must both be given");
+  const int64_t width = static_cast<int64_t>(h_q + 2 * h_kv) * head_dim;
+  if (stride_qkv < width || (q_lora && (stride_ql < int64_t(h_q) * head_dim ||
+                                        stride_vl < int64_t(h_kv) * head_dim)))
+    return fail(RUS_ERR_INVALID, "rus_qkv_lora_rope_fwd: row strides smaller than rows");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+#define RUS_ROPE_FWD(T)                                                                          \
+  {                                                                                              \
+    RopeFwdArgs<T> a{static_cast<const T*>(qkv), static_cast<const T*>(q_lora),                 \
+                     static_cast<const T*>(v_lora), static_cast<const T*>(cos),                 \
+                     static_cast<const T*>(sin), pos_ids, static_cast<T*>(q_out),               \
+                     static_cast<T*>(k_out), static_cast<T*>(v_out), n_tokens, stride_qkv,      \
+                     stride_ql, stride_vl, stride_cos, n_pos, scale_q, scale_v, h_q, h_kv,      \
+                     head_dim, err_flag};                                                        \
+    return fwd_typed<T>(a, st);                                                                  \
+  }
+  if (dtype == RUS_DTYPE_F16) RUS_ROPE_FWD(f16)
+  RUS_ROPE_FWD(float)
+#undef RUS_ROPE_FWD
+}
+
+extern "C" int rus_qkv_rope_bwd(const void* dq_rot, const void* dk_rot, const void* dv,
+                                const void* cos, const void* sin, const int64_t* pos_ids,
+                                void* dqkv, void* dq_lora, void* dv_lora, int64_t n_tokens,
+                                int64_t stride_dqkv, int64_t stride_cos, int64_t n_pos,
+                                float scale_q, float scale_v, int32_t h_q, int32_t h_kv,
+                                int32_t head_dim, int32_t* err_flag, int32_t dtype,
+                                void* stream) {
+  using namespace rus;
+  if (int e = check_heads("rus_qkv_rope_bwd", n_tokens, h_q, h_kv, head_dim, n_pos, stride_cos,
+                          dtype))
+    return e;
+  if (n_tokens == 0) return RUS_OK;
+  if (!dq_rot || !dk_rot || !dv || !cos || !sin || !pos_ids || !dqkv)
+    return fail(RUS_ERR_INVALID, "rus_qkv_rope_bwd: null pointer argument");
+  if ((dq_lora == nullptr) != (dv_lora == nullptr))
+    return fail(RUS_ERR_INVALID, "rus_qkv_rope_bwd: dq_lora and dv_lora must both be given");
+  if (stride_dqkv < static_cast<int64_t>(h_q + 2 * h_kv) * head_dim)
+    return fail(RUS_ERR_INVALID, "rus_qkv_rope_bwd: stride_dqkv smaller than a row");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+#define RUS_ROPE_BWD(T)                                                                         \
+  {                                                                                             \
+    RopeBwdArgs<T> a{static_cast<const T*>(dq_rot), static_cast<const T*>(dk_rot),             \
+                     static_cast<const T*>(dv),     static_cast<const T*>(cos),                \
+                     static_cast<const T*>(sin),    pos_ids,                                   \
+                     static_cast<T*>(dqkv),         static_cast<T*>(dq_lora),                  \
+                     static_cast<T*>(dv_lora),      n_tokens,                                  \
+                     stride_dqkv,                   stride_cos,                                \
+                     n_pos,                         scale_q,                                   \
+                     scale_v,                       h_q,                                       \
+                     h_kv,                          head_dim,                                  \
+                     err_flag};                                                                 \
+    return bwd_typed<T>(a, st);                                                                 \
+  }
+  if (dtype == RUS_DTYPE_F16) RUS_ROPE_BWD(f16)
+  RUS_ROPE_BWD(float)
+#undef RUS_ROPE_BWD
+}

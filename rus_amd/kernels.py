@@ -1,0 +1,431 @@
+"""Kernel launchers with the names and signatures of ``solution/kernels.py`` (the reference).
+
+Each launcher validates its tensors, allocates outputs with ``torch.empty`` on the input's device
+(as the reference does, kernels.py:588, 633-634, 684, 732-734, 778, 810, 892-893) and enqueues one
+gfx950 kernel from ``librus_amd.so`` on the current HIP stream through the C ABI
+(``include/rus_amd.h``). Nothing here computes on the host: a CPU tensor or a missing library
+raises ``RuntimeError``.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+from ._lib import DTYPE_F16, DTYPE_F32
+
+__all__ = [
+    "dequant_nf4_tensor",
+    "nf4_absmax2_bases",
+    "rms_norm_fwd",
+    "rms_norm_bwd",
+    "qkv_rope_fwd",
+    "qkv_rope_bwd",
+    "qkv_rope_bwd_lora",
+    "mlp_glu_fwd",
+    "mlp_glu_bwd",
+]
+
+
+def _require_device(fn: str, *tensors: torch.Tensor | None) -> None:
+    for t in tensors:
+        if t is not None and not t.is_cuda:
+            raise RuntimeError(f"{fn}: rus_amd kernels need HIP device tensors, got {t.device}")
+
+
+def _dtype_code(fn: str, dtype: torch.dtype) -> int:
+    if dtype == torch.float16:
+        return DTYPE_F16
+    if dtype == torch.float32:
+        return DTYPE_F32
+    raise TypeError(f"{fn}: unsupported dtype {dtype} (fp16 or fp32)")
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+# ---------------------------------------------------------------------------------------------
+# NF4 double-quant dequantisation (reference: kernels.py:27-118, launcher kernels.py:572-619)
+# ---------------------------------------------------------------------------------------------
+
+
+def nf4_absmax2_bases(
+    n_bytes: int, split_bytes: tuple[int, int] | None, blocksize: int, super_blocksize: int
+) -> tuple[int, int]:
+    """absmax2 index at which segments 1 and 2 start when each segment was double-quantised on
+    its own (ceil(blocks / super_blocksize) entries per segment, concatenated)."""
+    if split_bytes is None:
+        return 0, 0
+    hb = blocksize // 2
+    s1, s2 = int(split_bytes[0]), int(split_bytes[1])
+    n0 = -(-(s1 // hb) // super_blocksize) if s1 > 0 else 0
+    n1 = -(-((s2 - s1) // hb) // super_blocksize) if s2 > s1 else 0
+    return n0, n0 + n1
+
+
+def dequant_nf4_tensor(
+    packed: torch.Tensor,
+    absmax: torch.Tensor,
+    code2: torch.Tensor,
+    absmax2: torch.Tensor,
+    offset: float | tuple[float, float, float],
+    out_shape: tuple[int, int],
+    out_buf: torch.Tensor | None = None,
+    split_bytes: tuple[int, int] | None = None,
+    blocksize: int = 64,
+    super_blocksize: int = 256,
+    absmax2_bases: tuple[int, int] | None = None,
+) -> torch.Tensor:
+    """Dequantise packed NF4 (2 codes per byte, high nibble first) with double-quantised absmax
+    into fp16 ``out_shape`` (a new tensor, or a view at the start of ``out_buf``).
+
+    ``offset`` is one float or one per segment; ``split_bytes`` gives the byte offsets where
+    segments 1 and 2 start (fused [q|k|v] or [gate|up]). ``absmax2_bases`` (an extension of the
+    reference signature) gives where each segment's absmax2 entries start; by default each segment
+    is taken to have been double-quantised on its own, which equals the reference's global
+    super-block indexing whenever segment block counts are multiples of ``super_blocksize``.
+    """
+    fn = "dequant_nf4_tensor"
+    _require_device(fn, packed, absmax, code2, absmax2, out_buf)
+    n_elements = int(out_shape[0]) * int(out_shape[1])
+    if n_elements % 2:
+        raise ValueError(f"{fn}: element count {n_elements} must be even (2 codes per byte)")
+    n_bytes = n_elements // 2
+    if packed.dtype != torch.uint8 or absmax.dtype != torch.uint8:
+        raise TypeError(f"{fn}: packed and absmax must be uint8")
+    if code2.dtype != torch.float32 or absmax2.dtype != torch.float32:
+        raise TypeError(f"{fn}: code2 and absmax2 must be float32")
+    packed = packed.reshape(-1)
+    absmax = absmax.reshape(-1)
+    code2 = code2.reshape(-1)
+    absmax2 = absmax2.reshape(-1)
+    for name, t in (("packed", packed), ("absmax", absmax), ("code2", code2), ("absmax2", absmax2)):
+        if not t.is_contiguous():
+            raise ValueError(f"{fn}: {name} must be contiguous")
+    if packed.numel() < n_bytes:
+        raise ValueError(f"{fn}: packed has {packed.numel()} bytes, need {n_bytes}")
+    if code2.numel() != 256:
+        raise ValueError(f"{fn}: code2 must have 256 entries, got {code2.numel()}")
+    if out_buf is None:
+        out = torch.empty(out_shape, dtype=torch.float16, device=packed.device)
+    else:
+        if out_buf.dtype != torch.float16 or out_buf.numel() < n_elements:
+            raise ValueError(f"{fn}: out_buf must be fp16 with at least {n_elements} elements")
+        out = out_buf.view(-1)[:n_elements].view(out_shape)
+    if isinstance(offset, (tuple, list)):
+        off0, off1, off2 = float(offset[0]), float(offset[1]), float(offset[2])
+    else:
+        off0 = off1 = off2 = float(offset)
+    if split_bytes is not None:
+        sb1, sb2 = int(split_bytes[0]), int(split_bytes[1])
+    else:
+        sb1 = sb2 = n_bytes
+    if absmax2_bases is None:
+        absmax2_bases = nf4_absmax2_bases(n_bytes, (sb1, sb2), blocksize, super_blocksize)
+    _lib.call(
+        "rus_nf4_dequant",
+        packed.data_ptr(), absmax.data_ptr(), code2.data_ptr(), absmax2.data_ptr(),
+        off0, off1, off2, sb1, sb2, int(absmax2_bases[0]), int(absmax2_bases[1]),
+        n_bytes, absmax.numel(), absmax2.numel(), int(blocksize), int(super_blocksize),
+        out.data_ptr(), _stream(out),
+    )
+    return out
+
+
+# ---------------------------------------------------------------------------------------------
+# Residual + RMSNorm (reference: kernels.py:125-199, launchers kernels.py:622-714)
+# ---------------------------------------------------------------------------------------------
+
+
+def rms_norm_fwd(
+    x: torch.Tensor,
+    weight: torch.Tensor,
+    eps: float = 1e-6,
+    residual: torch.Tensor | None = None,
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Fused residual add + RMSNorm forward. Returns (norm_out, sum_out_or_x, rstd)."""
+    fn = "rms_norm_fwd"
+    _require_device(fn, x, weight, residual)
+    dt = _dtype_code(fn, x.dtype)
+    wdt = _dtype_code(fn, weight.dtype)
+    orig_shape = x.shape
+    n_cols = orig_shape[-1]
+    x_2d = x.contiguous().view(-1, n_cols)
+    n_rows = x_2d.shape[0]
+    w = weight.contiguous()
+    if w.numel() != n_cols:
+        raise ValueError(f"{fn}: weight has {w.numel()} entries, rows have {n_cols}")
+    norm_out = torch.empty_like(x_2d)
+    rstd = torch.empty((n_rows,), dtype=torch.float32, device=x.device)
+    if residual is not None:
+        if residual.dtype != x.dtype or residual.shape != orig_shape:
+            raise ValueError(f"{fn}: residual must match x in shape and dtype")
+        res_2d = residual.contiguous().view(-1, n_cols)
+        sum_out = torch.empty_like(x_2d)
+        _lib.call("rus_rmsnorm_fwd", x_2d.data_ptr(), res_2d.data_ptr(), w.data_ptr(), wdt,
+                  sum_out.data_ptr(), norm_out.data_ptr(), rstd.data_ptr(), n_rows, n_cols,
+                  x_2d.stride(0), float(eps), dt, _stream(x))
+        return norm_out.view(orig_shape), sum_out.view(orig_shape), rstd
+    _lib.call("rus_rmsnorm_fwd", x_2d.data_ptr(), None, w.data_ptr(), wdt, None,
+              norm_out.data_ptr(), rstd.data_ptr(), n_rows, n_cols, x_2d.stride(0), float(eps), dt,
+              _stream(x))
+    return norm_out.view(orig_shape), x, rstd
+
+
+def rms_norm_bwd(
+    dy: torch.Tensor,
+    h: torch.Tensor,
+    weight: torch.Tensor,
+    rstd: torch.Tensor,
+    dresidual: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """RMSNorm backward with optional residual-gradient accumulation (no weight gradient)."""
+    fn = "rms_norm_bwd"
+    _require_device(fn, dy, h, weight, rstd, dresidual)
+    dt = _dtype_code(fn, h.dtype)
+    wdt = _dtype_code(fn, weight.dtype)
+    orig_shape = dy.shape
+    n_cols = orig_shape[-1]
+    dy_2d = dy.contiguous().view(-1, n_cols)
+    h_2d = h.contiguous().view(-1, n_cols)
+    if dy_2d.dtype != h_2d.dtype or dy_2d.shape != h_2d.shape:
+        raise ValueError(f"{fn}: dy and h must match in shape and dtype")
+    n_rows = dy_2d.shape[0]
+    w = weight.contiguous()
+    rs = rstd.contiguous()
+    if rs.dtype != torch.float32 or rs.numel() != n_rows:
+        raise ValueError(f"{fn}: rstd must be float32 with {n_rows} entries")
+    dx = torch.empty_like(h_2d)
+    dres_ptr = None
+    if dresidual is not None:
+        dres_2d = dresidual.contiguous().view(-1, n_cols)
+        if dres_2d.dtype != h_2d.dtype or dres_2d.shape != h_2d.shape:
+            raise ValueError(f"{fn}: dresidual must match h in shape and dtype")
+        dres_ptr = dres_2d.data_ptr()
+    _lib.call("rus_rmsnorm_bwd", dy_2d.data_ptr(), h_2d.data_ptr(), w.data_ptr(), wdt,
+              rs.data_ptr(), dres_ptr, dx.data_ptr(), n_rows, n_cols, dy_2d.stride(0), dt,
+              _stream(dy))
+    return dx.view(orig_shape)
+
+
+# ---------------------------------------------------------------------------------------------
+# LoRA-delta + NeoX RoPE (reference: kernels.py:206-348, launchers kernels.py:717-798)
+# ---------------------------------------------------------------------------------------------
+
+
+def _rows(fn: str, t: torch.Tensor, width: int, name: str) -> torch.Tensor:
+    if t.dim() != 2 or t.shape[1] < width:
+        raise ValueError(f"{fn}: {name} must be 2-D with at least {width} columns, got {tuple(t.shape)}")
+    return t if t.stride(1) == 1 else t.contiguous()
+
+
+def qkv_rope_fwd(
+    qkv: torch.Tensor,
+    cos: torch.Tensor,
+    sin: torch.Tensor,
+    pos_ids: torch.Tensor,
+    q_lora: torch.Tensor | None = None,
+    v_lora: torch.Tensor | None = None,
+    scale_q: float = 2.0,
+    scale_v: float = 2.0,
+    h_q: int = 12,
+    h_kv: int = 2,
+    head_dim: int = 128,
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Q = rope(q + scale_q*q_lora), K = rope(k), V = v + scale_v*v_lora; returns (q, k, v) as
+    contiguous [n_tokens, heads, head_dim]. LoRA is applied only when both deltas are given."""
+    fn = "qkv_rope_fwd"
+    _require_device(fn, qkv, cos, sin, pos_ids, q_lora, v_lora)
+    dt = _dtype_code(fn, qkv.dtype)
+    n_tokens = qkv.shape[0]
+    q_dim, kv_dim = h_q * head_dim, h_kv * head_dim
+    qkv = _rows(fn, qkv, q_dim + 2 * kv_dim, "qkv")
+    cos = _rows(fn, cos, head_dim, "cos")
+    sin = _rows(fn, sin, head_dim, "sin")
+    if cos.dtype != qkv.dtype or sin.dtype != qkv.dtype or sin.stride(0) != cos.stride(0):
+        raise ValueError(f"{fn}: cos/sin must share qkv's dtype and a row stride")
+    if sin.shape[0] != cos.shape[0]:
+        raise ValueError(f"{fn}: cos and sin tables differ in length")
+    pos = pos_ids.reshape(-1)
+    if pos.dtype != torch.int64 or pos.numel() != n_tokens:
+        raise ValueError(f"{fn}: pos_ids must be int64 with {n_tokens} entries")
+    pos = pos.contiguous()
+    has_lora = q_lora is not None and v_lora is not None
+    ql = vl = None
+    if has_lora:
+        ql = _rows(fn, q_lora, q_dim, "q_lora")
+        vl = _rows(fn, v_lora, kv_dim, "v_lora")
+        if ql.dtype != qkv.dtype or vl.dtype != qkv.dtype:
+            raise ValueError(f"{fn}: LoRA deltas must share qkv's dtype")
+        if ql.shape[0] != n_tokens or vl.shape[0] != n_tokens:
+            raise ValueError(f"{fn}: LoRA deltas must have {n_tokens} rows")
+    q_out = torch.empty((n_tokens, h_q, head_dim), dtype=qkv.dtype, device=qkv.device)
+    k_out = torch.empty((n_tokens, h_kv, head_dim), dtype=qkv.dtype, device=qkv.device)
+    v_out = torch.empty((n_tokens, h_kv, head_dim), dtype=qkv.dtype, device=qkv.device)
+    _lib.call(
+        "rus_qkv_lora_rope_fwd",
+        qkv.data_ptr(), _ptr(ql), _ptr(vl), cos.data_ptr(), sin.data_ptr(), pos.data_ptr(),
+        q_out.data_ptr(), k_out.data_ptr(), v_out.data_ptr(), n_tokens, qkv.stride(0),
+        ql.stride(0) if has_lora else 0, vl.stride(0) if has_lora else 0, cos.stride(0),
+        cos.shape[0], float(scale_q), float(scale_v), h_q, h_kv, head_dim, None, dt, _stream(qkv),
+    )
+    return q_out, k_out, v_out
+
+
+def _rope_bwd(fn, dq_rot, dk_rot, dv_out, cos, sin, pos_ids, h_q, h_kv, head_dim, scale_q,
+              scale_v, with_lora):
+    _require_device(fn, dq_rot, dk_rot, dv_out, cos, sin, pos_ids)
+    dt = _dtype_code(fn, dq_rot.dtype)
+    n_tokens = dq_rot.shape[0]
+    q_dim, kv_dim = h_q * head_dim, h_kv * head_dim
+    dq_c = dq_rot.contiguous()
+    dk_c = dk_rot.contiguous()
+    dv_c = dv_out.contiguous()
+    for name, t, width in (("dq_rot", dq_c, q_dim), ("dk_rot", dk_c, kv_dim), ("dv_out", dv_c, kv_dim)):
+        if t.numel() != n_tokens * width or t.dtype != dq_c.dtype:
+            raise ValueError(f"{fn}: {name} must hold [{n_tokens}, {width}] of {dq_c.dtype}")
+    cos = _rows(fn, cos, head_dim, "cos")
+    sin = _rows(fn, sin, head_dim, "sin")
+    if cos.dtype != dq_c.dtype or sin.dtype != dq_c.dtype or sin.stride(0) != cos.stride(0):
+        raise ValueError(f"{fn}: cos/sin must share the gradient dtype and a row stride")
+    pos = pos_ids.reshape(-1).contiguous()
+    if pos.dtype != torch.int64 or pos.numel() != n_tokens:
+        raise ValueError(f"{fn}: pos_ids must be int64 with {n_tokens} entries")
+    dqkv = torch.empty((n_tokens, q_dim + 2 * kv_dim), dtype=dq_c.dtype, device=dq_c.device)
+    dql = dvl = None
+    if with_lora:
+        dql = torch.empty((n_tokens, q_dim), dtype=dq_c.dtype, device=dq_c.device)
+        dvl = torch.empty((n_tokens, kv_dim), dtype=dq_c.dtype, device=dq_c.device)
+    _lib.call(
+        "rus_qkv_rope_bwd",
+        dq_c.data_ptr(), dk_c.data_ptr(), dv_c.data_ptr(), cos.data_ptr(), sin.data_ptr(),
+        pos.data_ptr(), dqkv.data_ptr(), _ptr(dql), _ptr(dvl), n_tokens, dqkv.stride(0),
+        cos.stride(0), cos.shape[0], float(scale_q), float(scale_v), h_q, h_kv, head_dim, None,
+        dt, _stream(dq_c),
+    )
+    return dqkv, dql, dvl
+
+
+def qkv_rope_bwd(
+    dq_rot: torch.Tensor,
+    dk_rot: torch.Tensor,
+    dv_out: torch.Tensor,
+    cos: torch.Tensor,
+    sin: torch.Tensor,
+    pos_ids: torch.Tensor,
+    h_q: int = 12,
+    h_kv: int = 2,
+    head_dim: int = 128,
+) -> torch.Tensor:
+    """Adjoint RoPE on dQ/dK, copy of dV, packed into dqkv [n_tokens, (h_q + 2 h_kv) * head_dim]."""
+    dqkv, _, _ = _rope_bwd("qkv_rope_bwd", dq_rot, dk_rot, dv_out, cos, sin, pos_ids, h_q, h_kv,
+                           head_dim, 1.0, 1.0, False)
+    return dqkv
+
+
+def qkv_rope_bwd_lora(
+    dq_rot: torch.Tensor,
+    dk_rot: torch.Tensor,
+    dv_out: torch.Tensor,
+    cos: torch.Tensor,
+    sin: torch.Tensor,
+    pos_ids: torch.Tensor,
+    scale_q: float,
+    scale_v: float,
+    h_q: int = 12,
+    h_kv: int = 2,
+    head_dim: int = 128,
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """``qkv_rope_bwd`` that also returns the LoRA-delta gradients dq_lora = T(dQ*scale_q) and
+    dv_lora = T(dV*scale_v) from the same launch (the reference computes them with two torch
+    elementwise ops, ops.py:144-147 and ops.py:972-973)."""
+    return _rope_bwd("qkv_rope_bwd_lora", dq_rot, dk_rot, dv_out, cos, sin, pos_ids, h_q, h_kv,
+                     head_dim, scale_q, scale_v, True)
+
+
+# ---------------------------------------------------------------------------------------------
+# SwiGLU (reference: kernels.py:355-446, launchers kernels.py:801-912)
+# ---------------------------------------------------------------------------------------------
+
+
+def mlp_glu_fwd(gate_or_gu: torch.Tensor, up: torch.Tensor | None = None) -> torch.Tensor:
+    """silu(gate) * up over a fused [gate | up] tensor (up=None) or separate gate and up."""
+    fn = "mlp_glu_fwd"
+    _require_device(fn, gate_or_gu, up)
+    dt = _dtype_code(fn, gate_or_gu.dtype)
+    if up is None:
+        orig_shape = gate_or_gu.shape
+        if orig_shape[-1] % 2:
+            raise ValueError(f"{fn}: fused [gate|up] width {orig_shape[-1]} must be even")
+        n_cols = orig_shape[-1] // 2
+        gu_2d = gate_or_gu.contiguous().view(-1, 2 * n_cols)
+        n_rows = gu_2d.shape[0]
+        out_2d = torch.empty((n_rows, n_cols), dtype=gate_or_gu.dtype, device=gate_or_gu.device)
+        base = gu_2d.data_ptr()
+        _lib.call("rus_swiglu_fwd", base, base + n_cols * gu_2d.element_size(), out_2d.data_ptr(),
+                  n_rows, n_cols, gu_2d.stride(0), gu_2d.stride(0), out_2d.stride(0), dt,
+                  _stream(gu_2d))
+        return out_2d.view(*orig_shape[:-1], n_cols)
+    orig_shape = gate_or_gu.shape
+    if up.shape != orig_shape or up.dtype != gate_or_gu.dtype:
+        raise ValueError(f"{fn}: gate and up must match in shape and dtype")
+    n_cols = orig_shape[-1]
+    gate_2d = gate_or_gu.contiguous().view(-1, n_cols)
+    up_2d = up.contiguous().view(-1, n_cols)
+    n_rows = gate_2d.shape[0]
+    out_2d = torch.empty((n_rows, n_cols), dtype=gate_or_gu.dtype, device=gate_or_gu.device)
+    _lib.call("rus_swiglu_fwd", gate_2d.data_ptr(), up_2d.data_ptr(), out_2d.data_ptr(), n_rows,
+              n_cols, gate_2d.stride(0), up_2d.stride(0), out_2d.stride(0), dt, _stream(gate_2d))
+    return out_2d.view(orig_shape)
+
+
+def mlp_glu_bwd(
+    dout: torch.Tensor,
+    gate_or_gu: torch.Tensor,
+    up: torch.Tensor | None = None,
+    dgu_out: torch.Tensor | None = None,
+) -> torch.Tensor | tuple[torch.Tensor, torch.Tensor]:
+    """SwiGLU backward. Fused (up=None): writes [d_gate | d_up] into ``dgu_out``, or in place over
+    ``gate_or_gu`` when ``dgu_out`` is None, and returns it as [rows, 2*n_cols]. Separate: returns
+    (d_gate, d_up) as new tensors."""
+    fn = "mlp_glu_bwd"
+    _require_device(fn, dout, gate_or_gu, up, dgu_out)
+    dt = _dtype_code(fn, gate_or_gu.dtype)
+    if dout.dtype != gate_or_gu.dtype:
+        raise ValueError(f"{fn}: dout dtype {dout.dtype} != activations {gate_or_gu.dtype}")
+    if up is None:
+        n_cols = dout.shape[-1]
+        dout_2d = dout.contiguous().view(-1, n_cols)
+        gu_2d = gate_or_gu.view(-1, 2 * n_cols)  # in place needs the caller's own storage
+        n_rows = gu_2d.shape[0]
+        if dout_2d.shape[0] != n_rows:
+            raise ValueError(f"{fn}: dout has {dout_2d.shape[0]} rows, [gate|up] has {n_rows}")
+        dgu_2d = gu_2d if dgu_out is None else dgu_out.view(-1, 2 * n_cols)
+        if dgu_2d.dtype != gu_2d.dtype or dgu_2d.shape != gu_2d.shape:
+            raise ValueError(f"{fn}: dgu_out must match [gate|up] in shape and dtype")
+        es = gu_2d.element_size()
+        g, d = gu_2d.data_ptr(), dgu_2d.data_ptr()
+        _lib.call("rus_swiglu_bwd", dout_2d.data_ptr(), g, g + n_cols * es, d, d + n_cols * es,
+                  n_rows, n_cols, dout_2d.stride(0), gu_2d.stride(0), gu_2d.stride(0),
+                  dgu_2d.stride(0), dgu_2d.stride(0), dt, _stream(dout_2d))
+        return dgu_2d
+    orig_shape = gate_or_gu.shape
+    n_cols = orig_shape[-1]
+    dout_2d = dout.contiguous().view(-1, n_cols)
+    gate_2d = gate_or_gu.contiguous().view(-1, n_cols)
+    up_2d = up.contiguous().view(-1, n_cols)
+    n_rows = gate_2d.shape[0]
+    if up_2d.shape != gate_2d.shape or dout_2d.shape != gate_2d.shape:
+        raise ValueError(f"{fn}: dout, gate and up must match in shape")
+    dg_2d = torch.empty_like(dout_2d)
+    du_2d = torch.empty_like(dout_2d)
+    _lib.call("rus_swiglu_bwd", dout_2d.data_ptr(), gate_2d.data_ptr(), up_2d.data_ptr(),
+              dg_2d.data_ptr(), du_2d.data_ptr(), n_rows, n_cols, dout_2d.stride(0),
+              gate_2d.stride(0), up_2d.stride(0), dg_2d.stride(0), du_2d.stride(0), dt,
+              _stream(dout_2d))
+    return dg_2d.view(orig_shape), du_2d.view(orig_shape)

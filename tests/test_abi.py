@@ -1,0 +1,74 @@
+"""CPU checks of the C ABI: the library builds and loads, exports exactly the entry points that
+include/rus_amd.h declares, and rejects invalid arguments before touching the GPU."""
+
+from __future__ import annotations
+
+import re
+import subprocess
+from pathlib import Path
+
+import pytest
+
+from rus_amd import _lib
+
+REPO = Path(__file__).resolve().parents[1]
+HEADER = REPO / "include" / "rus_amd.h"
+
+
+def _declared() -> set[str]:
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return set(re.findall(r"\b(rus_[a-z0-9_]+)\s*\(", text))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    assert lib.rus_abi_version() == _lib.ABI_VERSION
+    out = subprocess.run(["nm", "-D", "--defined-only", str(_lib.LIB_PATH)], capture_output=True,
+                         text=True, check=True).stdout
+    exported = set(re.findall(r" T (rus_[a-z0-9_]+)$", out, flags=re.M))
+    declared = _declared()
+    assert declared, "no declarations parsed from include/rus_amd.h"
+    assert declared == exported
+    # every declared compute entry point has a ctypes signature
+    assert declared - {"rus_last_error", "rus_abi_version"} == set(_lib.SIGNATURES)
+
+
+def test_header_compiles_as_c():
+    src = '#include "rus_amd.h"\nint main(void){return RUS_OK;}\n'
+    res = subprocess.run(["gcc", "-std=c99", "-Wall", "-Werror", f"-I{REPO / 'include'}", "-x", "c",
+                          "-", "-o", "/dev/null"], input=src, capture_output=True, text=True)
+    assert res.returncode == 0, res.stderr
+
+
+@pytest.mark.parametrize(
+    "name,args,msg",
+    [
+        # n_bytes beyond 2^31
+        ("rus_nf4_dequant", (1, 1, 1, 1, 0.0, 0.0, 0.0, 0, 0, 0, 0, 1 << 31, 1, 1, 64, 256, 16, None),
+         "n_bytes"),
+        # blocksize not a power of two
+        ("rus_nf4_dequant", (16, 16, 16, 16, 0.0, 0.0, 0.0, 64, 64, 0, 0, 64, 4, 1, 48, 256, 16, None),
+         "blocksize"),
+        # absmax too short for the bytes
+        ("rus_nf4_dequant", (16, 16, 16, 16, 0.0, 0.0, 0.0, 64, 64, 0, 0, 64, 1, 1, 64, 256, 16, None),
+         "absmax"),
+        # stride smaller than the row
+        ("rus_rmsnorm_fwd", (16, None, 16, 0, None, 16, 16, 4, 128, 64, 1e-6, 0, None), "stride"),
+        # bad dtype
+        ("rus_rmsnorm_bwd", (16, 16, 16, 0, 16, None, 16, 4, 128, 128, 7, None), "dtype"),
+        # head_dim not a multiple of 16
+        ("rus_qkv_lora_rope_fwd", (16, None, None, 16, 16, 16, 16, 16, 16, 4, 2000, 0, 0, 120, 8,
+                                   1.0, 1.0, 12, 2, 120, None, 0, None), "head_dim"),
+        # only one of the LoRA gradients requested
+        ("rus_qkv_rope_bwd", (16, 16, 16, 16, 16, 16, 16, 16, None, 4, 2048, 128, 8, 1.0, 1.0, 12,
+                              2, 128, None, 0, None), "both"),
+        ("rus_swiglu_fwd", (16, 16, 16, 4, 100, 50, 100, 100, 0, None), "stride"),
+        ("rus_swiglu_bwd", (16, 16, 16, 16, 16, 1 << 20, 1 << 12, 1 << 12, 1 << 12, 1 << 12,
+                            1 << 12, 1 << 12, 0, None), "2\\^31"),
+    ],
+)
+def test_invalid_arguments_are_rejected_on_the_host(name, args, msg):
+    # Pointer values here are never dereferenced: validation fails before any launch.
+    with pytest.raises(RuntimeError, match=msg):
+        _lib.call(name, *args)
