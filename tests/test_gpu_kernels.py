@@ -118,10 +118,22 @@ def test_rmsnorm_fwd_bwd(dtype, wdtype, has_residual, shape):
     dx_r = ref.rms_norm_bwd(dy, h_r, w, rstd_r, dresidual=dres)
 
     assert torch.equal(h.cpu(), h_r)  # T(x + res): one correctly rounded add, exact
-    assert torch.allclose(rstd.cpu(), rstd_r, rtol=2e-6, atol=0)  # fp32 sum order only
+    assert torch.allclose(rstd.cpu(), rstd_r.reshape(-1), rtol=2e-6, atol=0)  # fp32 sum order only
     if dtype == torch.float16:
-        assert torch.all(_ulp_ok(y.cpu(), y_r))  # tolerance: 1 fp16 ulp
-        assert torch.all(_ulp_ok(dx.cpu(), dx_r))
+        # y = T(T(h*rstd) * w) rounds to fp16 twice; rstd may differ in its last fp32 bit (sum
+        # order), so allow one fp16 ulp at each rounding: ulp(y) + ulp(T(h*rstd)) * |w|.
+        n_r = (h_r.float() * rstd_r.unsqueeze(-1)).half().float()
+        tol_y = ref.fp16_ulp(y_r) + ref.fp16_ulp(n_r) * w.float().abs()
+        assert torch.all((y.cpu().float() - y_r.float()).abs() <= tol_y)
+        assert (y.cpu() == y_r).float().mean() > 0.99  # and nearly all bit-exact
+        # dx = T((g - xhat*c)*rstd + dres): one fp16 ulp plus an fp32 budget for the reduction
+        # order of c under cancellation (1e-5 relative to the terms being cancelled).
+        xh = h_r.float() * rstd_r.unsqueeze(-1)
+        gw = w.float() * dy.float()
+        c = (xh * gw).sum(-1, keepdim=True) / shape[-1]
+        tol_dx = ref.fp16_ulp(dx_r) + 1e-5 * rstd_r.unsqueeze(-1) * (gw.abs() + (xh * c).abs())
+        assert torch.all((dx.cpu().float() - dx_r.float()).abs() <= tol_dx)
+        assert (dx.cpu() == dx_r).float().mean() > 0.98
     else:
         assert torch.allclose(y.cpu(), y_r, rtol=1e-5, atol=1e-6)
         assert torch.allclose(dx.cpu(), dx_r, rtol=1e-4, atol=1e-5)
