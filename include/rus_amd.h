@@ -151,6 +151,65 @@ int rus_swiglu_bwd(const void* dout, const void* gate, const void* up, void* dga
                    int64_t stride_u, int64_t stride_dg, int64_t stride_du, int32_t dtype,
                    void* stream);
 
+/*
+ * lm_head cross-entropy, forward statistics over vocabulary rows [vocab_start, vocab_start+n_vocab)
+ * of W (weight points at row vocab_start; [n_vocab, ld_w] fp16) against hidden [n_tok, ld_h] fp16.
+ * Replaces: the forward chunk loop of solution/ops.py:217-251 (torch.mm into an fp16 logits chunk +
+ *           lm_head_piece_kernel MODE 0, solution/kernels.py:480-516). No logits are stored: for
+ * every token and every 256 vocabulary rows this writes one partial (m = max z, s = sum e^{z-m},
+ * w = sum e^{z-m} z, idx = first global index of the max) at partial row part_base + r/256 of the
+ * [*, part_stride] arrays, with z = fp16(H.W^T) (fp32 accumulation), and stores target[t] = z at
+ * the token's label when the label falls in the range. d must be a multiple of 64; rows 16-byte
+ * aligned; each operand < 4 GiB.
+ */
+int rus_lmhead_ce_fwd(const void* hidden, const void* weight, const int64_t* labels, int64_t n_tok,
+                      int64_t d, int64_t ld_h, int64_t ld_w, int64_t n_vocab, int64_t vocab_start,
+                      float* part_m, float* part_s, float* part_w, int32_t* part_idx,
+                      int64_t part_base, int64_t part_stride, float* target, void* stream);
+
+/*
+ * Merges n_parts partial rows per token and finishes the statistics.
+ * Replaces: solution/kernels.py:534-565 (lm_head_finish_kernel) plus the cross-chunk argmax of
+ *           kernels.py:494-498. lse = M + ln S, entropy = lse - W/S, nll = lse - target (0 where the
+ * label is -100), argmax = smallest vocabulary index attaining the maximum.
+ */
+int rus_lmhead_ce_combine(const float* part_m, const float* part_s, const float* part_w,
+                          const int32_t* part_idx, int64_t n_parts, int64_t part_stride,
+                          const float* target, const int64_t* labels, int64_t n_tok, float* lse,
+                          float* nll, float* entropy, int64_t* argmax, void* stream);
+
+/*
+ * Logit gradient for vocabulary rows [vocab_start, vocab_start+n_vocab):
+ *   grad_logits[t][v - vocab_start] = fp16((e^{z - lse[t]} - 1[v = label[t]]) * 2^16 / max(*denom, 1))
+ * and 0 for tokens whose label is -100; columns up to round_up(n_vocab, 64) are written (zeros past
+ * n_vocab). denom is a device scalar (float32).
+ * Replaces: lm_head_piece_kernel MODE 1 (solution/kernels.py:517-531) and its recompute GEMM
+ *           (solution/ops.py:287-319).
+ */
+int rus_lmhead_ce_grad_logits(const void* hidden, const void* weight, const int64_t* labels,
+                              const float* lse, const float* denom, int64_t n_tok, int64_t d,
+                              int64_t ld_h, int64_t ld_w, int64_t n_vocab, int64_t vocab_start,
+                              void* grad_logits, int64_t ld_g, void* stream);
+
+/*
+ * Hidden-state gradient partials: parts[s] (+)= grad_logits[:, Ks] . (W^T[:, Ks])^T over split s of
+ * the round_up(n_vocab, 64) columns, parts = [n_split][n_tok][d] fp32 (accumulate != 0 adds to the
+ * existing contents). weight_t is W^T ([d, ld_wt] fp16, K-contiguous) positioned at the same first
+ * vocabulary column as grad_logits, with zero columns up to round_up(n_vocab, 64). n_split must be
+ * ceil(K / round_up(ceil(K / n_split), 64)) for K = round_up(n_vocab, 64).
+ * Replaces: d_h_prescaled.addmm_(G, W_chunk) of solution/ops.py:320 (fp16 accumulator there).
+ */
+int rus_lmhead_ce_grad_hidden(const void* grad_logits, int64_t ld_g, const void* weight_t,
+                              int64_t ld_wt, int64_t n_tok, int64_t d, int64_t n_vocab,
+                              float* parts, int32_t n_split, int32_t accumulate, void* stream);
+
+/*
+ * out[i] = T(scale * sum_p parts[p * n_elem + i]), T = out_dtype (fp16 or fp32).
+ * Replaces: the prescale undo of solution/ops.py:337-338 (and the split-K sum).
+ */
+int rus_lmhead_dh_reduce(const float* parts, int32_t n_parts, int64_t n_elem, float scale,
+                         void* out, int32_t out_dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

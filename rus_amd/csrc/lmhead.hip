@@ -1,0 +1,694 @@
+// Vocab-tiled lm_head cross-entropy on fp16 MFMA for gfx950.
+//
+// Behaviour follows the reference's chunked lm_head (solution/ops.py:174-349 with
+// lm_head_piece_kernel / lm_head_finish_kernel, solution/kernels.py:453-565): logits are the fp16
+// rounding of H.W^T (fp32 accumulation), per token the forward keeps an online max m,
+// s = sum e^{z-m}, w = sum e^{z-m} z, the first-index argmax and the target logit, and finishes
+// lse = m + ln s, entropy = lse - w/s, nll = lse - z[label]. The backward forms
+// G = fp16((e^{z-lse} - 1[v=label]) * 2^16/denom) and dH = sum_v G[:, v] W[v, :].
+// The [N, V] logits never exist in memory. Design (CDNA4, wave64, 160 KiB LDS):
+//   * one NT GEMM mainloop (both operands K-contiguous) feeds every kernel: 256x256 block tiles,
+//     4 waves of 128x128 (4x4 v_mfma_f32_32x32x16_f16 tiles, 256 accumulators in AGPRs),
+//     K stepped by 64 through double-buffered LDS (2 x 64 KiB) with one barrier per step;
+//     LDS rows are XOR-swizzled per 16-byte chunk so both the 16-byte stores and the MFMA
+//     operand reads are bank-conflict free;
+//   * blocks are numbered XCD-aware: block b runs on XCD b%8, and each XCD receives a contiguous
+//     range of (vocab tile, token tile) work with token tiles fastest, so the blocks that share a
+//     W tile run on one XCD at the same time and read it from HBM once into that XCD's L2;
+//   * forward statistics: W is the M operand and H the N operand, so each lane's accumulators
+//     hold 64 vocabulary entries of one token: max/argmax/sum-exp are in-register reductions,
+//     one lane-pair exchange and one LDS merge of the two vocab halves; each block writes one
+//     (m, s, w, argmax) partial per token per 256 vocab rows, merged by a small combine kernel;
+//   * backward: a second pass of the same mainloop turns each logit tile into fp16 G, staged
+//     through LDS for 16-byte coalesced stores, then a split-K GEMM G . (W^T) accumulates dH in
+//     fp32 partials that a reduction kernel sums (the reference accumulates in fp16, ops.py:320).
+#include <math.h>
+
+#include "common.h"
+
+namespace rus {
+namespace {
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kBM = 256, kBN = 256, kBK = 64;
+constexpr int kThreads = 256;
+constexpr int kWM = 128, kWN = 128;
+constexpr int kMT = kWM / 32, kNT = kWN / 32;
+constexpr int kTileBytes = kBM * kBK * 2;  // one operand, one stage: 32 KiB
+constexpr int kSmemBytes = 4 * kTileBytes;  // 2 stages x (A, B) = 128 KiB
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kPrescale = 65536.0f;  // solution/ops.py:171
+
+struct GemmArgs {
+  const f16* A;  // [M, lda], rows K-contiguous
+  const f16* B;  // [N, ldb]
+  int64_t lda, ldb;
+  int M, N;
+  int K;            // multiple of kBK
+  int k_per_split;  // multiple of kBK
+  int splits;
+  int tiles_m, tiles_n;
+};
+
+struct Tile {
+  int m0, n0, split;
+};
+
+// Byte offset of 16-byte chunk `chunk` (0..7) of row `row` in a [256][64] fp16 LDS tile.
+__device__ __forceinline__ uint32_t lds_off(int row, int chunk) {
+  return row * (kBK * 2) + ((chunk ^ (row & 7) ^ ((row >> 3) & 1)) << 4);
+}
+
+__device__ __forceinline__ bool tile_of(const GemmArgs& g, Tile& t) {
+  const int total = g.tiles_m * g.tiles_n * g.splits;
+  const int per_xcd = (total + 7) >> 3;
+  const int local = blockIdx.x >> 3;
+  const int work = (blockIdx.x & 7) * per_xcd + local;
+  if (local >= per_xcd || work >= total) return false;
+  const int tn = work % g.tiles_n;
+  const int rest = work / g.tiles_n;
+  t.m0 = (rest % g.tiles_m) * kBM;
+  t.split = rest / g.tiles_m;
+  t.n0 = tn * kBN;
+  return true;
+}
+
+// One LDS stage (kBK of K) of MFMAs for this wave's 128x128 tile.
+__device__ __forceinline__ void mma_stage(const char* sa, int arow, int brow, int half, int asw,
+                                          int bsw, f32x16 (&acc)[kMT][kNT]) {
+  const char* sb = sa + kTileBytes;
+#pragma unroll
+  for (int kk = 0; kk < kBK / 16; ++kk) {
+    const int ch = kk * 2 + half;
+    const char* pa = sa + arow * (kBK * 2) + ((ch ^ asw) << 4);
+    const char* pb = sb + brow * (kBK * 2) + ((ch ^ bsw) << 4);
+    f16x8 fa[kMT], fb[kNT];
+#pragma unroll
+    for (int mt = 0; mt < kMT; ++mt) fa[mt] = *reinterpret_cast<const f16x8*>(pa + mt * 32 * (kBK * 2));
+#pragma unroll
+    for (int nt = 0; nt < kNT; ++nt) fb[nt] = *reinterpret_cast<const f16x8*>(pb + nt * 32 * (kBK * 2));
+#pragma unroll
+    for (int mt = 0; mt < kMT; ++mt)
+#pragma unroll
+      for (int nt = 0; nt < kNT; ++nt)
+        acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[mt], fb[nt], acc[mt][nt], 0, 0, 0);
+  }
+}
+
+// acc[mt][nt] += A[m0 + wm*128 + mt*32 .. +32, k] . B[n0 + wn*128 + nt*32 .. +32, k]^T over the
+// split's K range. Accumulator layout (v_mfma_f32_32x32x16_f16): register r of lane l holds
+// row 8*(r/4) + 4*(l/32) + r%4, column l%32 of the 32x32 tile.
+//
+// Register budget (one wave per SIMD, 512 registers): 256 accumulators, 64 for the next stage's
+// global loads, 32 for MFMA operands; addresses are kept small: global loads use a uniform base
+// plus a 32-bit byte offset per row (the host checks that every operand is < 4 GiB), and LDS
+// addresses are one per-lane base plus immediate offsets, because the swizzle only depends on
+// row bits 0..3, which the 32-row steps between i / mt do not change.
+__device__ __forceinline__ void mainloop(const GemmArgs& g, const Tile& tl, char* smem,
+                                         f32x16 (&acc)[kMT][kNT]) {
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int kb = tl.split * g.k_per_split;
+  const int ke = min(kb + g.k_per_split, g.K);
+  const int KT = ke > kb ? (ke - kb) / kBK : 0;
+
+  const int lrow = t >> 3, lch = t & 7;
+  uint32_t oa[8], ob[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    // Rows past the matrix edge re-read the last row: finite values the epilogues discard.
+    const int ra_ = min(tl.m0 + lrow + 32 * i, g.M - 1);
+    const int rb_ = min(tl.n0 + lrow + 32 * i, g.N - 1);
+    oa[i] = static_cast<uint32_t>((ra_ * g.lda + kb + lch * 8) * 2);
+    ob[i] = static_cast<uint32_t>((rb_ * g.ldb + kb + lch * 8) * 2);
+  }
+  const char* gA = reinterpret_cast<const char*>(g.A);
+  const char* gB = reinterpret_cast<const char*>(g.B);
+  const uint32_t so = lds_off(lrow, lch);  // store offset of row lrow; row lrow + 32i adds 4096*i
+#pragma unroll
+  for (int mt = 0; mt < kMT; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < kNT; ++nt) acc[mt][nt] = f32x16{};
+
+  u32x4 ra[8], rb[8];
+  if (KT > 0) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      ra[i] = *reinterpret_cast<const u32x4*>(gA + oa[i]);
+      rb[i] = *reinterpret_cast<const u32x4*>(gB + ob[i]);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      *reinterpret_cast<u32x4*>(smem + so + 4096 * i) = ra[i];
+      *reinterpret_cast<u32x4*>(smem + kTileBytes + so + 4096 * i) = rb[i];
+    }
+  }
+  __syncthreads();
+
+  const int arow = wm * kWM + (lane & 31);
+  const int brow = wn * kWN + (lane & 31);
+  const int half = lane >> 5;
+  const int asw = (arow & 7) ^ ((arow >> 3) & 1);
+  const int bsw = (brow & 7) ^ ((brow >> 3) & 1);
+  // Steady state: load stage kt+1 into registers, compute stage kt, store stage kt+1, barrier.
+  for (int kt = 0; kt + 1 < KT; ++kt) {
+    const char* nA = gA + (kt + 1) * (kBK * 2);
+    const char* nB = gB + (kt + 1) * (kBK * 2);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      ra[i] = *reinterpret_cast<const u32x4*>(nA + oa[i]);
+      rb[i] = *reinterpret_cast<const u32x4*>(nB + ob[i]);
+    }
+    // Keep the next stage's loads ahead of this stage's MFMAs so their latency is hidden.
+    __builtin_amdgcn_sched_barrier(0);
+    mma_stage(smem + (kt & 1) * 2 * kTileBytes, arow, brow, half, asw, bsw, acc);
+    __builtin_amdgcn_sched_barrier(0);
+    char* da = smem + ((kt + 1) & 1) * 2 * kTileBytes;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      *reinterpret_cast<u32x4*>(da + so + 4096 * i) = ra[i];
+      *reinterpret_cast<u32x4*>(da + kTileBytes + so + 4096 * i) = rb[i];
+    }
+    __syncthreads();
+  }
+  if (KT > 0) mma_stage(smem + ((KT - 1) & 1) * 2 * kTileBytes, arow, brow, half, asw, bsw, acc);
+  __syncthreads();  // the epilogues reuse the LDS
+}
+
+__device__ __forceinline__ float round16(float x) {
+  return static_cast<float>(static_cast<_Float16>(x));
+}
+
+__device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// ---------------------------------------------------------------------------------------------
+// Forward statistics: A = W rows (vocab), B = H rows (tokens).
+// ---------------------------------------------------------------------------------------------
+
+struct StatsParams {
+  const int64_t* labels;
+  float* part_m;
+  float* part_s;
+  float* part_w;
+  int32_t* part_idx;
+  float* target;
+  int64_t part_stride;  // entries per partial row (>= n_tok)
+  int part_base;        // partial row of A's first 256-row tile
+  int vocab_start;      // global vocabulary index of A's row 0
+};
+
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))) void
+lmhead_stats_kernel(GemmArgs g, StatsParams p) {
+  __shared__ __attribute__((aligned(16))) char smem[kSmemBytes];
+  Tile tl;
+  if (!tile_of(g, tl)) return;
+  f32x16 acc[kMT][kNT];
+  mainloop(g, tl, smem, acc);
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave >> 1, wn = wave & 1, h = lane >> 5;
+  const int vrow0 = tl.m0 + wm * kWM;  // local vocab row of this wave's first accumulator row
+  const bool full = tl.m0 + kBM <= g.M;
+  float rm[kNT], rs[kNT], rw[kNT];
+  int ri[kNT];
+#pragma unroll
+  for (int nt = 0; nt < kNT; ++nt) {
+    const int tok = tl.n0 + wn * kWN + nt * 32 + (lane & 31);
+    int lab = -1;
+    if (tok < g.N) {
+      const int64_t l = p.labels[tok] - p.vocab_start;
+      lab = (l >= 0 && l < g.M) ? static_cast<int>(l) : -1;
+    }
+    float m = -INFINITY, tgt = 0.0f;
+    int idx = 0x7fffffff;
+#pragma unroll
+    for (int mt = 0; mt < kMT; ++mt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = vrow0 + mt * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+        const float z = round16(acc[mt][nt][r]);
+        if ((full || row < g.M) && z > m) {  // rows ascend: strict > keeps the first index
+          m = z;
+          idx = row;
+        }
+        tgt = row == lab ? z : tgt;
+      }
+    // The lane pair (l, l^32) holds the two interleaved halves of the wave's 128 rows.
+    const float m2 = __shfl_xor(m, 32, kWave);
+    const int i2 = __shfl_xor(idx, 32, kWave);
+    if (m2 > m || (m2 == m && i2 < idx)) {
+      m = m2;
+      idx = i2;
+    }
+    float s = 0.0f, w = 0.0f;
+    if (m > -INFINITY) {
+      const float mb = m * kLog2e;
+#pragma unroll
+      for (int mt = 0; mt < kMT; ++mt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int row = vrow0 + mt * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+          if (full || row < g.M) {
+            const float z = round16(acc[mt][nt][r]);
+            const float e = exp2_fast(__builtin_fmaf(z, kLog2e, -mb));
+            s += e;
+            w += e * z;
+          }
+        }
+    }
+    s += __shfl_xor(s, 32, kWave);
+    w += __shfl_xor(w, 32, kWave);
+    rm[nt] = m;
+    rs[nt] = s;
+    rw[nt] = w;
+    ri[nt] = idx;
+    // The label's row lives in exactly one lane of one block: that lane writes the target.
+    if (lab >= vrow0 && lab < vrow0 + kWM && ((lab >> 2) & 1) == h) p.target[tok] = tgt;
+  }
+
+  // Merge the two vocab halves (wm = 0, 1) of the block through LDS; wm = 0 writes the partial.
+  float* xm = reinterpret_cast<float*>(smem);  // [wn][nt*32 + lane] x (m, s, w, idx)
+  if (wm == 1 && h == 0) {
+#pragma unroll
+    for (int nt = 0; nt < kNT; ++nt) {
+      const int o = wn * kWN + nt * 32 + lane;
+      xm[o] = rm[nt];
+      xm[2 * kWN + o] = rs[nt];
+      xm[4 * kWN + o] = rw[nt];
+      reinterpret_cast<int*>(xm)[6 * kWN + o] = ri[nt];
+    }
+  }
+  __syncthreads();
+  if (wm == 0 && h == 0) {
+    const int part = p.part_base + tl.m0 / kBM;
+#pragma unroll
+    for (int nt = 0; nt < kNT; ++nt) {
+      const int tok = tl.n0 + wn * kWN + nt * 32 + lane;
+      const int o = wn * kWN + nt * 32 + lane;
+      const float mB = xm[o], sB = xm[2 * kWN + o], wB = xm[4 * kWN + o];
+      const int iB = reinterpret_cast<int*>(xm)[6 * kWN + o];
+      float m = rm[nt], s = rs[nt], w = rw[nt];
+      int idx = ri[nt];
+      const float M = fmaxf(m, mB);
+      if (M > -INFINITY) {
+        const float ca = exp2_fast((m - M) * kLog2e), cb = exp2_fast((mB - M) * kLog2e);
+        s = s * ca + sB * cb;
+        w = w * ca + wB * cb;
+      }
+      if (mB > m) idx = iB;  // the second half's rows all follow the first half's
+      m = M;
+      if (tok < g.N && idx != 0x7fffffff) {
+        const int64_t o2 = static_cast<int64_t>(part) * p.part_stride + tok;
+        p.part_m[o2] = m;
+        p.part_s[o2] = s;
+        p.part_w[o2] = w;
+        p.part_idx[o2] = idx + p.vocab_start;
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// Logit gradient: A = W rows (vocab chunk), B = H rows (tokens) -> G[token][vocab] fp16.
+// ---------------------------------------------------------------------------------------------
+
+struct GradParams {
+  const int64_t* labels;
+  const float* lse;
+  const float* denom;  // device scalar: loss denominator (clamped to >= 1 here)
+  f16* g;              // [n_tok][ld_g]
+  int64_t ld_g;
+  int kpad;            // columns written: round_up(n_vocab, 64); rows >= n_vocab get zeros
+  int vocab_start;
+};
+
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))) void
+lmhead_grad_logits_kernel(GemmArgs g, GradParams p) {
+  __shared__ __attribute__((aligned(16))) char smem[kSmemBytes];
+  Tile tl;
+  if (!tile_of(g, tl)) return;
+  f32x16 acc[kMT][kNT];
+  mainloop(g, tl, smem, acc);
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave >> 1, wn = wave & 1, h = lane >> 5;
+  const float scale_all = kPrescale / fmaxf(*p.denom, 1.0f);
+  const int vrow0 = tl.m0 + wm * kWM;
+#pragma unroll
+  for (int nt = 0; nt < kNT; ++nt) {
+    const int trow = wn * kWN + nt * 32 + (lane & 31);  // token row within the block tile
+    const int tok = tl.n0 + trow;
+    int lab = -1;
+    float scale = 0.0f, l2 = 0.0f;
+    if (tok < g.N) {
+      const int64_t lg = p.labels[tok];
+      if (lg != -100) {
+        scale = scale_all;
+        const int64_t l = lg - p.vocab_start;
+        lab = (l >= 0 && l < g.M) ? static_cast<int>(l) : -1;
+      }
+      l2 = p.lse[tok] * kLog2e;
+    }
+    // Stage as [token][vocab] fp16, 8-byte quads XOR-swizzled by row (pairs kept adjacent).
+    char* srow = smem + trow * 512;
+#pragma unroll
+    for (int mt = 0; mt < kMT; ++mt)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        f16x4 v;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int r = q * 4 + e;
+          const int row = vrow0 + mt * 32 + 8 * q + 4 * h + e;
+          const float z = round16(acc[mt][nt][r]);
+          const float pr = exp2_fast(__builtin_fmaf(z, kLog2e, -l2));
+          const float gv = (pr - (row == lab ? 1.0f : 0.0f)) * scale;
+          v[e] = static_cast<_Float16>(row < g.M ? gv : 0.0f);
+        }
+        const int col = wm * kWM + mt * 32 + 8 * q + 4 * h;  // vocab column within the tile
+        const int pq = (col >> 2) ^ ((trow & 31) << 1);
+        *reinterpret_cast<f16x4*>(srow + pq * 8) = v;
+      }
+  }
+  __syncthreads();
+  const int t = threadIdx.x;
+  const int c = t & 31;
+#pragma unroll 4
+  for (int it = 0; it < kBN / 8; ++it) {
+    const int trow = it * 8 + (t >> 5);
+    const int tok = tl.n0 + trow;
+    const int col = tl.m0 + c * 8;
+    if (tok < g.N && col < p.kpad) {
+      const int pq = (2 * c) ^ ((trow & 31) << 1);
+      const uint4 v = *reinterpret_cast<const uint4*>(smem + trow * 512 + pq * 8);
+      *reinterpret_cast<uint4*>(p.g + static_cast<int64_t>(tok) * p.ld_g + col) = v;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// Hidden gradient: A = G rows (tokens), B = W^T rows (hidden dims), split-K over vocab.
+// ---------------------------------------------------------------------------------------------
+
+struct StoreParams {
+  float* parts;  // [splits][M][N] fp32
+  int accumulate;
+};
+
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))) void
+lmhead_grad_hidden_kernel(GemmArgs g, StoreParams p) {
+  __shared__ __attribute__((aligned(16))) char smem[kSmemBytes];
+  Tile tl;
+  if (!tile_of(g, tl)) return;
+  f32x16 acc[kMT][kNT];
+  mainloop(g, tl, smem, acc);
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave >> 1, wn = wave & 1, h = lane >> 5;
+  float* base = p.parts + static_cast<int64_t>(tl.split) * g.M * g.N;
+#pragma unroll
+  for (int nt = 0; nt < kNT; ++nt) {
+    const int col = tl.n0 + wn * kWN + nt * 32 + (lane & 31);
+    if (col >= g.N) continue;
+#pragma unroll
+    for (int mt = 0; mt < kMT; ++mt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = tl.m0 + wm * kWM + mt * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+        if (row < g.M) {
+          float* dst = base + static_cast<int64_t>(row) * g.N + col;
+          *dst = p.accumulate ? *dst + acc[mt][nt][r] : acc[mt][nt][r];
+        }
+      }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// Combine partial statistics (one lane per token, four waves over the partials) and finish.
+// ---------------------------------------------------------------------------------------------
+
+__global__ __launch_bounds__(256) void lmhead_combine_kernel(
+    const float* __restrict__ pm, const float* __restrict__ ps, const float* __restrict__ pw,
+    const int32_t* __restrict__ pi, int n_parts, int64_t stride, const float* __restrict__ target,
+    const int64_t* __restrict__ labels, int n_tok, float* __restrict__ lse,
+    float* __restrict__ nll, float* __restrict__ ent, int64_t* __restrict__ amax) {
+  __shared__ float sm[4][64], ss[4][64], sw[4][64];
+  __shared__ int si[4][64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int tok = blockIdx.x * 64 + lane;
+  float M = -INFINITY, S = 0.0f, W = 0.0f;
+  int I = 0x7fffffff;
+  if (tok < n_tok) {
+    for (int q = wave; q < n_parts; q += 4) {
+      const int64_t o = static_cast<int64_t>(q) * stride + tok;
+      const float m = pm[o], s = ps[o], w = pw[o];
+      const int i = pi[o];
+      if (m > M) {
+        const float c = exp2_fast((M - m) * kLog2e);
+        S = S * c + s;
+        W = W * c + w;
+        M = m;
+        I = i;
+      } else if (m > -INFINITY) {
+        const float c = exp2_fast((m - M) * kLog2e);
+        S = S + s * c;
+        W = W + w * c;
+        if (m == M && i < I) I = i;
+      }
+    }
+  }
+  sm[wave][lane] = M;
+  ss[wave][lane] = S;
+  sw[wave][lane] = W;
+  si[wave][lane] = I;
+  __syncthreads();
+  if (wave != 0 || tok >= n_tok) return;
+  M = sm[0][lane];
+  for (int k = 1; k < 4; ++k) M = fmaxf(M, sm[k][lane]);
+  S = 0.0f;
+  W = 0.0f;
+  I = 0x7fffffff;
+  for (int k = 0; k < 4; ++k) {
+    const float m = sm[k][lane];
+    if (m > -INFINITY) {
+      const float c = exp2_fast((m - M) * kLog2e);
+      S += ss[k][lane] * c;
+      W += sw[k][lane] * c;
+      if (m == M && si[k][lane] < I) I = si[k][lane];
+    }
+  }
+  const float L = M + logf(S);
+  lse[tok] = L;
+  ent[tok] = L - W / S;
+  nll[tok] = labels[tok] != -100 ? L - target[tok] : 0.0f;
+  amax[tok] = I;
+}
+
+// out[i] = T( scale * sum_p parts[p][i] ), four elements per thread (16-byte accesses when every
+// partial starts 16-byte aligned, i.e. n % 4 == 0).
+template <typename T, bool VEC>
+__global__ __launch_bounds__(256) void dh_reduce_kernel(const float* __restrict__ parts,
+                                                        int n_parts, int64_t n, float scale,
+                                                        T* __restrict__ out) {
+  const int64_t i = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) * 4;
+  if (i >= n) return;
+  if (VEC && i + 4 <= n) {
+    f32x4 s = *reinterpret_cast<const f32x4*>(parts + i);
+    for (int q = 1; q < n_parts; ++q) s += *reinterpret_cast<const f32x4*>(parts + q * n + i);
+    float o[4] = {s[0] * scale, s[1] * scale, s[2] * scale, s[3] * scale};
+    store_from_f32<T, 4>(out + i, o);
+  } else {
+    for (int64_t j = i; j < n && j < i + 4; ++j) {
+      float s = parts[j];
+      for (int q = 1; q < n_parts; ++q) s += parts[q * n + j];
+      out[j] = static_cast<T>(s * scale);
+    }
+  }
+}
+
+int launch_grid(const GemmArgs& g) {
+  const int total = g.tiles_m * g.tiles_n * g.splits;
+  return 8 * ((total + 7) / 8);
+}
+
+int check_operand(const char* fn, const void* p, int64_t ld, const char* name) {
+  if (!p) return fail(RUS_ERR_INVALID, "%s: %s is null", fn, name);
+  if (!aligned(p, 16) || ld % 8)
+    return fail(RUS_ERR_INVALID, "%s: %s must be 16-byte aligned with a row stride multiple of 8",
+                fn, name);
+  return RUS_OK;
+}
+
+}  // namespace
+}  // namespace rus
+
+using namespace rus;
+
+extern "C" int rus_lmhead_ce_fwd(const void* hidden, const void* weight, const int64_t* labels,
+                                 int64_t n_tok, int64_t d, int64_t ld_h, int64_t ld_w,
+                                 int64_t n_vocab, int64_t vocab_start, float* part_m,
+                                 float* part_s, float* part_w, int32_t* part_idx,
+                                 int64_t part_base, int64_t part_stride, float* target,
+                                 void* stream) {
+  const char* fn = "rus_lmhead_ce_fwd";
+  if (n_tok < 0 || n_tok >= (1 << 30) || n_vocab < 0 || n_vocab >= (1 << 30) || d <= 0 ||
+      d % kBK || vocab_start < 0 || vocab_start + n_vocab >= (int64_t(1) << 31))
+    return fail(RUS_ERR_INVALID,
+                "%s: bad sizes n_tok=%lld n_vocab=%lld d=%lld (d must be a multiple of %d)", fn,
+                (long long)n_tok, (long long)n_vocab, (long long)d, kBK);
+  if (n_tok == 0 || n_vocab == 0) return RUS_OK;
+  if (ld_h < d || ld_w < d) return fail(RUS_ERR_INVALID, "%s: row strides smaller than d", fn);
+  if (int e = check_operand(fn, hidden, ld_h, "hidden")) return e;
+  if (int e = check_operand(fn, weight, ld_w, "weight")) return e;
+  if (!labels || !part_m || !part_s || !part_w || !part_idx || !target || part_base < 0 ||
+      part_stride < n_tok)
+    return fail(RUS_ERR_INVALID, "%s: null output or bad partial layout", fn);
+  GemmArgs g;
+  g.A = static_cast<const f16*>(weight);
+  g.lda = ld_w;
+  g.M = static_cast<int>(n_vocab);
+  g.B = static_cast<const f16*>(hidden);
+  g.ldb = ld_h;
+  g.N = static_cast<int>(n_tok);
+  g.K = static_cast<int>(d);
+  g.k_per_split = g.K;
+  g.splits = 1;
+  g.tiles_m = (g.M + kBM - 1) / kBM;
+  g.tiles_n = (g.N + kBN - 1) / kBN;
+  StatsParams p{labels,      part_m,      part_s, part_w, part_idx, target, part_stride,
+                static_cast<int>(part_base), static_cast<int>(vocab_start)};
+  hipLaunchKernelGGL(lmhead_stats_kernel, dim3(launch_grid(g)), dim3(kThreads), 0,
+                     static_cast<hipStream_t>(stream), g, p);
+  return check_launch(fn);
+}
+
+extern "C" int rus_lmhead_ce_combine(const float* part_m, const float* part_s, const float* part_w,
+                                     const int32_t* part_idx, int64_t n_parts,
+                                     int64_t part_stride, const float* target,
+                                     const int64_t* labels, int64_t n_tok, float* lse,
+                                     float* nll, float* entropy, int64_t* argmax, void* stream) {
+  const char* fn = "rus_lmhead_ce_combine";
+  if (n_tok < 0 || n_tok >= (1 << 30) || n_parts <= 0 || n_parts >= (1 << 30) ||
+      part_stride < n_tok)
+    return fail(RUS_ERR_INVALID, "%s: bad sizes", fn);
+  if (n_tok == 0) return RUS_OK;
+  if (!part_m || !part_s || !part_w || !part_idx || !target || !labels || !lse || !nll ||
+      !entropy || !argmax)
+    return fail(RUS_ERR_INVALID, "%s: null pointer argument", fn);
+  const dim3 grid(static_cast<unsigned>((n_tok + 63) / 64));
+  hipLaunchKernelGGL(lmhead_combine_kernel, grid, dim3(256), 0, static_cast<hipStream_t>(stream),
+                     part_m, part_s, part_w, part_idx, static_cast<int>(n_parts), part_stride,
+                     target, labels, static_cast<int>(n_tok), lse, nll, entropy, argmax);
+  return check_launch(fn);
+}
+
+extern "C" int rus_lmhead_ce_grad_logits(const void* hidden, const void* weight,
+                                         const int64_t* labels, const float* lse,
+                                         const float* denom, int64_t n_tok, int64_t d,
+                                         int64_t ld_h, int64_t ld_w, int64_t n_vocab,
+                                         int64_t vocab_start, void* grad_logits, int64_t ld_g,
+                                         void* stream) {
+  const char* fn = "rus_lmhead_ce_grad_logits";
+  if (n_tok < 0 || n_tok >= (1 << 30) || n_vocab < 0 || n_vocab >= (1 << 30) || d <= 0 ||
+      d % kBK || vocab_start < 0 || vocab_start + n_vocab >= (int64_t(1) << 31))
+    return fail(RUS_ERR_INVALID, "%s: bad sizes (d must be a multiple of %d)", fn, kBK);
+  if (n_tok == 0 || n_vocab == 0) return RUS_OK;
+  const int64_t kpad = (n_vocab + kBK - 1) / kBK * kBK;
+  if (ld_h < d || ld_w < d || ld_g < kpad)
+    return fail(RUS_ERR_INVALID, "%s: row strides too small (ld_g must be >= %lld)", fn,
+                (long long)kpad);
+  if (int e = check_operand(fn, hidden, ld_h, "hidden")) return e;
+  if (int e = check_operand(fn, weight, ld_w, "weight")) return e;
+  if (int e = check_operand(fn, grad_logits, ld_g, "grad_logits")) return e;
+  if (!labels || !lse || !denom) return fail(RUS_ERR_INVALID, "%s: null pointer argument", fn);
+  GemmArgs g;
+  g.A = static_cast<const f16*>(weight);
+  g.lda = ld_w;
+  g.M = static_cast<int>(n_vocab);
+  g.B = static_cast<const f16*>(hidden);
+  g.ldb = ld_h;
+  g.N = static_cast<int>(n_tok);
+  g.K = static_cast<int>(d);
+  g.k_per_split = g.K;
+  g.splits = 1;
+  g.tiles_m = (g.M + kBM - 1) / kBM;
+  g.tiles_n = (g.N + kBN - 1) / kBN;
+  GradParams p{labels, lse, denom, static_cast<f16*>(grad_logits), ld_g, static_cast<int>(kpad),
+               static_cast<int>(vocab_start)};
+  hipLaunchKernelGGL(lmhead_grad_logits_kernel, dim3(launch_grid(g)), dim3(kThreads), 0,
+                     static_cast<hipStream_t>(stream), g, p);
+  return check_launch(fn);
+}
+
+extern "C" int rus_lmhead_ce_grad_hidden(const void* grad_logits, int64_t ld_g,
+                                         const void* weight_t, int64_t ld_wt, int64_t n_tok,
+                                         int64_t d, int64_t n_vocab, float* parts,
+                                         int32_t n_split, int32_t accumulate, void* stream) {
+  const char* fn = "rus_lmhead_ce_grad_hidden";
+  if (n_tok < 0 || n_tok >= (1 << 30) || d <= 0 || d >= (1 << 30) || n_vocab < 0 ||
+      n_vocab >= (1 << 30) || n_split <= 0 || n_split > 64)
+    return fail(RUS_ERR_INVALID, "%s: bad sizes or n_split=%d (1..64)", fn, n_split);
+  if (n_tok == 0) return RUS_OK;
+  const int64_t kpad = (n_vocab + kBK - 1) / kBK * kBK;
+  if (ld_g < kpad || ld_wt < kpad)
+    return fail(RUS_ERR_INVALID,
+                "%s: grad_logits / weight_t rows must hold round_up(n_vocab, 64)=%lld columns",
+                fn, (long long)kpad);
+  if (int e = check_operand(fn, grad_logits, ld_g, "grad_logits")) return e;
+  if (int e = check_operand(fn, weight_t, ld_wt, "weight_t")) return e;
+  if (!parts) return fail(RUS_ERR_INVALID, "%s: parts is null", fn);
+  if (kpad == 0) return RUS_OK;
+  GemmArgs g;
+  g.A = static_cast<const f16*>(grad_logits);
+  g.lda = ld_g;
+  g.M = static_cast<int>(n_tok);
+  g.B = static_cast<const f16*>(weight_t);
+  g.ldb = ld_wt;
+  g.N = static_cast<int>(d);
+  g.K = static_cast<int>(kpad);
+  const int64_t per = (kpad + n_split - 1) / n_split;
+  g.k_per_split = static_cast<int>((per + kBK - 1) / kBK * kBK);
+  g.splits = static_cast<int>((kpad + g.k_per_split - 1) / g.k_per_split);
+  if (g.splits != n_split)
+    return fail(RUS_ERR_INVALID, "%s: n_split=%d does not divide K=%lld into 64-wide pieces", fn,
+                n_split, (long long)kpad);
+  g.tiles_m = (g.M + kBM - 1) / kBM;
+  g.tiles_n = (g.N + kBN - 1) / kBN;
+  StoreParams p{parts, accumulate};
+  hipLaunchKernelGGL(lmhead_grad_hidden_kernel, dim3(launch_grid(g)), dim3(kThreads), 0,
+                     static_cast<hipStream_t>(stream), g, p);
+  return check_launch(fn);
+}
+
+extern "C" int rus_lmhead_dh_reduce(const float* parts, int32_t n_parts, int64_t n_elem,
+                                    float scale, void* out, int32_t out_dtype, void* stream) {
+  const char* fn = "rus_lmhead_dh_reduce";
+  if (n_parts <= 0 || n_elem < 0 || (out_dtype != RUS_DTYPE_F16 && out_dtype != RUS_DTYPE_F32))
+    return fail(RUS_ERR_INVALID, "%s: bad arguments", fn);
+  if (n_elem == 0) return RUS_OK;
+  if (!parts || !out || !aligned(parts, 16) || !aligned(out, 16))
+    return fail(RUS_ERR_INVALID, "%s: parts/out must be non-null and 16-byte aligned", fn);
+  const dim3 grid(static_cast<unsigned>((n_elem + 1023) / 1024));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const bool vec = n_elem % 4 == 0;
+  if (out_dtype == RUS_DTYPE_F16) {
+    if (vec)
+      hipLaunchKernelGGL((dh_reduce_kernel<f16, true>), grid, dim3(256), 0, st, parts, n_parts,
+                         n_elem, scale, static_cast<f16*>(out));
+    else
+      hipLaunchKernelGGL((dh_reduce_kernel<f16, false>), grid, dim3(256), 0, st, parts, n_parts,
+                         n_elem, scale, static_cast<f16*>(out));
+  } else {
+    if (vec)
+      hipLaunchKernelGGL((dh_reduce_kernel<float, true>), grid, dim3(256), 0, st, parts, n_parts,
+                         n_elem, scale, static_cast<float*>(out));
+    else
+      hipLaunchKernelGGL((dh_reduce_kernel<float, false>), grid, dim3(256), 0, st, parts, n_parts,
+                         n_elem, scale, static_cast<float*>(out));
+  }
+  return check_launch(fn);
+}

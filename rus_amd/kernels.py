@@ -24,6 +24,13 @@ __all__ = [
     "qkv_rope_bwd_lora",
     "mlp_glu_fwd",
     "mlp_glu_bwd",
+    "lm_head_ce",
+    "lm_head_ce_fwd_chunk",
+    "lm_head_ce_combine",
+    "lm_head_ce_grad_logits",
+    "lm_head_ce_grad_hidden",
+    "lm_head_dh_reduce",
+    "lm_head_weight_t",
 ]
 
 
@@ -429,3 +436,223 @@ def mlp_glu_bwd(
               gate_2d.stride(0), up_2d.stride(0), dg_2d.stride(0), du_2d.stride(0), dt,
               _stream(dout_2d))
     return dg_2d.view(orig_shape), du_2d.view(orig_shape)
+
+
+# ---------------------------------------------------------------------------------------------
+# Vocab-tiled lm_head cross-entropy on fp16 MFMA (reference: lm_head_piece_kernel /
+# lm_head_finish_kernel, kernels.py:453-565, and the chunk loops of ops.py:174-349)
+# ---------------------------------------------------------------------------------------------
+
+LM_TILE = 256  # vocabulary rows per forward partial (the kernels' block tile)
+LM_K = 64  # K granularity of the MFMA mainloop
+
+
+def _round_up(x: int, m: int) -> int:
+    return (x + m - 1) // m * m
+
+
+def lm_head_num_parts(vocab_size: int) -> int:
+    """Partial rows the forward writes for ``vocab_size`` vocabulary rows."""
+    return (vocab_size + LM_TILE - 1) // LM_TILE
+
+
+def lm_head_split_count(n_tok: int, d: int, n_vocab: int, target_blocks: int = 512) -> int:
+    """Split-K count for the hidden-gradient GEMM: enough (token, hidden) tiles x splits for two
+    workgroups per CU, each split a multiple of 64 vocabulary columns (the C ABI's rule)."""
+    kpad = _round_up(n_vocab, LM_K)
+    if kpad == 0:
+        return 1
+    tiles = max(1, -(-n_tok // 256) * -(-d // 256))
+    want = max(1, min(64, -(-target_blocks // tiles), kpad // LM_K))
+    per = _round_up(-(-kpad // want), LM_K)
+    return -(-kpad // per)
+
+
+class LMHeadPartials:
+    """Device buffers for the forward partial statistics: [n_parts, n_tok] m, s, w, idx."""
+
+    def __init__(self, n_parts: int, n_tok: int, device):
+        self.n_parts, self.n_tok = n_parts, n_tok
+        self.m = torch.empty((n_parts, n_tok), dtype=torch.float32, device=device)
+        self.s = torch.empty((n_parts, n_tok), dtype=torch.float32, device=device)
+        self.w = torch.empty((n_parts, n_tok), dtype=torch.float32, device=device)
+        self.idx = torch.empty((n_parts, n_tok), dtype=torch.int32, device=device)
+
+
+def _lm_operand(fn: str, t: torch.Tensor, d: int, name: str) -> torch.Tensor:
+    if t.dtype != torch.float16:
+        raise TypeError(f"{fn}: {name} must be fp16, got {t.dtype}")
+    if t.dim() != 2 or t.shape[1] < d:
+        raise ValueError(f"{fn}: {name} must be 2-D with {d} columns")
+    if t.stride(1) != 1 or t.stride(0) % 8 or t.data_ptr() % 16:
+        t = t.contiguous()
+    if t.shape[0] * t.stride(0) * 2 >= 1 << 32:
+        raise ValueError(f"{fn}: {name} exceeds the 4 GiB operand limit of the MFMA kernels")
+    return t
+
+
+def lm_head_ce_fwd_chunk(hidden: torch.Tensor, weight_rows: torch.Tensor, labels: torch.Tensor,
+                         vocab_start: int, parts: LMHeadPartials, target: torch.Tensor) -> None:
+    """Forward partial statistics of vocabulary rows [vocab_start, vocab_start + len(weight_rows))
+    (replaces one iteration of the reference's forward chunk loop, ops.py:217-251)."""
+    fn = "lm_head_ce_fwd_chunk"
+    _require_device(fn, hidden, weight_rows, labels, target)
+    if vocab_start % LM_TILE:
+        raise ValueError(f"{fn}: vocab_start must be a multiple of {LM_TILE}")
+    d = hidden.shape[1]
+    h = _lm_operand(fn, hidden, d, "hidden")
+    w = _lm_operand(fn, weight_rows, d, "weight")
+    n_tok, n_vocab = h.shape[0], w.shape[0]
+    part_base = vocab_start // LM_TILE
+    if part_base + lm_head_num_parts(n_vocab) > parts.n_parts or parts.n_tok != n_tok:
+        raise ValueError(f"{fn}: partial buffers too small for this chunk")
+    lab = labels.reshape(-1)
+    if lab.dtype != torch.int64 or lab.numel() != n_tok:
+        raise ValueError(f"{fn}: labels must be int64 with {n_tok} entries")
+    lab = lab.contiguous()
+    _lib.call("rus_lmhead_ce_fwd", h.data_ptr(), w.data_ptr(), lab.data_ptr(), n_tok, d,
+              h.stride(0), w.stride(0), n_vocab, vocab_start, parts.m.data_ptr(),
+              parts.s.data_ptr(), parts.w.data_ptr(), parts.idx.data_ptr(), part_base, n_tok,
+              target.data_ptr(), _stream(h))
+
+
+def lm_head_ce_combine(parts: LMHeadPartials, target: torch.Tensor, labels: torch.Tensor):
+    """(lse, nll, entropy, argmax) per token from the partials (replaces lm_head_finish_kernel,
+    kernels.py:534-565)."""
+    fn = "lm_head_ce_combine"
+    _require_device(fn, target, labels)
+    n = parts.n_tok
+    dev = target.device
+    lse = torch.empty(n, dtype=torch.float32, device=dev)
+    nll = torch.empty(n, dtype=torch.float32, device=dev)
+    ent = torch.empty(n, dtype=torch.float32, device=dev)
+    amax = torch.empty(n, dtype=torch.int64, device=dev)
+    lab = labels.reshape(-1).contiguous()
+    _lib.call("rus_lmhead_ce_combine", parts.m.data_ptr(), parts.s.data_ptr(), parts.w.data_ptr(),
+              parts.idx.data_ptr(), parts.n_parts, n, target.data_ptr(), lab.data_ptr(), n,
+              lse.data_ptr(), nll.data_ptr(), ent.data_ptr(), amax.data_ptr(), _stream(target))
+    return lse, nll, ent, amax
+
+
+def lm_head_ce_grad_logits(hidden: torch.Tensor, weight_rows: torch.Tensor, labels: torch.Tensor,
+                           lse: torch.Tensor, denom: torch.Tensor, vocab_start: int,
+                           out: torch.Tensor) -> torch.Tensor:
+    """fp16 logit gradient of one vocabulary range into ``out`` [n_tok, >= round_up(n, 64)]
+    (replaces lm_head_piece_kernel MODE 1 and its recompute GEMM, ops.py:287-319)."""
+    fn = "lm_head_ce_grad_logits"
+    _require_device(fn, hidden, weight_rows, labels, lse, denom, out)
+    d = hidden.shape[1]
+    h = _lm_operand(fn, hidden, d, "hidden")
+    w = _lm_operand(fn, weight_rows, d, "weight")
+    n_tok, n_vocab = h.shape[0], w.shape[0]
+    if out.dtype != torch.float16 or out.shape[0] != n_tok or out.stride(1) != 1:
+        raise ValueError(f"{fn}: out must be fp16 [n_tok, *] with contiguous rows")
+    if denom.dtype != torch.float32 or denom.numel() != 1:
+        raise ValueError(f"{fn}: denom must be a one-element float32 device tensor")
+    lab = labels.reshape(-1).contiguous()
+    _lib.call("rus_lmhead_ce_grad_logits", h.data_ptr(), w.data_ptr(), lab.data_ptr(),
+              lse.data_ptr(), denom.data_ptr(), n_tok, d, h.stride(0), w.stride(0), n_vocab,
+              vocab_start, out.data_ptr(), out.stride(0), _stream(h))
+    return out
+
+
+def lm_head_ce_grad_hidden(grad_logits: torch.Tensor, weight_t_cols: torch.Tensor, n_vocab: int,
+                           parts: torch.Tensor, accumulate: bool) -> None:
+    """parts[s] (+)= grad_logits . (W^T cols)^T split over vocabulary (replaces the fp16
+    ``addmm_`` accumulation of ops.py:320 with fp32 split-K partials)."""
+    fn = "lm_head_ce_grad_hidden"
+    _require_device(fn, grad_logits, weight_t_cols, parts)
+    n_tok = grad_logits.shape[0]
+    d = weight_t_cols.shape[0]
+    n_split = parts.shape[0]
+    if parts.dtype != torch.float32 or tuple(parts.shape[1:]) != (n_tok, d) or not parts.is_contiguous():
+        raise ValueError(f"{fn}: parts must be contiguous float32 [n_split, {n_tok}, {d}]")
+    for name, t in (("grad_logits", grad_logits), ("weight_t", weight_t_cols)):
+        if t.dtype != torch.float16 or t.stride(1) != 1:
+            raise ValueError(f"{fn}: {name} must be fp16 with contiguous rows")
+        if t.shape[0] * t.stride(0) * 2 >= 1 << 32:
+            raise ValueError(f"{fn}: {name} exceeds the 4 GiB operand limit of the MFMA kernels")
+    _lib.call("rus_lmhead_ce_grad_hidden", grad_logits.data_ptr(), grad_logits.stride(0),
+              weight_t_cols.data_ptr(), weight_t_cols.stride(0), n_tok, d, n_vocab,
+              parts.data_ptr(), n_split, 1 if accumulate else 0, _stream(grad_logits))
+
+
+def lm_head_dh_reduce(parts: torch.Tensor, scale: float, out_dtype=torch.float16) -> torch.Tensor:
+    """out = out_dtype(scale * sum over the leading split dimension of ``parts``)."""
+    fn = "lm_head_dh_reduce"
+    _require_device(fn, parts)
+    if parts.dtype != torch.float32 or not parts.is_contiguous():
+        raise ValueError(f"{fn}: parts must be contiguous float32")
+    out = torch.empty(parts.shape[1:], dtype=out_dtype, device=parts.device)
+    _lib.call("rus_lmhead_dh_reduce", parts.data_ptr(), parts.shape[0], out.numel(), float(scale),
+              out.data_ptr(), _dtype_code(fn, out_dtype), _stream(parts))
+    return out
+
+
+_WT_CACHE: "weakref.WeakKeyDictionary[torch.Tensor, tuple]" = None  # type: ignore[assignment]
+
+
+def lm_head_weight_t(weight: torch.Tensor) -> torch.Tensor:
+    """W^T [d, round_up(V, 64)] fp16 with zero padding columns, cached per weight tensor (the
+    lm_head is frozen in QLoRA, so this is built once; rebuilt if the weight is modified)."""
+    global _WT_CACHE
+    import weakref
+
+    if _WT_CACHE is None:
+        _WT_CACHE = weakref.WeakKeyDictionary()
+    hit = _WT_CACHE.get(weight)
+    if hit is not None and hit[0] == weight._version and hit[1].device == weight.device:
+        return hit[1]
+    V, d = weight.shape
+    wt = torch.zeros((d, _round_up(V, LM_K)), dtype=torch.float16, device=weight.device)
+    wt[:, :V].copy_(weight.detach().t())
+    _WT_CACHE[weight] = (weight._version, wt)
+    return wt
+
+
+def lm_head_ce(hidden: torch.Tensor, weight: torch.Tensor, labels: torch.Tensor,
+               num_items_in_batch=None, v_chunk: int | None = None, need_grad: bool = True,
+               weight_t: torch.Tensor | None = None):
+    """Whole vocab-tiled CE on a device-resident fp16 lm_head weight [V, d].
+
+    Returns (nll, lse, entropy, argmax, denom, dh_pre) where denom is a float32 device scalar
+    (num_items_in_batch, else the count of labels != -100, clamped to >= 1) and dh_pre the fp32
+    hidden gradient of sum(nll)/denom times 2^16 (None without need_grad). ``v_chunk`` bounds the
+    fp16 logit-gradient buffer to [n_tok, v_chunk] (default: the whole vocabulary in one pass).
+    """
+    fn = "lm_head_ce"
+    _require_device(fn, hidden, weight, labels)
+    n_tok, d = hidden.shape
+    V = weight.shape[0]
+    dev = hidden.device
+    lab = labels.reshape(-1).to(torch.int64).contiguous()
+    chunk = V if v_chunk is None else int(v_chunk)
+    if chunk <= 0 or (chunk < V and chunk % LM_TILE):
+        raise ValueError(f"{fn}: v_chunk must be a positive multiple of {LM_TILE}")
+    parts = LMHeadPartials(lm_head_num_parts(V), n_tok, dev)
+    target = torch.zeros(n_tok, dtype=torch.float32, device=dev)
+    for start in range(0, V, chunk):
+        lm_head_ce_fwd_chunk(hidden, weight[start:start + chunk], lab, start, parts, target)
+    lse, nll, ent, amax = lm_head_ce_combine(parts, target, lab)
+    if num_items_in_batch is None:
+        denom = (lab != -100).sum().to(torch.float32).clamp_(min=1.0).reshape(1)
+    elif isinstance(num_items_in_batch, torch.Tensor):
+        denom = num_items_in_batch.detach().to(device=dev, dtype=torch.float32).reshape(1).clamp(min=1.0)
+    else:
+        denom = torch.full((1,), max(float(num_items_in_batch), 1.0), dtype=torch.float32, device=dev)
+    dh_pre = None
+    if need_grad:
+        wt = weight_t if weight_t is not None else lm_head_weight_t(weight)
+        g = torch.empty((n_tok, _round_up(min(chunk, V), LM_K)), dtype=torch.float16, device=dev)
+        n_split = lm_head_split_count(n_tok, d, min(chunk, V))
+        dparts = torch.empty((n_split, n_tok, d), dtype=torch.float32, device=dev)
+        first = True
+        for start in range(0, V, chunk):
+            end = min(start + chunk, V)
+            lm_head_ce_grad_logits(hidden, weight[start:end], lab, lse, denom, start, g)
+            # A shorter last chunk may use fewer splits; it accumulates into the leading ones.
+            ns = lm_head_split_count(n_tok, d, end - start)
+            lm_head_ce_grad_hidden(g, wt[:, start:], end - start, dparts[:ns], accumulate=not first)
+            first = False
+        dh_pre = lm_head_dh_reduce(dparts, 1.0, torch.float32)
+    return nll, lse, ent, amax, denom, dh_pre
