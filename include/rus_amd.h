@@ -204,11 +204,13 @@ int rus_lmhead_ce_grad_hidden(const void* grad_logits, int64_t ld_g, const void*
                               float* parts, int32_t n_split, int32_t accumulate, void* stream);
 
 /*
- * out[i] = T(scale * sum_p parts[p * n_elem + i]), T = out_dtype (fp16 or fp32).
+ * out[i] = T(scale * (*scale_dev) * sum_p parts[p * n_elem + i]), T = out_dtype (fp16 or fp32);
+ * scale_dev is an optional device scalar (NULL = 1), e.g. the incoming loss gradient, so the
+ * caller never has to read it back to the host.
  * Replaces: the prescale undo of solution/ops.py:337-338 (and the split-K sum).
  */
 int rus_lmhead_dh_reduce(const float* parts, int32_t n_parts, int64_t n_elem, float scale,
-                         void* out, int32_t out_dtype, void* stream);
+                         const float* scale_dev, void* out, int32_t out_dtype, void* stream);
 
 #ifdef __cplusplus
 }

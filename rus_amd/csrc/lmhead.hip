@@ -492,10 +492,12 @@ __global__ __launch_bounds__(256) void lmhead_combine_kernel(
 // partial starts 16-byte aligned, i.e. n % 4 == 0).
 template <typename T, bool VEC>
 __global__ __launch_bounds__(256) void dh_reduce_kernel(const float* __restrict__ parts,
-                                                        int n_parts, int64_t n, float scale,
+                                                        int n_parts, int64_t n, float scale_h,
+                                                        const float* __restrict__ scale_d,
                                                         T* __restrict__ out) {
   const int64_t i = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) * 4;
   if (i >= n) return;
+  const float scale = scale_d ? scale_h * *scale_d : scale_h;
   if (VEC && i + 4 <= n) {
     f32x4 s = *reinterpret_cast<const f32x4*>(parts + i);
     for (int q = 1; q < n_parts; ++q) s += *reinterpret_cast<const f32x4*>(parts + q * n + i);
@@ -665,7 +667,8 @@ extern "C" int rus_lmhead_ce_grad_hidden(const void* grad_logits, int64_t ld_g,
 }
 
 extern "C" int rus_lmhead_dh_reduce(const float* parts, int32_t n_parts, int64_t n_elem,
-                                    float scale, void* out, int32_t out_dtype, void* stream) {
+                                    float scale, const float* scale_dev, void* out,
+                                    int32_t out_dtype, void* stream) {
   const char* fn = "rus_lmhead_dh_reduce";
   if (n_parts <= 0 || n_elem < 0 || (out_dtype != RUS_DTYPE_F16 && out_dtype != RUS_DTYPE_F32))
     return fail(RUS_ERR_INVALID, "%s: bad arguments", fn);
@@ -678,17 +681,17 @@ extern "C" int rus_lmhead_dh_reduce(const float* parts, int32_t n_parts, int64_t
   if (out_dtype == RUS_DTYPE_F16) {
     if (vec)
       hipLaunchKernelGGL((dh_reduce_kernel<f16, true>), grid, dim3(256), 0, st, parts, n_parts,
-                         n_elem, scale, static_cast<f16*>(out));
+                         n_elem, scale, scale_dev, static_cast<f16*>(out));
     else
       hipLaunchKernelGGL((dh_reduce_kernel<f16, false>), grid, dim3(256), 0, st, parts, n_parts,
-                         n_elem, scale, static_cast<f16*>(out));
+                         n_elem, scale, scale_dev, static_cast<f16*>(out));
   } else {
     if (vec)
       hipLaunchKernelGGL((dh_reduce_kernel<float, true>), grid, dim3(256), 0, st, parts, n_parts,
-                         n_elem, scale, static_cast<float*>(out));
+                         n_elem, scale, scale_dev, static_cast<float*>(out));
     else
       hipLaunchKernelGGL((dh_reduce_kernel<float, false>), grid, dim3(256), 0, st, parts, n_parts,
-                         n_elem, scale, static_cast<float*>(out));
+                         n_elem, scale, scale_dev, static_cast<float*>(out));
   }
   return check_launch(fn);
 }

@@ -1,0 +1,291 @@
+"""Weight, lm_head and activation residency for the fused Qwen2 stack (solution/hostload.py).
+
+* ``WeightStream`` packs each layer's seven NF4 projections into four fused segments
+  ([q|k|v], o, [gate|up], down; solution/hostload.py:159-258) in one byte buffer per layer and
+  serves fp16 weights through the gfx950 dequant kernel. Two residencies:
+    - ``resident=False`` (the reference's policy): packed layers live in pinned
+      host memory and are copied per step into two device slots on a side stream, ordered by
+      events (prefetch / wait_slot / release_slot, hostload.py:297-323);
+    - ``resident=True`` (MI355X: 28 packed layers are 0.65 GB of 288 GB HBM): packed layers stay in
+      HBM and prefetch / wait_slot / release_slot do nothing.
+  Each segment dequantises into its own fp16 workspace, so the stack dequantises a segment once
+  per layer per pass instead of re-dequantising a single shared workspace (the reference does 17
+  dequants per layer per step, hostload.py:295, 325-342; this layout needs 8).
+* ``HostHead`` holds the tied embedding / lm_head: HBM-resident with its W^T for the gradient GEMM
+  (default), or in pinned host memory streamed in vocabulary chunks through two device slots
+  (hostload.py:345-408).
+* ``InputStream`` keeps each layer's input for the backward recompute: in HBM (default) or
+  offloaded to pinned host memory with a one-ahead reverse prefetch (hostload.py:411-488, whose
+  three-ahead prefetch into a two-slot ring is always overwritten before use).
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import kernels as K
+from .quant import NF4Weight, concat_segments
+
+MAX_MLP_TOKENS = 1 << 30  # the reference chunks the MLP at 512 tokens for a 15 GB T4; not needed
+V_CHUNK_DEFAULT = 8192  # vocabulary rows per streamed lm_head chunk (hostload.py:24)
+SEGMENTS = ("qkv", "o", "gu", "down")
+
+
+class PackedNF4Segment:
+    """One fused segment of a layer's packed buffer (hostload.py:27-62), plus the absmax2 base of
+    each sub-segment (the reference assumes global super-block indexing)."""
+
+    __slots__ = ("out_features", "in_features", "packed_slice", "absmax_slice", "absmax2_slice",
+                 "offsets", "split_bytes", "absmax2_bases", "blocksize", "super_blocksize")
+
+    def __init__(self, out_features, in_features, packed_slice, absmax_slice, absmax2_slice,
+                 offsets, split_bytes, absmax2_bases, blocksize=64, super_blocksize=256):
+        self.out_features = out_features
+        self.in_features = in_features
+        self.packed_slice = packed_slice
+        self.absmax_slice = absmax_slice
+        self.absmax2_slice = absmax2_slice
+        self.offsets = offsets
+        self.split_bytes = split_bytes
+        self.absmax2_bases = absmax2_bases
+        self.blocksize = blocksize
+        self.super_blocksize = super_blocksize
+
+
+def _pinned(t: torch.Tensor) -> torch.Tensor:
+    cpu = t.detach().contiguous().cpu()
+    return cpu.pin_memory() if torch.cuda.is_available() else cpu
+
+
+class WeightStream:
+    """Packed NF4 layers served as fp16 weights through the dequant kernel."""
+
+    def __init__(self, layers, device, resident: bool = False):
+        self.device = torch.device(device)
+        self.num_layers = len(layers)
+        self.resident = resident
+        self.layer_segments: list[dict[str, PackedNF4Segment]] = []
+        self.layer_biases: list[torch.Tensor | None] = []
+        self.code2_gpu: torch.Tensor | None = None
+        packed_l, absmax_l, absmax2_l = [], [], []
+        ws_elems = {s: 0 for s in SEGMENTS}
+        for L in layers:
+            parts = {"qkv": [L.q, L.k, L.v], "o": [L.o], "gu": [L.gate, L.up], "down": [L.down]}
+            if self.code2_gpu is None:
+                self.code2_gpu = L.q.code2.to(self.device, torch.float32).contiguous()
+            biases = [L.q_bias, L.k_bias, L.v_bias]
+            self.layer_biases.append(
+                torch.cat([b.to(self.device, torch.float16) for b in biases]).contiguous()
+                if all(b is not None for b in biases) else None)
+            segs = {}
+            pb, ab, a2b = [], [], []
+            p_cur = a_cur = a2_cur = 0
+            for name in SEGMENTS:
+                fused, splits, offs, bases = concat_segments(parts[name])
+                nb, na, na2 = fused.packed.numel(), fused.absmax.numel(), fused.absmax2.numel()
+                segs[name] = PackedNF4Segment(
+                    fused.shape[0], fused.shape[1], slice(p_cur, p_cur + nb),
+                    slice(a_cur, a_cur + na), slice(a2_cur, a2_cur + na2), offs, splits, bases,
+                    fused.blocksize, fused.super_blocksize)
+                pb.append(fused.packed)
+                ab.append(fused.absmax)
+                a2b.append(fused.absmax2)
+                p_cur, a_cur, a2_cur = p_cur + nb, a_cur + na, a2_cur + na2
+                ws_elems[name] = max(ws_elems[name], fused.shape[0] * fused.shape[1])
+            self.layer_segments.append(segs)
+            packed_l.append(torch.cat([t.reshape(-1).cpu() for t in pb]))
+            absmax_l.append(torch.cat([t.reshape(-1).cpu() for t in ab]))
+            absmax2_l.append(torch.cat([t.reshape(-1).float().cpu() for t in a2b]))
+        self.layer_bytes = [int(p.numel() + a.numel() + 4 * a2.numel())
+                            for p, a, a2 in zip(packed_l, absmax_l, absmax2_l)]
+        if resident:
+            self.gpu_layers = [(p.to(self.device), a.to(self.device), a2.to(self.device))
+                               for p, a, a2 in zip(packed_l, absmax_l, absmax2_l)]
+        else:
+            self.cpu_packed = [_pinned(p) for p in packed_l]
+            self.cpu_absmax = [_pinned(a) for a in absmax_l]
+            self.cpu_absmax2 = [_pinned(a) for a in absmax2_l]
+            mp = max(p.numel() for p in packed_l)
+            ma = max(a.numel() for a in absmax_l)
+            ma2 = max(a.numel() for a in absmax2_l)
+            self.gpu_packed_slots = [torch.empty(mp, dtype=torch.uint8, device=self.device) for _ in range(2)]
+            self.gpu_absmax_slots = [torch.empty(ma, dtype=torch.uint8, device=self.device) for _ in range(2)]
+            self.gpu_absmax2_slots = [torch.empty(ma2, dtype=torch.float32, device=self.device) for _ in range(2)]
+            self.stream = torch.cuda.Stream(device=self.device)
+            self.slot_events = [torch.cuda.Event() for _ in range(2)]
+            self.compute_done_events = [torch.cuda.Event() for _ in range(2)]
+            self.slot_layer = [-1, -1]
+        self.workspaces = {s: torch.empty(n, dtype=torch.float16, device=self.device)
+                           for s, n in ws_elems.items()}
+
+    # -- streaming protocol (hostload.py:297-323) ------------------------------------------------
+    def prefetch(self, layer_idx: int) -> None:
+        if self.resident or layer_idx < 0 or layer_idx >= self.num_layers:
+            return
+        slot = layer_idx % 2
+        if self.slot_layer[slot] == layer_idx:
+            return
+        with torch.cuda.stream(self.stream):
+            self.stream.wait_event(self.compute_done_events[slot])
+            for dst, src in ((self.gpu_packed_slots, self.cpu_packed),
+                             (self.gpu_absmax_slots, self.cpu_absmax),
+                             (self.gpu_absmax2_slots, self.cpu_absmax2)):
+                s = src[layer_idx]
+                dst[slot][: s.numel()].copy_(s, non_blocking=True)
+            self.slot_events[slot].record(self.stream)
+            self.slot_layer[slot] = layer_idx
+
+    def wait_slot(self, layer_idx: int) -> int:
+        if self.resident:
+            return 0
+        slot = layer_idx % 2
+        if self.slot_layer[slot] != layer_idx:
+            self.prefetch(layer_idx)
+        torch.cuda.current_stream(self.device).wait_event(self.slot_events[slot])
+        return slot
+
+    def release_slot(self, layer_idx: int) -> None:
+        if self.resident:
+            return
+        self.compute_done_events[layer_idx % 2].record(torch.cuda.current_stream(self.device))
+
+    def _arrays(self, layer_idx: int):
+        if self.resident:
+            return self.gpu_layers[layer_idx]
+        slot = layer_idx % 2
+        return self.gpu_packed_slots[slot], self.gpu_absmax_slots[slot], self.gpu_absmax2_slots[slot]
+
+    def dequant(self, layer_idx: int, seg_name: str) -> torch.Tensor:
+        """fp16 [out, in] weight of one segment (a view of that segment's workspace, valid until
+        the same segment is dequantised again)."""
+        seg = self.layer_segments[layer_idx][seg_name]
+        packed, absmax, absmax2 = self._arrays(layer_idx)
+        return K.dequant_nf4_tensor(
+            packed[seg.packed_slice], absmax[seg.absmax_slice], self.code2_gpu,
+            absmax2[seg.absmax2_slice], seg.offsets, (seg.out_features, seg.in_features),
+            out_buf=self.workspaces[seg_name], split_bytes=seg.split_bytes,
+            blocksize=seg.blocksize, super_blocksize=seg.super_blocksize,
+            absmax2_bases=seg.absmax2_bases)
+
+
+class HostHead:
+    """Tied embedding / lm_head: HBM-resident (with W^T for the gradient GEMM) or streamed from
+    pinned host memory in ``v_chunk``-row chunks through two device slots."""
+
+    def __init__(self, weight: torch.Tensor, device, v_chunk: int = V_CHUNK_DEFAULT,
+                 resident: bool = True):
+        self.device = torch.device(device)
+        self.v_chunk = v_chunk
+        self.resident = resident
+        self.vocab_size, self.hidden_size = weight.shape
+        if resident:
+            self.gpu_weight = weight.detach().to(self.device, torch.float16).contiguous()
+            self.gpu_weight_t = K.lm_head_weight_t(self.gpu_weight)
+        else:
+            self.cpu_weight = _pinned(weight.detach().to(torch.float16))
+            self.stream = torch.cuda.Stream(device=self.device)
+            self.slot_events = [torch.cuda.Event() for _ in range(2)]
+            self.compute_done_events = [torch.cuda.Event() for _ in range(2)]
+            self.slot_chunk = [-1, -1]
+            self.gpu_slots = [torch.empty((v_chunk, self.hidden_size), dtype=torch.float16,
+                                          device=self.device) for _ in range(2)]
+
+    def embed(self, input_ids: torch.Tensor) -> torch.Tensor:
+        ids = input_ids.reshape(-1)
+        if self.resident:
+            out = torch.nn.functional.embedding(ids.to(self.device), self.gpu_weight)
+        else:  # host gather + async copy, as hostload.py:381-386
+            emb = self.cpu_weight.index_select(0, ids.cpu())
+            out = emb.pin_memory().to(self.device, non_blocking=True)
+        return out.view(*input_ids.shape, self.hidden_size)
+
+    def prefetch_chunk(self, chunk_idx: int, start_v: int, end_v: int) -> None:
+        slot = chunk_idx % 2
+        if self.slot_chunk[slot] == start_v:
+            return
+        with torch.cuda.stream(self.stream):
+            self.stream.wait_event(self.compute_done_events[slot])
+            self.gpu_slots[slot][: end_v - start_v].copy_(self.cpu_weight[start_v:end_v], non_blocking=True)
+            self.slot_events[slot].record(self.stream)
+            self.slot_chunk[slot] = start_v
+
+    def get_chunk(self, chunk_idx: int, start_v: int, end_v: int) -> torch.Tensor:
+        slot = chunk_idx % 2
+        if self.slot_chunk[slot] != start_v:
+            self.prefetch_chunk(chunk_idx, start_v, end_v)
+        torch.cuda.current_stream(self.device).wait_event(self.slot_events[slot])
+        return self.gpu_slots[slot][: end_v - start_v]
+
+    def release_chunk(self, chunk_idx: int) -> None:
+        self.compute_done_events[chunk_idx % 2].record(torch.cuda.current_stream(self.device))
+
+
+class InputStream:
+    """Per-layer inputs kept for the backward recompute (solution/hostload.py:411-488)."""
+
+    def __init__(self, num_layers: int, hidden_size: int, max_tokens: int, device,
+                 offload: bool = False):
+        self.num_layers = num_layers
+        self.hidden_size = hidden_size
+        self.max_tokens = max_tokens
+        self.device = torch.device(device)
+        self.offload = offload
+        self.gpu_saved: dict[int, torch.Tensor] = {}
+        if offload:
+            self.stream = torch.cuda.Stream(device=self.device)
+            self.d2h_events = [torch.cuda.Event() for _ in range(num_layers)]
+            self.h2d_events = [torch.cuda.Event() for _ in range(2)]
+            self.slot_ready_events = [torch.cuda.Event() for _ in range(2)]
+            self.slot_layer = [-1, -1]
+            self._alloc(max_tokens)
+
+    def _alloc(self, n: int) -> None:
+        self.max_tokens = n
+        self.cpu_buffers = [torch.empty((n, self.hidden_size), dtype=torch.float16, pin_memory=True)
+                            for _ in range(self.num_layers)]
+        self.gpu_slots = [torch.empty((n, self.hidden_size), dtype=torch.float16, device=self.device)
+                          for _ in range(2)]
+
+    def save(self, layer_idx: int, x: torch.Tensor) -> None:
+        if not self.offload or layer_idx >= self.num_layers - 2:
+            self.gpu_saved[layer_idx] = x.detach()  # the stack never modifies a layer input
+            return
+        n = x.shape[0]
+        if n > self.max_tokens:
+            torch.cuda.current_stream(self.device).synchronize()
+            self._alloc(max(n, 2 * self.max_tokens))
+            self.slot_layer = [-1, -1]
+        ev = torch.cuda.Event()
+        ev.record(torch.cuda.current_stream(self.device))
+        with torch.cuda.stream(self.stream):
+            self.stream.wait_event(ev)
+            self.cpu_buffers[layer_idx][:n].copy_(x.detach(), non_blocking=True)
+            self.d2h_events[layer_idx].record(self.stream)
+
+    def prefetch(self, layer_idx: int, n_tokens: int) -> None:
+        if not self.offload or layer_idx < 0 or layer_idx in self.gpu_saved:
+            return
+        slot = layer_idx % 2
+        if self.slot_layer[slot] == layer_idx:
+            return
+        with torch.cuda.stream(self.stream):
+            self.stream.wait_event(self.d2h_events[layer_idx])
+            self.stream.wait_event(self.slot_ready_events[slot])
+            self.gpu_slots[slot][:n_tokens].copy_(self.cpu_buffers[layer_idx][:n_tokens], non_blocking=True)
+            self.h2d_events[slot].record(self.stream)
+            self.slot_layer[slot] = layer_idx
+
+    def load(self, layer_idx: int, n_tokens: int) -> torch.Tensor:
+        if layer_idx in self.gpu_saved:
+            return self.gpu_saved.pop(layer_idx)
+        slot = layer_idx % 2
+        if self.slot_layer[slot] != layer_idx:
+            self.prefetch(layer_idx, n_tokens)
+        torch.cuda.current_stream(self.device).wait_event(self.h2d_events[slot])
+        return self.gpu_slots[slot][:n_tokens]
+
+    def release(self, layer_idx: int) -> None:
+        if self.offload and layer_idx < self.num_layers - 2:
+            slot = layer_idx % 2
+            self.slot_ready_events[slot].record(torch.cuda.current_stream(self.device))
+            self.slot_layer[slot] = -1

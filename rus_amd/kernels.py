@@ -577,36 +577,32 @@ def lm_head_ce_grad_hidden(grad_logits: torch.Tensor, weight_t_cols: torch.Tenso
               parts.data_ptr(), n_split, 1 if accumulate else 0, _stream(grad_logits))
 
 
-def lm_head_dh_reduce(parts: torch.Tensor, scale: float, out_dtype=torch.float16) -> torch.Tensor:
-    """out = out_dtype(scale * sum over the leading split dimension of ``parts``)."""
+def lm_head_dh_reduce(parts: torch.Tensor, scale: float, out_dtype=torch.float16,
+                      scale_dev: torch.Tensor | None = None) -> torch.Tensor:
+    """out = out_dtype(scale * scale_dev * sum over the leading split dimension of ``parts``);
+    ``scale_dev`` is an optional one-element float32 device tensor (read on the device)."""
     fn = "lm_head_dh_reduce"
-    _require_device(fn, parts)
+    _require_device(fn, parts, scale_dev)
     if parts.dtype != torch.float32 or not parts.is_contiguous():
         raise ValueError(f"{fn}: parts must be contiguous float32")
+    if scale_dev is not None and (scale_dev.dtype != torch.float32 or scale_dev.numel() != 1):
+        raise ValueError(f"{fn}: scale_dev must be a one-element float32 tensor")
     out = torch.empty(parts.shape[1:], dtype=out_dtype, device=parts.device)
     _lib.call("rus_lmhead_dh_reduce", parts.data_ptr(), parts.shape[0], out.numel(), float(scale),
-              out.data_ptr(), _dtype_code(fn, out_dtype), _stream(parts))
+              _ptr(scale_dev), out.data_ptr(), _dtype_code(fn, out_dtype), _stream(parts))
     return out
 
 
-_WT_CACHE: "weakref.WeakKeyDictionary[torch.Tensor, tuple]" = None  # type: ignore[assignment]
-
-
 def lm_head_weight_t(weight: torch.Tensor) -> torch.Tensor:
-    """W^T [d, round_up(V, 64)] fp16 with zero padding columns, cached per weight tensor (the
+    """W^T [d, round_up(V, 64)] fp16 with zero padding columns, cached on the weight tensor (the
     lm_head is frozen in QLoRA, so this is built once; rebuilt if the weight is modified)."""
-    global _WT_CACHE
-    import weakref
-
-    if _WT_CACHE is None:
-        _WT_CACHE = weakref.WeakKeyDictionary()
-    hit = _WT_CACHE.get(weight)
+    hit = getattr(weight, "_rus_weight_t", None)
     if hit is not None and hit[0] == weight._version and hit[1].device == weight.device:
         return hit[1]
     V, d = weight.shape
     wt = torch.zeros((d, _round_up(V, LM_K)), dtype=torch.float16, device=weight.device)
     wt[:, :V].copy_(weight.detach().t())
-    _WT_CACHE[weight] = (weight._version, wt)
+    weight._rus_weight_t = (weight._version, wt)
     return wt
 
 

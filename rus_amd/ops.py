@@ -1,0 +1,548 @@
+"""Autograd functions, the fused Qwen2 stack and the chunked lm_head (solution/ops.py surface).
+
+Names, signatures and return values follow the reference so its callers can switch to this
+module: ``rms_norm`` / ``FusedRMSNormFn``, ``mlp_glu`` / ``FusedMLPGLUFn``, ``qkv_lora_rope`` /
+``FusedQKVLoRARoPEFn``, ``chunked_lm_head`` / ``FusedChunkedLMHeadFn`` / ``PRESCALE_GRAD``,
+``Qwen2FusedEngine`` and ``FusedQwen2StackFn.apply(h_packed, pos_ids, row_lengths, engine,
+training, *lora_params)``. Every elementwise / normalisation / rotary / dequant / lm_head step runs
+a gfx950 kernel from ``rus_amd.kernels``; the projections are torch GEMMs (hipBLASLt) and
+attention is torch SDPA per packed row, as in the reference.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+import torch.nn.functional as F
+
+from . import kernels as K
+from .hostload import MAX_MLP_TOKENS, V_CHUNK_DEFAULT, HostHead, InputStream, WeightStream
+
+PRESCALE_GRAD = 65536.0  # solution/ops.py:171: gradients of the loss are formed times 2^16
+
+
+# ---------------------------------------------------------------------------------------------
+# Per-op autograd functions (solution/ops.py:30-164)
+# ---------------------------------------------------------------------------------------------
+
+
+class FusedRMSNormFn(torch.autograd.Function):
+    """Residual + RMSNorm; saves (h, weight, rstd) only and returns the same gradient for x and
+    residual (solution/ops.py:30-50)."""
+
+    @staticmethod
+    def forward(ctx, x, weight, eps=1e-6, residual=None):
+        norm_out, sum_out, rstd = K.rms_norm_fwd(x, weight, eps=eps, residual=residual)
+        ctx.save_for_backward(sum_out, weight, rstd)
+        ctx.has_residual = residual is not None
+        return (norm_out, sum_out) if residual is not None else norm_out
+
+    @staticmethod
+    def backward(ctx, *grads):
+        sum_out, weight, rstd = ctx.saved_tensors
+        if ctx.has_residual:
+            dy, dres = grads[0], grads[1]
+            dx = K.rms_norm_bwd(dy, sum_out, weight, rstd, dresidual=dres)
+            return dx, None, None, dx
+        dx = K.rms_norm_bwd(grads[0], sum_out, weight, rstd)
+        return dx, None, None, None
+
+
+def rms_norm(x, weight, eps: float = 1e-6, residual=None):
+    return FusedRMSNormFn.apply(x, weight, eps, residual)
+
+
+class FusedMLPGLUFn(torch.autograd.Function):
+    """SwiGLU over fused [gate|up] (up=None) or separate tensors (solution/ops.py:57-81)."""
+
+    @staticmethod
+    def forward(ctx, gate_or_gu, up=None):
+        out = K.mlp_glu_fwd(gate_or_gu, up)
+        ctx.fused = up is None
+        ctx.save_for_backward(*((gate_or_gu,) if up is None else (gate_or_gu, up)))
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        if ctx.fused:
+            (gu,) = ctx.saved_tensors
+            dgu = torch.empty_like(gu)
+            K.mlp_glu_bwd(dout, gu, None, dgu_out=dgu)
+            return dgu, None
+        gate, up = ctx.saved_tensors
+        return K.mlp_glu_bwd(dout, gate, up)
+
+
+def mlp_glu(gate_or_gu, up=None):
+    return FusedMLPGLUFn.apply(gate_or_gu, up)
+
+
+class FusedQKVLoRARoPEFn(torch.autograd.Function):
+    """LoRA delta + NeoX RoPE; the backward returns dqkv and the scaled LoRA-delta gradients from
+    one kernel (solution/ops.py:88-148)."""
+
+    @staticmethod
+    def forward(ctx, qkv, cos, sin, pos_ids, q_lora=None, v_lora=None, scale_q=2.0, scale_v=2.0,
+                h_q=12, h_kv=2, head_dim=128):
+        q_out, k_out, v_out = K.qkv_rope_fwd(qkv, cos, sin, pos_ids, q_lora=q_lora, v_lora=v_lora,
+                                             scale_q=scale_q, scale_v=scale_v, h_q=h_q, h_kv=h_kv,
+                                             head_dim=head_dim)
+        ctx.save_for_backward(cos, sin, pos_ids)
+        ctx.has_lora = q_lora is not None and v_lora is not None
+        ctx.scale_q, ctx.scale_v = float(scale_q), float(scale_v)
+        ctx.h_q, ctx.h_kv, ctx.head_dim = h_q, h_kv, head_dim
+        return q_out, k_out, v_out
+
+    @staticmethod
+    def backward(ctx, dq_rot, dk_rot, dv_out):
+        cos, sin, pos_ids = ctx.saved_tensors
+        if not ctx.has_lora:
+            dqkv = K.qkv_rope_bwd(dq_rot, dk_rot, dv_out, cos, sin, pos_ids, h_q=ctx.h_q,
+                                  h_kv=ctx.h_kv, head_dim=ctx.head_dim)
+            return dqkv, None, None, None, None, None, None, None, None, None, None
+        dqkv, dq_lora, dv_lora = K.qkv_rope_bwd_lora(dq_rot, dk_rot, dv_out, cos, sin, pos_ids,
+                                                     ctx.scale_q, ctx.scale_v, h_q=ctx.h_q,
+                                                     h_kv=ctx.h_kv, head_dim=ctx.head_dim)
+        return dqkv, None, None, None, dq_lora, dv_lora, None, None, None, None, None
+
+
+def qkv_lora_rope(qkv, cos, sin, pos_ids, q_lora=None, v_lora=None, scale_q=2.0, scale_v=2.0,
+                  h_q=12, h_kv=2, head_dim=128):
+    return FusedQKVLoRARoPEFn.apply(qkv, cos, sin, pos_ids, q_lora, v_lora, scale_q, scale_v, h_q,
+                                    h_kv, head_dim)
+
+
+# ---------------------------------------------------------------------------------------------
+# Chunked lm_head cross-entropy (solution/ops.py:174-349)
+# ---------------------------------------------------------------------------------------------
+
+
+def _lm_head_streamed(h_2d, labels, head: HostHead, num_items_in_batch, need_grad):
+    """lm_head over a HostHead streamed from pinned host memory chunk by chunk (forward chunks in
+    order, gradient chunks in reverse so the last chunk is reused, as ops.py:217-322)."""
+    n_tok, d = h_2d.shape
+    V, vc = head.vocab_size, head.v_chunk
+    dev = h_2d.device
+    starts = list(range(0, V, vc))
+    parts = K.LMHeadPartials(K.lm_head_num_parts(V), n_tok, dev)
+    target = torch.zeros(n_tok, dtype=torch.float32, device=dev)
+    head.prefetch_chunk(0, 0, min(vc, V))
+    for c, s in enumerate(starts):
+        e = min(s + vc, V)
+        if c + 1 < len(starts):
+            head.prefetch_chunk(c + 1, starts[c + 1], min(starts[c + 1] + vc, V))
+        K.lm_head_ce_fwd_chunk(h_2d, head.get_chunk(c, s, e), labels, s, parts, target)
+        if c + 1 < len(starts) or need_grad:
+            head.release_chunk(c)
+    lse, nll, ent, amax = K.lm_head_ce_combine(parts, target, labels)
+    denom = _denominator(labels, num_items_in_batch, dev)
+    dh_pre = None
+    if need_grad:
+        g = torch.empty((n_tok, K._round_up(vc, K.LM_K)), dtype=torch.float16, device=dev)
+        n_split = K.lm_head_split_count(n_tok, d, vc, target_blocks=256)
+        dparts = torch.zeros((n_split, n_tok, d), dtype=torch.float32, device=dev)
+        for c in range(len(starts) - 1, -1, -1):
+            s = starts[c]
+            e = min(s + vc, V)
+            if c - 1 >= 0:
+                head.prefetch_chunk(c - 1, starts[c - 1], min(starts[c - 1] + vc, V))
+            w = head.get_chunk(c, s, e)
+            K.lm_head_ce_grad_logits(h_2d, w, labels, lse, denom, s, g)
+            wt = torch.zeros((d, K._round_up(e - s, K.LM_K)), dtype=torch.float16, device=dev)
+            wt[:, : e - s].copy_(w.t())
+            ns = K.lm_head_split_count(n_tok, d, e - s, target_blocks=256)
+            K.lm_head_ce_grad_hidden(g, wt, e - s, dparts[:ns], accumulate=True)
+            head.release_chunk(c)
+        dh_pre = K.lm_head_dh_reduce(dparts, 1.0, torch.float32)
+    return nll, lse, ent, amax, denom, dh_pre
+
+
+def _denominator(labels, num_items_in_batch, dev):
+    if num_items_in_batch is None:
+        return (labels != -100).sum().to(torch.float32).clamp_(min=1.0).reshape(1)
+    if isinstance(num_items_in_batch, torch.Tensor):
+        return num_items_in_batch.detach().to(dev, torch.float32).reshape(1).clamp(min=1.0)
+    return torch.full((1,), max(float(num_items_in_batch), 1.0), dtype=torch.float32, device=dev)
+
+
+class FusedChunkedLMHeadFn(torch.autograd.Function):
+    """Cross-entropy loss, per-token NLL, entropy and argmax without the [N, V] logits; the
+    hidden gradient (times 2^16) is formed in forward and rescaled by the incoming loss gradient
+    in backward (solution/ops.py:174-339). Accumulation is fp32 (the reference's is fp16)."""
+
+    @staticmethod
+    def forward(ctx, hidden_states, shift_labels, weight_or_host_head, num_items_in_batch=None,
+                v_chunk=None):
+        h_2d = hidden_states.contiguous().view(-1, hidden_states.shape[-1])
+        labels = shift_labels.contiguous().view(-1).to(torch.int64)
+        is_head = isinstance(weight_or_host_head, HostHead)
+        # Function.forward always runs with grad mode off, so torch.is_grad_enabled() (what the
+        # reference tests, ops.py:280) is False here; ask autograd whether dH is needed instead.
+        need_grad = bool(ctx.needs_input_grad[0])
+        if is_head and not weight_or_host_head.resident:
+            nll, lse, ent, amax, denom, dh_pre = _lm_head_streamed(
+                h_2d, labels, weight_or_host_head, num_items_in_batch, need_grad)
+        else:
+            if is_head:
+                w, wt = weight_or_host_head.gpu_weight, weight_or_host_head.gpu_weight_t
+            else:
+                w, wt = weight_or_host_head.detach(), None
+            nll, lse, ent, amax, denom, dh_pre = K.lm_head_ce(
+                h_2d, w, labels, num_items_in_batch=num_items_in_batch, v_chunk=v_chunk,
+                need_grad=need_grad, weight_t=wt)
+        loss = nll.sum() / denom[0]
+        ctx.save_for_backward(dh_pre)
+        ctx.orig_shape = hidden_states.shape
+        ctx.orig_dtype = hidden_states.dtype
+        ctx.mark_non_differentiable(nll, ent, amax)
+        return loss, nll, ent, amax
+
+    @staticmethod
+    def backward(ctx, grad_loss, _g_nll=None, _g_ent=None, _g_arg=None):
+        (dh_pre,) = ctx.saved_tensors
+        if dh_pre is None:
+            return None, None, None, None, None
+        g = grad_loss.detach().to(torch.float32).reshape(1)
+        d_h = K.lm_head_dh_reduce(dh_pre.unsqueeze(0), 1.0 / PRESCALE_GRAD, ctx.orig_dtype,
+                                  scale_dev=g)
+        return d_h.view(ctx.orig_shape), None, None, None, None
+
+
+def chunked_lm_head(hidden_states, shift_labels, weight_or_host_head, num_items_in_batch=None,
+                    v_chunk=None):
+    """(loss, nll, entropy, argmax) of the lm_head cross-entropy (solution/ops.py:342-349).
+    ``v_chunk`` bounds the logit-gradient buffer to [N, v_chunk] (default: one pass over V)."""
+    return FusedChunkedLMHeadFn.apply(hidden_states, shift_labels, weight_or_host_head,
+                                      num_items_in_batch, v_chunk)
+
+
+# ---------------------------------------------------------------------------------------------
+# Fused 28-layer engine (solution/ops.py:599-1009)
+# ---------------------------------------------------------------------------------------------
+
+
+def rope_cache(max_pos: int, head_dim: int, theta: float, device, dtype=torch.float16):
+    """cos/sin [max_pos, head_dim] of Qwen2's default rotary embedding (built once, in fp32 on the
+    host, then cast; the reference takes it from the model's rotary module, ops.py:658-666)."""
+    inv = 1.0 / (theta ** (torch.arange(0, head_dim, 2, dtype=torch.int64).float() / head_dim))
+    freqs = torch.arange(max_pos, dtype=torch.float32)[:, None] * inv[None, :]
+    emb = torch.cat([freqs, freqs], dim=-1)
+    return emb.cos().to(device, dtype).contiguous(), emb.sin().to(device, dtype).contiguous()
+
+
+class Qwen2FusedEngine:
+    """Streams, RoPE cache, norm weights and LoRA references of a QLoRA Qwen2 (ops.py:603-666).
+
+    ``model`` is a ``rus_amd.model.QLoRAQwen2`` or a transformers/PEFT/bitsandbytes causal LM
+    (read through ``rus_amd.adapters.layers_from_causal_lm``). ``layer_biases`` is defined here
+    (the reference reads it from the engine but only defines it on its WeightStream).
+    """
+
+    def __init__(self, model, device, resident_weights: bool = False, resident_head: bool = True,
+                 offload_inputs: bool = False, max_pos: int = 2048,
+                 max_mlp_tokens: int = MAX_MLP_TOKENS, v_chunk: int = V_CHUNK_DEFAULT):
+        from .model import QLoRAQwen2
+
+        if not isinstance(model, QLoRAQwen2):
+            from .adapters import model_from_causal_lm
+
+            model = model_from_causal_lm(model)
+        cfg = model.config
+        self.device = torch.device(device)
+        self.config = cfg
+        self.num_layers = len(model.layers)
+        self.hidden_size = cfg.hidden_size
+        self.intermediate_size = cfg.intermediate_size
+        self.num_heads = cfg.num_attention_heads
+        self.num_kv_heads = cfg.num_key_value_heads
+        self.head_dim = cfg.hidden_size // cfg.num_attention_heads
+        self.rms_eps = float(cfg.rms_norm_eps)
+        self.max_mlp_tokens = max_mlp_tokens
+        self.weight_stream = WeightStream(model.layers, self.device, resident=resident_weights)
+        self.layer_biases = self.weight_stream.layer_biases
+        self.host_head = HostHead(model.embed, self.device, v_chunk=v_chunk, resident=resident_head)
+        self.input_stream = InputStream(self.num_layers, self.hidden_size, 2048, self.device,
+                                        offload=offload_inputs)
+        self.ln1_weights = [L.ln1.to(self.device) for L in model.layers]
+        self.ln2_weights = [L.ln2.to(self.device) for L in model.layers]
+        self.final_norm_weight = model.final_norm.to(self.device)
+        self.lora_params = model.lora_parameters()
+        self.layer_lora_meta = model.meta.get("layer_lora_meta") or [
+            {"scale_q": cfg.lora_scaling, "scale_v": cfg.lora_scaling, "p_q": cfg.lora_dropout,
+             "p_v": cfg.lora_dropout} for _ in model.layers]
+        self.cos_table, self.sin_table = rope_cache(max_pos, self.head_dim, cfg.rope_theta,
+                                                    self.device)
+
+
+def _run_packed_sdpa(q_rot, k_rot, v_out, row_lengths, num_heads, num_kv_heads, head_dim):
+    """Causal GQA attention per packed row (solution/ops.py:669-696)."""
+    n_tokens = q_rot.shape[0]
+    out = torch.empty((n_tokens, num_heads * head_dim), dtype=q_rot.dtype, device=q_rot.device)
+    groups = num_heads // num_kv_heads
+    cur = 0
+    for L in row_lengths:
+        if L <= 0:
+            continue
+        nxt = cur + L
+        q = q_rot[cur:nxt].transpose(0, 1).unsqueeze(0)
+        k = k_rot[cur:nxt].transpose(0, 1).unsqueeze(0)
+        v = v_out[cur:nxt].transpose(0, 1).unsqueeze(0)
+        if groups > 1:
+            k = k.unsqueeze(2).expand(1, num_kv_heads, groups, L, head_dim).reshape(1, num_heads, L, head_dim)
+            v = v.unsqueeze(2).expand(1, num_kv_heads, groups, L, head_dim).reshape(1, num_heads, L, head_dim)
+        o = F.scaled_dot_product_attention(q, k, v, is_causal=True)
+        out[cur:nxt] = o.squeeze(0).transpose(0, 1).reshape(L, num_heads * head_dim)
+        cur = nxt
+    return out
+
+
+def _lora_deltas(norm1, q_A, q_B, v_A, v_B, meta, training):
+    """(x_drop_q, mid_q, q_lora, x_drop_v, mid_v, v_lora, fp16 A/B) with the dropout order of
+    solution/ops.py:775-778 (q first, then v)."""
+    dt = norm1.dtype
+    qA, qB, vA, vB = q_A.to(dt), q_B.to(dt), v_A.to(dt), v_B.to(dt)
+    x_q = F.dropout(norm1, p=meta["p_q"], training=True) if (training and meta["p_q"] > 0) else norm1
+    mid_q = F.linear(x_q, qA)
+    q_lora = F.linear(mid_q, qB)
+    x_v = F.dropout(norm1, p=meta["p_v"], training=True) if (training and meta["p_v"] > 0) else norm1
+    mid_v = F.linear(x_v, vA)
+    v_lora = F.linear(mid_v, vB)
+    return x_q, mid_q, q_lora, x_v, mid_v, v_lora, (qA, qB, vA, vB)
+
+
+def _mlp_fwd(norm2, w_gu, w_down, max_tokens):
+    n = norm2.shape[0]
+    if n <= max_tokens:
+        return F.linear(K.mlp_glu_fwd(F.linear(norm2, w_gu)), w_down)
+    out = torch.empty((n, w_down.shape[0]), dtype=norm2.dtype, device=norm2.device)
+    for s in range(0, n, max_tokens):
+        e = min(s + max_tokens, n)
+        out[s:e] = F.linear(K.mlp_glu_fwd(F.linear(norm2[s:e], w_gu)), w_down)
+    return out
+
+
+class FusedQwen2StackFn(torch.autograd.Function):
+    """All decoder layers on packed tokens with layer-input checkpointing, dropout RNG replay and
+    recompute in backward (solution/ops.py:729-1009). Returns the final-norm hidden states; the
+    gradient flows to the LoRA parameters only.
+
+    Each layer's input residual add is fused into the RMSNorm kernel (h_{l+1} = h_mid + mlp is
+    formed by the next layer's input norm), each weight segment is dequantised once per layer
+    per pass, and the backward's LoRA-delta gradients come out of the RoPE-adjoint kernel."""
+
+    @staticmethod
+    def forward(ctx, h_packed, pos_ids, row_lengths, engine, training, *lora_params):
+        ws, ins = engine.weight_stream, engine.input_stream
+        L = engine.num_layers
+        cos, sin, eps = engine.cos_table, engine.sin_table, engine.rms_eps
+        rng_states = []
+        h = h_packed.contiguous()
+        carry = None  # (h_mid, mlp_out) of the previous layer, added inside the next norm
+        if L > 0:
+            ws.prefetch(0)
+        for l in range(L):
+            if l + 1 < L:
+                ws.prefetch(l + 1)
+            if carry is None:
+                norm1, _, _ = K.rms_norm_fwd(h, engine.ln1_weights[l], eps=eps)
+            else:
+                norm1, h, _ = K.rms_norm_fwd(carry[1], engine.ln1_weights[l], eps=eps, residual=carry[0])
+            ins.save(l, h)
+            rng_states.append(torch.cuda.get_rng_state(engine.device) if training else None)
+            ws.wait_slot(l)
+            qkv = F.linear(norm1, ws.dequant(l, "qkv"), engine.layer_biases[l])
+            meta = engine.layer_lora_meta[l]
+            _, _, q_lora, _, _, v_lora, _ = _lora_deltas(norm1, *lora_params[4 * l: 4 * l + 4], meta, training)
+            q_rot, k_rot, v_out = K.qkv_rope_fwd(qkv, cos, sin, pos_ids, q_lora=q_lora, v_lora=v_lora,
+                                                 scale_q=meta["scale_q"], scale_v=meta["scale_v"],
+                                                 h_q=engine.num_heads, h_kv=engine.num_kv_heads,
+                                                 head_dim=engine.head_dim)
+            del qkv, q_lora, v_lora, norm1
+            attn = _run_packed_sdpa(q_rot, k_rot, v_out, row_lengths, engine.num_heads,
+                                    engine.num_kv_heads, engine.head_dim)
+            del q_rot, k_rot, v_out
+            o_out = F.linear(attn, ws.dequant(l, "o"))
+            del attn
+            norm2, h_mid, _ = K.rms_norm_fwd(o_out, engine.ln2_weights[l], eps=eps, residual=h)
+            del o_out
+            mlp_out = _mlp_fwd(norm2, ws.dequant(l, "gu"), ws.dequant(l, "down"), engine.max_mlp_tokens)
+            ws.release_slot(l)
+            del norm2
+            carry = (h_mid, mlp_out)
+        if carry is None:
+            final_norm, h_last, final_rstd = K.rms_norm_fwd(h, engine.final_norm_weight, eps=eps)
+        else:
+            final_norm, h_last, final_rstd = K.rms_norm_fwd(carry[1], engine.final_norm_weight,
+                                                            eps=eps, residual=carry[0])
+        ctx.save_for_backward(pos_ids, h_last, final_rstd, *lora_params)
+        ctx.row_lengths = row_lengths
+        ctx.engine = engine
+        ctx.training = training
+        ctx.rng_states = rng_states
+        return final_norm
+
+    @staticmethod
+    def backward(ctx, d_final_norm):
+        saved = ctx.saved_tensors
+        pos_ids, h_last, final_rstd = saved[0], saved[1], saved[2]
+        lora_params = saved[3:]
+        engine = ctx.engine
+        ws, ins = engine.weight_stream, engine.input_stream
+        L = engine.num_layers
+        cos, sin, eps = engine.cos_table, engine.sin_table, engine.rms_eps
+        training = ctx.training
+        saved_rng = torch.cuda.get_rng_state(engine.device)
+        n_tokens = pos_ids.shape[0]
+        hq, hkv, hd = engine.num_heads, engine.num_kv_heads, engine.head_dim
+        q_dim = hq * hd
+
+        dh = K.rms_norm_bwd(d_final_norm.contiguous(), h_last, engine.final_norm_weight, final_rstd)
+        lora_grads = [None] * (4 * L)
+        if L > 0:
+            ws.prefetch(L - 1)
+        for l in range(L - 1, -1, -1):
+            if l - 1 >= 0:
+                ws.prefetch(l - 1)
+                ins.prefetch(l - 1, n_tokens)
+            h_in = ins.load(l, n_tokens)
+            ws.wait_slot(l)
+            w_qkv = ws.dequant(l, "qkv")
+            w_o = ws.dequant(l, "o")
+            w_gu = ws.dequant(l, "gu")
+            w_down = ws.dequant(l, "down")
+            ws.release_slot(l)  # every read of the packed slot is enqueued
+            if training and ctx.rng_states[l] is not None:
+                torch.cuda.set_rng_state(ctx.rng_states[l], engine.device)
+
+            # Recompute the layer forward.
+            norm1, _, rstd1 = K.rms_norm_fwd(h_in, engine.ln1_weights[l], eps=eps)
+            qkv = F.linear(norm1, w_qkv, engine.layer_biases[l])
+            meta = engine.layer_lora_meta[l]
+            q_A, q_B, v_A, v_B = lora_params[4 * l: 4 * l + 4]
+            x_q, mid_q, q_lora, x_v, mid_v, v_lora, (qA, qB, vA, vB) = _lora_deltas(
+                norm1, q_A, q_B, v_A, v_B, meta, training)
+            q_rot, k_rot, v_out = K.qkv_rope_fwd(qkv, cos, sin, pos_ids, q_lora=q_lora, v_lora=v_lora,
+                                                 scale_q=meta["scale_q"], scale_v=meta["scale_v"],
+                                                 h_q=hq, h_kv=hkv, head_dim=hd)
+            del qkv, q_lora, v_lora
+            with torch.enable_grad():
+                q_req = q_rot.detach().requires_grad_(True)
+                k_req = k_rot.detach().requires_grad_(True)
+                v_req = v_out.detach().requires_grad_(True)
+                attn = _run_packed_sdpa(q_req, k_req, v_req, ctx.row_lengths, hq, hkv, hd)
+            o_out = F.linear(attn.detach(), w_o)
+            norm2, h_mid, rstd2 = K.rms_norm_fwd(o_out, engine.ln2_weights[l], eps=eps, residual=h_in)
+            del o_out
+
+            # MLP backward: d_act = dh . W_down; SwiGLU backward in place over gu; d_norm2.
+            d_norm2 = torch.empty_like(norm2)
+            step = min(engine.max_mlp_tokens, n_tokens)
+            for s in range(0, n_tokens, step):
+                e = min(s + step, n_tokens)
+                gu = F.linear(norm2[s:e], w_gu)
+                K.mlp_glu_bwd(torch.mm(dh[s:e], w_down), gu)
+                torch.mm(gu, w_gu, out=d_norm2[s:e])
+                del gu
+            del norm2
+            dh_mid = K.rms_norm_bwd(d_norm2, h_mid, engine.ln2_weights[l], rstd2, dresidual=dh)
+            del d_norm2, h_mid, rstd2, dh
+
+            # Attention backward, adjoint RoPE with [dQ|dK|dV] packing and LoRA-delta gradients.
+            d_attn = torch.mm(dh_mid, w_o)
+            dq, dk, dv = torch.autograd.grad(attn, (q_req, k_req, v_req), d_attn)
+            del attn, q_req, k_req, v_req, d_attn, q_rot, k_rot, v_out
+            dqkv, dq_scaled, dv_scaled = K.qkv_rope_bwd_lora(dq, dk, dv, cos, sin, pos_ids,
+                                                             meta["scale_q"], meta["scale_v"],
+                                                             h_q=hq, h_kv=hkv, head_dim=hd)
+            del dq, dk, dv
+
+            # LoRA parameter gradients (solution/ops.py:975-983).
+            d_qB = torch.mm(dq_scaled.t(), mid_q).to(q_B.dtype)
+            d_mid_q = torch.mm(dq_scaled, qB)
+            d_qA = torch.mm(d_mid_q.t(), x_q).to(q_A.dtype)
+            dx_q = torch.mm(d_mid_q, qA)
+            d_vB = torch.mm(dv_scaled.t(), mid_v).to(v_B.dtype)
+            d_mid_v = torch.mm(dv_scaled, vB)
+            d_vA = torch.mm(d_mid_v.t(), x_v).to(v_A.dtype)
+            dx_v = torch.mm(d_mid_v, vA)
+            del mid_q, mid_v, x_q, x_v, d_mid_q, d_mid_v, dq_scaled, dv_scaled
+            if training and ctx.rng_states[l] is not None:
+                torch.cuda.set_rng_state(ctx.rng_states[l], engine.device)
+            if training and meta["p_q"] > 0:
+                dx_q = F.dropout(dx_q, p=meta["p_q"], training=True)
+            if training and meta["p_v"] > 0:
+                dx_v = F.dropout(dx_v, p=meta["p_v"], training=True)
+
+            d_norm1 = torch.mm(dqkv, w_qkv)
+            d_norm1.add_(dx_q).add_(dx_v)
+            del dqkv, dx_q, dx_v, norm1
+            dh = K.rms_norm_bwd(d_norm1, h_in, engine.ln1_weights[l], rstd1, dresidual=dh_mid)
+            ins.release(l)
+            del d_norm1, h_in, rstd1, dh_mid
+            lora_grads[4 * l: 4 * l + 4] = [d_qA, d_qB, d_vA, d_vB]
+        torch.cuda.set_rng_state(saved_rng, engine.device)
+        ctx.d_h_packed = dh  # gradient w.r.t. the embedding output (frozen), kept for tests
+        return (None, None, None, None, None, *lora_grads)
+
+
+# ---------------------------------------------------------------------------------------------
+# Padding-free varlen packing (solution/ops.py:1103-1127) and scatter back (ops.py:1151-1164)
+# ---------------------------------------------------------------------------------------------
+
+
+@dataclass
+class PackedBatch:
+    input_ids: torch.Tensor  # [N] int64
+    pos_ids: torch.Tensor  # [N] int64, restarting per row
+    shift_labels: torch.Tensor  # [N] int64, -100 where ignored
+    row_lengths: list[int]
+    valid_idx: torch.Tensor  # [N] flat indices into [B*S]
+    batch_shape: tuple[int, int]
+
+
+def pack_varlen(input_ids, attention_mask=None, labels=None, position_ids=None) -> PackedBatch:
+    """keep = attention_mask | (shifted label != -100); positions = cumsum(mask) - 1 per row;
+    the kept tokens of every row, concatenated (solution/ops.py:1103-1127)."""
+    B, S = input_ids.shape
+    dev = input_ids.device
+    if attention_mask is None:
+        attention_mask = torch.ones((B, S), dtype=torch.long, device=dev)
+    shift = torch.full((B, S), -100, dtype=torch.int64, device=dev)
+    if labels is not None and S > 1:
+        shift[:, :-1] = labels[:, 1:].to(torch.int64)
+    keep = attention_mask.bool() | (shift != -100)
+    if not keep.any():
+        keep[:, 0] = True
+    row_lengths = keep.sum(dim=-1, dtype=torch.int32).tolist()
+    valid_idx = torch.nonzero(keep.reshape(-1), as_tuple=False).squeeze(-1)
+    pos_full = (position_ids.to(torch.long) if position_ids is not None
+                else (attention_mask.to(torch.long).cumsum(dim=-1) - 1).clamp_(min=0))
+    return PackedBatch(input_ids.reshape(-1).index_select(0, valid_idx),
+                       pos_full.reshape(-1).index_select(0, valid_idx),
+                       shift.reshape(-1).index_select(0, valid_idx), row_lengths, valid_idx, (B, S))
+
+
+def scatter_per_token(values: torch.Tensor, packed: PackedBatch, fill=0.0) -> torch.Tensor:
+    """[N] packed values -> [B, S], ``fill`` at positions that were not packed."""
+    B, S = packed.batch_shape
+    out = torch.full((B * S,), fill, dtype=values.dtype, device=values.device)
+    out.index_copy_(0, packed.valid_idx, values)
+    return out.view(B, S)
+
+
+def fused_causal_lm_forward(engine: Qwen2FusedEngine, input_ids, attention_mask=None, labels=None,
+                            num_items_in_batch=None, training: bool = True, position_ids=None):
+    """Packed forward of the whole model with the fused lm_head (the body of the reference's
+    patched Qwen2ForCausalLM.forward, solution/ops.py:1097-1164). Returns (loss, per-token nll,
+    entropy, argmax) scattered back to [B, S]; padding positions get the mean entropy."""
+    pb = pack_varlen(input_ids, attention_mask, labels, position_ids)
+    h = engine.host_head.embed(pb.input_ids)
+    final = FusedQwen2StackFn.apply(h, pb.pos_ids, pb.row_lengths, engine, training, *engine.lora_params)
+    loss, nll, ent, amax = chunked_lm_head(final, pb.shift_labels, engine.host_head,
+                                           num_items_in_batch=num_items_in_batch)
+    mean_ent = ent.mean() if ent.numel() else torch.zeros((), device=ent.device)
+    full_ent = mean_ent.expand(pb.batch_shape[0] * pb.batch_shape[1]).clone()
+    full_ent.index_copy_(0, pb.valid_idx, ent)
+    return (loss, scatter_per_token(nll, pb), full_ent.view(pb.batch_shape),
+            scatter_per_token(amax, pb, 0))
