@@ -1,0 +1,261 @@
+#!/usr/bin/env python3
+"""Benchmark of the fused QLoRA training step on one MI355X.
+
+Workload: one training step = packed forward + backward of a random-init, NF4 double-quantised
+Qwen2.5-1.5B-shaped model (28 layers, LoRA r=16 / alpha=32 / dropout 0.05 on q and v) over a batch
+of 4 rows with lognormal lengths (median 140, mean 220, clipped to [16, 512]) of uniform random
+token ids, followed by an AdamW step on the LoRA parameters (lr 2e-4). Base layers are streamed
+per step from pinned host memory through two device slots (as configured); batches are resident
+in HBM before the timed region.
+
+Prints one JSON line: tokens/s over the K timed steps (value), the dominant kernel's roofline
+(HIP events around each of its launches inside the timed region), the CPU baseline (the oracle
+on a bounded sample, extrapolated), peak HBM per step against the unfused eager step, per-kernel
+rates and a resident-weights ablation.
+
+Usage: python bench.py [--gpus 1] [--steps 64] [--warmup 2]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+if REPO not in sys.path:
+    sys.path.insert(0, REPO)
+
+METRIC = "train tokens/s (packed 1.5B NF4 QLoRA); lm_head-CE & NF4-dequant HBM GB/s"
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E
+FP16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA
+MFMA_KERNELS = ("lmhead_ce_fwd", "lmhead_ce_grad_logits", "lmhead_ce_grad_hidden")
+
+
+def make_batches(cfg, n_batches, rows, max_len, seed, device):
+    import torch
+
+    from rus_amd.model import lengths_lognormal
+
+    out = []
+    for b in range(n_batches):
+        lengths = lengths_lognormal(rows, seed=seed + b, hi=max_len)
+        S = max(lengths)
+        g = torch.Generator().manual_seed(seed + 1000 + b)
+        ids = torch.randint(0, cfg.vocab_size, (rows, S), generator=g)
+        mask = torch.zeros(rows, S, dtype=torch.long)
+        for r, L in enumerate(lengths):
+            mask[r, :L] = 1
+        labels = torch.where(mask.bool(), ids, torch.full_like(ids, -100))
+        out.append((ids.to(device), mask.to(device), labels.to(device), sum(lengths)))
+    return out
+
+
+def train_step(engine, opt, batch):
+    from rus_amd.ops import fused_causal_lm_forward
+
+    ids, mask, labels, _ = batch
+    loss, _, _, _ = fused_causal_lm_forward(engine, ids, mask, labels, training=True)
+    loss.backward()
+    opt.step()
+    opt.zero_grad(set_to_none=True)
+    return loss
+
+
+def timed_run(engine, opt, batches, steps, warmup, kernel_filter=None):
+    """Runs warmup + timed steps; returns (seconds, tokens, per-step seconds, timer summary)."""
+    import torch
+
+    from rus_amd.kernels import KernelTimer
+
+    for i in range(warmup):
+        train_step(engine, opt, batches[i % len(batches)])
+    torch.cuda.synchronize()
+    timer = KernelTimer(only=kernel_filter)
+    per_step = []
+    tokens = 0
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    with timer:
+        for i in range(steps):
+            s0 = time.perf_counter()
+            b = batches[(warmup + i) % len(batches)]
+            train_step(engine, opt, b)
+            tokens += b[3]
+            per_step.append(time.perf_counter() - s0)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    return t1 - t0, tokens, per_step, timer.summary()
+
+
+def kernel_rates(summary, steps):
+    out = {}
+    for name, r in summary.items():
+        sec = r["ms"] / 1e3
+        e = {"launches_per_step": r["launches"] / steps, "ms_per_step": r["ms"] / steps}
+        if name in MFMA_KERNELS:
+            e["tflops"] = r["flops"] / sec / 1e12 if sec > 0 else None
+        e["gbps"] = r["bytes"] / sec / 1e9 if sec > 0 else None
+        out[name] = e
+    return out
+
+
+def cpu_baseline(seed=0):
+    """The CPU oracle on a bounded sample of the same workload: one config-5 layer plus the
+    lm_head over one packed row of 128 tokens, forward + backward including the NF4 dequant of
+    the layer's weights; extrapolated to the 28-layer step as tokens/s."""
+    import torch
+
+    from oracle import ops as oref
+    from oracle import stack as ostack
+    from rus_amd import model as M
+
+    threads = max(1, min(len(os.sched_getaffinity(0)), 16))
+    torch.set_num_threads(threads)
+    cfg = M.qwen2_1p5b()
+    cfg1 = M.Qwen2Config(**{**cfg.__dict__, "num_hidden_layers": 1, "lora_dropout": 0.0})
+    model = M.build_random_qlora_qwen2(cfg1, "cpu", seed=seed)
+    n = 128
+    g = torch.Generator().manual_seed(seed)
+    ids = torch.randint(0, cfg.vocab_size, (n,), generator=g)
+    pos = torch.arange(n)
+    labels = torch.cat([ids[1:], torch.tensor([-100])])
+    reps = []
+    for _ in range(2):
+        t0 = time.perf_counter()
+        deq = ostack.dequant_model(model)
+        t1 = time.perf_counter()
+        lora = ostack.lora_leaves(model)
+        loss, final = ostack.step_loss(model, deq, lora, ids, pos, labels, [n])
+        loss.backward()
+        t2 = time.perf_counter()
+        oref.lm_head_ce(final.detach().half(), model.embed, labels, need_grad=True)
+        t3 = time.perf_counter()
+        reps.append((t1 - t0, t2 - t1, t3 - t2))
+    t_deq, t_fb, t_head = (min(r[i] for r in reps) for i in range(3))
+    t_layer = t_deq + max(t_fb - t_head, 0.0)
+    t_step = cfg.num_hidden_layers * t_layer + t_head
+    return {"value": n / t_step, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": (f"oracle (eager fp32 torch + numpy NF4 dequant) on 1 of 28 config-5 layers "
+                       f"+ lm_head, one packed row of {n} tokens, fwd+bwd; per-step estimate "
+                       f"28*{t_layer:.3f}s + {t_head:.3f}s (lm_head)")}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=64)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--rows", type=int, default=4)
+    ap.add_argument("--max-len", type=int, default=512)
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-eager", action="store_true")
+    ap.add_argument("--no-resident", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); the "
+              "multi-GPU design is described in DESIGN.md", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from rus_amd import model as M
+    from rus_amd.eager_reference import eager_step_loss
+    from rus_amd.ops import Qwen2FusedEngine, pack_varlen
+
+    dev = torch.device("cuda:0")
+    torch.manual_seed(args.seed)
+    cfg = M.qwen2_1p5b()
+    model = M.build_random_qlora_qwen2(cfg, dev, seed=args.seed)
+    batches = make_batches(cfg, 8, args.rows, args.max_len, args.seed, dev)
+    params = model.lora_parameters()
+    opt = torch.optim.AdamW(params, lr=2e-4)
+
+    # Configured engine: NF4 layers streamed per step from pinned host memory.
+    engine = Qwen2FusedEngine(model, dev, resident_weights=False)
+    # Calibration pass: every kernel timed, to name the dominant one.
+    _, _, _, calib = timed_run(engine, opt, batches, 2, args.warmup, kernel_filter=None)
+    dominant = max(calib, key=lambda k: calib[k]["ms"])
+    torch.cuda.reset_peak_memory_stats(dev)
+    base_alloc = torch.cuda.memory_allocated(dev)
+    secs, tokens, per_step, summary = timed_run(engine, opt, batches, args.steps, 0,
+                                                kernel_filter={dominant})
+    peak = torch.cuda.max_memory_allocated(dev)
+    value = tokens / secs
+    d = summary[dominant]
+    avg_ms = d["ms"] / d["launches"]
+    if dominant in MFMA_KERNELS:
+        achieved = d["flops"] / (d["ms"] / 1e3) / 1e12
+        roof = {"bound": "mfma", "achieved": achieved, "peak": FP16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                "frac": achieved / FP16_PEAK_TFLOPS, "traffic": None}
+    else:
+        achieved = d["bytes"] / (d["ms"] / 1e3) / 1e9
+        roof = {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": achieved / HBM_PEAK_GBS, "traffic": None}
+    roof.update({"kernel": dominant, "avg_launch_ms": avg_ms, "launches": d["launches"],
+                 "per_launch": d["flops"] / d["launches"] if dominant in MFMA_KERNELS
+                 else d["bytes"] / d["launches"]})
+
+    out = {
+        "metric": METRIC, "value": value, "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": secs / args.steps * 1e3, "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "fp16",
+        "data": "synthetic: uniform random token ids, lognormal row lengths; random-init NF4 model",
+        "config": {"workload": "BASELINE config 5: 28-layer packed QLoRA train step + AdamW, "
+                               "Qwen2.5-1.5B shapes, NF4 layers streamed from pinned host memory",
+                   "rows": args.rows, "max_len": args.max_len,
+                   "tokens_per_step": tokens / args.steps, "lora": "r16 alpha32 dropout0.05 q,v"},
+        "roofline": roof,
+        "median_step_tokens_per_s": (tokens / args.steps) / statistics.median(per_step),
+        "peak_hbm_mib": (peak - base_alloc) / 2**20,
+        "kernels_calibration": kernel_rates(calib, 2),
+    }
+    lm = [calib[k] for k in MFMA_KERNELS if k in calib]
+    if lm:
+        out["lm_head_ce_tflops"] = sum(r["flops"] for r in lm) / (sum(r["ms"] for r in lm) / 1e3) / 1e12
+        out["lm_head_ce_tflops_credited_4NDV"] = (2.0 / 3.0) * out["lm_head_ce_tflops"]
+    if "nf4_dequant" in calib:
+        r = calib["nf4_dequant"]
+        out["nf4_dequant_gbps"] = r["bytes"] / (r["ms"] / 1e3) / 1e9
+
+    if not args.no_resident:
+        eng_r = Qwen2FusedEngine(model, dev, resident_weights=True)
+        s_r, t_r, _, _ = timed_run(eng_r, opt, batches, min(args.steps, 16), 1)
+        out["resident_weights_tokens_per_s"] = t_r / s_r
+        del eng_r
+
+    if not args.no_eager:
+        eng_e = Qwen2FusedEngine(model, dev, resident_weights=False)
+        b = batches[0]
+        pb = pack_varlen(b[0], b[1], b[2])
+        torch.cuda.synchronize()
+        torch.cuda.reset_peak_memory_stats(dev)
+        base_e = torch.cuda.memory_allocated(dev)
+        t0 = time.perf_counter()
+        for _ in range(2):
+            h = eng_e.host_head.embed(pb.input_ids)
+            loss = eager_step_loss(eng_e, h, pb.pos_ids, pb.shift_labels, pb.row_lengths, training=True)
+            loss.backward()
+            opt.step()
+            opt.zero_grad(set_to_none=True)
+        torch.cuda.synchronize()
+        out["eager_ms_per_step"] = (time.perf_counter() - t0) / 2 * 1e3
+        out["eager_tokens_per_s"] = b[3] / (out["eager_ms_per_step"] / 1e3)
+        out["eager_peak_hbm_mib"] = (torch.cuda.max_memory_allocated(dev) - base_e) / 2**20
+        del eng_e
+
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline(args.seed)
+    else:
+        out["cpu_baseline"] = None
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

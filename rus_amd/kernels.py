@@ -56,6 +56,50 @@ def _ptr(t: torch.Tensor | None) -> int | None:
     return None if t is None else t.data_ptr()
 
 
+class KernelTimer:
+    """Per-launch device timing for the launchers in this module: while active, every launch is
+    bracketed by two HIP events recorded on the stream it is enqueued on (the current stream) and
+    tagged with its algorithmic bytes and FLOPs. ``summary()`` synchronises and aggregates."""
+
+    active: "KernelTimer | None" = None
+
+    def __init__(self, only: set[str] | None = None):
+        self.only = only  # record only these kernels (None: all)
+        self.records: list[tuple[str, torch.cuda.Event, torch.cuda.Event, float, float]] = []
+
+    def __enter__(self):
+        KernelTimer.active = self
+        return self
+
+    def __exit__(self, *exc):
+        KernelTimer.active = None
+        return False
+
+    def summary(self) -> dict[str, dict]:
+        torch.cuda.synchronize()
+        out: dict[str, dict] = {}
+        for name, e0, e1, nbytes, flops in self.records:
+            r = out.setdefault(name, {"launches": 0, "ms": 0.0, "bytes": 0.0, "flops": 0.0})
+            r["launches"] += 1
+            r["ms"] += e0.elapsed_time(e1)
+            r["bytes"] += nbytes
+            r["flops"] += flops
+        return out
+
+
+def _launch(kernel: str, nbytes: float, flops: float, fn: str, *args) -> None:
+    """Calls C entry point ``fn``; under an active KernelTimer also records its duration."""
+    t = KernelTimer.active
+    if t is None or (t.only is not None and kernel not in t.only):
+        _lib.call(fn, *args)
+        return
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    _lib.call(fn, *args)
+    e1.record()
+    t.records.append((kernel, e0, e1, float(nbytes), float(flops)))
+
+
 # ---------------------------------------------------------------------------------------------
 # NF4 double-quant dequantisation (reference: kernels.py:27-118, launcher kernels.py:572-619)
 # ---------------------------------------------------------------------------------------------
@@ -134,7 +178,8 @@ def dequant_nf4_tensor(
         sb1 = sb2 = n_bytes
     if absmax2_bases is None:
         absmax2_bases = nf4_absmax2_bases(n_bytes, (sb1, sb2), blocksize, super_blocksize)
-    _lib.call(
+    _launch(
+        "nf4_dequant", n_bytes + absmax.numel() + 4 * absmax2.numel() + 1024 + 2 * n_elements, 0,
         "rus_nf4_dequant",
         packed.data_ptr(), absmax.data_ptr(), code2.data_ptr(), absmax2.data_ptr(),
         off0, off1, off2, sb1, sb2, int(absmax2_bases[0]), int(absmax2_bases[1]),
@@ -174,11 +219,13 @@ def rms_norm_fwd(
             raise ValueError(f"{fn}: residual must match x in shape and dtype")
         res_2d = residual.contiguous().view(-1, n_cols)
         sum_out = torch.empty_like(x_2d)
-        _lib.call("rus_rmsnorm_fwd", x_2d.data_ptr(), res_2d.data_ptr(), w.data_ptr(), wdt,
+        _launch("rmsnorm_fwd", 4 * n_rows * n_cols * x_2d.element_size() + w.numel() * w.element_size()
+                + 4 * n_rows, 0, "rus_rmsnorm_fwd", x_2d.data_ptr(), res_2d.data_ptr(), w.data_ptr(), wdt,
                   sum_out.data_ptr(), norm_out.data_ptr(), rstd.data_ptr(), n_rows, n_cols,
                   x_2d.stride(0), float(eps), dt, _stream(x))
         return norm_out.view(orig_shape), sum_out.view(orig_shape), rstd
-    _lib.call("rus_rmsnorm_fwd", x_2d.data_ptr(), None, w.data_ptr(), wdt, None,
+    _launch("rmsnorm_fwd", 2 * n_rows * n_cols * x_2d.element_size() + w.numel() * w.element_size()
+            + 4 * n_rows, 0, "rus_rmsnorm_fwd", x_2d.data_ptr(), None, w.data_ptr(), wdt, None,
               norm_out.data_ptr(), rstd.data_ptr(), n_rows, n_cols, x_2d.stride(0), float(eps), dt,
               _stream(x))
     return norm_out.view(orig_shape), x, rstd
@@ -214,7 +261,9 @@ def rms_norm_bwd(
         if dres_2d.dtype != h_2d.dtype or dres_2d.shape != h_2d.shape:
             raise ValueError(f"{fn}: dresidual must match h in shape and dtype")
         dres_ptr = dres_2d.data_ptr()
-    _lib.call("rus_rmsnorm_bwd", dy_2d.data_ptr(), h_2d.data_ptr(), w.data_ptr(), wdt,
+    _launch("rmsnorm_bwd", (4 if dres_ptr is not None else 3) * n_rows * n_cols * h_2d.element_size()
+            + w.numel() * w.element_size() + 4 * n_rows, 0,
+            "rus_rmsnorm_bwd", dy_2d.data_ptr(), h_2d.data_ptr(), w.data_ptr(), wdt,
               rs.data_ptr(), dres_ptr, dx.data_ptr(), n_rows, n_cols, dy_2d.stride(0), dt,
               _stream(dy))
     return dx.view(orig_shape)
@@ -274,8 +323,11 @@ def qkv_rope_fwd(
     q_out = torch.empty((n_tokens, h_q, head_dim), dtype=qkv.dtype, device=qkv.device)
     k_out = torch.empty((n_tokens, h_kv, head_dim), dtype=qkv.dtype, device=qkv.device)
     v_out = torch.empty((n_tokens, h_kv, head_dim), dtype=qkv.dtype, device=qkv.device)
-    _lib.call(
-        "rus_qkv_lora_rope_fwd",
+    es = qkv.element_size()
+    width = q_dim + 2 * kv_dim
+    _launch(
+        "rope_fwd", n_tokens * (es * (2 * width + (q_dim + kv_dim if has_lora else 0) + 2 * head_dim) + 8),
+        0, "rus_qkv_lora_rope_fwd",
         qkv.data_ptr(), _ptr(ql), _ptr(vl), cos.data_ptr(), sin.data_ptr(), pos.data_ptr(),
         q_out.data_ptr(), k_out.data_ptr(), v_out.data_ptr(), n_tokens, qkv.stride(0),
         ql.stride(0) if has_lora else 0, vl.stride(0) if has_lora else 0, cos.stride(0),
@@ -308,8 +360,11 @@ def _rope_bwd(fn, dq_rot, dk_rot, dv_out, cos, sin, pos_ids, h_q, h_kv, head_dim
     if with_lora:
         dql = torch.empty((n_tokens, q_dim), dtype=dq_c.dtype, device=dq_c.device)
         dvl = torch.empty((n_tokens, kv_dim), dtype=dq_c.dtype, device=dq_c.device)
-    _lib.call(
-        "rus_qkv_rope_bwd",
+    es = dq_c.element_size()
+    width = q_dim + 2 * kv_dim
+    _launch(
+        "rope_bwd", n_tokens * (es * (2 * width + 2 * head_dim + (q_dim + kv_dim if with_lora else 0)) + 8),
+        0, "rus_qkv_rope_bwd",
         dq_c.data_ptr(), dk_c.data_ptr(), dv_c.data_ptr(), cos.data_ptr(), sin.data_ptr(),
         pos.data_ptr(), dqkv.data_ptr(), _ptr(dql), _ptr(dvl), n_tokens, dqkv.stride(0),
         cos.stride(0), cos.shape[0], float(scale_q), float(scale_v), h_q, h_kv, head_dim, None,
@@ -374,7 +429,8 @@ def mlp_glu_fwd(gate_or_gu: torch.Tensor, up: torch.Tensor | None = None) -> tor
         n_rows = gu_2d.shape[0]
         out_2d = torch.empty((n_rows, n_cols), dtype=gate_or_gu.dtype, device=gate_or_gu.device)
         base = gu_2d.data_ptr()
-        _lib.call("rus_swiglu_fwd", base, base + n_cols * gu_2d.element_size(), out_2d.data_ptr(),
+        _launch("swiglu_fwd", 3 * n_rows * n_cols * gu_2d.element_size(), 0,
+                "rus_swiglu_fwd", base, base + n_cols * gu_2d.element_size(), out_2d.data_ptr(),
                   n_rows, n_cols, gu_2d.stride(0), gu_2d.stride(0), out_2d.stride(0), dt,
                   _stream(gu_2d))
         return out_2d.view(*orig_shape[:-1], n_cols)
@@ -386,7 +442,8 @@ def mlp_glu_fwd(gate_or_gu: torch.Tensor, up: torch.Tensor | None = None) -> tor
     up_2d = up.contiguous().view(-1, n_cols)
     n_rows = gate_2d.shape[0]
     out_2d = torch.empty((n_rows, n_cols), dtype=gate_or_gu.dtype, device=gate_or_gu.device)
-    _lib.call("rus_swiglu_fwd", gate_2d.data_ptr(), up_2d.data_ptr(), out_2d.data_ptr(), n_rows,
+    _launch("swiglu_fwd", 3 * n_rows * n_cols * gate_2d.element_size(), 0,
+            "rus_swiglu_fwd", gate_2d.data_ptr(), up_2d.data_ptr(), out_2d.data_ptr(), n_rows,
               n_cols, gate_2d.stride(0), up_2d.stride(0), out_2d.stride(0), dt, _stream(gate_2d))
     return out_2d.view(orig_shape)
 
@@ -417,7 +474,8 @@ def mlp_glu_bwd(
             raise ValueError(f"{fn}: dgu_out must match [gate|up] in shape and dtype")
         es = gu_2d.element_size()
         g, d = gu_2d.data_ptr(), dgu_2d.data_ptr()
-        _lib.call("rus_swiglu_bwd", dout_2d.data_ptr(), g, g + n_cols * es, d, d + n_cols * es,
+        _launch("swiglu_bwd", 5 * n_rows * n_cols * es, 0,
+                "rus_swiglu_bwd", dout_2d.data_ptr(), g, g + n_cols * es, d, d + n_cols * es,
                   n_rows, n_cols, dout_2d.stride(0), gu_2d.stride(0), gu_2d.stride(0),
                   dgu_2d.stride(0), dgu_2d.stride(0), dt, _stream(dout_2d))
         return dgu_2d
@@ -431,7 +489,8 @@ def mlp_glu_bwd(
         raise ValueError(f"{fn}: dout, gate and up must match in shape")
     dg_2d = torch.empty_like(dout_2d)
     du_2d = torch.empty_like(dout_2d)
-    _lib.call("rus_swiglu_bwd", dout_2d.data_ptr(), gate_2d.data_ptr(), up_2d.data_ptr(),
+    _launch("swiglu_bwd", 5 * n_rows * n_cols * gate_2d.element_size(), 0,
+            "rus_swiglu_bwd", dout_2d.data_ptr(), gate_2d.data_ptr(), up_2d.data_ptr(),
               dg_2d.data_ptr(), du_2d.data_ptr(), n_rows, n_cols, dout_2d.stride(0),
               gate_2d.stride(0), up_2d.stride(0), dg_2d.stride(0), du_2d.stride(0), dt,
               _stream(dout_2d))
@@ -510,7 +569,9 @@ def lm_head_ce_fwd_chunk(hidden: torch.Tensor, weight_rows: torch.Tensor, labels
     if lab.dtype != torch.int64 or lab.numel() != n_tok:
         raise ValueError(f"{fn}: labels must be int64 with {n_tok} entries")
     lab = lab.contiguous()
-    _lib.call("rus_lmhead_ce_fwd", h.data_ptr(), w.data_ptr(), lab.data_ptr(), n_tok, d,
+    _launch("lmhead_ce_fwd", (n_tok + n_vocab) * d * 2 + 16 * n_tok * lm_head_num_parts(n_vocab),
+            2.0 * n_tok * d * n_vocab,
+            "rus_lmhead_ce_fwd", h.data_ptr(), w.data_ptr(), lab.data_ptr(), n_tok, d,
               h.stride(0), w.stride(0), n_vocab, vocab_start, parts.m.data_ptr(),
               parts.s.data_ptr(), parts.w.data_ptr(), parts.idx.data_ptr(), part_base, n_tok,
               target.data_ptr(), _stream(h))
@@ -528,7 +589,8 @@ def lm_head_ce_combine(parts: LMHeadPartials, target: torch.Tensor, labels: torc
     ent = torch.empty(n, dtype=torch.float32, device=dev)
     amax = torch.empty(n, dtype=torch.int64, device=dev)
     lab = labels.reshape(-1).contiguous()
-    _lib.call("rus_lmhead_ce_combine", parts.m.data_ptr(), parts.s.data_ptr(), parts.w.data_ptr(),
+    _launch("lmhead_ce_combine", 16 * n * parts.n_parts + 32 * n, 0,
+            "rus_lmhead_ce_combine", parts.m.data_ptr(), parts.s.data_ptr(), parts.w.data_ptr(),
               parts.idx.data_ptr(), parts.n_parts, n, target.data_ptr(), lab.data_ptr(), n,
               lse.data_ptr(), nll.data_ptr(), ent.data_ptr(), amax.data_ptr(), _stream(target))
     return lse, nll, ent, amax
@@ -550,7 +612,9 @@ def lm_head_ce_grad_logits(hidden: torch.Tensor, weight_rows: torch.Tensor, labe
     if denom.dtype != torch.float32 or denom.numel() != 1:
         raise ValueError(f"{fn}: denom must be a one-element float32 device tensor")
     lab = labels.reshape(-1).contiguous()
-    _lib.call("rus_lmhead_ce_grad_logits", h.data_ptr(), w.data_ptr(), lab.data_ptr(),
+    _launch("lmhead_ce_grad_logits", (n_tok + n_vocab) * d * 2 + n_tok * _round_up(n_vocab, LM_K) * 2,
+            2.0 * n_tok * d * n_vocab,
+            "rus_lmhead_ce_grad_logits", h.data_ptr(), w.data_ptr(), lab.data_ptr(),
               lse.data_ptr(), denom.data_ptr(), n_tok, d, h.stride(0), w.stride(0), n_vocab,
               vocab_start, out.data_ptr(), out.stride(0), _stream(h))
     return out
@@ -572,7 +636,10 @@ def lm_head_ce_grad_hidden(grad_logits: torch.Tensor, weight_t_cols: torch.Tenso
             raise ValueError(f"{fn}: {name} must be fp16 with contiguous rows")
         if t.shape[0] * t.stride(0) * 2 >= 1 << 32:
             raise ValueError(f"{fn}: {name} exceeds the 4 GiB operand limit of the MFMA kernels")
-    _lib.call("rus_lmhead_ce_grad_hidden", grad_logits.data_ptr(), grad_logits.stride(0),
+    kp = _round_up(n_vocab, LM_K)
+    _launch("lmhead_ce_grad_hidden", (n_tok + d) * kp * 2 + 4 * n_split * n_tok * d * (2 if accumulate else 1),
+            2.0 * n_tok * d * n_vocab,
+            "rus_lmhead_ce_grad_hidden", grad_logits.data_ptr(), grad_logits.stride(0),
               weight_t_cols.data_ptr(), weight_t_cols.stride(0), n_tok, d, n_vocab,
               parts.data_ptr(), n_split, 1 if accumulate else 0, _stream(grad_logits))
 
@@ -588,7 +655,8 @@ def lm_head_dh_reduce(parts: torch.Tensor, scale: float, out_dtype=torch.float16
     if scale_dev is not None and (scale_dev.dtype != torch.float32 or scale_dev.numel() != 1):
         raise ValueError(f"{fn}: scale_dev must be a one-element float32 tensor")
     out = torch.empty(parts.shape[1:], dtype=out_dtype, device=parts.device)
-    _lib.call("rus_lmhead_dh_reduce", parts.data_ptr(), parts.shape[0], out.numel(), float(scale),
+    _launch("lmhead_dh_reduce", parts.numel() * 4 + out.numel() * out.element_size(), 0,
+            "rus_lmhead_dh_reduce", parts.data_ptr(), parts.shape[0], out.numel(), float(scale),
               _ptr(scale_dev), out.data_ptr(), _dtype_code(fn, out_dtype), _stream(parts))
     return out
 

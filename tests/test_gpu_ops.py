@@ -27,8 +27,8 @@ def test_rms_norm_autograd(dtype, has_residual, shape):
     res = torch.randn(shape, generator=g).to(dtype) if has_residual else None
     gy = torch.randn(shape, generator=g).to(dtype)
     # reference formula (test_kernels.py:64-69), autograd on the CPU in fp32
-    xr = x.float().requires_grad_(True)
-    rr = res.float().requires_grad_(True) if has_residual else None
+    xr = x.detach().float().clone().requires_grad_(True)
+    rr = res.detach().float().clone().requires_grad_(True) if has_residual else None
     h = (xr + rr).to(dtype).float() if has_residual else xr
     y_ref = w.float() * (h * torch.rsqrt(h.pow(2).mean(-1, keepdim=True) + 1e-6)).to(dtype).float()
     y_ref.backward(gy.float())
@@ -63,9 +63,9 @@ def test_qkv_lora_rope_autograd(dtype, n_tokens):
     dq, dk, dv = (torch.randn(n_tokens, h, hd, generator=g).to(dtype) for h in (hq, hkv, hkv))
 
     # reference formula (test_kernels.py:111-131) with CPU autograd in fp32
-    a = qkv.float().requires_grad_(True)
-    b = ql.float().requires_grad_(True)
-    c = vl.float().requires_grad_(True)
+    a = qkv.float().clone().requires_grad_(True)
+    b = ql.float().clone().requires_grad_(True)
+    c = vl.float().clone().requires_grad_(True)
 
     def rot_half(t):
         return torch.cat((-t[..., hd // 2:], t[..., : hd // 2]), dim=-1)
@@ -99,7 +99,7 @@ def test_mlp_glu_autograd(dtype, fused, shape):
     gate = torch.randn(shape, generator=g).to(dtype)
     up = torch.randn(shape, generator=g).to(dtype)
     grad = torch.randn(shape, generator=g).to(dtype)
-    gr, ur = gate.float().requires_grad_(True), up.float().requires_grad_(True)
+    gr, ur = gate.float().clone().requires_grad_(True), up.float().clone().requires_grad_(True)
     ref_out = F.silu(gr) * ur
     ref_out.backward(grad.float())
     if fused:
@@ -128,7 +128,7 @@ def test_chunked_lm_head_autograd():
     labels[:, :8] = -100
     shift = torch.full((B, S), -100, dtype=torch.long)
     shift[:, :-1] = labels[:, 1:]
-    hr = hidden.float().requires_grad_(True)
+    hr = hidden.float().clone().requires_grad_(True)
     logits = hr @ weight.float().t()
     loss_ref = F.cross_entropy(logits[:, :-1].reshape(-1, V), labels[:, 1:].reshape(-1), ignore_index=-100)
     loss_ref.backward()
