@@ -241,7 +241,8 @@ class Qwen2FusedEngine:
 
     def __init__(self, model, device, resident_weights: bool = False, resident_head: bool = True,
                  offload_inputs: bool = False, max_pos: int = 2048,
-                 max_mlp_tokens: int = MAX_MLP_TOKENS, v_chunk: int = V_CHUNK_DEFAULT):
+                 max_mlp_tokens: int = MAX_MLP_TOKENS, v_chunk: int = V_CHUNK_DEFAULT,
+                 attention: str = "varlen"):
         from .model import QLoRAQwen2
 
         if not isinstance(model, QLoRAQwen2):
@@ -273,6 +274,36 @@ class Qwen2FusedEngine:
              "p_v": cfg.lora_dropout} for _ in model.layers]
         self.cos_table, self.sin_table = rope_cache(max_pos, self.head_dim, cfg.rope_theta,
                                                     self.device)
+        if attention not in ("varlen", "sdpa_rows"):
+            raise ValueError("attention must be 'varlen' (one flash launch over all packed rows) "
+                             "or 'sdpa_rows' (torch SDPA per row, as the reference)")
+        self.attention = attention
+        self._flatten_lora()
+
+    def _flatten_lora(self) -> None:
+        """Makes the LoRA parameters views of one flat fp32 device buffer (same Parameter
+        objects, so optimizers keep working) so that their fp16 copies for a step are one cast."""
+        params = self.lora_params
+        flat = torch.cat([p.detach().reshape(-1).to(self.device, torch.float32) for p in params])
+        off = 0
+        for p in params:
+            n = p.numel()
+            p.data = flat[off: off + n].view(p.shape)
+            off += n
+        self._lora_flat = flat
+        self._lora_ptrs = [p.data_ptr() for p in params]
+
+    def lora_fp16(self) -> list[torch.Tensor]:
+        """fp16 copies of [q_A, q_B, v_A, v_B] per layer for one step (one cast kernel)."""
+        if [p.data_ptr() for p in self.lora_params] != self._lora_ptrs:
+            self._flatten_lora()  # a parameter was re-assigned since the last step
+        flat16 = self._lora_flat.to(torch.float16)
+        out, off = [], 0
+        for p in self.lora_params:
+            n = p.numel()
+            out.append(flat16[off: off + n].view(p.shape))
+            off += n
+        return out
 
 
 def _run_packed_sdpa(q_rot, k_rot, v_out, row_lengths, num_heads, num_kv_heads, head_dim):
@@ -297,11 +328,37 @@ def _run_packed_sdpa(q_rot, k_rot, v_out, row_lengths, num_heads, num_kv_heads, 
     return out
 
 
+class VarlenMeta:
+    """cu_seqlens of the packed rows (int32 on the device) and the longest row."""
+
+    def __init__(self, row_lengths, device):
+        lens = [int(L) for L in row_lengths if L > 0]
+        cu = [0]
+        for L in lens:
+            cu.append(cu[-1] + L)
+        self.cu = torch.tensor(cu, dtype=torch.int32, device=device)
+        self.max_len = max(lens) if lens else 0
+
+
+def _varlen_attn_fwd(q, k, v, vm: VarlenMeta):
+    """Causal GQA flash attention over all packed rows in one launch: q [N, Hq, D], k/v
+    [N, Hkv, D] (the RoPE kernel's output layout) -> (out [N, Hq, D], lse, rng, unused)."""
+    out, lse, rng, unused, _ = torch.ops.aten._flash_attention_forward(
+        q, k, v, vm.cu, vm.cu, vm.max_len, vm.max_len, 0.0, True, False)
+    return out, lse, rng, unused
+
+
+def _varlen_attn_bwd(dout, q, k, v, out, lse, rng, unused, vm: VarlenMeta):
+    dq, dk, dv = torch.ops.aten._flash_attention_backward(
+        dout, q, k, v, out, lse, vm.cu, vm.cu, vm.max_len, vm.max_len, 0.0, True, rng, unused)
+    return dq, dk, dv
+
+
 def _lora_deltas(norm1, q_A, q_B, v_A, v_B, meta, training):
     """(x_drop_q, mid_q, q_lora, x_drop_v, mid_v, v_lora, fp16 A/B) with the dropout order of
     solution/ops.py:775-778 (q first, then v)."""
     dt = norm1.dtype
-    qA, qB, vA, vB = q_A.to(dt), q_B.to(dt), v_A.to(dt), v_B.to(dt)
+    qA, qB, vA, vB = (p if p.dtype == dt else p.to(dt) for p in (q_A, q_B, v_A, v_B))
     x_q = F.dropout(norm1, p=meta["p_q"], training=True) if (training and meta["p_q"] > 0) else norm1
     mid_q = F.linear(x_q, qA)
     q_lora = F.linear(mid_q, qB)
@@ -339,6 +396,10 @@ class FusedQwen2StackFn(torch.autograd.Function):
         rng_states = []
         h = h_packed.contiguous()
         carry = None  # (h_mid, mlp_out) of the previous layer, added inside the next norm
+        n_tok = h.shape[0]
+        hq, hd = engine.num_heads, engine.head_dim
+        vm = VarlenMeta(row_lengths, engine.device) if engine.attention == "varlen" else None
+        lora16 = engine.lora_fp16()
         if L > 0:
             ws.prefetch(0)
         for l in range(L):
@@ -353,14 +414,17 @@ class FusedQwen2StackFn(torch.autograd.Function):
             ws.wait_slot(l)
             qkv = F.linear(norm1, ws.dequant(l, "qkv"), engine.layer_biases[l])
             meta = engine.layer_lora_meta[l]
-            _, _, q_lora, _, _, v_lora, _ = _lora_deltas(norm1, *lora_params[4 * l: 4 * l + 4], meta, training)
+            _, _, q_lora, _, _, v_lora, _ = _lora_deltas(norm1, *lora16[4 * l: 4 * l + 4], meta, training)
             q_rot, k_rot, v_out = K.qkv_rope_fwd(qkv, cos, sin, pos_ids, q_lora=q_lora, v_lora=v_lora,
                                                  scale_q=meta["scale_q"], scale_v=meta["scale_v"],
                                                  h_q=engine.num_heads, h_kv=engine.num_kv_heads,
                                                  head_dim=engine.head_dim)
             del qkv, q_lora, v_lora, norm1
-            attn = _run_packed_sdpa(q_rot, k_rot, v_out, row_lengths, engine.num_heads,
-                                    engine.num_kv_heads, engine.head_dim)
+            if vm is not None:
+                attn = _varlen_attn_fwd(q_rot, k_rot, v_out, vm)[0].view(n_tok, hq * hd)
+            else:
+                attn = _run_packed_sdpa(q_rot, k_rot, v_out, row_lengths, engine.num_heads,
+                                        engine.num_kv_heads, engine.head_dim)
             del q_rot, k_rot, v_out
             o_out = F.linear(attn, ws.dequant(l, "o"))
             del attn
@@ -377,6 +441,8 @@ class FusedQwen2StackFn(torch.autograd.Function):
                                                             eps=eps, residual=carry[0])
         ctx.save_for_backward(pos_ids, h_last, final_rstd, *lora_params)
         ctx.row_lengths = row_lengths
+        ctx.vm = vm
+        ctx.lora16 = lora16
         ctx.engine = engine
         ctx.training = training
         ctx.rng_states = rng_states
@@ -421,17 +487,22 @@ class FusedQwen2StackFn(torch.autograd.Function):
             meta = engine.layer_lora_meta[l]
             q_A, q_B, v_A, v_B = lora_params[4 * l: 4 * l + 4]
             x_q, mid_q, q_lora, x_v, mid_v, v_lora, (qA, qB, vA, vB) = _lora_deltas(
-                norm1, q_A, q_B, v_A, v_B, meta, training)
+                norm1, *ctx.lora16[4 * l: 4 * l + 4], meta, training)
             q_rot, k_rot, v_out = K.qkv_rope_fwd(qkv, cos, sin, pos_ids, q_lora=q_lora, v_lora=v_lora,
                                                  scale_q=meta["scale_q"], scale_v=meta["scale_v"],
                                                  h_q=hq, h_kv=hkv, head_dim=hd)
             del qkv, q_lora, v_lora
-            with torch.enable_grad():
-                q_req = q_rot.detach().requires_grad_(True)
-                k_req = k_rot.detach().requires_grad_(True)
-                v_req = v_out.detach().requires_grad_(True)
-                attn = _run_packed_sdpa(q_req, k_req, v_req, ctx.row_lengths, hq, hkv, hd)
-            o_out = F.linear(attn.detach(), w_o)
+            if ctx.vm is not None:
+                attn, lse, rng, unused = _varlen_attn_fwd(q_rot, k_rot, v_out, ctx.vm)
+                attn2d = attn.view(n_tokens, q_dim)
+            else:
+                with torch.enable_grad():
+                    q_req = q_rot.detach().requires_grad_(True)
+                    k_req = k_rot.detach().requires_grad_(True)
+                    v_req = v_out.detach().requires_grad_(True)
+                    attn = _run_packed_sdpa(q_req, k_req, v_req, ctx.row_lengths, hq, hkv, hd)
+                attn2d = attn.detach()
+            o_out = F.linear(attn2d, w_o)
             norm2, h_mid, rstd2 = K.rms_norm_fwd(o_out, engine.ln2_weights[l], eps=eps, residual=h_in)
             del o_out
 
@@ -450,8 +521,14 @@ class FusedQwen2StackFn(torch.autograd.Function):
 
             # Attention backward, adjoint RoPE with [dQ|dK|dV] packing and LoRA-delta gradients.
             d_attn = torch.mm(dh_mid, w_o)
-            dq, dk, dv = torch.autograd.grad(attn, (q_req, k_req, v_req), d_attn)
-            del attn, q_req, k_req, v_req, d_attn, q_rot, k_rot, v_out
+            if ctx.vm is not None:
+                dq, dk, dv = _varlen_attn_bwd(d_attn.view(n_tokens, hq, hd), q_rot, k_rot, v_out,
+                                              attn, lse, rng, unused, ctx.vm)
+                del lse, rng, unused
+            else:
+                dq, dk, dv = torch.autograd.grad(attn, (q_req, k_req, v_req), d_attn)
+                del q_req, k_req, v_req
+            del attn, attn2d, d_attn, q_rot, k_rot, v_out
             dqkv, dq_scaled, dv_scaled = K.qkv_rope_bwd_lora(dq, dk, dv, cos, sin, pos_ids,
                                                              meta["scale_q"], meta["scale_v"],
                                                              h_q=hq, h_kv=hkv, head_dim=hd)

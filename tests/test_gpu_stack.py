@@ -57,11 +57,12 @@ def _rel(a, b):
     return float((a.float() - b.float()).norm() / (b.float().norm() + 1e-30))
 
 
-@pytest.mark.parametrize("resident", [False, True])
-def test_fused_stack_matches_cpu_oracle(resident):
+@pytest.mark.parametrize("resident,attention", [(False, "varlen"), (True, "varlen"),
+                                                (True, "sdpa_rows")])
+def test_fused_stack_matches_cpu_oracle(resident, attention):
     cfg = small_config()
     model = M.build_random_qlora_qwen2(cfg, DEV, seed=1, std=0.05)
-    engine = ops.Qwen2FusedEngine(model, DEV, resident_weights=resident)
+    engine = ops.Qwen2FusedEngine(model, DEV, resident_weights=resident, attention=attention)
     ids, mask, labels = _batch(cfg, [37, 64, 21])
     pb = ops.pack_varlen(ids, mask, labels)
     loss, grads = _fused_step(engine, pb, training=False)
