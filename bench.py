@@ -145,6 +145,44 @@ def cpu_baseline(seed=0):
                        f"28*{t_layer:.3f}s + {t_head:.3f}s (lm_head)")}
 
 
+def kernel_probe(reps: int = 5) -> None:
+    """Fixed launches for hardware-counter runs: a plain 128 MiB device copy (the calibration for
+    the FETCH_SIZE / WRITE_SIZE counters) and one config-5 layer's four-segment NF4 dequant."""
+    import torch
+
+    from rus_amd import model as M
+    from rus_amd.hostload import WeightStream
+
+    dev = torch.device("cuda:0")
+    cfg = M.qwen2_1p5b()
+    cfg1 = M.Qwen2Config(**{**cfg.__dict__, "num_hidden_layers": 1})
+    model = M.build_random_qlora_qwen2(cfg1, dev, seed=0)
+    ws = WeightStream(model.layers, dev, resident=True)
+    src = torch.empty(64 << 20, dtype=torch.float16, device=dev).normal_()
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(f"probe: {reps} copies of {src.numel() * 2} bytes", flush=True)
+    for _ in range(reps):
+        ws.dequant_layer(0)
+    torch.cuda.synchronize()
+    print(f"probe: {reps} four-segment dequants of layer 0", flush=True)
+
+
+def measured_traffic(kernel: str):
+    """HBM bytes per launch of ``kernel`` from the committed counter summary, if there is one."""
+    path = os.path.join(REPO, "profiles", f"{kernel}_traffic_config5.txt")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        for line in f:
+            if line.startswith("traffic_bytes_per_launch"):
+                return float(line.split("=")[1])
+    return None
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -156,11 +194,16 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-eager", action="store_true")
     ap.add_argument("--no-resident", action="store_true")
+    ap.add_argument("--probe", action="store_true",
+                    help="only the fixed copy + dequant launches used for counter runs")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); the "
               "multi-GPU design is described in DESIGN.md", file=sys.stderr)
         return 2
+    if args.probe:
+        kernel_probe()
+        return 0
 
     import torch
 
@@ -196,8 +239,11 @@ def main() -> int:
     else:
         achieved = d["bytes"] / (d["ms"] / 1e3) / 1e9
         roof = {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": achieved / HBM_PEAK_GBS, "traffic": None}
+                "frac": achieved / HBM_PEAK_GBS, "traffic": measured_traffic(dominant)}
+    from rus_amd.kernels import KernelTimer
+
     roof.update({"kernel": dominant, "avg_launch_ms": avg_ms, "launches": d["launches"],
+                 "event_pair_overhead_ms": KernelTimer.pair_overhead_ms(),
                  "per_launch": d["flops"] / d["launches"] if dominant in MFMA_KERNELS
                  else d["bytes"] / d["launches"]})
 

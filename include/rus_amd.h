@@ -67,6 +67,28 @@ int rus_nf4_dequant(const uint8_t* packed, const uint8_t* absmax, const float* c
                     int64_t n_absmax2, int32_t blocksize, int32_t super_blocksize,
                     uint32_t* out_u32, void* stream);
 
+/* One segment job of rus_nf4_dequant_multi: the per-segment arguments of rus_nf4_dequant. */
+typedef struct rus_nf4_job {
+  const uint8_t* packed;
+  const uint8_t* absmax;
+  const float* absmax2;
+  float off0, off1, off2;
+  int64_t split_byte_1, split_byte_2;
+  int64_t absmax2_base_1, absmax2_base_2;
+  int64_t n_bytes, n_absmax, n_absmax2;
+  uint32_t* out_u32;
+} rus_nf4_job;
+
+/*
+ * rus_nf4_dequant over 1..4 independent segment jobs (e.g. the four fused segments
+ * [q|k|v], o, [gate|up], down of one layer) in a single launch, sharing one code2 table and one
+ * (blocksize, super_blocksize). Each job is validated as rus_nf4_dequant validates its arguments.
+ * Replaces: the per-segment WeightStream.dequant calls of solution/hostload.py:325-342 (one launch
+ *           per segment there); no single reference counterpart.
+ */
+int rus_nf4_dequant_multi(const rus_nf4_job* jobs, int32_t n_jobs, const float* code2,
+                          int32_t blocksize, int32_t super_blocksize, void* stream);
+
 /*
  * Fused residual add + RMSNorm forward, one row per wavefront.
  * Replaces: solution/kernels.py:125-163 (rms_norm_residual_fwd_kernel), launcher

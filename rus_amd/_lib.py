@@ -21,10 +21,24 @@ _i64 = ctypes.c_int64
 _i32 = ctypes.c_int32
 _f32 = ctypes.c_float
 
+class Nf4Job(ctypes.Structure):
+    """struct rus_nf4_job of include/rus_amd.h."""
+
+    _fields_ = [
+        ("packed", ctypes.c_void_p), ("absmax", ctypes.c_void_p), ("absmax2", ctypes.c_void_p),
+        ("off0", ctypes.c_float), ("off1", ctypes.c_float), ("off2", ctypes.c_float),
+        ("split_byte_1", ctypes.c_int64), ("split_byte_2", ctypes.c_int64),
+        ("absmax2_base_1", ctypes.c_int64), ("absmax2_base_2", ctypes.c_int64),
+        ("n_bytes", ctypes.c_int64), ("n_absmax", ctypes.c_int64), ("n_absmax2", ctypes.c_int64),
+        ("out_u32", ctypes.c_void_p),
+    ]
+
+
 # name -> argtypes, in the order of include/rus_amd.h. Every entry point returns int.
 SIGNATURES: dict[str, list] = {
     "rus_nf4_dequant": [_vp, _vp, _vp, _vp, _f32, _f32, _f32, _i64, _i64, _i64, _i64, _i64, _i64,
                         _i64, _i32, _i32, _vp, _vp],
+    "rus_nf4_dequant_multi": [ctypes.POINTER(Nf4Job), _i32, _vp, _i32, _i32, _vp],
     "rus_rmsnorm_fwd": [_vp, _vp, _vp, _i32, _vp, _vp, _vp, _i64, _i64, _i64, _f32, _i32, _vp],
     "rus_rmsnorm_bwd": [_vp, _vp, _vp, _i32, _vp, _vp, _vp, _i64, _i64, _i64, _i32, _vp],
     "rus_qkv_lora_rope_fwd": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64,

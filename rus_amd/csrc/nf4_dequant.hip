@@ -93,19 +93,16 @@ __device__ __forceinline__ uint32_t decode_byte(uint32_t b, float scale,
   return __builtin_bit_cast(uint32_t, r);
 }
 
+// Dequantises block `blk` (of `nblk`) of one segment job; the LDS tables are already loaded.
 template <int UNROLL>
-__global__ __launch_bounds__(kThreads) void nf4_dequant_kernel(Nf4Args a) {
-  __shared__ float s_code2[256];
-  __shared__ float s_nf4[16];
+__device__ __forceinline__ void dequant_block(const Nf4Args& a, uint32_t blk, uint32_t nblk,
+                                              const float* __restrict__ s_code2,
+                                              const float* __restrict__ s_nf4) {
   const uint32_t t = threadIdx.x;
-  s_code2[t] = a.code2[t];
-  if (t < 16) s_nf4[t] = kNF4[t];
-  __syncthreads();
-
-  const uint32_t base = blockIdx.x * (kThreads * UNROLL) + t;
+  const uint32_t base = blk * (kThreads * UNROLL) + t;
   uint32_t p[UNROLL];
   float sc[UNROLL];
-  if ((blockIdx.x + 1) * (kThreads * UNROLL) <= a.n_units) {
+  if ((blk + 1) * (kThreads * UNROLL) <= a.n_units) {
     // Whole block in range (all but the last block): no per-unit checks, all loads issued first.
 #pragma unroll
     for (int u = 0; u < UNROLL; ++u) p[u] = a.packed[base + u * kThreads];
@@ -146,13 +143,50 @@ __global__ __launch_bounds__(kThreads) void nf4_dequant_kernel(Nf4Args a) {
   }
 
   // Trailing bytes that do not fill a 4-byte unit (n_bytes % 4 != 0): the last block does them.
-  if (blockIdx.x == gridDim.x - 1) {
+  if (blk == nblk - 1) {
     const uint32_t byte = a.n_units * 4u + t;
     if (byte < a.n_bytes) {
       const float s = block_scale(a, byte, s_code2);
       a.out[byte] = decode_byte(a.packed_bytes[byte], s, s_nf4);
     }
   }
+}
+
+__device__ __forceinline__ void load_tables(const float* __restrict__ code2, float* s_code2,
+                                            float* s_nf4) {
+  const uint32_t t = threadIdx.x;
+  s_code2[t] = code2[t];
+  if (t < 16) s_nf4[t] = kNF4[t];
+  __syncthreads();
+}
+
+template <int UNROLL>
+__global__ __launch_bounds__(kThreads) void nf4_dequant_kernel(Nf4Args a) {
+  __shared__ float s_code2[256];
+  __shared__ float s_nf4[16];
+  load_tables(a.code2, s_code2, s_nf4);
+  dequant_block<UNROLL>(a, blockIdx.x, gridDim.x, s_code2, s_nf4);
+}
+
+constexpr int kMaxJobs = 4;
+
+// Up to four segment jobs in one launch: blocks [start[j], start[j+1]) belong to job j.
+struct Nf4Multi {
+  Nf4Args job[kMaxJobs];
+  uint32_t start[kMaxJobs + 1];
+  int n_jobs;
+};
+
+template <int UNROLL>
+__global__ __launch_bounds__(kThreads) void nf4_dequant_multi_kernel(Nf4Multi m) {
+  __shared__ float s_code2[256];
+  __shared__ float s_nf4[16];
+  load_tables(m.job[0].code2, s_code2, s_nf4);  // one code2 table for every job
+  int j = 0;
+#pragma unroll
+  for (int k = 1; k < kMaxJobs; ++k) j += (k < m.n_jobs && blockIdx.x >= m.start[k]) ? 1 : 0;
+  dequant_block<UNROLL>(m.job[j], blockIdx.x - m.start[j], m.start[j + 1] - m.start[j], s_code2,
+                        s_nf4);
 }
 
 bool is_pow2(int64_t v) { return v > 0 && (v & (v - 1)) == 0; }
@@ -166,61 +200,55 @@ int ilog2(int64_t v) {
 }  // namespace
 }  // namespace rus
 
-extern "C" int rus_nf4_dequant(const uint8_t* packed, const uint8_t* absmax, const float* code2,
-                               const float* absmax2, float off0, float off1, float off2,
-                               int64_t split_byte_1, int64_t split_byte_2, int64_t absmax2_base_1,
-                               int64_t absmax2_base_2, int64_t n_bytes, int64_t n_absmax,
-                               int64_t n_absmax2, int32_t blocksize, int32_t super_blocksize,
-                               uint32_t* out_u32, void* stream) {
-  using namespace rus;
-  if (n_bytes < 0 || n_bytes >= (int64_t(1) << 31))
-    return fail(RUS_ERR_UNSUPPORTED, "rus_nf4_dequant: n_bytes=%lld outside [0, 2^31)",
-                (long long)n_bytes);
-  if (n_bytes == 0) return RUS_OK;
+namespace rus {
+namespace {
+
+constexpr int kUnrollMain = 4;
+
+// Validates one segment job and fills its kernel arguments (see rus_nf4_dequant).
+int make_job(const char* fn, const uint8_t* packed, const uint8_t* absmax, const float* code2,
+             const float* absmax2, float off0, float off1, float off2, int64_t split_byte_1,
+             int64_t split_byte_2, int64_t absmax2_base_1, int64_t absmax2_base_2,
+             int64_t n_bytes, int64_t n_absmax, int64_t n_absmax2, int32_t blocksize,
+             int32_t super_blocksize, uint32_t* out_u32, Nf4Args& a) {
+  if (n_bytes <= 0 || n_bytes >= (int64_t(1) << 31))
+    return fail(RUS_ERR_UNSUPPORTED, "%s: n_bytes=%lld outside [1, 2^31)", fn, (long long)n_bytes);
   if (!packed || !absmax || !code2 || !absmax2 || !out_u32)
-    return fail(RUS_ERR_INVALID, "rus_nf4_dequant: null pointer argument");
+    return fail(RUS_ERR_INVALID, "%s: null pointer argument", fn);
   if (!is_pow2(blocksize) || blocksize < 8 || !is_pow2(super_blocksize))
     return fail(RUS_ERR_INVALID,
-                "rus_nf4_dequant: blocksize=%d (power of two >= 8) / super_blocksize=%d "
-                "(power of two) invalid",
-                blocksize, super_blocksize);
+                "%s: blocksize=%d (power of two >= 8) / super_blocksize=%d (power of two) invalid",
+                fn, blocksize, super_blocksize);
   if (!aligned(packed, 4) || !aligned(out_u32, 16))
-    return fail(RUS_ERR_INVALID,
-                "rus_nf4_dequant: packed must be 4-byte and out 16-byte aligned");
+    return fail(RUS_ERR_INVALID, "%s: packed must be 4-byte and out 16-byte aligned", fn);
   const int64_t half_block = blocksize / 2;
   if (split_byte_1 < 0 || split_byte_2 < split_byte_1 || split_byte_2 > n_bytes)
-    return fail(RUS_ERR_INVALID, "rus_nf4_dequant: splits (%lld, %lld) not ordered in [0, %lld]",
+    return fail(RUS_ERR_INVALID, "%s: splits (%lld, %lld) not ordered in [0, %lld]", fn,
                 (long long)split_byte_1, (long long)split_byte_2, (long long)n_bytes);
   if ((split_byte_1 < n_bytes && split_byte_1 % half_block) ||
       (split_byte_2 < n_bytes && split_byte_2 % half_block))
     return fail(RUS_ERR_INVALID,
-                "rus_nf4_dequant: segment starts (%lld, %lld) must be multiples of blocksize/2=%lld",
+                "%s: segment starts (%lld, %lld) must be multiples of blocksize/2=%lld", fn,
                 (long long)split_byte_1, (long long)split_byte_2, (long long)half_block);
   if (absmax2_base_1 < 0 || absmax2_base_2 < absmax2_base_1)
-    return fail(RUS_ERR_INVALID, "rus_nf4_dequant: absmax2 bases must be non-negative, ordered");
-
+    return fail(RUS_ERR_INVALID, "%s: absmax2 bases must be non-negative, ordered", fn);
   // Every absmax / absmax2 index the kernel can form must be in range.
-  {
-    const int hb = ilog2(half_block), sb = ilog2(super_blocksize);
-    const int64_t last_blk = (n_bytes - 1) >> hb;
-    if (last_blk >= n_absmax)
-      return fail(RUS_ERR_INVALID, "rus_nf4_dequant: absmax has %lld entries, needs %lld",
-                  (long long)n_absmax, (long long)(last_blk + 1));
-    const int64_t starts[3] = {0, split_byte_1, split_byte_2};
-    const int64_t ends[3] = {split_byte_1, split_byte_2, n_bytes};
-    const int64_t bases[3] = {0, absmax2_base_1, absmax2_base_2};
-    for (int s = 0; s < 3; ++s) {
-      if (ends[s] <= starts[s]) continue;
-      const int64_t blk_first = starts[s] >> hb, blk_last = (ends[s] - 1) >> hb;
-      const int64_t sup_last = bases[s] + ((blk_last - blk_first) >> sb);
-      if (sup_last >= n_absmax2)
-        return fail(RUS_ERR_INVALID,
-                    "rus_nf4_dequant: absmax2 has %lld entries, segment %d needs index %lld",
-                    (long long)n_absmax2, s, (long long)sup_last);
-    }
+  const int hb = ilog2(half_block), sb = ilog2(super_blocksize);
+  const int64_t last_blk = (n_bytes - 1) >> hb;
+  if (last_blk >= n_absmax)
+    return fail(RUS_ERR_INVALID, "%s: absmax has %lld entries, needs %lld", fn,
+                (long long)n_absmax, (long long)(last_blk + 1));
+  const int64_t starts[3] = {0, split_byte_1, split_byte_2};
+  const int64_t ends[3] = {split_byte_1, split_byte_2, n_bytes};
+  const int64_t bases[3] = {0, absmax2_base_1, absmax2_base_2};
+  for (int s = 0; s < 3; ++s) {
+    if (ends[s] <= starts[s]) continue;
+    const int64_t blk_first = starts[s] >> hb, blk_last = (ends[s] - 1) >> hb;
+    const int64_t sup_last = bases[s] + ((blk_last - blk_first) >> sb);
+    if (sup_last >= n_absmax2)
+      return fail(RUS_ERR_INVALID, "%s: absmax2 has %lld entries, segment %d needs index %lld",
+                  fn, (long long)n_absmax2, s, (long long)sup_last);
   }
-
-  Nf4Args a;
   a.packed = reinterpret_cast<const uint32_t*>(packed);
   a.packed_bytes = packed;
   a.absmax = absmax;
@@ -230,23 +258,68 @@ extern "C" int rus_nf4_dequant(const uint8_t* packed, const uint8_t* absmax, con
   a.off0 = off0;
   a.off1 = off1;
   a.off2 = off2;
-  // A split equal to n_bytes means "segment absent"; keep it unreachable.
+  // A split equal to n_bytes means "segment absent"; it is never reached.
   a.split1 = static_cast<uint32_t>(split_byte_1);
   a.split2 = static_cast<uint32_t>(split_byte_2);
-  a.hb_shift = ilog2(half_block);
-  a.sb_shift = ilog2(super_blocksize);
-  a.blk0_1 = static_cast<uint32_t>(split_byte_1 >> a.hb_shift);
-  a.blk0_2 = static_cast<uint32_t>(split_byte_2 >> a.hb_shift);
+  a.hb_shift = hb;
+  a.sb_shift = sb;
+  a.blk0_1 = static_cast<uint32_t>(split_byte_1 >> hb);
+  a.blk0_2 = static_cast<uint32_t>(split_byte_2 >> hb);
   a.sbase1 = static_cast<uint32_t>(absmax2_base_1);
   a.sbase2 = static_cast<uint32_t>(absmax2_base_2);
   a.n_bytes = static_cast<uint32_t>(n_bytes);
   a.n_units = static_cast<uint32_t>(n_bytes / 4);
+  return RUS_OK;
+}
 
-  constexpr int kUnroll = 4;
-  const uint32_t per_block = kThreads * kUnroll;
-  uint32_t grid = (a.n_units + per_block - 1) / per_block;
-  if (grid == 0) grid = 1;  // tail-only input
-  hipLaunchKernelGGL(nf4_dequant_kernel<kUnroll>, dim3(grid), dim3(kThreads), 0,
+uint32_t blocks_for(const Nf4Args& a) {
+  const uint32_t per_block = kThreads * kUnrollMain;
+  const uint32_t g = (a.n_units + per_block - 1) / per_block;
+  return g == 0 ? 1 : g;  // tail-only input
+}
+
+}  // namespace
+}  // namespace rus
+
+extern "C" int rus_nf4_dequant(const uint8_t* packed, const uint8_t* absmax, const float* code2,
+                               const float* absmax2, float off0, float off1, float off2,
+                               int64_t split_byte_1, int64_t split_byte_2, int64_t absmax2_base_1,
+                               int64_t absmax2_base_2, int64_t n_bytes, int64_t n_absmax,
+                               int64_t n_absmax2, int32_t blocksize, int32_t super_blocksize,
+                               uint32_t* out_u32, void* stream) {
+  using namespace rus;
+  if (n_bytes == 0) return RUS_OK;
+  Nf4Args a;
+  if (int e = make_job("rus_nf4_dequant", packed, absmax, code2, absmax2, off0, off1, off2,
+                       split_byte_1, split_byte_2, absmax2_base_1, absmax2_base_2, n_bytes,
+                       n_absmax, n_absmax2, blocksize, super_blocksize, out_u32, a))
+    return e;
+  hipLaunchKernelGGL(nf4_dequant_kernel<kUnrollMain>, dim3(blocks_for(a)), dim3(kThreads), 0,
                      static_cast<hipStream_t>(stream), a);
   return check_launch("rus_nf4_dequant");
+}
+
+extern "C" int rus_nf4_dequant_multi(const rus_nf4_job* jobs, int32_t n_jobs, const float* code2,
+                                     int32_t blocksize, int32_t super_blocksize, void* stream) {
+  using namespace rus;
+  const char* fn = "rus_nf4_dequant_multi";
+  if (n_jobs <= 0 || n_jobs > kMaxJobs || !jobs)
+    return fail(RUS_ERR_INVALID, "%s: n_jobs=%d outside [1, %d]", fn, n_jobs, kMaxJobs);
+  Nf4Multi m{};
+  m.n_jobs = n_jobs;
+  uint32_t total = 0;
+  for (int j = 0; j < n_jobs; ++j) {
+    const rus_nf4_job& q = jobs[j];
+    if (int e = make_job(fn, q.packed, q.absmax, code2, q.absmax2, q.off0, q.off1, q.off2,
+                         q.split_byte_1, q.split_byte_2, q.absmax2_base_1, q.absmax2_base_2,
+                         q.n_bytes, q.n_absmax, q.n_absmax2, blocksize, super_blocksize,
+                         q.out_u32, m.job[j]))
+      return e;
+    m.start[j] = total;
+    total += blocks_for(m.job[j]);
+  }
+  for (int j = n_jobs; j <= kMaxJobs; ++j) m.start[j] = total;
+  hipLaunchKernelGGL(nf4_dequant_multi_kernel<kUnrollMain>, dim3(total), dim3(kThreads), 0,
+                     static_cast<hipStream_t>(stream), m);
+  return check_launch(fn);
 }

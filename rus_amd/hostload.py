@@ -167,6 +167,20 @@ class WeightStream:
             blocksize=seg.blocksize, super_blocksize=seg.super_blocksize,
             absmax2_bases=seg.absmax2_bases)
 
+    def dequant_layer(self, layer_idx: int) -> dict[str, torch.Tensor]:
+        """All four segments of a layer in one dequant launch: {"qkv", "o", "gu", "down"} ->
+        fp16 weights (views of the per-segment workspaces)."""
+        packed, absmax, absmax2 = self._arrays(layer_idx)
+        segs = self.layer_segments[layer_idx]
+        first = segs[SEGMENTS[0]]
+        jobs = [{"packed": packed[sg.packed_slice], "absmax": absmax[sg.absmax_slice],
+                 "absmax2": absmax2[sg.absmax2_slice], "offset": sg.offsets,
+                 "out_shape": (sg.out_features, sg.in_features), "out_buf": self.workspaces[name],
+                 "split_bytes": sg.split_bytes, "absmax2_bases": sg.absmax2_bases}
+                for name, sg in ((n, segs[n]) for n in SEGMENTS)]
+        outs = K.dequant_nf4_segments(jobs, self.code2_gpu, first.blocksize, first.super_blocksize)
+        return dict(zip(SEGMENTS, outs))
+
 
 class HostHead:
     """Tied embedding / lm_head: HBM-resident (with W^T for the gradient GEMM) or streamed from

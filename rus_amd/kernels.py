@@ -16,6 +16,7 @@ from ._lib import DTYPE_F16, DTYPE_F32
 
 __all__ = [
     "dequant_nf4_tensor",
+    "dequant_nf4_segments",
     "nf4_absmax2_bases",
     "rms_norm_fwd",
     "rms_norm_bwd",
@@ -74,6 +75,20 @@ class KernelTimer:
     def __exit__(self, *exc):
         KernelTimer.active = None
         return False
+
+    @staticmethod
+    def pair_overhead_ms(n: int = 64) -> float:
+        """Median elapsed time of an empty event pair on the current stream (the floor under
+        every per-launch figure)."""
+        pairs = []
+        for _ in range(n):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            e1.record()
+            pairs.append((e0, e1))
+        torch.cuda.synchronize()
+        ts = sorted(a.elapsed_time(b) for a, b in pairs)
+        return ts[len(ts) // 2]
 
     def summary(self) -> dict[str, dict]:
         torch.cuda.synchronize()
@@ -187,6 +202,63 @@ def dequant_nf4_tensor(
         out.data_ptr(), _stream(out),
     )
     return out
+
+
+def dequant_nf4_segments(segments: list[dict], code2: torch.Tensor, blocksize: int = 64,
+                         super_blocksize: int = 256) -> list[torch.Tensor]:
+    """Dequantise 1..4 NF4 segments in one launch (one layer's [q|k|v], o, [gate|up], down).
+
+    Each entry: packed, absmax, absmax2 (device tensors), offset (float or 3-tuple), out_shape,
+    out_buf (fp16, optional), split_bytes and absmax2_bases (optional), as for
+    ``dequant_nf4_tensor``. Returns the fp16 weights in order."""
+    fn = "dequant_nf4_segments"
+    if not 1 <= len(segments) <= 4:
+        raise ValueError(f"{fn}: 1..4 segments")
+    _require_device(fn, code2)
+    if code2.dtype != torch.float32 or code2.numel() != 256:
+        raise ValueError(f"{fn}: code2 must be 256 float32 values")
+    code2 = code2.reshape(-1).contiguous()
+    jobs = (_lib.Nf4Job * len(segments))()
+    outs = []
+    total_bytes = 1024
+    for j, sg in enumerate(segments):
+        packed, absmax, absmax2 = (sg[k].reshape(-1) for k in ("packed", "absmax", "absmax2"))
+        _require_device(fn, packed, absmax, absmax2, sg.get("out_buf"))
+        if packed.dtype != torch.uint8 or absmax.dtype != torch.uint8 or absmax2.dtype != torch.float32:
+            raise TypeError(f"{fn}: packed/absmax must be uint8 and absmax2 float32")
+        for t in (packed, absmax, absmax2):
+            if not t.is_contiguous():
+                raise ValueError(f"{fn}: segment arrays must be contiguous")
+        shape = sg["out_shape"]
+        n_el = int(shape[0]) * int(shape[1])
+        if n_el % 2 or n_el == 0:
+            raise ValueError(f"{fn}: element count {n_el} must be even and positive")
+        nb = n_el // 2
+        if packed.numel() < nb:
+            raise ValueError(f"{fn}: packed has {packed.numel()} bytes, need {nb}")
+        ob = sg.get("out_buf")
+        if ob is None:
+            out = torch.empty(shape, dtype=torch.float16, device=packed.device)
+        else:
+            if ob.dtype != torch.float16 or ob.numel() < n_el:
+                raise ValueError(f"{fn}: out_buf must be fp16 with at least {n_el} elements")
+            out = ob.view(-1)[:n_el].view(shape)
+        off = sg["offset"]
+        offs = (off, off, off) if not isinstance(off, (tuple, list)) else tuple(off)
+        sp = sg.get("split_bytes") or (nb, nb)
+        bases = sg.get("absmax2_bases") or nf4_absmax2_bases(nb, sp, blocksize, super_blocksize)
+        jb = jobs[j]
+        jb.packed, jb.absmax, jb.absmax2 = packed.data_ptr(), absmax.data_ptr(), absmax2.data_ptr()
+        jb.off0, jb.off1, jb.off2 = (float(o) for o in offs)
+        jb.split_byte_1, jb.split_byte_2 = int(sp[0]), int(sp[1])
+        jb.absmax2_base_1, jb.absmax2_base_2 = int(bases[0]), int(bases[1])
+        jb.n_bytes, jb.n_absmax, jb.n_absmax2 = nb, absmax.numel(), absmax2.numel()
+        jb.out_u32 = out.data_ptr()
+        outs.append(out)
+        total_bytes += nb + absmax.numel() + 4 * absmax2.numel() + 2 * n_el
+    _launch("nf4_dequant", total_bytes, 0, "rus_nf4_dequant_multi", jobs, len(segments),
+            code2.data_ptr(), int(blocksize), int(super_blocksize), _stream(code2))
+    return outs
 
 
 # ---------------------------------------------------------------------------------------------

@@ -412,7 +412,9 @@ class FusedQwen2StackFn(torch.autograd.Function):
             ins.save(l, h)
             rng_states.append(torch.cuda.get_rng_state(engine.device) if training else None)
             ws.wait_slot(l)
-            qkv = F.linear(norm1, ws.dequant(l, "qkv"), engine.layer_biases[l])
+            W = ws.dequant_layer(l)  # one launch for [q|k|v], o, [gate|up], down
+            ws.release_slot(l)
+            qkv = F.linear(norm1, W["qkv"], engine.layer_biases[l])
             meta = engine.layer_lora_meta[l]
             _, _, q_lora, _, _, v_lora, _ = _lora_deltas(norm1, *lora16[4 * l: 4 * l + 4], meta, training)
             q_rot, k_rot, v_out = K.qkv_rope_fwd(qkv, cos, sin, pos_ids, q_lora=q_lora, v_lora=v_lora,
@@ -426,13 +428,12 @@ class FusedQwen2StackFn(torch.autograd.Function):
                 attn = _run_packed_sdpa(q_rot, k_rot, v_out, row_lengths, engine.num_heads,
                                         engine.num_kv_heads, engine.head_dim)
             del q_rot, k_rot, v_out
-            o_out = F.linear(attn, ws.dequant(l, "o"))
+            o_out = F.linear(attn, W["o"])
             del attn
             norm2, h_mid, _ = K.rms_norm_fwd(o_out, engine.ln2_weights[l], eps=eps, residual=h)
             del o_out
-            mlp_out = _mlp_fwd(norm2, ws.dequant(l, "gu"), ws.dequant(l, "down"), engine.max_mlp_tokens)
-            ws.release_slot(l)
-            del norm2
+            mlp_out = _mlp_fwd(norm2, W["gu"], W["down"], engine.max_mlp_tokens)
+            del norm2, W
             carry = (h_mid, mlp_out)
         if carry is None:
             final_norm, h_last, final_rstd = K.rms_norm_fwd(h, engine.final_norm_weight, eps=eps)
@@ -473,10 +474,8 @@ class FusedQwen2StackFn(torch.autograd.Function):
                 ins.prefetch(l - 1, n_tokens)
             h_in = ins.load(l, n_tokens)
             ws.wait_slot(l)
-            w_qkv = ws.dequant(l, "qkv")
-            w_o = ws.dequant(l, "o")
-            w_gu = ws.dequant(l, "gu")
-            w_down = ws.dequant(l, "down")
+            W = ws.dequant_layer(l)
+            w_qkv, w_o, w_gu, w_down = W["qkv"], W["o"], W["gu"], W["down"]
             ws.release_slot(l)  # every read of the packed slot is enqueued
             if training and ctx.rng_states[l] is not None:
                 torch.cuda.set_rng_state(ctx.rng_states[l], engine.device)

@@ -53,6 +53,7 @@ def test_header_compiles_as_c():
         # absmax too short for the bytes
         ("rus_nf4_dequant", (16, 16, 16, 16, 0.0, 0.0, 0.0, 64, 64, 0, 0, 64, 1, 1, 64, 256, 16, None),
          "absmax"),
+        ("rus_nf4_dequant_multi", (None, 0, 16, 64, 256, None), "n_jobs"),
         # stride smaller than the row
         ("rus_rmsnorm_fwd", (16, None, 16, 0, None, 16, 16, 4, 128, 64, 1e-6, 0, None), "stride"),
         # bad dtype
@@ -72,3 +73,14 @@ def test_invalid_arguments_are_rejected_on_the_host(name, args, msg):
     # Pointer values here are never dereferenced: validation fails before any launch.
     with pytest.raises(RuntimeError, match=msg):
         _lib.call(name, *args)
+
+
+def test_multi_dequant_validates_every_job():
+    jobs = (_lib.Nf4Job * 2)()
+    for j in jobs:
+        j.packed = j.absmax = j.absmax2 = j.out_u32 = 16
+        j.split_byte_1 = j.split_byte_2 = j.n_bytes = 64
+        j.n_absmax, j.n_absmax2 = 4, 1
+    jobs[1].n_absmax = 1  # second job's absmax too short for its bytes
+    with pytest.raises(RuntimeError, match="absmax has 1 entries"):
+        _lib.call("rus_nf4_dequant_multi", jobs, 2, 16, 64, 256, None)

@@ -87,6 +87,33 @@ def test_nf4_dequant_unaligned_super_blocks_and_out_buf():
     assert torch.all(ws[fused.shape[0] * fused.shape[1]:] == 7.0)  # nothing written past the view
 
 
+def test_nf4_dequant_segments_one_launch_bit_exact():
+    # One launch over a layer's four segments ([q|k|v], o, [gate|up], down shapes at reduced width,
+    # plus ragged ones), each into its own guarded buffer; must equal the per-segment oracle.
+    g = torch.Generator().manual_seed(5)
+    mk = lambda r, c: quant.quantize_nf4((torch.randn(r, c, generator=g) * 0.02).half())
+    layer = [[mk(384, 256), mk(64, 256), mk(64, 256)], [mk(384, 384)], [mk(1000, 256), mk(1000, 256)],
+             [mk(256, 1000)]]
+    ragged = [[mk(3, 70)], [mk(200, 128), mk(72, 128), mk(136, 128)], [mk(1, 10)]]
+    for segs in (layer, ragged):
+        jobs, refs, bufs = [], [], []
+        for parts in segs:
+            fused, splits, offs, bases = quant.concat_segments(parts)
+            n = fused.shape[0] * fused.shape[1]
+            buf = torch.full((n + 64,), 7.0, dtype=torch.float16, device=DEV)
+            bufs.append((buf, n))
+            jobs.append({"packed": fused.packed.to(DEV), "absmax": fused.absmax.to(DEV),
+                         "absmax2": fused.absmax2.to(DEV), "offset": offs, "out_shape": fused.shape,
+                         "out_buf": buf, "split_bytes": splits, "absmax2_bases": bases})
+            refs.append(np.concatenate([_dequant_ref(p) for p in parts]))
+        outs = K.dequant_nf4_segments(jobs, segs[0][0].code2.to(DEV))
+        torch.cuda.synchronize()
+        for out, want, (buf, n) in zip(outs, refs, bufs):
+            assert out.data_ptr() == buf.data_ptr()
+            assert _bits_equal(out, want)
+            assert torch.all(buf[n:] == 7.0)
+
+
 def test_nf4_dequant_rejects_short_absmax():
     q = quant.quantize_nf4(torch.randn(64, 64).half())
     with pytest.raises(RuntimeError, match="absmax"):
