@@ -40,6 +40,14 @@ const char* rus_last_error(void);
 int rus_abi_version(void);
 
 /*
+ * Diagnostic (no counterpart in the reference): node census of a captured hipGraph_t.
+ * counts[t] = number of nodes of hipGraphNodeType t (0 kernel, 1 memcpy, 2 memset, 3 host,
+ * 4 child graph, 5 empty, 6 wait event, 7 event record, ...) for t < n_counts; later types are
+ * added to counts[n_counts - 1]. Used to check that a captured training step holds no memset.
+ */
+int rus_graph_node_counts(void* graph, int64_t* counts, int32_t n_counts);
+
+/*
  * NF4 double-quant dequantisation over 1..3 concatenated segments.
  * Replaces: solution/kernels.py:27-118 (nf4_dequant_turing_kernel) and its launcher
  *           solution/kernels.py:572-619 (dequant_nf4_tensor); called by
@@ -152,6 +160,32 @@ int rus_qkv_rope_bwd(const void* dq_rot, const void* dk_rot, const void* dv, con
                      int32_t head_dim, int32_t* err_flag, int32_t dtype, void* stream);
 
 /*
+ * LoRA-input dropout, both branches in one pass: out_a = dropout(x; stream_a, p_a),
+ * out_b = dropout(x; stream_b, p_b), out = keep ? T(x * (1/(1-p))) : 0.
+ * Replaces: the two F.dropout calls on the attention-norm output, solution/ops.py:775-777 (and
+ * their RNG-replayed recompute, ops.py:868-869, 882-886).
+ * The mask is a pure function of (*seed, stream, row * n_cols + col): element e is kept when the
+ * 32-bit word e % 8 of Philox4x64-10(counter = (e / 8, 0, 0, 0), key = (*seed, stream)) is
+ * >= round(p * 2^32) (words in order w0.lo, w0.hi, w1.lo, ..., w3.hi). *seed is read on the
+ * device. 0 <= p < 1.
+ */
+int rus_lora_dropout_fwd(const void* x, void* out_a, void* out_b, int64_t n_rows, int64_t n_cols,
+                         int64_t stride_x, int64_t stride_a, int64_t stride_b,
+                         const uint64_t* seed, uint64_t stream_a, uint64_t stream_b, float p_a,
+                         float p_b, int32_t dtype, void* stream);
+
+/*
+ * Backward of both dropouts plus the two adds into the input gradient, in place:
+ *   acc = T( T(acc + T(dropout(grad_a; stream_a, p_a))) + T(dropout(grad_b; stream_b, p_b)) )
+ * with the masks of rus_lora_dropout_fwd.
+ * Replaces: solution/ops.py:986-992 (RNG replay, two F.dropout, d_norm1.add_(dx_q).add_(dx_v)).
+ */
+int rus_lora_dropout_bwd_add(void* acc, const void* grad_a, const void* grad_b, int64_t n_rows,
+                             int64_t n_cols, int64_t stride_acc, int64_t stride_a,
+                             int64_t stride_b, const uint64_t* seed, uint64_t stream_a,
+                             uint64_t stream_b, float p_a, float p_b, int32_t dtype, void* stream);
+
+/*
  * SwiGLU forward: out = T( g*sigmoid(g) * u ), sigmoid(g) = 1/(1+exp(-g)).
  * Replaces: solution/kernels.py:355-392 (tiled_mlp_glu_fwd_kernel), launcher kernels.py:801-847.
  * For the fused [gate | up] layout pass up = gate + n_cols and stride_u = stride_g.
@@ -199,6 +233,14 @@ int rus_lmhead_ce_combine(const float* part_m, const float* part_s, const float*
                           const int32_t* part_idx, int64_t n_parts, int64_t part_stride,
                           const float* target, const int64_t* labels, int64_t n_tok, float* lse,
                           float* nll, float* entropy, int64_t* argmax, void* stream);
+
+/*
+ * Loss reduction: denom = max(*num_items, 1) when num_items is not NULL, else
+ * max(#(labels != -100), 1); loss = sum(nll) / denom. One workgroup; both outputs on the device.
+ * Replaces: solution/ops.py:268-277 (loss = nll.sum() / denominator, with its host .item()).
+ */
+int rus_lmhead_ce_loss(const float* nll, const int64_t* labels, int64_t n_tok,
+                       const float* num_items, float* loss, float* denom, void* stream);
 
 /*
  * Logit gradient for vocabulary rows [vocab_start, vocab_start+n_vocab):

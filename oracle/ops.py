@@ -222,6 +222,80 @@ def swiglu_bwd(dout: torch.Tensor, g: torch.Tensor, u: torch.Tensor):
 
 
 # ---------------------------------------------------------------------------------------------
+# LoRA-input dropout — solution/ops.py:775-777 (forward), 882-886 (recompute), 986-992 (backward)
+# The reference replays torch's generator state; the build draws each mask from a counter-based
+# Philox4x64-10 stream instead (same masks in forward, recompute and backward by construction).
+# ---------------------------------------------------------------------------------------------
+
+_PHILOX_M = (0xD2E7470EE14C6C93, 0xCA5A826395121157)
+_PHILOX_W = (0x9E3779B97F4A7C15, 0xBB67AE8584CAA73B)
+_LO32 = np.uint64(0xFFFFFFFF)
+
+
+def _mulhilo64(a: int, b: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """(hi, lo) 64-bit halves of the 128-bit products a * b (uint64 arrays, 32-bit limbs)."""
+    a_lo, a_hi = np.uint64(a & 0xFFFFFFFF), np.uint64(a >> 32)
+    b_lo, b_hi = b & _LO32, b >> np.uint64(32)
+    ll, lh, hl, hh = a_lo * b_lo, a_lo * b_hi, a_hi * b_lo, a_hi * b_hi
+    mid = (ll >> np.uint64(32)) + (lh & _LO32) + (hl & _LO32)
+    lo = (ll & _LO32) | ((mid & _LO32) << np.uint64(32))
+    hi = hh + (lh >> np.uint64(32)) + (hl >> np.uint64(32)) + (mid >> np.uint64(32))
+    return hi, lo
+
+
+def philox4x64_10(counters: np.ndarray, key: tuple[int, int]) -> np.ndarray:
+    """Philox4x64 with 10 rounds (Salmon et al., SC'11) over uint64 counters [n, 4] -> [n, 4]."""
+    c = [counters[:, i].astype(np.uint64).copy() for i in range(4)]
+    k0, k1 = int(key[0]) & (2**64 - 1), int(key[1]) & (2**64 - 1)
+    with np.errstate(over="ignore"):
+        for _ in range(10):
+            hi0, lo0 = _mulhilo64(_PHILOX_M[0], c[0])
+            hi1, lo1 = _mulhilo64(_PHILOX_M[1], c[2])
+            c = [hi1 ^ c[1] ^ np.uint64(k0), lo1, hi0 ^ c[3] ^ np.uint64(k1), lo0]
+            k0, k1 = (k0 + _PHILOX_W[0]) % 2**64, (k1 + _PHILOX_W[1]) % 2**64
+    return np.stack(c, axis=1)
+
+
+def dropout_keep_mask(seed: int, stream: int, n_rows: int, n_cols: int, p: float) -> np.ndarray:
+    """bool [n_rows, n_cols]: element e = row * n_cols + col is kept when 32-bit word e % 8 of
+    Philox4x64-10((e // 8, 0, 0, 0), (seed, stream)) (words w0.lo, w0.hi, ..., w3.hi) is
+    >= round(p * 2^32)."""
+    n = n_rows * n_cols
+    nb = (n + 7) // 8
+    ctr = np.zeros((nb, 4), dtype=np.uint64)
+    ctr[:, 0] = np.arange(nb, dtype=np.uint64)
+    w = philox4x64_10(ctr, (seed, stream))
+    words = np.empty((nb, 8), dtype=np.uint64)
+    words[:, 0::2] = w & _LO32
+    words[:, 1::2] = w >> np.uint64(32)
+    thresh = min(int(float(np.float32(p)) * 4294967296.0 + 0.5), 0xFFFFFFFF)
+    return (words.reshape(-1)[:n] >= np.uint64(thresh)).reshape(n_rows, n_cols)
+
+
+def _drop(x: torch.Tensor, keep: np.ndarray, p: float) -> torch.Tensor:
+    scale = torch.tensor(1.0, dtype=torch.float32) / (1.0 - torch.tensor(p, dtype=torch.float32))
+    y = torch.where(torch.from_numpy(keep), x.float() * scale, torch.zeros((), dtype=torch.float32))
+    return y.to(x.dtype)
+
+
+def lora_dropout_fwd(x: torch.Tensor, seed: int, stream_a: int, stream_b: int, p_a: float,
+                     p_b: float):
+    """(dropout_a(x), dropout_b(x)) with x [rows, cols]: T(x * fp32(1 / (1 - p))) where kept."""
+    r, c = x.shape
+    return (_drop(x, dropout_keep_mask(seed, stream_a, r, c, p_a), p_a),
+            _drop(x, dropout_keep_mask(seed, stream_b, r, c, p_b), p_b))
+
+
+def lora_dropout_bwd_add(acc: torch.Tensor, ga: torch.Tensor, gb: torch.Tensor, seed: int,
+                         stream_a: int, stream_b: int, p_a: float, p_b: float) -> torch.Tensor:
+    """T(T(acc + dropout_a(ga)) + dropout_b(gb)): ops.py:988-992 with the forward's masks."""
+    r, c = acc.shape
+    ta = _drop(ga, dropout_keep_mask(seed, stream_a, r, c, p_a), p_a)
+    tb = _drop(gb, dropout_keep_mask(seed, stream_b, r, c, p_b), p_b)
+    return (acc.float() + ta.float()).to(acc.dtype).float().add(tb.float()).to(acc.dtype)
+
+
+# ---------------------------------------------------------------------------------------------
 # Chunked lm_head cross-entropy — solution/kernels.py:453-565, ops.py:174-349
 # ---------------------------------------------------------------------------------------------
 

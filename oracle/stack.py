@@ -11,8 +11,9 @@ composition whose LoRA gradients come from torch autograd:
                x2 = RMSNorm(h); h += (silu(x2 Wg^T) * (x2 Wu^T)) Wd^T
     loss = sum CE(RMSNorm(h) E^T, shifted labels) / denom
 
-with base weights dequantised by ``oracle.ops.nf4_dequant``. Dropout is not modelled (parity runs
-use p = 0). Pinned against transformers' Qwen2ForCausalLM (eager attention) with the LoRA deltas
+with base weights dequantised by ``oracle.ops.nf4_dequant``. With ``dropout_seed`` the q- and
+v-branch LoRA inputs are x * mask / (1 - p) with the counter-based masks of
+``oracle.ops.dropout_keep_mask`` (streams 2*layer and 2*layer + 1, p = config.lora_dropout). Pinned against transformers' Qwen2ForCausalLM (eager attention) with the LoRA deltas
 merged into the projection weights (tests/test_oracle_stack.py).
 """
 
@@ -75,7 +76,16 @@ def _attention(q, k, v, row_lengths):
     return out.reshape(n, hq * d)
 
 
-def stack_forward(model, deq, lora, ids, pos, row_lengths, rope_dtype=torch.float16):
+def _dropped(x, seed, stream, p):
+    if seed is None or p <= 0:
+        return x
+    keep = torch.from_numpy(ref.dropout_keep_mask(seed, stream, x.shape[0], x.shape[1], p))
+    scale = torch.tensor(1.0) / (1.0 - torch.tensor(p, dtype=torch.float32))
+    return torch.where(keep, x * scale, torch.zeros((), dtype=x.dtype))
+
+
+def stack_forward(model, deq, lora, ids, pos, row_lengths, rope_dtype=torch.float16,
+                  dropout_seed=None):
     """Final-norm hidden states [N, D] (fp32) of the packed batch."""
     cfg = model.config
     hq, hkv, hd = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
@@ -88,9 +98,11 @@ def stack_forward(model, deq, lora, ids, pos, row_lengths, rope_dtype=torch.floa
         W = deq[li]
         qA, qB, vA, vB = lora[4 * li: 4 * li + 4]
         x = _rms(h, L.ln1.cpu().float(), eps)
-        q = x @ W["q"].t() + L.q_bias.cpu().float() + cfg.lora_scaling * ((x @ qA.t()) @ qB.t())
+        xq = _dropped(x, dropout_seed, 2 * li, cfg.lora_dropout)
+        xv = _dropped(x, dropout_seed, 2 * li + 1, cfg.lora_dropout)
+        q = x @ W["q"].t() + L.q_bias.cpu().float() + cfg.lora_scaling * ((xq @ qA.t()) @ qB.t())
         k = x @ W["k"].t() + L.k_bias.cpu().float()
-        v = x @ W["v"].t() + L.v_bias.cpu().float() + cfg.lora_scaling * ((x @ vA.t()) @ vB.t())
+        v = x @ W["v"].t() + L.v_bias.cpu().float() + cfg.lora_scaling * ((xv @ vA.t()) @ vB.t())
         q = _rope(q.view(n, hq, hd), c, s)
         k = _rope(k.view(n, hkv, hd), c, s)
         h = h + _attention(q, k, v.view(n, hkv, hd), row_lengths) @ W["o"].t()
@@ -100,9 +112,9 @@ def stack_forward(model, deq, lora, ids, pos, row_lengths, rope_dtype=torch.floa
 
 
 def step_loss(model, deq, lora, ids, pos, shift_labels, row_lengths, num_items_in_batch=None,
-              rope_dtype=torch.float16):
+              rope_dtype=torch.float16, dropout_seed=None):
     """Mean cross-entropy over labels != -100 (or sum / num_items_in_batch)."""
-    final = stack_forward(model, deq, lora, ids, pos, row_lengths, rope_dtype)
+    final = stack_forward(model, deq, lora, ids, pos, row_lengths, rope_dtype, dropout_seed)
     logits = final @ model.embed.cpu().float().t()
     nll = F.cross_entropy(logits, shift_labels, ignore_index=-100, reduction="sum")
     denom = float(num_items_in_batch) if num_items_in_batch is not None else float((shift_labels != -100).sum())

@@ -20,6 +20,7 @@ _vp = ctypes.c_void_p
 _i64 = ctypes.c_int64
 _i32 = ctypes.c_int32
 _f32 = ctypes.c_float
+_u64 = ctypes.c_uint64
 
 class Nf4Job(ctypes.Structure):
     """struct rus_nf4_job of include/rus_amd.h."""
@@ -39,6 +40,10 @@ SIGNATURES: dict[str, list] = {
     "rus_nf4_dequant": [_vp, _vp, _vp, _vp, _f32, _f32, _f32, _i64, _i64, _i64, _i64, _i64, _i64,
                         _i64, _i32, _i32, _vp, _vp],
     "rus_nf4_dequant_multi": [ctypes.POINTER(Nf4Job), _i32, _vp, _i32, _i32, _vp],
+    "rus_lora_dropout_fwd": [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _vp, _u64, _u64, _f32, _f32, _i32, _vp],
+    "rus_lora_dropout_bwd_add": [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _vp, _u64, _u64, _f32, _f32, _i32, _vp],
+    "rus_graph_node_counts": [_vp, _vp, _i32],
+    "rus_lmhead_ce_loss": [_vp, _vp, _i64, _vp, _vp, _vp, _vp],
     "rus_rmsnorm_fwd": [_vp, _vp, _vp, _i32, _vp, _vp, _vp, _i64, _i64, _i64, _f32, _i32, _vp],
     "rus_rmsnorm_bwd": [_vp, _vp, _vp, _i32, _vp, _vp, _vp, _i64, _i64, _i64, _i32, _vp],
     "rus_qkv_lora_rope_fwd": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64,

@@ -588,6 +588,60 @@ extern "C" int rus_lmhead_ce_combine(const float* part_m, const float* part_s, c
   return check_launch(fn);
 }
 
+namespace rus {
+namespace {
+
+// loss = sum(nll) / denom, denom = max(*num_items, 1) if given, else max(#(labels != -100), 1).
+// One workgroup of 1024 threads (16 waves); fixed summation order, so repeated calls agree bitwise.
+__global__ __launch_bounds__(1024) void lmhead_loss_kernel(const float* __restrict__ nll,
+                                                           const int64_t* __restrict__ labels,
+                                                           int n_tok,
+                                                           const float* __restrict__ num_items,
+                                                           float* __restrict__ loss,
+                                                           float* __restrict__ denom) {
+  __shared__ float s_sum[16], s_cnt[16];
+  float sum = 0.0f, cnt = 0.0f;
+  for (int i = threadIdx.x; i < n_tok; i += 1024) {
+    sum += nll[i];
+    cnt += labels[i] != -100 ? 1.0f : 0.0f;
+  }
+  sum = wave_sum(sum);
+  cnt = wave_sum(cnt);
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  if (lane == 0) {
+    s_sum[wave] = sum;
+    s_cnt[wave] = cnt;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float t = 0.0f, c = 0.0f;
+    for (int w = 0; w < 16; ++w) {
+      t += s_sum[w];
+      c += s_cnt[w];
+    }
+    const float d = fmaxf(num_items ? *num_items : c, 1.0f);
+    denom[0] = d;
+    loss[0] = t / d;
+  }
+}
+
+}  // namespace
+}  // namespace rus
+
+extern "C" int rus_lmhead_ce_loss(const float* nll, const int64_t* labels, int64_t n_tok,
+                                  const float* num_items, float* loss, float* denom,
+                                  void* stream) {
+  using namespace rus;
+  const char* fn = "rus_lmhead_ce_loss";
+  if (n_tok < 0 || n_tok >= (int64_t(1) << 31))
+    return fail(RUS_ERR_INVALID, "%s: n_tok=%lld outside [0, 2^31)", fn, (long long)n_tok);
+  if ((n_tok > 0 && (!nll || !labels)) || !loss || !denom)
+    return fail(RUS_ERR_INVALID, "%s: null pointer argument", fn);
+  hipLaunchKernelGGL(lmhead_loss_kernel, dim3(1), dim3(1024), 0, static_cast<hipStream_t>(stream),
+                     nll, labels, static_cast<int>(n_tok), num_items, loss, denom);
+  return check_launch(fn);
+}
+
 extern "C" int rus_lmhead_ce_grad_logits(const void* hidden, const void* weight,
                                          const int64_t* labels, const float* lse,
                                          const float* denom, int64_t n_tok, int64_t d,

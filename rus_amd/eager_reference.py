@@ -4,8 +4,9 @@ This is what the reference's stack replaces: the transformers + PEFT + bitsandby
 torch autograd, which stores every activation and materialises the fp16 [N, V] logits and their
 fp32 copy (README.md:10-11 of the reference). It uses the same NF4 weights, dequantised per use
 like bitsandbytes' ``MatMul4Bit`` (forward and again in backward, only the input saved), fp16
-activations, fp32 norm weights and LoRA on q/v with dropout consuming the RNG in the fused stack's
-order (q then v per layer), so with equal RNG state both paths draw identical dropout masks.
+activations, fp32 norm weights and LoRA on q/v with dropout. The dropout masks are the fused
+stack's counter-based ones for a given seed (drawn by the dropout kernel on a tensor of ones and
+applied with plain torch ops under autograd), so both paths drop the same elements.
 
 Used by bench.py for the peak-memory / throughput comparison and by the GPU tests as a second,
 independent GPU reference for dropout replay and the full-size step.
@@ -56,9 +57,19 @@ def _rope(x, cos, sin):
     return (xf * cos[:, None, :].float() + rot * sin[:, None, :].float()).to(x.dtype)
 
 
+def _dropped(x, seed, layer, meta):
+    """(x_q, x_v) with the masks of streams 2*layer, 2*layer + 1, differentiable in x."""
+    ones = torch.ones(x.shape, dtype=torch.float32, device=x.device)
+    mq, mv = K.lora_dropout_fwd(ones, seed, 2 * layer, 2 * layer + 1, meta["p_q"], meta["p_v"])
+    return (x.float() * mq).to(x.dtype), (x.float() * mv).to(x.dtype)
+
+
 def eager_step_loss(engine, h_packed, pos_ids, shift_labels, row_lengths, training=True,
-                    num_items_in_batch=None):
-    """Loss of the packed batch through plain torch autograd (gradients reach the LoRA params)."""
+                    num_items_in_batch=None, seed=None):
+    """Loss of the packed batch through plain torch autograd (gradients reach the LoRA params).
+    ``seed``: the dropout seed tensor to use (default: the engine's last forward's)."""
+    if seed is None:
+        seed = engine.last_dropout_seed
     ws = engine.weight_stream
     cos, sin = engine.cos_table[pos_ids], engine.sin_table[pos_ids]
     hq, hkv, hd, eps = engine.num_heads, engine.num_kv_heads, engine.head_dim, engine.rms_eps
@@ -72,9 +83,11 @@ def eager_step_loss(engine, h_packed, pos_ids, shift_labels, row_lengths, traini
         x = _rms(h, engine.ln1_weights[l], eps)
         qkv = _NF4Linear.apply(x, _deq_fn(ws, l, "qkv"), engine.layer_biases[l])
         q, k, v = qkv.split([hq * hd, hkv * hd, hkv * hd], dim=-1)
-        xq = F.dropout(x, p=meta["p_q"], training=True) if (training and meta["p_q"] > 0) else x
+        if training and (meta["p_q"] > 0 or meta["p_v"] > 0):
+            xq, xv = _dropped(x, seed, l, meta)
+        else:
+            xq = xv = x
         q = q + meta["scale_q"] * F.linear(F.linear(xq, qA), qB)
-        xv = F.dropout(x, p=meta["p_v"], training=True) if (training and meta["p_v"] > 0) else x
         v = v + meta["scale_v"] * F.linear(F.linear(xv, vA), vB)
         q = _rope(q.reshape(n, hq, hd), cos, sin)
         k = _rope(k.reshape(n, hkv, hd), cos, sin)

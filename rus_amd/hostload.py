@@ -58,12 +58,25 @@ def _pinned(t: torch.Tensor) -> torch.Tensor:
 
 
 class WeightStream:
-    """Packed NF4 layers served as fp16 weights through the dequant kernel."""
+    """Packed NF4 layers served as fp16 weights through the dequant kernel.
 
-    def __init__(self, layers, device, resident: bool = False):
+    ``unit`` (when not resident) sets what is streamed from pinned host memory:
+      * "layer": two one-layer device slots refilled per layer per pass (the reference's policy,
+        hostload.py:286-323; 2 x 28 layer copies per step);
+      * "model": two whole-model device buffers; each step copies the packed model once (one
+        645 MiB H2D copy at Qwen2.5-1.5B) into the buffer the previous step did not use, on the
+        copy stream, overlapping the previous step. The step waits for its copy, uses that
+        buffer for forward and backward and then releases it (``begin_step`` / ``end_step``).
+        Copies that overlap a reader of the same buffer write identical bytes (the base weights
+        are frozen)."""
+
+    def __init__(self, layers, device, resident: bool = False, unit: str = "layer"):
+        if unit not in ("layer", "model"):
+            raise ValueError("unit must be 'layer' or 'model'")
         self.device = torch.device(device)
         self.num_layers = len(layers)
         self.resident = resident
+        self.unit = "resident" if resident else unit
         self.layer_segments: list[dict[str, PackedNF4Segment]] = []
         self.layer_biases: list[torch.Tensor | None] = []
         self.code2_gpu: torch.Tensor | None = None
@@ -101,6 +114,8 @@ class WeightStream:
         if resident:
             self.gpu_layers = [(p.to(self.device), a.to(self.device), a2.to(self.device))
                                for p, a, a2 in zip(packed_l, absmax_l, absmax2_l)]
+        elif self.unit == "model":
+            self._init_model_buffers(packed_l, absmax_l, absmax2_l)
         else:
             self.cpu_packed = [_pinned(p) for p in packed_l]
             self.cpu_absmax = [_pinned(a) for a in absmax_l]
@@ -118,9 +133,81 @@ class WeightStream:
         self.workspaces = {s: torch.empty(n, dtype=torch.float16, device=self.device)
                            for s, n in ws_elems.items()}
 
+    def _init_model_buffers(self, packed_l, absmax_l, absmax2_l) -> None:
+        """One pinned host blob holding every layer (packed | absmax | absmax2, each 256-byte
+        aligned) and two device blobs of the same layout."""
+        def up(x):
+            return (x + 255) // 256 * 256
+
+        offs, cur = [], 0
+        for p, a, a2 in zip(packed_l, absmax_l, absmax2_l):
+            po = cur
+            ao = up(po + p.numel())
+            a2o = up(ao + a.numel())
+            cur = up(a2o + 4 * a2.numel())
+            offs.append((po, ao, a2o))
+        self.model_bytes = cur
+        blob = torch.zeros(cur, dtype=torch.uint8)
+        for (po, ao, a2o), p, a, a2 in zip(offs, packed_l, absmax_l, absmax2_l):
+            blob[po: po + p.numel()] = p
+            blob[ao: ao + a.numel()] = a
+            blob[a2o: a2o + 4 * a2.numel()] = a2.contiguous().view(torch.uint8)
+        self.host_blob = _pinned(blob)
+        self.dev_blobs = [torch.empty(cur, dtype=torch.uint8, device=self.device) for _ in range(2)]
+        self.blob_views = []
+        for b in self.dev_blobs:
+            views = []
+            for (po, ao, a2o), p, a, a2 in zip(offs, packed_l, absmax_l, absmax2_l):
+                views.append((b[po: po + p.numel()], b[ao: ao + a.numel()],
+                              b[a2o: a2o + 4 * a2.numel()].view(torch.float32)))
+            self.blob_views.append(views)
+        self.stream = torch.cuda.Stream(device=self.device)
+        self.ready_events = [torch.cuda.Event() for _ in range(2)]
+        self.free_events = [torch.cuda.Event() for _ in range(2)]
+        self.staged = [False, False]
+        self.active = 0
+        self.next_buffer = 0
+
+    # -- whole-model streaming (unit="model") --------------------------------------------------
+    def stage(self, buf: int) -> None:
+        """Copies the packed model into device buffer ``buf`` on the copy stream, after the last
+        step that used ``buf`` released it."""
+        with torch.cuda.stream(self.stream):
+            self.stream.wait_event(self.free_events[buf])
+            self.dev_blobs[buf].copy_(self.host_blob, non_blocking=True)
+            self.ready_events[buf].record(self.stream)
+        self.staged[buf] = True
+
+    def begin_step(self) -> int:
+        """Starts a step on the next buffer (staging it if the previous step did not) and stages
+        the other buffer for the following step. Returns the buffer index; no-op (0) unless
+        unit="model"."""
+        if self.unit != "model":
+            return 0
+        buf = self.next_buffer
+        if not self.staged[buf]:
+            self.stage(buf)
+        torch.cuda.current_stream(self.device).wait_event(self.ready_events[buf])
+        self.staged[buf] = False
+        self.active = buf
+        self.next_buffer = 1 - buf
+        self.stage(self.next_buffer)
+        return buf
+
+    def use_buffer(self, buf: int) -> None:
+        """Reads of the following dequants come from device buffer ``buf`` (a backward pass
+        resuming the buffer its forward used)."""
+        if self.unit == "model":
+            self.active = buf
+
+    def end_step(self, buf: int) -> None:
+        """Releases ``buf`` after the work enqueued so far on the current stream."""
+        if self.unit == "model":
+            self.free_events[buf].record(torch.cuda.current_stream(self.device))
+
     # -- streaming protocol (hostload.py:297-323) ------------------------------------------------
     def prefetch(self, layer_idx: int) -> None:
-        if self.resident or layer_idx < 0 or layer_idx >= self.num_layers:
+        if self.unit != "layer" or layer_idx < 0 or layer_idx >= self.num_layers:
             return
         slot = layer_idx % 2
         if self.slot_layer[slot] == layer_idx:
@@ -136,7 +223,7 @@ class WeightStream:
             self.slot_layer[slot] = layer_idx
 
     def wait_slot(self, layer_idx: int) -> int:
-        if self.resident:
+        if self.unit != "layer":
             return 0
         slot = layer_idx % 2
         if self.slot_layer[slot] != layer_idx:
@@ -144,14 +231,41 @@ class WeightStream:
         torch.cuda.current_stream(self.device).wait_event(self.slot_events[slot])
         return slot
 
+    def begin_capture(self) -> None:
+        """Before capturing a step into a HIP graph: the side stream's first waits depend on an
+        event recorded in the capturing stream, and the slots are taken as empty so that the
+        graph copies every layer it uses (unit="layer"; nothing to do otherwise)."""
+        if self.unit != "layer":
+            return
+        cur = torch.cuda.current_stream(self.device)
+        self.compute_done_events = [torch.cuda.Event() for _ in range(2)]
+        for ev in self.compute_done_events:
+            ev.record(cur)
+        self.slot_events = [torch.cuda.Event() for _ in range(2)]
+        self.slot_layer = [-1, -1]
+
+    def after_replay(self) -> None:
+        """After a graph replay (or capture) on the current stream: later eager prefetches wait
+        for it before overwriting the slots, and take the slots as empty (unit="layer")."""
+        if self.unit != "layer":
+            return
+        cur = torch.cuda.current_stream(self.device)
+        self.compute_done_events = [torch.cuda.Event() for _ in range(2)]
+        for ev in self.compute_done_events:
+            ev.record(cur)
+        self.slot_events = [torch.cuda.Event() for _ in range(2)]
+        self.slot_layer = [-1, -1]
+
     def release_slot(self, layer_idx: int) -> None:
-        if self.resident:
+        if self.unit != "layer":
             return
         self.compute_done_events[layer_idx % 2].record(torch.cuda.current_stream(self.device))
 
     def _arrays(self, layer_idx: int):
-        if self.resident:
+        if self.unit == "resident":
             return self.gpu_layers[layer_idx]
+        if self.unit == "model":
+            return self.blob_views[self.active][layer_idx]
         slot = layer_idx % 2
         return self.gpu_packed_slots[slot], self.gpu_absmax_slots[slot], self.gpu_absmax2_slots[slot]
 

@@ -23,9 +23,12 @@ __all__ = [
     "qkv_rope_fwd",
     "qkv_rope_bwd",
     "qkv_rope_bwd_lora",
+    "lora_dropout_fwd",
+    "lora_dropout_bwd_add",
     "mlp_glu_fwd",
     "mlp_glu_bwd",
     "lm_head_ce",
+    "lm_head_ce_loss",
     "lm_head_ce_fwd_chunk",
     "lm_head_ce_combine",
     "lm_head_ce_grad_logits",
@@ -570,6 +573,67 @@ def mlp_glu_bwd(
 
 
 # ---------------------------------------------------------------------------------------------
+# LoRA-input dropout with a counter-based mask (reference: ops.py:775-777, 882-886, 986-992)
+# ---------------------------------------------------------------------------------------------
+
+
+def _drop_rows(fn: str, t: torch.Tensor, n_cols: int, name: str) -> torch.Tensor:
+    t2 = t.view(-1, n_cols) if t.is_contiguous() else t
+    if t2.dim() != 2 or t2.shape[1] != n_cols or t2.stride(1) != 1:
+        raise ValueError(f"{fn}: {name} must be [rows, {n_cols}] with unit column stride")
+    return t2
+
+
+def lora_dropout_fwd(x: torch.Tensor, seed: torch.Tensor, stream_a: int, stream_b: int,
+                     p_a: float, p_b: float, out_a: torch.Tensor | None = None,
+                     out_b: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """(dropout(x; stream_a, p_a), dropout(x; stream_b, p_b)) in one pass. ``seed`` is a one-element
+    int64 device tensor read by the kernel (so a captured graph sees its current value)."""
+    fn = "lora_dropout_fwd"
+    _require_device(fn, x, seed, out_a, out_b)
+    dt = _dtype_code(fn, x.dtype)
+    if seed.dtype != torch.int64 or seed.numel() != 1:
+        raise ValueError(f"{fn}: seed must be one int64 element")
+    n_cols = x.shape[-1]
+    x2 = _drop_rows(fn, x, n_cols, "x")
+    shape = (x2.shape[0], n_cols)
+    oa = torch.empty(shape, dtype=x.dtype, device=x.device) if out_a is None else _drop_rows(fn, out_a, n_cols, "out_a")
+    ob = torch.empty(shape, dtype=x.dtype, device=x.device) if out_b is None else _drop_rows(fn, out_b, n_cols, "out_b")
+    for o in (oa, ob):
+        if o.shape[0] != shape[0] or o.dtype != x.dtype:
+            raise ValueError(f"{fn}: outputs must be {shape} {x.dtype}")
+    n = shape[0] * n_cols
+    _launch("lora_dropout_fwd", 3 * n * x.element_size(), 0, "rus_lora_dropout_fwd",
+            x2.data_ptr(), oa.data_ptr(), ob.data_ptr(), shape[0], n_cols, x2.stride(0),
+            oa.stride(0), ob.stride(0), seed.data_ptr(), int(stream_a), int(stream_b), float(p_a),
+            float(p_b), dt, _stream(x2))
+    return oa.view(x.shape), ob.view(x.shape)
+
+
+def lora_dropout_bwd_add(acc: torch.Tensor, grad_a: torch.Tensor, grad_b: torch.Tensor,
+                         seed: torch.Tensor, stream_a: int, stream_b: int, p_a: float,
+                         p_b: float) -> torch.Tensor:
+    """acc += dropout(grad_a) then += dropout(grad_b), in place, with the forward's masks."""
+    fn = "lora_dropout_bwd_add"
+    _require_device(fn, acc, grad_a, grad_b, seed)
+    dt = _dtype_code(fn, acc.dtype)
+    if seed.dtype != torch.int64 or seed.numel() != 1:
+        raise ValueError(f"{fn}: seed must be one int64 element")
+    n_cols = acc.shape[-1]
+    a2 = _drop_rows(fn, acc, n_cols, "acc")
+    ga = _drop_rows(fn, grad_a, n_cols, "grad_a")
+    gb = _drop_rows(fn, grad_b, n_cols, "grad_b")
+    if not (ga.shape == gb.shape == a2.shape) or not (ga.dtype == gb.dtype == acc.dtype):
+        raise ValueError(f"{fn}: acc, grad_a and grad_b must match in shape and dtype")
+    n = a2.shape[0] * n_cols
+    _launch("lora_dropout_bwd", 4 * n * acc.element_size(), 0, "rus_lora_dropout_bwd_add",
+            a2.data_ptr(), ga.data_ptr(), gb.data_ptr(), a2.shape[0], n_cols, a2.stride(0),
+            ga.stride(0), gb.stride(0), seed.data_ptr(), int(stream_a), int(stream_b), float(p_a),
+            float(p_b), dt, _stream(a2))
+    return acc
+
+
+# ---------------------------------------------------------------------------------------------
 # Vocab-tiled lm_head cross-entropy on fp16 MFMA (reference: lm_head_piece_kernel /
 # lm_head_finish_kernel, kernels.py:453-565, and the chunk loops of ops.py:174-349)
 # ---------------------------------------------------------------------------------------------
@@ -746,15 +810,38 @@ def lm_head_weight_t(weight: torch.Tensor) -> torch.Tensor:
     return wt
 
 
+def lm_head_ce_loss(nll: torch.Tensor, labels: torch.Tensor, num_items_in_batch=None):
+    """(loss, denom) as one-element float32 device tensors: denom = max(num_items_in_batch, 1)
+    if given, else max(#(labels != -100), 1); loss = sum(nll) / denom (no host read)."""
+    fn = "lm_head_ce_loss"
+    _require_device(fn, nll, labels)
+    dev = nll.device
+    n = nll.numel()
+    if labels.numel() != n or nll.dtype != torch.float32 or labels.dtype != torch.int64:
+        raise ValueError(f"{fn}: nll float32 [n] and labels int64 [n] expected")
+    ni = None
+    if isinstance(num_items_in_batch, torch.Tensor):
+        ni = num_items_in_batch.detach().to(device=dev, dtype=torch.float32).reshape(1)
+    elif num_items_in_batch is not None:
+        ni = torch.full((1,), float(num_items_in_batch), dtype=torch.float32, device=dev)
+    out = torch.empty(2, dtype=torch.float32, device=dev)
+    _launch("lmhead_ce_loss", n * 12, 0, "rus_lmhead_ce_loss", nll.contiguous().data_ptr(),
+            labels.contiguous().data_ptr(), n, _ptr(ni), out.data_ptr(), out.data_ptr() + 4,
+            _stream(nll))
+    return out[0:1], out[1:2]
+
+
 def lm_head_ce(hidden: torch.Tensor, weight: torch.Tensor, labels: torch.Tensor,
                num_items_in_batch=None, v_chunk: int | None = None, need_grad: bool = True,
-               weight_t: torch.Tensor | None = None):
+               weight_t: torch.Tensor | None = None, dh_scale: float = 1.0,
+               dh_dtype: torch.dtype = torch.float32):
     """Whole vocab-tiled CE on a device-resident fp16 lm_head weight [V, d].
 
-    Returns (nll, lse, entropy, argmax, denom, dh_pre) where denom is a float32 device scalar
-    (num_items_in_batch, else the count of labels != -100, clamped to >= 1) and dh_pre the fp32
-    hidden gradient of sum(nll)/denom times 2^16 (None without need_grad). ``v_chunk`` bounds the
-    fp16 logit-gradient buffer to [n_tok, v_chunk] (default: the whole vocabulary in one pass).
+    Returns (nll, lse, entropy, argmax, denom, dh, loss) where denom is a float32 device scalar
+    (num_items_in_batch, else the count of labels != -100, clamped to >= 1), loss = sum(nll) /
+    denom (device scalar) and dh the hidden gradient of loss times 2^16, scaled by ``dh_scale``
+    and stored as ``dh_dtype`` (None without need_grad). ``v_chunk`` bounds the fp16
+    logit-gradient buffer to [n_tok, v_chunk] (default: the whole vocabulary in one pass).
     """
     fn = "lm_head_ce"
     _require_device(fn, hidden, weight, labels)
@@ -770,12 +857,7 @@ def lm_head_ce(hidden: torch.Tensor, weight: torch.Tensor, labels: torch.Tensor,
     for start in range(0, V, chunk):
         lm_head_ce_fwd_chunk(hidden, weight[start:start + chunk], lab, start, parts, target)
     lse, nll, ent, amax = lm_head_ce_combine(parts, target, lab)
-    if num_items_in_batch is None:
-        denom = (lab != -100).sum().to(torch.float32).clamp_(min=1.0).reshape(1)
-    elif isinstance(num_items_in_batch, torch.Tensor):
-        denom = num_items_in_batch.detach().to(device=dev, dtype=torch.float32).reshape(1).clamp(min=1.0)
-    else:
-        denom = torch.full((1,), max(float(num_items_in_batch), 1.0), dtype=torch.float32, device=dev)
+    loss, denom = lm_head_ce_loss(nll, lab, num_items_in_batch)
     dh_pre = None
     if need_grad:
         wt = weight_t if weight_t is not None else lm_head_weight_t(weight)
@@ -790,5 +872,5 @@ def lm_head_ce(hidden: torch.Tensor, weight: torch.Tensor, labels: torch.Tensor,
             ns = lm_head_split_count(n_tok, d, end - start)
             lm_head_ce_grad_hidden(g, wt[:, start:], end - start, dparts[:ns], accumulate=not first)
             first = False
-        dh_pre = lm_head_dh_reduce(dparts, 1.0, torch.float32)
-    return nll, lse, ent, amax, denom, dh_pre
+        dh_pre = lm_head_dh_reduce(dparts, dh_scale, dh_dtype)
+    return nll, lse, ent, amax, denom, dh_pre, loss

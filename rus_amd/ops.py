@@ -136,7 +136,7 @@ def _lm_head_streamed(h_2d, labels, head: HostHead, num_items_in_batch, need_gra
         if c + 1 < len(starts) or need_grad:
             head.release_chunk(c)
     lse, nll, ent, amax = K.lm_head_ce_combine(parts, target, labels)
-    denom = _denominator(labels, num_items_in_batch, dev)
+    loss, denom = K.lm_head_ce_loss(nll, labels, num_items_in_batch)
     dh_pre = None
     if need_grad:
         g = torch.empty((n_tok, K._round_up(vc, K.LM_K)), dtype=torch.float16, device=dev)
@@ -155,15 +155,7 @@ def _lm_head_streamed(h_2d, labels, head: HostHead, num_items_in_batch, need_gra
             K.lm_head_ce_grad_hidden(g, wt, e - s, dparts[:ns], accumulate=True)
             head.release_chunk(c)
         dh_pre = K.lm_head_dh_reduce(dparts, 1.0, torch.float32)
-    return nll, lse, ent, amax, denom, dh_pre
-
-
-def _denominator(labels, num_items_in_batch, dev):
-    if num_items_in_batch is None:
-        return (labels != -100).sum().to(torch.float32).clamp_(min=1.0).reshape(1)
-    if isinstance(num_items_in_batch, torch.Tensor):
-        return num_items_in_batch.detach().to(dev, torch.float32).reshape(1).clamp(min=1.0)
-    return torch.full((1,), max(float(num_items_in_batch), 1.0), dtype=torch.float32, device=dev)
+    return nll, lse, ent, amax, denom, dh_pre, loss
 
 
 class FusedChunkedLMHeadFn(torch.autograd.Function):
@@ -181,17 +173,18 @@ class FusedChunkedLMHeadFn(torch.autograd.Function):
         # reference tests, ops.py:280) is False here; ask autograd whether dH is needed instead.
         need_grad = bool(ctx.needs_input_grad[0])
         if is_head and not weight_or_host_head.resident:
-            nll, lse, ent, amax, denom, dh_pre = _lm_head_streamed(
+            nll, lse, ent, amax, denom, dh_pre, loss = _lm_head_streamed(
                 h_2d, labels, weight_or_host_head, num_items_in_batch, need_grad)
+            loss = loss[0]
         else:
             if is_head:
                 w, wt = weight_or_host_head.gpu_weight, weight_or_host_head.gpu_weight_t
             else:
                 w, wt = weight_or_host_head.detach(), None
-            nll, lse, ent, amax, denom, dh_pre = K.lm_head_ce(
+            nll, lse, ent, amax, denom, dh_pre, loss = K.lm_head_ce(
                 h_2d, w, labels, num_items_in_batch=num_items_in_batch, v_chunk=v_chunk,
                 need_grad=need_grad, weight_t=wt)
-        loss = nll.sum() / denom[0]
+            loss = loss[0]
         ctx.save_for_backward(dh_pre)
         ctx.orig_shape = hidden_states.shape
         ctx.orig_dtype = hidden_states.dtype
@@ -242,7 +235,8 @@ class Qwen2FusedEngine:
     def __init__(self, model, device, resident_weights: bool = False, resident_head: bool = True,
                  offload_inputs: bool = False, max_pos: int = 2048,
                  max_mlp_tokens: int = MAX_MLP_TOKENS, v_chunk: int = V_CHUNK_DEFAULT,
-                 attention: str = "varlen"):
+                 attention: str = "varlen", dropout_seed: int | None = None,
+                 stream_unit: str = "layer"):
         from .model import QLoRAQwen2
 
         if not isinstance(model, QLoRAQwen2):
@@ -260,7 +254,8 @@ class Qwen2FusedEngine:
         self.head_dim = cfg.hidden_size // cfg.num_attention_heads
         self.rms_eps = float(cfg.rms_norm_eps)
         self.max_mlp_tokens = max_mlp_tokens
-        self.weight_stream = WeightStream(model.layers, self.device, resident=resident_weights)
+        self.weight_stream = WeightStream(model.layers, self.device, resident=resident_weights,
+                                          unit=stream_unit)
         self.layer_biases = self.weight_stream.layer_biases
         self.host_head = HostHead(model.embed, self.device, v_chunk=v_chunk, resident=resident_head)
         self.input_stream = InputStream(self.num_layers, self.hidden_size, 2048, self.device,
@@ -279,12 +274,41 @@ class Qwen2FusedEngine:
                              "or 'sdpa_rows' (torch SDPA per row, as the reference)")
         self.attention = attention
         self._flatten_lora()
+        # LoRA dropout: the counter-based masks of step k use seed (base + k), held on the device
+        # so that a captured graph advances it by itself. The base comes from torch's CPU
+        # generator unless given.
+        if dropout_seed is None:
+            dropout_seed = int(torch.randint(0, 2**62, (1,)).item())
+        self.dropout_seed = torch.tensor([dropout_seed], dtype=torch.int64, device=self.device)
+        self.last_dropout_seed = self.dropout_seed
+
+    def next_dropout_seed(self) -> torch.Tensor:
+        """Advances the device seed and returns a copy for one forward/backward pair."""
+        self.dropout_seed.add_(1)
+        self.last_dropout_seed = self.dropout_seed.clone()
+        return self.last_dropout_seed
+
+    @property
+    def lora_numel(self) -> int:
+        return self._lora_flat.numel()
+
+    def lora_views(self, flat: torch.Tensor) -> list[torch.Tensor]:
+        """Views of a flat buffer shaped like the LoRA parameters, in their order."""
+        out, off = [], 0
+        for p in self.lora_params:
+            n = p.numel()
+            out.append(flat[off: off + n].view(p.shape))
+            off += n
+        return out
 
     def _flatten_lora(self) -> None:
         """Makes the LoRA parameters views of one flat fp32 device buffer (same Parameter
         objects, so optimizers keep working) so that their fp16 copies for a step are one cast."""
         params = self.lora_params
         flat = torch.cat([p.detach().reshape(-1).to(self.device, torch.float32) for p in params])
+        if getattr(self, "_lora_flat", None) is not None and self._lora_flat.numel() == flat.numel():
+            self._lora_flat.copy_(flat)  # keep the address a captured graph reads
+            flat = self._lora_flat
         off = 0
         for p in params:
             n = p.numel()
@@ -293,17 +317,15 @@ class Qwen2FusedEngine:
         self._lora_flat = flat
         self._lora_ptrs = [p.data_ptr() for p in params]
 
+    def sync_lora_storage(self) -> None:
+        """Re-points the LoRA parameters at the flat buffer if any was re-assigned (values kept)."""
+        if [p.data_ptr() for p in self.lora_params] != self._lora_ptrs:
+            self._flatten_lora()
+
     def lora_fp16(self) -> list[torch.Tensor]:
         """fp16 copies of [q_A, q_B, v_A, v_B] per layer for one step (one cast kernel)."""
-        if [p.data_ptr() for p in self.lora_params] != self._lora_ptrs:
-            self._flatten_lora()  # a parameter was re-assigned since the last step
-        flat16 = self._lora_flat.to(torch.float16)
-        out, off = [], 0
-        for p in self.lora_params:
-            n = p.numel()
-            out.append(flat16[off: off + n].view(p.shape))
-            off += n
-        return out
+        self.sync_lora_storage()
+        return self.lora_views(self._lora_flat.to(torch.float16))
 
 
 def _run_packed_sdpa(q_rot, k_rot, v_out, row_lengths, num_heads, num_kv_heads, head_dim):
@@ -339,6 +361,14 @@ class VarlenMeta:
         self.cu = torch.tensor(cu, dtype=torch.int32, device=device)
         self.max_len = max(lens) if lens else 0
 
+    @classmethod
+    def from_device(cls, cu: torch.Tensor, max_len: int) -> "VarlenMeta":
+        """From an existing int32 device buffer (a captured graph's static cu_seqlens)."""
+        vm = cls.__new__(cls)
+        vm.cu = cu
+        vm.max_len = int(max_len)
+        return vm
+
 
 def _varlen_attn_fwd(q, k, v, vm: VarlenMeta):
     """Causal GQA flash attention over all packed rows in one launch: q [N, Hq, D], k/v
@@ -354,18 +384,23 @@ def _varlen_attn_bwd(dout, q, k, v, out, lse, rng, unused, vm: VarlenMeta):
     return dq, dk, dv
 
 
-def _lora_deltas(norm1, q_A, q_B, v_A, v_B, meta, training):
-    """(x_drop_q, mid_q, q_lora, x_drop_v, mid_v, v_lora, fp16 A/B) with the dropout order of
-    solution/ops.py:775-778 (q first, then v)."""
-    dt = norm1.dtype
-    qA, qB, vA, vB = (p if p.dtype == dt else p.to(dt) for p in (q_A, q_B, v_A, v_B))
-    x_q = F.dropout(norm1, p=meta["p_q"], training=True) if (training and meta["p_q"] > 0) else norm1
+def _dropout_on(meta, training) -> bool:
+    return bool(training) and (meta["p_q"] > 0 or meta["p_v"] > 0)
+
+
+def _lora_inputs(norm1, layer, meta, training, seed):
+    """(x_q, x_v): the q- and v-branch LoRA inputs, dropped out with the counter-based masks of
+    streams 2*layer and 2*layer + 1 (one kernel), or norm1 itself without dropout."""
+    if _dropout_on(meta, training):
+        return K.lora_dropout_fwd(norm1, seed, 2 * layer, 2 * layer + 1, meta["p_q"], meta["p_v"])
+    return norm1, norm1
+
+
+def _lora_deltas(x_q, x_v, qA, qB, vA, vB):
+    """(mid_q, q_lora, mid_v, v_lora) = (x_q A_q^T, mid_q B_q^T, x_v A_v^T, mid_v B_v^T)."""
     mid_q = F.linear(x_q, qA)
-    q_lora = F.linear(mid_q, qB)
-    x_v = F.dropout(norm1, p=meta["p_v"], training=True) if (training and meta["p_v"] > 0) else norm1
     mid_v = F.linear(x_v, vA)
-    v_lora = F.linear(mid_v, vB)
-    return x_q, mid_q, q_lora, x_v, mid_v, v_lora, (qA, qB, vA, vB)
+    return mid_q, F.linear(mid_q, qB), mid_v, F.linear(mid_v, vB)
 
 
 def _mlp_fwd(norm2, w_gu, w_down, max_tokens):
@@ -379,187 +414,221 @@ def _mlp_fwd(norm2, w_gu, w_down, max_tokens):
     return out
 
 
-class FusedQwen2StackFn(torch.autograd.Function):
-    """All decoder layers on packed tokens with layer-input checkpointing, dropout RNG replay and
-    recompute in backward (solution/ops.py:729-1009). Returns the final-norm hidden states; the
-    gradient flows to the LoRA parameters only.
+class StackState:
+    """What the stack's backward needs from its forward: final-norm input and rstd, positions,
+    attention metadata, the step's fp16 LoRA copies, the dropout seed tensor and whether it ran
+    in training mode (layer inputs live in the engine's InputStream)."""
 
-    Each layer's input residual add is fused into the RMSNorm kernel (h_{l+1} = h_mid + mlp is
-    formed by the next layer's input norm), each weight segment is dequantised once per layer
-    per pass, and the backward's LoRA-delta gradients come out of the RoPE-adjoint kernel."""
+    __slots__ = ("pos_ids", "h_last", "final_rstd", "vm", "row_lengths", "lora16", "training",
+                 "seed", "buf")
+
+    def __init__(self, **kw):
+        for k, v in kw.items():
+            setattr(self, k, v)
+
+
+def stack_forward(engine, h_packed, pos_ids, row_lengths, training, lora16, seed, vm=None):
+    """All decoder layers over packed tokens (solution/ops.py:736-830) -> (final_norm, state).
+
+    No host synchronisation and no allocation outside torch's caching allocator, so it can run
+    inside a captured HIP graph. Each layer's input residual add is fused into the RMSNorm kernel
+    (h_{l+1} = h_mid + mlp is formed by the next layer's input norm) and the four weight segments
+    of a layer are dequantised in one launch."""
+    ws, ins = engine.weight_stream, engine.input_stream
+    L = engine.num_layers
+    cos, sin, eps = engine.cos_table, engine.sin_table, engine.rms_eps
+    h = h_packed.contiguous()
+    carry = None  # (h_mid, mlp_out) of the previous layer, added inside the next norm
+    n_tok = h.shape[0]
+    hq, hd = engine.num_heads, engine.head_dim
+    if vm is None and engine.attention == "varlen":
+        vm = VarlenMeta(row_lengths, engine.device)
+    if L > 0:
+        ws.prefetch(0)
+    for l in range(L):
+        if l + 1 < L:
+            ws.prefetch(l + 1)
+        if carry is None:
+            norm1, _, _ = K.rms_norm_fwd(h, engine.ln1_weights[l], eps=eps)
+        else:
+            norm1, h, _ = K.rms_norm_fwd(carry[1], engine.ln1_weights[l], eps=eps, residual=carry[0])
+        ins.save(l, h)
+        ws.wait_slot(l)
+        W = ws.dequant_layer(l)  # one launch for [q|k|v], o, [gate|up], down
+        ws.release_slot(l)
+        qkv = F.linear(norm1, W["qkv"], engine.layer_biases[l])
+        meta = engine.layer_lora_meta[l]
+        x_q, x_v = _lora_inputs(norm1, l, meta, training, seed)
+        _, q_lora, _, v_lora = _lora_deltas(x_q, x_v, *lora16[4 * l: 4 * l + 4])
+        del x_q, x_v
+        q_rot, k_rot, v_out = K.qkv_rope_fwd(qkv, cos, sin, pos_ids, q_lora=q_lora, v_lora=v_lora,
+                                             scale_q=meta["scale_q"], scale_v=meta["scale_v"],
+                                             h_q=engine.num_heads, h_kv=engine.num_kv_heads,
+                                             head_dim=engine.head_dim)
+        del qkv, q_lora, v_lora, norm1
+        if vm is not None:
+            attn = _varlen_attn_fwd(q_rot, k_rot, v_out, vm)[0].view(n_tok, hq * hd)
+        else:
+            attn = _run_packed_sdpa(q_rot, k_rot, v_out, row_lengths, engine.num_heads,
+                                    engine.num_kv_heads, engine.head_dim)
+        del q_rot, k_rot, v_out
+        o_out = F.linear(attn, W["o"])
+        del attn
+        norm2, h_mid, _ = K.rms_norm_fwd(o_out, engine.ln2_weights[l], eps=eps, residual=h)
+        del o_out
+        mlp_out = _mlp_fwd(norm2, W["gu"], W["down"], engine.max_mlp_tokens)
+        del norm2, W
+        carry = (h_mid, mlp_out)
+    if carry is None:
+        final_norm, h_last, final_rstd = K.rms_norm_fwd(h, engine.final_norm_weight, eps=eps)
+    else:
+        final_norm, h_last, final_rstd = K.rms_norm_fwd(carry[1], engine.final_norm_weight,
+                                                        eps=eps, residual=carry[0])
+    st = StackState(pos_ids=pos_ids, h_last=h_last, final_rstd=final_rstd, vm=vm,
+                    row_lengths=row_lengths, lora16=lora16, training=training, seed=seed,
+                    buf=ws.active if ws.unit == "model" else 0)
+    return final_norm, st
+
+
+def stack_backward(engine, st: StackState, d_final_norm, grad16) -> torch.Tensor:
+    """Recompute + manual backward of every layer (solution/ops.py:832-1009). Writes the fp16
+    LoRA gradients into ``grad16`` (flat, in the engine's parameter order) and returns the
+    gradient of the packed embedding output."""
+    ws, ins = engine.weight_stream, engine.input_stream
+    L = engine.num_layers
+    cos, sin, eps = engine.cos_table, engine.sin_table, engine.rms_eps
+    training, seed, pos_ids = st.training, st.seed, st.pos_ids
+    n_tokens = pos_ids.shape[0]
+    hq, hkv, hd = engine.num_heads, engine.num_kv_heads, engine.head_dim
+    q_dim = hq * hd
+    gviews = engine.lora_views(grad16)
+
+    dh = K.rms_norm_bwd(d_final_norm.contiguous(), st.h_last, engine.final_norm_weight,
+                        st.final_rstd)
+    ws.use_buffer(st.buf)
+    if L > 0:
+        ws.prefetch(L - 1)
+    for l in range(L - 1, -1, -1):
+        if l - 1 >= 0:
+            ws.prefetch(l - 1)
+            ins.prefetch(l - 1, n_tokens)
+        h_in = ins.load(l, n_tokens)
+        ws.wait_slot(l)
+        W = ws.dequant_layer(l)
+        w_qkv, w_o, w_gu, w_down = W["qkv"], W["o"], W["gu"], W["down"]
+        ws.release_slot(l)  # every read of the packed slot is enqueued
+
+        # Recompute the layer forward (same dropout masks: same seed and streams).
+        norm1, _, rstd1 = K.rms_norm_fwd(h_in, engine.ln1_weights[l], eps=eps)
+        qkv = F.linear(norm1, w_qkv, engine.layer_biases[l])
+        meta = engine.layer_lora_meta[l]
+        qA, qB, vA, vB = st.lora16[4 * l: 4 * l + 4]
+        x_q, x_v = _lora_inputs(norm1, l, meta, training, seed)
+        mid_q, q_lora, mid_v, v_lora = _lora_deltas(x_q, x_v, qA, qB, vA, vB)
+        q_rot, k_rot, v_out = K.qkv_rope_fwd(qkv, cos, sin, pos_ids, q_lora=q_lora, v_lora=v_lora,
+                                             scale_q=meta["scale_q"], scale_v=meta["scale_v"],
+                                             h_q=hq, h_kv=hkv, head_dim=hd)
+        del qkv, q_lora, v_lora
+        if st.vm is not None:
+            attn, lse, rng, unused = _varlen_attn_fwd(q_rot, k_rot, v_out, st.vm)
+            attn2d = attn.view(n_tokens, q_dim)
+        else:
+            with torch.enable_grad():
+                q_req = q_rot.detach().requires_grad_(True)
+                k_req = k_rot.detach().requires_grad_(True)
+                v_req = v_out.detach().requires_grad_(True)
+                attn = _run_packed_sdpa(q_req, k_req, v_req, st.row_lengths, hq, hkv, hd)
+            attn2d = attn.detach()
+        o_out = F.linear(attn2d, w_o)
+        norm2, h_mid, rstd2 = K.rms_norm_fwd(o_out, engine.ln2_weights[l], eps=eps, residual=h_in)
+        del o_out
+
+        # MLP backward: d_act = dh . W_down; SwiGLU backward in place over gu; d_norm2.
+        d_norm2 = torch.empty_like(norm2)
+        step = min(engine.max_mlp_tokens, n_tokens)
+        for s in range(0, n_tokens, step):
+            e = min(s + step, n_tokens)
+            gu = F.linear(norm2[s:e], w_gu)
+            K.mlp_glu_bwd(torch.mm(dh[s:e], w_down), gu)
+            torch.mm(gu, w_gu, out=d_norm2[s:e])
+            del gu
+        del norm2
+        dh_mid = K.rms_norm_bwd(d_norm2, h_mid, engine.ln2_weights[l], rstd2, dresidual=dh)
+        del d_norm2, h_mid, rstd2, dh
+
+        # Attention backward, adjoint RoPE with [dQ|dK|dV] packing and LoRA-delta gradients.
+        d_attn = torch.mm(dh_mid, w_o)
+        if st.vm is not None:
+            dq, dk, dv = _varlen_attn_bwd(d_attn.view(n_tokens, hq, hd), q_rot, k_rot, v_out,
+                                          attn, lse, rng, unused, st.vm)
+            del lse, rng, unused
+        else:
+            dq, dk, dv = torch.autograd.grad(attn, (q_req, k_req, v_req), d_attn)
+            del q_req, k_req, v_req
+        del attn, attn2d, d_attn, q_rot, k_rot, v_out
+        dqkv, dq_scaled, dv_scaled = K.qkv_rope_bwd_lora(dq, dk, dv, cos, sin, pos_ids,
+                                                         meta["scale_q"], meta["scale_v"],
+                                                         h_q=hq, h_kv=hkv, head_dim=hd)
+        del dq, dk, dv
+
+        # LoRA parameter gradients (solution/ops.py:975-983), written into the flat buffer.
+        g_qA, g_qB, g_vA, g_vB = gviews[4 * l: 4 * l + 4]
+        torch.mm(dq_scaled.t(), mid_q, out=g_qB)
+        d_mid_q = torch.mm(dq_scaled, qB)
+        torch.mm(d_mid_q.t(), x_q, out=g_qA)
+        dx_q = torch.mm(d_mid_q, qA)
+        torch.mm(dv_scaled.t(), mid_v, out=g_vB)
+        d_mid_v = torch.mm(dv_scaled, vB)
+        torch.mm(d_mid_v.t(), x_v, out=g_vA)
+        dx_v = torch.mm(d_mid_v, vA)
+        del mid_q, mid_v, x_q, x_v, d_mid_q, d_mid_v, dq_scaled, dv_scaled
+
+        d_norm1 = torch.mm(dqkv, w_qkv)
+        if _dropout_on(meta, training):  # masks of the forward, then the two adds (ops.py:986-992)
+            K.lora_dropout_bwd_add(d_norm1, dx_q, dx_v, seed, 2 * l, 2 * l + 1, meta["p_q"],
+                                   meta["p_v"])
+        else:
+            d_norm1.add_(dx_q).add_(dx_v)
+        del dqkv, dx_q, dx_v, norm1
+        dh = K.rms_norm_bwd(d_norm1, h_in, engine.ln1_weights[l], rstd1, dresidual=dh_mid)
+        ins.release(l)
+        del d_norm1, h_in, rstd1, dh_mid
+    return dh
+
+
+class FusedQwen2StackFn(torch.autograd.Function):
+    """All decoder layers on packed tokens with layer-input checkpointing and recompute in
+    backward (solution/ops.py:729-1009). Returns the final-norm hidden states; the gradient flows
+    to the LoRA parameters only.
+
+    LoRA dropout masks come from a counter-based generator keyed by a per-forward seed (a device
+    tensor drawn from the engine), so the recompute draws the same masks without saving or
+    restoring torch's generator state."""
 
     @staticmethod
     def forward(ctx, h_packed, pos_ids, row_lengths, engine, training, *lora_params):
-        ws, ins = engine.weight_stream, engine.input_stream
-        L = engine.num_layers
-        cos, sin, eps = engine.cos_table, engine.sin_table, engine.rms_eps
-        rng_states = []
-        h = h_packed.contiguous()
-        carry = None  # (h_mid, mlp_out) of the previous layer, added inside the next norm
-        n_tok = h.shape[0]
-        hq, hd = engine.num_heads, engine.head_dim
-        vm = VarlenMeta(row_lengths, engine.device) if engine.attention == "varlen" else None
+        seed = engine.next_dropout_seed() if training else engine.dropout_seed
         lora16 = engine.lora_fp16()
-        if L > 0:
-            ws.prefetch(0)
-        for l in range(L):
-            if l + 1 < L:
-                ws.prefetch(l + 1)
-            if carry is None:
-                norm1, _, _ = K.rms_norm_fwd(h, engine.ln1_weights[l], eps=eps)
-            else:
-                norm1, h, _ = K.rms_norm_fwd(carry[1], engine.ln1_weights[l], eps=eps, residual=carry[0])
-            ins.save(l, h)
-            rng_states.append(torch.cuda.get_rng_state(engine.device) if training else None)
-            ws.wait_slot(l)
-            W = ws.dequant_layer(l)  # one launch for [q|k|v], o, [gate|up], down
-            ws.release_slot(l)
-            qkv = F.linear(norm1, W["qkv"], engine.layer_biases[l])
-            meta = engine.layer_lora_meta[l]
-            _, _, q_lora, _, _, v_lora, _ = _lora_deltas(norm1, *lora16[4 * l: 4 * l + 4], meta, training)
-            q_rot, k_rot, v_out = K.qkv_rope_fwd(qkv, cos, sin, pos_ids, q_lora=q_lora, v_lora=v_lora,
-                                                 scale_q=meta["scale_q"], scale_v=meta["scale_v"],
-                                                 h_q=engine.num_heads, h_kv=engine.num_kv_heads,
-                                                 head_dim=engine.head_dim)
-            del qkv, q_lora, v_lora, norm1
-            if vm is not None:
-                attn = _varlen_attn_fwd(q_rot, k_rot, v_out, vm)[0].view(n_tok, hq * hd)
-            else:
-                attn = _run_packed_sdpa(q_rot, k_rot, v_out, row_lengths, engine.num_heads,
-                                        engine.num_kv_heads, engine.head_dim)
-            del q_rot, k_rot, v_out
-            o_out = F.linear(attn, W["o"])
-            del attn
-            norm2, h_mid, _ = K.rms_norm_fwd(o_out, engine.ln2_weights[l], eps=eps, residual=h)
-            del o_out
-            mlp_out = _mlp_fwd(norm2, W["gu"], W["down"], engine.max_mlp_tokens)
-            del norm2, W
-            carry = (h_mid, mlp_out)
-        if carry is None:
-            final_norm, h_last, final_rstd = K.rms_norm_fwd(h, engine.final_norm_weight, eps=eps)
-        else:
-            final_norm, h_last, final_rstd = K.rms_norm_fwd(carry[1], engine.final_norm_weight,
-                                                            eps=eps, residual=carry[0])
-        ctx.save_for_backward(pos_ids, h_last, final_rstd, *lora_params)
-        ctx.row_lengths = row_lengths
-        ctx.vm = vm
-        ctx.lora16 = lora16
+        ws = engine.weight_stream
+        buf = ws.begin_step()
+        final_norm, st = stack_forward(engine, h_packed, pos_ids, row_lengths, training, lora16,
+                                       seed)
+        ws.end_step(buf)  # released again after the backward
+        ctx.save_for_backward(*lora_params)
+        ctx.st = st
         ctx.engine = engine
-        ctx.training = training
-        ctx.rng_states = rng_states
         return final_norm
 
     @staticmethod
     def backward(ctx, d_final_norm):
-        saved = ctx.saved_tensors
-        pos_ids, h_last, final_rstd = saved[0], saved[1], saved[2]
-        lora_params = saved[3:]
         engine = ctx.engine
-        ws, ins = engine.weight_stream, engine.input_stream
-        L = engine.num_layers
-        cos, sin, eps = engine.cos_table, engine.sin_table, engine.rms_eps
-        training = ctx.training
-        saved_rng = torch.cuda.get_rng_state(engine.device)
-        n_tokens = pos_ids.shape[0]
-        hq, hkv, hd = engine.num_heads, engine.num_kv_heads, engine.head_dim
-        q_dim = hq * hd
-
-        dh = K.rms_norm_bwd(d_final_norm.contiguous(), h_last, engine.final_norm_weight, final_rstd)
-        lora_grads = [None] * (4 * L)
-        if L > 0:
-            ws.prefetch(L - 1)
-        for l in range(L - 1, -1, -1):
-            if l - 1 >= 0:
-                ws.prefetch(l - 1)
-                ins.prefetch(l - 1, n_tokens)
-            h_in = ins.load(l, n_tokens)
-            ws.wait_slot(l)
-            W = ws.dequant_layer(l)
-            w_qkv, w_o, w_gu, w_down = W["qkv"], W["o"], W["gu"], W["down"]
-            ws.release_slot(l)  # every read of the packed slot is enqueued
-            if training and ctx.rng_states[l] is not None:
-                torch.cuda.set_rng_state(ctx.rng_states[l], engine.device)
-
-            # Recompute the layer forward.
-            norm1, _, rstd1 = K.rms_norm_fwd(h_in, engine.ln1_weights[l], eps=eps)
-            qkv = F.linear(norm1, w_qkv, engine.layer_biases[l])
-            meta = engine.layer_lora_meta[l]
-            q_A, q_B, v_A, v_B = lora_params[4 * l: 4 * l + 4]
-            x_q, mid_q, q_lora, x_v, mid_v, v_lora, (qA, qB, vA, vB) = _lora_deltas(
-                norm1, *ctx.lora16[4 * l: 4 * l + 4], meta, training)
-            q_rot, k_rot, v_out = K.qkv_rope_fwd(qkv, cos, sin, pos_ids, q_lora=q_lora, v_lora=v_lora,
-                                                 scale_q=meta["scale_q"], scale_v=meta["scale_v"],
-                                                 h_q=hq, h_kv=hkv, head_dim=hd)
-            del qkv, q_lora, v_lora
-            if ctx.vm is not None:
-                attn, lse, rng, unused = _varlen_attn_fwd(q_rot, k_rot, v_out, ctx.vm)
-                attn2d = attn.view(n_tokens, q_dim)
-            else:
-                with torch.enable_grad():
-                    q_req = q_rot.detach().requires_grad_(True)
-                    k_req = k_rot.detach().requires_grad_(True)
-                    v_req = v_out.detach().requires_grad_(True)
-                    attn = _run_packed_sdpa(q_req, k_req, v_req, ctx.row_lengths, hq, hkv, hd)
-                attn2d = attn.detach()
-            o_out = F.linear(attn2d, w_o)
-            norm2, h_mid, rstd2 = K.rms_norm_fwd(o_out, engine.ln2_weights[l], eps=eps, residual=h_in)
-            del o_out
-
-            # MLP backward: d_act = dh . W_down; SwiGLU backward in place over gu; d_norm2.
-            d_norm2 = torch.empty_like(norm2)
-            step = min(engine.max_mlp_tokens, n_tokens)
-            for s in range(0, n_tokens, step):
-                e = min(s + step, n_tokens)
-                gu = F.linear(norm2[s:e], w_gu)
-                K.mlp_glu_bwd(torch.mm(dh[s:e], w_down), gu)
-                torch.mm(gu, w_gu, out=d_norm2[s:e])
-                del gu
-            del norm2
-            dh_mid = K.rms_norm_bwd(d_norm2, h_mid, engine.ln2_weights[l], rstd2, dresidual=dh)
-            del d_norm2, h_mid, rstd2, dh
-
-            # Attention backward, adjoint RoPE with [dQ|dK|dV] packing and LoRA-delta gradients.
-            d_attn = torch.mm(dh_mid, w_o)
-            if ctx.vm is not None:
-                dq, dk, dv = _varlen_attn_bwd(d_attn.view(n_tokens, hq, hd), q_rot, k_rot, v_out,
-                                              attn, lse, rng, unused, ctx.vm)
-                del lse, rng, unused
-            else:
-                dq, dk, dv = torch.autograd.grad(attn, (q_req, k_req, v_req), d_attn)
-                del q_req, k_req, v_req
-            del attn, attn2d, d_attn, q_rot, k_rot, v_out
-            dqkv, dq_scaled, dv_scaled = K.qkv_rope_bwd_lora(dq, dk, dv, cos, sin, pos_ids,
-                                                             meta["scale_q"], meta["scale_v"],
-                                                             h_q=hq, h_kv=hkv, head_dim=hd)
-            del dq, dk, dv
-
-            # LoRA parameter gradients (solution/ops.py:975-983).
-            d_qB = torch.mm(dq_scaled.t(), mid_q).to(q_B.dtype)
-            d_mid_q = torch.mm(dq_scaled, qB)
-            d_qA = torch.mm(d_mid_q.t(), x_q).to(q_A.dtype)
-            dx_q = torch.mm(d_mid_q, qA)
-            d_vB = torch.mm(dv_scaled.t(), mid_v).to(v_B.dtype)
-            d_mid_v = torch.mm(dv_scaled, vB)
-            d_vA = torch.mm(d_mid_v.t(), x_v).to(v_A.dtype)
-            dx_v = torch.mm(d_mid_v, vA)
-            del mid_q, mid_v, x_q, x_v, d_mid_q, d_mid_v, dq_scaled, dv_scaled
-            if training and ctx.rng_states[l] is not None:
-                torch.cuda.set_rng_state(ctx.rng_states[l], engine.device)
-            if training and meta["p_q"] > 0:
-                dx_q = F.dropout(dx_q, p=meta["p_q"], training=True)
-            if training and meta["p_v"] > 0:
-                dx_v = F.dropout(dx_v, p=meta["p_v"], training=True)
-
-            d_norm1 = torch.mm(dqkv, w_qkv)
-            d_norm1.add_(dx_q).add_(dx_v)
-            del dqkv, dx_q, dx_v, norm1
-            dh = K.rms_norm_bwd(d_norm1, h_in, engine.ln1_weights[l], rstd1, dresidual=dh_mid)
-            ins.release(l)
-            del d_norm1, h_in, rstd1, dh_mid
-            lora_grads[4 * l: 4 * l + 4] = [d_qA, d_qB, d_vA, d_vB]
-        torch.cuda.set_rng_state(saved_rng, engine.device)
+        grad16 = torch.empty(engine.lora_numel, dtype=torch.float16, device=engine.device)
+        dh = stack_backward(engine, ctx.st, d_final_norm, grad16)
+        engine.weight_stream.end_step(ctx.st.buf)
+        grads = engine.lora_views(grad16.float())  # the reference's .to(param dtype), one cast
         ctx.d_h_packed = dh  # gradient w.r.t. the embedding output (frozen), kept for tests
-        return (None, None, None, None, None, *lora_grads)
+        del ctx.st
+        return (None, None, None, None, None, *grads)
 
 
 # ---------------------------------------------------------------------------------------------

@@ -269,3 +269,36 @@ def test_swiglu_fwd_bwd(dtype, fused, shape):
         assert torch.allclose(out, out_r, rtol=1e-5, atol=1e-6)
         assert torch.allclose(dg, dg_r, rtol=1e-5, atol=1e-6)
         assert torch.allclose(du, du_r, rtol=1e-5, atol=1e-6)
+
+
+# ---------------------------------------------------------------------------------------------
+# LoRA-input dropout: bit-exact against the oracle's Philox masks
+# ---------------------------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+@pytest.mark.parametrize("shape,strided", [((311, 1536), False), ((77, 1001), False), ((64, 256), True)])
+def test_lora_dropout_fwd_bwd_bit_exact(dtype, shape, strided):
+    g = torch.Generator().manual_seed(9)
+    n, c = shape
+    seed_v, sa, sb, pa, pb = 123456789, 6, 7, 0.05, 0.1
+    x = torch.randn(n, c, generator=g).to(dtype)
+    acc, ga, gb = (torch.randn(n, c, generator=g).to(dtype) for _ in range(3))
+    seed = torch.tensor([seed_v], dtype=torch.int64, device=DEV)
+    xd = x.to(DEV)
+    if strided:  # rows of a wider buffer (the vector path needs 8-aligned strides)
+        xd = torch.zeros(n, c + 64, dtype=dtype, device=DEV)[:, :c]
+        xd.copy_(x.to(DEV))
+    a, b = K.lora_dropout_fwd(xd, seed, sa, sb, pa, pb)
+    wa, wb = ref.lora_dropout_fwd(x, seed_v, sa, sb, pa, pb)
+    torch.cuda.synchronize()
+    assert torch.equal(a.cpu(), wa) and torch.equal(b.cpu(), wb)
+    accd = acc.to(DEV)
+    K.lora_dropout_bwd_add(accd, ga.to(DEV), gb.to(DEV), seed, sa, sb, pa, pb)
+    torch.cuda.synchronize()
+    assert torch.equal(accd.cpu(), ref.lora_dropout_bwd_add(acc, ga, gb, seed_v, sa, sb, pa, pb))
+    # the kernel reads the seed from device memory on every launch
+    seed.fill_(seed_v + 1)
+    a2, _ = K.lora_dropout_fwd(xd, seed, sa, sb, pa, pb)
+    torch.cuda.synchronize()
+    assert torch.equal(a2.cpu(), ref.lora_dropout_fwd(x, seed_v + 1, sa, sb, pa, pb)[0])

@@ -24,7 +24,7 @@ DEV = "cuda"
 
 
 def _check_against_oracle(h, w, labels, out, rows=None, denom=None, check_dh=True):
-    nll, lse, ent, amax, dn, dh_pre = out
+    nll, lse, ent, amax, dn, dh_pre = out[:6]
     rows = torch.arange(h.shape[0]) if rows is None else rows
     o = ref.lm_head_ce(h[rows], w, labels[rows], num_items_in_batch=denom, v_chunk=16384,
                        need_grad=check_dh)
@@ -70,6 +70,7 @@ def test_lmhead_reference_case(v_chunk):
     o = _check_against_oracle(h2, weight, lab, out)
     loss = out[0].sum().cpu() / out[4].cpu()
     assert abs(float(loss) - float(o["loss"])) <= 1e-3
+    assert abs(float(out[6].cpu()) - float(loss)) <= 1e-6 * abs(float(loss))  # device loss kernel
     # Full-logit library reference, as the reference test does (test_kernels.py:203-217).
     z = h2.float() @ weight.float().t()
     loss_lib = torch.nn.functional.cross_entropy(z, lab, ignore_index=-100)
@@ -120,9 +121,9 @@ def test_lmhead_all_masked_and_ties():
     w[3] = 0.01
     w[600] = 0.01  # tie between index 3 and 600 (different 256-row partials)
     lab = torch.full((N,), -100, dtype=torch.long)
-    nll, lse, ent, amax, denom, dh_pre = K.lm_head_ce(h.to(DEV), w.to(DEV), lab.to(DEV))
+    nll, lse, ent, amax, denom, dh_pre, loss = K.lm_head_ce(h.to(DEV), w.to(DEV), lab.to(DEV))
     torch.cuda.synchronize()
-    assert float(denom.item()) == 1.0
+    assert float(denom.item()) == 1.0 and float(loss.item()) == 0.0
     assert torch.all(nll.cpu() == 0)
     assert torch.all(amax.cpu() == 3)
     assert torch.all(dh_pre.cpu() == 0)

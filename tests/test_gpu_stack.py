@@ -4,8 +4,9 @@
   model with dropout off: loss within 2e-3 relative, every LoRA gradient tensor within 1e-2 in
   relative Frobenius norm (||g - g_ref|| <= 1e-2 ||g_ref||; fp16 activations against fp32).
 * Streamed (pinned host, two slots) and HBM-resident weights give bit-identical results.
-* With dropout on, the fused stack's RNG replay draws the same masks as a plain autograd eager
-  step started from the same RNG state (rus_amd.eager_reference): same tolerances.
+* With dropout on, the fused stack (forward masks re-drawn in the backward recompute) matches a
+  plain autograd eager step using the same counter-based masks (rus_amd.eager_reference) and the
+  CPU oracle given the oracle's own Philox masks: same tolerances.
 """
 
 from __future__ import annotations
@@ -83,39 +84,52 @@ def test_streamed_and_resident_weights_agree_bitwise():
     ids, mask, labels = _batch(cfg, [30, 50], seed=1)
     pb = ops.pack_varlen(ids, mask, labels)
     out = []
-    for resident in (False, True):
-        engine = ops.Qwen2FusedEngine(model, DEV, resident_weights=resident)
+    for resident, unit in ((False, "layer"), (False, "model"), (True, "layer")):
+        engine = ops.Qwen2FusedEngine(model, DEV, resident_weights=resident, stream_unit=unit)
         out.append(_fused_step(engine, pb, training=False))
-    assert torch.equal(out[0][0], out[1][0])
-    for a, b in zip(out[0][1], out[1][1]):
-        assert torch.equal(a, b)
+        out.append(_fused_step(engine, pb, training=False))  # second step: the other buffer
+    for o in out[1:]:
+        assert torch.equal(out[0][0], o[0])
+        for a, b in zip(out[0][1], o[1]):
+            assert torch.equal(a, b)
 
 
-def test_dropout_replay_matches_eager_autograd():
+def test_dropout_masks_match_eager_autograd_and_oracle():
     cfg = small_config(dropout=0.05)
     model = M.build_random_qlora_qwen2(cfg, DEV, seed=3, std=0.05)
     engine = ops.Qwen2FusedEngine(model, DEV, resident_weights=True)
     ids, mask, labels = _batch(cfg, [40, 33, 60], seed=2)
     pb = ops.pack_varlen(ids, mask, labels)
-    torch.manual_seed(1234)
     loss_f, grads_f = _fused_step(engine, pb, training=True)
+    seed = engine.last_dropout_seed
 
     for p in engine.lora_params:
         p.grad = None
-    torch.manual_seed(1234)
     h = engine.host_head.embed(pb.input_ids.to(DEV))
     loss_e = eager_step_loss(engine, h, pb.pos_ids.to(DEV), pb.shift_labels.to(DEV),
-                             pb.row_lengths, training=True)
+                             pb.row_lengths, training=True, seed=seed)
     loss_e.backward()
     torch.cuda.synchronize()
     assert abs(float(loss_f) - float(loss_e)) <= 2e-3 * abs(float(loss_e))
     for gi, (g_f, p) in enumerate(zip(grads_f, engine.lora_params)):
         assert _rel(g_f, p.grad.cpu()) <= 1e-2, (gi, _rel(g_f, p.grad.cpu()))
+    # the CPU oracle with its own Philox masks for the same seed
+    deq = ostack.dequant_model(model)
+    lora = ostack.lora_leaves(model)
+    loss_ref, _ = ostack.step_loss(model, deq, lora, pb.input_ids, pb.pos_ids, pb.shift_labels,
+                                   pb.row_lengths, dropout_seed=int(seed.item()))
+    loss_ref.backward()
+    assert abs(float(loss_f) - float(loss_ref)) <= 2e-3 * abs(float(loss_ref))
+    for gi, (g_f, leaf) in enumerate(zip(grads_f, lora)):
+        assert _rel(g_f, leaf.grad) <= 1e-2, (gi, _rel(g_f, leaf.grad))
     # and the masks were really applied: without dropout the gradients differ
     for p in engine.lora_params:
         p.grad = None
     _, grads_nodrop = _fused_step(engine, pb, training=False)
     assert _rel(grads_nodrop[0], grads_f[0]) > 1e-2
+    # each training forward draws a new seed
+    _fused_step(engine, pb, training=True)
+    assert int(engine.last_dropout_seed.item()) == int(seed.item()) + 1
 
 
 def test_fused_causal_lm_forward_scatter():

@@ -291,6 +291,66 @@ def test_swiglu_fp16_within_one_ulp_of_float64():
 
 
 # ---------------------------------------------------------------------------------------------
+# LoRA-input dropout (Philox4x64-10 counter-based masks)
+# ---------------------------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("key", [(0, 0), (1, 2), (2**64 - 1, 12345), (20251201, 55)])
+@pytest.mark.parametrize("block", [1, 7, 2**40 + 3])
+def test_philox_matches_numpy_bit_generator(key, block):
+    # numpy.random.Philox is Philox4x64-10; it increments its 256-bit counter before each block.
+    raw = np.random.Philox(key=np.array(key, dtype=np.uint64),
+                           counter=np.array([block - 1, 0, 0, 0], dtype=np.uint64)).random_raw(4 * 3)
+    ctr = np.zeros((3, 4), dtype=np.uint64)
+    ctr[:, 0] = np.arange(block, block + 3, dtype=np.uint64)
+    got = ref.philox4x64_10(ctr, key)
+    assert np.array_equal(got.reshape(-1), raw.astype(np.uint64))
+
+
+def test_philox_counter_wraps_like_numpy():
+    raw = np.random.Philox(key=[3, 4], counter=[2**64 - 1] * 4).random_raw(4)
+    got = ref.philox4x64_10(np.zeros((1, 4), dtype=np.uint64), (3, 4))
+    assert np.array_equal(got.reshape(-1), raw.astype(np.uint64))
+
+
+def test_dropout_mask_rate_and_independence():
+    n_rows, n_cols, p = 625, 1600, 0.05  # 1e6 elements
+    m = ref.dropout_keep_mask(7, 0, n_rows, n_cols, p)
+    frac = 1.0 - m.mean()
+    assert abs(frac - p) < 5 * math.sqrt(p * (1 - p) / m.size)
+    m2 = ref.dropout_keep_mask(7, 1, n_rows, n_cols, p)
+    m3 = ref.dropout_keep_mask(8, 0, n_rows, n_cols, p)
+    both = ((~m) & (~m2)).mean()  # independent streams: P(both dropped) = p^2
+    assert abs(both - p * p) < 5 * math.sqrt(p * p * (1 - p * p) / m.size)
+    assert (m != m3).any()
+    assert ref.dropout_keep_mask(7, 0, n_rows, n_cols, 0.0).all()
+    # the mask of an element depends on its row-major index only, not on the row count
+    assert np.array_equal(ref.dropout_keep_mask(7, 0, 10, n_cols, p), m[:10])
+
+
+def test_dropout_fwd_values_and_bwd_rounding_order():
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(37, 96, generator=g).half()
+    a, b = ref.lora_dropout_fwd(x, 11, 4, 5, 0.05, 0.1)
+    ka = ref.dropout_keep_mask(11, 4, 37, 96, 0.05)
+    kt = torch.from_numpy(ka)
+    scale = torch.tensor(1.0) / (1.0 - torch.tensor(0.05))
+    assert torch.equal(a[~kt], torch.zeros_like(a[~kt]))
+    assert torch.equal(a[kt], (x[kt].float() * scale).half())
+    assert not torch.equal(a, b)
+    a0, _ = ref.lora_dropout_fwd(x, 11, 4, 5, 0.0, 0.0)
+    assert torch.equal(a0, x)
+    # backward: the reference's sequence of fp16 tensor ops (mask*scale, then two in-place adds)
+    acc = torch.randn(37, 96, generator=g).half()
+    ga = torch.randn(37, 96, generator=g).half()
+    gb = torch.randn(37, 96, generator=g).half()
+    da, _ = ref.lora_dropout_fwd(ga, 11, 4, 5, 0.05, 0.1)
+    _, db = ref.lora_dropout_fwd(gb, 11, 4, 5, 0.05, 0.1)
+    want = acc.clone().add_(da).add_(db)
+    assert torch.equal(ref.lora_dropout_bwd_add(acc, ga, gb, 11, 4, 5, 0.05, 0.1), want)
+
+
+# ---------------------------------------------------------------------------------------------
 # Chunked lm_head cross-entropy
 # ---------------------------------------------------------------------------------------------
 

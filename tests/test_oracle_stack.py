@@ -207,3 +207,26 @@ def test_model_from_duck_typed_causal_lm():
     assert torch.equal(G.q.packed, L.q.packed) and torch.equal(G.down.absmax2, L.down.absmax2)
     assert G.q_A is L.q_A and G.v_B is L.v_B
     assert got.meta["layer_lora_meta"][0]["p_q"] == 0.05
+
+
+def test_stack_oracle_dropout_uses_branch_masks():
+    # p > 0 with a seed changes the loss; the q-branch mask enters only through x A_q^T, so a
+    # zero A_q / A_v (no LoRA signal) makes dropout invisible.
+    cfg = M.Qwen2Config(**{**tiny_config().__dict__, "lora_dropout": 0.1})
+    model = M.build_random_qlora_qwen2(cfg, "cpu", seed=2, std=0.05)
+    deq = ostack.dequant_model(model)
+    lengths, S = [9, 14], 14
+    ids, mask, labels = _batch(cfg, lengths, S)
+    pb = pack_varlen(ids, mask, labels)
+    args = (pb.input_ids, pb.pos_ids, pb.shift_labels, pb.row_lengths)
+    lora = ostack.lora_leaves(model)
+    base, _ = ostack.step_loss(model, deq, lora, *args)
+    dropped, _ = ostack.step_loss(model, deq, lora, *args, dropout_seed=5)
+    again, _ = ostack.step_loss(model, deq, lora, *args, dropout_seed=5)
+    assert float(dropped) != float(base) and float(again) == float(dropped)
+    for li in range(cfg.num_hidden_layers):
+        for j in (4 * li, 4 * li + 2):  # A_q, A_v
+            lora[j] = torch.zeros_like(lora[j])
+    z0, _ = ostack.step_loss(model, deq, lora, *args)
+    z1, _ = ostack.step_loss(model, deq, lora, *args, dropout_seed=5)
+    assert float(z0) == float(z1)
