@@ -781,7 +781,8 @@ def lm_head_ce_grad_hidden(grad_logits: torch.Tensor, weight_t_cols: torch.Tenso
 
 
 def lm_head_dh_reduce(parts: torch.Tensor, scale: float, out_dtype=torch.float16,
-                      scale_dev: torch.Tensor | None = None) -> torch.Tensor:
+                      scale_dev: torch.Tensor | None = None,
+                      _tag: str = "lmhead_dh_reduce") -> torch.Tensor:
     """out = out_dtype(scale * scale_dev * sum over the leading split dimension of ``parts``);
     ``scale_dev`` is an optional one-element float32 device tensor (read on the device)."""
     fn = "lm_head_dh_reduce"
@@ -791,10 +792,15 @@ def lm_head_dh_reduce(parts: torch.Tensor, scale: float, out_dtype=torch.float16
     if scale_dev is not None and (scale_dev.dtype != torch.float32 or scale_dev.numel() != 1):
         raise ValueError(f"{fn}: scale_dev must be a one-element float32 tensor")
     out = torch.empty(parts.shape[1:], dtype=out_dtype, device=parts.device)
-    _launch("lmhead_dh_reduce", parts.numel() * 4 + out.numel() * out.element_size(), 0,
+    _launch(_tag, parts.numel() * 4 + out.numel() * out.element_size(), 0,
             "rus_lmhead_dh_reduce", parts.data_ptr(), parts.shape[0], out.numel(), float(scale),
               _ptr(scale_dev), out.data_ptr(), _dtype_code(fn, out_dtype), _stream(parts))
     return out
+
+
+def sum_splits(parts: torch.Tensor, out_dtype=torch.float16) -> torch.Tensor:
+    """out_dtype(sum over the leading dimension of fp32 ``parts``): the reduce of a split-K GEMM."""
+    return lm_head_dh_reduce(parts, 1.0, out_dtype, _tag="splitk_reduce")
 
 
 def lm_head_weight_t(weight: torch.Tensor) -> torch.Tensor:

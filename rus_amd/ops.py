@@ -414,6 +414,24 @@ def _mlp_fwd(norm2, w_gu, w_down, max_tokens):
     return out
 
 
+SPLIT_K_MIN = 8192  # reduction length from which the [N, K] x [K, D] backward GEMM is split
+
+
+def _mm_split_k(a: torch.Tensor, b: torch.Tensor, splits: int = 4) -> torch.Tensor:
+    """a [M, K] @ b [K, D] (fp16) with K split into ``splits`` slices: one batched GEMM into fp32
+    partials and one reduce kernel that rounds the sum to fp16 once (the single GEMM's rounding).
+    For the long-K, narrow-output MLP backward product (K = 17920, D = 1536), where one GEMM
+    leaves most of the GPU idle."""
+    M, Kd = a.shape
+    D = b.shape[1]
+    if Kd < SPLIT_K_MIN or Kd % splits or a.stride(1) != 1 or not b.is_contiguous():
+        return torch.mm(a, b)
+    ks = Kd // splits
+    parts = torch.bmm(a.view(M, splits, ks).permute(1, 0, 2), b.view(splits, ks, D),
+                      out_dtype=torch.float32)
+    return K.sum_splits(parts, a.dtype)
+
+
 class StackState:
     """What the stack's backward needs from its forward: final-norm input and rstd, positions,
     attention metadata, the step's fp16 LoRA copies, the dropout seed tensor and whether it ran
@@ -544,14 +562,20 @@ def stack_backward(engine, st: StackState, d_final_norm, grad16) -> torch.Tensor
         del o_out
 
         # MLP backward: d_act = dh . W_down; SwiGLU backward in place over gu; d_norm2.
-        d_norm2 = torch.empty_like(norm2)
         step = min(engine.max_mlp_tokens, n_tokens)
-        for s in range(0, n_tokens, step):
-            e = min(s + step, n_tokens)
-            gu = F.linear(norm2[s:e], w_gu)
-            K.mlp_glu_bwd(torch.mm(dh[s:e], w_down), gu)
-            torch.mm(gu, w_gu, out=d_norm2[s:e])
+        if step >= n_tokens:
+            gu = F.linear(norm2, w_gu)
+            K.mlp_glu_bwd(torch.mm(dh, w_down), gu)
+            d_norm2 = _mm_split_k(gu, w_gu)
             del gu
+        else:
+            d_norm2 = torch.empty_like(norm2)
+            for s in range(0, n_tokens, step):
+                e = min(s + step, n_tokens)
+                gu = F.linear(norm2[s:e], w_gu)
+                K.mlp_glu_bwd(torch.mm(dh[s:e], w_down), gu)
+                d_norm2[s:e] = _mm_split_k(gu, w_gu)
+                del gu
         del norm2
         dh_mid = K.rms_norm_bwd(d_norm2, h_mid, engine.ln2_weights[l], rstd2, dresidual=dh)
         del d_norm2, h_mid, rstd2, dh
