@@ -296,6 +296,49 @@ def lora_dropout_bwd_add(acc: torch.Tensor, ga: torch.Tensor, gb: torch.Tensor, 
 
 
 # ---------------------------------------------------------------------------------------------
+# Rank-r LoRA branches — solution/ops.py:775-778 (forward), 975-992 (backward). Each product is
+# an fp16 tensor computed with fp32 accumulation, as torch's fp16 F.linear / torch.mm.
+# ---------------------------------------------------------------------------------------------
+
+
+def _mm16(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    return (a.float() @ b.float()).half()
+
+
+def lora_down_fwd(x, a_q, a_v, seed=None, stream_q=0, stream_v=1, p_q=0.0, p_v=0.0):
+    """(mid_q, mid_v, x_q, x_v): x_q = drop_q(x), mid_q = fp16(x_q A_q^T) (ops.py:775-778)."""
+    if seed is None:
+        x_q = x_v = x
+    else:
+        x_q, x_v = lora_dropout_fwd(x, seed, stream_q, stream_v, p_q, p_v)
+    return _mm16(x_q, a_q.t()), _mm16(x_v, a_v.t()), x_q, x_v
+
+
+def lora_up(mid, b):
+    """fp16(mid B^T): the LoRA delta the RoPE kernel adds (ops.py:776, 778)."""
+    return _mm16(mid, b.t())
+
+
+def lora_bwd_x(dq, dv, a_q, a_v, b_q, b_v, dx, seed=None, stream_q=0, stream_v=1, p_q=0.0,
+               p_v=0.0):
+    """(d_mid_q, d_mid_v, dx_new): d_mid = fp16(dq B), dx_branch = fp16(d_mid A), then the masked
+    adds of ops.py:986-992."""
+    dmq, dmv = _mm16(dq, b_q), _mm16(dv, b_v)
+    dxq, dxv = _mm16(dmq, a_q), _mm16(dmv, a_v)
+    if seed is None:
+        out = (dx.float() + dxq.float()).half().float().add(dxv.float()).half()
+    else:
+        out = lora_dropout_bwd_add(dx, dxq, dxv, seed, stream_q, stream_v, p_q, p_v)
+    return dmq, dmv, out
+
+
+def lora_bwd_w(x_q, x_v, dq, dv, mid_q, mid_v, d_mid_q, d_mid_v):
+    """(g_a_q, g_b_q, g_a_v, g_b_v) = (d_mid_q^T x_q, dq^T mid_q, ...) in fp16 (ops.py:975-981)."""
+    return (_mm16(d_mid_q.t(), x_q), _mm16(dq.t(), mid_q), _mm16(d_mid_v.t(), x_v),
+            _mm16(dv.t(), mid_v))
+
+
+# ---------------------------------------------------------------------------------------------
 # Chunked lm_head cross-entropy — solution/kernels.py:453-565, ops.py:174-349
 # ---------------------------------------------------------------------------------------------
 

@@ -43,6 +43,14 @@ SIGNATURES: dict[str, list] = {
     "rus_lora_dropout_fwd": [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _vp, _u64, _u64, _f32, _f32, _i32, _vp],
     "rus_lora_dropout_bwd_add": [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _vp, _u64, _u64, _f32, _f32, _i32, _vp],
     "rus_graph_node_counts": [_vp, _vp, _i32],
+    "rus_lora_down_fwd": [_vp, _i64, _i64, _i64, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _u64,
+                          _u64, _f32, _f32, _vp],
+    "rus_qkv_lora_rope_fwd_mid": [_vp, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp,
+                                  _i64, _i64, _i64, _i64, _f32, _f32, _i32, _i32, _i32, _vp, _vp],
+    "rus_lora_bwd_x": [_vp, _vp, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _i32, _i64, _vp, _vp, _vp,
+                       _i64, _vp, _u64, _u64, _f32, _f32, _vp],
+    "rus_lora_bwd_w": [_vp, _vp, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i32,
+                       _vp, _vp, _vp, _vp, _vp],
     "rus_lmhead_ce_loss": [_vp, _vp, _i64, _vp, _vp, _vp, _vp],
     "rus_rmsnorm_fwd": [_vp, _vp, _vp, _i32, _vp, _vp, _vp, _i64, _i64, _i64, _f32, _i32, _vp],
     "rus_rmsnorm_bwd": [_vp, _vp, _vp, _i32, _vp, _vp, _vp, _i64, _i64, _i64, _i32, _vp],

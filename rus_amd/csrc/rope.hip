@@ -47,10 +47,39 @@ struct RopeFwdArgs {
   float scale_q, scale_v;
   int h_q, h_kv, head_dim;
   int32_t* err_flag;
+  // LoRA from the rank-r factors instead (fp16 only): delta = fp16(mid[t] . B[col]), mid [N, r],
+  // B [cols, r] row-major.
+  const T* mid_q;
+  const T* mid_v;
+  const T* b_q;
+  const T* b_v;
 };
 
-template <typename T, bool HAS_LORA>
+// The LoRA delta of columns col0 .. col0+7 and col0+half .. +7 from mid row m and B [cols, R]:
+// fp16(sum_k m[k] * B[col, k]), the reference's fp16 mid B^T product (ops.py:776-778).
+template <typename T, int R>
+__device__ __forceinline__ void lora_up(const float (&m)[R], const T* __restrict__ b, int64_t col0,
+                                        int half, float (&dl)[kSpan], float (&dh)[kSpan]) {
+#pragma unroll
+  for (int i = 0; i < kSpan; ++i) {
+    float bl[R], bh[R];
+    load_f32<T, R>(b + (col0 + i) * R, bl);
+    load_f32<T, R>(b + (col0 + half + i) * R, bh);
+    float sl = 0.0f, sh = 0.0f;
+#pragma unroll
+    for (int k = 0; k < R; ++k) {
+      sl = __builtin_fmaf(m[k], bl[k], sl);
+      sh = __builtin_fmaf(m[k], bh[k], sh);
+    }
+    dl[i] = round_to<T>(sl);
+    dh[i] = round_to<T>(sh);
+  }
+}
+
+// LORA: 0 none, 1 precomputed q_lora / v_lora rows, 2 rank-R factors (mid, B).
+template <typename T, int LORA, int R>
 __global__ __launch_bounds__(kThreads) void rope_fwd_kernel(RopeFwdArgs<T> a) {
+  constexpr bool HAS_LORA = LORA == 1;
   const int half = a.head_dim / 2;
   const int per_head = half / kSpan;
   const int heads = a.h_q + 2 * a.h_kv;
@@ -69,6 +98,16 @@ __global__ __launch_bounds__(kThreads) void rope_fwd_kernel(RopeFwdArgs<T> a) {
 
   if (hd >= a.h_q + a.h_kv) {  // V head: LoRA delta only
     const int kv = hd - a.h_q - a.h_kv;
+    if constexpr (LORA == 2) {
+      float m[R], dl[kSpan], dh[kSpan];
+      load_f32<T, R>(a.mid_v + t * R, m);
+      lora_up<T, R>(m, a.b_v, static_cast<int64_t>(kv) * a.head_dim + j, half, dl, dh);
+#pragma unroll
+      for (int i = 0; i < kSpan; ++i) {
+        lo[i] = lo[i] + dl[i] * a.scale_v;
+        hi[i] = hi[i] + dh[i] * a.scale_v;
+      }
+    }
     if (HAS_LORA) {
       float dl[kSpan], dh[kSpan];
       const T* vl = a.v_lora + t * a.stride_vl + static_cast<int64_t>(kv) * a.head_dim;
@@ -86,6 +125,18 @@ __global__ __launch_bounds__(kThreads) void rope_fwd_kernel(RopeFwdArgs<T> a) {
     return;
   }
 
+  if constexpr (LORA == 2) {
+    if (hd < a.h_q) {
+      float m[R], dl[kSpan], dh[kSpan];
+      load_f32<T, R>(a.mid_q + t * R, m);
+      lora_up<T, R>(m, a.b_q, static_cast<int64_t>(hd) * a.head_dim + j, half, dl, dh);
+#pragma unroll
+      for (int i = 0; i < kSpan; ++i) {
+        lo[i] = lo[i] + dl[i] * a.scale_q;
+        hi[i] = hi[i] + dh[i] * a.scale_q;
+      }
+    }
+  }
   if (HAS_LORA && hd < a.h_q) {
     float dl[kSpan], dh[kSpan];
     const T* ql = a.q_lora + t * a.stride_ql + static_cast<int64_t>(hd) * a.head_dim;
@@ -234,10 +285,31 @@ int fwd_typed(const RopeFwdArgs<T>& a, hipStream_t st) {
   const int64_t threads = a.n_tokens * slots;
   const dim3 grid(static_cast<unsigned>((threads + kThreads - 1) / kThreads));
   if (a.q_lora)
-    hipLaunchKernelGGL((rope_fwd_kernel<T, true>), grid, dim3(kThreads), 0, st, a);
+    hipLaunchKernelGGL((rope_fwd_kernel<T, 1, 0>), grid, dim3(kThreads), 0, st, a);
   else
-    hipLaunchKernelGGL((rope_fwd_kernel<T, false>), grid, dim3(kThreads), 0, st, a);
+    hipLaunchKernelGGL((rope_fwd_kernel<T, 0, 0>), grid, dim3(kThreads), 0, st, a);
   return check_launch("rus_qkv_lora_rope_fwd");
+}
+
+int fwd_mid(const RopeFwdArgs<f16>& a, int r, hipStream_t st) {
+  const char* fn = "rus_qkv_lora_rope_fwd_mid";
+  if (!aligned8<f16>(a.qkv, a.stride_qkv) || !aligned8<f16>(a.cos, a.stride_cos) ||
+      !aligned8<f16>(a.sin, a.stride_cos) || !aligned(a.q_out, 16) || !aligned(a.k_out, 16) ||
+      !aligned(a.v_out, 16) || !aligned(a.mid_q, 8) || !aligned(a.mid_v, 8) ||
+      !aligned(a.b_q, 8) || !aligned(a.b_v, 8))
+    return fail(RUS_ERR_INVALID, "%s: pointers/strides must be aligned (16 B rows, 8 B factors)",
+                fn);
+  const int64_t slots = static_cast<int64_t>(a.h_q + 2 * a.h_kv) * (a.head_dim / 2 / kSpan);
+  const int64_t threads = a.n_tokens * slots;
+  const dim3 grid(static_cast<unsigned>((threads + kThreads - 1) / kThreads));
+  switch (r) {
+    case 4: hipLaunchKernelGGL((rope_fwd_kernel<f16, 2, 4>), grid, dim3(kThreads), 0, st, a); break;
+    case 8: hipLaunchKernelGGL((rope_fwd_kernel<f16, 2, 8>), grid, dim3(kThreads), 0, st, a); break;
+    case 16: hipLaunchKernelGGL((rope_fwd_kernel<f16, 2, 16>), grid, dim3(kThreads), 0, st, a); break;
+    case 32: hipLaunchKernelGGL((rope_fwd_kernel<f16, 2, 32>), grid, dim3(kThreads), 0, st, a); break;
+    default: return fail(RUS_ERR_UNSUPPORTED, "%s: rank %d not in {4,8,16,32}", fn, r);
+  }
+  return check_launch(fn);
 }
 
 template <typename T>
@@ -332,4 +404,47 @@ extern "C" int rus_qkv_rope_bwd(const void* dq_rot, const void* dk_rot, const vo
   if (dtype == RUS_DTYPE_F16) RUS_ROPE_BWD(f16)
   RUS_ROPE_BWD(float)
 #undef RUS_ROPE_BWD
+}
+
+extern "C" int rus_qkv_lora_rope_fwd_mid(const void* qkv, const void* mid_q, const void* mid_v,
+                                         const void* b_q, const void* b_v, int32_t r,
+                                         const void* cos, const void* sin,
+                                         const int64_t* pos_ids, void* q_out, void* k_out,
+                                         void* v_out, int64_t n_tokens, int64_t stride_qkv,
+                                         int64_t stride_cos, int64_t n_pos, float scale_q,
+                                         float scale_v, int32_t h_q, int32_t h_kv,
+                                         int32_t head_dim, int32_t* err_flag, void* stream) {
+  using namespace rus;
+  const char* fn = "rus_qkv_lora_rope_fwd_mid";
+  if (int e = check_heads(fn, n_tokens, h_q, h_kv, head_dim, n_pos, stride_cos, RUS_DTYPE_F16))
+    return e;
+  if (n_tokens == 0) return RUS_OK;
+  if (!qkv || !mid_q || !mid_v || !b_q || !b_v || !cos || !sin || !pos_ids || !q_out || !k_out ||
+      !v_out)
+    return fail(RUS_ERR_INVALID, "%s: null pointer argument", fn);
+  if (stride_qkv < static_cast<int64_t>(h_q + 2 * h_kv) * head_dim)
+    return fail(RUS_ERR_INVALID, "%s: stride_qkv smaller than a row", fn);
+  RopeFwdArgs<f16> a{};
+  a.qkv = static_cast<const f16*>(qkv);
+  a.cos = static_cast<const f16*>(cos);
+  a.sin = static_cast<const f16*>(sin);
+  a.pos = pos_ids;
+  a.q_out = static_cast<f16*>(q_out);
+  a.k_out = static_cast<f16*>(k_out);
+  a.v_out = static_cast<f16*>(v_out);
+  a.n_tokens = n_tokens;
+  a.stride_qkv = stride_qkv;
+  a.stride_cos = stride_cos;
+  a.n_pos = n_pos;
+  a.scale_q = scale_q;
+  a.scale_v = scale_v;
+  a.h_q = h_q;
+  a.h_kv = h_kv;
+  a.head_dim = head_dim;
+  a.err_flag = err_flag;
+  a.mid_q = static_cast<const f16*>(mid_q);
+  a.mid_v = static_cast<const f16*>(mid_v);
+  a.b_q = static_cast<const f16*>(b_q);
+  a.b_v = static_cast<const f16*>(b_v);
+  return fwd_mid(a, r, static_cast<hipStream_t>(stream));
 }

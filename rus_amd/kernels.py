@@ -25,6 +25,10 @@ __all__ = [
     "qkv_rope_bwd_lora",
     "lora_dropout_fwd",
     "lora_dropout_bwd_add",
+    "lora_down_fwd",
+    "qkv_rope_fwd_mid",
+    "lora_bwd_x",
+    "lora_bwd_w",
     "mlp_glu_fwd",
     "mlp_glu_bwd",
     "lm_head_ce",
@@ -631,6 +635,158 @@ def lora_dropout_bwd_add(acc: torch.Tensor, grad_a: torch.Tensor, grad_b: torch.
             ga.stride(0), gb.stride(0), seed.data_ptr(), int(stream_a), int(stream_b), float(p_a),
             float(p_b), dt, _stream(a2))
     return acc
+
+
+# ---------------------------------------------------------------------------------------------
+# Fused rank-r LoRA branches (reference: ops.py:775-778, 882-888, 975-992)
+# ---------------------------------------------------------------------------------------------
+
+LORA_RANKS = (4, 8, 16, 32)
+
+
+def _lora_operand(fn, t, shape, name):
+    if t.dtype != torch.float16 or not t.is_contiguous() or tuple(t.shape) != tuple(shape):
+        raise ValueError(f"{fn}: {name} must be contiguous fp16 {tuple(shape)}, got "
+                         f"{t.dtype} {tuple(t.shape)}")
+    return t
+
+
+def _drop_args(seed, stream_q, stream_v, p_q, p_v):
+    if seed is not None and (seed.dtype != torch.int64 or seed.numel() != 1):
+        raise ValueError("lora: seed must be one int64 element")
+    return _ptr(seed), int(stream_q), int(stream_v), float(p_q), float(p_v)
+
+
+def lora_down_fwd(x: torch.Tensor, a_q: torch.Tensor, a_v: torch.Tensor,
+                  seed: torch.Tensor | None = None, stream_q: int = 0, stream_v: int = 1,
+                  p_q: float = 0.0, p_v: float = 0.0, want_x: bool = False):
+    """(mid_q, mid_v) = (drop_q(x) A_q^T, drop_v(x) A_v^T) in fp16, one launch; with ``want_x``
+    also the dropped inputs (x_q, x_v) (a seed is then required). Without a seed no dropout."""
+    fn = "lora_down_fwd"
+    _require_device(fn, x, a_q, a_v, seed)
+    r, d = a_q.shape
+    if r not in LORA_RANKS:
+        raise ValueError(f"{fn}: rank {r} not in {LORA_RANKS}")
+    x2 = _rows(fn, x, d, "x")
+    if x2.dtype != torch.float16:
+        raise ValueError(f"{fn}: fp16 activations only")
+    _lora_operand(fn, a_q, (r, d), "a_q")
+    _lora_operand(fn, a_v, (r, d), "a_v")
+    n = x2.shape[0]
+    dev = x.device
+    mid_q = torch.empty((n, r), dtype=torch.float16, device=dev)
+    mid_v = torch.empty((n, r), dtype=torch.float16, device=dev)
+    xq = xv = None
+    if want_x:
+        if seed is None:
+            raise ValueError(f"{fn}: want_x needs a seed (without dropout the inputs are x)")
+        xq = torch.empty((n, d), dtype=torch.float16, device=dev)
+        xv = torch.empty((n, d), dtype=torch.float16, device=dev)
+    _launch("lora_down", n * d * 2 * (1 + (2 if want_x else 0)) + 4 * r * d + 4 * n * r,
+            4 * n * d * r, "rus_lora_down_fwd", x2.data_ptr(), n, d, x2.stride(0),
+            a_q.data_ptr(), a_v.data_ptr(), r, mid_q.data_ptr(), mid_v.data_ptr(), _ptr(xq),
+            _ptr(xv), *_drop_args(seed, stream_q, stream_v, p_q, p_v), _stream(x2))
+    if want_x:
+        return mid_q, mid_v, xq, xv
+    return mid_q, mid_v
+
+
+def qkv_rope_fwd_mid(qkv: torch.Tensor, mid_q: torch.Tensor, mid_v: torch.Tensor,
+                     b_q: torch.Tensor, b_v: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
+                     pos_ids: torch.Tensor, scale_q: float = 2.0, scale_v: float = 2.0,
+                     h_q: int = 12, h_kv: int = 2, head_dim: int = 128):
+    """qkv_rope_fwd with q_lora = mid_q B_q^T and v_lora = mid_v B_v^T formed in the kernel."""
+    fn = "qkv_rope_fwd_mid"
+    _require_device(fn, qkv, mid_q, mid_v, b_q, b_v, cos, sin, pos_ids)
+    n_tokens = qkv.shape[0]
+    q_dim, kv_dim = h_q * head_dim, h_kv * head_dim
+    r = mid_q.shape[1]
+    if qkv.dtype != torch.float16 or r not in LORA_RANKS:
+        raise ValueError(f"{fn}: fp16 and rank in {LORA_RANKS} only")
+    qkv = _rows(fn, qkv, q_dim + 2 * kv_dim, "qkv")
+    cos = _rows(fn, cos, head_dim, "cos")
+    sin = _rows(fn, sin, head_dim, "sin")
+    if cos.dtype != qkv.dtype or sin.dtype != qkv.dtype or sin.stride(0) != cos.stride(0):
+        raise ValueError(f"{fn}: cos/sin must share qkv's dtype and a row stride")
+    for t, shp, nm in ((mid_q, (n_tokens, r), "mid_q"), (mid_v, (n_tokens, r), "mid_v"),
+                       (b_q, (q_dim, r), "b_q"), (b_v, (kv_dim, r), "b_v")):
+        _lora_operand(fn, t, shp, nm)
+    pos = pos_ids.reshape(-1)
+    if pos.dtype != torch.int64 or pos.numel() != n_tokens:
+        raise ValueError(f"{fn}: pos_ids must be int64 with {n_tokens} entries")
+    pos = pos.contiguous()
+    q_out = torch.empty((n_tokens, h_q, head_dim), dtype=qkv.dtype, device=qkv.device)
+    k_out = torch.empty((n_tokens, h_kv, head_dim), dtype=qkv.dtype, device=qkv.device)
+    v_out = torch.empty((n_tokens, h_kv, head_dim), dtype=qkv.dtype, device=qkv.device)
+    width = q_dim + 2 * kv_dim
+    _launch("rope_fwd", n_tokens * (2 * (2 * width + 2 * head_dim + 2 * r) + 8), 0,
+            "rus_qkv_lora_rope_fwd_mid", qkv.data_ptr(), mid_q.data_ptr(), mid_v.data_ptr(),
+            b_q.data_ptr(), b_v.data_ptr(), r, cos.data_ptr(), sin.data_ptr(), pos.data_ptr(),
+            q_out.data_ptr(), k_out.data_ptr(), v_out.data_ptr(), n_tokens, qkv.stride(0),
+            cos.stride(0), cos.shape[0], float(scale_q), float(scale_v), h_q, h_kv, head_dim,
+            None, _stream(qkv))
+    return q_out, k_out, v_out
+
+
+def lora_bwd_x(dq_lora: torch.Tensor, dv_lora: torch.Tensor, a_q: torch.Tensor,
+               a_v: torch.Tensor, b_q: torch.Tensor, b_v: torch.Tensor, dx: torch.Tensor,
+               seed: torch.Tensor | None = None, stream_q: int = 0, stream_v: int = 1,
+               p_q: float = 0.0, p_v: float = 0.0):
+    """d_mid = dq B per branch; dx += drop_q(d_mid_q A_q), then += drop_v(d_mid_v A_v), in
+    place. Returns (d_mid_q, d_mid_v)."""
+    fn = "lora_bwd_x"
+    _require_device(fn, dq_lora, dv_lora, a_q, a_v, b_q, b_v, dx, seed)
+    r, d = a_q.shape
+    if r not in LORA_RANKS:
+        raise ValueError(f"{fn}: rank {r} not in {LORA_RANKS}")
+    n = dq_lora.shape[0]
+    d_q, d_v = dq_lora.shape[1], dv_lora.shape[1]
+    for t, shp, nm in ((dq_lora, (n, d_q), "dq_lora"), (dv_lora, (n, d_v), "dv_lora"),
+                       (a_q, (r, d), "a_q"), (a_v, (r, d), "a_v"), (b_q, (d_q, r), "b_q"),
+                       (b_v, (d_v, r), "b_v")):
+        _lora_operand(fn, t, shp, nm)
+    dx2 = _rows(fn, dx, d, "dx")
+    if dx2.dtype != torch.float16 or dx2.shape[0] != n:
+        raise ValueError(f"{fn}: dx must be fp16 [{n}, {d}]")
+    dmq = torch.empty((n, r), dtype=torch.float16, device=dx.device)
+    dmv = torch.empty((n, r), dtype=torch.float16, device=dx.device)
+    _launch("lora_bwd_x", 2 * n * (d_q + d_v + 2 * d + 2 * r) + 4 * r * (d + d_q),
+            2 * n * r * (d_q + d_v + 2 * d), "rus_lora_bwd_x", dq_lora.data_ptr(),
+            dv_lora.data_ptr(), n, d_q, d_v, a_q.data_ptr(), a_v.data_ptr(), b_q.data_ptr(),
+            b_v.data_ptr(), r, d, dmq.data_ptr(), dmv.data_ptr(), dx2.data_ptr(), dx2.stride(0),
+            *_drop_args(seed, stream_q, stream_v, p_q, p_v), _stream(dx2))
+    return dmq, dmv
+
+
+def lora_bwd_w(x_q: torch.Tensor, x_v: torch.Tensor, dq_lora: torch.Tensor,
+               dv_lora: torch.Tensor, mid_q: torch.Tensor, mid_v: torch.Tensor,
+               d_mid_q: torch.Tensor, d_mid_v: torch.Tensor, g_a_q: torch.Tensor,
+               g_b_q: torch.Tensor, g_a_v: torch.Tensor, g_b_v: torch.Tensor) -> None:
+    """g_a = d_mid^T x_drop [r, d], g_b = dq^T mid [d_q, r] for both branches, fp16 outputs
+    written in place (e.g. views of a flat gradient buffer)."""
+    fn = "lora_bwd_w"
+    _require_device(fn, x_q, x_v, dq_lora, dv_lora, mid_q, mid_v, d_mid_q, d_mid_v, g_a_q, g_b_q,
+                    g_a_v, g_b_v)
+    n, r = mid_q.shape
+    d = x_q.shape[1]
+    d_q, d_v = dq_lora.shape[1], dv_lora.shape[1]
+    if r not in LORA_RANKS:
+        raise ValueError(f"{fn}: rank {r} not in {LORA_RANKS}")
+    xq2 = _rows(fn, x_q, d, "x_q")
+    xv2 = _rows(fn, x_v, d, "x_v")
+    if xq2.stride(0) != xv2.stride(0) or xq2.dtype != torch.float16 or xv2.dtype != torch.float16:
+        raise ValueError(f"{fn}: x_q and x_v must be fp16 with one row stride")
+    for t, shp, nm in ((dq_lora, (n, d_q), "dq_lora"), (dv_lora, (n, d_v), "dv_lora"),
+                       (mid_q, (n, r), "mid_q"), (mid_v, (n, r), "mid_v"),
+                       (d_mid_q, (n, r), "d_mid_q"), (d_mid_v, (n, r), "d_mid_v"),
+                       (g_a_q, (r, d), "g_a_q"), (g_b_q, (d_q, r), "g_b_q"),
+                       (g_a_v, (r, d), "g_a_v"), (g_b_v, (d_v, r), "g_b_v")):
+        _lora_operand(fn, t, shp, nm)
+    _launch("lora_bwd_w", 2 * n * (2 * d + d_q + d_v + 4 * r), 2 * n * r * (2 * d + d_q + d_v),
+            "rus_lora_bwd_w", xq2.data_ptr(), xv2.data_ptr(), xq2.stride(0), dq_lora.data_ptr(),
+            dv_lora.data_ptr(), mid_q.data_ptr(), mid_v.data_ptr(), d_mid_q.data_ptr(),
+            d_mid_v.data_ptr(), n, d, d_q, d_v, r, g_a_q.data_ptr(), g_b_q.data_ptr(),
+            g_a_v.data_ptr(), g_b_v.data_ptr(), _stream(mid_q))
 
 
 # ---------------------------------------------------------------------------------------------

@@ -236,7 +236,7 @@ class Qwen2FusedEngine:
                  offload_inputs: bool = False, max_pos: int = 2048,
                  max_mlp_tokens: int = MAX_MLP_TOKENS, v_chunk: int = V_CHUNK_DEFAULT,
                  attention: str = "varlen", dropout_seed: int | None = None,
-                 stream_unit: str = "layer"):
+                 stream_unit: str = "layer", lora_kernels: bool = True):
         from .model import QLoRAQwen2
 
         if not isinstance(model, QLoRAQwen2):
@@ -274,6 +274,10 @@ class Qwen2FusedEngine:
                              "or 'sdpa_rows' (torch SDPA per row, as the reference)")
         self.attention = attention
         self._flatten_lora()
+        # The fused LoRA kernels (one launch for dropout + both A products, the B products inside
+        # RoPE, two backward launches) cover ranks 4/8/16/32; other ranks use library GEMMs.
+        ranks = {int(p.shape[0]) for p in self.lora_params[0::2]}
+        self.fused_lora = bool(lora_kernels) and len(ranks) == 1 and ranks <= set(K.LORA_RANKS)
         # LoRA dropout: the counter-based masks of step k use seed (base + k), held on the device
         # so that a captured graph advances it by itself. The base comes from torch's CPU
         # generator unless given.
@@ -396,6 +400,13 @@ def _lora_inputs(norm1, layer, meta, training, seed):
     return norm1, norm1
 
 
+def _lora_drop_args(layer, meta, training, seed):
+    """(seed, stream_q, stream_v, p_q, p_v) for the fused LoRA kernels (seed None: no dropout)."""
+    if _dropout_on(meta, training):
+        return seed, 2 * layer, 2 * layer + 1, meta["p_q"], meta["p_v"]
+    return None, 2 * layer, 2 * layer + 1, 0.0, 0.0
+
+
 def _lora_deltas(x_q, x_v, qA, qB, vA, vB):
     """(mid_q, q_lora, mid_v, v_lora) = (x_q A_q^T, mid_q B_q^T, x_v A_v^T, mid_v B_v^T)."""
     mid_q = F.linear(x_q, qA)
@@ -476,14 +487,24 @@ def stack_forward(engine, h_packed, pos_ids, row_lengths, training, lora16, seed
         ws.release_slot(l)
         qkv = F.linear(norm1, W["qkv"], engine.layer_biases[l])
         meta = engine.layer_lora_meta[l]
-        x_q, x_v = _lora_inputs(norm1, l, meta, training, seed)
-        _, q_lora, _, v_lora = _lora_deltas(x_q, x_v, *lora16[4 * l: 4 * l + 4])
-        del x_q, x_v
-        q_rot, k_rot, v_out = K.qkv_rope_fwd(qkv, cos, sin, pos_ids, q_lora=q_lora, v_lora=v_lora,
-                                             scale_q=meta["scale_q"], scale_v=meta["scale_v"],
-                                             h_q=engine.num_heads, h_kv=engine.num_kv_heads,
-                                             head_dim=engine.head_dim)
-        del qkv, q_lora, v_lora, norm1
+        qA, qB, vA, vB = lora16[4 * l: 4 * l + 4]
+        if engine.fused_lora:  # dropout + A products in one launch, B products inside RoPE
+            mid_q, mid_v = K.lora_down_fwd(norm1, qA, vA, *_lora_drop_args(l, meta, training, seed))
+            q_rot, k_rot, v_out = K.qkv_rope_fwd_mid(
+                qkv, mid_q, mid_v, qB, vB, cos, sin, pos_ids, meta["scale_q"], meta["scale_v"],
+                engine.num_heads, engine.num_kv_heads, engine.head_dim)
+            del mid_q, mid_v
+        else:
+            x_q, x_v = _lora_inputs(norm1, l, meta, training, seed)
+            _, q_lora, _, v_lora = _lora_deltas(x_q, x_v, qA, qB, vA, vB)
+            del x_q, x_v
+            q_rot, k_rot, v_out = K.qkv_rope_fwd(qkv, cos, sin, pos_ids, q_lora=q_lora,
+                                                 v_lora=v_lora, scale_q=meta["scale_q"],
+                                                 scale_v=meta["scale_v"], h_q=engine.num_heads,
+                                                 h_kv=engine.num_kv_heads,
+                                                 head_dim=engine.head_dim)
+            del q_lora, v_lora
+        del qkv, norm1
         if vm is not None:
             attn = _varlen_attn_fwd(q_rot, k_rot, v_out, vm)[0].view(n_tok, hq * hd)
         else:
@@ -541,12 +562,26 @@ def stack_backward(engine, st: StackState, d_final_norm, grad16) -> torch.Tensor
         qkv = F.linear(norm1, w_qkv, engine.layer_biases[l])
         meta = engine.layer_lora_meta[l]
         qA, qB, vA, vB = st.lora16[4 * l: 4 * l + 4]
-        x_q, x_v = _lora_inputs(norm1, l, meta, training, seed)
-        mid_q, q_lora, mid_v, v_lora = _lora_deltas(x_q, x_v, qA, qB, vA, vB)
-        q_rot, k_rot, v_out = K.qkv_rope_fwd(qkv, cos, sin, pos_ids, q_lora=q_lora, v_lora=v_lora,
-                                             scale_q=meta["scale_q"], scale_v=meta["scale_v"],
-                                             h_q=hq, h_kv=hkv, head_dim=hd)
-        del qkv, q_lora, v_lora
+        fused = engine.fused_lora
+        if fused:
+            drop = _lora_drop_args(l, meta, training, seed)
+            if drop[0] is not None:
+                mid_q, mid_v, x_q, x_v = K.lora_down_fwd(norm1, qA, vA, *drop, want_x=True)
+            else:
+                mid_q, mid_v = K.lora_down_fwd(norm1, qA, vA)
+                x_q = x_v = norm1
+            q_rot, k_rot, v_out = K.qkv_rope_fwd_mid(
+                qkv, mid_q, mid_v, qB, vB, cos, sin, pos_ids, meta["scale_q"], meta["scale_v"],
+                hq, hkv, hd)
+        else:
+            x_q, x_v = _lora_inputs(norm1, l, meta, training, seed)
+            mid_q, q_lora, mid_v, v_lora = _lora_deltas(x_q, x_v, qA, qB, vA, vB)
+            q_rot, k_rot, v_out = K.qkv_rope_fwd(qkv, cos, sin, pos_ids, q_lora=q_lora,
+                                                 v_lora=v_lora, scale_q=meta["scale_q"],
+                                                 scale_v=meta["scale_v"], h_q=hq, h_kv=hkv,
+                                                 head_dim=hd)
+            del q_lora, v_lora
+        del qkv
         if st.vm is not None:
             attn, lse, rng, unused = _varlen_attn_fwd(q_rot, k_rot, v_out, st.vm)
             attn2d = attn.view(n_tokens, q_dim)
@@ -595,25 +630,31 @@ def stack_backward(engine, st: StackState, d_final_norm, grad16) -> torch.Tensor
                                                          h_q=hq, h_kv=hkv, head_dim=hd)
         del dq, dk, dv
 
-        # LoRA parameter gradients (solution/ops.py:975-983), written into the flat buffer.
+        # LoRA gradients (solution/ops.py:975-992): weight gradients into the flat buffer, input
+        # gradients (through the forward's dropout masks) added into d_norm1.
         g_qA, g_qB, g_vA, g_vB = gviews[4 * l: 4 * l + 4]
-        torch.mm(dq_scaled.t(), mid_q, out=g_qB)
-        d_mid_q = torch.mm(dq_scaled, qB)
-        torch.mm(d_mid_q.t(), x_q, out=g_qA)
-        dx_q = torch.mm(d_mid_q, qA)
-        torch.mm(dv_scaled.t(), mid_v, out=g_vB)
-        d_mid_v = torch.mm(dv_scaled, vB)
-        torch.mm(d_mid_v.t(), x_v, out=g_vA)
-        dx_v = torch.mm(d_mid_v, vA)
-        del mid_q, mid_v, x_q, x_v, d_mid_q, d_mid_v, dq_scaled, dv_scaled
-
         d_norm1 = torch.mm(dqkv, w_qkv)
-        if _dropout_on(meta, training):  # masks of the forward, then the two adds (ops.py:986-992)
-            K.lora_dropout_bwd_add(d_norm1, dx_q, dx_v, seed, 2 * l, 2 * l + 1, meta["p_q"],
-                                   meta["p_v"])
+        del dqkv
+        if fused:  # d_mid, the expansion, masks and both adds; then all four weight gradients
+            d_mid_q, d_mid_v = K.lora_bwd_x(dq_scaled, dv_scaled, qA, vA, qB, vB, d_norm1, *drop)
+            K.lora_bwd_w(x_q, x_v, dq_scaled, dv_scaled, mid_q, mid_v, d_mid_q, d_mid_v, g_qA,
+                         g_qB, g_vA, g_vB)
         else:
-            d_norm1.add_(dx_q).add_(dx_v)
-        del dqkv, dx_q, dx_v, norm1
+            torch.mm(dq_scaled.t(), mid_q, out=g_qB)
+            d_mid_q = torch.mm(dq_scaled, qB)
+            torch.mm(d_mid_q.t(), x_q, out=g_qA)
+            dx_q = torch.mm(d_mid_q, qA)
+            torch.mm(dv_scaled.t(), mid_v, out=g_vB)
+            d_mid_v = torch.mm(dv_scaled, vB)
+            torch.mm(d_mid_v.t(), x_v, out=g_vA)
+            dx_v = torch.mm(d_mid_v, vA)
+            if _dropout_on(meta, training):  # the forward's masks, then the two adds
+                K.lora_dropout_bwd_add(d_norm1, dx_q, dx_v, seed, 2 * l, 2 * l + 1, meta["p_q"],
+                                       meta["p_v"])
+            else:
+                d_norm1.add_(dx_q).add_(dx_v)
+            del dx_q, dx_v
+        del mid_q, mid_v, x_q, x_v, d_mid_q, d_mid_v, dq_scaled, dv_scaled, norm1
         dh = K.rms_norm_bwd(d_norm1, h_in, engine.ln1_weights[l], rstd1, dresidual=dh_mid)
         ins.release(l)
         del d_norm1, h_in, rstd1, dh_mid

@@ -1,0 +1,150 @@
+"""GPU tests of the fused rank-r LoRA kernels against the CPU oracle (oracle.ops.lora_*).
+
+Every output is an fp16 value that the reference rounds once from an fp32 sum; the kernels sum
+in a different order, so each element may differ by one fp16 ulp (at the larger of the two
+magnitudes; plus 1e-6 for sums that cancel to near zero). Dropout masks, copies of dropped rows and the untouched elements are
+bit-exact.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from oracle import ops as ref
+from rus_amd import kernels as K
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _close(got, want, ulps=1.0, a=None, b=None):
+    """One fp16 ulp at the larger of the two magnitudes (a sum landing on a power of two rounds
+    into the wider binade), plus, for a product a @ b, the fp32 accumulation error of either
+    summation order: 2 sqrt(K) 2^-24 (|a| @ |b|), which matters only where the sum cancels."""
+    g, w = got.float().cpu(), want.float()
+    tol = ulps * ref.fp16_ulp(torch.maximum(g.abs(), w.abs())) + 1e-6
+    if a is not None:
+        k = a.shape[1]
+        tol = tol + 2.0 * k ** 0.5 * 2.0**-24 * (a.float().abs() @ b.float().abs())
+    ok = (g - w).abs() <= tol
+    return bool(ok.all()), float(((g - w).abs() - tol).max())
+
+
+def _inputs(n, d, dq_dim, dv_dim, r, seed):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(n, d, generator=g).half()
+    aq, av = ((torch.randn(r, d, generator=g) * 0.05).half() for _ in range(2))
+    bq = (torch.randn(dq_dim, r, generator=g) * 0.05).half()
+    bv = (torch.randn(dv_dim, r, generator=g) * 0.05).half()
+    return g, x, aq, av, bq, bv
+
+
+@pytest.mark.parametrize("r", [4, 8, 16, 32])
+@pytest.mark.parametrize("drop", [False, True])
+@pytest.mark.parametrize("n", [1, 37, 300])
+def test_lora_down_and_rope_mid(r, drop, n):
+    h_q, h_kv, hd = 12, 2, 128
+    d = 1536
+    g, x, aq, av, bq, bv = _inputs(n, d, h_q * hd, h_kv * hd, r, seed=r * 100 + n)
+    seed_v = 4242
+    seed = torch.tensor([seed_v], dtype=torch.int64, device=DEV) if drop else None
+    args = (seed_v, 6, 7, 0.05, 0.1) if drop else (None,)
+    mq, mv, xq, xv = ref.lora_down_fwd(x, aq, av, *args)
+    out = K.lora_down_fwd(x.to(DEV), aq.to(DEV), av.to(DEV), seed, 6, 7, 0.05, 0.1, want_x=drop)
+    torch.cuda.synchronize()
+    for got, want, xx, aa in zip(out[:2], (mq, mv), (xq, xv), (aq, av)):
+        ok, err = _close(got, want, a=xx, b=aa.t())
+        assert ok, err
+    if drop:
+        assert torch.equal(out[2].cpu(), xq) and torch.equal(out[3].cpu(), xv)
+    # RoPE with the deltas formed from (mid, B), against the oracle given the same mid values
+    qkv = torch.randn(n, (h_q + 2 * h_kv) * hd, generator=g).half()
+    cos, sin = ref.rope_tables(512, hd, 1e6)
+    pos = torch.randint(0, 512, (n,), generator=g)
+    mid_q, mid_v = out[0].cpu(), out[1].cpu()
+    want = ref.qkv_rope_fwd(qkv, cos, sin, pos, ref.lora_up(mid_q, bq), ref.lora_up(mid_v, bv),
+                            2.0, 2.0, h_q, h_kv, hd)
+    got = K.qkv_rope_fwd_mid(qkv.to(DEV), out[0], out[1], bq.to(DEV), bv.to(DEV), cos.to(DEV),
+                             sin.to(DEV), pos.to(DEV), 2.0, 2.0, h_q, h_kv, hd)
+    torch.cuda.synchronize()
+    # Each delta element may differ by one fp16 ulp of its value (fp32 sums in another order);
+    # the output then moves by at most scale * (ulp(d_lo) |cos| + ulp(d_hi) |sin|) before its own
+    # rounding (one output ulp). K has no delta: one ulp.
+    half = hd // 2
+    c, sn = cos[pos].float().unsqueeze(1), sin[pos].float().unsqueeze(1)
+    for gt, wt, delta, heads, rot in ((got[0], want[0], ref.lora_up(mid_q, bq), h_q, True),
+                                      (got[1], want[1], None, h_kv, True),
+                                      (got[2], want[2], ref.lora_up(mid_v, bv), h_kv, False)):
+        wt = wt.reshape(gt.shape).float()
+        tol = ref.fp16_ulp(wt)
+        if delta is not None:
+            u = ref.fp16_ulp(delta.float()).view(n, heads, hd)
+            if rot:
+                u_sw = torch.cat([u[..., half:], u[..., :half]], dim=-1)
+                tol = tol + 2.0 * (u * c.abs() + u_sw * sn.abs())
+            else:
+                tol = tol + 2.0 * u
+        err = (gt.float().cpu() - wt).abs()
+        assert bool((err <= tol + 1e-6).all()), float((err - tol).max())
+
+
+@pytest.mark.parametrize("r", [4, 16, 32])
+@pytest.mark.parametrize("drop", [False, True])
+@pytest.mark.parametrize("n", [5, 300])
+def test_lora_bwd_x_and_w(r, drop, n):
+    d, dq_dim, dv_dim = 1536, 1536, 256
+    g, x, aq, av, bq, bv = _inputs(n, d, dq_dim, dv_dim, r, seed=7 + r + n)
+    dq = torch.randn(n, dq_dim, generator=g).half()
+    dv = torch.randn(n, dv_dim, generator=g).half()
+    dx = torch.randn(n, d, generator=g).half()
+    seed_v = 99
+    seed = torch.tensor([seed_v], dtype=torch.int64, device=DEV) if drop else None
+    dargs = (seed_v, 2, 3, 0.05, 0.05) if drop else (None,)
+    dmq, dmv, dx_want = ref.lora_bwd_x(dq, dv, aq, av, bq, bv, dx, *dargs)
+    dxd = dx.to(DEV)
+    got_mq, got_mv = K.lora_bwd_x(dq.to(DEV), dv.to(DEV), aq.to(DEV), av.to(DEV), bq.to(DEV),
+                                  bv.to(DEV), dxd, seed, 2, 3, 0.05, 0.05)
+    torch.cuda.synchronize()
+    for got, want, dd, bb in ((got_mq, dmq, dq, bq), (got_mv, dmv, dv, bv)):
+        ok, err = _close(got, want, a=dd, b=bb)
+        assert ok, err
+    # dx: with the kernel's own d_mid (the oracle fed the same values), two chained roundings
+    dxq = ref._mm16(got_mq.cpu(), aq)
+    dxv = ref._mm16(got_mv.cpu(), av)
+    if drop:
+        dx_ref = ref.lora_dropout_bwd_add(dx, dxq, dxv, seed_v, 2, 3, 0.05, 0.05)
+    else:
+        dx_ref = (dx.float() + dxq.float()).half().float().add(dxv.float()).half()
+    # each branch product may differ by one ulp of itself; scaled by the dropout factor and
+    # rounded again (one ulp of the scaled term), then each of the two chained roundings (the
+    # intermediate dx + term_q, then the result) adds one ulp of its value
+    sc = 1.0 / 0.95 if drop else 1.0
+    inter = (dx.float() + dxq.float() * sc).half().float()
+    tol = (ref.fp16_ulp(dx_ref.float()) + ref.fp16_ulp(inter) +
+           sc * (ref.fp16_ulp(dxq.float()) + ref.fp16_ulp(dxv.float())) +
+           ref.fp16_ulp(sc * dxq.float()) + ref.fp16_ulp(sc * dxv.float()))
+    err = (dxd.float().cpu() - dx_ref.float()).abs()
+    assert bool((err <= tol + 1e-6).all()), float((err - tol).max())
+
+    # weight gradients from the kernel's d_mid and a forward's mid / dropped rows
+    mq, mv, xq, xv = ref.lora_down_fwd(x, aq, av, *((seed_v, 2, 3, 0.05, 0.05) if drop else (None,)))
+    want = ref.lora_bwd_w(xq, xv, dq, dv, mq, mv, got_mq.cpu(), got_mv.cpu())
+    outs = [torch.full(w.shape, 7.0, dtype=torch.float16, device=DEV) for w in want]
+    K.lora_bwd_w(xq.to(DEV), xv.to(DEV), dq.to(DEV), dv.to(DEV), mq.to(DEV), mv.to(DEV), got_mq,
+                 got_mv, *outs)
+    torch.cuda.synchronize()
+    operands = ((got_mq.cpu().t(), xq), (dq.t(), mq), (got_mv.cpu().t(), xv), (dv.t(), mv))
+    for got, w, (aa, bb) in zip(outs, want, operands):
+        ok, err = _close(got, w, a=aa, b=bb)
+        assert ok, err
+
+
+def test_lora_kernels_reject_bad_rank_and_layout():
+    x = torch.randn(8, 64, device=DEV).half()
+    a = torch.randn(6, 64, device=DEV).half()
+    with pytest.raises(ValueError, match="rank"):
+        K.lora_down_fwd(x, a, a)
+    a4 = torch.randn(4, 64, device=DEV).half()
+    with pytest.raises(ValueError, match="seed"):
+        K.lora_down_fwd(x, a4, a4, want_x=True)

@@ -143,3 +143,21 @@ def test_fused_causal_lm_forward_scatter():
     assert nll.shape == ids.shape and ent.shape == ids.shape and amax.shape == ids.shape
     assert torch.all(nll[0, 12:].cpu() == 0)  # padding
     assert all(p.grad is not None for p in engine.lora_params)
+
+
+def test_fused_lora_kernels_match_library_gemm_path():
+    # The fused LoRA kernels against the same stack with torch GEMMs for the rank-r products
+    # (same dropout masks): loss within 1e-3 relative, LoRA gradients within 5e-3.
+    cfg = small_config(dropout=0.05)
+    model = M.build_random_qlora_qwen2(cfg, DEV, seed=6, std=0.05)
+    ids, mask, labels = _batch(cfg, [45, 20, 61], seed=4)
+    pb = ops.pack_varlen(ids, mask, labels)
+    out = []
+    for fused in (True, False):
+        engine = ops.Qwen2FusedEngine(model, DEV, resident_weights=True, lora_kernels=fused,
+                                      dropout_seed=555)
+        assert engine.fused_lora == fused
+        out.append(_fused_step(engine, pb, training=True))
+    assert abs(float(out[0][0]) - float(out[1][0])) <= 1e-3 * abs(float(out[1][0]))
+    for gi, (a, b) in enumerate(zip(out[0][1], out[1][1])):
+        assert _rel(a, b) <= 5e-3, (gi, _rel(a, b))

@@ -351,6 +351,46 @@ def test_dropout_fwd_values_and_bwd_rounding_order():
 
 
 # ---------------------------------------------------------------------------------------------
+# Rank-r LoRA branches
+# ---------------------------------------------------------------------------------------------
+
+
+def test_lora_branch_grads_match_float64_autograd():
+    # q_lora = s * ((drop(x) A^T) B^T): the closed-form d_mid / dx / gA / gB of the oracle against
+    # float64 autograd of the same function (same masks), within the fp16 roundings.
+    g = torch.Generator().manual_seed(12)
+    n, d, dq_dim, dv_dim, r = 37, 64, 48, 16, 8
+    x = torch.randn(n, d, generator=g).half()
+    aq, av = ((torch.randn(r, d, generator=g) * 0.1).half() for _ in range(2))
+    bq = (torch.randn(dq_dim, r, generator=g) * 0.1).half()
+    bv = (torch.randn(dv_dim, r, generator=g) * 0.1).half()
+    dq = torch.randn(n, dq_dim, generator=g).half()
+    dv = torch.randn(n, dv_dim, generator=g).half()
+    dx0 = torch.randn(n, d, generator=g).half()
+    seed, pq, pv = 77, 0.1, 0.2
+    mid_q, mid_v, xq, xv = ref.lora_down_fwd(x, aq, av, seed, 4, 5, pq, pv)
+    dmq, dmv, dx = ref.lora_bwd_x(dq, dv, aq, av, bq, bv, dx0, seed, 4, 5, pq, pv)
+    gaq, gbq, gav, gbv = ref.lora_bwd_w(xq, xv, dq, dv, mid_q, mid_v, dmq, dmv)
+
+    kq = torch.from_numpy(ref.dropout_keep_mask(seed, 4, n, d, pq)).double() / (1 - pq)
+    kv = torch.from_numpy(ref.dropout_keep_mask(seed, 5, n, d, pv)).double() / (1 - pv)
+    X = x.double().requires_grad_(True)
+    A_q, A_v, B_q, B_v = (t.double().requires_grad_(True) for t in (aq, av, bq, bv))
+    ql = ((X * kq) @ A_q.t()) @ B_q.t()
+    vl = ((X * kv) @ A_v.t()) @ B_v.t()
+    ((ql * dq.double()).sum() + (vl * dv.double()).sum()).backward()
+
+    def close(a, b, tol):
+        return float((a.double() - b).abs().max()) <= tol * float(b.abs().max())
+
+    assert close(mid_q, (X * kq).detach() @ A_q.detach().t(), 2e-3)
+    assert close(dx.double() - dx0.double(), X.grad, 5e-3)
+    assert close(gaq, A_q.grad, 5e-3) and close(gav, A_v.grad, 5e-3)
+    assert close(gbq, B_q.grad, 5e-3) and close(gbv, B_v.grad, 5e-3)
+    assert close(dmq, dq.double() @ B_q.detach(), 2e-3)
+
+
+# ---------------------------------------------------------------------------------------------
 # Chunked lm_head cross-entropy
 # ---------------------------------------------------------------------------------------------
 
