@@ -162,10 +162,12 @@ __device__ __forceinline__ void load_row(const f16* __restrict__ p, float (&o)[R
   }
 }
 
-// Accumulates, for Tile<R>::TT tokens starting at t0, the 2R reductions of branch q (input xq,
-// length dq, weights wq) and branch v into acc[(tt * 2 + br) * R + j]. WT: weights stored
-// [len, R] (B) instead of [R, len] (A). With a Drop seed, inputs are dropped (and the dropped
-// fp16 rows written to xq_out / xv_out when given).
+// Accumulates, for the Tile<R>::TT tokens t0 .. t0+TT-1, this wave's share of the 2R reductions
+// of branch q (input xq, length dq, weights wq) and branch v into acc[(tt * 2 + br) * R + j]:
+// the four waves of the block take consecutive quarters of each branch's 8-element chunks, the
+// lanes of a wave consecutive chunks of its quarter. WT: weights stored [len, R] (B) instead of
+// [R, len] (A). With a Drop seed the inputs are dropped (and the dropped fp16 rows written to
+// xq_out / xv_out when given).
 template <int R, bool WT>
 __device__ __forceinline__ void reduce_rows(float (&acc)[Tile<R>::V], int64_t t0, int64_t n_tok,
                                             const f16* __restrict__ xq, int64_t sxq, int64_t dq,
@@ -174,7 +176,7 @@ __device__ __forceinline__ void reduce_rows(float (&acc)[Tile<R>::V], int64_t t0
                                             const Drop& dr, f16* __restrict__ xq_out,
                                             f16* __restrict__ xv_out) {
   constexpr int TT = Tile<R>::TT;
-  const int lane = threadIdx.x & 63;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x / 64;
   const uint64_t seed = dr.seed ? *dr.seed : 0ull;
 #pragma unroll
   for (int br = 0; br < 2; ++br) {
@@ -187,51 +189,85 @@ __device__ __forceinline__ void reduce_rows(float (&acc)[Tile<R>::V], int64_t t0
     const uint32_t thresh = br ? dr.thresh_v : dr.thresh_q;
     const float scale = br ? dr.scale_v : dr.scale_q;
     const int64_t chunks = len / 8;
-    for (int64_t c = lane; c < chunks; c += 64) {
-      // weights of this chunk: wc[j] = 8 consecutive reduction entries of output j
-      u32x4 wc[R];
-      if (WT) {
-        // [len, R]: rows c*8 .. c*8+7, each R contiguous; gather column j across the 8 rows
-        const f16* base = w + c * 8 * R;
-#pragma unroll
-        for (int j = 0; j < R; ++j) {
-          f16x8 col;
-#pragma unroll
-          for (int i = 0; i < 8; ++i) col[i] = base[i * R + j];
-          wc[j] = __builtin_bit_cast(u32x4, col);
-        }
-      } else {
-#pragma unroll
-        for (int j = 0; j < R; ++j) wc[j] = load16(w + j * len + c * 8);
-      }
+    const int64_t per_wave = (chunks + 3) / 4;
+    const int64_t c_end = min(chunks, (wave + 1) * per_wave);
+    for (int64_t c = wave * per_wave + lane; c < c_end; c += 64) {
+      u32x4 xr[TT];
 #pragma unroll
       for (int tt = 0; tt < TT; ++tt) {
         const int64_t t = t0 + tt;
+        xr[tt] = u32x4{0u, 0u, 0u, 0u};
         if (t >= n_tok) continue;
-        u32x4 xr = load16(x + t * sx + c * 8);
+        xr[tt] = load16(x + t * sx + c * 8);
         if (dr.seed) {
-          const uint32_t bits = philox_keep_bits(seed, stream, static_cast<uint64_t>(t * chunks + c),
-                                                 thresh);
+          const uint32_t bits =
+              philox_keep_bits(seed, stream, static_cast<uint64_t>(t * chunks + c), thresh);
           float xf[8];
-          unpack8(xr, xf);
+          unpack8(xr[tt], xf);
 #pragma unroll
           for (int i = 0; i < 8; ++i) xf[i] = (bits >> i) & 1u ? xf[i] * scale : 0.0f;
-          xr = pack8(xf);  // the reference's fp16 dropout output
-          if (xo) *reinterpret_cast<u32x4*>(xo + t * len + c * 8) = xr;
+          xr[tt] = pack8(xf);  // the reference's fp16 dropout output
+          if (xo) *reinterpret_cast<u32x4*>(xo + t * len + c * 8) = xr[tt];
         }
+      }
+      if (WT) {
+        // [len, R]: row i of the chunk holds the i-th reduction entry of all R outputs
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          float b[R];
+          load_row<R>(w + (c * 8 + i) * R, b);
+#pragma unroll
+          for (int tt = 0; tt < TT; ++tt) {
+            const f16x8 xh = __builtin_bit_cast(f16x8, xr[tt]);
+            const float xi = static_cast<float>(xh[i]);
+#pragma unroll
+            for (int j = 0; j < R; ++j)
+              acc[(tt * 2 + br) * R + j] = __builtin_fmaf(xi, b[j], acc[(tt * 2 + br) * R + j]);
+          }
+        }
+      } else {
+        // [R, len]: wc = 8 consecutive reduction entries of output j
 #pragma unroll
         for (int j = 0; j < R; ++j) {
-          float s = acc[(tt * 2 + br) * R + j];
+          const u32x4 wc = load16(w + j * len + c * 8);
 #pragma unroll
-          for (int i = 0; i < 4; ++i) s = dot2(xr[i], wc[j][i], s);
-          acc[(tt * 2 + br) * R + j] = s;
+          for (int tt = 0; tt < TT; ++tt) {
+            float s = acc[(tt * 2 + br) * R + j];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) s = dot2(xr[tt][i], wc[i], s);
+            acc[(tt * 2 + br) * R + j] = s;
+          }
         }
       }
     }
   }
 }
 
+// Block-wide totals of the V entries: wave butterflies, then a fixed-order sum over the four
+// waves through LDS. Afterwards s_tot[e] holds entry e (rounded to fp16 and back) for every
+// thread of the block.
+template <int R>
+__device__ __forceinline__ void block_totals(float (&acc)[Tile<R>::V], float* s_part,
+                                             float* s_tot) {
+  using TL = Tile<R>;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x / 64;
+  butterfly<TL::V>(acc);
+  if (TL::V >= 64 || (lane & 1) == 0) {
+    const int idx = first_entry<TL::V>(lane);
+#pragma unroll
+    for (int k = 0; k < TL::KEEP; ++k) s_part[wave * TL::V + idx + k] = acc[k];
+  }
+  __syncthreads();
+  if (threadIdx.x < TL::V) {
+    const int e = threadIdx.x;
+    const float t = ((s_part[e] + s_part[TL::V + e]) + s_part[2 * TL::V + e]) + s_part[3 * TL::V + e];
+    s_tot[e] = static_cast<float>(static_cast<f16>(t));
+  }
+  __syncthreads();
+}
+
 // mid_q = fp16(drop_q(x) A_q^T), mid_v = fp16(drop_v(x) A_v^T); optionally the dropped rows.
+// One block of four waves per Tile<R>::TT tokens.
 template <int R>
 __global__ __launch_bounds__(256) void lora_down_kernel(const f16* __restrict__ x, int64_t sx,
                                                         int64_t n_tok, int64_t d,
@@ -242,26 +278,24 @@ __global__ __launch_bounds__(256) void lora_down_kernel(const f16* __restrict__ 
                                                         f16* __restrict__ xq_out,
                                                         f16* __restrict__ xv_out, Drop dr) {
   using TL = Tile<R>;
-  const int64_t wave = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) / 64;
-  const int64_t t0 = wave * TL::TT;
-  if (t0 >= n_tok) return;
+  __shared__ float s_part[4 * TL::V];
+  __shared__ float s_tot[TL::V];
+  const int64_t t0 = static_cast<int64_t>(blockIdx.x) * TL::TT;
   float acc[TL::V];
 #pragma unroll
   for (int i = 0; i < TL::V; ++i) acc[i] = 0.0f;
   reduce_rows<R, false>(acc, t0, n_tok, x, sx, d, x, sx, d, aq, av, dr, xq_out, xv_out);
-  butterfly<TL::V>(acc);
-  const int lane = threadIdx.x & 63;
-  const int idx = first_entry<TL::V>(lane);  // KEEP consecutive entries share (tt, br)
-  const int tt = idx / (2 * R), br = (idx / R) & 1, j = idx % R;
-  const int64_t t = t0 + tt;
-  if (t < n_tok && (TL::V >= 64 || (lane & 1) == 0)) {
-    f16* out = (br ? mid_v : mid_q) + t * R + j;
-#pragma unroll
-    for (int k = 0; k < TL::KEEP; ++k) out[k] = static_cast<f16>(acc[k]);
+  block_totals<R>(acc, s_part, s_tot);
+  if (threadIdx.x < TL::V) {
+    const int e = threadIdx.x;
+    const int tt = e / (2 * R), br = (e / R) & 1, j = e % R;
+    const int64_t t = t0 + tt;
+    if (t < n_tok) (br ? mid_v : mid_q)[t * R + j] = static_cast<f16>(s_tot[e]);
   }
 }
 
 // d_mid = fp16(dq B) per branch, then dx += fp16 drop_q(fp16(d_mid_q A_q)), += drop_v(...).
+// One block of four waves per Tile<R>::TT tokens; the waves split the chunks of both phases.
 template <int R>
 __global__ __launch_bounds__(256) void lora_bwd_x_kernel(
     const f16* __restrict__ dq, const f16* __restrict__ dv, int64_t n_tok, int64_t len_q,
@@ -270,58 +304,53 @@ __global__ __launch_bounds__(256) void lora_bwd_x_kernel(
     f16* __restrict__ dmid_v, f16* __restrict__ dx, int64_t sdx, Drop dr) {
   using TL = Tile<R>;
   constexpr int TT = TL::TT;
-  __shared__ float s_mid[4][TT][2][R];
-  const int wave_in_block = threadIdx.x / 64;
-  const int64_t wave = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) / 64;
-  const int64_t t0 = wave * TT;
-  const int lane = threadIdx.x & 63;
+  __shared__ float s_part[4 * TL::V];
+  __shared__ float s_mid[TL::V];  // entry (tt * 2 + br) * R + j
+  const int64_t t0 = static_cast<int64_t>(blockIdx.x) * TT;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x / 64;
   float acc[TL::V];
 #pragma unroll
   for (int i = 0; i < TL::V; ++i) acc[i] = 0.0f;
   const Drop none{nullptr, 0, 0, 0, 0, 1.0f, 1.0f};
-  if (t0 < n_tok)
-    reduce_rows<R, true>(acc, t0, n_tok, dq, len_q, len_q, dv, len_v, len_v, bq, bv, none,
-                         nullptr, nullptr);
-  butterfly<TL::V>(acc);
-  if (TL::V >= 64 || (lane & 1) == 0) {
-    const int idx = first_entry<TL::V>(lane);
-    const int tt = idx / (2 * R), br = (idx / R) & 1, j = idx % R;
+  reduce_rows<R, true>(acc, t0, n_tok, dq, len_q, len_q, dv, len_v, len_v, bq, bv, none,
+                       nullptr, nullptr);
+  block_totals<R>(acc, s_part, s_mid);
+  if (threadIdx.x < TL::V) {
+    const int e = threadIdx.x;
+    const int tt = e / (2 * R), br = (e / R) & 1, j = e % R;
     const int64_t t = t0 + tt;
-#pragma unroll
-    for (int k = 0; k < TL::KEEP; ++k) {
-      const f16 m = static_cast<f16>(acc[k]);
-      s_mid[wave_in_block][tt][br][j + k] = static_cast<float>(m);
-      if (t < n_tok) (br ? dmid_v : dmid_q)[t * R + j + k] = m;
-    }
+    if (t < n_tok) (br ? dmid_v : dmid_q)[t * R + j] = static_cast<f16>(s_mid[e]);
   }
-  __syncthreads();
-  if (t0 >= n_tok) return;
   const uint64_t seed = dr.seed ? *dr.seed : 0ull;
   const int64_t chunks = d / 8;
-  for (int64_t c = lane; c < chunks; c += 64) {
-    u32x4 wq[R], wv[R];
+  const int64_t per_wave = (chunks + 3) / 4;
+  const int64_t c_end = min(chunks, (wave + 1) * per_wave);
+  for (int64_t c = wave * per_wave + lane; c < c_end; c += 64) {
+    float xq[TT][8], xv[TT][8];
 #pragma unroll
-    for (int j = 0; j < R; ++j) {
-      wq[j] = load16(aq + j * d + c * 8);
-      wv[j] = load16(av + j * d + c * 8);
+    for (int br = 0; br < 2; ++br) {
+      const f16* a = br ? av : aq;
+#pragma unroll
+      for (int tt = 0; tt < TT; ++tt)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) (br ? xv : xq)[tt][i] = 0.0f;
+#pragma unroll
+      for (int j = 0; j < R; ++j) {
+        float arow[8];
+        unpack8(load16(a + j * d + c * 8), arow);
+#pragma unroll
+        for (int tt = 0; tt < TT; ++tt) {
+          const float m = s_mid[(tt * 2 + br) * R + j];
+#pragma unroll
+          for (int i = 0; i < 8; ++i)
+            (br ? xv : xq)[tt][i] = __builtin_fmaf(m, arow[i], (br ? xv : xq)[tt][i]);
+        }
+      }
     }
 #pragma unroll
     for (int tt = 0; tt < TT; ++tt) {
       const int64_t t = t0 + tt;
       if (t >= n_tok) continue;
-      float xq[8], xv[8], tmp[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) xq[i] = xv[i] = 0.0f;
-#pragma unroll
-      for (int j = 0; j < R; ++j) {
-        const float mq = s_mid[wave_in_block][tt][0][j], mv = s_mid[wave_in_block][tt][1][j];
-        unpack8(wq[j], tmp);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) xq[i] = __builtin_fmaf(mq, tmp[i], xq[i]);
-        unpack8(wv[j], tmp);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) xv[i] = __builtin_fmaf(mv, tmp[i], xv[i]);
-      }
       uint32_t bq_bits = 0xffu, bv_bits = 0xffu;
       if (dr.seed) {
         const uint64_t blk = static_cast<uint64_t>(t * chunks + c);
@@ -333,7 +362,7 @@ __global__ __launch_bounds__(256) void lora_bwd_x_kernel(
       unpack8(load16(p), cur);
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        const float hq = round_to<f16>(xq[i]), hv = round_to<f16>(xv[i]);  // dx_q, dx_v (fp16)
+        const float hq = round_to<f16>(xq[tt][i]), hv = round_to<f16>(xv[tt][i]);  // fp16 dx_q/v
         const float tq = round_to<f16>((bq_bits >> i) & 1u ? hq * dr.scale_q : 0.0f);
         const float tv = round_to<f16>((bv_bits >> i) & 1u ? hv * dr.scale_v : 0.0f);
         cur[i] = round_to<f16>(cur[i] + tq) + tv;
@@ -451,9 +480,8 @@ extern "C" int rus_lora_down_fwd(const void* x, int64_t n_tokens, int64_t d, int
   Drop dr;
   if (int e = make_drop(fn, seed, stream_q, stream_v, p_q, p_v, dr)) return e;
   if (n_tokens == 0) return RUS_OK;
-  const int64_t tt = r >= 32 ? 2 : 4;  // Tile<R>::TT
-  const int64_t waves = (n_tokens + tt - 1) / tt;
-  const dim3 grid(static_cast<uint32_t>((waves + 3) / 4));
+  const int64_t tt = r >= 32 ? 2 : 4;  // Tile<R>::TT tokens per block
+  const dim3 grid(static_cast<uint32_t>((n_tokens + tt - 1) / tt));
   hipStream_t st = static_cast<hipStream_t>(stream);
   const f16* xp = static_cast<const f16*>(x);
   const f16* aq = static_cast<const f16*>(a_q);
@@ -492,9 +520,8 @@ extern "C" int rus_lora_bwd_x(const void* dq_lora, const void* dv_lora, int64_t 
   Drop dr;
   if (int e = make_drop(fn, seed, stream_q, stream_v, p_q, p_v, dr)) return e;
   if (n_tokens == 0) return RUS_OK;
-  const int64_t tt = r >= 32 ? 2 : 4;  // Tile<R>::TT
-  const int64_t waves = (n_tokens + tt - 1) / tt;
-  const dim3 grid(static_cast<uint32_t>((waves + 3) / 4));
+  const int64_t tt = r >= 32 ? 2 : 4;  // Tile<R>::TT tokens per block
+  const dim3 grid(static_cast<uint32_t>((n_tokens + tt - 1) / tt));
   hipStream_t st = static_cast<hipStream_t>(stream);
 #define RUS_BX(RR)                                                                             \
   case RR:                                                                                     \
