@@ -152,6 +152,29 @@ def cpu_baseline(seed=0):
                        f"28*{t_layer:.3f}s + {t_head:.3f}s (lm_head)")}
 
 
+def lmhead_probe(reps: int = 5) -> None:
+    """Fixed launches for counter runs of the lm_head CE kernels at BASELINE config 2: hidden
+    [2048, 1536] ~ N(0,1), W [151936, 1536] ~ N(0, 0.02), 10% labels -100, whole vocabulary per
+    pass (forward statistics, logit gradient, hidden gradient)."""
+    import torch
+
+    from rus_amd import kernels as K
+
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(0)
+    n, d, v = 2048, 1536, 151936
+    h = torch.randn(n, d, device=dev, generator=g).half()
+    w = (torch.randn(v, d, device=dev, generator=g) * 0.02).half()
+    lab = torch.randint(0, v, (n,), device=dev, generator=g)
+    lab[torch.rand(n, device=dev, generator=g) < 0.1] = -100
+    wt = K.lm_head_weight_t(w)
+    torch.cuda.synchronize()
+    for _ in range(reps):
+        K.lm_head_ce(h, w, lab, weight_t=wt)
+    torch.cuda.synchronize()
+    print(f"probe: {reps} lm_head CE forward+gradient passes at N={n}, V={v}, d={d}", flush=True)
+
+
 def kernel_probe(reps: int = 5) -> None:
     """Fixed launches for hardware-counter runs: a plain 128 MiB device copy (the calibration for
     the FETCH_SIZE / WRITE_SIZE counters) and one config-5 layer's four-segment NF4 dequant."""
@@ -207,13 +230,17 @@ def main() -> int:
     ap.add_argument("--stream-unit", choices=("model", "layer"), default="model",
                     help="per step, copy the packed model once (model) or each layer per pass "
                          "through two one-layer slots (layer, the reference's policy)")
-    ap.add_argument("--probe", action="store_true",
-                    help="only the fixed copy + dequant launches used for counter runs")
+    ap.add_argument("--probe", nargs="?", const="dequant", choices=("dequant", "lmhead"),
+                    help="only fixed launches for counter runs: copy + dequant (default) or the "
+                         "lm_head CE kernels at config 2")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); the "
               "multi-GPU design is described in DESIGN.md", file=sys.stderr)
         return 2
+    if args.probe == "lmhead":
+        lmhead_probe()
+        return 0
     if args.probe:
         kernel_probe()
         return 0

@@ -77,26 +77,47 @@ __device__ __forceinline__ bool tile_of(const GemmArgs& g, Tile& t) {
   return true;
 }
 
-// One LDS stage (kBK of K) of MFMAs for this wave's 128x128 tile.
+// The 16-byte operand fragments of MFMA step kk (16 of K) for this wave's 128x128 tile.
+__device__ __forceinline__ void load_frags(const char* sa, int arow, int brow, int half, int asw,
+                                           int bsw, int kk, f16x8 (&fa)[kMT], f16x8 (&fb)[kNT]) {
+  const char* sb = sa + kTileBytes;
+  const int ch = kk * 2 + half;
+  const char* pa = sa + arow * (kBK * 2) + ((ch ^ asw) << 4);
+  const char* pb = sb + brow * (kBK * 2) + ((ch ^ bsw) << 4);
+#pragma unroll
+  for (int mt = 0; mt < kMT; ++mt) fa[mt] = *reinterpret_cast<const f16x8*>(pa + mt * 32 * (kBK * 2));
+#pragma unroll
+  for (int nt = 0; nt < kNT; ++nt) fb[nt] = *reinterpret_cast<const f16x8*>(pb + nt * 32 * (kBK * 2));
+}
+
+// One LDS stage (kBK of K) of MFMAs for this wave's 128x128 tile. The fragments of step kk+1
+// are read from LDS while step kk's 16 MFMAs issue (two register sets), so each read's latency
+// is covered by a block of MFMAs instead of stalling the first MFMA that needs it.
 __device__ __forceinline__ void mma_stage(const char* sa, int arow, int brow, int half, int asw,
                                           int bsw, f32x16 (&acc)[kMT][kNT]) {
-  const char* sb = sa + kTileBytes;
+  f16x8 fa[2][kMT], fb[2][kNT];
+  load_frags(sa, arow, brow, half, asw, bsw, 0, fa[0], fb[0]);
 #pragma unroll
   for (int kk = 0; kk < kBK / 16; ++kk) {
-    const int ch = kk * 2 + half;
-    const char* pa = sa + arow * (kBK * 2) + ((ch ^ asw) << 4);
-    const char* pb = sb + brow * (kBK * 2) + ((ch ^ bsw) << 4);
-    f16x8 fa[kMT], fb[kNT];
-#pragma unroll
-    for (int mt = 0; mt < kMT; ++mt) fa[mt] = *reinterpret_cast<const f16x8*>(pa + mt * 32 * (kBK * 2));
-#pragma unroll
-    for (int nt = 0; nt < kNT; ++nt) fb[nt] = *reinterpret_cast<const f16x8*>(pb + nt * 32 * (kBK * 2));
+    const int cur = kk & 1;
+    if (kk + 1 < kBK / 16)
+      load_frags(sa, arow, brow, half, asw, bsw, kk + 1, fa[cur ^ 1], fb[cur ^ 1]);
 #pragma unroll
     for (int mt = 0; mt < kMT; ++mt)
 #pragma unroll
       for (int nt = 0; nt < kNT; ++nt)
-        acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[mt], fb[nt], acc[mt][nt], 0, 0, 0);
+        acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[cur][mt], fb[cur][nt],
+                                                             acc[mt][nt], 0, 0, 0);
   }
+  // Issue order: reads of steps 0 and 1, MFMAs of step 0, reads of step 2, MFMAs of step 1,
+  // reads of step 3, MFMAs of steps 2 and 3.
+  static_assert(kBK / 16 == 4 && kMT * kNT == 16 && kMT + kNT == 8, "schedule assumes 4x4 tiles");
+  __builtin_amdgcn_sched_group_barrier(0x100, 16, 0);
+  __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);
+  __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+  __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);
+  __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+  __builtin_amdgcn_sched_group_barrier(0x008, 32, 0);
 }
 
 // acc[mt][nt] += A[m0 + wm*128 + mt*32 .. +32, k] . B[n0 + wn*128 + nt*32 .. +32, k]^T over the
@@ -215,28 +236,51 @@ lmhead_stats_kernel(GemmArgs g, StatsParams p) {
   const bool full = tl.m0 + kBM <= g.M;
   float rm[kNT], rs[kNT], rw[kNT];
   int ri[kNT];
+  // Logits as the reference's fp16 GEMM output: rounded once, in place.
+#pragma unroll
+  for (int mt = 0; mt < kMT; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < kNT; ++nt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[mt][nt][r] = round16(acc[mt][nt][r]);
+  // Accumulator row of (mt, r) for this lane: mt*32 + 8*(r/4) + 4*h + r%4 (local to vrow0).
+  const int rows_left = g.M - vrow0;  // rows at or past this are padding (edge tile only)
 #pragma unroll
   for (int nt = 0; nt < kNT; ++nt) {
     const int tok = tl.n0 + wn * kWN + nt * 32 + (lane & 31);
-    int lab = -1;
+    int lab_adj = -1000;  // label row local to vrow0, minus 4h (compared with the r/mt part)
     if (tok < g.N) {
-      const int64_t l = p.labels[tok] - p.vocab_start;
-      lab = (l >= 0 && l < g.M) ? static_cast<int>(l) : -1;
+      const int64_t l = p.labels[tok] - p.vocab_start - vrow0;
+      lab_adj = (l >= 0 && l < kWM) ? static_cast<int>(l) - 4 * h : -1000;
     }
     float m = -INFINITY, tgt = 0.0f;
-    int idx = 0x7fffffff;
+    int idx = 0x7fffffff;  // local row minus 4h until the end
+    if (full) {
 #pragma unroll
-    for (int mt = 0; mt < kMT; ++mt)
+      for (int mt = 0; mt < kMT; ++mt)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int row = vrow0 + mt * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-        const float z = round16(acc[mt][nt][r]);
-        if ((full || row < g.M) && z > m) {  // rows ascend: strict > keeps the first index
-          m = z;
-          idx = row;
+        for (int r = 0; r < 16; ++r) {
+          const int rl = mt * 32 + 8 * (r >> 2) + (r & 3);
+          const float z = acc[mt][nt][r];
+          idx = z > m ? rl : idx;  // rows ascend: strict > keeps the first index
+          m = fmaxf(m, z);
+          tgt = rl == lab_adj ? z : tgt;
         }
-        tgt = row == lab ? z : tgt;
-      }
+    } else {
+#pragma unroll
+      for (int mt = 0; mt < kMT; ++mt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int rl = mt * 32 + 8 * (r >> 2) + (r & 3);
+          const float z = acc[mt][nt][r];
+          if (rl + 4 * h < rows_left && z > m) {
+            m = z;
+            idx = rl;
+          }
+          tgt = rl == lab_adj ? z : tgt;
+        }
+    }
+    idx = idx == 0x7fffffff ? idx : vrow0 + idx + 4 * h;
     // The lane pair (l, l^32) holds the two interleaved halves of the wave's 128 rows.
     const float m2 = __shfl_xor(m, 32, kWave);
     const int i2 = __shfl_xor(idx, 32, kWave);
@@ -247,18 +291,30 @@ lmhead_stats_kernel(GemmArgs g, StatsParams p) {
     float s = 0.0f, w = 0.0f;
     if (m > -INFINITY) {
       const float mb = m * kLog2e;
+      if (full) {
 #pragma unroll
-      for (int mt = 0; mt < kMT; ++mt)
+        for (int mt = 0; mt < kMT; ++mt)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int row = vrow0 + mt * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-          if (full || row < g.M) {
-            const float z = round16(acc[mt][nt][r]);
+          for (int r = 0; r < 16; ++r) {
+            const float z = acc[mt][nt][r];
             const float e = exp2_fast(__builtin_fmaf(z, kLog2e, -mb));
             s += e;
-            w += e * z;
+            w = __builtin_fmaf(e, z, w);
           }
-        }
+      } else {
+#pragma unroll
+        for (int mt = 0; mt < kMT; ++mt)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int rl = mt * 32 + 8 * (r >> 2) + (r & 3);
+            if (rl + 4 * h < rows_left) {
+              const float z = acc[mt][nt][r];
+              const float e = exp2_fast(__builtin_fmaf(z, kLog2e, -mb));
+              s += e;
+              w = __builtin_fmaf(e, z, w);
+            }
+          }
+      }
     }
     s += __shfl_xor(s, 32, kWave);
     w += __shfl_xor(w, 32, kWave);
@@ -267,7 +323,7 @@ lmhead_stats_kernel(GemmArgs g, StatsParams p) {
     rw[nt] = w;
     ri[nt] = idx;
     // The label's row lives in exactly one lane of one block: that lane writes the target.
-    if (lab >= vrow0 && lab < vrow0 + kWM && ((lab >> 2) & 1) == h) p.target[tok] = tgt;
+    if (lab_adj + 4 * h >= 0 && ((lab_adj + 4 * h) >> 2 & 1) == h) p.target[tok] = tgt;
   }
 
   // Merge the two vocab halves (wm = 0, 1) of the block through LDS; wm = 0 writes the partial.
