@@ -230,6 +230,12 @@ def main() -> int:
     ap.add_argument("--stream-unit", choices=("model", "layer"), default="model",
                     help="per step, copy the packed model once (model) or each layer per pass "
                          "through two one-layer slots (layer, the reference's policy)")
+    ap.add_argument("--recompute", choices=("off", "on"), default="off",
+                    help="off: the forward keeps every layer's activations for the backward; on: "
+                         "the backward recomputes them from the saved layer inputs (the "
+                         "reference's checkpointing); the other setting is timed as an ablation")
+    ap.add_argument("--no-ablation", action="store_true",
+                    help="skip the timing of the other --recompute setting")
     ap.add_argument("--probe", nargs="?", const="dequant", choices=("dequant", "lmhead"),
                     help="only fixed launches for counter runs: copy + dequant (default) or the "
                          "lm_head CE kernels at config 2")
@@ -260,7 +266,9 @@ def main() -> int:
     opt = torch.optim.AdamW(params, lr=2e-4)
 
     # Configured engine: NF4 layers streamed per step from pinned host memory.
-    engine = Qwen2FusedEngine(model, dev, resident_weights=False, stream_unit=args.stream_unit)
+    recompute = args.recompute == "on"
+    engine = Qwen2FusedEngine(model, dev, resident_weights=False, stream_unit=args.stream_unit,
+                              recompute=recompute)
     # Calibration pass (eager): every kernel timed, to name the dominant one.
     _, _, _, calib = timed_run(engine, opt, batches, 2, args.warmup, kernel_filter=None)
     dominant = max(calib, key=lambda k: calib[k]["ms"])
@@ -312,7 +320,7 @@ def main() -> int:
                                "Qwen2.5-1.5B shapes, NF4 layers streamed from pinned host memory",
                    "rows": args.rows, "max_len": args.max_len,
                    "tokens_per_step": tokens / args.steps, "lora": "r16 alpha32 dropout0.05 q,v",
-                   "stream_unit": args.stream_unit},
+                   "stream_unit": args.stream_unit, "recompute": args.recompute},
         "roofline": roof,
         "median_step_tokens_per_s": (tokens / args.steps) / statistics.median(per_step),
         "peak_hbm_mib": (peak - base_alloc) / 2**20,
@@ -330,8 +338,29 @@ def main() -> int:
         r = calib["nf4_dequant"]
         out["nf4_dequant_gbps"] = r["bytes"] / (r["ms"] / 1e3) / 1e9
 
+    if not args.no_ablation:
+        # The other activation policy: same streamed weights, graphs, batches; its throughput
+        # and its working set (peak allocation of one eager step, as for the headline engine).
+        eng_a = Qwen2FusedEngine(model, dev, resident_weights=False, stream_unit=args.stream_unit,
+                                 recompute=not recompute)
+        torch.cuda.synchronize()
+        torch.cuda.reset_peak_memory_stats(dev)
+        base_a = torch.cuda.memory_allocated(dev)
+        timed_run(eng_a, opt, batches, 1, 0)
+        peak_a = (torch.cuda.max_memory_allocated(dev) - base_a) / 2**20
+        g_a = None
+        if graph is not None:
+            g_a = GraphedTrainStep(eng_a)
+            for b in batches:
+                g_a.prepare(b[0], b[1], b[2])
+        s_a, t_a, _, _ = timed_run(eng_a, opt, batches, min(args.steps, 16), 1, graph=g_a)
+        other = "on" if not recompute else "off"
+        out[f"recompute_{other}_tokens_per_s"] = t_a / s_a
+        out[f"recompute_{other}_peak_hbm_mib"] = peak_a
+        del eng_a, g_a
+
     if not args.no_resident:
-        eng_r = Qwen2FusedEngine(model, dev, resident_weights=True)
+        eng_r = Qwen2FusedEngine(model, dev, resident_weights=True, recompute=recompute)
         g_r = None
         if graph is not None:
             g_r = GraphedTrainStep(eng_r)

@@ -336,6 +336,36 @@ int rus_lmhead_ce_grad_hidden(const void* grad_logits, int64_t ld_g, const void*
 int rus_lmhead_dh_reduce(const float* parts, int32_t n_parts, int64_t n_elem, float scale,
                          const float* scale_dev, void* out, int32_t out_dtype, void* stream);
 
+/*
+ * Varlen causal GQA attention forward over packed tokens (fp16, head_dim 128 only):
+ *   out[t, h, :] = softmax_j( scale * q[t, h, :] . k[j, g, :] ) v[j, g, :],  g = h / (h_q / h_kv),
+ * j over the tokens of t's row with j <= t; rows are [cu[i], cu[i+1]) of the device int32
+ * cu_seqlens [n_seq + 1], which must cover all n_tokens tokens. q [n_tokens, h_q, 128],
+ * k/v [n_tokens, h_kv, 128], out like q (all contiguous, 16-byte aligned); lse [h_q, n_tokens]
+ * fp32 natural-log sum-exp of the scaled scores. max_blocks >= sum_i ceil(len_i / 32)
+ * (n_tokens / 32 + n_seq always suffices); extra blocks exit. P is rounded to fp16 for the PV
+ * product, accumulation is fp32.
+ * Replaces: solution/ops.py:669-696 (_run_packed_sdpa: torch SDPA per row with K/V expanded
+ * to the query heads, is_causal=True).
+ */
+int rus_attn_varlen_fwd(const void* q, const void* k, const void* v, const int32_t* cu_seqlens,
+                        int32_t n_seq, int64_t n_tokens, int32_t max_blocks, int32_t h_q,
+                        int32_t h_kv, int32_t head_dim, float scale, void* out, float* lse,
+                        void* stream);
+
+/*
+ * Backward of rus_attn_varlen_fwd: dq like q, dk / dv like k / v (fp16; dk and dv sum the h_q /
+ * h_kv query heads of each group in fp32 and are rounded once). out and lse are the forward's.
+ * workspace: fp32, at least round_up(h_q * n_tokens, 64) + 2 * h_q * n_tokens * 128 elements.
+ * Replaces: the autograd backward of solution/ops.py:669-696 (torch SDPA backward plus the
+ * sum over the expanded K/V heads), run by solution/ops.py:903-928.
+ */
+int rus_attn_varlen_bwd(const void* q, const void* k, const void* v, const void* out,
+                        const void* dout, const float* lse, const int32_t* cu_seqlens,
+                        int32_t n_seq, int64_t n_tokens, int32_t max_blocks, int32_t h_q,
+                        int32_t h_kv, int32_t head_dim, float scale, void* dq, void* dk,
+                        void* dv, float* workspace, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -427,6 +427,73 @@ def softmax_stats_reference(z: torch.Tensor, labels: torch.Tensor) -> dict:
     return {"lse": lse, "entropy": ent, "nll": nll, "argmax": z.argmax(-1)}
 
 
+# ---------------------------------------------------------------------------------------------
+# Varlen causal GQA attention — solution/ops.py:669-696 (_run_packed_sdpa) and its autograd
+# backward (ops.py:903-928)
+# ---------------------------------------------------------------------------------------------
+
+
+def _rows(cu) -> list[tuple[int, int]]:
+    cu = [int(c) for c in cu]
+    return [(cu[i], cu[i + 1]) for i in range(len(cu) - 1) if cu[i + 1] > cu[i]]
+
+
+def attention_varlen_fwd(q, k, v, cu, scale=None):
+    """(out [n, h_q, d], lse [h_q, n]) in float64: per row [cu[i], cu[i+1]), causal softmax of
+    scale * q k^T (k/v head g = h // (h_q / h_kv), as the expand+reshape of ops.py:690-692) times
+    v; lse is the natural-log sum-exp of the scaled scores."""
+    n, hq, d = q.shape
+    grp = hq // k.shape[1]
+    scale = 1.0 / math.sqrt(d) if scale is None else scale
+    q, k, v = q.double(), k.double(), v.double()
+    out = torch.zeros(n, hq, d, dtype=torch.float64)
+    lse = torch.zeros(hq, n, dtype=torch.float64)
+    for a, e in _rows(cu):
+        ks = k[a:e].repeat_interleave(grp, dim=1).transpose(0, 1)  # [h_q, L, d]
+        vs = v[a:e].repeat_interleave(grp, dim=1).transpose(0, 1)
+        s = scale * (q[a:e].transpose(0, 1) @ ks.transpose(1, 2))  # [h_q, L, L]
+        causal = torch.ones(e - a, e - a, dtype=torch.bool).tril()
+        s = s.masked_fill(~causal, float("-inf"))
+        m = s.amax(-1, keepdim=True)
+        p = torch.exp(s - m)
+        den = p.sum(-1, keepdim=True)
+        out[a:e] = ((p / den) @ vs).transpose(0, 1)
+        lse[:, a:e] = (m + torch.log(den)).squeeze(-1)
+    return out, lse
+
+
+def attention_varlen_bwd(dout, q, k, v, cu, scale=None):
+    """(dq, dk, dv) in float64 by the softmax adjoint per row and head: P = softmax(S),
+    dV = P^T dO, dP = dO V^T, dS = P o (dP - rowsum(dO o O)), dQ = scale dS K, dK = scale dS^T Q;
+    dk / dv sum the query heads sharing a KV head (the adjoint of the expand of ops.py:690-692)."""
+    n, hq, d = q.shape
+    hkv = k.shape[1]
+    grp = hq // hkv
+    scale = 1.0 / math.sqrt(d) if scale is None else scale
+    q, k, v, dout = q.double(), k.double(), v.double(), dout.double()
+    dq = torch.zeros(n, hq, d, dtype=torch.float64)
+    dk = torch.zeros(n, hkv, d, dtype=torch.float64)
+    dv = torch.zeros(n, hkv, d, dtype=torch.float64)
+    for a, e in _rows(cu):
+        L = e - a
+        qh = q[a:e].transpose(0, 1)
+        ks = k[a:e].repeat_interleave(grp, dim=1).transpose(0, 1)
+        vs = v[a:e].repeat_interleave(grp, dim=1).transpose(0, 1)
+        do = dout[a:e].transpose(0, 1)
+        s = scale * (qh @ ks.transpose(1, 2))
+        s = s.masked_fill(~torch.ones(L, L, dtype=torch.bool).tril(), float("-inf"))
+        p = torch.softmax(s, dim=-1)
+        o = p @ vs
+        dvs = p.transpose(1, 2) @ do
+        dp = do @ vs.transpose(1, 2)
+        ds = p * (dp - (do * o).sum(-1, keepdim=True))
+        dq[a:e] = (scale * (ds @ ks)).transpose(0, 1)
+        dks = scale * (ds.transpose(1, 2) @ qh)
+        dk[a:e] = dks.reshape(hkv, grp, L, d).sum(1).transpose(0, 1)
+        dv[a:e] = dvs.reshape(hkv, grp, L, d).sum(1).transpose(0, 1)
+    return dq, dk, dv
+
+
 def fp16_ulp(x: torch.Tensor) -> torch.Tensor:
     """Spacing of fp16 numbers at |x| (subnormal spacing below 2^-14)."""
     a = x.abs().float().clamp(min=2.0**-14)

@@ -52,6 +52,10 @@ SIGNATURES: dict[str, list] = {
     "rus_lora_bwd_w": [_vp, _vp, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i32,
                        _vp, _vp, _vp, _vp, _vp],
     "rus_lmhead_ce_loss": [_vp, _vp, _i64, _vp, _vp, _vp, _vp],
+    "rus_attn_varlen_fwd": [_vp, _vp, _vp, _vp, _i32, _i64, _i32, _i32, _i32, _i32, _f32, _vp, _vp,
+                            _vp],
+    "rus_attn_varlen_bwd": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i64, _i32, _i32, _i32, _i32,
+                            _f32, _vp, _vp, _vp, _vp, _vp],
     "rus_rmsnorm_fwd": [_vp, _vp, _vp, _i32, _vp, _vp, _vp, _i64, _i64, _i64, _f32, _i32, _vp],
     "rus_rmsnorm_bwd": [_vp, _vp, _vp, _i32, _vp, _vp, _vp, _i64, _i64, _i64, _i32, _vp],
     "rus_qkv_lora_rope_fwd": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64,

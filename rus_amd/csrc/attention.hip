@@ -1,0 +1,668 @@
+// Varlen causal GQA attention (forward and backward) on packed tokens for gfx950, head_dim 128.
+//
+// Reference behaviour (solution/ops.py:669-696, _run_packed_sdpa): per packed row, causal scaled
+// dot-product attention with softmax scale 1/sqrt(head_dim) and K/V shared by h_q / h_kv query
+// heads; its backward is torch's. Layout here: q [N, h_q, 128], k / v [N, h_kv, 128] token-major
+// (the RoPE kernel's outputs), rows delimited by cu_seqlens [n_seq + 1] (int32, on the device).
+//
+// Design (CDNA4, v_mfma_f32_32x32x16_f16; operand / accumulator lane layouts as in lmhead.hip):
+//   * one block of 4 waves per (row, 32-token block, query head); the waves split the loop over
+//     the other operand's 32-token blocks (prefetching each next block into registers), stage
+//     their transposed tiles in LDS of their own, and merge their partials through LDS at the
+//     end in a fixed order (softmax partials rescaled by their running maxima);
+//   * forward computes S^T = K Q^T, so a lane owns one query (column) and 16 of the block's 32
+//     keys: the running max / sum and the O rescale are per-lane scalars, and P^T feeds the
+//     O^T += V^T P^T product straight from the accumulator registers. An accumulator tile used
+//     as an MFMA operand carries its reduction index in the order
+//         k(h, i) = 16 s + 8 (i / 4) + 4 h + i % 4      (lane half h, slot i of step s),
+//     so the other operand is read in the same order from a transposed LDS copy (two 8-byte
+//     reads per fragment);
+//   * P and dS are rounded to fp16 for their MFMAs, as flash attention does; O, LSE, dQ, dK, dV
+//     accumulate in fp32;
+//   * backward: kernel 1 per (row, query block, head) forms D = rowsum(dO o O) and dQ;
+//     kernel 2 per (row, key block, query head) forms that head's dK and dV contributions in fp32;
+//     kernel 3 sums the h_q / h_kv heads of each KV group and rounds once (no atomics).
+#include <math.h>
+
+#include "common.h"
+
+namespace rus {
+namespace {
+
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int kHD = 128;       // head_dim
+constexpr int kBlk = 32;       // tokens per block
+constexpr int kTS = kBlk + 4;  // transposed-tile row stride (halfs): 72 B, conflict-free reads
+constexpr int kW = 4;          // waves per block (one 32x32 head-dim tile each in the merges)
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+constexpr float kLazy = 8.0f;  // lazy-rescale threshold (log2 units)
+
+struct AttnArgs {
+  const f16* q;
+  const f16* k;
+  const f16* v;
+  const f16* o;    // forward output (backward input)
+  const f16* dout;
+  const int32_t* cu;
+  f16* out;        // forward: O; backward kernel 1: dQ
+  float* lse;      // [h_q, n_tok], natural log
+  float* dsum;     // [h_q, n_tok], D = rowsum(dO o O)
+  float* dk_part;  // [h_q, n_tok, 128]
+  float* dv_part;
+  int64_t n_tok;
+  int n_seq, h_q, h_kv;
+  float scale, scale_log2;
+};
+
+// 2^x by the hardware instruction (v_exp_f32): 2^-inf = 0; results below the normal range
+// flush to zero, far below what the fp16 operands they feed can hold.
+__device__ __forceinline__ float exp2_raw(float x) { return __builtin_amdgcn_exp2f(x); }
+
+__device__ __forceinline__ f32x16 mfma(f16x8 a, f16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+// Row bounds of row s (clamped to [0, n_tok] and non-decreasing, so a malformed cu_seqlens
+// cannot send an access outside the token arrays) and its number of 32-token blocks.
+struct RowInfo {
+  int a, e, nb;
+};
+
+__device__ __forceinline__ RowInfo row_info(const int32_t* cu, int s, int n_seq, int n_tok) {
+  RowInfo r{0, 0, 0};
+  if (s < n_seq) {
+    r.a = min(max(cu[s], 0), n_tok);
+    r.e = min(max(cu[s + 1], r.a), n_tok);
+    r.nb = (r.e - r.a + kBlk - 1) / kBlk;
+  }
+  return r;
+}
+
+// Index of the n-th set bit of m (n < popcount(m)).
+__device__ __forceinline__ int nth_bit(uint64_t m, int n) {
+  for (int i = 0; i < n; ++i) m &= m - 1;
+  return __ffsll(static_cast<unsigned long long>(m)) - 1;
+}
+
+// Block id -> (row start, row end, block start), heaviest blocks first. A row of nb blocks has
+// one block of each work level w = 1 .. nb (the number of 32-token blocks on the other side of
+// the causal loop): block w - 1 when the work grows towards the row's end (kDiagLast: forward
+// and dQ, which loop over the keys up to the diagonal), block nb - w otherwise (dK/dV, which loop
+// over the queries from the diagonal on). Ids run over levels from the highest down, rows in
+// order within a level, so the longest blocks are dispatched first. Each lane holds one row of
+// a 64-row chunk; false if blk is past the last block. Uniform over the block.
+template <bool kDiagLast>
+__device__ __forceinline__ bool find_block(const int32_t* cu, int n_seq, int n_tok, int blk,
+                                           int& start, int& end, int& b0) {
+  const int lane = threadIdx.x & 63;
+  const int n_chunks = (n_seq + 63) / 64;
+  const RowInfo r0 = row_info(cu, lane, n_seq, n_tok);
+  int max_nb = r0.nb;
+  for (int c = 1; c < n_chunks; ++c) max_nb = max(max_nb, row_info(cu, 64 * c + lane, n_seq, n_tok).nb);
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) max_nb = max(max_nb, __shfl_xor(max_nb, off, 64));
+  for (int w = max_nb; w >= 1; --w) {
+    for (int c = 0; c < n_chunks; ++c) {
+      const RowInfo r = c == 0 ? r0 : row_info(cu, 64 * c + lane, n_seq, n_tok);
+      const uint64_t mask = __ballot(r.nb >= w);
+      const int cnt = __popcll(mask);
+      if (blk < cnt) {
+        const int src = nth_bit(mask, blk);
+        start = __shfl(r.a, src, 64);
+        end = __shfl(r.e, src, 64);
+        const int nb = __shfl(r.nb, src, 64);
+        b0 = start + (kDiagLast ? w - 1 : nb - w) * kBlk;
+        return true;
+      }
+      blk -= cnt;
+    }
+  }
+  return false;
+}
+
+// 8 consecutive halfs of row `row`, column `col` (16-byte load).
+__device__ __forceinline__ f16x8 ld8(const f16* base, int64_t row, int64_t stride, int col) {
+  return *reinterpret_cast<const f16x8*>(base + row * stride + col);
+}
+
+// Rows r0 .. r0+31 (clamped to [lo, hi)) of a [*, stride] head slice, loaded for a transposed
+// LDS copy: lane (rq = lane % 8, cc = lane / 8 + 8 G) holds rows 4 rq .. 4 rq + 3, columns
+// 8 cc .. 8 cc + 7 in v[4 G + i].
+__device__ __forceinline__ void load_rows4(f16x8 (&v)[8], const f16* x, int64_t stride, int r0,
+                                           int lo, int hi) {
+  const int lane = threadIdx.x & 63, rq = lane & 7, cc = lane >> 3;
+#pragma unroll
+  for (int G = 0; G < 2; ++G)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      int r = r0 + 4 * rq + i;
+      r = r < hi ? r : hi - 1;
+      r = r < lo ? lo : r;
+      v[4 * G + i] = ld8(x, r, stride, (cc + 8 * G) * 8);
+    }
+}
+
+// t[d * kTS + j] = X[r0 + j][d] from load_rows4's registers: one 8-byte write per column and
+// row quad. Lanes 0..31 cover all 64 LDS banks (row stride 18 words, quads 2 words apart).
+__device__ __forceinline__ void write_t4(f16* t, const f16x8 (&v)[8]) {
+  const int lane = threadIdx.x & 63, rq = lane & 7, cc = lane >> 3;
+#pragma unroll
+  for (int G = 0; G < 2; ++G)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const f16x4 w{v[4 * G][e], v[4 * G + 1][e], v[4 * G + 2][e], v[4 * G + 3][e]};
+      *reinterpret_cast<f16x4*>(t + ((cc + 8 * G) * 8 + e) * kTS + 4 * rq) = w;
+    }
+}
+
+// MFMA operand fragments of row `row` (lane % 32) for the 8 k-steps over head_dim:
+// f[s] = x[row][16 s + 8 h .. +7].
+__device__ __forceinline__ void load_frags(f16x8 (&f)[8], const f16* x, int64_t row,
+                                           int64_t stride, int h) {
+#pragma unroll
+  for (int s = 0; s < 8; ++s) f[s] = ld8(x, row, stride, 16 * s + 8 * h);
+}
+
+// Operand fragment of k-step s (reduction index in the accumulator order k(h, i)) for row `row`
+// of a transposed LDS tile.
+__device__ __forceinline__ f16x8 frag_t(const f16* t, int row, int s, int h) {
+  const f16* p = t + row * kTS + 16 * s + 4 * h;
+  const f16x4 a = *reinterpret_cast<const f16x4*>(p);
+  const f16x4 b = *reinterpret_cast<const f16x4*>(p + 8);
+  return f16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+}
+
+// fp16 operand of k-step s from accumulator registers 8s .. 8s+7.
+__device__ __forceinline__ f16x8 frag_acc(const f32x16& c, int s) {
+  f16x8 r;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) r[i] = static_cast<_Float16>(c[8 * s + i]);
+  return r;
+}
+
+// Accumulator row of register r for lane half h.
+__device__ __forceinline__ int acc_row(int r, int h) { return 8 * (r >> 2) + 4 * h + (r & 3); }
+
+// Partial accumulators of the block's kW waves, summed in a fixed order: every wave stores its
+// four 32x32 tiles (the accumulator layout, lane-contiguous), then thread (wave w, lane) reads
+// tile w of every wave. buf holds kW * 64 * 64 floats.
+__device__ __forceinline__ void park(float* buf, const f32x16 (&acc)[4], int wave, int lane) {
+#pragma unroll
+  for (int d = 0; d < 4; ++d)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) buf[(wave * 64 + d * 16 + r) * 64 + lane] = acc[d][r];
+}
+
+__device__ __forceinline__ float parked(const float* buf, int w, int tile, int r, int lane) {
+  return buf[(w * 64 + tile * 16 + r) * 64 + lane];
+}
+
+// fp16 store of the 16 accumulator values of tile d (head dims d*32 + 8 r4 + 4 h + i) of one
+// query's row.
+__device__ __forceinline__ void store_tile_row(f16* row, const float (&x)[16], int d, int h) {
+#pragma unroll
+  for (int r4 = 0; r4 < 4; ++r4) {
+    f16x4 w;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) w[i] = static_cast<_Float16>(x[4 * r4 + i]);
+    *reinterpret_cast<f16x4*>(row + d * 32 + 8 * r4 + 4 * h) = w;
+  }
+}
+
+constexpr int kStageHalfs = kHD * kTS;                   // one transposed 32 x 128 tile
+constexpr int kParkBytes = kW * 64 * 64 * 4;             // 64 KiB
+constexpr int kMax(int x, int y) { return x > y ? x : y; }
+
+// ---------------------------------------------------------------------------------------------
+// Forward: O = softmax(Q K^T * scale, causal) V and LSE. Block = (row, query block, head); its
+// kW waves take key blocks w, w + kW, ... with their own running max / sum, merged at the end.
+// ---------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(64 * kW) void attn_fwd_kernel(AttnArgs a) {
+  constexpr int kBytes = kMax(kW * kStageHalfs * 2, kParkBytes + kW * 64 * 4);
+  __shared__ __attribute__((aligned(16))) char smem[kBytes];
+  int start, end, q0;
+  if (!find_block<true>(a.cu, a.n_seq, static_cast<int>(a.n_tok), blockIdx.y, start, end, q0)) return;
+  const int head = blockIdx.x, g = head / (a.h_q / a.h_kv);
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, h = lane >> 5, col = lane & 31;
+  const int64_t sq = static_cast<int64_t>(a.h_q) * kHD, skv = static_cast<int64_t>(a.h_kv) * kHD;
+  const f16* qh = a.q + head * kHD;
+  const f16* kh = a.k + g * kHD;
+  const f16* vh = a.v + g * kHD;
+  f16* vt = reinterpret_cast<f16*>(smem) + wave * kStageHalfs;
+
+  const int qi = q0 + col;  // this lane's query
+  f16x8 qf[8];
+  load_frags(qf, qh, qi < end ? qi : end - 1, sq, h);
+  f32x16 o[4];
+#pragma unroll
+  for (int d = 0; d < 4; ++d) o[d] = f32x16{};
+  float m = -INFINITY, l = 0.0f;
+  const int nk = (q0 - start) / kBlk + 1;  // key blocks up to and including the diagonal
+  f16x8 kf[8], vv[8];
+  if (wave < nk) {
+    const int k0 = start + wave * kBlk;
+    load_frags(kf, kh, min(k0 + col, end - 1), skv, h);
+    load_rows4(vv, vh, skv, k0, start, end);
+  }
+  for (int kb = wave; kb < nk; kb += kW) {
+    const int k0 = start + kb * kBlk;
+    f32x16 st = f32x16{};  // S^T = K Q^T: rows keys, columns queries
+#pragma unroll
+    for (int s = 0; s < 8; ++s) st = mfma(kf[s], qf[s], st);
+    write_t4(vt, vv);
+    if (kb + kW < nk) {  // prefetch the wave's next key block
+      const int k1 = k0 + kW * kBlk;
+      load_frags(kf, kh, min(k1 + col, end - 1), skv, h);
+      load_rows4(vv, vh, skv, k1, start, end);
+    }
+    // Only the diagonal block holds keys past the query or past the row's end.
+    float mx = -INFINITY;
+    if (kb == nk - 1) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int key = k0 + acc_row(r, h);
+        st[r] = (key <= qi && key < end) ? st[r] * a.scale_log2 : -INFINITY;
+        mx = fmaxf(mx, st[r]);
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        st[r] *= a.scale_log2;
+        mx = fmaxf(mx, st[r]);
+      }
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));  // finite: key k0 <= q0 <= qi is always allowed
+    // Lazy rescaling: the reference point m moves only when a block's maximum exceeds it by
+    // more than 8 (log2 units), so p = 2^(s - m) <= 256 (exact in range for fp16) and O and l
+    // share one reference, leaving O / l unchanged; the rescale of O is a wave-uniform branch
+    // that is rarely taken after the first block.
+    const bool bump = mx > m + kLazy;
+    if (__ballot(bump)) {
+      const float mn = bump ? mx : m;
+      const float alpha = exp2_raw(m - mn);  // 0 on the first block (m = -inf)
+      l *= alpha;
+      m = mn;
+#pragma unroll
+      for (int d = 0; d < 4; ++d)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[d][r] *= alpha;
+    }
+    float rs = 0.0f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const float p = exp2_raw(st[r] - m);
+      st[r] = p;
+      rs += p;
+    }
+    rs += __shfl_xor(rs, 32, 64);
+    l += rs;
+    // The wave's own LDS writes above are visible to its reads below (LDS executes a wave's
+    // instructions in order); the next iteration's writes follow these reads likewise.
+    const f16x8 p0 = frag_acc(st, 0), p1 = frag_acc(st, 1);
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      o[d] = mfma(frag_t(vt, d * 32 + col, 0, h), p0, o[d]);
+      o[d] = mfma(frag_t(vt, d * 32 + col, 1, h), p1, o[d]);
+    }
+  }
+  __syncthreads();  // all waves are done with their V^T tiles; the space is reused below
+  float* buf = reinterpret_cast<float*>(smem);
+  float* ml = buf + kW * 64 * 64;  // per wave: m of columns 0..31, then l
+  park(buf, o, wave, lane);
+  if (h == 0) {
+    ml[wave * 64 + col] = m;
+    ml[wave * 64 + 32 + col] = l;
+  }
+  __syncthreads();
+  float M = -INFINITY;
+#pragma unroll
+  for (int w = 0; w < kW; ++w) M = fmaxf(M, ml[w * 64 + col]);
+  float f[kW], L = 0.0f;
+#pragma unroll
+  for (int w = 0; w < kW; ++w) {
+    const float mw = ml[w * 64 + col];
+    f[w] = exp2_raw(mw - M);  // 0 for a wave without key blocks (mw = -inf)
+    L += ml[w * 64 + 32 + col] * f[w];
+  }
+  if (qi < end) {
+    const float inv = 1.0f / L;
+    float x[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      float acc = 0.0f;
+#pragma unroll
+      for (int w = 0; w < kW; ++w) acc += parked(buf, w, wave, r, lane) * f[w];
+      x[r] = acc * inv;
+    }
+    store_tile_row(a.out + qi * sq + head * kHD, x, wave, h);
+    if (wave == 0 && h == 0) a.lse[head * a.n_tok + qi] = (M + log2f(L)) * kLn2;
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// Backward 1: D = rowsum(dO o O) and dQ = scale * dS K. Block = (row, query block, head); the
+// kW waves split the key blocks and their dQ partials are summed at the end.
+// ---------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(64 * kW) void attn_bwd_dq_kernel(AttnArgs a) {
+  constexpr int kBytes = kMax(kW * kStageHalfs * 2, kParkBytes);
+  __shared__ __attribute__((aligned(16))) char smem[kBytes];
+  int start, end, q0;
+  if (!find_block<true>(a.cu, a.n_seq, static_cast<int>(a.n_tok), blockIdx.y, start, end, q0)) return;
+  const int head = blockIdx.x, g = head / (a.h_q / a.h_kv);
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, h = lane >> 5, col = lane & 31;
+  const int64_t sq = static_cast<int64_t>(a.h_q) * kHD, skv = static_cast<int64_t>(a.h_kv) * kHD;
+  const f16* qh = a.q + head * kHD;
+  const f16* kh = a.k + g * kHD;
+  const f16* vh = a.v + g * kHD;
+  f16* kt = reinterpret_cast<f16*>(smem) + wave * kStageHalfs;
+
+  const int qi = q0 + col;
+  const int qr = qi < end ? qi : end - 1;
+  f16x8 qf[8], df[8];
+  load_frags(qf, qh, qr, sq, h);
+  load_frags(df, a.dout + head * kHD, qr, sq, h);
+  float dsum = 0.0f;
+#pragma unroll
+  for (int s = 0; s < 8; ++s) {
+    const f16x8 of = ld8(a.o + head * kHD, qr, sq, 16 * s + 8 * h);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) dsum += static_cast<float>(df[s][i]) * static_cast<float>(of[i]);
+  }
+  dsum += __shfl_xor(dsum, 32, 64);
+  const float lse2 = a.lse[head * a.n_tok + qr] * kLog2e;
+  if (wave == 0 && qi < end && h == 0) a.dsum[head * a.n_tok + qi] = dsum;
+
+  f32x16 dq[4];
+#pragma unroll
+  for (int d = 0; d < 4; ++d) dq[d] = f32x16{};
+  const int nk = (q0 - start) / kBlk + 1;
+  f16x8 kf[8], vf[8], kk[8];
+  if (wave < nk) {
+    const int k0 = start + wave * kBlk, kr = min(k0 + col, end - 1);
+    load_frags(kf, kh, kr, skv, h);
+    load_frags(vf, vh, kr, skv, h);
+    load_rows4(kk, kh, skv, k0, start, end);
+  }
+  for (int kb = wave; kb < nk; kb += kW) {
+    const int k0 = start + kb * kBlk;
+    f32x16 st = f32x16{}, dp = f32x16{};
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      st = mfma(kf[s], qf[s], st);  // S^T = K Q^T
+      dp = mfma(vf[s], df[s], dp);  // dP^T = V dO^T
+    }
+    write_t4(kt, kk);
+    if (kb + kW < nk) {
+      const int k1 = k0 + kW * kBlk, kr = min(k1 + col, end - 1);
+      load_frags(kf, kh, kr, skv, h);
+      load_frags(vf, vh, kr, skv, h);
+      load_rows4(kk, kh, skv, k1, start, end);
+    }
+    if (kb == nk - 1) {  // diagonal block: causal and row-end mask
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int key = k0 + acc_row(r, h);
+        const float p = exp2_raw(st[r] * a.scale_log2 - lse2);
+        st[r] = (key <= qi && key < end) ? p * (dp[r] - dsum) : 0.0f;  // dS^T
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) st[r] = exp2_raw(st[r] * a.scale_log2 - lse2) * (dp[r] - dsum);
+    }
+    const f16x8 s0 = frag_acc(st, 0), s1 = frag_acc(st, 1);
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      dq[d] = mfma(frag_t(kt, d * 32 + col, 0, h), s0, dq[d]);  // dQ^T += K^T dS^T
+      dq[d] = mfma(frag_t(kt, d * 32 + col, 1, h), s1, dq[d]);
+    }
+  }
+  __syncthreads();
+  float* buf = reinterpret_cast<float*>(smem);
+  park(buf, dq, wave, lane);
+  __syncthreads();
+  if (qi < end) {
+    float x[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      float acc = 0.0f;
+#pragma unroll
+      for (int w = 0; w < kW; ++w) acc += parked(buf, w, wave, r, lane);
+      x[r] = acc * a.scale;
+    }
+    store_tile_row(a.out + qi * sq + head * kHD, x, wave, h);
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// Backward 2: this query head's dK = scale * dS^T Q and dV = P^T dO for one 32-key block, fp32.
+// Block = (row, key block, head); the kW waves split the query blocks.
+// ---------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(64 * kW) void attn_bwd_dkdv_kernel(AttnArgs a) {
+  constexpr int kBytes = kMax(2 * kW * kStageHalfs * 2, kParkBytes);
+  __shared__ __attribute__((aligned(16))) char smem[kBytes];
+  int start, end, k0;
+  if (!find_block<false>(a.cu, a.n_seq, static_cast<int>(a.n_tok), blockIdx.y, start, end, k0)) return;
+  const int head = blockIdx.x, g = head / (a.h_q / a.h_kv);
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, h = lane >> 5, col = lane & 31;
+  const int64_t sq = static_cast<int64_t>(a.h_q) * kHD, skv = static_cast<int64_t>(a.h_kv) * kHD;
+  const f16* qh = a.q + head * kHD;
+  const f16* doh = a.dout + head * kHD;
+  const f16* kh = a.k + g * kHD;
+  const f16* vh = a.v + g * kHD;
+  f16* qt = reinterpret_cast<f16*>(smem) + 2 * wave * kStageHalfs;
+  f16* dt = qt + kStageHalfs;
+  const float* lse = a.lse + head * a.n_tok;
+  const float* dsum = a.dsum + head * a.n_tok;
+
+  const int kj = k0 + col;  // this lane's key (column of S = Q K^T)
+  f16x8 kf[8], vf[8];
+  load_frags(kf, kh, kj < end ? kj : end - 1, skv, h);
+  load_frags(vf, vh, kj < end ? kj : end - 1, skv, h);
+  f32x16 dk[4], dv[4];
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    dk[d] = f32x16{};
+    dv[d] = f32x16{};
+  }
+  const int nq = (end - k0 + kBlk - 1) / kBlk;  // query blocks from the diagonal to the row end
+  f16x8 qa[8], da[8], qs[8], ds[8];
+  if (wave < nq) {
+    const int q0 = k0 + wave * kBlk, qrow = min(q0 + col, end - 1);
+    load_frags(qa, qh, qrow, sq, h);
+    load_frags(da, doh, qrow, sq, h);
+    load_rows4(qs, qh, sq, q0, start, end);
+    load_rows4(ds, doh, sq, q0, start, end);
+  }
+  for (int qb = wave; qb < nq; qb += kW) {
+    const int q0 = k0 + qb * kBlk;
+    float lq[16], dr[16];  // lse (log2 units) and D of this lane's 16 query rows
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int qi = min(q0 + acc_row(r, h), end - 1);
+      lq[r] = lse[qi] * kLog2e;
+      dr[r] = dsum[qi];
+    }
+    f32x16 st = f32x16{}, dp = f32x16{};
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      st = mfma(qa[s], kf[s], st);  // S = Q K^T
+      dp = mfma(da[s], vf[s], dp);  // dP = dO V^T
+    }
+    write_t4(qt, qs);
+    write_t4(dt, ds);
+    if (qb + kW < nq) {
+      const int q1 = q0 + kW * kBlk, qrow = min(q1 + col, end - 1);
+      load_frags(qa, qh, qrow, sq, h);
+      load_frags(da, doh, qrow, sq, h);
+      load_rows4(qs, qh, sq, q1, start, end);
+      load_rows4(ds, doh, sq, q1, start, end);
+    }
+    // Query rows past the row's end (last block) and before the key (diagonal block) are
+    // masked; key columns past the row's end only feed dK / dV rows that are not written.
+    const bool edge = q0 == k0 || q0 + kBlk > end;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int qi = q0 + acc_row(r, h);
+      float p = exp2_raw(st[r] * a.scale_log2 - lq[r]);
+      if (edge) p = (kj <= qi && qi < end) ? p : 0.0f;
+      st[r] = p;                    // P
+      dp[r] = p * (dp[r] - dr[r]);  // dS
+    }
+    const f16x8 p0 = frag_acc(st, 0), p1 = frag_acc(st, 1);
+    const f16x8 s0 = frag_acc(dp, 0), s1 = frag_acc(dp, 1);
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      dv[d] = mfma(p0, frag_t(dt, d * 32 + col, 0, h), dv[d]);  // dV += P^T dO
+      dv[d] = mfma(p1, frag_t(dt, d * 32 + col, 1, h), dv[d]);
+      dk[d] = mfma(s0, frag_t(qt, d * 32 + col, 0, h), dk[d]);  // dK += dS^T Q
+      dk[d] = mfma(s1, frag_t(qt, d * 32 + col, 1, h), dk[d]);
+    }
+  }
+  // Sum the waves' partials (dK, then dV through the same buffer). Rows are keys (accumulator
+  // rows), columns head dims (lanes); thread (wave w, lane) writes head-dim tile w.
+  float* buf = reinterpret_cast<float*>(smem);
+#pragma unroll
+  for (int pass = 0; pass < 2; ++pass) {
+    __syncthreads();
+    park(buf, pass == 0 ? dk : dv, wave, lane);
+    __syncthreads();
+    float* dst = pass == 0 ? a.dk_part : a.dv_part;
+    const float sc = pass == 0 ? a.scale : 1.0f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int key = k0 + acc_row(r, h);
+      float acc = 0.0f;
+#pragma unroll
+      for (int w = 0; w < kW; ++w) acc += parked(buf, w, wave, r, lane);
+      if (key < end) dst[(static_cast<int64_t>(head) * a.n_tok + key) * kHD + wave * 32 + col] = acc * sc;
+    }
+  }
+}
+
+// Backward 3: dk[t, g, :] = fp16(sum of the group's heads), same for dv. 8 elements per thread.
+__global__ __launch_bounds__(256) void attn_gqa_reduce_kernel(const float* __restrict__ dk_part,
+                                                              const float* __restrict__ dv_part,
+                                                              f16* __restrict__ dk,
+                                                              f16* __restrict__ dv,
+                                                              int64_t n_tok, int h_q, int h_kv) {
+  const int64_t total = n_tok * h_kv * (kHD / 8);
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= total) return;
+  const int c = static_cast<int>(i % (kHD / 8)) * 8;
+  const int64_t tg = i / (kHD / 8);
+  const int g = static_cast<int>(tg % h_kv);
+  const int64_t t = tg / h_kv;
+  const int grp = h_q / h_kv;
+  float sk[8] = {}, sv[8] = {};
+  for (int j = 0; j < grp; ++j) {
+    const int64_t off = (static_cast<int64_t>(g * grp + j) * n_tok + t) * kHD + c;
+    float x[8];
+    load_f32<float, 8>(dk_part + off, x);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) sk[e] += x[e];
+    load_f32<float, 8>(dv_part + off, x);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) sv[e] += x[e];
+  }
+  const int64_t o = (t * h_kv + g) * kHD + c;
+  store_from_f32<f16, 8>(dk + o, sk);
+  store_from_f32<f16, 8>(dv + o, sv);
+}
+
+int check(const char* fn, const void* q, const void* k, const void* v, const int32_t* cu,
+          int64_t n_tok, int32_t n_seq, int32_t h_q, int32_t h_kv, int32_t head_dim,
+          int32_t max_blocks) {
+  if (!q || !k || !v || !cu) return fail(RUS_ERR_INVALID, "%s: null pointer argument", fn);
+  if (head_dim != kHD) return fail(RUS_ERR_UNSUPPORTED, "%s: head_dim %d (only 128)", fn, head_dim);
+  if (h_q <= 0 || h_kv <= 0 || h_q % h_kv)
+    return fail(RUS_ERR_INVALID, "%s: h_q=%d must be a multiple of h_kv=%d", fn, h_q, h_kv);
+  if (n_tok <= 0 || n_tok >= (int64_t(1) << 31) || n_seq <= 0 || max_blocks <= 0 ||
+      max_blocks > 65535)
+    return fail(RUS_ERR_INVALID, "%s: n_tok=%lld n_seq=%d max_blocks=%d", fn, (long long)n_tok,
+                n_seq, max_blocks);
+  if (!aligned(q, 16) || !aligned(k, 16) || !aligned(v, 16))
+    return fail(RUS_ERR_INVALID, "%s: q/k/v must be 16-byte aligned", fn);
+  return RUS_OK;
+}
+
+}  // namespace
+}  // namespace rus
+
+using rus::f16;
+
+extern "C" int rus_attn_varlen_fwd(const void* q, const void* k, const void* v,
+                                   const int32_t* cu_seqlens, int32_t n_seq, int64_t n_tokens,
+                                   int32_t max_blocks, int32_t h_q, int32_t h_kv,
+                                   int32_t head_dim, float scale, void* out, float* lse,
+                                   void* stream) {
+  using namespace rus;
+  const char* fn = "rus_attn_varlen_fwd";
+  if (int e = check(fn, q, k, v, cu_seqlens, n_tokens, n_seq, h_q, h_kv, head_dim, max_blocks))
+    return e;
+  if (!out || !lse || !aligned(out, 16)) return fail(RUS_ERR_INVALID, "%s: bad output", fn);
+  AttnArgs a{};
+  a.q = static_cast<const f16*>(q);
+  a.k = static_cast<const f16*>(k);
+  a.v = static_cast<const f16*>(v);
+  a.cu = cu_seqlens;
+  a.out = static_cast<f16*>(out);
+  a.lse = lse;
+  a.n_tok = n_tokens;
+  a.n_seq = n_seq;
+  a.h_q = h_q;
+  a.h_kv = h_kv;
+  a.scale = scale;
+  a.scale_log2 = scale * kLog2e;
+  hipLaunchKernelGGL(attn_fwd_kernel, dim3(h_q, max_blocks), dim3(64 * kW), 0,
+                     static_cast<hipStream_t>(stream), a);
+  return check_launch(fn);
+}
+
+extern "C" int rus_attn_varlen_bwd(const void* q, const void* k, const void* v, const void* out,
+                                   const void* dout, const float* lse,
+                                   const int32_t* cu_seqlens, int32_t n_seq, int64_t n_tokens,
+                                   int32_t max_blocks, int32_t h_q, int32_t h_kv,
+                                   int32_t head_dim, float scale, void* dq, void* dk, void* dv,
+                                   float* workspace, void* stream) {
+  using namespace rus;
+  const char* fn = "rus_attn_varlen_bwd";
+  if (int e = check(fn, q, k, v, cu_seqlens, n_tokens, n_seq, h_q, h_kv, head_dim, max_blocks))
+    return e;
+  if (!out || !dout || !lse || !dq || !dk || !dv || !workspace || !aligned(out, 16) ||
+      !aligned(dout, 16) || !aligned(dq, 16) || !aligned(dk, 16) || !aligned(dv, 16) ||
+      !aligned(workspace, 16))
+    return fail(RUS_ERR_INVALID, "%s: null or misaligned argument", fn);
+  AttnArgs a{};
+  a.q = static_cast<const f16*>(q);
+  a.k = static_cast<const f16*>(k);
+  a.v = static_cast<const f16*>(v);
+  a.o = static_cast<const f16*>(out);
+  a.dout = static_cast<const f16*>(dout);
+  a.cu = cu_seqlens;
+  a.lse = const_cast<float*>(lse);
+  a.n_tok = n_tokens;
+  a.n_seq = n_seq;
+  a.h_q = h_q;
+  a.h_kv = h_kv;
+  a.scale = scale;
+  a.scale_log2 = scale * kLog2e;
+  // workspace: dsum [h_q, n_tok] | dk_part [h_q, n_tok, 128] | dv_part [h_q, n_tok, 128]
+  a.dsum = workspace;
+  a.dk_part = workspace + ((static_cast<int64_t>(h_q) * n_tokens + 63) / 64) * 64;
+  a.dv_part = a.dk_part + static_cast<int64_t>(h_q) * n_tokens * kHD;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  a.out = static_cast<f16*>(dq);
+  hipLaunchKernelGGL(attn_bwd_dq_kernel, dim3(h_q, max_blocks), dim3(64 * kW), 0, st, a);
+  if (int e = check_launch(fn)) return e;
+  hipLaunchKernelGGL(attn_bwd_dkdv_kernel, dim3(h_q, max_blocks), dim3(64 * kW), 0, st, a);
+  if (int e = check_launch(fn)) return e;
+  const int64_t total = n_tokens * h_kv * (kHD / 8);
+  hipLaunchKernelGGL(attn_gqa_reduce_kernel, dim3(static_cast<unsigned>((total + 255) / 256)),
+                     dim3(256), 0, st, a.dk_part, a.dv_part, static_cast<f16*>(dk),
+                     static_cast<f16*>(dv), n_tokens, h_q, h_kv);
+  return check_launch(fn);
+}

@@ -90,8 +90,9 @@ class GraphedTrainStep:
             raise ValueError("GraphedTrainStep needs an HBM-resident lm_head (resident_head=True)")
         if engine.input_stream.offload:
             raise ValueError("GraphedTrainStep keeps layer inputs in HBM (offload_inputs=False)")
-        if engine.attention != "varlen":
-            raise ValueError("GraphedTrainStep needs attention='varlen'")
+        if engine.attention not in ("varlen", "varlen_aten"):
+            raise ValueError("GraphedTrainStep needs one launch over all packed rows "
+                             "(attention='varlen' or 'varlen_aten')")
         self.engine = engine
         self.bucket = int(bucket)
         self.training = training
@@ -113,7 +114,8 @@ class GraphedTrainStep:
             seed.add_(1)
         h = eng.host_head.embed(cap.ids)
         lora16 = eng.lora_fp16()
-        final, st = stack_forward(eng, h, cap.pos, None, self.training, lora16, seed, vm=cap.vm)
+        final, st = stack_forward(eng, h, cap.pos, None, self.training, lora16, seed, vm=cap.vm,
+                                  save=not eng.recompute)
         head = eng.host_head
         nll, _lse, ent, amax, _denom, d_final, loss = K.lm_head_ce(
             final, head.gpu_weight, cap.labels, num_items_in_batch=self.num_items,

@@ -9,6 +9,8 @@ raises ``RuntimeError``.
 
 from __future__ import annotations
 
+import math
+
 import torch
 
 from . import _lib
@@ -39,6 +41,8 @@ __all__ = [
     "lm_head_ce_grad_hidden",
     "lm_head_dh_reduce",
     "lm_head_weight_t",
+    "attn_varlen_fwd",
+    "attn_varlen_bwd",
 ]
 
 
@@ -957,6 +961,90 @@ def lm_head_dh_reduce(parts: torch.Tensor, scale: float, out_dtype=torch.float16
 def sum_splits(parts: torch.Tensor, out_dtype=torch.float16) -> torch.Tensor:
     """out_dtype(sum over the leading dimension of fp32 ``parts``): the reduce of a split-K GEMM."""
     return lm_head_dh_reduce(parts, 1.0, out_dtype, _tag="splitk_reduce")
+
+
+# ---------------------------------------------------------------------------------------------
+# Varlen causal GQA attention (reference: ops.py:669-696, torch SDPA per packed row)
+# ---------------------------------------------------------------------------------------------
+
+ATTN_HEAD_DIM = 128
+ATTN_BLOCK = 32
+
+
+def attn_max_blocks(n_tokens: int, n_rows: int) -> int:
+    """Upper bound of sum_i ceil(len_i / 32) over rows that cover n_tokens tokens."""
+    return -(-n_tokens // ATTN_BLOCK) + n_rows
+
+
+def _attn_operands(fn, q, k, v, cu):
+    _require_device(fn, q, k, v, cu)
+    if q.dim() != 3 or k.dim() != 3 or v.shape != k.shape or q.shape[0] != k.shape[0]:
+        raise ValueError(f"{fn}: q [N, h_q, 128], k/v [N, h_kv, 128] expected, got "
+                         f"{tuple(q.shape)}, {tuple(k.shape)}, {tuple(v.shape)}")
+    if q.shape[2] != ATTN_HEAD_DIM or k.shape[2] != ATTN_HEAD_DIM:
+        raise ValueError(f"{fn}: head_dim must be {ATTN_HEAD_DIM}")
+    if q.shape[1] % k.shape[1]:
+        raise ValueError(f"{fn}: h_q={q.shape[1]} is not a multiple of h_kv={k.shape[1]}")
+    for name, t in (("q", q), ("k", k), ("v", v)):
+        if t.dtype != torch.float16 or not t.is_contiguous():
+            raise ValueError(f"{fn}: {name} must be contiguous fp16")
+    if cu.dtype != torch.int32 or cu.dim() != 1 or cu.numel() < 2 or not cu.is_contiguous():
+        raise ValueError(f"{fn}: cu_seqlens must be a contiguous int32 [n_rows + 1] tensor")
+
+
+def _attn_flops(lens, hq):
+    # 2 products of 2 * L(L+1)/2 * 128 multiply-adds each per head (causal half).
+    return 0.0 if lens is None else float(sum(2 * L * (L + 1) * ATTN_HEAD_DIM * hq for L in lens))
+
+
+def attn_varlen_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cu_seqlens: torch.Tensor,
+                    max_blocks: int | None = None, scale: float | None = None, lens=None):
+    """(out [N, h_q, 128] fp16, lse [h_q, N] fp32): causal softmax(scale q k^T) v per packed row
+    [cu[i], cu[i+1]) with K/V head h // (h_q / h_kv); cu_seqlens (device int32) must cover all
+    N tokens. ``lens`` (host row lengths) only feeds the timer's FLOP count."""
+    fn = "attn_varlen_fwd"
+    _attn_operands(fn, q, k, v, cu_seqlens)
+    n, hq, d = q.shape
+    n_rows = cu_seqlens.numel() - 1
+    mb = attn_max_blocks(n, n_rows) if max_blocks is None else int(max_blocks)
+    scale = 1.0 / math.sqrt(d) if scale is None else float(scale)
+    out = torch.empty_like(q)
+    lse = torch.empty((hq, n), dtype=torch.float32, device=q.device)
+    nbytes = 2 * (q.numel() * 2 + k.numel() * 2) + lse.numel() * 4
+    _launch("attn_fwd", nbytes, _attn_flops(lens, hq), "rus_attn_varlen_fwd", q.data_ptr(),
+            k.data_ptr(), v.data_ptr(), cu_seqlens.data_ptr(), n_rows, n, mb, hq, k.shape[1], d,
+            scale, out.data_ptr(), lse.data_ptr(), _stream(q))
+    return out, lse
+
+
+def attn_varlen_bwd(dout: torch.Tensor, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                    out: torch.Tensor, lse: torch.Tensor, cu_seqlens: torch.Tensor,
+                    max_blocks: int | None = None, scale: float | None = None, lens=None):
+    """(dq, dk, dv) fp16 for ``attn_varlen_fwd``'s inputs, given its (out, lse); dk / dv sum the
+    query heads of each KV group in fp32 and are rounded once."""
+    fn = "attn_varlen_bwd"
+    _attn_operands(fn, q, k, v, cu_seqlens)
+    n, hq, d = q.shape
+    for name, t in (("dout", dout), ("out", out)):
+        if t.shape != q.shape or t.dtype != torch.float16 or not t.is_contiguous():
+            raise ValueError(f"{fn}: {name} must be contiguous fp16 like q")
+    if lse.shape != (hq, n) or lse.dtype != torch.float32 or not lse.is_contiguous():
+        raise ValueError(f"{fn}: lse must be contiguous fp32 [h_q, N]")
+    _require_device(fn, dout, out, lse)
+    n_rows = cu_seqlens.numel() - 1
+    mb = attn_max_blocks(n, n_rows) if max_blocks is None else int(max_blocks)
+    scale = 1.0 / math.sqrt(d) if scale is None else float(scale)
+    dq = torch.empty_like(q)
+    dk = torch.empty_like(k)
+    dv = torch.empty_like(v)
+    ws = torch.empty(_round_up(hq * n, 64) + 2 * hq * n * d, dtype=torch.float32,
+                     device=q.device)
+    nbytes = 2 * (4 * q.numel() + 4 * k.numel()) + 4 * 2 * hq * n * d * 2 + lse.numel() * 8
+    _launch("attn_bwd", nbytes, 2.5 * _attn_flops(lens, hq), "rus_attn_varlen_bwd",
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), dout.data_ptr(),
+            lse.data_ptr(), cu_seqlens.data_ptr(), n_rows, n, mb, hq, k.shape[1], d, scale,
+            dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), ws.data_ptr(), _stream(q))
+    return dq, dk, dv
 
 
 def lm_head_weight_t(weight: torch.Tensor) -> torch.Tensor:

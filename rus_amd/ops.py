@@ -20,6 +20,7 @@ from . import kernels as K
 from .hostload import MAX_MLP_TOKENS, V_CHUNK_DEFAULT, HostHead, InputStream, WeightStream
 
 PRESCALE_GRAD = 65536.0  # solution/ops.py:171: gradients of the loss are formed times 2^16
+ATTENTION_IMPLS = ("varlen", "varlen_aten", "sdpa_rows")
 
 
 # ---------------------------------------------------------------------------------------------
@@ -236,7 +237,7 @@ class Qwen2FusedEngine:
                  offload_inputs: bool = False, max_pos: int = 2048,
                  max_mlp_tokens: int = MAX_MLP_TOKENS, v_chunk: int = V_CHUNK_DEFAULT,
                  attention: str = "varlen", dropout_seed: int | None = None,
-                 stream_unit: str = "layer", lora_kernels: bool = True):
+                 stream_unit: str = "layer", lora_kernels: bool = True, recompute: bool = True):
         from .model import QLoRAQwen2
 
         if not isinstance(model, QLoRAQwen2):
@@ -269,10 +270,21 @@ class Qwen2FusedEngine:
              "p_v": cfg.lora_dropout} for _ in model.layers]
         self.cos_table, self.sin_table = rope_cache(max_pos, self.head_dim, cfg.rope_theta,
                                                     self.device)
-        if attention not in ("varlen", "sdpa_rows"):
-            raise ValueError("attention must be 'varlen' (one flash launch over all packed rows) "
+        if attention not in ATTENTION_IMPLS:
+            raise ValueError("attention must be 'varlen' (the gfx950 varlen kernels over all "
+                             "packed rows), 'varlen_aten' (torch's flash attention, one launch) "
                              "or 'sdpa_rows' (torch SDPA per row, as the reference)")
+        if attention == "varlen" and self.head_dim != K.ATTN_HEAD_DIM:
+            raise ValueError(f"attention='varlen' runs head_dim {K.ATTN_HEAD_DIM} only (got "
+                             f"{self.head_dim}); choose 'varlen_aten' or 'sdpa_rows'")
         self.attention = attention
+        # recompute=True re-forms every layer's activations in the backward from its saved input
+        # (the reference's memory-lean checkpointing); False keeps them from the forward (about
+        # 60 bytes per token and hidden unit per layer for Qwen2.5-1.5B shapes), so the backward
+        # skips three GEMMs, both norms, LoRA-down, RoPE and the attention forward per layer.
+        if not recompute and attention == "sdpa_rows":
+            raise ValueError("recompute=False needs attention='varlen' or 'varlen_aten'")
+        self.recompute = bool(recompute)
         self._flatten_lora()
         # The fused LoRA kernels (one launch for dropout + both A products, the B products inside
         # RoPE, two backward launches) cover ranks 4/8/16/32; other ranks use library GEMMs.
@@ -364,6 +376,7 @@ class VarlenMeta:
             cu.append(cu[-1] + L)
         self.cu = torch.tensor(cu, dtype=torch.int32, device=device)
         self.max_len = max(lens) if lens else 0
+        self.lens = lens  # host copy (FLOP counts of the kernel timer only)
 
     @classmethod
     def from_device(cls, cu: torch.Tensor, max_len: int) -> "VarlenMeta":
@@ -371,18 +384,25 @@ class VarlenMeta:
         vm = cls.__new__(cls)
         vm.cu = cu
         vm.max_len = int(max_len)
+        vm.lens = None
         return vm
 
 
-def _varlen_attn_fwd(q, k, v, vm: VarlenMeta):
-    """Causal GQA flash attention over all packed rows in one launch: q [N, Hq, D], k/v
-    [N, Hkv, D] (the RoPE kernel's output layout) -> (out [N, Hq, D], lse, rng, unused)."""
+def _varlen_attn_fwd(q, k, v, vm: VarlenMeta, impl: str = "varlen"):
+    """Causal GQA attention over all packed rows in one launch: q [N, Hq, D], k/v [N, Hkv, D]
+    (the RoPE kernel's output layout) -> (out [N, Hq, D], lse, rng, unused). ``impl`` "varlen"
+    runs the gfx950 kernels (rng / unused None), "varlen_aten" torch's flash attention."""
+    if impl == "varlen":
+        out, lse = K.attn_varlen_fwd(q, k, v, vm.cu, lens=vm.lens)
+        return out, lse, None, None
     out, lse, rng, unused, _ = torch.ops.aten._flash_attention_forward(
         q, k, v, vm.cu, vm.cu, vm.max_len, vm.max_len, 0.0, True, False)
     return out, lse, rng, unused
 
 
-def _varlen_attn_bwd(dout, q, k, v, out, lse, rng, unused, vm: VarlenMeta):
+def _varlen_attn_bwd(dout, q, k, v, out, lse, rng, unused, vm: VarlenMeta, impl: str = "varlen"):
+    if impl == "varlen":
+        return K.attn_varlen_bwd(dout, q, k, v, out, lse, vm.cu, lens=vm.lens)
     dq, dk, dv = torch.ops.aten._flash_attention_backward(
         dout, q, k, v, out, lse, vm.cu, vm.cu, vm.max_len, vm.max_len, 0.0, True, rng, unused)
     return dq, dk, dv
@@ -445,78 +465,108 @@ def _mm_split_k(a: torch.Tensor, b: torch.Tensor, splits: int = 4) -> torch.Tens
 
 class StackState:
     """What the stack's backward needs from its forward: final-norm input and rstd, positions,
-    attention metadata, the step's fp16 LoRA copies, the dropout seed tensor and whether it ran
-    in training mode (layer inputs live in the engine's InputStream)."""
+    attention metadata, the step's fp16 LoRA copies, the dropout seed tensor, whether it ran
+    in training mode, and (without recompute) each layer's saved activations (layer inputs live
+    in the engine's InputStream)."""
 
     __slots__ = ("pos_ids", "h_last", "final_rstd", "vm", "row_lengths", "lora16", "training",
-                 "seed", "buf")
+                 "seed", "buf", "saved")
 
     def __init__(self, **kw):
+        self.saved = None
         for k, v in kw.items():
             setattr(self, k, v)
 
 
-def stack_forward(engine, h_packed, pos_ids, row_lengths, training, lora16, seed, vm=None):
+def _layer_front(engine, l, norm1, w_qkv, lora16, training, seed, pos_ids, want_x):
+    """q/k/v projection, LoRA deltas and RoPE of layer ``l`` (solution/ops.py:768-790) ->
+    (q_rot, k_rot, v_out, lora) where lora = (mid_q, mid_v, x_q, x_v, drop): the rank-r
+    intermediates and the dropped LoRA inputs (norm1 itself without dropout; only formed when
+    ``want_x``), and the fused kernels' dropout arguments."""
+    cos, sin = engine.cos_table, engine.sin_table
+    hq, hkv, hd = engine.num_heads, engine.num_kv_heads, engine.head_dim
+    qkv = F.linear(norm1, w_qkv, engine.layer_biases[l])
+    meta = engine.layer_lora_meta[l]
+    qA, qB, vA, vB = lora16[4 * l: 4 * l + 4]
+    drop = None
+    if engine.fused_lora:  # dropout + A products in one launch, B products inside RoPE
+        drop = _lora_drop_args(l, meta, training, seed)
+        if want_x and drop[0] is not None:
+            mid_q, mid_v, x_q, x_v = K.lora_down_fwd(norm1, qA, vA, *drop, want_x=True)
+        else:
+            mid_q, mid_v = K.lora_down_fwd(norm1, qA, vA, *drop)
+            x_q = x_v = norm1
+        q_rot, k_rot, v_out = K.qkv_rope_fwd_mid(
+            qkv, mid_q, mid_v, qB, vB, cos, sin, pos_ids, meta["scale_q"], meta["scale_v"],
+            hq, hkv, hd)
+    else:
+        x_q, x_v = _lora_inputs(norm1, l, meta, training, seed)
+        mid_q, q_lora, mid_v, v_lora = _lora_deltas(x_q, x_v, qA, qB, vA, vB)
+        q_rot, k_rot, v_out = K.qkv_rope_fwd(qkv, cos, sin, pos_ids, q_lora=q_lora,
+                                             v_lora=v_lora, scale_q=meta["scale_q"],
+                                             scale_v=meta["scale_v"], h_q=hq, h_kv=hkv,
+                                             head_dim=hd)
+    return q_rot, k_rot, v_out, (mid_q, mid_v, x_q, x_v, drop)
+
+
+def stack_forward(engine, h_packed, pos_ids, row_lengths, training, lora16, seed, vm=None,
+                  save=False):
     """All decoder layers over packed tokens (solution/ops.py:736-830) -> (final_norm, state).
 
     No host synchronisation and no allocation outside torch's caching allocator, so it can run
     inside a captured HIP graph. Each layer's input residual add is fused into the RMSNorm kernel
     (h_{l+1} = h_mid + mlp is formed by the next layer's input norm) and the four weight segments
-    of a layer are dequantised in one launch."""
+    of a layer are dequantised in one launch. With ``save`` every layer keeps what its backward
+    reads (norm outputs and rstd, LoRA intermediates, rotated q/k/v, attention output and lse,
+    the [gate|up] pre-activation), so the backward recomputes nothing; the values are the ones
+    the recompute would produce, bit for bit."""
     ws, ins = engine.weight_stream, engine.input_stream
     L = engine.num_layers
-    cos, sin, eps = engine.cos_table, engine.sin_table, engine.rms_eps
+    eps = engine.rms_eps
     h = h_packed.contiguous()
     carry = None  # (h_mid, mlp_out) of the previous layer, added inside the next norm
     n_tok = h.shape[0]
     hq, hd = engine.num_heads, engine.head_dim
-    if vm is None and engine.attention == "varlen":
+    if vm is None and engine.attention != "sdpa_rows":
         vm = VarlenMeta(row_lengths, engine.device)
+    if save and vm is None:
+        raise ValueError("saving activations needs a varlen attention (one launch over all rows)")
+    saved = [] if save else None
     if L > 0:
         ws.prefetch(0)
     for l in range(L):
         if l + 1 < L:
             ws.prefetch(l + 1)
         if carry is None:
-            norm1, _, _ = K.rms_norm_fwd(h, engine.ln1_weights[l], eps=eps)
+            norm1, _, rstd1 = K.rms_norm_fwd(h, engine.ln1_weights[l], eps=eps)
         else:
-            norm1, h, _ = K.rms_norm_fwd(carry[1], engine.ln1_weights[l], eps=eps, residual=carry[0])
+            norm1, h, rstd1 = K.rms_norm_fwd(carry[1], engine.ln1_weights[l], eps=eps,
+                                             residual=carry[0])
         ins.save(l, h)
         ws.wait_slot(l)
         W = ws.dequant_layer(l)  # one launch for [q|k|v], o, [gate|up], down
         ws.release_slot(l)
-        qkv = F.linear(norm1, W["qkv"], engine.layer_biases[l])
-        meta = engine.layer_lora_meta[l]
-        qA, qB, vA, vB = lora16[4 * l: 4 * l + 4]
-        if engine.fused_lora:  # dropout + A products in one launch, B products inside RoPE
-            mid_q, mid_v = K.lora_down_fwd(norm1, qA, vA, *_lora_drop_args(l, meta, training, seed))
-            q_rot, k_rot, v_out = K.qkv_rope_fwd_mid(
-                qkv, mid_q, mid_v, qB, vB, cos, sin, pos_ids, meta["scale_q"], meta["scale_v"],
-                engine.num_heads, engine.num_kv_heads, engine.head_dim)
-            del mid_q, mid_v
-        else:
-            x_q, x_v = _lora_inputs(norm1, l, meta, training, seed)
-            _, q_lora, _, v_lora = _lora_deltas(x_q, x_v, qA, qB, vA, vB)
-            del x_q, x_v
-            q_rot, k_rot, v_out = K.qkv_rope_fwd(qkv, cos, sin, pos_ids, q_lora=q_lora,
-                                                 v_lora=v_lora, scale_q=meta["scale_q"],
-                                                 scale_v=meta["scale_v"], h_q=engine.num_heads,
-                                                 h_kv=engine.num_kv_heads,
-                                                 head_dim=engine.head_dim)
-            del q_lora, v_lora
-        del qkv, norm1
+        q_rot, k_rot, v_out, lora = _layer_front(engine, l, norm1, W["qkv"], lora16, training,
+                                                 seed, pos_ids, want_x=save)
         if vm is not None:
-            attn = _varlen_attn_fwd(q_rot, k_rot, v_out, vm)[0].view(n_tok, hq * hd)
+            attn, lse, rng, unused = _varlen_attn_fwd(q_rot, k_rot, v_out, vm, engine.attention)
+            attn = attn.view(n_tok, hq * hd)
         else:
             attn = _run_packed_sdpa(q_rot, k_rot, v_out, row_lengths, engine.num_heads,
                                     engine.num_kv_heads, engine.head_dim)
-        del q_rot, k_rot, v_out
         o_out = F.linear(attn, W["o"])
-        del attn
-        norm2, h_mid, _ = K.rms_norm_fwd(o_out, engine.ln2_weights[l], eps=eps, residual=h)
+        norm2, h_mid, rstd2 = K.rms_norm_fwd(o_out, engine.ln2_weights[l], eps=eps, residual=h)
         del o_out
-        mlp_out = _mlp_fwd(norm2, W["gu"], W["down"], engine.max_mlp_tokens)
-        del norm2, W
+        if save:
+            gu = F.linear(norm2, W["gu"])
+            mlp_out = F.linear(K.mlp_glu_fwd(gu), W["down"])
+            saved.append({"norm1": norm1, "rstd1": rstd1, "lora": lora, "q_rot": q_rot,
+                          "k_rot": k_rot, "v_out": v_out, "attn": attn, "lse": lse, "rng": rng,
+                          "unused": unused, "h_mid": h_mid, "rstd2": rstd2, "norm2": norm2,
+                          "gu": gu})
+        else:
+            mlp_out = _mlp_fwd(norm2, W["gu"], W["down"], engine.max_mlp_tokens)
+        del norm1, lora, q_rot, k_rot, v_out, attn, norm2, W
         carry = (h_mid, mlp_out)
     if carry is None:
         final_norm, h_last, final_rstd = K.rms_norm_fwd(h, engine.final_norm_weight, eps=eps)
@@ -525,14 +575,15 @@ def stack_forward(engine, h_packed, pos_ids, row_lengths, training, lora16, seed
                                                         eps=eps, residual=carry[0])
     st = StackState(pos_ids=pos_ids, h_last=h_last, final_rstd=final_rstd, vm=vm,
                     row_lengths=row_lengths, lora16=lora16, training=training, seed=seed,
-                    buf=ws.active if ws.unit == "model" else 0)
+                    buf=ws.active if ws.unit == "model" else 0, saved=saved)
     return final_norm, st
 
 
 def stack_backward(engine, st: StackState, d_final_norm, grad16) -> torch.Tensor:
-    """Recompute + manual backward of every layer (solution/ops.py:832-1009). Writes the fp16
-    LoRA gradients into ``grad16`` (flat, in the engine's parameter order) and returns the
-    gradient of the packed embedding output."""
+    """Manual backward of every layer (solution/ops.py:832-1009), recomputing each layer's
+    forward from its saved input as the reference does unless the forward saved its
+    activations. Writes the fp16 LoRA gradients into ``grad16`` (flat, in the engine's
+    parameter order) and returns the gradient of the packed embedding output."""
     ws, ins = engine.weight_stream, engine.input_stream
     L = engine.num_layers
     cos, sin, eps = engine.cos_table, engine.sin_table, engine.rms_eps
@@ -556,50 +607,49 @@ def stack_backward(engine, st: StackState, d_final_norm, grad16) -> torch.Tensor
         W = ws.dequant_layer(l)
         w_qkv, w_o, w_gu, w_down = W["qkv"], W["o"], W["gu"], W["down"]
         ws.release_slot(l)  # every read of the packed slot is enqueued
-
-        # Recompute the layer forward (same dropout masks: same seed and streams).
-        norm1, _, rstd1 = K.rms_norm_fwd(h_in, engine.ln1_weights[l], eps=eps)
-        qkv = F.linear(norm1, w_qkv, engine.layer_biases[l])
         meta = engine.layer_lora_meta[l]
         qA, qB, vA, vB = st.lora16[4 * l: 4 * l + 4]
         fused = engine.fused_lora
-        if fused:
-            drop = _lora_drop_args(l, meta, training, seed)
-            if drop[0] is not None:
-                mid_q, mid_v, x_q, x_v = K.lora_down_fwd(norm1, qA, vA, *drop, want_x=True)
+        gu = None
+        if st.saved is not None:
+            rec = st.saved[l]
+            st.saved[l] = None  # freed as the backward moves down the stack
+            norm1, rstd1 = rec["norm1"], rec["rstd1"]
+            mid_q, mid_v, x_q, x_v, drop = rec["lora"]
+            q_rot, k_rot, v_out = rec["q_rot"], rec["k_rot"], rec["v_out"]
+            attn2d = rec["attn"]
+            attn = attn2d.view(n_tokens, hq, hd)
+            lse, rng, unused = rec["lse"], rec["rng"], rec["unused"]
+            h_mid, rstd2, norm2, gu = rec["h_mid"], rec["rstd2"], rec["norm2"], rec["gu"]
+            del rec
+        else:
+            # Recompute the layer forward (same dropout masks: same seed and streams).
+            norm1, _, rstd1 = K.rms_norm_fwd(h_in, engine.ln1_weights[l], eps=eps)
+            q_rot, k_rot, v_out, lora = _layer_front(engine, l, norm1, w_qkv, st.lora16,
+                                                     training, seed, pos_ids, want_x=True)
+            mid_q, mid_v, x_q, x_v, drop = lora
+            del lora
+            if st.vm is not None:
+                attn, lse, rng, unused = _varlen_attn_fwd(q_rot, k_rot, v_out, st.vm,
+                                                          engine.attention)
+                attn2d = attn.view(n_tokens, q_dim)
             else:
-                mid_q, mid_v = K.lora_down_fwd(norm1, qA, vA)
-                x_q = x_v = norm1
-            q_rot, k_rot, v_out = K.qkv_rope_fwd_mid(
-                qkv, mid_q, mid_v, qB, vB, cos, sin, pos_ids, meta["scale_q"], meta["scale_v"],
-                hq, hkv, hd)
-        else:
-            x_q, x_v = _lora_inputs(norm1, l, meta, training, seed)
-            mid_q, q_lora, mid_v, v_lora = _lora_deltas(x_q, x_v, qA, qB, vA, vB)
-            q_rot, k_rot, v_out = K.qkv_rope_fwd(qkv, cos, sin, pos_ids, q_lora=q_lora,
-                                                 v_lora=v_lora, scale_q=meta["scale_q"],
-                                                 scale_v=meta["scale_v"], h_q=hq, h_kv=hkv,
-                                                 head_dim=hd)
-            del q_lora, v_lora
-        del qkv
-        if st.vm is not None:
-            attn, lse, rng, unused = _varlen_attn_fwd(q_rot, k_rot, v_out, st.vm)
-            attn2d = attn.view(n_tokens, q_dim)
-        else:
-            with torch.enable_grad():
-                q_req = q_rot.detach().requires_grad_(True)
-                k_req = k_rot.detach().requires_grad_(True)
-                v_req = v_out.detach().requires_grad_(True)
-                attn = _run_packed_sdpa(q_req, k_req, v_req, st.row_lengths, hq, hkv, hd)
-            attn2d = attn.detach()
-        o_out = F.linear(attn2d, w_o)
-        norm2, h_mid, rstd2 = K.rms_norm_fwd(o_out, engine.ln2_weights[l], eps=eps, residual=h_in)
-        del o_out
+                with torch.enable_grad():
+                    q_req = q_rot.detach().requires_grad_(True)
+                    k_req = k_rot.detach().requires_grad_(True)
+                    v_req = v_out.detach().requires_grad_(True)
+                    attn = _run_packed_sdpa(q_req, k_req, v_req, st.row_lengths, hq, hkv, hd)
+                attn2d = attn.detach()
+            o_out = F.linear(attn2d, w_o)
+            norm2, h_mid, rstd2 = K.rms_norm_fwd(o_out, engine.ln2_weights[l], eps=eps,
+                                                 residual=h_in)
+            del o_out
 
         # MLP backward: d_act = dh . W_down; SwiGLU backward in place over gu; d_norm2.
         step = min(engine.max_mlp_tokens, n_tokens)
-        if step >= n_tokens:
-            gu = F.linear(norm2, w_gu)
+        if gu is not None or step >= n_tokens:
+            if gu is None:
+                gu = F.linear(norm2, w_gu)
             K.mlp_glu_bwd(torch.mm(dh, w_down), gu)
             d_norm2 = _mm_split_k(gu, w_gu)
             del gu
@@ -619,7 +669,7 @@ def stack_backward(engine, st: StackState, d_final_norm, grad16) -> torch.Tensor
         d_attn = torch.mm(dh_mid, w_o)
         if st.vm is not None:
             dq, dk, dv = _varlen_attn_bwd(d_attn.view(n_tokens, hq, hd), q_rot, k_rot, v_out,
-                                          attn, lse, rng, unused, st.vm)
+                                          attn, lse, rng, unused, st.vm, engine.attention)
             del lse, rng, unused
         else:
             dq, dk, dv = torch.autograd.grad(attn, (q_req, k_req, v_req), d_attn)
@@ -663,8 +713,9 @@ def stack_backward(engine, st: StackState, d_final_norm, grad16) -> torch.Tensor
 
 class FusedQwen2StackFn(torch.autograd.Function):
     """All decoder layers on packed tokens with layer-input checkpointing and recompute in
-    backward (solution/ops.py:729-1009). Returns the final-norm hidden states; the gradient flows
-    to the LoRA parameters only.
+    backward (solution/ops.py:729-1009); with the engine's ``recompute=False`` the forward keeps
+    every layer's activations instead (same values, no recompute). Returns the final-norm hidden
+    states; the gradient flows to the LoRA parameters only.
 
     LoRA dropout masks come from a counter-based generator keyed by a per-forward seed (a device
     tensor drawn from the engine), so the recompute draws the same masks without saving or
@@ -676,8 +727,9 @@ class FusedQwen2StackFn(torch.autograd.Function):
         lora16 = engine.lora_fp16()
         ws = engine.weight_stream
         buf = ws.begin_step()
+        save = not engine.recompute and any(ctx.needs_input_grad[5:])
         final_norm, st = stack_forward(engine, h_packed, pos_ids, row_lengths, training, lora16,
-                                       seed)
+                                       seed, save=save)
         ws.end_step(buf)  # released again after the backward
         ctx.save_for_backward(*lora_params)
         ctx.st = st

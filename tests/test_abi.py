@@ -67,6 +67,15 @@ def test_header_compiles_as_c():
         ("rus_swiglu_fwd", (16, 16, 16, 4, 100, 50, 100, 100, 0, None), "stride"),
         ("rus_swiglu_bwd", (16, 16, 16, 16, 16, 1 << 20, 1 << 12, 1 << 12, 1 << 12, 1 << 12,
                             1 << 12, 1 << 12, 0, None), "2\\^31"),
+        # attention: head_dim other than 128, GQA ratio not integral, misaligned output
+        ("rus_attn_varlen_fwd", (16, 16, 16, 16, 1, 32, 2, 12, 2, 64, 0.1, 16, 16, None),
+         "head_dim"),
+        ("rus_attn_varlen_fwd", (16, 16, 16, 16, 1, 32, 2, 12, 5, 128, 0.1, 16, 16, None),
+         "multiple"),
+        ("rus_attn_varlen_fwd", (16, 16, 16, 16, 1, 32, 2, 12, 2, 128, 0.1, 18, 16, None),
+         "output"),
+        ("rus_attn_varlen_bwd", (16, 16, 16, 16, 16, 16, 16, 1, 32, 2, 12, 2, 128, 0.1, 16, 16,
+                                 16, None, None), "misaligned"),
     ],
 )
 def test_invalid_arguments_are_rejected_on_the_host(name, args, msg):

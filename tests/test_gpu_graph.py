@@ -25,7 +25,7 @@ DEV = "cuda"
 
 
 def small_config(layers=2, dropout=0.0):
-    return M.Qwen2Config(hidden_size=128, intermediate_size=256, num_hidden_layers=layers,
+    return M.Qwen2Config(hidden_size=512, intermediate_size=256, num_hidden_layers=layers,
                          num_attention_heads=4, num_key_value_heads=2, vocab_size=1000,
                          lora_r=4, lora_alpha=8.0, lora_dropout=dropout)
 
@@ -144,3 +144,29 @@ def test_graph_replays_repeatable_across_buckets(unit):
         torch.cuda.synchronize()
         for g0, g1 in zip(ref_grads, _grads(eng_r)):
             assert torch.equal(g0, g1)
+
+
+def test_graph_saved_activations_match_recompute_bitwise():
+    # The captured step with activations kept from the forward gives the recompute's bits,
+    # dropout included, on two buckets and repeated replays.
+    cfg = small_config(dropout=0.1)
+    model = M.build_random_qlora_qwen2(cfg, DEV, seed=6, std=0.05)
+    a = _batch(cfg, [30, 50], seed=1)
+    b = _batch(cfg, [90, 70, 12], seed=2)
+    res = []
+    for recompute in (True, False):
+        engine = ops.Qwen2FusedEngine(model, DEV, resident_weights=False, stream_unit="model",
+                                      dropout_seed=77, recompute=recompute)
+        gs = GraphedTrainStep(engine, bucket=64, training=True)
+        out = []
+        for batch in (a, b, a):
+            out.append(float(gs.step(*batch)))
+            torch.cuda.synchronize()
+            out.append(_grads(engine))
+        res.append(out)
+    for x, y in zip(*res):
+        if isinstance(x, float):
+            assert x == y
+        else:
+            for g0, g1 in zip(x, y):
+                assert torch.equal(g0, g1)

@@ -24,7 +24,7 @@ DEV = "cuda"
 
 
 def small_config(layers=2, dropout=0.0):
-    return M.Qwen2Config(hidden_size=128, intermediate_size=256, num_hidden_layers=layers,
+    return M.Qwen2Config(hidden_size=512, intermediate_size=256, num_hidden_layers=layers,
                          num_attention_heads=4, num_key_value_heads=2, vocab_size=1000,
                          lora_r=4, lora_alpha=8.0, lora_dropout=dropout)
 
@@ -59,6 +59,7 @@ def _rel(a, b):
 
 
 @pytest.mark.parametrize("resident,attention", [(False, "varlen"), (True, "varlen"),
+                                                (True, "varlen_aten"),
                                                 (True, "sdpa_rows")])
 def test_fused_stack_matches_cpu_oracle(resident, attention):
     cfg = small_config()
@@ -161,3 +162,26 @@ def test_fused_lora_kernels_match_library_gemm_path():
     assert abs(float(out[0][0]) - float(out[1][0])) <= 1e-3 * abs(float(out[1][0]))
     for gi, (a, b) in enumerate(zip(out[0][1], out[1][1])):
         assert _rel(a, b) <= 5e-3, (gi, _rel(a, b))
+
+
+@pytest.mark.parametrize("dropout,lora_kernels", [(0.0, True), (0.1, True), (0.1, False)])
+def test_saved_activations_match_recompute_bitwise(dropout, lora_kernels):
+    cfg = small_config(dropout=dropout)
+    model = M.build_random_qlora_qwen2(cfg, DEV, seed=4, std=0.05)
+    ids, mask, labels = _batch(cfg, [45, 70, 12], seed=3)
+    pb = ops.pack_varlen(ids, mask, labels)
+    out = []
+    for recompute in (True, False):
+        engine = ops.Qwen2FusedEngine(model, DEV, resident_weights=True, dropout_seed=123,
+                                      lora_kernels=lora_kernels, recompute=recompute)
+        out.append(_fused_step(engine, pb, training=True))
+    assert torch.equal(out[0][0], out[1][0])
+    for a, b in zip(out[0][1], out[1][1]):
+        assert torch.equal(a, b)
+
+
+def test_recompute_off_needs_varlen_attention():
+    cfg = small_config()
+    model = M.build_random_qlora_qwen2(cfg, DEV, seed=4, std=0.05)
+    with pytest.raises(ValueError, match="recompute=False"):
+        ops.Qwen2FusedEngine(model, DEV, attention="sdpa_rows", recompute=False)

@@ -446,3 +446,66 @@ def test_ce_tie_takes_first_index():
     w[17] = 1  # equal logits at 3 and 17 (17 is in a later chunk)
     out = ref.lm_head_ce(h, w, torch.tensor([3, -100]), v_chunk=8, need_grad=False)
     assert out["argmax"].tolist() == [3, 3]
+
+
+# ---------------------------------------------------------------------------------------------
+# Varlen causal GQA attention
+# ---------------------------------------------------------------------------------------------
+
+
+def _attn_inputs(lens, hq=4, hkv=2, d=16, seed=0, dtype=torch.float64):
+    g = torch.Generator().manual_seed(seed)
+    n = sum(lens)
+    q = torch.randn(n, hq, d, generator=g, dtype=dtype)
+    k = torch.randn(n, hkv, d, generator=g, dtype=dtype)
+    v = torch.randn(n, hkv, d, generator=g, dtype=dtype)
+    cu = [0]
+    for L in lens:
+        cu.append(cu[-1] + L)
+    return q, k, v, cu
+
+
+def test_attention_matches_sdpa_per_row():
+    # The reference's own routine: torch SDPA per row with K/V expanded to the query heads.
+    q, k, v, cu = _attn_inputs([5, 1, 12, 7], hq=6, hkv=2, d=32, dtype=torch.float32)
+    out, _ = ref.attention_varlen_fwd(q, k, v, cu)
+    for a, e in zip(cu[:-1], cu[1:]):
+        L = e - a
+        kb = k[a:e].transpose(0, 1).unsqueeze(1).expand(2, 3, L, 32).reshape(6, L, 32)
+        vb = v[a:e].transpose(0, 1).unsqueeze(1).expand(2, 3, L, 32).reshape(6, L, 32)
+        sd = F.scaled_dot_product_attention(q[a:e].transpose(0, 1)[None], kb[None], vb[None],
+                                            is_causal=True)[0].transpose(0, 1)
+        torch.testing.assert_close(out[a:e].float(), sd, rtol=1e-5, atol=1e-6)
+
+
+def test_attention_closed_forms():
+    # q = 0: every allowed key scores 0, so out is the causal running mean of v and
+    # lse = log(#keys); a row of length 1 returns its own v.
+    q, k, v, cu = _attn_inputs([9, 1, 4])
+    out, lse = ref.attention_varlen_fwd(torch.zeros_like(q), k, v, cu)
+    for a, e in zip(cu[:-1], cu[1:]):
+        for t in range(a, e):
+            mean = v[a:t + 1].mean(0).repeat_interleave(2, dim=0)
+            torch.testing.assert_close(out[t], mean, rtol=1e-12, atol=1e-12)
+            torch.testing.assert_close(lse[:, t], torch.full((4,), math.log(t - a + 1),
+                                                             dtype=torch.float64))
+    out1, _ = ref.attention_varlen_fwd(q, k, v, cu)
+    torch.testing.assert_close(out1[9], v[9].repeat_interleave(2, dim=0))
+    # lse = log sum_j exp(scale q.k_j) over j <= t, brute force for one element.
+    _, lse = ref.attention_varlen_fwd(q, k, v, cu)
+    t, h = 12, 3
+    s = [math.exp((q[t, h] @ k[j, h // 2]).item() / 4.0) for j in range(10, t + 1)]
+    assert abs(lse[h, t].item() - math.log(sum(s))) < 1e-12
+
+
+def test_attention_bwd_matches_float64_autograd():
+    q, k, v, cu = _attn_inputs([7, 3, 11], hq=6, hkv=2, d=8, seed=3)
+    q.requires_grad_(True)
+    k.requires_grad_(True)
+    v.requires_grad_(True)
+    out, _ = ref.attention_varlen_fwd(q, k, v, cu)
+    dout = torch.randn_like(out)
+    gq, gk, gv = torch.autograd.grad(out, (q, k, v), dout)
+    dq, dk, dv = ref.attention_varlen_bwd(dout, q.detach(), k.detach(), v.detach(), cu)
+    for a, b in ((dq, gq), (dk, gk), (dv, gv)):
+        torch.testing.assert_close(a, b, rtol=1e-10, atol=1e-12)
