@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define RUS_ABI_VERSION 1
+#define RUS_ABI_VERSION 2
 
 #define RUS_DTYPE_F16 0
 #define RUS_DTYPE_F32 1
@@ -186,19 +186,31 @@ int rus_lora_dropout_bwd_add(void* acc, const void* grad_a, const void* grad_b, 
                              uint64_t stream_b, float p_a, float p_b, int32_t dtype, void* stream);
 
 /*
+ * Packed dropout keep bits of n_streams masks [n_rows, n_cols] (n_cols % 8 == 0), the masks of
+ * rus_lora_dropout_fwd for streams stream0 .. stream0 + n_streams - 1: bits is uint32
+ * [n_streams, n_rows, ceil(n_cols / 32)], bit i of word w of row t of stream s set when element
+ * (t, 32 w + i) is kept (0 past the row's end); stream s uses p_even when s is even, else p_odd
+ * (so streams 2l / 2l + 1 are the q / v branch of layer l). *seed is read on the device.
+ * Replaces: the generator state the reference saves and replays for the LoRA dropouts
+ * (solution/ops.py:775-777, 868-869, 882-886, 986-992): all layers' masks of a step in one launch.
+ */
+int rus_dropout_keep_bits(const uint64_t* seed, uint64_t stream0, int32_t n_streams,
+                          int64_t n_rows, int64_t n_cols, float p_even, float p_odd,
+                          uint32_t* bits, void* stream);
+
+/*
  * Rank-r LoRA down projections of both branches, fp16 (r in {4, 8, 16, 32}):
  *   mid_q = fp16(x_q A_q^T), mid_v = fp16(x_v A_v^T)   x [n_tokens, d] (row stride stride_x),
  *   A [r, d] row-major, mid [n_tokens, r] contiguous,
- * with x_q = dropout(x; stream_q, p_q), x_v = dropout(x; stream_v, p_v) (the masks of
- * rus_lora_dropout_fwd) when seed is not NULL, else x_q = x_v = x. With x_q_out / x_v_out (both,
- * [n_tokens, d] contiguous, seed required) the dropped rows are also written.
+ * x_q = keep_q ? fp16(x / (1 - p_q)) : 0 with the keep bits bits_q [n_tokens, ceil(d / 32)] of
+ * rus_dropout_keep_bits (NULL: x_q = x), x_v likewise.
  * Replaces: the dropouts and the first F.linear of each branch, solution/ops.py:775-778 and the
- * recompute ops.py:882-888. d % 8 == 0, stride_x % 8 == 0, x / A / x outputs 16-byte aligned.
+ * recompute ops.py:882-888. d % 16 == 0, stride_x % 8 == 0, x and A 16-byte aligned.
  */
 int rus_lora_down_fwd(const void* x, int64_t n_tokens, int64_t d, int64_t stride_x,
                       const void* a_q, const void* a_v, int32_t r, void* mid_q, void* mid_v,
-                      void* x_q_out, void* x_v_out, const uint64_t* seed, uint64_t stream_q,
-                      uint64_t stream_v, float p_q, float p_v, void* stream);
+                      const uint32_t* bits_q, const uint32_t* bits_v, float p_q, float p_v,
+                      void* stream);
 
 /*
  * rus_qkv_lora_rope_fwd with the LoRA deltas formed in-kernel from the rank-r factors (fp16):
@@ -218,28 +230,32 @@ int rus_qkv_lora_rope_fwd_mid(const void* qkv, const void* mid_q, const void* mi
 /*
  * LoRA backward into the input gradient, fp16, in place on dx [n_tokens, d] (row stride
  * stride_dx):
- *   d_mid_q = fp16(dq_lora b_q)  [n_tokens, r]    (dq_lora [n_tokens, d_q] contiguous, b_q [d_q, r])
- *   d_mid_v = fp16(dv_lora b_v)
- *   dx = fp16(fp16(dx + fp16 drop_q(fp16(d_mid_q a_q))) + fp16 drop_v(fp16(d_mid_v a_v)))
- * with the forward's masks (seed NULL: no dropout). d_mid_q / d_mid_v are written for
+ *   d_mid_q = fp16(dq_lora B_q)  [n_tokens, r]    (dq_lora [n_tokens, d_q] contiguous)
+ *   d_mid_v = fp16(dv_lora B_v)
+ *   dx = fp16(fp16(dx + fp16 drop_q(fp16(d_mid_q A_q))) + fp16 drop_v(fp16(d_mid_v A_v)))
+ * with the forward's keep bits (NULL: no dropout on that branch). The factors come rank-major:
+ * a_t_q = A_q^T [d, r], b_t_q = B_q^T [r, d_q] (v alike). d_mid_q / d_mid_v are written for
  * rus_lora_bwd_w. Replaces: solution/ops.py:976-978, 980-982 (d_mid and dx_drop products) and
  * 986-992 (mask replay, two F.dropout, d_norm1.add_(dx_q).add_(dx_v)).
+ * d % 32 == 0, d_q % 16 == 0, d_v % 16 == 0, stride_dx % 4 == 0.
  */
 int rus_lora_bwd_x(const void* dq_lora, const void* dv_lora, int64_t n_tokens, int64_t d_q,
-                   int64_t d_v, const void* a_q, const void* a_v, const void* b_q,
-                   const void* b_v, int32_t r, int64_t d, void* d_mid_q, void* d_mid_v, void* dx,
-                   int64_t stride_dx, const uint64_t* seed, uint64_t stream_q, uint64_t stream_v,
+                   int64_t d_v, const void* a_t_q, const void* a_t_v, const void* b_t_q,
+                   const void* b_t_v, int32_t r, int64_t d, void* d_mid_q, void* d_mid_v,
+                   void* dx, int64_t stride_dx, const uint32_t* bits_q, const uint32_t* bits_v,
                    float p_q, float p_v, void* stream);
 
 /*
  * LoRA weight gradients, fp16 (each an fp32 sum over tokens in a fixed order, rounded once):
  *   g_a_q [r, d]   = d_mid_q^T x_q      g_b_q [d_q, r] = dq_lora^T mid_q
  *   g_a_v [r, d]   = d_mid_v^T x_v      g_b_v [d_v, r] = dv_lora^T mid_v
- * x_q / x_v: the dropped LoRA inputs [n_tokens, d] (row stride stride_x); the [n_tokens, r]
- * operands contiguous and 8-byte aligned. Replaces: solution/ops.py:975, 977, 979, 981
- * (d_qB, d_qA, d_vB, d_vA as torch.mm in fp16).
+ * x_q / x_v: the dropped LoRA inputs, formed from x [n_tokens, d] (row stride stride_x) and the
+ * forward's keep bits as in rus_lora_down_fwd; the [n_tokens, r] operands contiguous and 8-byte
+ * aligned. Replaces: solution/ops.py:975, 977, 979, 981 (d_qB, d_qA, d_vB, d_vA as torch.mm in
+ * fp16).
  */
-int rus_lora_bwd_w(const void* x_q, const void* x_v, int64_t stride_x, const void* dq_lora,
+int rus_lora_bwd_w(const void* x, int64_t stride_x, const uint32_t* bits_q,
+                   const uint32_t* bits_v, float p_q, float p_v, const void* dq_lora,
                    const void* dv_lora, const void* mid_q, const void* mid_v,
                    const void* d_mid_q, const void* d_mid_v, int64_t n_tokens, int64_t d,
                    int64_t d_q, int64_t d_v, int32_t r, void* g_a_q, void* g_b_q, void* g_a_v,

@@ -272,6 +272,18 @@ def dropout_keep_mask(seed: int, stream: int, n_rows: int, n_cols: int, p: float
     return (words.reshape(-1)[:n] >= np.uint64(thresh)).reshape(n_rows, n_cols)
 
 
+def dropout_keep_bits(seed: int, stream: int, n_rows: int, n_cols: int, p: float) -> np.ndarray:
+    """The mask of ``dropout_keep_mask`` packed as int32 [n_rows, ceil(n_cols / 32)]: bit i of
+    word w of a row is element 32 w + i of that row (0 past its end), the layout the fused LoRA
+    kernels read (one launch per step forms every layer's masks in it)."""
+    keep = dropout_keep_mask(seed, stream, n_rows, n_cols, p)
+    words = (n_cols + 31) // 32
+    padded = np.zeros((n_rows, words * 32), dtype=np.uint64)
+    padded[:, :n_cols] = keep
+    packed = (padded.reshape(n_rows, words, 32) << np.arange(32, dtype=np.uint64)).sum(-1)
+    return packed.astype(np.uint32).view(np.int32)
+
+
 def _drop(x: torch.Tensor, keep: np.ndarray, p: float) -> torch.Tensor:
     scale = torch.tensor(1.0, dtype=torch.float32) / (1.0 - torch.tensor(p, dtype=torch.float32))
     y = torch.where(torch.from_numpy(keep), x.float() * scale, torch.zeros((), dtype=torch.float32))

@@ -150,6 +150,40 @@ __global__ __launch_bounds__(kThreads) void dropout_bwd_add_kernel(T* __restrict
   }
 }
 
+// Packed keep bits of n_streams masks [n_rows, n_cols] (n_cols % 8 == 0): word w of row t of
+// stream s (stream0 + s) holds elements 32 w .. 32 w + 31 of that row, bit i for element 32 w + i
+// (0 past the row's end), thresholds alternating thresh_even / thresh_odd with s. One word (four
+// Philox blocks) per thread.
+struct BitsShape {
+  uint64_t stream0;
+  int64_t n_streams, n_rows, n_cols, words, total;
+  uint32_t thresh_even, thresh_odd;
+};
+
+__global__ __launch_bounds__(kThreads) void keep_bits_kernel(const uint64_t* __restrict__ seed_p,
+                                                             uint32_t* __restrict__ out,
+                                                             BitsShape s) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if (i >= s.total) return;
+  const int64_t w = i % s.words;
+  const int64_t rs = i / s.words;
+  const int64_t t = rs % s.n_rows;
+  const int64_t st = rs / s.n_rows;
+  const uint64_t seed = *seed_p;
+  const uint32_t thresh = (st & 1) ? s.thresh_odd : s.thresh_even;
+  const int64_t chunks = s.n_cols / 8;  // Philox blocks per row
+  uint32_t word = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int64_t c = 4 * w + j;  // block within the row
+    if (c < chunks)
+      word |= keep_bits(seed, s.stream0 + static_cast<uint64_t>(st),
+                        static_cast<uint64_t>(t * chunks + c), thresh)
+              << (8 * j);
+  }
+  out[i] = word;
+}
+
 uint32_t threshold(float p) {
   const double t = static_cast<double>(p) * 4294967296.0 + 0.5;
   return t >= 4294967295.0 ? 0xffffffffu : static_cast<uint32_t>(t);
@@ -239,5 +273,33 @@ extern "C" int rus_lora_dropout_bwd_add(void* acc, const void* grad_a, const voi
     hipLaunchKernelGGL(dropout_bwd_add_kernel<float>, grid, dim3(kThreads), 0, st,
                        static_cast<float*>(acc), static_cast<const float*>(grad_a),
                        static_cast<const float*>(grad_b), seed, s);
+  return check_launch(fn);
+}
+
+extern "C" int rus_dropout_keep_bits(const uint64_t* seed, uint64_t stream0, int32_t n_streams,
+                                     int64_t n_rows, int64_t n_cols, float p_even, float p_odd,
+                                     uint32_t* bits, void* stream) {
+  using namespace rus;
+  const char* fn = "rus_dropout_keep_bits";
+  if (!seed || !bits) return fail(RUS_ERR_INVALID, "%s: null pointer argument", fn);
+  if (n_streams <= 0 || n_rows < 0 || n_cols <= 0 || n_cols % 8)
+    return fail(RUS_ERR_INVALID, "%s: need n_streams > 0, n_rows >= 0, n_cols > 0 and a multiple "
+                "of 8", fn);
+  if (!(p_even >= 0.0f && p_even < 1.0f && p_odd >= 0.0f && p_odd < 1.0f))
+    return fail(RUS_ERR_INVALID, "%s: dropout probabilities must be in [0, 1)", fn);
+  BitsShape s;
+  s.stream0 = stream0;
+  s.n_streams = n_streams;
+  s.n_rows = n_rows;
+  s.n_cols = n_cols;
+  s.words = (n_cols + 31) / 32;
+  s.total = s.n_streams * n_rows * s.words;
+  s.thresh_even = threshold(p_even);
+  s.thresh_odd = threshold(p_odd);
+  if (s.total == 0) return RUS_OK;
+  if (s.total / kThreads >= (int64_t(1) << 31))
+    return fail(RUS_ERR_UNSUPPORTED, "%s: too many words", fn);
+  hipLaunchKernelGGL(keep_bits_kernel, dim3(static_cast<uint32_t>((s.total + kThreads - 1) / kThreads)),
+                     dim3(kThreads), 0, static_cast<hipStream_t>(stream), seed, bits, s);
   return check_launch(fn);
 }

@@ -40,6 +40,7 @@ __constant__ float kNF4[16] = {
 };
 
 constexpr int kThreads = 256;
+constexpr int kUnrollTab = 4;  // 4-byte units per thread on the table path
 
 struct Nf4Args {
   const uint32_t* packed;  // packed codes viewed as 32-bit units
@@ -54,6 +55,7 @@ struct Nf4Args {
   uint32_t sbase1, sbase2;  // first absmax2 entry of segment 1 / 2
   uint32_t n_units;         // complete 4-byte units
   uint32_t n_bytes;
+  int wide;                 // table path (blocksize >= 32)
   int hb_shift;  // log2(blocksize / 2): bytes per absmax block
   int sb_shift;  // log2(super_blocksize): absmax blocks per absmax2 entry
 };
@@ -152,6 +154,78 @@ __device__ __forceinline__ void dequant_block(const Nf4Args& a, uint32_t blk, ui
   }
 }
 
+// Table path (blocksize >= 32): a block's 4 KiB of packed bytes span at most 128 absmax blocks;
+// their 16 products NF4[i] * scale (the fp32 values the reference rounds to fp16) are formed
+// once in LDS, so each output is one LDS read and one conversion, with no global scale loads in
+// the streaming loop. Same coalesced 4-byte loads / 16-byte stores as dequant_block.
+constexpr int kTabMaxBlocks = kThreads * kUnrollTab * 4 / 16;  // 4 KiB / (blocksize/2 >= 16)
+
+template <int UNROLL>
+__device__ __forceinline__ void dequant_block_tab(const Nf4Args& a, uint32_t blk, uint32_t nblk,
+                                                  float* __restrict__ s_code2,
+                                                  float* __restrict__ s_nf4,
+                                                  float* __restrict__ s_scale,
+                                                  float* __restrict__ s_tab) {
+  static_assert(UNROLL == kUnrollTab, "table sized for kUnrollTab units per thread");
+  const uint32_t t = threadIdx.x;
+  const uint32_t base = blk * (kThreads * UNROLL) + t;
+  // 1. The block's packed words, issued before the table set-up so that their latency overlaps it.
+  uint32_t p[UNROLL];
+#pragma unroll
+  for (int u = 0; u < UNROLL; ++u) {
+    const uint32_t idx = base + u * kThreads;
+    p[u] = idx < a.n_units ? a.packed[idx] : 0u;
+  }
+  const uint32_t byte0 = blk * (kThreads * UNROLL * 4u);
+  // The last block also covers the (< 4) bytes past the last whole unit: one more absmax block
+  // at most, hence the table's spare row.
+  const uint32_t byte_end =
+      blk == nblk - 1 ? a.n_bytes : min(byte0 + kThreads * UNROLL * 4u, a.n_bytes);
+  const uint32_t ab0 = byte0 >> a.hb_shift;
+  const uint32_t n_ab = ((byte_end - 1u) >> a.hb_shift) - ab0 + 1u;
+  // 2. Lookup tables, then one scale per absmax block of the block's range.
+  s_code2[t] = a.code2[t];
+  if (t < 16) s_nf4[t] = kNF4[t];
+  __syncthreads();
+  for (uint32_t i = t; i < n_ab; i += kThreads)
+    s_scale[i] = block_scale(a, (ab0 + i) << a.hb_shift, s_code2);
+  __syncthreads();
+  // 3. The 16 products per absmax block.
+  for (uint32_t e = t; e < n_ab * 16u; e += kThreads)
+    s_tab[e] = s_nf4[e & 15u] * s_scale[e >> 4];  // rounded product (no contraction here)
+  __syncthreads();
+#pragma unroll
+  for (int u = 0; u < UNROLL; ++u) {
+    const uint32_t idx = base + u * kThreads;
+    if (idx < a.n_units) {
+      const float* row = s_tab + (((idx * 4u) >> a.hb_shift) - ab0) * 16u;
+      uint4 w;
+      uint32_t* ww = reinterpret_cast<uint32_t*>(&w);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const uint32_t b = (p[u] >> (8 * k)) & 0xffu;
+        h2 r;
+        r.x = static_cast<_Float16>(row[b >> 4]);
+        r.y = static_cast<_Float16>(row[b & 15u]);
+        ww[k] = __builtin_bit_cast(uint32_t, r);
+      }
+      reinterpret_cast<uint4*>(a.out)[idx] = w;
+    }
+  }
+  // Trailing bytes past the last 4-byte unit (n_bytes % 4 != 0): the last block does them.
+  if (blk == nblk - 1) {
+    const uint32_t byte = a.n_units * 4u + t;
+    if (byte < a.n_bytes) {
+      const float* row = s_tab + ((byte >> a.hb_shift) - ab0) * 16u;
+      const uint32_t b = a.packed_bytes[byte];
+      h2 r;
+      r.x = static_cast<_Float16>(row[b >> 4]);
+      r.y = static_cast<_Float16>(row[b & 15u]);
+      a.out[byte] = __builtin_bit_cast(uint32_t, r);
+    }
+  }
+}
+
 __device__ __forceinline__ void load_tables(const float* __restrict__ code2, float* s_code2,
                                             float* s_nf4) {
   const uint32_t t = threadIdx.x;
@@ -164,8 +238,14 @@ template <int UNROLL>
 __global__ __launch_bounds__(kThreads) void nf4_dequant_kernel(Nf4Args a) {
   __shared__ float s_code2[256];
   __shared__ float s_nf4[16];
-  load_tables(a.code2, s_code2, s_nf4);
-  dequant_block<UNROLL>(a, blockIdx.x, gridDim.x, s_code2, s_nf4);
+  __shared__ float s_scale[kTabMaxBlocks + 1];
+  __shared__ float s_tab[(kTabMaxBlocks + 1) * 16];
+  if (a.wide) {
+    dequant_block_tab<UNROLL>(a, blockIdx.x, gridDim.x, s_code2, s_nf4, s_scale, s_tab);
+  } else {
+    load_tables(a.code2, s_code2, s_nf4);
+    dequant_block<UNROLL>(a, blockIdx.x, gridDim.x, s_code2, s_nf4);
+  }
 }
 
 constexpr int kMaxJobs = 4;
@@ -181,12 +261,19 @@ template <int UNROLL>
 __global__ __launch_bounds__(kThreads) void nf4_dequant_multi_kernel(Nf4Multi m) {
   __shared__ float s_code2[256];
   __shared__ float s_nf4[16];
-  load_tables(m.job[0].code2, s_code2, s_nf4);  // one code2 table for every job
+  __shared__ float s_scale[kTabMaxBlocks + 1];
+  __shared__ float s_tab[(kTabMaxBlocks + 1) * 16];
   int j = 0;
 #pragma unroll
   for (int k = 1; k < kMaxJobs; ++k) j += (k < m.n_jobs && blockIdx.x >= m.start[k]) ? 1 : 0;
-  dequant_block<UNROLL>(m.job[j], blockIdx.x - m.start[j], m.start[j + 1] - m.start[j], s_code2,
-                        s_nf4);
+  if (m.job[j].wide) {  // uniform over the block; every job shares one code2 table
+    dequant_block_tab<UNROLL>(m.job[j], blockIdx.x - m.start[j], m.start[j + 1] - m.start[j],
+                              s_code2, s_nf4, s_scale, s_tab);
+  } else {
+    load_tables(m.job[0].code2, s_code2, s_nf4);
+    dequant_block<UNROLL>(m.job[j], blockIdx.x - m.start[j], m.start[j + 1] - m.start[j],
+                          s_code2, s_nf4);
+  }
 }
 
 bool is_pow2(int64_t v) { return v > 0 && (v & (v - 1)) == 0; }
@@ -204,6 +291,7 @@ namespace rus {
 namespace {
 
 constexpr int kUnrollMain = 4;
+static_assert(kUnrollMain == kUnrollTab, "both paths cover 4 KiB of packed bytes per block");
 
 // Validates one segment job and fills its kernel arguments (see rus_nf4_dequant).
 int make_job(const char* fn, const uint8_t* packed, const uint8_t* absmax, const float* code2,
@@ -269,11 +357,12 @@ int make_job(const char* fn, const uint8_t* packed, const uint8_t* absmax, const
   a.sbase2 = static_cast<uint32_t>(absmax2_base_2);
   a.n_bytes = static_cast<uint32_t>(n_bytes);
   a.n_units = static_cast<uint32_t>(n_bytes / 4);
+  a.wide = half_block >= 16 ? 1 : 0;
   return RUS_OK;
 }
 
 uint32_t blocks_for(const Nf4Args& a) {
-  const uint32_t per_block = kThreads * kUnrollMain;
+  const uint32_t per_block = kThreads * kUnrollMain;  // kUnrollTab == kUnrollMain
   const uint32_t g = (a.n_units + per_block - 1) / per_block;
   return g == 0 ? 1 : g;  // tail-only input
 }

@@ -281,19 +281,59 @@ class WeightStream:
             blocksize=seg.blocksize, super_blocksize=seg.super_blocksize,
             absmax2_bases=seg.absmax2_bases)
 
-    def dequant_layer(self, layer_idx: int) -> dict[str, torch.Tensor]:
+    def dequant_layer(self, layer_idx: int, workspaces=None) -> dict[str, torch.Tensor]:
         """All four segments of a layer in one dequant launch: {"qkv", "o", "gu", "down"} ->
-        fp16 weights (views of the per-segment workspaces)."""
+        fp16 weights (views of the per-segment workspaces, or of ``workspaces``)."""
         packed, absmax, absmax2 = self._arrays(layer_idx)
         segs = self.layer_segments[layer_idx]
         first = segs[SEGMENTS[0]]
+        wsp = self.workspaces if workspaces is None else workspaces
         jobs = [{"packed": packed[sg.packed_slice], "absmax": absmax[sg.absmax_slice],
                  "absmax2": absmax2[sg.absmax2_slice], "offset": sg.offsets,
-                 "out_shape": (sg.out_features, sg.in_features), "out_buf": self.workspaces[name],
+                 "out_shape": (sg.out_features, sg.in_features), "out_buf": wsp[name],
                  "split_bytes": sg.split_bytes, "absmax2_bases": sg.absmax2_bases}
                 for name, sg in ((n, segs[n]) for n in SEGMENTS)]
         outs = K.dequant_nf4_segments(jobs, self.code2_gpu, first.blocksize, first.super_blocksize)
         return dict(zip(SEGMENTS, outs))
+
+    # -- dequantisation one layer ahead on a second stream ---------------------------------------
+    @property
+    def dequant_ahead(self) -> bool:
+        return getattr(self, "_ahead", False)
+
+    def enable_dequant_ahead(self) -> None:
+        """Dequantises each layer on a second stream into one of two workspace sets while the
+        previous layer computes (HBM-bound dequant beside MFMA-bound GEMMs). Whole-model and
+        resident units only: their packed bytes are on the device for the whole step."""
+        if self.unit == "layer":
+            raise ValueError("dequant-ahead needs stream_unit='model' or resident weights")
+        self._ahead = True
+        self.workspace_sets = [self.workspaces,
+                               {k: torch.empty_like(t) for k, t in self.workspaces.items()}]
+        self.dq_stream = torch.cuda.Stream(device=self.device)
+        self.dq_events = [torch.cuda.Event() for _ in range(2)]
+        self.dq_out: list = [None, None]
+
+    def issue_dequant(self, layer_idx: int) -> None:
+        """Enqueues the dequant of ``layer_idx`` into workspace set ``layer_idx % 2`` on the
+        dequant stream, after all work enqueued so far on the current stream (which holds the
+        last use of that set, two layers back in either direction)."""
+        k = layer_idx % 2
+        main = torch.cuda.current_stream(self.device)
+        self.dq_stream.wait_stream(main)
+        with torch.cuda.stream(self.dq_stream):
+            w = self.dequant_layer(layer_idx, self.workspace_sets[k])
+            self.dq_events[k].record(self.dq_stream)
+        self.dq_out[k] = (layer_idx, w)
+
+    def take_dequant(self, layer_idx: int) -> dict[str, torch.Tensor]:
+        """The weights of ``layer_idx`` from issue_dequant; the current stream waits for them."""
+        k = layer_idx % 2
+        got = self.dq_out[k]
+        if got is None or got[0] != layer_idx:
+            raise RuntimeError(f"dequant of layer {layer_idx} was not issued")
+        torch.cuda.current_stream(self.device).wait_event(self.dq_events[k])
+        return got[1]
 
 
 class HostHead:

@@ -27,6 +27,7 @@ __all__ = [
     "qkv_rope_bwd_lora",
     "lora_dropout_fwd",
     "lora_dropout_bwd_add",
+    "dropout_keep_bits",
     "lora_down_fwd",
     "qkv_rope_fwd_mid",
     "lora_bwd_x",
@@ -655,19 +656,44 @@ def _lora_operand(fn, t, shape, name):
     return t
 
 
-def _drop_args(seed, stream_q, stream_v, p_q, p_v):
-    if seed is not None and (seed.dtype != torch.int64 or seed.numel() != 1):
-        raise ValueError("lora: seed must be one int64 element")
-    return _ptr(seed), int(stream_q), int(stream_v), float(p_q), float(p_v)
+def dropout_keep_bits(seed: torch.Tensor, stream0: int, n_streams: int, n_rows: int, n_cols: int,
+                      p_even: float, p_odd: float) -> torch.Tensor:
+    """Packed keep bits of the LoRA dropout masks of streams stream0 .. stream0 + n_streams - 1
+    (the masks of ``lora_dropout_fwd``): int32 [n_streams, n_rows, ceil(n_cols / 32)], bit i of
+    word w of row t set when element (t, 32 w + i) is kept; even streams use p_even, odd p_odd.
+    One launch for all layers of a step (streams 2l / 2l + 1: q / v of layer l)."""
+    fn = "dropout_keep_bits"
+    _require_device(fn, seed)
+    if seed.dtype != torch.int64 or seed.numel() != 1:
+        raise ValueError(f"{fn}: seed must be one int64 element")
+    words = (n_cols + 31) // 32
+    out = torch.empty((n_streams, n_rows, words), dtype=torch.int32, device=seed.device)
+    _launch("dropout_bits", out.numel() * 4, 0, "rus_dropout_keep_bits", seed.data_ptr(),
+            int(stream0), int(n_streams), int(n_rows), int(n_cols), float(p_even), float(p_odd),
+            out.data_ptr(), _stream(seed))
+    return out
+
+
+def _bits(fn, bits, n, d, name):
+    """Device pointer of one branch's keep bits [n, ceil(d / 32)] (None: no dropout)."""
+    if bits is None:
+        return None
+    _require_device(fn, bits)
+    if bits.dtype != torch.int32 or tuple(bits.shape) != (n, (d + 31) // 32) or \
+            not bits.is_contiguous():
+        raise ValueError(f"{fn}: {name} must be contiguous int32 [{n}, {(d + 31) // 32}]")
+    return bits.data_ptr()
 
 
 def lora_down_fwd(x: torch.Tensor, a_q: torch.Tensor, a_v: torch.Tensor,
-                  seed: torch.Tensor | None = None, stream_q: int = 0, stream_v: int = 1,
-                  p_q: float = 0.0, p_v: float = 0.0, want_x: bool = False):
-    """(mid_q, mid_v) = (drop_q(x) A_q^T, drop_v(x) A_v^T) in fp16, one launch; with ``want_x``
-    also the dropped inputs (x_q, x_v) (a seed is then required). Without a seed no dropout."""
+                  bits_q: torch.Tensor | None = None, bits_v: torch.Tensor | None = None,
+                  p_q: float = 0.0, p_v: float = 0.0, out=None):
+    """(mid_q, mid_v) = (drop_q(x) A_q^T, drop_v(x) A_v^T) in fp16, one launch; drop_* applies
+    the keep bits of ``dropout_keep_bits`` with scale 1 / (1 - p) (None: no dropout). ``out``:
+    preallocated (mid_q, mid_v) [n, r] fp16 (e.g. allocated on another stream than the one
+    the kernel runs on)."""
     fn = "lora_down_fwd"
-    _require_device(fn, x, a_q, a_v, seed)
+    _require_device(fn, x, a_q, a_v)
     r, d = a_q.shape
     if r not in LORA_RANKS:
         raise ValueError(f"{fn}: rank {r} not in {LORA_RANKS}")
@@ -677,21 +703,20 @@ def lora_down_fwd(x: torch.Tensor, a_q: torch.Tensor, a_v: torch.Tensor,
     _lora_operand(fn, a_q, (r, d), "a_q")
     _lora_operand(fn, a_v, (r, d), "a_v")
     n = x2.shape[0]
+    bq = _bits(fn, bits_q, n, d, "bits_q")
+    bv = _bits(fn, bits_v, n, d, "bits_v")
     dev = x.device
-    mid_q = torch.empty((n, r), dtype=torch.float16, device=dev)
-    mid_v = torch.empty((n, r), dtype=torch.float16, device=dev)
-    xq = xv = None
-    if want_x:
-        if seed is None:
-            raise ValueError(f"{fn}: want_x needs a seed (without dropout the inputs are x)")
-        xq = torch.empty((n, d), dtype=torch.float16, device=dev)
-        xv = torch.empty((n, d), dtype=torch.float16, device=dev)
-    _launch("lora_down", n * d * 2 * (1 + (2 if want_x else 0)) + 4 * r * d + 4 * n * r,
-            4 * n * d * r, "rus_lora_down_fwd", x2.data_ptr(), n, d, x2.stride(0),
-            a_q.data_ptr(), a_v.data_ptr(), r, mid_q.data_ptr(), mid_v.data_ptr(), _ptr(xq),
-            _ptr(xv), *_drop_args(seed, stream_q, stream_v, p_q, p_v), _stream(x2))
-    if want_x:
-        return mid_q, mid_v, xq, xv
+    if out is None:
+        mid_q = torch.empty((n, r), dtype=torch.float16, device=dev)
+        mid_v = torch.empty((n, r), dtype=torch.float16, device=dev)
+    else:
+        mid_q, mid_v = out
+        _lora_operand(fn, mid_q, (n, r), "mid_q")
+        _lora_operand(fn, mid_v, (n, r), "mid_v")
+    _launch("lora_down", n * d * 2 + 4 * r * d + 4 * n * r + n * d // 4, 4 * n * d * r,
+            "rus_lora_down_fwd", x2.data_ptr(), n, d, x2.stride(0), a_q.data_ptr(),
+            a_v.data_ptr(), r, mid_q.data_ptr(), mid_v.data_ptr(), bq, bv, float(p_q), float(p_v),
+            _stream(x2))
     return mid_q, mid_v
 
 
@@ -732,65 +757,72 @@ def qkv_rope_fwd_mid(qkv: torch.Tensor, mid_q: torch.Tensor, mid_v: torch.Tensor
     return q_out, k_out, v_out
 
 
-def lora_bwd_x(dq_lora: torch.Tensor, dv_lora: torch.Tensor, a_q: torch.Tensor,
-               a_v: torch.Tensor, b_q: torch.Tensor, b_v: torch.Tensor, dx: torch.Tensor,
-               seed: torch.Tensor | None = None, stream_q: int = 0, stream_v: int = 1,
+def lora_bwd_x(dq_lora: torch.Tensor, dv_lora: torch.Tensor, a_t_q: torch.Tensor,
+               a_t_v: torch.Tensor, b_t_q: torch.Tensor, b_t_v: torch.Tensor, dx: torch.Tensor,
+               bits_q: torch.Tensor | None = None, bits_v: torch.Tensor | None = None,
                p_q: float = 0.0, p_v: float = 0.0):
     """d_mid = dq B per branch; dx += drop_q(d_mid_q A_q), then += drop_v(d_mid_v A_v), in
-    place. Returns (d_mid_q, d_mid_v)."""
+    place, with the forward's keep bits. The factors come rank-major: a_t = A^T [d, r],
+    b_t = B^T [r, d_q]. Returns (d_mid_q, d_mid_v)."""
     fn = "lora_bwd_x"
-    _require_device(fn, dq_lora, dv_lora, a_q, a_v, b_q, b_v, dx, seed)
-    r, d = a_q.shape
+    _require_device(fn, dq_lora, dv_lora, a_t_q, a_t_v, b_t_q, b_t_v, dx)
+    d, r = a_t_q.shape
     if r not in LORA_RANKS:
         raise ValueError(f"{fn}: rank {r} not in {LORA_RANKS}")
     n = dq_lora.shape[0]
     d_q, d_v = dq_lora.shape[1], dv_lora.shape[1]
     for t, shp, nm in ((dq_lora, (n, d_q), "dq_lora"), (dv_lora, (n, d_v), "dv_lora"),
-                       (a_q, (r, d), "a_q"), (a_v, (r, d), "a_v"), (b_q, (d_q, r), "b_q"),
-                       (b_v, (d_v, r), "b_v")):
+                       (a_t_q, (d, r), "a_t_q"), (a_t_v, (d, r), "a_t_v"),
+                       (b_t_q, (r, d_q), "b_t_q"), (b_t_v, (r, d_v), "b_t_v")):
         _lora_operand(fn, t, shp, nm)
     dx2 = _rows(fn, dx, d, "dx")
     if dx2.dtype != torch.float16 or dx2.shape[0] != n:
         raise ValueError(f"{fn}: dx must be fp16 [{n}, {d}]")
+    bq = _bits(fn, bits_q, n, d, "bits_q")
+    bv = _bits(fn, bits_v, n, d, "bits_v")
     dmq = torch.empty((n, r), dtype=torch.float16, device=dx.device)
     dmv = torch.empty((n, r), dtype=torch.float16, device=dx.device)
-    _launch("lora_bwd_x", 2 * n * (d_q + d_v + 2 * d + 2 * r) + 4 * r * (d + d_q),
+    _launch("lora_bwd_x", 2 * n * (d_q + d_v + 2 * d + 2 * r) + 4 * r * (d + d_q) + n * d // 4,
             2 * n * r * (d_q + d_v + 2 * d), "rus_lora_bwd_x", dq_lora.data_ptr(),
-            dv_lora.data_ptr(), n, d_q, d_v, a_q.data_ptr(), a_v.data_ptr(), b_q.data_ptr(),
-            b_v.data_ptr(), r, d, dmq.data_ptr(), dmv.data_ptr(), dx2.data_ptr(), dx2.stride(0),
-            *_drop_args(seed, stream_q, stream_v, p_q, p_v), _stream(dx2))
+            dv_lora.data_ptr(), n, d_q, d_v, a_t_q.data_ptr(), a_t_v.data_ptr(),
+            b_t_q.data_ptr(), b_t_v.data_ptr(), r, d, dmq.data_ptr(), dmv.data_ptr(),
+            dx2.data_ptr(), dx2.stride(0), bq, bv, float(p_q), float(p_v), _stream(dx2))
     return dmq, dmv
 
 
-def lora_bwd_w(x_q: torch.Tensor, x_v: torch.Tensor, dq_lora: torch.Tensor,
-               dv_lora: torch.Tensor, mid_q: torch.Tensor, mid_v: torch.Tensor,
-               d_mid_q: torch.Tensor, d_mid_v: torch.Tensor, g_a_q: torch.Tensor,
-               g_b_q: torch.Tensor, g_a_v: torch.Tensor, g_b_v: torch.Tensor) -> None:
-    """g_a = d_mid^T x_drop [r, d], g_b = dq^T mid [d_q, r] for both branches, fp16 outputs
-    written in place (e.g. views of a flat gradient buffer)."""
+def lora_bwd_w(x: torch.Tensor, dq_lora: torch.Tensor, dv_lora: torch.Tensor,
+               mid_q: torch.Tensor, mid_v: torch.Tensor, d_mid_q: torch.Tensor,
+               d_mid_v: torch.Tensor, g_a_q: torch.Tensor, g_b_q: torch.Tensor,
+               g_a_v: torch.Tensor, g_b_v: torch.Tensor, bits_q: torch.Tensor | None = None,
+               bits_v: torch.Tensor | None = None, p_q: float = 0.0, p_v: float = 0.0) -> None:
+    """g_a = d_mid^T drop(x) [r, d], g_b = dq^T mid [d_q, r] for both branches (the dropped
+    inputs formed from x and the forward's keep bits), fp16 outputs written in place (e.g. views
+    of a flat gradient buffer)."""
     fn = "lora_bwd_w"
-    _require_device(fn, x_q, x_v, dq_lora, dv_lora, mid_q, mid_v, d_mid_q, d_mid_v, g_a_q, g_b_q,
+    _require_device(fn, x, dq_lora, dv_lora, mid_q, mid_v, d_mid_q, d_mid_v, g_a_q, g_b_q,
                     g_a_v, g_b_v)
     n, r = mid_q.shape
-    d = x_q.shape[1]
+    d = x.shape[1]
     d_q, d_v = dq_lora.shape[1], dv_lora.shape[1]
     if r not in LORA_RANKS:
         raise ValueError(f"{fn}: rank {r} not in {LORA_RANKS}")
-    xq2 = _rows(fn, x_q, d, "x_q")
-    xv2 = _rows(fn, x_v, d, "x_v")
-    if xq2.stride(0) != xv2.stride(0) or xq2.dtype != torch.float16 or xv2.dtype != torch.float16:
-        raise ValueError(f"{fn}: x_q and x_v must be fp16 with one row stride")
+    x2 = _rows(fn, x, d, "x")
+    if x2.dtype != torch.float16 or x2.shape[0] != n:
+        raise ValueError(f"{fn}: x must be fp16 [{n}, {d}]")
     for t, shp, nm in ((dq_lora, (n, d_q), "dq_lora"), (dv_lora, (n, d_v), "dv_lora"),
                        (mid_q, (n, r), "mid_q"), (mid_v, (n, r), "mid_v"),
                        (d_mid_q, (n, r), "d_mid_q"), (d_mid_v, (n, r), "d_mid_v"),
                        (g_a_q, (r, d), "g_a_q"), (g_b_q, (d_q, r), "g_b_q"),
                        (g_a_v, (r, d), "g_a_v"), (g_b_v, (d_v, r), "g_b_v")):
         _lora_operand(fn, t, shp, nm)
-    _launch("lora_bwd_w", 2 * n * (2 * d + d_q + d_v + 4 * r), 2 * n * r * (2 * d + d_q + d_v),
-            "rus_lora_bwd_w", xq2.data_ptr(), xv2.data_ptr(), xq2.stride(0), dq_lora.data_ptr(),
-            dv_lora.data_ptr(), mid_q.data_ptr(), mid_v.data_ptr(), d_mid_q.data_ptr(),
-            d_mid_v.data_ptr(), n, d, d_q, d_v, r, g_a_q.data_ptr(), g_b_q.data_ptr(),
-            g_a_v.data_ptr(), g_b_v.data_ptr(), _stream(mid_q))
+    bq = _bits(fn, bits_q, n, d, "bits_q")
+    bv = _bits(fn, bits_v, n, d, "bits_v")
+    _launch("lora_bwd_w", 2 * n * (d + d_q + d_v + 4 * r) + n * d // 4,
+            2 * n * r * (2 * d + d_q + d_v), "rus_lora_bwd_w", x2.data_ptr(), x2.stride(0), bq,
+            bv, float(p_q), float(p_v), dq_lora.data_ptr(), dv_lora.data_ptr(),
+            mid_q.data_ptr(), mid_v.data_ptr(), d_mid_q.data_ptr(), d_mid_v.data_ptr(), n, d,
+            d_q, d_v, r, g_a_q.data_ptr(), g_b_q.data_ptr(), g_a_v.data_ptr(), g_b_v.data_ptr(),
+            _stream(mid_q))
 
 
 # ---------------------------------------------------------------------------------------------

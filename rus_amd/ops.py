@@ -237,7 +237,8 @@ class Qwen2FusedEngine:
                  offload_inputs: bool = False, max_pos: int = 2048,
                  max_mlp_tokens: int = MAX_MLP_TOKENS, v_chunk: int = V_CHUNK_DEFAULT,
                  attention: str = "varlen", dropout_seed: int | None = None,
-                 stream_unit: str = "layer", lora_kernels: bool = True, recompute: bool = True):
+                 stream_unit: str = "layer", lora_kernels: bool = True, recompute: bool = True,
+                 overlap: bool = False):
         from .model import QLoRAQwen2
 
         if not isinstance(model, QLoRAQwen2):
@@ -285,6 +286,13 @@ class Qwen2FusedEngine:
         if not recompute and attention == "sdpa_rows":
             raise ValueError("recompute=False needs attention='varlen' or 'varlen_aten'")
         self.recompute = bool(recompute)
+        # overlap=True: each layer's NF4 dequant runs on a second stream one layer ahead (into
+        # a second workspace set) while the current layer computes; needs the weights' packed
+        # bytes on the device for the whole step (resident or stream_unit="model").
+        self.overlap = bool(overlap)
+        if self.overlap:
+            self.weight_stream.enable_dequant_ahead()
+            self.side_stream = torch.cuda.Stream(device=self.device)  # default priority
         self._flatten_lora()
         # The fused LoRA kernels (one launch for dropout + both A products, the B products inside
         # RoPE, two backward launches) cover ranks 4/8/16/32; other ranks use library GEMMs.
@@ -342,6 +350,27 @@ class Qwen2FusedEngine:
         """fp16 copies of [q_A, q_B, v_A, v_B] per layer for one step (one cast kernel)."""
         self.sync_lora_storage()
         return self.lora_views(self._lora_flat.to(torch.float16))
+
+    def lora_fp16_t(self, lora16: list[torch.Tensor]) -> list[torch.Tensor] | None:
+        """Rank-major copies [q_A^T [D, r], q_B^T [r, Dq], v_A^T, v_B^T] per layer of a step's
+        fp16 factors, for the fused LoRA backward: four batched transposes over all layers (the
+        factors of every layer lie at one stride in the flat buffer). None without fused LoRA."""
+        if not self.fused_lora:
+            return None
+        L = self.num_layers
+        base = lora16[0]
+        per_layer = sum(t.numel() for t in lora16[:4])
+        out = [None] * (4 * L)
+        off = 0
+        for j in range(4):
+            r0, c0 = lora16[j].shape
+            v = torch.as_strided(base, (L, r0, c0), (per_layer, c0, 1),
+                                 base.storage_offset() + off)
+            t = v.transpose(1, 2).contiguous()  # [L, c0, r0]
+            for l in range(L):
+                out[4 * l + j] = t[l]
+            off += r0 * c0
+        return out
 
 
 def _run_packed_sdpa(q_rot, k_rot, v_out, row_lengths, num_heads, num_kv_heads, head_dim):
@@ -420,11 +449,31 @@ def _lora_inputs(norm1, layer, meta, training, seed):
     return norm1, norm1
 
 
-def _lora_drop_args(layer, meta, training, seed):
-    """(seed, stream_q, stream_v, p_q, p_v) for the fused LoRA kernels (seed None: no dropout)."""
-    if _dropout_on(meta, training):
-        return seed, 2 * layer, 2 * layer + 1, meta["p_q"], meta["p_v"]
-    return None, 2 * layer, 2 * layer + 1, 0.0, 0.0
+def _dropout_masks(engine, n_tok, training, seed):
+    """Packed keep bits of every layer's two LoRA dropout masks for this step (streams 2l, 2l+1
+    of the counter-based generator): per layer an int32 [2, n_tok, ceil(D / 32)] tensor, or None
+    for a layer without dropout; one launch when all layers share their probabilities."""
+    L = engine.num_layers
+    metas = engine.layer_lora_meta
+    if not training or not any(_dropout_on(m, training) for m in metas) or n_tok == 0:
+        return [None] * L
+    d = engine.hidden_size
+    ps = {(m["p_q"], m["p_v"]) for m in metas}
+    if len(ps) == 1:
+        p_q, p_v = ps.pop()
+        bits = K.dropout_keep_bits(seed, 0, 2 * L, n_tok, d, p_q, p_v)
+        return [bits[2 * l: 2 * l + 2] for l in range(L)]
+    return [K.dropout_keep_bits(seed, 2 * l, 2, n_tok, d, m["p_q"], m["p_v"])
+            if _dropout_on(m, training) else None for l, m in enumerate(metas)]
+
+
+def _lora_bits(masks, layer, meta):
+    """(bits_q, bits_v, p_q, p_v) for the fused LoRA kernels of one layer (None: no dropout)."""
+    m = masks[layer]
+    if m is None:
+        return None, None, 0.0, 0.0
+    # both branches' bits (a branch with p = 0 keeps every element at scale 1)
+    return m[0], m[1], meta["p_q"], meta["p_v"]
 
 
 def _lora_deltas(x_q, x_v, qA, qB, vA, vB):
@@ -470,43 +519,56 @@ class StackState:
     in the engine's InputStream)."""
 
     __slots__ = ("pos_ids", "h_last", "final_rstd", "vm", "row_lengths", "lora16", "training",
-                 "seed", "buf", "saved")
+                 "seed", "buf", "saved", "masks", "lora16t")
 
     def __init__(self, **kw):
         self.saved = None
+        self.masks = None
+        self.lora16t = None
         for k, v in kw.items():
             setattr(self, k, v)
 
 
-def _layer_front(engine, l, norm1, w_qkv, lora16, training, seed, pos_ids, want_x):
+def _layer_front(engine, l, norm1, w_qkv, lora16, training, seed, masks, pos_ids):
     """q/k/v projection, LoRA deltas and RoPE of layer ``l`` (solution/ops.py:768-790) ->
-    (q_rot, k_rot, v_out, lora) where lora = (mid_q, mid_v, x_q, x_v, drop): the rank-r
-    intermediates and the dropped LoRA inputs (norm1 itself without dropout; only formed when
-    ``want_x``), and the fused kernels' dropout arguments."""
+    (q_rot, k_rot, v_out, lora) where lora = (mid_q, mid_v, x_q, x_v, bits): the rank-r
+    intermediates, the dropped LoRA inputs of the library path (None with the fused kernels,
+    which re-form them from norm1 and the keep bits) and the fused kernels' dropout arguments."""
     cos, sin = engine.cos_table, engine.sin_table
     hq, hkv, hd = engine.num_heads, engine.num_kv_heads, engine.head_dim
-    qkv = F.linear(norm1, w_qkv, engine.layer_biases[l])
     meta = engine.layer_lora_meta[l]
     qA, qB, vA, vB = lora16[4 * l: 4 * l + 4]
-    drop = None
+    bits = None
     if engine.fused_lora:  # dropout + A products in one launch, B products inside RoPE
-        drop = _lora_drop_args(l, meta, training, seed)
-        if want_x and drop[0] is not None:
-            mid_q, mid_v, x_q, x_v = K.lora_down_fwd(norm1, qA, vA, *drop, want_x=True)
+        bits = _lora_bits(masks, l, meta)
+        if engine.overlap:  # the rank-r products on the side stream, beside the q/k/v GEMM
+            main = torch.cuda.current_stream(norm1.device)
+            n, r = norm1.shape[0], qA.shape[0]
+            mids = (torch.empty((n, r), dtype=torch.float16, device=norm1.device),
+                    torch.empty((n, r), dtype=torch.float16, device=norm1.device))
+            side = engine.side_stream
+            side.wait_stream(main)
+            with torch.cuda.stream(side):
+                K.lora_down_fwd(norm1, qA, vA, *bits, out=mids)
+            qkv = F.linear(norm1, w_qkv, engine.layer_biases[l])
+            main.wait_stream(side)
+            mid_q, mid_v = mids
         else:
-            mid_q, mid_v = K.lora_down_fwd(norm1, qA, vA, *drop)
-            x_q = x_v = norm1
+            mid_q, mid_v = K.lora_down_fwd(norm1, qA, vA, *bits)
+            qkv = F.linear(norm1, w_qkv, engine.layer_biases[l])
+        x_q = x_v = None
         q_rot, k_rot, v_out = K.qkv_rope_fwd_mid(
             qkv, mid_q, mid_v, qB, vB, cos, sin, pos_ids, meta["scale_q"], meta["scale_v"],
             hq, hkv, hd)
     else:
+        qkv = F.linear(norm1, w_qkv, engine.layer_biases[l])
         x_q, x_v = _lora_inputs(norm1, l, meta, training, seed)
         mid_q, q_lora, mid_v, v_lora = _lora_deltas(x_q, x_v, qA, qB, vA, vB)
         q_rot, k_rot, v_out = K.qkv_rope_fwd(qkv, cos, sin, pos_ids, q_lora=q_lora,
                                              v_lora=v_lora, scale_q=meta["scale_q"],
                                              scale_v=meta["scale_v"], h_q=hq, h_kv=hkv,
                                              head_dim=hd)
-    return q_rot, k_rot, v_out, (mid_q, mid_v, x_q, x_v, drop)
+    return q_rot, k_rot, v_out, (mid_q, mid_v, x_q, x_v, bits)
 
 
 def stack_forward(engine, h_packed, pos_ids, row_lengths, training, lora16, seed, vm=None,
@@ -532,22 +594,31 @@ def stack_forward(engine, h_packed, pos_ids, row_lengths, training, lora16, seed
     if save and vm is None:
         raise ValueError("saving activations needs a varlen attention (one launch over all rows)")
     saved = [] if save else None
+    masks = _dropout_masks(engine, n_tok, training, seed) if engine.fused_lora else [None] * L
     if L > 0:
         ws.prefetch(0)
+    ahead = ws.dequant_ahead
+    if ahead and L > 0:
+        ws.issue_dequant(0)
     for l in range(L):
         if l + 1 < L:
             ws.prefetch(l + 1)
+        if ahead and l + 1 < L:
+            ws.issue_dequant(l + 1)  # beside this layer's compute
         if carry is None:
             norm1, _, rstd1 = K.rms_norm_fwd(h, engine.ln1_weights[l], eps=eps)
         else:
             norm1, h, rstd1 = K.rms_norm_fwd(carry[1], engine.ln1_weights[l], eps=eps,
                                              residual=carry[0])
         ins.save(l, h)
-        ws.wait_slot(l)
-        W = ws.dequant_layer(l)  # one launch for [q|k|v], o, [gate|up], down
-        ws.release_slot(l)
+        if ahead:
+            W = ws.take_dequant(l)
+        else:
+            ws.wait_slot(l)
+            W = ws.dequant_layer(l)  # one launch for [q|k|v], o, [gate|up], down
+            ws.release_slot(l)
         q_rot, k_rot, v_out, lora = _layer_front(engine, l, norm1, W["qkv"], lora16, training,
-                                                 seed, pos_ids, want_x=save)
+                                                 seed, masks, pos_ids)
         if vm is not None:
             attn, lse, rng, unused = _varlen_attn_fwd(q_rot, k_rot, v_out, vm, engine.attention)
             attn = attn.view(n_tok, hq * hd)
@@ -575,6 +646,7 @@ def stack_forward(engine, h_packed, pos_ids, row_lengths, training, lora16, seed
                                                         eps=eps, residual=carry[0])
     st = StackState(pos_ids=pos_ids, h_last=h_last, final_rstd=final_rstd, vm=vm,
                     row_lengths=row_lengths, lora16=lora16, training=training, seed=seed,
+                    masks=masks,
                     buf=ws.active if ws.unit == "model" else 0, saved=saved)
     return final_norm, st
 
@@ -595,18 +667,27 @@ def stack_backward(engine, st: StackState, d_final_norm, grad16) -> torch.Tensor
 
     dh = K.rms_norm_bwd(d_final_norm.contiguous(), st.h_last, engine.final_norm_weight,
                         st.final_rstd)
+    st.lora16t = engine.lora_fp16_t(st.lora16)  # rank-major factors of the fused LoRA backward
     ws.use_buffer(st.buf)
+    ahead = ws.dequant_ahead
     if L > 0:
         ws.prefetch(L - 1)
+        if ahead:
+            ws.issue_dequant(L - 1)
     for l in range(L - 1, -1, -1):
         if l - 1 >= 0:
             ws.prefetch(l - 1)
             ins.prefetch(l - 1, n_tokens)
+            if ahead:
+                ws.issue_dequant(l - 1)  # beside this layer's backward
         h_in = ins.load(l, n_tokens)
-        ws.wait_slot(l)
-        W = ws.dequant_layer(l)
+        if ahead:
+            W = ws.take_dequant(l)
+        else:
+            ws.wait_slot(l)
+            W = ws.dequant_layer(l)
+            ws.release_slot(l)  # every read of the packed slot is enqueued
         w_qkv, w_o, w_gu, w_down = W["qkv"], W["o"], W["gu"], W["down"]
-        ws.release_slot(l)  # every read of the packed slot is enqueued
         meta = engine.layer_lora_meta[l]
         qA, qB, vA, vB = st.lora16[4 * l: 4 * l + 4]
         fused = engine.fused_lora
@@ -615,7 +696,7 @@ def stack_backward(engine, st: StackState, d_final_norm, grad16) -> torch.Tensor
             rec = st.saved[l]
             st.saved[l] = None  # freed as the backward moves down the stack
             norm1, rstd1 = rec["norm1"], rec["rstd1"]
-            mid_q, mid_v, x_q, x_v, drop = rec["lora"]
+            mid_q, mid_v, x_q, x_v, bits = rec["lora"]
             q_rot, k_rot, v_out = rec["q_rot"], rec["k_rot"], rec["v_out"]
             attn2d = rec["attn"]
             attn = attn2d.view(n_tokens, hq, hd)
@@ -626,8 +707,8 @@ def stack_backward(engine, st: StackState, d_final_norm, grad16) -> torch.Tensor
             # Recompute the layer forward (same dropout masks: same seed and streams).
             norm1, _, rstd1 = K.rms_norm_fwd(h_in, engine.ln1_weights[l], eps=eps)
             q_rot, k_rot, v_out, lora = _layer_front(engine, l, norm1, w_qkv, st.lora16,
-                                                     training, seed, pos_ids, want_x=True)
-            mid_q, mid_v, x_q, x_v, drop = lora
+                                                     training, seed, st.masks, pos_ids)
+            mid_q, mid_v, x_q, x_v, bits = lora
             del lora
             if st.vm is not None:
                 attn, lse, rng, unused = _varlen_attn_fwd(q_rot, k_rot, v_out, st.vm,
@@ -686,9 +767,11 @@ def stack_backward(engine, st: StackState, d_final_norm, grad16) -> torch.Tensor
         d_norm1 = torch.mm(dqkv, w_qkv)
         del dqkv
         if fused:  # d_mid, the expansion, masks and both adds; then all four weight gradients
-            d_mid_q, d_mid_v = K.lora_bwd_x(dq_scaled, dv_scaled, qA, vA, qB, vB, d_norm1, *drop)
-            K.lora_bwd_w(x_q, x_v, dq_scaled, dv_scaled, mid_q, mid_v, d_mid_q, d_mid_v, g_qA,
-                         g_qB, g_vA, g_vB)
+            qAt, qBt, vAt, vBt = st.lora16t[4 * l: 4 * l + 4]
+            d_mid_q, d_mid_v = K.lora_bwd_x(dq_scaled, dv_scaled, qAt, vAt, qBt, vBt, d_norm1,
+                                            *bits)
+            K.lora_bwd_w(norm1, dq_scaled, dv_scaled, mid_q, mid_v, d_mid_q, d_mid_v, g_qA, g_qB,
+                         g_vA, g_vB, *bits)
         else:
             torch.mm(dq_scaled.t(), mid_q, out=g_qB)
             d_mid_q = torch.mm(dq_scaled, qB)

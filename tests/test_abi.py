@@ -67,6 +67,10 @@ def test_header_compiles_as_c():
         ("rus_swiglu_fwd", (16, 16, 16, 4, 100, 50, 100, 100, 0, None), "stride"),
         ("rus_swiglu_bwd", (16, 16, 16, 16, 16, 1 << 20, 1 << 12, 1 << 12, 1 << 12, 1 << 12,
                             1 << 12, 1 << 12, 0, None), "2\\^31"),
+        # keep bits need n_cols % 8 == 0; the LoRA input-gradient kernel d % 32 == 0
+        ("rus_dropout_keep_bits", (16, 0, 2, 4, 12, 0.1, 0.1, 16, None), "multiple of 8"),
+        ("rus_lora_bwd_x", (16, 16, 4, 64, 64, 16, 16, 16, 16, 16, 48, 16, 16, 16, 48, None,
+                            None, 0.0, 0.0, None), "d % 32"),
         # attention: head_dim other than 128, GQA ratio not integral, misaligned output
         ("rus_attn_varlen_fwd", (16, 16, 16, 16, 1, 32, 2, 12, 2, 64, 0.1, 16, 16, None),
          "head_dim"),

@@ -147,16 +147,17 @@ def test_graph_replays_repeatable_across_buckets(unit):
 
 
 def test_graph_saved_activations_match_recompute_bitwise():
-    # The captured step with activations kept from the forward gives the recompute's bits,
-    # dropout included, on two buckets and repeated replays.
+    # The captured step with activations kept from the forward (and with the second stream:
+    # dequant ahead, LoRA-down beside the q/k/v GEMM) gives the recompute's bits, dropout
+    # included, on two buckets and repeated replays.
     cfg = small_config(dropout=0.1)
     model = M.build_random_qlora_qwen2(cfg, DEV, seed=6, std=0.05)
     a = _batch(cfg, [30, 50], seed=1)
     b = _batch(cfg, [90, 70, 12], seed=2)
     res = []
-    for recompute in (True, False):
+    for recompute, ov in ((True, False), (False, False), (False, True)):
         engine = ops.Qwen2FusedEngine(model, DEV, resident_weights=False, stream_unit="model",
-                                      dropout_seed=77, recompute=recompute)
+                                      dropout_seed=77, recompute=recompute, overlap=ov)
         gs = GraphedTrainStep(engine, bucket=64, training=True)
         out = []
         for batch in (a, b, a):
@@ -164,9 +165,10 @@ def test_graph_saved_activations_match_recompute_bitwise():
             torch.cuda.synchronize()
             out.append(_grads(engine))
         res.append(out)
-    for x, y in zip(*res):
-        if isinstance(x, float):
-            assert x == y
-        else:
-            for g0, g1 in zip(x, y):
-                assert torch.equal(g0, g1)
+    for other in res[1:]:
+        for x, y in zip(res[0], other):
+            if isinstance(x, float):
+                assert x == y
+            else:
+                for g0, g1 in zip(x, y):
+                    assert torch.equal(g0, g1)

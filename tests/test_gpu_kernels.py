@@ -302,3 +302,23 @@ def test_lora_dropout_fwd_bwd_bit_exact(dtype, shape, strided):
     a2, _ = K.lora_dropout_fwd(xd, seed, sa, sb, pa, pb)
     torch.cuda.synchronize()
     assert torch.equal(a2.cpu(), ref.lora_dropout_fwd(x, seed_v + 1, sa, sb, pa, pb)[0])
+
+
+@pytest.mark.parametrize("blocksize", [16, 32, 64])
+@pytest.mark.parametrize("offset_bytes", [0, 4])
+@pytest.mark.parametrize("shape", [(3, 1002), (2, 4098)])
+def test_nf4_dequant_table_and_direct_paths_bit_exact(blocksize, offset_bytes, shape):
+    # blocksize >= 32 takes the path with an LDS table of NF4 x scale per absmax block,
+    # blocksize 16 the direct one; packed views 4 bytes into their allocation. 3 x 1002
+    # elements leave a ragged tail past the last 4-byte unit; 2 x 4098 (4098 packed bytes) put
+    # that tail just past the first 4 KiB block, in an absmax block of its own.
+    g = torch.Generator().manual_seed(blocksize + offset_bytes)
+    w = (torch.randn(*shape, generator=g) * 0.02).half()
+    q = quant.quantize_nf4(w, blocksize=blocksize)
+    packed = torch.zeros(q.packed.numel() + offset_bytes, dtype=torch.uint8, device=DEV)
+    packed[offset_bytes:].copy_(q.packed.reshape(-1).to(DEV))
+    out = K.dequant_nf4_tensor(packed[offset_bytes:], q.absmax.to(DEV), q.code2.to(DEV),
+                               q.absmax2.to(DEV), q.offset, q.shape, blocksize=q.blocksize,
+                               super_blocksize=q.super_blocksize)
+    torch.cuda.synchronize()
+    assert _bits_equal(out, _dequant_ref(q))

@@ -8,6 +8,7 @@ bit-exact.
 
 from __future__ import annotations
 
+import numpy as np
 import pytest
 import torch
 
@@ -40,6 +41,28 @@ def _inputs(n, d, dq_dim, dv_dim, r, seed):
     return g, x, aq, av, bq, bv
 
 
+def _bits(seed_v, stream0, n, d, p_even, p_odd):
+    """Device keep bits of two streams and their oracle values (bit-exact)."""
+    seed = torch.tensor([seed_v], dtype=torch.int64, device=DEV)
+    bits = K.dropout_keep_bits(seed, stream0, 2, n, d, p_even, p_odd)
+    torch.cuda.synchronize()
+    for s, p in ((0, p_even), (1, p_odd)):
+        want = ref.dropout_keep_bits(seed_v, stream0 + s, n, d, p)
+        assert np.array_equal(bits[s].cpu().numpy(), want)
+    return bits[0], bits[1]
+
+
+@pytest.mark.parametrize("n,d,streams", [(1, 1536, 2), (37, 40, 3), (300, 1536, 56)])
+def test_dropout_keep_bits_match_oracle(n, d, streams):
+    seed_v = 77 + n
+    seed = torch.tensor([seed_v], dtype=torch.int64, device=DEV)
+    bits = K.dropout_keep_bits(seed, 4, streams, n, d, 0.05, 0.3)
+    torch.cuda.synchronize()
+    for s in (0, 1, streams - 1):
+        want = ref.dropout_keep_bits(seed_v, 4 + s, n, d, 0.05 if s % 2 == 0 else 0.3)
+        assert np.array_equal(bits[s].cpu().numpy(), want), s
+
+
 @pytest.mark.parametrize("r", [4, 8, 16, 32])
 @pytest.mark.parametrize("drop", [False, True])
 @pytest.mark.parametrize("n", [1, 37, 300])
@@ -48,16 +71,14 @@ def test_lora_down_and_rope_mid(r, drop, n):
     d = 1536
     g, x, aq, av, bq, bv = _inputs(n, d, h_q * hd, h_kv * hd, r, seed=r * 100 + n)
     seed_v = 4242
-    seed = torch.tensor([seed_v], dtype=torch.int64, device=DEV) if drop else None
     args = (seed_v, 6, 7, 0.05, 0.1) if drop else (None,)
     mq, mv, xq, xv = ref.lora_down_fwd(x, aq, av, *args)
-    out = K.lora_down_fwd(x.to(DEV), aq.to(DEV), av.to(DEV), seed, 6, 7, 0.05, 0.1, want_x=drop)
+    bits = _bits(seed_v, 6, n, d, 0.05, 0.1) if drop else (None, None)
+    out = K.lora_down_fwd(x.to(DEV), aq.to(DEV), av.to(DEV), *bits, 0.05, 0.1)
     torch.cuda.synchronize()
     for got, want, xx, aa in zip(out[:2], (mq, mv), (xq, xv), (aq, av)):
         ok, err = _close(got, want, a=xx, b=aa.t())
         assert ok, err
-    if drop:
-        assert torch.equal(out[2].cpu(), xq) and torch.equal(out[3].cpu(), xv)
     # RoPE with the deltas formed from (mid, B), against the oracle given the same mid values
     qkv = torch.randn(n, (h_q + 2 * h_kv) * hd, generator=g).half()
     cos, sin = ref.rope_tables(512, hd, 1e6)
@@ -89,7 +110,7 @@ def test_lora_down_and_rope_mid(r, drop, n):
         assert bool((err <= tol + 1e-6).all()), float((err - tol).max())
 
 
-@pytest.mark.parametrize("r", [4, 16, 32])
+@pytest.mark.parametrize("r", [4, 8, 16, 32])
 @pytest.mark.parametrize("drop", [False, True])
 @pytest.mark.parametrize("n", [5, 300])
 def test_lora_bwd_x_and_w(r, drop, n):
@@ -99,12 +120,12 @@ def test_lora_bwd_x_and_w(r, drop, n):
     dv = torch.randn(n, dv_dim, generator=g).half()
     dx = torch.randn(n, d, generator=g).half()
     seed_v = 99
-    seed = torch.tensor([seed_v], dtype=torch.int64, device=DEV) if drop else None
     dargs = (seed_v, 2, 3, 0.05, 0.05) if drop else (None,)
+    bits = _bits(seed_v, 2, n, d, 0.05, 0.05) if drop else (None, None)
     dmq, dmv, dx_want = ref.lora_bwd_x(dq, dv, aq, av, bq, bv, dx, *dargs)
     dxd = dx.to(DEV)
-    got_mq, got_mv = K.lora_bwd_x(dq.to(DEV), dv.to(DEV), aq.to(DEV), av.to(DEV), bq.to(DEV),
-                                  bv.to(DEV), dxd, seed, 2, 3, 0.05, 0.05)
+    ts = [t.t().contiguous().to(DEV) for t in (aq, av, bq, bv)]
+    got_mq, got_mv = K.lora_bwd_x(dq.to(DEV), dv.to(DEV), *ts, dxd, *bits, 0.05, 0.05)
     torch.cuda.synchronize()
     for got, want, dd, bb in ((got_mq, dmq, dq, bq), (got_mv, dmv, dv, bv)):
         ok, err = _close(got, want, a=dd, b=bb)
@@ -127,12 +148,13 @@ def test_lora_bwd_x_and_w(r, drop, n):
     err = (dxd.float().cpu() - dx_ref.float()).abs()
     assert bool((err <= tol + 1e-6).all()), float((err - tol).max())
 
-    # weight gradients from the kernel's d_mid and a forward's mid / dropped rows
+    # weight gradients from the kernel's d_mid and a forward's mid; the dropped rows are formed
+    # in the kernel from x and the keep bits
     mq, mv, xq, xv = ref.lora_down_fwd(x, aq, av, *((seed_v, 2, 3, 0.05, 0.05) if drop else (None,)))
     want = ref.lora_bwd_w(xq, xv, dq, dv, mq, mv, got_mq.cpu(), got_mv.cpu())
     outs = [torch.full(w.shape, 7.0, dtype=torch.float16, device=DEV) for w in want]
-    K.lora_bwd_w(xq.to(DEV), xv.to(DEV), dq.to(DEV), dv.to(DEV), mq.to(DEV), mv.to(DEV), got_mq,
-                 got_mv, *outs)
+    K.lora_bwd_w(x.to(DEV), dq.to(DEV), dv.to(DEV), mq.to(DEV), mv.to(DEV), got_mq, got_mv, *outs,
+                 *bits, 0.05, 0.05)
     torch.cuda.synchronize()
     operands = ((got_mq.cpu().t(), xq), (dq.t(), mq), (got_mv.cpu().t(), xv), (dv.t(), mv))
     for got, w, (aa, bb) in zip(outs, want, operands):
@@ -146,5 +168,6 @@ def test_lora_kernels_reject_bad_rank_and_layout():
     with pytest.raises(ValueError, match="rank"):
         K.lora_down_fwd(x, a, a)
     a4 = torch.randn(4, 64, device=DEV).half()
-    with pytest.raises(ValueError, match="seed"):
-        K.lora_down_fwd(x, a4, a4, want_x=True)
+    bad = torch.zeros(8, 3, dtype=torch.int32, device=DEV)  # 64 columns need 2 words per row
+    with pytest.raises(ValueError, match="bits_q"):
+        K.lora_down_fwd(x, a4, a4, bad, None, 0.1, 0.0)

@@ -85,8 +85,11 @@ def test_streamed_and_resident_weights_agree_bitwise():
     ids, mask, labels = _batch(cfg, [30, 50], seed=1)
     pb = ops.pack_varlen(ids, mask, labels)
     out = []
-    for resident, unit in ((False, "layer"), (False, "model"), (True, "layer")):
-        engine = ops.Qwen2FusedEngine(model, DEV, resident_weights=resident, stream_unit=unit)
+    for resident, unit, ov in ((False, "layer", False), (False, "model", False),
+                               (True, "layer", False), (False, "model", True),
+                               (True, "layer", True)):
+        engine = ops.Qwen2FusedEngine(model, DEV, resident_weights=resident, stream_unit=unit,
+                                      overlap=ov)
         out.append(_fused_step(engine, pb, training=False))
         out.append(_fused_step(engine, pb, training=False))  # second step: the other buffer
     for o in out[1:]:
@@ -166,18 +169,21 @@ def test_fused_lora_kernels_match_library_gemm_path():
 
 @pytest.mark.parametrize("dropout,lora_kernels", [(0.0, True), (0.1, True), (0.1, False)])
 def test_saved_activations_match_recompute_bitwise(dropout, lora_kernels):
+    # recompute on / off, each without and with the second stream (dequant ahead, LoRA-down
+    # beside the q/k/v GEMM): the same bits
     cfg = small_config(dropout=dropout)
     model = M.build_random_qlora_qwen2(cfg, DEV, seed=4, std=0.05)
     ids, mask, labels = _batch(cfg, [45, 70, 12], seed=3)
     pb = ops.pack_varlen(ids, mask, labels)
     out = []
-    for recompute in (True, False):
+    for recompute, ov in ((True, False), (False, False), (True, True), (False, True)):
         engine = ops.Qwen2FusedEngine(model, DEV, resident_weights=True, dropout_seed=123,
-                                      lora_kernels=lora_kernels, recompute=recompute)
+                                      lora_kernels=lora_kernels, recompute=recompute, overlap=ov)
         out.append(_fused_step(engine, pb, training=True))
-    assert torch.equal(out[0][0], out[1][0])
-    for a, b in zip(out[0][1], out[1][1]):
-        assert torch.equal(a, b)
+    for o in out[1:]:
+        assert torch.equal(out[0][0], o[0])
+        for a, b in zip(out[0][1], o[1]):
+            assert torch.equal(a, b)
 
 
 def test_recompute_off_needs_varlen_attention():

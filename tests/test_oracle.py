@@ -328,6 +328,19 @@ def test_dropout_mask_rate_and_independence():
     assert np.array_equal(ref.dropout_keep_mask(7, 0, 10, n_cols, p), m[:10])
 
 
+def test_dropout_keep_bits_layout():
+    # The packed layout against an independent unpacking (numpy's little-endian bit order) and
+    # known answers: p = 0 keeps every element and pads the last word's tail with zeros.
+    keep = ref.dropout_keep_mask(3, 5, 7, 72, 0.3)
+    bits = ref.dropout_keep_bits(3, 5, 7, 72, 0.3)
+    assert bits.shape == (7, 3) and bits.dtype == np.int32
+    unpacked = np.unpackbits(bits.view(np.uint8).reshape(7, 12), axis=1, bitorder="little")
+    assert np.array_equal(unpacked[:, :72].astype(bool), keep)
+    assert not unpacked[:, 72:].any()
+    full = ref.dropout_keep_bits(3, 5, 2, 40, 0.0).view(np.uint32)
+    assert (full[:, 0] == 0xFFFFFFFF).all() and (full[:, 1] == 0xFF).all()
+
+
 def test_dropout_fwd_values_and_bwd_rounding_order():
     g = torch.Generator().manual_seed(0)
     x = torch.randn(37, 96, generator=g).half()
