@@ -21,6 +21,7 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kSpan = 8;  // elements per thread in each half of a head
+constexpr int kMaxMidHead = 256;  // largest head_dim of the in-kernel LoRA delta (B rows in LDS)
 
 __device__ __forceinline__ int64_t clamp_pos(const int64_t* __restrict__ pos, int64_t t,
                                              int64_t n_pos, int32_t* err_flag) {
@@ -82,14 +83,29 @@ __global__ __launch_bounds__(kThreads) void rope_fwd_kernel(RopeFwdArgs<T> a) {
   constexpr bool HAS_LORA = LORA == 1;
   const int half = a.head_dim / 2;
   const int per_head = half / kSpan;
-  const int heads = a.h_q + 2 * a.h_kv;
-  const int slots = heads * per_head;
-  const int64_t gid = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
-  const int64_t t = gid / slots;
-  if (t >= a.n_tokens) return;
-  const int slot = static_cast<int>(gid - t * slots);
-  const int hd = slot / per_head;
-  const int j = (slot - hd * per_head) * kSpan;
+  // Head-major blocks: one head x kThreads / per_head tokens, so a block touches one head's
+  // rows of the LoRA factor B (L1-resident) instead of all of them.
+  const int tpb = kThreads / per_head;
+  const int64_t n_tiles = (a.n_tokens + tpb - 1) / tpb;
+  const int hd = static_cast<int>(blockIdx.x / n_tiles);
+  const int64_t t = (blockIdx.x - hd * n_tiles) * tpb + threadIdx.x / per_head;
+  const int j = (threadIdx.x % per_head) * kSpan;
+  // LORA == 2: this head's rows of B (head_dim x R fp16) staged in LDS once per block.
+  __shared__ __attribute__((aligned(16))) T s_b[LORA == 2 ? kMaxMidHead * R : 1];
+  if constexpr (LORA == 2) {
+    const T* bsrc = nullptr;
+    if (hd < a.h_q)
+      bsrc = a.b_q + static_cast<int64_t>(hd) * a.head_dim * R;
+    else if (hd >= a.h_q + a.h_kv)
+      bsrc = a.b_v + static_cast<int64_t>(hd - a.h_q - a.h_kv) * a.head_dim * R;
+    if (bsrc) {
+      const int n4 = a.head_dim * R / 4;  // 8-byte chunks (B is 8-byte aligned)
+      for (int c = threadIdx.x; c < n4; c += kThreads)
+        reinterpret_cast<uint2*>(s_b)[c] = reinterpret_cast<const uint2*>(bsrc)[c];
+    }
+    __syncthreads();
+  }
+  if (t >= a.n_tokens || static_cast<int>(threadIdx.x) >= tpb * per_head) return;
 
   float lo[kSpan], hi[kSpan];
   const T* row = a.qkv + t * a.stride_qkv + static_cast<int64_t>(hd) * a.head_dim;
@@ -101,7 +117,7 @@ __global__ __launch_bounds__(kThreads) void rope_fwd_kernel(RopeFwdArgs<T> a) {
     if constexpr (LORA == 2) {
       float m[R], dl[kSpan], dh[kSpan];
       load_f32<T, R>(a.mid_v + t * R, m);
-      lora_up<T, R>(m, a.b_v, static_cast<int64_t>(kv) * a.head_dim + j, half, dl, dh);
+      lora_up<T, R>(m, s_b, j, half, dl, dh);
 #pragma unroll
       for (int i = 0; i < kSpan; ++i) {
         lo[i] = lo[i] + dl[i] * a.scale_v;
@@ -129,7 +145,7 @@ __global__ __launch_bounds__(kThreads) void rope_fwd_kernel(RopeFwdArgs<T> a) {
     if (hd < a.h_q) {
       float m[R], dl[kSpan], dh[kSpan];
       load_f32<T, R>(a.mid_q + t * R, m);
-      lora_up<T, R>(m, a.b_q, static_cast<int64_t>(hd) * a.head_dim + j, half, dl, dh);
+      lora_up<T, R>(m, s_b, j, half, dl, dh);
 #pragma unroll
       for (int i = 0; i < kSpan; ++i) {
         lo[i] = lo[i] + dl[i] * a.scale_q;
@@ -258,7 +274,8 @@ int check_heads(const char* fn, int64_t n_tokens, int32_t h_q, int32_t h_kv, int
     return fail(RUS_ERR_INVALID, "%s: dtype %d not fp16(0)/fp32(1)", fn, dtype);
   if (n_tokens < 0 || n_tokens >= (int64_t(1) << 31))
     return fail(RUS_ERR_INVALID, "%s: n_tokens=%lld", fn, (long long)n_tokens);
-  if (h_q <= 0 || h_kv <= 0 || head_dim <= 0 || head_dim % (2 * kSpan))
+  if (h_q <= 0 || h_kv <= 0 || head_dim <= 0 || head_dim % (2 * kSpan) ||
+      head_dim > 2 * kSpan * kThreads)
     return fail(RUS_ERR_INVALID, "%s: h_q=%d h_kv=%d head_dim=%d (multiple of 16 required)", fn,
                 h_q, h_kv, head_dim);
   if (n_pos <= 0 || stride_cos < head_dim)
@@ -281,9 +298,8 @@ int fwd_typed(const RopeFwdArgs<T>& a, hipStream_t st) {
       !aligned8<T>(a.sin, a.stride_cos) || !aligned(a.q_out, 16) || !aligned(a.k_out, 16) ||
       !aligned(a.v_out, 16))
     return fail(RUS_ERR_INVALID, "rus_qkv_lora_rope_fwd: pointers/strides must be 16-byte aligned");
-  const int64_t slots = static_cast<int64_t>(a.h_q + 2 * a.h_kv) * (a.head_dim / 2 / kSpan);
-  const int64_t threads = a.n_tokens * slots;
-  const dim3 grid(static_cast<unsigned>((threads + kThreads - 1) / kThreads));
+  const int64_t tpb = kThreads / (a.head_dim / 2 / kSpan);  // tokens per head-major block
+  const dim3 grid(static_cast<unsigned>((a.h_q + 2 * a.h_kv) * ((a.n_tokens + tpb - 1) / tpb)));
   if (a.q_lora)
     hipLaunchKernelGGL((rope_fwd_kernel<T, 1, 0>), grid, dim3(kThreads), 0, st, a);
   else
@@ -299,9 +315,10 @@ int fwd_mid(const RopeFwdArgs<f16>& a, int r, hipStream_t st) {
       !aligned(a.b_q, 8) || !aligned(a.b_v, 8))
     return fail(RUS_ERR_INVALID, "%s: pointers/strides must be aligned (16 B rows, 8 B factors)",
                 fn);
-  const int64_t slots = static_cast<int64_t>(a.h_q + 2 * a.h_kv) * (a.head_dim / 2 / kSpan);
-  const int64_t threads = a.n_tokens * slots;
-  const dim3 grid(static_cast<unsigned>((threads + kThreads - 1) / kThreads));
+  if (a.head_dim > kMaxMidHead)
+    return fail(RUS_ERR_UNSUPPORTED, "%s: head_dim %d above %d", fn, a.head_dim, kMaxMidHead);
+  const int64_t tpb = kThreads / (a.head_dim / 2 / kSpan);  // tokens per head-major block
+  const dim3 grid(static_cast<unsigned>((a.h_q + 2 * a.h_kv) * ((a.n_tokens + tpb - 1) / tpb)));
   switch (r) {
     case 4: hipLaunchKernelGGL((rope_fwd_kernel<f16, 2, 4>), grid, dim3(kThreads), 0, st, a); break;
     case 8: hipLaunchKernelGGL((rope_fwd_kernel<f16, 2, 8>), grid, dim3(kThreads), 0, st, a); break;
