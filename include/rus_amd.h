@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define RUS_ABI_VERSION 2
+#define RUS_ABI_VERSION 3
 
 #define RUS_DTYPE_F16 0
 #define RUS_DTYPE_F32 1
@@ -199,6 +199,20 @@ int rus_dropout_keep_bits(const uint64_t* seed, uint64_t stream0, int32_t n_stre
                           uint32_t* bits, void* stream);
 
 /*
+ * Scratch of the rank-r LoRA entry points below: which = RUS_LORA_DOWN (rus_lora_down_fwd),
+ * RUS_LORA_BWD_X (rus_lora_bwd_x) or RUS_LORA_BWD_W (rus_lora_bwd_w). Sets *workspace_floats, the
+ * fp32 elements of the caller's workspace (per-block partial sums, 16-byte aligned), and
+ * *n_counters, the int32 arrival counters that entry point uses. Counters must be zero before
+ * the entry point's first call and are left zero by every call; calls that share counters must
+ * not run concurrently (a buffer per entry point and stream). d_q and d_v are ignored for
+ * RUS_LORA_DOWN. No counterpart in the reference (its products are torch.mm calls that allocate
+ * their own scratch); the sizes follow from the block decomposition of the kernels.
+ */
+enum { RUS_LORA_DOWN = 0, RUS_LORA_BWD_X = 1, RUS_LORA_BWD_W = 2 };
+int rus_lora_workspace_size(int32_t which, int64_t n_tokens, int64_t d, int64_t d_q, int64_t d_v,
+                            int32_t r, int64_t* workspace_floats, int64_t* n_counters);
+
+/*
  * Rank-r LoRA down projections of both branches, fp16 (r in {4, 8, 16, 32}):
  *   mid_q = fp16(x_q A_q^T), mid_v = fp16(x_v A_v^T)   x [n_tokens, d] (row stride stride_x),
  *   A [r, d] row-major, mid [n_tokens, r] contiguous,
@@ -206,11 +220,13 @@ int rus_dropout_keep_bits(const uint64_t* seed, uint64_t stream0, int32_t n_stre
  * rus_dropout_keep_bits (NULL: x_q = x), x_v likewise.
  * Replaces: the dropouts and the first F.linear of each branch, solution/ops.py:775-778 and the
  * recompute ops.py:882-888. d % 16 == 0, stride_x % 8 == 0, x and A 16-byte aligned.
+ * workspace / counters: see rus_lora_workspace_size.
  */
 int rus_lora_down_fwd(const void* x, int64_t n_tokens, int64_t d, int64_t stride_x,
                       const void* a_q, const void* a_v, int32_t r, void* mid_q, void* mid_v,
                       const uint32_t* bits_q, const uint32_t* bits_v, float p_q, float p_v,
-                      void* stream);
+                      float* workspace, int64_t workspace_floats, int32_t* counters,
+                      int64_t n_counters, void* stream);
 
 /*
  * rus_qkv_lora_rope_fwd with the LoRA deltas formed in-kernel from the rank-r factors (fp16):
@@ -237,13 +253,15 @@ int rus_qkv_lora_rope_fwd_mid(const void* qkv, const void* mid_q, const void* mi
  * a_t_q = A_q^T [d, r], b_t_q = B_q^T [r, d_q] (v alike). d_mid_q / d_mid_v are written for
  * rus_lora_bwd_w. Replaces: solution/ops.py:976-978, 980-982 (d_mid and dx_drop products) and
  * 986-992 (mask replay, two F.dropout, d_norm1.add_(dx_q).add_(dx_v)).
- * d % 32 == 0, d_q % 16 == 0, d_v % 16 == 0, stride_dx % 4 == 0.
+ * d % 32 == 0, d_q % 16 == 0, d_v % 16 == 0, stride_dx % 4 == 0; workspace / counters: see
+ * rus_lora_workspace_size.
  */
 int rus_lora_bwd_x(const void* dq_lora, const void* dv_lora, int64_t n_tokens, int64_t d_q,
                    int64_t d_v, const void* a_t_q, const void* a_t_v, const void* b_t_q,
                    const void* b_t_v, int32_t r, int64_t d, void* d_mid_q, void* d_mid_v,
                    void* dx, int64_t stride_dx, const uint32_t* bits_q, const uint32_t* bits_v,
-                   float p_q, float p_v, void* stream);
+                   float p_q, float p_v, float* workspace, int64_t workspace_floats,
+                   int32_t* counters, int64_t n_counters, void* stream);
 
 /*
  * LoRA weight gradients, fp16 (each an fp32 sum over tokens in a fixed order, rounded once):
@@ -252,14 +270,15 @@ int rus_lora_bwd_x(const void* dq_lora, const void* dv_lora, int64_t n_tokens, i
  * x_q / x_v: the dropped LoRA inputs, formed from x [n_tokens, d] (row stride stride_x) and the
  * forward's keep bits as in rus_lora_down_fwd; the [n_tokens, r] operands contiguous and 8-byte
  * aligned. Replaces: solution/ops.py:975, 977, 979, 981 (d_qB, d_qA, d_vB, d_vA as torch.mm in
- * fp16).
+ * fp16). workspace / counters: see rus_lora_workspace_size.
  */
 int rus_lora_bwd_w(const void* x, int64_t stride_x, const uint32_t* bits_q,
                    const uint32_t* bits_v, float p_q, float p_v, const void* dq_lora,
                    const void* dv_lora, const void* mid_q, const void* mid_v,
                    const void* d_mid_q, const void* d_mid_v, int64_t n_tokens, int64_t d,
                    int64_t d_q, int64_t d_v, int32_t r, void* g_a_q, void* g_b_q, void* g_a_v,
-                   void* g_b_v, void* stream);
+                   void* g_b_v, float* workspace, int64_t workspace_floats, int32_t* counters,
+                   int64_t n_counters, void* stream);
 
 /*
  * SwiGLU forward: out = T( g*sigmoid(g) * u ), sigmoid(g) = 1/(1+exp(-g)).

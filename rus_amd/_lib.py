@@ -11,7 +11,7 @@ import threading
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "librus_amd.so"
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 DTYPE_F16 = 0
 DTYPE_F32 = 1
@@ -44,14 +44,16 @@ SIGNATURES: dict[str, list] = {
     "rus_lora_dropout_bwd_add": [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _vp, _u64, _u64, _f32, _f32, _i32, _vp],
     "rus_graph_node_counts": [_vp, _vp, _i32],
     "rus_dropout_keep_bits": [_vp, _u64, _i32, _i64, _i64, _f32, _f32, _vp, _vp],
+    "rus_lora_workspace_size": [_i32, _i64, _i64, _i64, _i64, _i32, ctypes.POINTER(_i64),
+                                ctypes.POINTER(_i64)],
     "rus_lora_down_fwd": [_vp, _i64, _i64, _i64, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _f32, _f32,
-                          _vp],
+                          _vp, _i64, _vp, _i64, _vp],
     "rus_qkv_lora_rope_fwd_mid": [_vp, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp,
                                   _i64, _i64, _i64, _i64, _f32, _f32, _i32, _i32, _i32, _vp, _vp],
     "rus_lora_bwd_x": [_vp, _vp, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _i32, _i64, _vp, _vp, _vp,
-                       _i64, _vp, _vp, _f32, _f32, _vp],
+                       _i64, _vp, _vp, _f32, _f32, _vp, _i64, _vp, _i64, _vp],
     "rus_lora_bwd_w": [_vp, _i64, _vp, _vp, _f32, _f32, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64,
-                       _i64, _i64, _i32, _vp, _vp, _vp, _vp, _vp],
+                       _i64, _i64, _i32, _vp, _vp, _vp, _vp, _vp, _i64, _vp, _i64, _vp],
     "rus_lmhead_ce_loss": [_vp, _vp, _i64, _vp, _vp, _vp, _vp],
     "rus_attn_varlen_fwd": [_vp, _vp, _vp, _vp, _i32, _i64, _i32, _i32, _i32, _i32, _f32, _vp, _vp,
                             _vp],

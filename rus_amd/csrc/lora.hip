@@ -9,18 +9,27 @@
 //   dx += drop_q(dx_q), then += drop_v(dx_v)
 // Dropout masks arrive as packed keep bits (rus_dropout_keep_bits: word w of row t holds
 // elements 32 w .. 32 w + 31), drawn once per step for every layer, so no kernel here runs the
-// generator and no dropped copy of x is stored. Kernels:
-//   * lora_down: one block of 8 waves per 32 tokens; the rank-r products on MFMA
-//     (v_mfma_f32_32x32x16_f16, tokens x ranks, ranks past r zero), the waves splitting the
-//     reduction over D and summing their partials through LDS in a fixed order;
-//   * q_lora / v_lora are formed inside the RoPE kernel from mid and B (rope.hip);
-//   * lora_bwd_x: the same for d_mid = dq B (from rank-major B^T copies), then the expansion
-//     d_mid A as MFMA tiles of dx^T (rank-major A^T copies), with the masks and both rounded adds
-//     into dx in place;
-//   * lora_bwd_w: the four weight gradients (reductions over tokens) on the vector units, one lane
-//     per output column and token phase, 16 columns per block, waves splitting the tokens and
-//     summing through LDS in a fixed order (deterministic).
+// generator and no dropped copy of x is stored.
+//
+// The products are tiny (r = 16) but stream megabytes, so every kernel spreads its bytes over
+// many short blocks:
+//   * the rank-r reductions over D (mid) and over Dq + Dv (d_mid) are split: block (reduction
+//     chunk, 32-token tile) forms an fp32 partial on MFMA (v_mfma_f32_32x32x16_f16, tokens x
+//     ranks; q and v packed into one 32-column accumulator for r <= 16), and the last block of a
+//     tile to finish (per-tile arrival counter) sums the chunks' partials in chunk order and
+//     rounds once: deterministic, in the same launch;
+//   * the expansion d_mid A runs as MFMA tiles of dx^T (32 columns x 32 tokens per wave) with the
+//     masks and both rounded adds into dx in place;
+//   * the weight gradients (reductions over tokens) run on the vector units, one lane per output
+//     column, the tokens split over the waves of a block and over blocks, summed through LDS and
+//     then across blocks by the same last-block rule;
+//   * q_lora / v_lora are formed inside the RoPE kernel from mid and B (rope.hip).
 // Every value the reference rounds to fp16 is rounded here at the same point; sums are fp32.
+// The loads of a batch are issued before any of their uses (a scheduling barrier keeps the
+// compiler from sinking them), so a wave waits on memory once per batch.
+//
+// Workspace: fp32 partials (rus_lora_workspace_size) and int32 arrival counters that are zero
+// when a launch starts and are left zero by it. Launches that share counters must not overlap.
 
 #include "common.h"
 
@@ -31,8 +40,8 @@ typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-constexpr int kTok = 32;  // tokens per block (down, bwd_x)
-constexpr int kMS = 40;   // row stride (halfs) of the fp16 d_mid tile in LDS: 32 ranks + pad
+constexpr int kTok = 32;  // tokens per tile (down, d_mid, expansion)
+constexpr int kSW = 4;    // waves per block (down, d_mid, expansion)
 
 __device__ __forceinline__ f32x16 mfma(f16x8 a, f16x8 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
@@ -61,34 +70,27 @@ __device__ __forceinline__ f16x8 frag_rank(const f16* row, int k0) {
   }
 }
 
-// Waves per block of lora_down / lora_bwd_x and the accumulator layout: for R <= 16 the q and
-// v results share one 32-column accumulator (q in columns 0 .. R-1, v in R .. 2R-1), for R = 32
-// each branch has its own.
+// The reference's fp16 dropout of 8 values (keep bit sh + i of word w for value i).
+__device__ __forceinline__ f16x8 drop8(f16x8 x, uint32_t w, int sh, float scale) {
+  f16x8 r;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const f16 v = static_cast<f16>(static_cast<float>(x[i]) * scale);
+    r[i] = (w >> (sh + i)) & 1u ? v : static_cast<f16>(0.0f);
+  }
+  return r;
+}
+
+// Accumulator layout of the tokens x ranks products: for R <= 16 the q and v results share one
+// 32-column accumulator (q in columns 0 .. R-1, v in R .. 2R-1); for R = 32 each branch has its
+// own.
 template <int R>
 struct Cfg {
   static constexpr bool PACK = R <= 16;
   static constexpr int NACC = PACK ? 1 : 2;
-  static constexpr int W = PACK ? 16 : 8;
 };
 
-// Stores a wave's accumulators in LDS (lane-contiguous) for the fixed-order sum over waves.
-template <int NACC>
-__device__ __forceinline__ void park(float* buf, const f32x16 (&c)[NACC], int wave, int lane) {
-#pragma unroll
-  for (int j = 0; j < NACC; ++j)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) buf[((wave * NACC + j) * 16 + r) * 64 + lane] = c[j][r];
-}
-
-template <int NACC, int W>
-__device__ __forceinline__ float parked_sum(const float* buf, int j, int r, int lane) {
-  float s = 0.0f;
-#pragma unroll
-  for (int w = 0; w < W; ++w) s += buf[((w * NACC + j) * 16 + r) * 64 + lane];
-  return s;
-}
-
-// Branch and rank of accumulator column n of accumulator j (-1: unused column).
+// Branch and rank of column n of accumulator j (branch -1: unused column).
 template <int R>
 __device__ __forceinline__ void col_owner(int j, int n, int& br, int& rank) {
   if constexpr (Cfg<R>::PACK) {
@@ -100,15 +102,97 @@ __device__ __forceinline__ void col_owner(int j, int n, int& br, int& rank) {
   }
 }
 
-// The reference's fp16 dropout of 8 values (keep bit sh + i of word w for value i).
-__device__ __forceinline__ f16x8 drop8(f16x8 x, uint32_t w, int sh, float scale) {
-  f16x8 r;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const f16 v = static_cast<f16>(static_cast<float>(x[i]) * scale);
-    r[i] = (w >> (sh + i)) & 1u ? v : static_cast<f16>(0.0f);
+// Partial sums cross blocks through device-coherent 4-byte accesses (agent-scope relaxed
+// atomics): a store is performed where every XCD's L2 agrees and a load reads from there, so no
+// cache-wide write-back or invalidate (what a device-scope fence costs) is needed.
+__device__ __forceinline__ void store_partial(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ float load_partial(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Called by every thread of a block once its partial is stored (store_partial): true, in every
+// thread, in the last of the n blocks sharing `counter` to arrive, which then reads all n
+// partials (load_partial). Each thread waits for its stores to complete before the block
+// arrives; the last block puts the counter back to 0. No block waits for another.
+__device__ __forceinline__ bool arrive_last(int* counter, int n) {
+  __shared__ int s_last;
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0);  // every memory access of this thread has completed
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const int old = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const bool last = old == n - 1;
+    if (last) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = last ? 1 : 0;
   }
-  return r;
+  __syncthreads();
+  return s_last != 0;
+}
+
+// Split-K end of the tokens x ranks kernels: the waves' accumulators are summed through LDS in
+// wave order into this block's partial part[chunk][tile] (NACC x 1024 fp32 in accumulator
+// order); the last block of the tile sums every chunk's partial in chunk order into tot
+// (element e = threadIdx.x + 256 k of the accumulator order) and returns true.
+template <int NACC>
+__device__ __forceinline__ bool split_reduce(const f32x16 (&acc)[NACC], float* s_park,
+                                             float* __restrict__ part, int* __restrict__ counters,
+                                             int chunk, int n_chunks, int tile, int n_tiles,
+                                             float (&tot)[NACC * 4]) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+#pragma unroll
+  for (int j = 0; j < NACC; ++j)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) s_park[((wave * NACC + j) * 16 + r) * 64 + lane] = acc[j][r];
+  __syncthreads();
+  constexpr int kTile = NACC * 1024;  // floats per partial
+  float* mine = part + (static_cast<int64_t>(chunk) * n_tiles + tile) * kTile;
+#pragma unroll
+  for (int k = 0; k < NACC * 4; ++k) {
+    const int e = threadIdx.x + 256 * k;  // (j, r, lane) = (e >> 10, (e >> 6) & 15, e & 63)
+    float s = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kSW; ++w) s += s_park[w * kTile + e];
+    store_partial(mine + e, s);
+  }
+  if (!arrive_last(counters + tile, n_chunks)) return false;
+#pragma unroll
+  for (int k = 0; k < NACC * 4; ++k) tot[k] = 0.0f;
+  // The partials of kB chunks are loaded together, then added in chunk order.
+  constexpr int kB = NACC == 1 ? 8 : 4;
+  for (int c0 = 0; c0 < n_chunks; c0 += kB) {
+    float v[kB][NACC * 4];
+#pragma unroll
+    for (int b = 0; b < kB; ++b) {
+      const int c = min(c0 + b, n_chunks - 1);
+      const float* pc = part + (static_cast<int64_t>(c) * n_tiles + tile) * kTile;
+#pragma unroll
+      for (int k = 0; k < NACC * 4; ++k) v[b][k] = load_partial(pc + threadIdx.x + 256 * k);
+    }
+#pragma unroll
+    for (int b = 0; b < kB; ++b)
+#pragma unroll
+      for (int k = 0; k < NACC * 4; ++k) tot[k] += c0 + b < n_chunks ? v[b][k] : 0.0f;
+  }
+  return true;
+}
+
+// Stores the totals of split_reduce as fp16 [n_tok, R] rows of the two branches' outputs.
+template <int R>
+__device__ __forceinline__ void store_ranks(const float (&tot)[Cfg<R>::NACC * 4], int64_t t0,
+                                            int64_t n_tok, f16* out_q, f16* out_v) {
+#pragma unroll
+  for (int k = 0; k < Cfg<R>::NACC * 4; ++k) {
+    const int e = threadIdx.x + 256 * k;
+    const int ln = e & 63, r = (e >> 6) & 15, j = e >> 10;
+    int br, rank;
+    col_owner<R>(j, ln & 31, br, rank);
+    const int64_t tt = t0 + acc_row(r, ln >> 5);
+    if (br >= 0 && tt < n_tok) (br ? out_v : out_q)[tt * R + rank] = static_cast<f16>(tot[k]);
+  }
 }
 
 struct DownArgs {
@@ -122,19 +206,22 @@ struct DownArgs {
   const uint32_t* bits_v;
   int64_t words;  // mask words per row
   float scale_q, scale_v;
+  float* part;
+  int* counters;
+  int kc;  // reduction columns per chunk (a multiple of 16 dividing d)
 };
 
-// mid_q = fp16(drop_q(x) A_q^T), mid_v = fp16(drop_v(x) A_v^T). C = tokens x ranks: the A operand
-// is 8 dropped x values of the lane's token, the B operand 8 entries of the A row that owns the
-// lane's column (zeros for unused columns). Wave w takes k-steps w, w + W, ...; the loads of up
-// to U steps are issued together before their MFMAs, so a wave waits on memory once per batch.
+// mid_q = fp16(drop_q(x) A_q^T), mid_v = fp16(drop_v(x) A_v^T). Block (chunk, tile) reduces
+// columns [chunk kc, +kc) for 32 tokens: the A operand is 8 dropped x values of the lane's
+// token, the B operand 8 entries of the A row owning the lane's column (zeros if unused).
 template <int R, bool DROP>
-__global__ __launch_bounds__(64 * Cfg<R>::W) void lora_down_kernel(DownArgs a) {
+__global__ __launch_bounds__(64 * kSW) void lora_down_kernel(DownArgs a) {
   using C = Cfg<R>;
-  constexpr int W = C::W, NACC = C::NACC, U = 6;
-  __shared__ float buf[W * NACC * 16 * 64];
+  constexpr int NACC = C::NACC, U = 2;
+  __shared__ float s_park[kSW * NACC * 1024];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, h = lane >> 5, col = lane & 31;
-  const int64_t t0 = static_cast<int64_t>(blockIdx.x) * kTok;
+  const int chunk = blockIdx.x, tile = blockIdx.y;
+  const int64_t t0 = static_cast<int64_t>(tile) * kTok;
   const int64_t t = min(t0 + col, a.n_tok - 1);  // rows past the end are computed, not stored
   const f16* xrow = a.x + t * a.sx;
   int br0, rk0;
@@ -146,16 +233,16 @@ __global__ __launch_bounds__(64 * Cfg<R>::W) void lora_down_kernel(DownArgs a) {
   const f16* b1 = a.av + (C::PACK ? 0 : col) * a.d;
   const uint32_t* mq = DROP ? a.bits_q + t * a.words : nullptr;
   const uint32_t* mv = DROP ? a.bits_v + t * a.words : nullptr;
-  const int ks = static_cast<int>(a.d / 16);
+  const int ks = a.kc / 16, c_base = chunk * a.kc;
   f32x16 acc[NACC];
 #pragma unroll
   for (int j = 0; j < NACC; ++j) acc[j] = f32x16{};
-  for (int s0 = wave; s0 < ks; s0 += W * U) {
+  for (int s0 = wave; s0 < ks; s0 += kSW * U) {
     f16x8 xs[U], f0[U], f1[U];
     uint32_t wq[U], wv[U];
 #pragma unroll
     for (int i = 0; i < U; ++i) {
-      const int c0 = 16 * min(s0 + W * i, ks - 1) + 8 * h;
+      const int c0 = c_base + 16 * min(s0 + kSW * i, ks - 1) + 8 * h;
       xs[i] = ld8(xrow + c0);
       f0[i] = ld8(b0 + c0);
       if constexpr (!C::PACK) f1[i] = ld8(b1 + c0);
@@ -167,48 +254,97 @@ __global__ __launch_bounds__(64 * Cfg<R>::W) void lora_down_kernel(DownArgs a) {
     __builtin_amdgcn_sched_barrier(0);  // every load of the batch is issued before any MFMA
 #pragma unroll
     for (int i = 0; i < U; ++i) {
-      // Steps past the end add zero products: no branch, so the batch's loads stay in front.
-      if (s0 + W * i >= ks) xs[i] = zero8();
-      const int sh = (16 * min(s0 + W * i, ks - 1) + 8 * h) & 31;
+      // Steps past the chunk add zero products: no branch, so the batch's loads stay in front.
+      if (s0 + kSW * i >= ks) xs[i] = zero8();
+      const int shc = (c_base + 16 * min(s0 + kSW * i, ks - 1) + 8 * h) & 31;  // bit of value 0
       if constexpr (C::PACK) {
         if constexpr (DROP) {
-          acc[0] = mfma(drop8(xs[i], wq[i], sh, a.scale_q), br0 == 0 ? f0[i] : zero8(), acc[0]);
-          acc[0] = mfma(drop8(xs[i], wv[i], sh, a.scale_v), br0 == 1 ? f0[i] : zero8(), acc[0]);
+          acc[0] = mfma(drop8(xs[i], wq[i], shc, a.scale_q), br0 == 0 ? f0[i] : zero8(), acc[0]);
+          acc[0] = mfma(drop8(xs[i], wv[i], shc, a.scale_v), br0 == 1 ? f0[i] : zero8(), acc[0]);
         } else {
           acc[0] = mfma(xs[i], br0 >= 0 ? f0[i] : zero8(), acc[0]);
         }
       } else {
-        const f16x8 xq = DROP ? drop8(xs[i], wq[i], sh, a.scale_q) : xs[i];
-        const f16x8 xv = DROP ? drop8(xs[i], wv[i], sh, a.scale_v) : xs[i];
+        const f16x8 xq = DROP ? drop8(xs[i], wq[i], shc, a.scale_q) : xs[i];
+        const f16x8 xv = DROP ? drop8(xs[i], wv[i], shc, a.scale_v) : xs[i];
         acc[0] = mfma(xq, f0[i], acc[0]);
         acc[NACC - 1] = mfma(xv, f1[i], acc[NACC - 1]);
       }
     }
   }
-  park<NACC>(buf, acc, wave, lane);
-  __syncthreads();
-  for (int e = threadIdx.x; e < NACC * 16 * 64; e += 64 * W) {
-    const int ln = e & 63, r = (e >> 6) & 15, j = e >> 10;
-    int br, rank;
-    col_owner<R>(j, ln & 31, br, rank);
-    const int64_t tt = t0 + acc_row(r, ln >> 5);
-    if (br < 0 || tt >= a.n_tok) continue;
-    (br ? a.mid_v : a.mid_q)[tt * R + rank] =
-        static_cast<f16>(parked_sum<NACC, W>(buf, j, r, ln));
-  }
+  float tot[NACC * 4];
+  if (split_reduce<NACC>(acc, s_park, a.part, a.counters, chunk, gridDim.x, tile, gridDim.y, tot))
+    store_ranks<R>(tot, t0, a.n_tok, a.mid_q, a.mid_v);
 }
 
-struct BwdXArgs {
+struct MidArgs {
   const f16* dq;
   const f16* dv;
   int64_t n_tok, len_q, len_v;
-  const f16* at_q;  // A^T [d, R]
-  const f16* at_v;
   const f16* bt_q;  // B^T [R, len]
   const f16* bt_v;
-  int64_t d;
   f16* dmid_q;
   f16* dmid_v;
+  float* part;
+  int* counters;
+  int kc, chunks_q;  // chunks [0, chunks_q) reduce dq, the rest dv
+};
+
+// d_mid_q = fp16(dq B_q), d_mid_v = fp16(dv B_v): block (chunk, tile) reduces 32 tokens over kc
+// columns of dq (or of dv) against the B^T row owning the lane's column.
+template <int R>
+__global__ __launch_bounds__(64 * kSW) void lora_bwd_mid_kernel(MidArgs a) {
+  using C = Cfg<R>;
+  constexpr int NACC = C::NACC, U = 2;
+  __shared__ float s_park[kSW * NACC * 1024];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, h = lane >> 5, col = lane & 31;
+  const int chunk = blockIdx.x, tile = blockIdx.y;
+  const int64_t t0 = static_cast<int64_t>(tile) * kTok;
+  const int64_t t = min(t0 + col, a.n_tok - 1);
+  int br0, rk0;
+  col_owner<R>(0, col, br0, rk0);
+  const bool is_q = chunk < a.chunks_q;  // uniform over the block
+  const bool use = C::PACK ? br0 == (is_q ? 0 : 1) : true;
+  const int64_t len = is_q ? a.len_q : a.len_v;
+  const f16* xrow = (is_q ? a.dq : a.dv) + t * len;
+  const f16* brow = (is_q ? a.bt_q : a.bt_v) + (C::PACK ? (use ? rk0 : 0) : col) * len;
+  const int c_base = (is_q ? chunk : chunk - a.chunks_q) * a.kc;
+  const int ks = a.kc / 16;
+  f32x16 acc[NACC];
+#pragma unroll
+  for (int j = 0; j < NACC; ++j) acc[j] = f32x16{};
+  f32x16 sum = f32x16{};
+  for (int s0 = wave; s0 < ks; s0 += kSW * U) {
+    f16x8 xs[U], fs[U];
+#pragma unroll
+    for (int i = 0; i < U; ++i) {
+      const int c0 = c_base + 16 * min(s0 + kSW * i, ks - 1) + 8 * h;
+      xs[i] = ld8(xrow + c0);
+      fs[i] = ld8(brow + c0);
+    }
+    __builtin_amdgcn_sched_barrier(0);  // every load of the batch is issued before any MFMA
+#pragma unroll
+    for (int i = 0; i < U; ++i) {
+      const f16x8 xi = s0 + kSW * i < ks ? xs[i] : zero8();
+      sum = mfma(xi, use ? fs[i] : zero8(), sum);
+    }
+  }
+  // The chunk's branch owns accumulator 0 (PACK: both branches share it) or NACC - 1 (v, R = 32).
+  if (C::PACK || is_q)
+    acc[0] = sum;
+  else
+    acc[NACC - 1] = sum;
+  float tot[NACC * 4];
+  if (split_reduce<NACC>(acc, s_park, a.part, a.counters, chunk, gridDim.x, tile, gridDim.y, tot))
+    store_ranks<R>(tot, t0, a.n_tok, a.dmid_q, a.dmid_v);
+}
+
+struct ExpandArgs {
+  const f16* dmid_q;
+  const f16* dmid_v;
+  const f16* at_q;  // A^T [d, R]
+  const f16* at_v;
+  int64_t n_tok, d;
   f16* dx;
   int64_t sdx;
   const uint32_t* bits_q;
@@ -217,134 +353,53 @@ struct BwdXArgs {
   float scale_q, scale_v;
 };
 
-// acc += sum over the wave's k-steps s = first, first + W, ... < ks of the MFMA of 8 values of
-// row x and of row bt at 16 s + 8 h (bt zeroed when use is false). Loads of U steps are issued
-// together; steps past the end multiply zeros (no branch between the loads and their MFMAs).
-template <int U, int W>
-__device__ __forceinline__ void reduce_batched(f32x16& acc, const f16* x, const f16* bt, bool use,
-                                               int first, int ks, int h) {
-  for (int s0 = first; s0 < ks; s0 += W * U) {
-    f16x8 xs[U], fs[U];
-#pragma unroll
-    for (int i = 0; i < U; ++i) {
-      const int c0 = 16 * min(s0 + W * i, ks - 1) + 8 * h;
-      xs[i] = ld8(x + c0);
-      fs[i] = ld8(bt + c0);
-    }
-    __builtin_amdgcn_sched_barrier(0);  // every load of the batch is issued before any MFMA
-#pragma unroll
-    for (int i = 0; i < U; ++i) {
-      const f16x8 xi = s0 + W * i < ks ? xs[i] : zero8();
-      acc = mfma(xi, use ? fs[i] : zero8(), acc);
-    }
-  }
-}
-
-// Phase 1: d_mid_q = fp16(dq B_q), d_mid_v = fp16(dv B_v) (tokens x ranks; the k-steps run over
-// the q reduction, then the v one, each with the B^T row owning the lane's column). Phase 2, per
-// 32 columns of dx: dx^T tile = A^T d_mid^T for each branch (MFMA, k = ranks), then per element
-// dx = fp16(fp16(dx + fp16(drop_q(fp16(dx_q)))) + fp16(drop_v(fp16(dx_v)))). In both phases a
-// wave issues the loads of a batch of its steps before their MFMAs.
+// dx = fp16(fp16(dx + fp16(drop_q(fp16(d_mid_q A_q)))) + fp16(drop_v(fp16(d_mid_v A_v)))).
+// Block (column group, tile): wave w forms the dx^T tiles of columns 32 (4 group + w) .. +31 and
+// the tile's 32 tokens (MFMA over the ranks), then updates dx for its lane's token in place.
 template <int R, bool DROP>
-__global__ __launch_bounds__(64 * Cfg<R>::W) void lora_bwd_x_kernel(BwdXArgs a) {
-  using C = Cfg<R>;
-  constexpr int W = C::W, NACC = C::NACC, U = 8, U2 = 3;
-  __shared__ float buf[W * NACC * 16 * 64];
-  __shared__ __attribute__((aligned(16))) f16 s_mid[2][kTok][kMS];
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, h = lane >> 5, col = lane & 31;
-  const int64_t t0 = static_cast<int64_t>(blockIdx.x) * kTok;
-  const int64_t t = min(t0 + col, a.n_tok - 1);
-  int br0, rk0;
-  col_owner<R>(0, col, br0, rk0);
-  const int ksq = static_cast<int>(a.len_q / 16), ksv = static_cast<int>(a.len_v / 16);
-  // The lane's B^T rows for q-steps and v-steps, and whether it contributes to each.
-  const bool in_q = C::PACK ? br0 == 0 : true;
-  const bool in_v = C::PACK ? br0 == 1 : true;
-  const f16* bq = a.bt_q + (C::PACK ? (in_q ? rk0 : 0) : col) * a.len_q;
-  const f16* bv = a.bt_v + (C::PACK ? (in_v ? rk0 : 0) : col) * a.len_v;
-  const f16* xq = a.dq + t * a.len_q;
-  const f16* xv = a.dv + t * a.len_v;
-  f32x16 acc[NACC];
-#pragma unroll
-  for (int j = 0; j < NACC; ++j) acc[j] = f32x16{};
-  reduce_batched<U, W>(acc[0], xq, bq, in_q, wave, ksq, h);
-  reduce_batched<U, W>(acc[NACC - 1], xv, bv, in_v, wave, ksv, h);
-  park<NACC>(buf, acc, wave, lane);
-  __syncthreads();
-  for (int e = threadIdx.x; e < 2 * kTok * 32; e += 64 * W) {  // every (branch, row, rank<32)
-    const int br = e >> 10, row = (e >> 5) & 31, n = e & 31;
-    f16 v = static_cast<f16>(0.0f);
-    if (n < R) {
-      // accumulator j, column cc and register r holding (branch br, token row, rank n)
-      const int j = C::PACK ? 0 : br, cc = C::PACK ? br * R + n : n;
-      const int hh = (row >> 2) & 1, r = ((row >> 3) << 2) | (row & 3);
-      v = static_cast<f16>(parked_sum<NACC, W>(buf, j, r, hh * 32 + cc));
-      const int64_t tt = t0 + row;
-      if (tt < a.n_tok) (br ? a.dmid_v : a.dmid_q)[tt * R + n] = v;
-    }
-    s_mid[br][row][n] = v;  // ranks past R are zero operands below
-  }
-  __syncthreads();
-
-  // Phase 2. This lane's token is column col of every dx^T tile; rows past the end read row
-  // n_tok - 1 and are not stored.
+__global__ __launch_bounds__(64 * kSW) void lora_bwd_expand_kernel(ExpandArgs a) {
   constexpr int KS = R > 16 ? 2 : 1;
-  f16x8 mq[KS], mv[KS];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, h = lane >> 5, col = lane & 31;
+  const int dt = blockIdx.x * kSW + wave;  // 32-column tile of dx
+  if (dt * 32 >= a.d) return;              // (no barrier in this kernel)
+  const int64_t t0 = static_cast<int64_t>(blockIdx.y) * kTok;
+  const int64_t t = min(t0 + col, a.n_tok - 1);  // this lane's token (column of dx^T)
+  const int64_t drow = static_cast<int64_t>(dt) * 32 + col;  // A-operand row of this lane
+  f16x8 aq[KS], av[KS], mq[KS], mv[KS];
 #pragma unroll
   for (int j = 0; j < KS; ++j) {
-    mq[j] = *reinterpret_cast<const f16x8*>(&s_mid[0][col][16 * j + 8 * h]);
-    mv[j] = *reinterpret_cast<const f16x8*>(&s_mid[1][col][16 * j + 8 * h]);
+    aq[j] = frag_rank<R>(a.at_q + drow * R, 16 * j + 8 * h);
+    av[j] = frag_rank<R>(a.at_v + drow * R, 16 * j + 8 * h);
+    mq[j] = frag_rank<R>(a.dmid_q + t * R, 16 * j + 8 * h);
+    mv[j] = frag_rank<R>(a.dmid_v + t * R, 16 * j + 8 * h);
   }
-  const bool tok_ok = t0 + col < a.n_tok;
-  const int n_dt = static_cast<int>(a.d / 32);
-  f16* dxrow = a.dx + t * a.sdx;
-  const uint32_t* wbq = DROP ? a.bits_q + t * a.words : nullptr;
-  const uint32_t* wbv = DROP ? a.bits_v + t * a.words : nullptr;
-  for (int d0 = wave; d0 < n_dt; d0 += W * U2) {
-    f16x8 aq[U2][KS], av[U2][KS];
-    f16x4 dxv[U2][4];
-    uint32_t wq[U2], wv[U2];
+  f16* p = a.dx + t * a.sdx + static_cast<int64_t>(dt) * 32;
+  f16x4 cur[4];
 #pragma unroll
-    for (int i = 0; i < U2; ++i) {
-      const int dt = min(d0 + W * i, n_dt - 1);
-      const int64_t drow = static_cast<int64_t>(dt) * 32 + col;  // A-operand row of this lane
+  for (int r4 = 0; r4 < 4; ++r4) cur[r4] = *reinterpret_cast<const f16x4*>(p + 8 * r4 + 4 * h);
+  const uint32_t wq = DROP ? a.bits_q[t * a.words + dt] : 0xffffffffu;
+  const uint32_t wv = DROP ? a.bits_v[t * a.words + dt] : 0xffffffffu;
+  __builtin_amdgcn_sched_barrier(0);  // every load is issued before any MFMA
+  f32x16 oq = f32x16{}, ov = f32x16{};
 #pragma unroll
-      for (int j = 0; j < KS; ++j) {
-        aq[i][j] = frag_rank<R>(a.at_q + drow * R, 16 * j + 8 * h);
-        av[i][j] = frag_rank<R>(a.at_v + drow * R, 16 * j + 8 * h);
-      }
+  for (int j = 0; j < KS; ++j) {
+    oq = mfma(aq[j], mq[j], oq);
+    ov = mfma(av[j], mv[j], ov);
+  }
+  if (t0 + col >= a.n_tok) return;
 #pragma unroll
-      for (int r4 = 0; r4 < 4; ++r4)
-        dxv[i][r4] = *reinterpret_cast<const f16x4*>(dxrow + dt * 32 + 8 * r4 + 4 * h);
-      wq[i] = DROP ? wbq[dt] : 0xffffffffu;
-      wv[i] = DROP ? wbv[dt] : 0xffffffffu;
+  for (int r4 = 0; r4 < 4; ++r4) {
+    const int off = 8 * r4 + 4 * h;
+    f16x4 c = cur[r4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int r = 4 * r4 + k, bit = off + k;
+      const float hq = round16(oq[r]), hv = round16(ov[r]);  // fp16 dx_q, dx_v
+      const float tq = round16((wq >> bit) & 1u ? hq * a.scale_q : 0.0f);
+      const float tv = round16((wv >> bit) & 1u ? hv * a.scale_v : 0.0f);
+      c[k] = static_cast<f16>(round16(static_cast<float>(c[k]) + tq) + tv);
     }
-    __builtin_amdgcn_sched_barrier(0);  // every load of the batch is issued before any MFMA
-#pragma unroll
-    for (int i = 0; i < U2; ++i) {
-      const int dt = min(d0 + W * i, n_dt - 1);
-      const bool store = tok_ok && d0 + W * i < n_dt;  // tiles past the end are not written
-      f32x16 oq = f32x16{}, ov = f32x16{};
-#pragma unroll
-      for (int j = 0; j < KS; ++j) {
-        oq = mfma(aq[i][j], mq[j], oq);
-        ov = mfma(av[i][j], mv[j], ov);
-      }
-#pragma unroll
-      for (int r4 = 0; r4 < 4; ++r4) {
-        const int off = 8 * r4 + 4 * h;
-        f16x4 c = dxv[i][r4];
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          const int r = 4 * r4 + k, bit = off + k;
-          const float hq = round16(oq[r]), hv = round16(ov[r]);  // fp16 dx_q, dx_v
-          const float tq = round16((wq[i] >> bit) & 1u ? hq * a.scale_q : 0.0f);
-          const float tv = round16((wv[i] >> bit) & 1u ? hv * a.scale_v : 0.0f);
-          c[k] = static_cast<f16>(round16(static_cast<float>(c[k]) + tq) + tv);
-        }
-        if (store) *reinterpret_cast<f16x4*>(dxrow + dt * 32 + off) = c;
-      }
-    }
+    *reinterpret_cast<f16x4*>(p + off) = c;
   }
 }
 
@@ -367,7 +422,9 @@ __device__ __forceinline__ void load_row(const f16* __restrict__ p, float (&o)[R
 
 // Weight gradients: G[c, j] = fp16(sum_t X[t, c] * M[t, j]) over four (X, M, G) problems laid
 // end to end in column space: A_q (X = drop_q(x), M = d_mid_q, G stored [R, D]), B_q (X = dq,
-// M = mid_q, G [Dq, R]), A_v, B_v. Block: 16 columns x (4 token phases per wave x 16 waves).
+// M = mid_q, G [Dq, R]), A_v, B_v. Block (column block, token chunk): 64 columns, one per lane,
+// x kWTok tokens split over kWWaves waves; partials [R][64] are summed across the chunks of a
+// column block by its last block.
 struct BwdWArgs {
   const f16* x[4];
   int64_t sx[4];
@@ -379,29 +436,31 @@ struct BwdWArgs {
   int32_t transposed[4];  // G stored [R, cols]
   int64_t first_block[5];
   int64_t n_tok, words;
+  float* part;
+  int* counters;
 };
 
-constexpr int kWCols = 8;    // columns per block
-constexpr int kWPh = 8;      // token phases per wave
-constexpr int kWWaves = 16;  // waves per block
+constexpr int kWCols = 64;   // columns per block
+constexpr int kWWaves = 8;   // waves per block
+constexpr int kWTok = 128;   // tokens per chunk
 
-// acc[j] += sum over this lane's tokens of X[t, c] * M[t, j] (X dropped with the keep bits
-// when MASK), tokens w * kWPh + ph + k * kWPh * kWWaves in batches of U whose loads are issued
-// together; past the end (or for a dead column) the weight is zero.
+// acc[j] += sum over tokens first, first + kWWaves, ... < t_end of X[t, c] * M[t, j] (X dropped
+// with the keep bits when MASK) in batches of U whose loads are issued together; past the end
+// (or for a dead column) the weight is zero.
 template <int R, bool MASK>
 __device__ __forceinline__ void bwd_w_tokens(float (&acc)[R], const f16* __restrict__ x,
                                              int64_t sx, const uint32_t* __restrict__ bits,
                                              float scale, const f16* __restrict__ m, int64_t c,
-                                             bool live, int64_t n_tok, int64_t words, int first) {
-  constexpr int U = R >= 32 ? 3 : 6;  // smaller batches keep 32 accumulators in registers
-  constexpr int64_t kStride = kWPh * kWWaves;
-  for (int64_t tb = first; tb < n_tok; tb += U * kStride) {
+                                             bool live, int64_t first, int64_t t_end,
+                                             int64_t words) {
+  constexpr int U = R >= 32 ? 4 : 8;  // smaller batches keep 32 accumulators in registers
+  for (int64_t tb = first; tb < t_end; tb += U * kWWaves) {
     float xv[U], mv[U][R];
     uint32_t word[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int64_t tt = tb + u * kStride;
-      const int64_t tc = tt < n_tok ? tt : n_tok - 1;
+      const int64_t tt = tb + u * kWWaves;
+      const int64_t tc = tt < t_end ? tt : t_end - 1;
       xv[u] = static_cast<float>(x[tc * sx + c]);
       if constexpr (MASK) word[u] = bits[tc * words + (c >> 5)];
       load_row<R>(m + tc * R, mv[u]);
@@ -411,7 +470,7 @@ __device__ __forceinline__ void bwd_w_tokens(float (&acc)[R], const f16* __restr
     for (int u = 0; u < U; ++u) {
       float v = xv[u];
       if constexpr (MASK) v = (word[u] >> (c & 31)) & 1u ? round16(v * scale) : 0.0f;
-      v = (tb + u * kStride < n_tok && live) ? v : 0.0f;
+      v = (tb + u * kWWaves < t_end && live) ? v : 0.0f;
 #pragma unroll
       for (int j = 0; j < R; ++j) acc[j] = __builtin_fmaf(v, mv[u][j], acc[j]);
     }
@@ -420,44 +479,72 @@ __device__ __forceinline__ void bwd_w_tokens(float (&acc)[R], const f16* __restr
 
 template <int R>
 __global__ __launch_bounds__(64 * kWWaves) void lora_bwd_w_kernel(BwdWArgs a) {
-  __shared__ float s_acc[kWWaves][kWCols][R + 1];
+  constexpr int RS = R < 16 ? R : 16;  // ranks summed through LDS per pass
+  __shared__ float s_acc[kWWaves][RS][kWCols];
+  const int blk = blockIdx.x, chunk = blockIdx.y;
   int p = 0;
 #pragma unroll
-  for (int k = 1; k < 4; ++k) p += blockIdx.x >= a.first_block[k] ? 1 : 0;
-  const int64_t c0 = (blockIdx.x - a.first_block[p]) * kWCols;
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, cl = lane & (kWCols - 1);
-  const int ph = lane / kWCols;
-  const int64_t c = c0 + cl;
+  for (int k = 1; k < 4; ++k) p += blk >= a.first_block[k] ? 1 : 0;
+  const int64_t c0 = (blk - a.first_block[p]) * kWCols;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int64_t c = c0 + lane;
   const bool live = c < a.cols[p];
   const int64_t cc = live ? c : c0;  // column read (clamped into the problem)
+  const int64_t t_begin = static_cast<int64_t>(chunk) * kWTok;
+  const int64_t t_end = min(t_begin + kWTok, a.n_tok);
   float acc[R];
 #pragma unroll
   for (int j = 0; j < R; ++j) acc[j] = 0.0f;
   if (a.bits[p])  // uniform over the block
-    bwd_w_tokens<R, true>(acc, a.x[p], a.sx[p], a.bits[p], a.scale[p], a.m[p], cc, live, a.n_tok,
-                          a.words, w * kWPh + ph);
+    bwd_w_tokens<R, true>(acc, a.x[p], a.sx[p], a.bits[p], a.scale[p], a.m[p], cc, live,
+                          t_begin + w, t_end, a.words);
   else
-    bwd_w_tokens<R, false>(acc, a.x[p], a.sx[p], nullptr, 1.0f, a.m[p], cc, live, a.n_tok,
-                           a.words, w * kWPh + ph);
+    bwd_w_tokens<R, false>(acc, a.x[p], a.sx[p], nullptr, 1.0f, a.m[p], cc, live, t_begin + w,
+                           t_end, a.words);
+  constexpr int kPart = R * kWCols;  // floats per partial, rank-major [R][64]
+  float* mine = a.part + (static_cast<int64_t>(chunk) * gridDim.x + blk) * kPart;
 #pragma unroll
-  for (int j = 0; j < R; ++j) {  // the eight token phases of the column (same order every run)
-    acc[j] += __shfl_xor(acc[j], 8, 64);
-    acc[j] += __shfl_xor(acc[j], 16, 64);
-    acc[j] += __shfl_xor(acc[j], 32, 64);
+  for (int j0 = 0; j0 < R; j0 += RS) {
+#pragma unroll
+    for (int j = 0; j < RS; ++j) s_acc[w][j][lane] = acc[j0 + j];
+    __syncthreads();
+    for (int o = threadIdx.x; o < RS * kWCols; o += 64 * kWWaves) {
+      float s = 0.0f;
+#pragma unroll
+      for (int ww = 0; ww < kWWaves; ++ww) s += s_acc[ww][o / kWCols][o % kWCols];
+      store_partial(mine + j0 * kWCols + o, s);
+    }
+    __syncthreads();
   }
-  if (ph == 0) {
+  if (!arrive_last(a.counters + blk, gridDim.y)) return;
+  // Every thread owns kO outputs; the partials of kB chunks are loaded together, then added in
+  // chunk order.
+  constexpr int kThr = 64 * kWWaves, kO = (kPart + kThr - 1) / kThr, kB = kO > 2 ? 4 : 8;
+  const int n_ch = static_cast<int>(gridDim.y);
+  float tot[kO];
 #pragma unroll
-    for (int j = 0; j < R; ++j) s_acc[w][cl][j] = acc[j];
+  for (int i = 0; i < kO; ++i) tot[i] = 0.0f;
+  for (int ch0 = 0; ch0 < n_ch; ch0 += kB) {
+    float v[kB][kO];
+#pragma unroll
+    for (int b = 0; b < kB; ++b) {
+      const float* pc =
+          a.part + (static_cast<int64_t>(min(ch0 + b, n_ch - 1)) * gridDim.x + blk) * kPart;
+#pragma unroll
+      for (int i = 0; i < kO; ++i) v[b][i] = load_partial(pc + min<int>(threadIdx.x + kThr * i, kPart - 1));
+    }
+#pragma unroll
+    for (int b = 0; b < kB; ++b)
+#pragma unroll
+      for (int i = 0; i < kO; ++i) tot[i] += ch0 + b < n_ch ? v[b][i] : 0.0f;
   }
-  __syncthreads();
-  for (int o = threadIdx.x; o < kWCols * R; o += 64 * kWWaves) {
-    const int ci = o / R, j = o % R;
-    const int64_t col = c0 + ci;
-    if (col >= a.cols[p]) continue;
-    float sum = 0.0f;
 #pragma unroll
-    for (int ww = 0; ww < kWWaves; ++ww) sum += s_acc[ww][ci][j];
-    const f16 hs = static_cast<f16>(sum);
+  for (int i = 0; i < kO; ++i) {
+    const int o = threadIdx.x + kThr * i;
+    const int j = o / kWCols;
+    const int64_t col = c0 + o % kWCols;
+    if (o >= kPart || col >= a.cols[p]) continue;
+    const f16 hs = static_cast<f16>(tot[i]);
     if (a.transposed[p])
       a.g[p][j * a.cols[p] + col] = hs;
     else
@@ -473,15 +560,90 @@ int check_p(const char* fn, float pq, float pv) {
   return RUS_OK;
 }
 
+// Largest chunk of {128, 64, 32, 16} columns dividing both lengths (0: none).
+int chunk_cols(int64_t a, int64_t b) {
+  for (int kc = 128; kc >= 16; kc /= 2)
+    if (a % kc == 0 && b % kc == 0) return kc;
+  return 0;
+}
+
+int64_t tiles(int64_t n) { return (n + kTok - 1) / kTok; }
+
+int64_t w_blocks(int64_t d, int64_t d_q, int64_t d_v) {
+  return 2 * ((d + kWCols - 1) / kWCols) + (d_q + kWCols - 1) / kWCols +
+         (d_v + kWCols - 1) / kWCols;
+}
+
+int64_t w_chunks(int64_t n) { return n > 0 ? (n + kWTok - 1) / kWTok : 1; }
+
+// Workspace floats and counters of each entry point (see rus_lora_workspace_size).
+void scratch_need(int which, int64_t n, int64_t d, int64_t d_q, int64_t d_v, int r,
+                  int64_t& floats, int64_t& counters) {
+  const int64_t per = (r > 16 ? 2 : 1) * 1024;  // floats per tokens x ranks partial
+  floats = counters = 0;
+  if (which == RUS_LORA_DOWN) {
+    const int kc = chunk_cols(d, d);
+    floats = kc ? (d / kc) * tiles(n) * per : 0;
+    counters = tiles(n);
+  } else if (which == RUS_LORA_BWD_X) {
+    const int kc = chunk_cols(d_q, d_v);
+    floats = kc ? (d_q / kc + d_v / kc) * tiles(n) * per : 0;
+    counters = tiles(n);
+  } else {
+    const int64_t nb = w_blocks(d, d_q, d_v);
+    floats = w_chunks(n) * nb * r * kWCols;
+    counters = nb;
+  }
+}
+
+constexpr int64_t kMaxCounters = 65536;  // bound on each entry point's counters
+
 }  // namespace
 }  // namespace rus
 
 using rus::f16;
 
+extern "C" int rus_lora_workspace_size(int32_t which, int64_t n_tokens, int64_t d, int64_t d_q,
+                                       int64_t d_v, int32_t r, int64_t* workspace_floats,
+                                       int64_t* n_counters) {
+  using namespace rus;
+  const char* fn = "rus_lora_workspace_size";
+  if (which != RUS_LORA_DOWN && which != RUS_LORA_BWD_X && which != RUS_LORA_BWD_W)
+    return fail(RUS_ERR_INVALID, "%s: unknown entry point %d", fn, which);
+  if (!workspace_floats || !n_counters) return fail(RUS_ERR_INVALID, "%s: null output", fn);
+  if (!rank_ok(r)) return fail(RUS_ERR_UNSUPPORTED, "%s: rank %d not in {4,8,16,32}", fn, r);
+  if (n_tokens < 0 || d <= 0 || d_q <= 0 || d_v <= 0)
+    return fail(RUS_ERR_INVALID, "%s: bad lengths", fn);
+  scratch_need(which, n_tokens, d, d_q, d_v, r, *workspace_floats, *n_counters);
+  return RUS_OK;
+}
+
+// Common checks of the workspace arguments.
+static int check_scratch(const char* fn, int which, int64_t n, int64_t d, int64_t d_q,
+                         int64_t d_v, int r, const float* workspace, int64_t workspace_floats,
+                         const int32_t* counters, int64_t n_counters) {
+  using namespace rus;
+  if (!workspace || !counters) return fail(RUS_ERR_INVALID, "%s: null workspace or counters", fn);
+  if (!aligned(workspace, 16) || !aligned(counters, 4))
+    return fail(RUS_ERR_INVALID, "%s: misaligned workspace or counters", fn);
+  int64_t need_f, need_c;
+  scratch_need(which, n, d, d_q, d_v, r, need_f, need_c);
+  if (need_c > kMaxCounters)
+    return fail(RUS_ERR_UNSUPPORTED, "%s: needs %lld counters (at most %lld)", fn,
+                static_cast<long long>(need_c), static_cast<long long>(kMaxCounters));
+  if (workspace_floats < need_f || n_counters < need_c)
+    return fail(RUS_ERR_INVALID, "%s: workspace holds %lld floats and %lld counters, needs %lld "
+                "and %lld", fn, static_cast<long long>(workspace_floats),
+                static_cast<long long>(n_counters), static_cast<long long>(need_f),
+                static_cast<long long>(need_c));
+  return RUS_OK;
+}
+
 extern "C" int rus_lora_down_fwd(const void* x, int64_t n_tokens, int64_t d, int64_t stride_x,
                                  const void* a_q, const void* a_v, int32_t r, void* mid_q,
                                  void* mid_v, const uint32_t* bits_q, const uint32_t* bits_v,
-                                 float p_q, float p_v, void* stream) {
+                                 float p_q, float p_v, float* workspace, int64_t workspace_floats,
+                                 int32_t* counters, int64_t n_counters, void* stream) {
   using namespace rus;
   const char* fn = "rus_lora_down_fwd";
   if ((bits_q == nullptr) != (bits_v == nullptr))
@@ -497,20 +659,25 @@ extern "C" int rus_lora_down_fwd(const void* x, int64_t n_tokens, int64_t d, int
     return fail(RUS_ERR_INVALID, "%s: x and A must be 16-byte aligned", fn);
   if (int e = check_p(fn, p_q, p_v)) return e;
   if (n_tokens >= (int64_t(1) << 31)) return fail(RUS_ERR_UNSUPPORTED, "%s: too many tokens", fn);
+  if (int e = check_scratch(fn, RUS_LORA_DOWN, n_tokens, d, 16, 16, r, workspace,
+                            workspace_floats, counters, n_counters))
+    return e;
   if (n_tokens == 0) return RUS_OK;
+  const int kc = chunk_cols(d, d);
+  if (tiles(n_tokens) > 65535) return fail(RUS_ERR_UNSUPPORTED, "%s: too many tokens", fn);
   DownArgs a{static_cast<const f16*>(x), stride_x, n_tokens, d,
              static_cast<const f16*>(a_q), static_cast<const f16*>(a_v),
              static_cast<f16*>(mid_q), static_cast<f16*>(mid_v), bits_q, bits_v,
              (d + 31) / 32, bits_q ? 1.0f / (1.0f - p_q) : 1.0f,
-             bits_v ? 1.0f / (1.0f - p_v) : 1.0f};
-  const dim3 grid(static_cast<uint32_t>((n_tokens + kTok - 1) / kTok));
+             bits_v ? 1.0f / (1.0f - p_v) : 1.0f, workspace, counters, kc};
+  const dim3 grid(static_cast<uint32_t>(d / kc), static_cast<uint32_t>(tiles(n_tokens)));
   hipStream_t st = static_cast<hipStream_t>(stream);
-#define RUS_DOWN(RR)                                                                  \
-  case RR:                                                                            \
-    if (bits_q)                                                                       \
-      hipLaunchKernelGGL((lora_down_kernel<RR, true>), grid, dim3(64 * Cfg<RR>::W), 0, st, a); \
-    else                                                                              \
-      hipLaunchKernelGGL((lora_down_kernel<RR, false>), grid, dim3(64 * Cfg<RR>::W), 0, st, a); \
+#define RUS_DOWN(RR)                                                                      \
+  case RR:                                                                                \
+    if (bits_q)                                                                           \
+      hipLaunchKernelGGL((lora_down_kernel<RR, true>), grid, dim3(64 * kSW), 0, st, a);  \
+    else                                                                                  \
+      hipLaunchKernelGGL((lora_down_kernel<RR, false>), grid, dim3(64 * kSW), 0, st, a); \
     break;
   switch (r) { RUS_DOWN(4) RUS_DOWN(8) RUS_DOWN(16) RUS_DOWN(32) }
 #undef RUS_DOWN
@@ -522,7 +689,8 @@ extern "C" int rus_lora_bwd_x(const void* dq_lora, const void* dv_lora, int64_t 
                               const void* b_t_q, const void* b_t_v, int32_t r, int64_t d,
                               void* d_mid_q, void* d_mid_v, void* dx, int64_t stride_dx,
                               const uint32_t* bits_q, const uint32_t* bits_v, float p_q,
-                              float p_v, void* stream) {
+                              float p_v, float* workspace, int64_t workspace_floats,
+                              int32_t* counters, int64_t n_counters, void* stream) {
   using namespace rus;
   const char* fn = "rus_lora_bwd_x";
   if ((bits_q == nullptr) != (bits_v == nullptr))
@@ -537,25 +705,39 @@ extern "C" int rus_lora_bwd_x(const void* dq_lora, const void* dv_lora, int64_t 
   const uintptr_t a_al = r >= 8 ? 16 : 8;
   if (!aligned(dq_lora, 16) || !aligned(dv_lora, 16) || !aligned(a_t_q, a_al) ||
       !aligned(a_t_v, a_al) || !aligned(b_t_q, 16) || !aligned(b_t_v, 16) || !aligned(dx, 8) ||
-      !aligned(d_mid_q, 2) || !aligned(d_mid_v, 2) || !aligned(bits_q, 4) || !aligned(bits_v, 4))
+      !aligned(d_mid_q, a_al) || !aligned(d_mid_v, a_al) || !aligned(bits_q, 4) ||
+      !aligned(bits_v, 4))
     return fail(RUS_ERR_INVALID, "%s: misaligned operand", fn);
   if (int e = check_p(fn, p_q, p_v)) return e;
   if (n_tokens >= (int64_t(1) << 31)) return fail(RUS_ERR_UNSUPPORTED, "%s: too many tokens", fn);
+  if (int e = check_scratch(fn, RUS_LORA_BWD_X, n_tokens, d, d_q, d_v, r, workspace,
+                            workspace_floats, counters, n_counters))
+    return e;
   if (n_tokens == 0) return RUS_OK;
-  BwdXArgs a{static_cast<const f16*>(dq_lora), static_cast<const f16*>(dv_lora), n_tokens, d_q,
-             d_v, static_cast<const f16*>(a_t_q), static_cast<const f16*>(a_t_v),
-             static_cast<const f16*>(b_t_q), static_cast<const f16*>(b_t_v), d,
-             static_cast<f16*>(d_mid_q), static_cast<f16*>(d_mid_v), static_cast<f16*>(dx),
-             stride_dx, bits_q, bits_v, (d + 31) / 32,
-             bits_q ? 1.0f / (1.0f - p_q) : 1.0f, bits_v ? 1.0f / (1.0f - p_v) : 1.0f};
-  const dim3 grid(static_cast<uint32_t>((n_tokens + kTok - 1) / kTok));
+  if (tiles(n_tokens) > 65535) return fail(RUS_ERR_UNSUPPORTED, "%s: too many tokens", fn);
+  const int kc = chunk_cols(d_q, d_v);
+  MidArgs m{static_cast<const f16*>(dq_lora), static_cast<const f16*>(dv_lora), n_tokens, d_q,
+            d_v, static_cast<const f16*>(b_t_q), static_cast<const f16*>(b_t_v),
+            static_cast<f16*>(d_mid_q), static_cast<f16*>(d_mid_v), workspace, counters, kc,
+            static_cast<int>(d_q / kc)};
+  ExpandArgs x{static_cast<const f16*>(d_mid_q), static_cast<const f16*>(d_mid_v),
+               static_cast<const f16*>(a_t_q), static_cast<const f16*>(a_t_v), n_tokens, d,
+               static_cast<f16*>(dx), stride_dx, bits_q, bits_v, (d + 31) / 32,
+               bits_q ? 1.0f / (1.0f - p_q) : 1.0f, bits_v ? 1.0f / (1.0f - p_v) : 1.0f};
+  const dim3 grid_m(static_cast<uint32_t>(d_q / kc + d_v / kc),
+                    static_cast<uint32_t>(tiles(n_tokens)));
+  const dim3 grid_x(static_cast<uint32_t>((d / 32 + kSW - 1) / kSW),
+                    static_cast<uint32_t>(tiles(n_tokens)));
   hipStream_t st = static_cast<hipStream_t>(stream);
+  const dim3 blk(64 * kSW);
 #define RUS_BX(RR)                                                                    \
   case RR:                                                                            \
+    hipLaunchKernelGGL((lora_bwd_mid_kernel<RR>), grid_m, blk, 0, st, m);             \
+    if (int e = check_launch(fn)) return e;                                           \
     if (bits_q)                                                                       \
-      hipLaunchKernelGGL((lora_bwd_x_kernel<RR, true>), grid, dim3(64 * Cfg<RR>::W), 0, st, a); \
+      hipLaunchKernelGGL((lora_bwd_expand_kernel<RR, true>), grid_x, blk, 0, st, x);  \
     else                                                                              \
-      hipLaunchKernelGGL((lora_bwd_x_kernel<RR, false>), grid, dim3(64 * Cfg<RR>::W), 0, st, a); \
+      hipLaunchKernelGGL((lora_bwd_expand_kernel<RR, false>), grid_x, blk, 0, st, x); \
     break;
   switch (r) { RUS_BX(4) RUS_BX(8) RUS_BX(16) RUS_BX(32) }
 #undef RUS_BX
@@ -567,7 +749,9 @@ extern "C" int rus_lora_bwd_w(const void* x, int64_t stride_x, const uint32_t* b
                               const void* dv_lora, const void* mid_q, const void* mid_v,
                               const void* d_mid_q, const void* d_mid_v, int64_t n_tokens,
                               int64_t d, int64_t d_q, int64_t d_v, int32_t r, void* g_a_q,
-                              void* g_b_q, void* g_a_v, void* g_b_v, void* stream) {
+                              void* g_b_q, void* g_a_v, void* g_b_v, float* workspace,
+                              int64_t workspace_floats, int32_t* counters, int64_t n_counters,
+                              void* stream) {
   using namespace rus;
   const char* fn = "rus_lora_bwd_w";
   if ((bits_q == nullptr) != (bits_v == nullptr))
@@ -583,6 +767,10 @@ extern "C" int rus_lora_bwd_w(const void* x, int64_t stride_x, const uint32_t* b
     return fail(RUS_ERR_INVALID, "%s: [N, r] operands must be 8-byte aligned", fn);
   if (int e = check_p(fn, p_q, p_v)) return e;
   if (n_tokens >= (int64_t(1) << 31)) return fail(RUS_ERR_UNSUPPORTED, "%s: too many tokens", fn);
+  if (int e = check_scratch(fn, RUS_LORA_BWD_W, n_tokens, d, d_q, d_v, r, workspace,
+                            workspace_floats, counters, n_counters))
+    return e;
+  if (w_chunks(n_tokens) > 65535) return fail(RUS_ERR_UNSUPPORTED, "%s: too many tokens", fn);
   BwdWArgs a;
   const f16* xs[4] = {static_cast<const f16*>(x), static_cast<const f16*>(dq_lora),
                       static_cast<const f16*>(x), static_cast<const f16*>(dv_lora)};
@@ -607,7 +795,10 @@ extern "C" int rus_lora_bwd_w(const void* x, int64_t stride_x, const uint32_t* b
   }
   a.n_tok = n_tokens;
   a.words = (d + 31) / 32;
-  const dim3 grid(static_cast<uint32_t>(a.first_block[4]));
+  a.part = workspace;
+  a.counters = counters;
+  const dim3 grid(static_cast<uint32_t>(a.first_block[4]),
+                  static_cast<uint32_t>(w_chunks(n_tokens)));
   hipStream_t st = static_cast<hipStream_t>(stream);
 #define RUS_BW(RR)                                                                       \
   case RR:                                                                               \

@@ -9,6 +9,7 @@ raises ``RuntimeError``.
 
 from __future__ import annotations
 
+import ctypes
 import math
 
 import torch
@@ -28,6 +29,7 @@ __all__ = [
     "lora_dropout_fwd",
     "lora_dropout_bwd_add",
     "dropout_keep_bits",
+    "lora_workspace_size",
     "lora_down_fwd",
     "qkv_rope_fwd_mid",
     "lora_bwd_x",
@@ -685,6 +687,36 @@ def _bits(fn, bits, n, d, name):
     return bits.data_ptr()
 
 
+LORA_DOWN, LORA_BWD_X, LORA_BWD_W = 0, 1, 2  # RUS_LORA_* of include/rus_amd.h
+LORA_MAX_COUNTERS = 65536  # arrival counters per buffer (the library's bound)
+_lora_counters: dict[tuple[int, int, int], torch.Tensor] = {}
+
+
+def lora_workspace_size(which: int, n: int, d: int, d_q: int, d_v: int, r: int) -> tuple[int, int]:
+    """(fp32 workspace elements, arrival counters) that LoRA entry point ``which``
+    (LORA_DOWN / LORA_BWD_X / LORA_BWD_W) needs for these sizes."""
+    floats, counters = ctypes.c_int64(), ctypes.c_int64()
+    _lib.call("rus_lora_workspace_size", int(which), int(n), int(d), int(d_q), int(d_v), int(r),
+              ctypes.byref(floats), ctypes.byref(counters))
+    return floats.value, counters.value
+
+
+def _lora_scratch(which: int, n: int, d: int, d_q: int, d_v: int, r: int, dev: torch.device):
+    """Workspace (stream-ordered, from torch's caching allocator) and the arrival counters of one
+    LoRA launch. Counters start at zero and every launch leaves them zero, so one buffer serves
+    every launch of an entry point on a stream (launches on one stream never overlap); buffers
+    are kept for the life of the process (captured graphs hold their addresses)."""
+    floats, counters = lora_workspace_size(which, n, d, d_q, d_v, r)
+    ws = torch.empty(max(floats, 4), dtype=torch.float32, device=dev)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    key = (dev.index if dev.index is not None else torch.cuda.current_device(), which, stream)
+    cnt = _lora_counters.get(key)
+    if cnt is None:
+        cnt = torch.zeros(LORA_MAX_COUNTERS, dtype=torch.int32, device=dev)
+        _lora_counters[key] = cnt
+    return ws, cnt
+
+
 def lora_down_fwd(x: torch.Tensor, a_q: torch.Tensor, a_v: torch.Tensor,
                   bits_q: torch.Tensor | None = None, bits_v: torch.Tensor | None = None,
                   p_q: float = 0.0, p_v: float = 0.0, out=None):
@@ -713,10 +745,11 @@ def lora_down_fwd(x: torch.Tensor, a_q: torch.Tensor, a_v: torch.Tensor,
         mid_q, mid_v = out
         _lora_operand(fn, mid_q, (n, r), "mid_q")
         _lora_operand(fn, mid_v, (n, r), "mid_v")
+    ws, cnt = _lora_scratch(LORA_DOWN, n, d, 16, 16, r, dev)
     _launch("lora_down", n * d * 2 + 4 * r * d + 4 * n * r + n * d // 4, 4 * n * d * r,
             "rus_lora_down_fwd", x2.data_ptr(), n, d, x2.stride(0), a_q.data_ptr(),
             a_v.data_ptr(), r, mid_q.data_ptr(), mid_v.data_ptr(), bq, bv, float(p_q), float(p_v),
-            _stream(x2))
+            ws.data_ptr(), ws.numel(), cnt.data_ptr(), cnt.numel(), _stream(x2))
     return mid_q, mid_v
 
 
@@ -782,11 +815,13 @@ def lora_bwd_x(dq_lora: torch.Tensor, dv_lora: torch.Tensor, a_t_q: torch.Tensor
     bv = _bits(fn, bits_v, n, d, "bits_v")
     dmq = torch.empty((n, r), dtype=torch.float16, device=dx.device)
     dmv = torch.empty((n, r), dtype=torch.float16, device=dx.device)
+    ws, cnt = _lora_scratch(LORA_BWD_X, n, d, d_q, d_v, r, dx.device)
     _launch("lora_bwd_x", 2 * n * (d_q + d_v + 2 * d + 2 * r) + 4 * r * (d + d_q) + n * d // 4,
             2 * n * r * (d_q + d_v + 2 * d), "rus_lora_bwd_x", dq_lora.data_ptr(),
             dv_lora.data_ptr(), n, d_q, d_v, a_t_q.data_ptr(), a_t_v.data_ptr(),
             b_t_q.data_ptr(), b_t_v.data_ptr(), r, d, dmq.data_ptr(), dmv.data_ptr(),
-            dx2.data_ptr(), dx2.stride(0), bq, bv, float(p_q), float(p_v), _stream(dx2))
+            dx2.data_ptr(), dx2.stride(0), bq, bv, float(p_q), float(p_v), ws.data_ptr(),
+            ws.numel(), cnt.data_ptr(), cnt.numel(), _stream(dx2))
     return dmq, dmv
 
 
@@ -817,12 +852,13 @@ def lora_bwd_w(x: torch.Tensor, dq_lora: torch.Tensor, dv_lora: torch.Tensor,
         _lora_operand(fn, t, shp, nm)
     bq = _bits(fn, bits_q, n, d, "bits_q")
     bv = _bits(fn, bits_v, n, d, "bits_v")
+    ws, cnt = _lora_scratch(LORA_BWD_W, n, d, d_q, d_v, r, x.device)
     _launch("lora_bwd_w", 2 * n * (d + d_q + d_v + 4 * r) + n * d // 4,
             2 * n * r * (2 * d + d_q + d_v), "rus_lora_bwd_w", x2.data_ptr(), x2.stride(0), bq,
             bv, float(p_q), float(p_v), dq_lora.data_ptr(), dv_lora.data_ptr(),
             mid_q.data_ptr(), mid_v.data_ptr(), d_mid_q.data_ptr(), d_mid_v.data_ptr(), n, d,
             d_q, d_v, r, g_a_q.data_ptr(), g_b_q.data_ptr(), g_a_v.data_ptr(), g_b_v.data_ptr(),
-            _stream(mid_q))
+            ws.data_ptr(), ws.numel(), cnt.data_ptr(), cnt.numel(), _stream(mid_q))
 
 
 # ---------------------------------------------------------------------------------------------

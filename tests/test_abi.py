@@ -70,7 +70,12 @@ def test_header_compiles_as_c():
         # keep bits need n_cols % 8 == 0; the LoRA input-gradient kernel d % 32 == 0
         ("rus_dropout_keep_bits", (16, 0, 2, 4, 12, 0.1, 0.1, 16, None), "multiple of 8"),
         ("rus_lora_bwd_x", (16, 16, 4, 64, 64, 16, 16, 16, 16, 16, 48, 16, 16, 16, 48, None,
-                            None, 0.0, 0.0, None), "d % 32"),
+                            None, 0.0, 0.0, 16, 1 << 20, 16, 64, None), "d % 32"),
+        # LoRA workspace smaller than the split reduction needs; no counters
+        ("rus_lora_down_fwd", (16, 100, 64, 64, 16, 16, 16, 16, 16, None, None, 0.0, 0.0, 16, 10,
+                               16, 64, None), "workspace holds"),
+        ("rus_lora_bwd_w", (16, 64, None, None, 0.0, 0.0, 16, 16, 16, 16, 16, 16, 100, 64, 64, 64,
+                            16, 16, 16, 16, 16, 16, 1 << 20, None, 0, None), "counters"),
         # attention: head_dim other than 128, GQA ratio not integral, misaligned output
         ("rus_attn_varlen_fwd", (16, 16, 16, 16, 1, 32, 2, 12, 2, 64, 0.1, 16, 16, None),
          "head_dim"),
@@ -97,3 +102,20 @@ def test_multi_dequant_validates_every_job():
     jobs[1].n_absmax = 1  # second job's absmax too short for its bytes
     with pytest.raises(RuntimeError, match="absmax has 1 entries"):
         _lib.call("rus_nf4_dequant_multi", jobs, 2, 16, 64, 256, None)
+
+
+def test_lora_workspace_sizes_follow_the_block_decomposition():
+    from rus_amd import kernels as K
+
+    # down: d / 128 reduction chunks x ceil(n / 32) token tiles x one 32 x 32 fp32 partial
+    assert K.lora_workspace_size(K.LORA_DOWN, 736, 1536, 1, 1, 16) == (12 * 23 * 1024, 23)
+    # rank 32 keeps the branches in two accumulators; d = 48 reduces in chunks of 16
+    assert K.lora_workspace_size(K.LORA_DOWN, 33, 48, 1, 1, 32) == (3 * 2 * 2048, 2)
+    # d_mid: (d_q + d_v) / 128 chunks per tile
+    assert K.lora_workspace_size(K.LORA_BWD_X, 736, 1536, 1536, 256, 16) == (14 * 23 * 1024, 23)
+    # weight gradients: 64-column blocks over (2 d + d_q + d_v) x 128-token chunks x [r, 64]
+    assert K.lora_workspace_size(K.LORA_BWD_W, 736, 1536, 1536, 256, 16) == \
+        (6 * 76 * 16 * 64, 76)
+    assert K.lora_workspace_size(K.LORA_BWD_W, 0, 1536, 1536, 256, 8) == (76 * 8 * 64, 76)
+    with pytest.raises(RuntimeError, match="unknown entry point"):
+        K.lora_workspace_size(7, 1, 64, 64, 64, 16)

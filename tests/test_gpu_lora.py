@@ -162,6 +162,43 @@ def test_lora_bwd_x_and_w(r, drop, n):
         assert ok, err
 
 
+@pytest.mark.parametrize("r", [16, 32])
+def test_lora_split_reductions_see_each_calls_partials(r):
+    """The rank-r reductions are split over blocks whose partial sums meet in a workspace (and
+    counters) that consecutive calls reuse: back-to-back calls with new inputs must each match
+    the products of their own inputs, and a repeated input reproduces its outputs bit for bit
+    (fixed summation order), whatever ran in between."""
+    n, d, dq_dim, dv_dim = 707, 1536, 1536, 256
+    sets = []
+    for s in range(3):
+        g, x, aq, av, bq, bv = _inputs(n, d, dq_dim, dv_dim, r, seed=500 + s)
+        dq = torch.randn(n, dq_dim, generator=g).half()
+        dv = torch.randn(n, dv_dim, generator=g).half()
+        sets.append((x, aq, av, bq, bv, dq, dv))
+    first = {}
+    for rep in range(2):
+        for i, (x, aq, av, bq, bv, dq, dv) in enumerate(sets):
+            xd, dqd, dvd = x.to(DEV), dq.to(DEV), dv.to(DEV)
+            ts = [t.t().contiguous().to(DEV) for t in (aq, av, bq, bv)]
+            mq, mv = K.lora_down_fwd(xd, aq.to(DEV), av.to(DEV))
+            dmq, dmv = K.lora_bwd_x(dqd, dvd, *ts, torch.zeros_like(xd))
+            gs = [torch.empty(shp, dtype=torch.float16, device=DEV)
+                  for shp in ((r, d), (dq_dim, r), (r, d), (dv_dim, r))]
+            K.lora_bwd_w(xd, dqd, dvd, mq, mv, dmq, dmv, *gs)
+            outs = [t.cpu() for t in (mq, mv, dmq, dmv, *gs)]
+            if rep == 1:
+                assert all(torch.equal(a, b) for a, b in zip(outs, first[i])), i
+                continue
+            first[i] = outs
+            checks = ((outs[0], x, aq.t()), (outs[1], x, av.t()), (outs[2], dq, bq),
+                      (outs[3], dv, bv), (outs[4], outs[2].t(), x), (outs[5], dq.t(), outs[0]),
+                      (outs[6], outs[3].t(), x), (outs[7], dv.t(), outs[1]))
+            for k, (got, a, b) in enumerate(checks):
+                want = (a.float() @ b.float()).half()
+                ok, err = _close(got, want, a=a, b=b)
+                assert ok, (i, k, err)
+
+
 def test_lora_kernels_reject_bad_rank_and_layout():
     x = torch.randn(8, 64, device=DEV).half()
     a = torch.randn(6, 64, device=DEV).half()
