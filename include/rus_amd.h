@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define RUS_ABI_VERSION 3
+#define RUS_ABI_VERSION 4
 
 #define RUS_DTYPE_F16 0
 #define RUS_DTYPE_F32 1
@@ -96,6 +96,32 @@ typedef struct rus_nf4_job {
  */
 int rus_nf4_dequant_multi(const rus_nf4_job* jobs, int32_t n_jobs, const float* code2,
                           int32_t blocksize, int32_t super_blocksize, void* stream);
+
+/*
+ * Product with an NF4 double-quant weight W [w_rows, w_cols] (one job of up to three row
+ * segments, blocksize 64) decoded inside the GEMM main loop; fp16 activations, fp32 sums rounded
+ * once:
+ *   trans = 0: y[m, n] = fp16(sum_k x[m, k] W[n, k] + bias[n])   x [m, w_cols], y [m, w_rows]
+ *   trans = 1: y[m, k] = fp16(sum_n x[m, n] W[n, k])             x [m, w_rows], y [m, w_cols]
+ * W[n, k] is exactly the fp16 value rus_nf4_dequant writes for the job (out_u32 is unused);
+ * segment starts must be whole rows and w_rows, w_cols multiples of 64. Row strides: stride_x
+ * (multiple of 8, x 16-byte aligned), stride_y (multiple of 4, y 8-byte aligned). bias: fp16
+ * [w_rows] or NULL (trans = 0 only).
+ * split: reduction splits (0: the library chooses). rus_nf4_gemm_plan returns the split it will
+ * use and the fp32 workspace elements and int32 counters that split needs (0 when unsplit);
+ * counters must be zero before the first call and are left zero; calls sharing counters must not
+ * run concurrently.
+ * Replaces: dequant_nf4_tensor (solution/kernels.py:572-619) into the shared workspace followed
+ *           by F.linear / torch.mm on it: solution/ops.py:771, 810, 710/720, 714/724 (forward),
+ *           873, 921, 932 (recompute), 934, 939, 949, 993 (backward).
+ */
+int rus_nf4_gemm_plan(int64_t m, int64_t w_rows, int64_t w_cols, int32_t trans, int32_t* split,
+                      int64_t* workspace_floats, int64_t* n_counters);
+int rus_nf4_gemm(const void* x, int64_t m, int64_t stride_x, const rus_nf4_job* w,
+                 const float* code2, int64_t w_rows, int64_t w_cols, int32_t blocksize,
+                 int32_t super_blocksize, int32_t trans, const void* bias, void* y,
+                 int64_t stride_y, int32_t split, float* workspace, int64_t workspace_floats,
+                 int32_t* counters, int64_t n_counters, void* stream);
 
 /*
  * Fused residual add + RMSNorm forward, one row per wavefront.

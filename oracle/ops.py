@@ -94,6 +94,22 @@ def nf4_dequant(
     return out.astype(np.float16).reshape(out_shape)
 
 
+def nf4_gemm(x: torch.Tensor, w16: np.ndarray, trans: bool = False,
+             bias: torch.Tensor | None = None) -> torch.Tensor:
+    """The product the fused NF4 GEMM computes, on the dequantised fp16 weight w16 [rows, cols]
+    (``nf4_dequant``): trans=False -> fp16(x @ w16^T + bias) (F.linear, solution/ops.py:771, 810,
+    710-724), trans=True -> fp16(x @ w16) (torch.mm, solution/ops.py:934, 939, 949, 993). The sum
+    is taken in float64 (the exact value that an fp32-accumulating GEMM approximates) and rounded
+    once to fp16. Pinned by numpy's float64 matmul (a library routine) on exactly representable
+    inputs and by the dequant pins above."""
+    xd = np.asarray(x.float().numpy(), dtype=np.float64)
+    wd = np.asarray(w16, dtype=np.float64)
+    y = xd @ (wd if trans else wd.T)
+    if bias is not None:
+        y = y + np.asarray(bias.float().numpy(), dtype=np.float64)[None, :]
+    return torch.from_numpy(y.astype(np.float16))  # one rounding, float64 -> fp16
+
+
 # ---------------------------------------------------------------------------------------------
 # Residual + RMSNorm — solution/kernels.py:125-199, wrapper ops.py:30-54
 # ---------------------------------------------------------------------------------------------

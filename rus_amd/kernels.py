@@ -20,6 +20,9 @@ from ._lib import DTYPE_F16, DTYPE_F32
 __all__ = [
     "dequant_nf4_tensor",
     "dequant_nf4_segments",
+    "NF4Operand",
+    "nf4_gemm_plan",
+    "nf4_gemm",
     "nf4_absmax2_bases",
     "rms_norm_fwd",
     "rms_norm_bwd",
@@ -273,6 +276,121 @@ def dequant_nf4_segments(segments: list[dict], code2: torch.Tensor, blocksize: i
     _launch("nf4_dequant", total_bytes, 0, "rus_nf4_dequant_multi", jobs, len(segments),
             code2.data_ptr(), int(blocksize), int(super_blocksize), _stream(code2))
     return outs
+
+
+# ---------------------------------------------------------------------------------------------
+# NF4 W4A16 products: dequantisation inside the GEMM main loop (replaces dequant_nf4_tensor +
+# F.linear / torch.mm on its output, solution/ops.py:710-724, 771, 810, 873-993)
+# ---------------------------------------------------------------------------------------------
+
+
+class NF4Operand:
+    """A device NF4 double-quant weight [out_features, in_features] (one segment job: up to
+    three row segments with their own offsets and absmax2 bases) for ``nf4_gemm``. Holds the
+    device arrays it points into."""
+
+    __slots__ = ("job", "code2", "shape", "blocksize", "super_blocksize", "_keep")
+
+    def __init__(self, packed, absmax, absmax2, code2, offset, shape, split_bytes=None,
+                 absmax2_bases=None, blocksize: int = 64, super_blocksize: int = 256):
+        fn = "NF4Operand"
+        packed, absmax, absmax2 = (t.reshape(-1) for t in (packed, absmax, absmax2))
+        _require_device(fn, packed, absmax, absmax2, code2)
+        if packed.dtype != torch.uint8 or absmax.dtype != torch.uint8 or \
+                absmax2.dtype != torch.float32 or code2.dtype != torch.float32:
+            raise TypeError(f"{fn}: packed/absmax must be uint8, absmax2/code2 float32")
+        if not (packed.is_contiguous() and absmax.is_contiguous() and absmax2.is_contiguous()):
+            raise ValueError(f"{fn}: arrays must be contiguous")
+        rows, cols = int(shape[0]), int(shape[1])
+        nb = rows * cols // 2
+        if packed.numel() < nb:
+            raise ValueError(f"{fn}: packed has {packed.numel()} bytes, need {nb}")
+        offs = (offset,) * 3 if not isinstance(offset, (tuple, list)) else tuple(offset)
+        sp = split_bytes or (nb, nb)
+        bases = absmax2_bases or nf4_absmax2_bases(nb, sp, blocksize, super_blocksize)
+        jb = _lib.Nf4Job()
+        jb.packed, jb.absmax, jb.absmax2 = packed.data_ptr(), absmax.data_ptr(), absmax2.data_ptr()
+        jb.off0, jb.off1, jb.off2 = (float(o) for o in offs)
+        jb.split_byte_1, jb.split_byte_2 = int(sp[0]), int(sp[1])
+        jb.absmax2_base_1, jb.absmax2_base_2 = int(bases[0]), int(bases[1])
+        jb.n_bytes, jb.n_absmax, jb.n_absmax2 = nb, absmax.numel(), absmax2.numel()
+        jb.out_u32 = None
+        self.job = jb
+        self.code2 = code2.reshape(-1).contiguous()
+        self.shape = (rows, cols)
+        self.blocksize = int(blocksize)
+        self.super_blocksize = int(super_blocksize)
+        self._keep = (packed, absmax, absmax2)
+
+    @property
+    def device(self) -> torch.device:
+        return self.code2.device
+
+
+_gemm_plans: dict[tuple[int, int, int, int, int], tuple[int, int, int]] = {}
+_gemm_counters: dict[tuple[int, int], torch.Tensor] = {}
+
+
+def nf4_gemm_plan(m: int, w_rows: int, w_cols: int, trans: bool, split: int = 0):
+    """(split, fp32 workspace elements, counters) that ``nf4_gemm`` uses for this shape."""
+    key = (int(m), int(w_rows), int(w_cols), int(bool(trans)), int(split))
+    got = _gemm_plans.get(key)
+    if got is None:
+        sp, fl, ct = ctypes.c_int32(int(split)), ctypes.c_int64(), ctypes.c_int64()
+        _lib.call("rus_nf4_gemm_plan", int(m), int(w_rows), int(w_cols), int(bool(trans)),
+                  ctypes.byref(sp), ctypes.byref(fl), ctypes.byref(ct))
+        got = _gemm_plans[key] = (sp.value, fl.value, ct.value)
+    return got
+
+
+def nf4_gemm(x: torch.Tensor, w: NF4Operand, trans: bool = False,
+             bias: torch.Tensor | None = None, out: torch.Tensor | None = None,
+             split: int = 0) -> torch.Tensor:
+    """trans=False: x [m, in] @ W^T (+ bias) -> [m, out] (F.linear); trans=True: x [m, out] @ W
+    -> [m, in] (the input-gradient product). W is decoded from NF4 inside the kernel; fp32 sums,
+    one fp16 rounding. ``out``: optional fp16 destination with unit column stride."""
+    fn = "nf4_gemm"
+    _require_device(fn, x, bias, out)
+    rows, cols = w.shape
+    n_in, n_out = (rows, cols) if trans else (cols, rows)
+    x2 = _rows(fn, x, n_in, "x")
+    if x2.dtype != torch.float16:
+        raise ValueError(f"{fn}: fp16 activations only")
+    m = x2.shape[0]
+    if bias is not None:
+        if trans or bias.dtype != torch.float16 or bias.numel() != n_out:
+            raise ValueError(f"{fn}: bias must be fp16 [{n_out}] (forward product only)")
+        bias = bias.reshape(-1).contiguous()
+    if out is None:
+        out = torch.empty((m, n_out), dtype=torch.float16, device=x2.device)
+    elif out.dtype != torch.float16 or tuple(out.shape) != (m, n_out) or out.stride(1) != 1:
+        raise ValueError(f"{fn}: out must be fp16 [{m}, {n_out}] with unit column stride")
+    ks, floats, counters = nf4_gemm_plan(m, rows, cols, trans, split)
+    ws = cnt = None
+    if ks > 1:
+        ws = torch.empty(floats, dtype=torch.float32, device=x2.device)
+        cnt = _counter_buffer(_gemm_counters, x2.device, counters)
+    _launch("nf4_gemm", m * n_in * 2 + rows * cols * 33 // 64 + m * n_out * 2, 2 * m * rows * cols,
+            "rus_nf4_gemm", x2.data_ptr(), m, x2.stride(0), ctypes.byref(w.job),
+            w.code2.data_ptr(), rows, cols, w.blocksize, w.super_blocksize, int(bool(trans)),
+            _ptr(bias), out.data_ptr(), out.stride(0), ks, _ptr(ws),
+            0 if ws is None else ws.numel(), _ptr(cnt), 0 if cnt is None else cnt.numel(),
+            _stream(x2))
+    return out
+
+
+def _counter_buffer(cache: dict, dev: torch.device, need: int) -> torch.Tensor:
+    """A zeroed int32 arrival-counter buffer for kernels that leave their counters at zero, one
+    per (device, stream) (launches on one stream never overlap), kept for the life of the process
+    (captured graphs hold its address)."""
+    if need > LORA_MAX_COUNTERS:
+        raise RuntimeError(f"kernel needs {need} arrival counters (at most {LORA_MAX_COUNTERS})")
+    key = (dev.index if dev.index is not None else torch.cuda.current_device(),
+           torch.cuda.current_stream(dev).cuda_stream)
+    cnt = cache.get(key)
+    if cnt is None:
+        cnt = cache[key] = torch.zeros(LORA_MAX_COUNTERS, dtype=torch.int32, device=dev)
+    return cnt
 
 
 # ---------------------------------------------------------------------------------------------
