@@ -238,6 +238,9 @@ def main() -> int:
                     help="on: each layer's NF4 dequant runs one layer ahead on a second stream "
                          "and LoRA-down beside the q/k/v GEMM (measured slower on this stack: "
                          "cross-stream joins inside a replayed graph cost more than they hide)")
+    ap.add_argument("--gemm", choices=("dequant", "fused"), default="dequant",
+                    help="dequant: NF4 -> fp16 workspace, then the library GEMM; fused: the "
+                         "products decode NF4 inside their MFMA loop (rus_nf4_gemm)")
     ap.add_argument("--no-ablation", action="store_true",
                     help="skip the timing of the other --recompute setting")
     ap.add_argument("--probe", nargs="?", const="dequant", choices=("dequant", "lmhead"),
@@ -271,9 +274,9 @@ def main() -> int:
 
     # Configured engine: NF4 layers streamed per step from pinned host memory.
     recompute = args.recompute == "on"
-    overlap = args.overlap == "on" and args.stream_unit == "model"
+    overlap = args.overlap == "on" and args.stream_unit == "model" and args.gemm == "dequant"
     engine = Qwen2FusedEngine(model, dev, resident_weights=False, stream_unit=args.stream_unit,
-                              recompute=recompute, overlap=overlap)
+                              recompute=recompute, overlap=overlap, gemm=args.gemm)
     # Calibration pass (eager): every kernel timed, to name the dominant one.
     _, _, _, calib = timed_run(engine, opt, batches, 2, args.warmup, kernel_filter=None)
     dominant = max(calib, key=lambda k: calib[k]["ms"])
@@ -326,7 +329,7 @@ def main() -> int:
                    "rows": args.rows, "max_len": args.max_len,
                    "tokens_per_step": tokens / args.steps, "lora": "r16 alpha32 dropout0.05 q,v",
                    "stream_unit": args.stream_unit, "recompute": args.recompute,
-                   "overlap": "on" if overlap else "off"},
+                   "overlap": "on" if overlap else "off", "gemm": args.gemm},
         "roofline": roof,
         "median_step_tokens_per_s": (tokens / args.steps) / statistics.median(per_step),
         "peak_hbm_mib": (peak - base_alloc) / 2**20,
@@ -348,7 +351,7 @@ def main() -> int:
         # The other activation policy: same streamed weights, graphs, batches; its throughput
         # and its working set (peak allocation of one eager step, as for the headline engine).
         eng_a = Qwen2FusedEngine(model, dev, resident_weights=False, stream_unit=args.stream_unit,
-                                 recompute=not recompute, overlap=overlap)
+                                 recompute=not recompute, overlap=overlap, gemm=args.gemm)
         torch.cuda.synchronize()
         torch.cuda.reset_peak_memory_stats(dev)
         base_a = torch.cuda.memory_allocated(dev)
@@ -367,7 +370,7 @@ def main() -> int:
 
     if not args.no_resident:
         eng_r = Qwen2FusedEngine(model, dev, resident_weights=True, recompute=recompute,
-                                 overlap=overlap)
+                                 overlap=overlap, gemm=args.gemm)
         g_r = None
         if graph is not None:
             g_r = GraphedTrainStep(eng_r)

@@ -296,6 +296,26 @@ class WeightStream:
         outs = K.dequant_nf4_segments(jobs, self.code2_gpu, first.blocksize, first.super_blocksize)
         return dict(zip(SEGMENTS, outs))
 
+    def nf4_layer(self, layer_idx: int) -> dict[str, "K.NF4Operand"]:
+        """The four segments of a layer as NF4 operands of the fused products (``K.nf4_gemm``):
+        no dequantisation; the kernels read the packed bytes where they lie (slot, whole-model
+        buffer or resident copy), so a streamed slot must stay unreleased until the layer's last
+        product is enqueued. Operands are cached per (buffer, layer)."""
+        key = (self.unit, getattr(self, "active", 0) if self.unit == "model" else 0, layer_idx)
+        cache = self.__dict__.setdefault("_nf4_ops", {})
+        got = cache.get(key)
+        if got is None:
+            packed, absmax, absmax2 = self._arrays(layer_idx)
+            got = {}
+            for name, sg in self.layer_segments[layer_idx].items():
+                got[name] = K.NF4Operand(
+                    packed[sg.packed_slice], absmax[sg.absmax_slice], absmax2[sg.absmax2_slice],
+                    self.code2_gpu, sg.offsets, (sg.out_features, sg.in_features),
+                    split_bytes=sg.split_bytes, absmax2_bases=sg.absmax2_bases,
+                    blocksize=sg.blocksize, super_blocksize=sg.super_blocksize)
+            cache[key] = got
+        return got
+
     # -- dequantisation one layer ahead on a second stream ---------------------------------------
     @property
     def dequant_ahead(self) -> bool:

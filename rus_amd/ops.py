@@ -238,7 +238,7 @@ class Qwen2FusedEngine:
                  max_mlp_tokens: int = MAX_MLP_TOKENS, v_chunk: int = V_CHUNK_DEFAULT,
                  attention: str = "varlen", dropout_seed: int | None = None,
                  stream_unit: str = "layer", lora_kernels: bool = True, recompute: bool = True,
-                 overlap: bool = False):
+                 overlap: bool = False, gemm: str = "dequant"):
         from .model import QLoRAQwen2
 
         if not isinstance(model, QLoRAQwen2):
@@ -289,6 +289,14 @@ class Qwen2FusedEngine:
         # overlap=True: each layer's NF4 dequant runs on a second stream one layer ahead (into
         # a second workspace set) while the current layer computes; needs the weights' packed
         # bytes on the device for the whole step (resident or stream_unit="model").
+        # gemm="dequant": each layer's four NF4 segments are dequantised into fp16 workspaces
+        # (one launch) and the products run on the library GEMM; "fused": the products decode
+        # the NF4 bytes inside their MFMA main loop (K.nf4_gemm; no fp16 weight in HBM).
+        if gemm not in ("dequant", "fused"):
+            raise ValueError("gemm must be 'dequant' or 'fused'")
+        if gemm == "fused" and overlap:
+            raise ValueError("overlap (dequant one layer ahead) applies to gemm='dequant' only")
+        self.gemm = gemm
         self.overlap = bool(overlap)
         if self.overlap:
             self.weight_stream.enable_dequant_ahead()
@@ -483,14 +491,31 @@ def _lora_deltas(x_q, x_v, qA, qB, vA, vB):
     return mid_q, F.linear(mid_q, qB), mid_v, F.linear(mid_v, vB)
 
 
+def _lin(x, w, bias=None):
+    """x W^T (+ bias) (F.linear, solution/ops.py:710-724, 771, 810): W is a dequantised fp16
+    weight (library GEMM) or an NF4 operand (the fused dequant-in-GEMM kernel)."""
+    if isinstance(w, K.NF4Operand):
+        return K.nf4_gemm(x, w, bias=bias)
+    return F.linear(x, w, bias)
+
+
+def _mm_w(x, w):
+    """x W, the input-gradient product (torch.mm, solution/ops.py:934, 939, 949, 993)."""
+    if isinstance(w, K.NF4Operand):
+        return K.nf4_gemm(x, w, trans=True)
+    if x.shape[1] >= SPLIT_K_MIN:
+        return _mm_split_k(x, w)
+    return torch.mm(x, w)
+
+
 def _mlp_fwd(norm2, w_gu, w_down, max_tokens):
     n = norm2.shape[0]
     if n <= max_tokens:
-        return F.linear(K.mlp_glu_fwd(F.linear(norm2, w_gu)), w_down)
+        return _lin(K.mlp_glu_fwd(_lin(norm2, w_gu)), w_down)
     out = torch.empty((n, w_down.shape[0]), dtype=norm2.dtype, device=norm2.device)
     for s in range(0, n, max_tokens):
         e = min(s + max_tokens, n)
-        out[s:e] = F.linear(K.mlp_glu_fwd(F.linear(norm2[s:e], w_gu)), w_down)
+        out[s:e] = _lin(K.mlp_glu_fwd(_lin(norm2[s:e], w_gu)), w_down)
     return out
 
 
@@ -550,18 +575,18 @@ def _layer_front(engine, l, norm1, w_qkv, lora16, training, seed, masks, pos_ids
             side.wait_stream(main)
             with torch.cuda.stream(side):
                 K.lora_down_fwd(norm1, qA, vA, *bits, out=mids)
-            qkv = F.linear(norm1, w_qkv, engine.layer_biases[l])
+            qkv = _lin(norm1, w_qkv, engine.layer_biases[l])
             main.wait_stream(side)
             mid_q, mid_v = mids
         else:
             mid_q, mid_v = K.lora_down_fwd(norm1, qA, vA, *bits)
-            qkv = F.linear(norm1, w_qkv, engine.layer_biases[l])
+            qkv = _lin(norm1, w_qkv, engine.layer_biases[l])
         x_q = x_v = None
         q_rot, k_rot, v_out = K.qkv_rope_fwd_mid(
             qkv, mid_q, mid_v, qB, vB, cos, sin, pos_ids, meta["scale_q"], meta["scale_v"],
             hq, hkv, hd)
     else:
-        qkv = F.linear(norm1, w_qkv, engine.layer_biases[l])
+        qkv = _lin(norm1, w_qkv, engine.layer_biases[l])
         x_q, x_v = _lora_inputs(norm1, l, meta, training, seed)
         mid_q, q_lora, mid_v, v_lora = _lora_deltas(x_q, x_v, qA, qB, vA, vB)
         q_rot, k_rot, v_out = K.qkv_rope_fwd(qkv, cos, sin, pos_ids, q_lora=q_lora,
@@ -611,7 +636,11 @@ def stack_forward(engine, h_packed, pos_ids, row_lengths, training, lora16, seed
             norm1, h, rstd1 = K.rms_norm_fwd(carry[1], engine.ln1_weights[l], eps=eps,
                                              residual=carry[0])
         ins.save(l, h)
-        if ahead:
+        fused_gemm = engine.gemm == "fused"
+        if fused_gemm:  # NF4 operands: the products decode the packed bytes themselves
+            ws.wait_slot(l)
+            W = ws.nf4_layer(l)
+        elif ahead:
             W = ws.take_dequant(l)
         else:
             ws.wait_slot(l)
@@ -625,18 +654,20 @@ def stack_forward(engine, h_packed, pos_ids, row_lengths, training, lora16, seed
         else:
             attn = _run_packed_sdpa(q_rot, k_rot, v_out, row_lengths, engine.num_heads,
                                     engine.num_kv_heads, engine.head_dim)
-        o_out = F.linear(attn, W["o"])
+        o_out = _lin(attn, W["o"])
         norm2, h_mid, rstd2 = K.rms_norm_fwd(o_out, engine.ln2_weights[l], eps=eps, residual=h)
         del o_out
         if save:
-            gu = F.linear(norm2, W["gu"])
-            mlp_out = F.linear(K.mlp_glu_fwd(gu), W["down"])
+            gu = _lin(norm2, W["gu"])
+            mlp_out = _lin(K.mlp_glu_fwd(gu), W["down"])
             saved.append({"norm1": norm1, "rstd1": rstd1, "lora": lora, "q_rot": q_rot,
                           "k_rot": k_rot, "v_out": v_out, "attn": attn, "lse": lse, "rng": rng,
                           "unused": unused, "h_mid": h_mid, "rstd2": rstd2, "norm2": norm2,
                           "gu": gu})
         else:
             mlp_out = _mlp_fwd(norm2, W["gu"], W["down"], engine.max_mlp_tokens)
+        if fused_gemm:
+            ws.release_slot(l)  # the layer's last read of the packed slot is enqueued
         del norm1, lora, q_rot, k_rot, v_out, attn, norm2, W
         carry = (h_mid, mlp_out)
     if carry is None:
@@ -681,7 +712,11 @@ def stack_backward(engine, st: StackState, d_final_norm, grad16) -> torch.Tensor
             if ahead:
                 ws.issue_dequant(l - 1)  # beside this layer's backward
         h_in = ins.load(l, n_tokens)
-        if ahead:
+        fused_gemm = engine.gemm == "fused"
+        if fused_gemm:
+            ws.wait_slot(l)
+            W = ws.nf4_layer(l)
+        elif ahead:
             W = ws.take_dequant(l)
         else:
             ws.wait_slot(l)
@@ -721,7 +756,7 @@ def stack_backward(engine, st: StackState, d_final_norm, grad16) -> torch.Tensor
                     v_req = v_out.detach().requires_grad_(True)
                     attn = _run_packed_sdpa(q_req, k_req, v_req, st.row_lengths, hq, hkv, hd)
                 attn2d = attn.detach()
-            o_out = F.linear(attn2d, w_o)
+            o_out = _lin(attn2d, w_o)
             norm2, h_mid, rstd2 = K.rms_norm_fwd(o_out, engine.ln2_weights[l], eps=eps,
                                                  residual=h_in)
             del o_out
@@ -730,24 +765,24 @@ def stack_backward(engine, st: StackState, d_final_norm, grad16) -> torch.Tensor
         step = min(engine.max_mlp_tokens, n_tokens)
         if gu is not None or step >= n_tokens:
             if gu is None:
-                gu = F.linear(norm2, w_gu)
-            K.mlp_glu_bwd(torch.mm(dh, w_down), gu)
-            d_norm2 = _mm_split_k(gu, w_gu)
+                gu = _lin(norm2, w_gu)
+            K.mlp_glu_bwd(_mm_w(dh, w_down), gu)
+            d_norm2 = _mm_w(gu, w_gu)
             del gu
         else:
             d_norm2 = torch.empty_like(norm2)
             for s in range(0, n_tokens, step):
                 e = min(s + step, n_tokens)
-                gu = F.linear(norm2[s:e], w_gu)
-                K.mlp_glu_bwd(torch.mm(dh[s:e], w_down), gu)
-                d_norm2[s:e] = _mm_split_k(gu, w_gu)
+                gu = _lin(norm2[s:e], w_gu)
+                K.mlp_glu_bwd(_mm_w(dh[s:e], w_down), gu)
+                d_norm2[s:e] = _mm_w(gu, w_gu)
                 del gu
         del norm2
         dh_mid = K.rms_norm_bwd(d_norm2, h_mid, engine.ln2_weights[l], rstd2, dresidual=dh)
         del d_norm2, h_mid, rstd2, dh
 
         # Attention backward, adjoint RoPE with [dQ|dK|dV] packing and LoRA-delta gradients.
-        d_attn = torch.mm(dh_mid, w_o)
+        d_attn = _mm_w(dh_mid, w_o)
         if st.vm is not None:
             dq, dk, dv = _varlen_attn_bwd(d_attn.view(n_tokens, hq, hd), q_rot, k_rot, v_out,
                                           attn, lse, rng, unused, st.vm, engine.attention)
@@ -764,8 +799,10 @@ def stack_backward(engine, st: StackState, d_final_norm, grad16) -> torch.Tensor
         # LoRA gradients (solution/ops.py:975-992): weight gradients into the flat buffer, input
         # gradients (through the forward's dropout masks) added into d_norm1.
         g_qA, g_qB, g_vA, g_vB = gviews[4 * l: 4 * l + 4]
-        d_norm1 = torch.mm(dqkv, w_qkv)
+        d_norm1 = _mm_w(dqkv, w_qkv)
         del dqkv
+        if fused_gemm:
+            ws.release_slot(l)  # the layer's last read of the packed slot is enqueued
         if fused:  # d_mid, the expansion, masks and both adds; then all four weight gradients
             qAt, qBt, vAt, vBt = st.lora16t[4 * l: 4 * l + 4]
             d_mid_q, d_mid_v = K.lora_bwd_x(dq_scaled, dv_scaled, qAt, vAt, qBt, vBt, d_norm1,

@@ -86,6 +86,38 @@ def test_graph_step_matches_oracle_and_eager():
         assert _rel(a, p.grad.cpu()) <= 5e-3, (gi, _rel(a, p.grad.cpu()))
 
 
+def test_graph_fused_nf4_gemm_replays_repeat_and_match_eager():
+    # The dequant-in-GEMM products inside a captured step: workspace from the graph pool,
+    # arrival counters left at zero by every replay; replays separated by eager work.
+    cfg = small_config()
+    model = M.build_random_qlora_qwen2(cfg, DEV, seed=1, std=0.05)
+    engine = ops.Qwen2FusedEngine(model, DEV, resident_weights=False, stream_unit="model",
+                                  gemm="fused", recompute=False)
+    batch = _batch(cfg, [37, 64, 21])
+    for p in engine.lora_params:
+        p.grad = None
+    loss_e, *_ = ops.fused_causal_lm_forward(engine, *batch, training=False)
+    loss_e.backward()
+    torch.cuda.synchronize()
+    grads_e = [p.grad.detach().cpu().clone() for p in engine.lora_params]
+    gs = GraphedTrainStep(engine, bucket=64, training=False)
+    first = None
+    for rep in range(3):
+        loss_g = float(gs.step(*batch))
+        torch.cuda.synchronize()
+        grads_g = [g.clone() for g in _grads(engine)]
+        if first is None:
+            first = (loss_g, grads_g)
+            assert abs(loss_g - float(loss_e)) <= 1e-3 * abs(float(loss_e))
+            for gi, (a, b) in enumerate(zip(grads_g, grads_e)):
+                assert _rel(a, b) <= 5e-3, (gi, _rel(a, b))
+        else:
+            assert loss_g == first[0]
+            assert all(torch.equal(a, b) for a, b in zip(grads_g, first[1]))
+        x = torch.randn(300, 512, device=DEV).half()  # eager work between replays
+        (x @ x.t()).sum().item()
+
+
 def test_graph_dropout_seed_advances_per_replay():
     cfg = small_config(dropout=0.05)
     model = M.build_random_qlora_qwen2(cfg, DEV, seed=3, std=0.05)

@@ -79,6 +79,29 @@ def test_fused_stack_matches_cpu_oracle(resident, attention):
         assert _rel(g_f, leaf.grad) <= 1e-2, (gi, _rel(g_f, leaf.grad))
 
 
+@pytest.mark.parametrize("resident,recompute", [(False, True), (True, False)])
+def test_fused_nf4_gemm_stack_matches_cpu_oracle(resident, recompute):
+    # Every base-weight product through the dequant-in-GEMM kernel (no fp16 weight copies).
+    cfg = small_config()
+    model = M.build_random_qlora_qwen2(cfg, DEV, seed=1, std=0.05)
+    engine = ops.Qwen2FusedEngine(model, DEV, resident_weights=resident, gemm="fused",
+                                  recompute=recompute)
+    ids, mask, labels = _batch(cfg, [37, 64, 21])
+    pb = ops.pack_varlen(ids, mask, labels)
+    loss, grads = _fused_step(engine, pb, training=False)
+    deq = ostack.dequant_model(model)
+    lora = ostack.lora_leaves(model)
+    loss_ref, _ = ostack.step_loss(model, deq, lora, pb.input_ids, pb.pos_ids, pb.shift_labels,
+                                   pb.row_lengths)
+    loss_ref.backward()
+    assert abs(float(loss) - float(loss_ref)) <= 2e-3 * abs(float(loss_ref))
+    for gi, (g_f, leaf) in enumerate(zip(grads, lora)):
+        assert _rel(g_f, leaf.grad) <= 1e-2, (gi, _rel(g_f, leaf.grad))
+    # and twice in a row bit for bit (fixed-order sums, counters left at zero)
+    loss2, grads2 = _fused_step(engine, pb, training=False)
+    assert torch.equal(loss, loss2) and all(torch.equal(a, b) for a, b in zip(grads, grads2))
+
+
 def test_streamed_and_resident_weights_agree_bitwise():
     cfg = small_config()
     model = M.build_random_qlora_qwen2(cfg, DEV, seed=2, std=0.05)
