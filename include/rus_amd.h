@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define RUS_ABI_VERSION 4
+#define RUS_ABI_VERSION 6
 
 #define RUS_DTYPE_F16 0
 #define RUS_DTYPE_F32 1
@@ -146,6 +146,18 @@ int rus_rmsnorm_fwd(const void* x, const void* residual, const void* weight, int
 int rus_rmsnorm_bwd(const void* dy, const void* h, const void* weight, int32_t w_dtype,
                     const float* rstd, const void* dresidual, void* dx, int64_t n_rows,
                     int64_t n_cols, int64_t stride_row, int32_t dtype, void* stream);
+
+/*
+ * rus_rmsnorm_bwd (fp16 activations) whose dy is the fp16 rounding of the sum, in part order, of
+ * n_parts fp32 partial products dy_parts [n_parts, n_rows, n_cols] (contiguous): the split-K
+ * MLP-backward product d_norm2 = gu W_gu (solution/ops.py:939) consumed by the following
+ * norm backward (ops.py:941-943) with exactly the values a separate reduce would write.
+ * n_cols and stride_row multiples of 8, operands 16-byte aligned.
+ */
+int rus_rmsnorm_bwd_parts(const float* dy_parts, int32_t n_parts, const void* h,
+                          const void* weight, int32_t w_dtype, const float* rstd,
+                          const void* dresidual, void* dx, int64_t n_rows, int64_t n_cols,
+                          int64_t stride_row, void* stream);
 
 /*
  * LoRA-delta add + NeoX rotary embedding on packed tokens.
@@ -418,6 +430,8 @@ int rus_attn_varlen_fwd(const void* q, const void* k, const void* v, const int32
  * Backward of rus_attn_varlen_fwd: dq like q, dk / dv like k / v (fp16; dk and dv sum the h_q /
  * h_kv query heads of each group in fp32 and are rounded once). out and lse are the forward's.
  * workspace: fp32, at least round_up(h_q * n_tokens, 64) + 2 * h_q * n_tokens * 128 elements.
+ * counters: int32, at least max_blocks * h_kv, zero before the first call and left zero (calls
+ * sharing them must not run concurrently).
  * Replaces: the autograd backward of solution/ops.py:669-696 (torch SDPA backward plus the
  * sum over the expanded K/V heads), run by solution/ops.py:903-928.
  */
@@ -425,7 +439,8 @@ int rus_attn_varlen_bwd(const void* q, const void* k, const void* v, const void*
                         const void* dout, const float* lse, const int32_t* cu_seqlens,
                         int32_t n_seq, int64_t n_tokens, int32_t max_blocks, int32_t h_q,
                         int32_t h_kv, int32_t head_dim, float scale, void* dq, void* dk,
-                        void* dv, float* workspace, void* stream);
+                        void* dv, float* workspace, int32_t* counters, int64_t n_counters,
+                        void* stream);
 
 #ifdef __cplusplus
 }

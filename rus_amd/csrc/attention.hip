@@ -21,7 +21,8 @@
 //     accumulate in fp32;
 //   * backward: kernel 1 per (row, query block, head) forms D = rowsum(dO o O) and dQ;
 //     kernel 2 per (row, key block, query head) forms that head's dK and dV contributions in fp32;
-//     kernel 3 sums the h_q / h_kv heads of each KV group and rounds once (no atomics).
+//     the last of a KV group's h_q / h_kv heads to finish a key block sums the group's fp32
+//     partials in head order and rounds once (arrival counter; no atomics on data).
 #include <math.h>
 
 #include "common.h"
@@ -53,6 +54,9 @@ struct AttnArgs {
   float* dsum;     // [h_q, n_tok], D = rowsum(dO o O)
   float* dk_part;  // [h_q, n_tok, 128]
   float* dv_part;
+  f16* dk;         // [n_tok, h_kv, 128]
+  f16* dv;
+  int* counters;   // [max_blocks, h_kv] arrival counters (zero on entry, left zero)
   int64_t n_tok;
   int n_seq, h_q, h_kv;
   float scale, scale_log2;
@@ -439,7 +443,9 @@ __global__ __launch_bounds__(64 * kW) void attn_bwd_dq_kernel(AttnArgs a) {
 
 // ---------------------------------------------------------------------------------------------
 // Backward 2: this query head's dK = scale * dS^T Q and dV = P^T dO for one 32-key block, fp32.
-// Block = (row, key block, head); the kW waves split the query blocks.
+// Block = (row, key block, head); the kW waves split the query blocks. The h_q / h_kv heads of a
+// KV group store fp32 partials; the last of them to finish sums the group in head order and
+// writes dK and dV once (no atomics on data, no separate reduce launch).
 // ---------------------------------------------------------------------------------------------
 __global__ __launch_bounds__(64 * kW) void attn_bwd_dkdv_kernel(AttnArgs a) {
   constexpr int kBytes = kMax(2 * kW * kStageHalfs * 2, kParkBytes);
@@ -538,39 +544,42 @@ __global__ __launch_bounds__(64 * kW) void attn_bwd_dkdv_kernel(AttnArgs a) {
       float acc = 0.0f;
 #pragma unroll
       for (int w = 0; w < kW; ++w) acc += parked(buf, w, wave, r, lane);
-      if (key < end) dst[(static_cast<int64_t>(head) * a.n_tok + key) * kHD + wave * 32 + col] = acc * sc;
+      if (key < end)
+        store_partial(dst + (static_cast<int64_t>(head) * a.n_tok + key) * kHD + wave * 32 + col,
+                      acc * sc);
     }
   }
-}
-
-// Backward 3: dk[t, g, :] = fp16(sum of the group's heads), same for dv. 8 elements per thread.
-__global__ __launch_bounds__(256) void attn_gqa_reduce_kernel(const float* __restrict__ dk_part,
-                                                              const float* __restrict__ dv_part,
-                                                              f16* __restrict__ dk,
-                                                              f16* __restrict__ dv,
-                                                              int64_t n_tok, int h_q, int h_kv) {
-  const int64_t total = n_tok * h_kv * (kHD / 8);
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-  if (i >= total) return;
-  const int c = static_cast<int>(i % (kHD / 8)) * 8;
-  const int64_t tg = i / (kHD / 8);
-  const int g = static_cast<int>(tg % h_kv);
-  const int64_t t = tg / h_kv;
-  const int grp = h_q / h_kv;
-  float sk[8] = {}, sv[8] = {};
-  for (int j = 0; j < grp; ++j) {
-    const int64_t off = (static_cast<int64_t>(g * grp + j) * n_tok + t) * kHD + c;
-    float x[8];
-    load_f32<float, 8>(dk_part + off, x);
+  const int grp = a.h_q / a.h_kv;
+  if (!arrive_last(a.counters + static_cast<int64_t>(blockIdx.y) * a.h_kv + g, grp)) return;
+  // Last head of the group: dk[key, g, :] = fp16(sum over the group's heads in head order).
+  // Thread (wave, lane) owns head dims wave*32 + col of its 16 keys, as in the partial stores.
 #pragma unroll
-    for (int e = 0; e < 8; ++e) sk[e] += x[e];
-    load_f32<float, 8>(dv_part + off, x);
+  for (int pass = 0; pass < 2; ++pass) {
+    const float* src = pass == 0 ? a.dk_part : a.dv_part;
+    f16* out = pass == 0 ? a.dk : a.dv;
+    float acc[16];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) sv[e] += x[e];
+    for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
+    // One head per round: its 16 loads are issued together, then added in head order.
+    for (int j = 0; j < grp; ++j) {
+      const float* hsrc = src + static_cast<int64_t>(g * grp + j) * a.n_tok * kHD + wave * 32 + col;
+      float v[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int key = min(k0 + acc_row(r, h), end - 1);  // rows past the end: read, not stored
+        v[r] = load_partial(hsrc + static_cast<int64_t>(key) * kHD);
+      }
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[r] += v[r];
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int key = k0 + acc_row(r, h);
+      if (key < end)
+        out[(static_cast<int64_t>(key) * a.h_kv + g) * kHD + wave * 32 + col] =
+            static_cast<f16>(acc[r]);
+    }
   }
-  const int64_t o = (t * h_kv + g) * kHD + c;
-  store_from_f32<f16, 8>(dk + o, sk);
-  store_from_f32<f16, 8>(dv + o, sv);
 }
 
 int check(const char* fn, const void* q, const void* k, const void* v, const int32_t* cu,
@@ -627,15 +636,20 @@ extern "C" int rus_attn_varlen_bwd(const void* q, const void* k, const void* v, 
                                    const int32_t* cu_seqlens, int32_t n_seq, int64_t n_tokens,
                                    int32_t max_blocks, int32_t h_q, int32_t h_kv,
                                    int32_t head_dim, float scale, void* dq, void* dk, void* dv,
-                                   float* workspace, void* stream) {
+                                   float* workspace, int32_t* counters, int64_t n_counters,
+                                   void* stream) {
   using namespace rus;
   const char* fn = "rus_attn_varlen_bwd";
   if (int e = check(fn, q, k, v, cu_seqlens, n_tokens, n_seq, h_q, h_kv, head_dim, max_blocks))
     return e;
   if (!out || !dout || !lse || !dq || !dk || !dv || !workspace || !aligned(out, 16) ||
       !aligned(dout, 16) || !aligned(dq, 16) || !aligned(dk, 16) || !aligned(dv, 16) ||
-      !aligned(workspace, 16))
+      !aligned(workspace, 16) || !counters || !aligned(counters, 4))
     return fail(RUS_ERR_INVALID, "%s: null or misaligned argument", fn);
+  if (n_counters < static_cast<int64_t>(max_blocks) * h_kv)
+    return fail(RUS_ERR_INVALID, "%s: %lld counters, need max_blocks * h_kv = %lld", fn,
+                static_cast<long long>(n_counters),
+                static_cast<long long>(max_blocks) * h_kv);
   AttnArgs a{};
   a.q = static_cast<const f16*>(q);
   a.k = static_cast<const f16*>(k);
@@ -658,11 +672,9 @@ extern "C" int rus_attn_varlen_bwd(const void* q, const void* k, const void* v, 
   a.out = static_cast<f16*>(dq);
   hipLaunchKernelGGL(attn_bwd_dq_kernel, dim3(h_q, max_blocks), dim3(64 * kW), 0, st, a);
   if (int e = check_launch(fn)) return e;
+  a.dk = static_cast<f16*>(dk);
+  a.dv = static_cast<f16*>(dv);
+  a.counters = counters;
   hipLaunchKernelGGL(attn_bwd_dkdv_kernel, dim3(h_q, max_blocks), dim3(64 * kW), 0, st, a);
-  if (int e = check_launch(fn)) return e;
-  const int64_t total = n_tokens * h_kv * (kHD / 8);
-  hipLaunchKernelGGL(attn_gqa_reduce_kernel, dim3(static_cast<unsigned>((total + 255) / 256)),
-                     dim3(256), 0, st, a.dk_part, a.dv_part, static_cast<f16*>(dk),
-                     static_cast<f16*>(dv), n_tokens, h_q, h_kv);
   return check_launch(fn);
 }

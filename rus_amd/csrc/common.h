@@ -62,4 +62,39 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+// ---------------------------------------------------------------------------------------------
+// Cross-block sums in one launch ("last block reduces"). Blocks store fp32 partials with
+// device-coherent 4-byte accesses (agent-scope relaxed atomics: performed where every XCD's L2
+// agrees, so no cache-wide write-back or invalidate is needed, which is what a device-scope
+// fence would cost), count their arrival on an int32 counter, and the last of n blocks to arrive
+// reads all n partials and sums them in a fixed order: deterministic, no atomics on data.
+// ---------------------------------------------------------------------------------------------
+__device__ __forceinline__ void store_partial(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ float load_partial(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Called by every thread of a block once its partial stores are issued: true, in every thread,
+// in the last of the n blocks sharing `counter` to arrive. Each thread waits for its own memory
+// accesses to complete before the block arrives; the last block puts the counter back to 0
+// (counters are zero when a launch starts and are left zero). No block waits for another.
+__device__ __forceinline__ bool arrive_last(int* counter, int n) {
+  __shared__ int s_last;
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0);  // every memory access of this thread has completed
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const int old = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const bool last = old == n - 1;
+    if (last) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = last ? 1 : 0;
+  }
+  __syncthreads();
+  return s_last != 0;
+}
+
 }  // namespace rus

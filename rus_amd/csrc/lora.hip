@@ -102,37 +102,6 @@ __device__ __forceinline__ void col_owner(int j, int n, int& br, int& rank) {
   }
 }
 
-// Partial sums cross blocks through device-coherent 4-byte accesses (agent-scope relaxed
-// atomics): a store is performed where every XCD's L2 agrees and a load reads from there, so no
-// cache-wide write-back or invalidate (what a device-scope fence costs) is needed.
-__device__ __forceinline__ void store_partial(float* p, float v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-__device__ __forceinline__ float load_partial(const float* p) {
-  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// Called by every thread of a block once its partial is stored (store_partial): true, in every
-// thread, in the last of the n blocks sharing `counter` to arrive, which then reads all n
-// partials (load_partial). Each thread waits for its stores to complete before the block
-// arrives; the last block puts the counter back to 0. No block waits for another.
-__device__ __forceinline__ bool arrive_last(int* counter, int n) {
-  __shared__ int s_last;
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  __builtin_amdgcn_s_waitcnt(0);  // every memory access of this thread has completed
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const int old = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const bool last = old == n - 1;
-    if (last) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    s_last = last ? 1 : 0;
-  }
-  __syncthreads();
-  return s_last != 0;
-}
-
 // Split-K end of the tokens x ranks kernels: the waves' accumulators are summed through LDS in
 // wave order into this block's partial part[chunk][tile] (NACC x 1024 fp32 in accumulator
 // order); the last block of the tile sums every chunk's partial in chunk order into tot

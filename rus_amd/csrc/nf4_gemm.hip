@@ -93,34 +93,6 @@ __device__ __forceinline__ f32x16 mfma(f16x8 a, f16x8 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
 
-// Device-coherent 4-byte accesses for the split partials (agent-scope relaxed atomics: no
-// cache-wide write-back or invalidate, which is what a device-scope fence would cost).
-__device__ __forceinline__ void store_partial(float* p, float v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-__device__ __forceinline__ float load_partial(const float* p) {
-  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// True, in every thread, in the last of the n blocks sharing `counter` to arrive (after every
-// thread's partial stores have completed); that block resets the counter. No block waits.
-__device__ __forceinline__ bool arrive_last(int* counter, int n) {
-  __shared__ int s_last;
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  __builtin_amdgcn_s_waitcnt(0);  // every memory access of this thread has completed
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const int old = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const bool last = old == n - 1;
-    if (last) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    s_last = last ? 1 : 0;
-  }
-  __syncthreads();
-  return s_last != 0;
-}
-
 // One reduction step's global operands of this thread, loaded one step ahead of their use:
 // 8 activation chunks of 16 bytes (rows r0 + 32 i, coalesced: 8 lanes cover a 128-byte row) and
 // the packed codes this thread decodes into the shared weight tile.

@@ -12,6 +12,8 @@
 //     to a scalar two-pass kernel (the second pass re-reads the row from L1/L2, not HBM);
 //   * built with -ffp-contract=off so every product and sum is rounded as in an eager fp32
 //     restatement (only the reduction order differs).
+#include <type_traits>
+
 #include "common.h"
 
 namespace rus {
@@ -162,6 +164,68 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_vec(const T* __restrict__ dy,
         for (int i = 0; i < V; ++i) o[i] = o[i] + d[i];
       }
       store_from_f32<T, V>(dx + off + c, o);
+    }
+  }
+}
+
+// rmsnorm_bwd_vec whose dy is the fp16 rounding of the sum of n_parts fp32 partial products
+// (parts [n_parts, n_rows, n_cols], added in part order): the split-K MLP-backward product
+// (d_norm2 = gu W_gu) feeds the norm backward without a separate reduce launch, with the values
+// that launch would have written.
+template <typename W, int NIT, int NP, bool HAS_DRES>
+__global__ __launch_bounds__(256) void rmsnorm_bwd_parts_vec(
+    const float* __restrict__ parts, int64_t part_stride, const f16* __restrict__ h,
+    const W* __restrict__ w, const float* __restrict__ rstd, const f16* __restrict__ dres,
+    f16* __restrict__ dx, int n_rows, int n_cols, int64_t stride) {
+  constexpr int V = 8;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int row = blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave;
+  if (row >= n_rows) return;
+  const int64_t off = static_cast<int64_t>(row) * stride;
+  const float* prow = parts + static_cast<int64_t>(row) * n_cols;
+  const float r = rstd[row];
+
+  float xh[NIT][V], g[NIT][V];
+  float acc = 0.0f;
+#pragma unroll
+  for (int it = 0; it < NIT; ++it) {
+    const int c = (it * kWave + lane) * V;
+    if (c < n_cols) {
+      float dv[V], wv[V], pv[NP][V];
+      load_f32<f16, V>(h + off + c, xh[it]);
+#pragma unroll
+      for (int q = 0; q < NP; ++q) load_f32<float, V>(prow + q * part_stride + c, pv[q]);
+      load16<W, V>(w + c, wv);
+#pragma unroll
+      for (int i = 0; i < V; ++i) {
+        dv[i] = pv[0][i];
+#pragma unroll
+        for (int q = 1; q < NP; ++q) dv[i] += pv[q][i];  // part order
+      }
+#pragma unroll
+      for (int i = 0; i < V; ++i) {
+        dv[i] = round_to<f16>(dv[i]);  // the fp16 product the reduce would have written
+        xh[it][i] = xh[it][i] * r;
+        g[it][i] = wv[i] * dv[i];
+        acc += xh[it][i] * g[it][i];
+      }
+    }
+  }
+  const float cm = wave_sum(acc) / static_cast<float>(n_cols);
+#pragma unroll
+  for (int it = 0; it < NIT; ++it) {
+    const int c = (it * kWave + lane) * V;
+    if (c < n_cols) {
+      float o[V];
+#pragma unroll
+      for (int i = 0; i < V; ++i) o[i] = (g[it][i] - xh[it][i] * cm) * r;
+      if (HAS_DRES) {
+        float d[V];
+        load_f32<f16, V>(dres + off + c, d);
+#pragma unroll
+        for (int i = 0; i < V; ++i) o[i] = o[i] + d[i];
+      }
+      store_from_f32<f16, V>(dx + off + c, o);
     }
   }
 }
@@ -347,6 +411,73 @@ extern "C" int rus_rmsnorm_fwd(const void* x, const void* residual, const void* 
                                  stride_row, eps, st);
   return fwd_typed<float, float>(x, residual, weight, sum_out, y, rstd, n_rows, n_cols,
                                  stride_row, eps, st);
+}
+
+extern "C" int rus_rmsnorm_bwd_parts(const float* dy_parts, int32_t n_parts, const void* h,
+                                     const void* weight, int32_t w_dtype, const float* rstd,
+                                     const void* dresidual, void* dx, int64_t n_rows,
+                                     int64_t n_cols, int64_t stride_row, void* stream) {
+  using namespace rus;
+  const char* fn = "rus_rmsnorm_bwd_parts";
+  if (int e = check_common(fn, n_rows, n_cols, stride_row, RUS_DTYPE_F16, w_dtype)) return e;
+  if (n_parts < 1 || n_parts > 8)
+    return fail(RUS_ERR_INVALID, "%s: n_parts=%d outside [1, 8]", fn, n_parts);
+  if (n_rows == 0) return RUS_OK;
+  if (!dy_parts || !h || !weight || !rstd || !dx)
+    return fail(RUS_ERR_INVALID, "%s: null pointer argument", fn);
+  if (n_cols % 8 || stride_row % 8 || !aligned(dy_parts, 16) || !aligned(h, 16) ||
+      !aligned(weight, 16) || !aligned(dx, 16) || (dresidual && !aligned(dresidual, 16)))
+    return fail(RUS_ERR_INVALID, "%s: need n_cols and stride_row multiples of 8 and 16-byte "
+                "aligned operands", fn);
+  const int nit = pick_nit(n_cols, 8, 8);
+  if (nit == 0 || nit * kWave * 8 < n_cols)
+    return fail(RUS_ERR_UNSUPPORTED, "%s: n_cols=%lld too wide", fn, (long long)n_cols);
+  const int64_t pstride = n_rows * n_cols;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const Launch l = row_launch(n_rows);
+  const f16* hp = static_cast<const f16*>(h);
+  const f16* dp = static_cast<const f16*>(dresidual);
+  f16* dxp = static_cast<f16*>(dx);
+  const int nr = static_cast<int>(n_rows), nc = static_cast<int>(n_cols);
+  // Parts count and width are compile-time so that every load of a row is issued together.
+  auto launch = [&](auto wtag, auto nit_c, auto np_c) {
+    using WT = decltype(wtag);
+    constexpr int NIT = decltype(nit_c)::value, NP = decltype(np_c)::value;
+    if (dp)
+      hipLaunchKernelGGL((rmsnorm_bwd_parts_vec<WT, NIT, NP, true>), l.grid, l.block, 0, st,
+                         dy_parts, pstride, hp, static_cast<const WT*>(weight), rstd, dp, dxp, nr,
+                         nc, stride_row);
+    else
+      hipLaunchKernelGGL((rmsnorm_bwd_parts_vec<WT, NIT, NP, false>), l.grid, l.block, 0, st,
+                         dy_parts, pstride, hp, static_cast<const WT*>(weight), rstd, dp, dxp, nr,
+                         nc, stride_row);
+  };
+  auto by_parts = [&](auto wtag, auto nit_c) {
+    switch (n_parts) {
+      case 1: launch(wtag, nit_c, std::integral_constant<int, 1>{}); break;
+      case 2: launch(wtag, nit_c, std::integral_constant<int, 2>{}); break;
+      case 3: launch(wtag, nit_c, std::integral_constant<int, 3>{}); break;
+      case 4: launch(wtag, nit_c, std::integral_constant<int, 4>{}); break;
+      case 5: launch(wtag, nit_c, std::integral_constant<int, 5>{}); break;
+      case 6: launch(wtag, nit_c, std::integral_constant<int, 6>{}); break;
+      case 7: launch(wtag, nit_c, std::integral_constant<int, 7>{}); break;
+      default: launch(wtag, nit_c, std::integral_constant<int, 8>{}); break;
+    }
+  };
+  auto by_width = [&](auto wtag) {
+    switch (nit) {
+      case 1: by_parts(wtag, std::integral_constant<int, 1>{}); return true;
+      case 2: by_parts(wtag, std::integral_constant<int, 2>{}); return true;
+      case 3: by_parts(wtag, std::integral_constant<int, 3>{}); return true;
+      case 4: by_parts(wtag, std::integral_constant<int, 4>{}); return true;
+      case 6: by_parts(wtag, std::integral_constant<int, 6>{}); return true;
+      case 8: by_parts(wtag, std::integral_constant<int, 8>{}); return true;
+      default: return false;
+    }
+  };
+  const bool ok = w_dtype == RUS_DTYPE_F16 ? by_width(f16{}) : by_width(float{});
+  if (!ok) return fail(RUS_ERR_UNSUPPORTED, "%s: n_cols=%lld unsupported", fn, (long long)n_cols);
+  return check_launch(fn);
 }
 
 extern "C" int rus_rmsnorm_bwd(const void* dy, const void* h, const void* weight, int32_t w_dtype,

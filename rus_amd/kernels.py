@@ -26,6 +26,7 @@ __all__ = [
     "nf4_absmax2_bases",
     "rms_norm_fwd",
     "rms_norm_bwd",
+    "rms_norm_bwd_parts",
     "qkv_rope_fwd",
     "qkv_rope_bwd",
     "qkv_rope_bwd_lora",
@@ -329,6 +330,7 @@ class NF4Operand:
 
 _gemm_plans: dict[tuple[int, int, int, int, int], tuple[int, int, int]] = {}
 _gemm_counters: dict[tuple[int, int], torch.Tensor] = {}
+_attn_counters: dict[tuple[int, int], torch.Tensor] = {}
 
 
 def nf4_gemm_plan(m: int, w_rows: int, w_cols: int, trans: bool, split: int = 0):
@@ -471,6 +473,43 @@ def rms_norm_bwd(
               rs.data_ptr(), dres_ptr, dx.data_ptr(), n_rows, n_cols, dy_2d.stride(0), dt,
               _stream(dy))
     return dx.view(orig_shape)
+
+
+def rms_norm_bwd_parts(dy_parts: torch.Tensor, h: torch.Tensor, weight: torch.Tensor,
+                       rstd: torch.Tensor, dresidual: torch.Tensor | None = None) -> torch.Tensor:
+    """``rms_norm_bwd`` whose dy is fp16(sum over the leading axis of the fp32 partials
+    dy_parts [S, n_rows, n_cols], in order): a split-K product consumed without a reduce
+    launch; equal bit for bit to ``rms_norm_bwd(sum_splits(dy_parts), ...)``."""
+    fn = "rms_norm_bwd_parts"
+    _require_device(fn, dy_parts, h, weight, rstd, dresidual)
+    if h.dtype != torch.float16:
+        raise ValueError(f"{fn}: fp16 activations only")
+    n_cols = h.shape[-1]
+    h_2d = h.contiguous().view(-1, n_cols)
+    n_rows = h_2d.shape[0]
+    if dy_parts.dtype != torch.float32 or dy_parts.dim() != 3 or \
+            tuple(dy_parts.shape[1:]) != (n_rows, n_cols) or not dy_parts.is_contiguous():
+        raise ValueError(f"{fn}: dy_parts must be contiguous float32 [S, {n_rows}, {n_cols}]")
+    if not 1 <= dy_parts.shape[0] <= 8:
+        raise ValueError(f"{fn}: 1 to 8 partials, got {dy_parts.shape[0]}")
+    wdt = _dtype_code(fn, weight.dtype)
+    w = weight.contiguous()
+    rs = rstd.contiguous()
+    if rs.dtype != torch.float32 or rs.numel() != n_rows:
+        raise ValueError(f"{fn}: rstd must be float32 with {n_rows} entries")
+    dx = torch.empty_like(h_2d)
+    dres_ptr = None
+    if dresidual is not None:
+        dres_2d = dresidual.contiguous().view(-1, n_cols)
+        if dres_2d.dtype != h_2d.dtype or dres_2d.shape != h_2d.shape:
+            raise ValueError(f"{fn}: dresidual must match h in shape and dtype")
+        dres_ptr = dres_2d.data_ptr()
+    n_parts = dy_parts.shape[0]
+    _launch("rmsnorm_bwd", (4 * n_parts + (3 if dres_ptr is not None else 2)) * n_rows * n_cols
+            + w.numel() * w.element_size() + 4 * n_rows, 0, "rus_rmsnorm_bwd_parts",
+            dy_parts.data_ptr(), n_parts, h_2d.data_ptr(), w.data_ptr(), wdt, rs.data_ptr(),
+            dres_ptr, dx.data_ptr(), n_rows, n_cols, h_2d.stride(0), _stream(h_2d))
+    return dx.view(h.shape)
 
 
 # ---------------------------------------------------------------------------------------------
@@ -1226,10 +1265,12 @@ def attn_varlen_bwd(dout: torch.Tensor, q: torch.Tensor, k: torch.Tensor, v: tor
     ws = torch.empty(_round_up(hq * n, 64) + 2 * hq * n * d, dtype=torch.float32,
                      device=q.device)
     nbytes = 2 * (4 * q.numel() + 4 * k.numel()) + 4 * 2 * hq * n * d * 2 + lse.numel() * 8
+    cnt = _counter_buffer(_attn_counters, q.device, mb * k.shape[1])
     _launch("attn_bwd", nbytes, 2.5 * _attn_flops(lens, hq), "rus_attn_varlen_bwd",
             q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), dout.data_ptr(),
             lse.data_ptr(), cu_seqlens.data_ptr(), n_rows, n, mb, hq, k.shape[1], d, scale,
-            dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), ws.data_ptr(), _stream(q))
+            dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), ws.data_ptr(), cnt.data_ptr(),
+            cnt.numel(), _stream(q))
     return dq, dk, dv
 
 

@@ -527,14 +527,20 @@ def _mm_split_k(a: torch.Tensor, b: torch.Tensor, splits: int = 4) -> torch.Tens
     partials and one reduce kernel that rounds the sum to fp16 once (the single GEMM's rounding).
     For the long-K, narrow-output MLP backward product (K = 17920, D = 1536), where one GEMM
     leaves most of the GPU idle."""
+    parts = _split_k_parts(a, b, splits)
+    return torch.mm(a, b) if parts is None else K.sum_splits(parts, a.dtype)
+
+
+def _split_k_parts(a: torch.Tensor, b: torch.Tensor, splits: int = 4):
+    """The fp32 partial products [splits, M, D] of a [M, K] @ b [K, D] over K slices (one batched
+    GEMM), or None where the split does not apply (short K, indivisible, non-contiguous)."""
     M, Kd = a.shape
     D = b.shape[1]
     if Kd < SPLIT_K_MIN or Kd % splits or a.stride(1) != 1 or not b.is_contiguous():
-        return torch.mm(a, b)
+        return None
     ks = Kd // splits
-    parts = torch.bmm(a.view(M, splits, ks).permute(1, 0, 2), b.view(splits, ks, D),
-                      out_dtype=torch.float32)
-    return K.sum_splits(parts, a.dtype)
+    return torch.bmm(a.view(M, splits, ks).permute(1, 0, 2), b.view(splits, ks, D),
+                     out_dtype=torch.float32)
 
 
 class StackState:
@@ -763,11 +769,14 @@ def stack_backward(engine, st: StackState, d_final_norm, grad16) -> torch.Tensor
 
         # MLP backward: d_act = dh . W_down; SwiGLU backward in place over gu; d_norm2.
         step = min(engine.max_mlp_tokens, n_tokens)
+        d_parts = None
         if gu is not None or step >= n_tokens:
             if gu is None:
                 gu = _lin(norm2, w_gu)
             K.mlp_glu_bwd(_mm_w(dh, w_down), gu)
-            d_norm2 = _mm_w(gu, w_gu)
+            if not isinstance(w_gu, K.NF4Operand):  # split-K partials go straight to the norm
+                d_parts = _split_k_parts(gu, w_gu)
+            d_norm2 = _mm_w(gu, w_gu) if d_parts is None else None
             del gu
         else:
             d_norm2 = torch.empty_like(norm2)
@@ -778,8 +787,12 @@ def stack_backward(engine, st: StackState, d_final_norm, grad16) -> torch.Tensor
                 d_norm2[s:e] = _mm_w(gu, w_gu)
                 del gu
         del norm2
-        dh_mid = K.rms_norm_bwd(d_norm2, h_mid, engine.ln2_weights[l], rstd2, dresidual=dh)
-        del d_norm2, h_mid, rstd2, dh
+        if d_parts is not None:
+            dh_mid = K.rms_norm_bwd_parts(d_parts, h_mid, engine.ln2_weights[l], rstd2,
+                                          dresidual=dh)
+        else:
+            dh_mid = K.rms_norm_bwd(d_norm2, h_mid, engine.ln2_weights[l], rstd2, dresidual=dh)
+        del d_norm2, d_parts, h_mid, rstd2, dh
 
         # Attention backward, adjoint RoPE with [dQ|dK|dV] packing and LoRA-delta gradients.
         d_attn = _mm_w(dh_mid, w_o)

@@ -84,7 +84,13 @@ def test_header_compiles_as_c():
         ("rus_attn_varlen_fwd", (16, 16, 16, 16, 1, 32, 2, 12, 2, 128, 0.1, 18, 16, None),
          "output"),
         ("rus_attn_varlen_bwd", (16, 16, 16, 16, 16, 16, 16, 1, 32, 2, 12, 2, 128, 0.1, 16, 16,
-                                 16, None, None), "misaligned"),
+                                 16, None, None, 0, None), "misaligned"),
+        ("rus_attn_varlen_bwd", (16, 16, 16, 16, 16, 16, 16, 1, 32, 2, 12, 2, 128, 0.1, 16, 16,
+                                 16, 16, 16, 3, None), "counters"),
+        # split-partial norm backward: n_parts out of range, width not a multiple of 8
+        ("rus_rmsnorm_bwd_parts", (16, 0, 16, 16, 0, 16, None, 16, 4, 64, 64, None), "n_parts"),
+        ("rus_rmsnorm_bwd_parts", (16, 2, 16, 16, 0, 16, None, 16, 4, 60, 60, None),
+         "multiples of 8"),
     ],
 )
 def test_invalid_arguments_are_rejected_on_the_host(name, args, msg):

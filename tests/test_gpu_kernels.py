@@ -166,6 +166,27 @@ def test_rmsnorm_fwd_bwd(dtype, wdtype, has_residual, shape):
         assert torch.allclose(dx.cpu(), dx_r, rtol=1e-4, atol=1e-5)
 
 
+@pytest.mark.parametrize("wdtype", [torch.float16, torch.float32])
+@pytest.mark.parametrize("n_parts", [1, 3, 4])
+@pytest.mark.parametrize("has_residual", [False, True])
+@pytest.mark.parametrize("shape", [(707, 1536), (5, 896)])
+def test_rmsnorm_bwd_over_split_partials_equals_reduce_then_bwd(wdtype, n_parts, has_residual,
+                                                                shape):
+    # dy = fp16(sum of fp32 partials in part order) formed inside the norm backward must equal,
+    # bit for bit, the separate reduce kernel followed by rms_norm_bwd.
+    g = torch.Generator().manual_seed(n_parts)
+    n, d = shape
+    x = torch.randn(shape, generator=g).half().to(DEV)
+    w = (1 + 0.05 * torch.randn(d, generator=g)).to(wdtype).to(DEV)
+    parts = (torch.randn((n_parts, n, d), generator=g) * 3).to(DEV)
+    dres = torch.randn(shape, generator=g).half().to(DEV) if has_residual else None
+    _, h, rstd = K.rms_norm_fwd(x, w, 1e-6)
+    want = K.rms_norm_bwd(K.sum_splits(parts), h, w, rstd, dresidual=dres)
+    got = K.rms_norm_bwd_parts(parts, h, w, rstd, dresidual=dres)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+
+
 # ---------------------------------------------------------------------------------------------
 # LoRA + RoPE
 # ---------------------------------------------------------------------------------------------
