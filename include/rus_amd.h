@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define RUS_ABI_VERSION 6
+#define RUS_ABI_VERSION 7
 
 #define RUS_DTYPE_F16 0
 #define RUS_DTYPE_F32 1
@@ -198,6 +198,22 @@ int rus_qkv_rope_bwd(const void* dq_rot, const void* dk_rot, const void* dv, con
                      int32_t head_dim, int32_t* err_flag, int32_t dtype, void* stream);
 
 /*
+ * rus_qkv_rope_bwd (fp16, dq_lora / dv_lora required) that also forms the LoRA products of the
+ * scaled gradients in the same launch: d_mid_q = fp16(dq_lora B_q), d_mid_v = fp16(dv_lora B_v)
+ * [n_tokens, r] (solution/ops.py:975-992: d_mid = dq @ B). bt_q / bt_v are B^T [r, h*head_dim]
+ * (contiguous, 16-byte aligned). r must be 16, and a token's (h_q + 2 h_kv) * head_dim / 16
+ * thread slots must divide 256 with each head kind's slots a multiple of 16 (12 / 2 heads of
+ * 128: yes); otherwise RUS_ERR_UNSUPPORTED.
+ */
+int rus_qkv_rope_bwd_mid(const void* dq_rot, const void* dk_rot, const void* dv, const void* cos,
+                         const void* sin, const int64_t* pos_ids, void* dqkv, void* dq_lora,
+                         void* dv_lora, const void* bt_q, const void* bt_v, int32_t r,
+                         void* d_mid_q, void* d_mid_v, int64_t n_tokens, int64_t stride_dqkv,
+                         int64_t stride_cos, int64_t n_pos, float scale_q, float scale_v,
+                         int32_t h_q, int32_t h_kv, int32_t head_dim, int32_t* err_flag,
+                         void* stream);
+
+/*
  * LoRA-input dropout, both branches in one pass: out_a = dropout(x; stream_a, p_a),
  * out_b = dropout(x; stream_b, p_b), out = keep ? T(x * (1/(1-p))) : 0.
  * Replaces: the two F.dropout calls on the attention-norm output, solution/ops.py:775-777 (and
@@ -317,6 +333,24 @@ int rus_lora_bwd_w(const void* x, int64_t stride_x, const uint32_t* bits_q,
                    int64_t d_q, int64_t d_v, int32_t r, void* g_a_q, void* g_b_q, void* g_a_v,
                    void* g_b_v, float* workspace, int64_t workspace_floats, int32_t* counters,
                    int64_t n_counters, void* stream);
+
+/*
+ * rus_lora_bwd_w plus the input-gradient expansion of rus_lora_bwd_x in the same launch, for a
+ * caller that already holds d_mid_q / d_mid_v (e.g. from rus_qkv_rope_bwd_mid):
+ *   dx = fp16(fp16(dx + fp16 drop_q(fp16(d_mid_q A_q))) + fp16 drop_v(fp16(d_mid_v A_v)))
+ * in place on dx [n_tokens, d] (row stride stride_dx), a_t_q = A_q^T [d, r] (v alike), with the
+ * weight gradients as rus_lora_bwd_w. Replaces: solution/ops.py:975-992 after d_mid (the dx_drop
+ * products, the masked adds and the four weight-gradient products). d % 32 == 0; workspace /
+ * counters: those of RUS_LORA_BWD_W.
+ */
+int rus_lora_bwd_xw(const void* x, int64_t stride_x, const uint32_t* bits_q,
+                    const uint32_t* bits_v, float p_q, float p_v, const void* dq_lora,
+                    const void* dv_lora, const void* mid_q, const void* mid_v,
+                    const void* d_mid_q, const void* d_mid_v, int64_t n_tokens, int64_t d,
+                    int64_t d_q, int64_t d_v, int32_t r, void* g_a_q, void* g_b_q, void* g_a_v,
+                    void* g_b_v, const void* a_t_q, const void* a_t_v, void* dx,
+                    int64_t stride_dx, float* workspace, int64_t workspace_floats,
+                    int32_t* counters, int64_t n_counters, void* stream);
 
 /*
  * SwiGLU forward: out = T( g*sigmoid(g) * u ), sigmoid(g) = 1/(1+exp(-g)).

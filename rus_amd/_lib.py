@@ -11,7 +11,7 @@ import threading
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "librus_amd.so"
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 DTYPE_F16 = 0
 DTYPE_F32 = 1
@@ -58,6 +58,9 @@ SIGNATURES: dict[str, list] = {
                        _i64, _vp, _vp, _f32, _f32, _vp, _i64, _vp, _i64, _vp],
     "rus_lora_bwd_w": [_vp, _i64, _vp, _vp, _f32, _f32, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64,
                        _i64, _i64, _i32, _vp, _vp, _vp, _vp, _vp, _i64, _vp, _i64, _vp],
+    "rus_lora_bwd_xw": [_vp, _i64, _vp, _vp, _f32, _f32, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64,
+                        _i64, _i64, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _vp, _i64, _vp,
+                        _i64, _vp],
     "rus_lmhead_ce_loss": [_vp, _vp, _i64, _vp, _vp, _vp, _vp],
     "rus_attn_varlen_fwd": [_vp, _vp, _vp, _vp, _i32, _i64, _i32, _i32, _i32, _i32, _f32, _vp, _vp,
                             _vp],
@@ -66,6 +69,8 @@ SIGNATURES: dict[str, list] = {
     "rus_rmsnorm_fwd": [_vp, _vp, _vp, _i32, _vp, _vp, _vp, _i64, _i64, _i64, _f32, _i32, _vp],
     "rus_rmsnorm_bwd": [_vp, _vp, _vp, _i32, _vp, _vp, _vp, _i64, _i64, _i64, _i32, _vp],
     "rus_rmsnorm_bwd_parts": [_vp, _i32, _vp, _vp, _i32, _vp, _vp, _vp, _i64, _i64, _i64, _vp],
+    "rus_qkv_rope_bwd_mid": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _vp,
+                             _i64, _i64, _i64, _i64, _f32, _f32, _i32, _i32, _i32, _vp, _vp],
     "rus_qkv_lora_rope_fwd": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64,
                               _i64, _i64, _f32, _f32, _i32, _i32, _i32, _vp, _i32, _vp],
     "rus_qkv_rope_bwd": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _f32,

@@ -484,64 +484,76 @@ lmhead_grad_hidden_kernel(GemmArgs g, StoreParams p) {
 }
 
 // ---------------------------------------------------------------------------------------------
-// Combine partial statistics (one lane per token, four waves over the partials) and finish.
+// Combine partial statistics: one lane per token, 16 waves per 64 tokens, each wave merging a
+// contiguous range of partials eight loads at a time, then wave 0 merging the 16 results in
+// wave order (deterministic; ties keep the smallest vocabulary index).
 // ---------------------------------------------------------------------------------------------
 
-__global__ __launch_bounds__(256) void lmhead_combine_kernel(
+constexpr int kCombWaves = 16, kCombDepth = 8;
+
+struct Stat {
+  float m, s, w;
+  int i;
+};
+
+__device__ __forceinline__ void merge_stat(Stat& a, float m, float s, float w, int i) {
+  if (m > a.m) {
+    const float c = exp2_fast((a.m - m) * kLog2e);
+    a.s = a.s * c + s;
+    a.w = a.w * c + w;
+    a.m = m;
+    a.i = i;
+  } else if (m > -INFINITY) {
+    const float c = exp2_fast((m - a.m) * kLog2e);
+    a.s += s * c;
+    a.w += w * c;
+    if (m == a.m && i < a.i) a.i = i;
+  }
+}
+
+__global__ __launch_bounds__(kCombWaves * 64) void lmhead_combine_kernel(
     const float* __restrict__ pm, const float* __restrict__ ps, const float* __restrict__ pw,
     const int32_t* __restrict__ pi, int n_parts, int64_t stride, const float* __restrict__ target,
     const int64_t* __restrict__ labels, int n_tok, float* __restrict__ lse,
     float* __restrict__ nll, float* __restrict__ ent, int64_t* __restrict__ amax) {
-  __shared__ float sm[4][64], ss[4][64], sw[4][64];
-  __shared__ int si[4][64];
+  __shared__ float sm[kCombWaves][64], ss[kCombWaves][64], sw[kCombWaves][64];
+  __shared__ int si[kCombWaves][64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int tok = blockIdx.x * 64 + lane;
-  float M = -INFINITY, S = 0.0f, W = 0.0f;
-  int I = 0x7fffffff;
+  Stat st{-INFINITY, 0.0f, 0.0f, 0x7fffffff};
+  const int per = (n_parts + kCombWaves - 1) / kCombWaves;
+  const int q0 = wave * per, q1 = min(q0 + per, n_parts);
   if (tok < n_tok) {
-    for (int q = wave; q < n_parts; q += 4) {
-      const int64_t o = static_cast<int64_t>(q) * stride + tok;
-      const float m = pm[o], s = ps[o], w = pw[o];
-      const int i = pi[o];
-      if (m > M) {
-        const float c = exp2_fast((M - m) * kLog2e);
-        S = S * c + s;
-        W = W * c + w;
-        M = m;
-        I = i;
-      } else if (m > -INFINITY) {
-        const float c = exp2_fast((m - M) * kLog2e);
-        S = S + s * c;
-        W = W + w * c;
-        if (m == M && i < I) I = i;
+    for (int q = q0; q < q1; q += kCombDepth) {
+      float m[kCombDepth], s[kCombDepth], w[kCombDepth];
+      int ix[kCombDepth];
+#pragma unroll
+      for (int j = 0; j < kCombDepth; ++j) {
+        const int64_t o = static_cast<int64_t>(min(q + j, q1 - 1)) * stride + tok;
+        m[j] = pm[o];
+        s[j] = ps[o];
+        w[j] = pw[o];
+        ix[j] = pi[o];
       }
+#pragma unroll
+      for (int j = 0; j < kCombDepth; ++j)
+        if (q + j < q1) merge_stat(st, m[j], s[j], w[j], ix[j]);
     }
   }
-  sm[wave][lane] = M;
-  ss[wave][lane] = S;
-  sw[wave][lane] = W;
-  si[wave][lane] = I;
+  sm[wave][lane] = st.m;
+  ss[wave][lane] = st.s;
+  sw[wave][lane] = st.w;
+  si[wave][lane] = st.i;
   __syncthreads();
   if (wave != 0 || tok >= n_tok) return;
-  M = sm[0][lane];
-  for (int k = 1; k < 4; ++k) M = fmaxf(M, sm[k][lane]);
-  S = 0.0f;
-  W = 0.0f;
-  I = 0x7fffffff;
-  for (int k = 0; k < 4; ++k) {
-    const float m = sm[k][lane];
-    if (m > -INFINITY) {
-      const float c = exp2_fast((m - M) * kLog2e);
-      S += ss[k][lane] * c;
-      W += sw[k][lane] * c;
-      if (m == M && si[k][lane] < I) I = si[k][lane];
-    }
-  }
-  const float L = M + logf(S);
+  Stat t{-INFINITY, 0.0f, 0.0f, 0x7fffffff};
+  for (int k = 0; k < kCombWaves; ++k)
+    merge_stat(t, sm[k][lane], ss[k][lane], sw[k][lane], si[k][lane]);
+  const float L = t.m + logf(t.s);
   lse[tok] = L;
-  ent[tok] = L - W / S;
+  ent[tok] = L - t.w / t.s;
   nll[tok] = labels[tok] != -100 ? L - target[tok] : 0.0f;
-  amax[tok] = I;
+  amax[tok] = t.i;
 }
 
 // out[i] = T( scale * sum_p parts[p][i] ), four elements per thread (16-byte accesses when every
@@ -638,9 +650,10 @@ extern "C" int rus_lmhead_ce_combine(const float* part_m, const float* part_s, c
       !entropy || !argmax)
     return fail(RUS_ERR_INVALID, "%s: null pointer argument", fn);
   const dim3 grid(static_cast<unsigned>((n_tok + 63) / 64));
-  hipLaunchKernelGGL(lmhead_combine_kernel, grid, dim3(256), 0, static_cast<hipStream_t>(stream),
-                     part_m, part_s, part_w, part_idx, static_cast<int>(n_parts), part_stride,
-                     target, labels, static_cast<int>(n_tok), lse, nll, entropy, argmax);
+  hipLaunchKernelGGL(lmhead_combine_kernel, grid, dim3(kCombWaves * 64), 0,
+                     static_cast<hipStream_t>(stream), part_m, part_s, part_w, part_idx,
+                     static_cast<int>(n_parts), part_stride, target, labels,
+                     static_cast<int>(n_tok), lse, nll, entropy, argmax);
   return check_launch(fn);
 }
 

@@ -325,13 +325,13 @@ struct ExpandArgs {
 // dx = fp16(fp16(dx + fp16(drop_q(fp16(d_mid_q A_q)))) + fp16(drop_v(fp16(d_mid_v A_v)))).
 // Block (column group, tile): wave w forms the dx^T tiles of columns 32 (4 group + w) .. +31 and
 // the tile's 32 tokens (MFMA over the ranks), then updates dx for its lane's token in place.
+// One wave's dx^T tile: columns 32 dt .. +31, tokens t0 .. t0 + 31 (no barrier: the caller may
+// return early per wave).
 template <int R, bool DROP>
-__global__ __launch_bounds__(64 * kSW) void lora_bwd_expand_kernel(ExpandArgs a) {
+__device__ __forceinline__ void expand_wave(const ExpandArgs& a, int dt, int64_t t0) {
   constexpr int KS = R > 16 ? 2 : 1;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, h = lane >> 5, col = lane & 31;
-  const int dt = blockIdx.x * kSW + wave;  // 32-column tile of dx
-  if (dt * 32 >= a.d) return;              // (no barrier in this kernel)
-  const int64_t t0 = static_cast<int64_t>(blockIdx.y) * kTok;
+  const int lane = threadIdx.x & 63, h = lane >> 5, col = lane & 31;
+  if (dt * 32 >= a.d) return;
   const int64_t t = min(t0 + col, a.n_tok - 1);  // this lane's token (column of dx^T)
   const int64_t drow = static_cast<int64_t>(dt) * 32 + col;  // A-operand row of this lane
   f16x8 aq[KS], av[KS], mq[KS], mv[KS];
@@ -370,6 +370,12 @@ __global__ __launch_bounds__(64 * kSW) void lora_bwd_expand_kernel(ExpandArgs a)
     }
     *reinterpret_cast<f16x4*>(p + off) = c;
   }
+}
+
+template <int R, bool DROP>
+__global__ __launch_bounds__(64 * kSW) void lora_bwd_expand_kernel(ExpandArgs a) {
+  expand_wave<R, DROP>(a, blockIdx.x * kSW + (threadIdx.x >> 6),
+                       static_cast<int64_t>(blockIdx.y) * kTok);
 }
 
 // R consecutive fp16 values (R = 4: one 8-byte load; else 16-byte loads) as floats.
@@ -446,11 +452,12 @@ __device__ __forceinline__ void bwd_w_tokens(float (&acc)[R], const f16* __restr
   }
 }
 
+// Block (blk, chunk) of the n_blk x n_chunk weight-gradient grid.
 template <int R>
-__global__ __launch_bounds__(64 * kWWaves) void lora_bwd_w_kernel(BwdWArgs a) {
+__device__ __forceinline__ void bwd_w_block(const BwdWArgs& a, int blk, int chunk, int n_blk,
+                                            int n_chunk) {
   constexpr int RS = R < 16 ? R : 16;  // ranks summed through LDS per pass
   __shared__ float s_acc[kWWaves][RS][kWCols];
-  const int blk = blockIdx.x, chunk = blockIdx.y;
   int p = 0;
 #pragma unroll
   for (int k = 1; k < 4; ++k) p += blk >= a.first_block[k] ? 1 : 0;
@@ -471,7 +478,7 @@ __global__ __launch_bounds__(64 * kWWaves) void lora_bwd_w_kernel(BwdWArgs a) {
     bwd_w_tokens<R, false>(acc, a.x[p], a.sx[p], nullptr, 1.0f, a.m[p], cc, live, t_begin + w,
                            t_end, a.words);
   constexpr int kPart = R * kWCols;  // floats per partial, rank-major [R][64]
-  float* mine = a.part + (static_cast<int64_t>(chunk) * gridDim.x + blk) * kPart;
+  float* mine = a.part + (static_cast<int64_t>(chunk) * n_blk + blk) * kPart;
 #pragma unroll
   for (int j0 = 0; j0 < R; j0 += RS) {
 #pragma unroll
@@ -485,11 +492,11 @@ __global__ __launch_bounds__(64 * kWWaves) void lora_bwd_w_kernel(BwdWArgs a) {
     }
     __syncthreads();
   }
-  if (!arrive_last(a.counters + blk, gridDim.y)) return;
+  if (!arrive_last(a.counters + blk, n_chunk)) return;
   // Every thread owns kO outputs; the partials of kB chunks are loaded together, then added in
   // chunk order.
   constexpr int kThr = 64 * kWWaves, kO = (kPart + kThr - 1) / kThr, kB = kO > 2 ? 4 : 8;
-  const int n_ch = static_cast<int>(gridDim.y);
+  const int n_ch = n_chunk;
   float tot[kO];
 #pragma unroll
   for (int i = 0; i < kO; ++i) tot[i] = 0.0f;
@@ -498,7 +505,7 @@ __global__ __launch_bounds__(64 * kWWaves) void lora_bwd_w_kernel(BwdWArgs a) {
 #pragma unroll
     for (int b = 0; b < kB; ++b) {
       const float* pc =
-          a.part + (static_cast<int64_t>(min(ch0 + b, n_ch - 1)) * gridDim.x + blk) * kPart;
+          a.part + (static_cast<int64_t>(min(ch0 + b, n_ch - 1)) * n_blk + blk) * kPart;
 #pragma unroll
       for (int i = 0; i < kO; ++i) v[b][i] = load_partial(pc + min<int>(threadIdx.x + kThr * i, kPart - 1));
     }
@@ -519,6 +526,30 @@ __global__ __launch_bounds__(64 * kWWaves) void lora_bwd_w_kernel(BwdWArgs a) {
     else
       a.g[p][col * R + j] = hs;
   }
+}
+
+template <int R>
+__global__ __launch_bounds__(64 * kWWaves) void lora_bwd_w_kernel(BwdWArgs a) {
+  bwd_w_block<R>(a, blockIdx.x, blockIdx.y, gridDim.x, gridDim.y);
+}
+
+// The weight gradients and the input-gradient expansion in one launch (both read the finished
+// d_mid): blocks [0, n_blk * n_chunk) are weight-gradient blocks (blk fastest), the rest
+// expansion blocks of kWWaves column tiles of one 32-token tile each. Each block's role is
+// uniform, so the weight-gradient blocks' barriers and arrival counters involve only them.
+template <int R, bool DROP>
+__global__ __launch_bounds__(64 * kWWaves) void lora_bwd_xw_kernel(BwdWArgs a, ExpandArgs x,
+                                                                  int n_blk, int n_chunk,
+                                                                  int x_col_blocks) {
+  const int b = blockIdx.x;
+  const int n_w = n_blk * n_chunk;
+  if (b < n_w) {
+    bwd_w_block<R>(a, b % n_blk, b / n_blk, n_blk, n_chunk);
+    return;
+  }
+  const int e = b - n_w;
+  expand_wave<R, DROP>(x, (e % x_col_blocks) * kWWaves + (threadIdx.x >> 6),
+                       static_cast<int64_t>(e / x_col_blocks) * kTok);
 }
 
 bool rank_ok(int r) { return r == 4 || r == 8 || r == 16 || r == 32; }
@@ -713,16 +744,15 @@ extern "C" int rus_lora_bwd_x(const void* dq_lora, const void* dv_lora, int64_t 
   return check_launch(fn);
 }
 
-extern "C" int rus_lora_bwd_w(const void* x, int64_t stride_x, const uint32_t* bits_q,
-                              const uint32_t* bits_v, float p_q, float p_v, const void* dq_lora,
-                              const void* dv_lora, const void* mid_q, const void* mid_v,
-                              const void* d_mid_q, const void* d_mid_v, int64_t n_tokens,
-                              int64_t d, int64_t d_q, int64_t d_v, int32_t r, void* g_a_q,
-                              void* g_b_q, void* g_a_v, void* g_b_v, float* workspace,
-                              int64_t workspace_floats, int32_t* counters, int64_t n_counters,
-                              void* stream) {
+// Checks and fills the weight-gradient arguments shared by rus_lora_bwd_w and rus_lora_bwd_xw.
+static int bwd_w_args(const char* fn, const void* x, int64_t stride_x, const uint32_t* bits_q,
+                      const uint32_t* bits_v, float p_q, float p_v, const void* dq_lora,
+                      const void* dv_lora, const void* mid_q, const void* mid_v,
+                      const void* d_mid_q, const void* d_mid_v, int64_t n_tokens, int64_t d,
+                      int64_t d_q, int64_t d_v, int32_t r, void* g_a_q, void* g_b_q,
+                      void* g_a_v, void* g_b_v, float* workspace, int64_t workspace_floats,
+                      int32_t* counters, int64_t n_counters, rus::BwdWArgs& a) {
   using namespace rus;
-  const char* fn = "rus_lora_bwd_w";
   if ((bits_q == nullptr) != (bits_v == nullptr))
     return fail(RUS_ERR_INVALID, "%s: give the keep bits of both branches or of neither", fn);
   if (!rank_ok(r)) return fail(RUS_ERR_UNSUPPORTED, "%s: rank %d not in {4,8,16,32}", fn, r);
@@ -740,7 +770,6 @@ extern "C" int rus_lora_bwd_w(const void* x, int64_t stride_x, const uint32_t* b
                             workspace_floats, counters, n_counters))
     return e;
   if (w_chunks(n_tokens) > 65535) return fail(RUS_ERR_UNSUPPORTED, "%s: too many tokens", fn);
-  BwdWArgs a;
   const f16* xs[4] = {static_cast<const f16*>(x), static_cast<const f16*>(dq_lora),
                       static_cast<const f16*>(x), static_cast<const f16*>(dv_lora)};
   const int64_t sxs[4] = {stride_x, d_q, stride_x, d_v};
@@ -766,6 +795,24 @@ extern "C" int rus_lora_bwd_w(const void* x, int64_t stride_x, const uint32_t* b
   a.words = (d + 31) / 32;
   a.part = workspace;
   a.counters = counters;
+  return RUS_OK;
+}
+
+extern "C" int rus_lora_bwd_w(const void* x, int64_t stride_x, const uint32_t* bits_q,
+                              const uint32_t* bits_v, float p_q, float p_v, const void* dq_lora,
+                              const void* dv_lora, const void* mid_q, const void* mid_v,
+                              const void* d_mid_q, const void* d_mid_v, int64_t n_tokens,
+                              int64_t d, int64_t d_q, int64_t d_v, int32_t r, void* g_a_q,
+                              void* g_b_q, void* g_a_v, void* g_b_v, float* workspace,
+                              int64_t workspace_floats, int32_t* counters, int64_t n_counters,
+                              void* stream) {
+  using namespace rus;
+  const char* fn = "rus_lora_bwd_w";
+  BwdWArgs a;
+  if (int e = bwd_w_args(fn, x, stride_x, bits_q, bits_v, p_q, p_v, dq_lora, dv_lora, mid_q,
+                         mid_v, d_mid_q, d_mid_v, n_tokens, d, d_q, d_v, r, g_a_q, g_b_q, g_a_v,
+                         g_b_v, workspace, workspace_floats, counters, n_counters, a))
+    return e;
   const dim3 grid(static_cast<uint32_t>(a.first_block[4]),
                   static_cast<uint32_t>(w_chunks(n_tokens)));
   hipStream_t st = static_cast<hipStream_t>(stream);
@@ -775,5 +822,53 @@ extern "C" int rus_lora_bwd_w(const void* x, int64_t stride_x, const uint32_t* b
     break;
   switch (r) { RUS_BW(4) RUS_BW(8) RUS_BW(16) RUS_BW(32) }
 #undef RUS_BW
+  return check_launch(fn);
+}
+
+extern "C" int rus_lora_bwd_xw(const void* x, int64_t stride_x, const uint32_t* bits_q,
+                               const uint32_t* bits_v, float p_q, float p_v, const void* dq_lora,
+                               const void* dv_lora, const void* mid_q, const void* mid_v,
+                               const void* d_mid_q, const void* d_mid_v, int64_t n_tokens,
+                               int64_t d, int64_t d_q, int64_t d_v, int32_t r, void* g_a_q,
+                               void* g_b_q, void* g_a_v, void* g_b_v, const void* a_t_q,
+                               const void* a_t_v, void* dx, int64_t stride_dx, float* workspace,
+                               int64_t workspace_floats, int32_t* counters, int64_t n_counters,
+                               void* stream) {
+  using namespace rus;
+  const char* fn = "rus_lora_bwd_xw";
+  BwdWArgs a;
+  if (int e = bwd_w_args(fn, x, stride_x, bits_q, bits_v, p_q, p_v, dq_lora, dv_lora, mid_q,
+                         mid_v, d_mid_q, d_mid_v, n_tokens, d, d_q, d_v, r, g_a_q, g_b_q, g_a_v,
+                         g_b_v, workspace, workspace_floats, counters, n_counters, a))
+    return e;
+  if (!a_t_q || !a_t_v || !dx) return fail(RUS_ERR_INVALID, "%s: null pointer argument", fn);
+  if (d % 32 || stride_dx < d || stride_dx % 4)
+    return fail(RUS_ERR_INVALID, "%s: need d %% 32 == 0 and stride_dx >= d, a multiple of 4", fn);
+  const uintptr_t a_al = r >= 8 ? 16 : 8;
+  if (!aligned(a_t_q, a_al) || !aligned(a_t_v, a_al) || !aligned(dx, 8) ||
+      !aligned(d_mid_q, a_al) || !aligned(d_mid_v, a_al))
+    return fail(RUS_ERR_INVALID, "%s: misaligned operand", fn);
+  // n_tokens == 0: no expansion blocks; the weight-gradient blocks still write zeros.
+  const int64_t n_blk = a.first_block[4], n_chunk = w_chunks(n_tokens);
+  const int64_t x_col_blocks = (d / 32 + kWWaves - 1) / kWWaves;
+  const int64_t blocks = n_blk * n_chunk + x_col_blocks * tiles(n_tokens);
+  if (blocks >= (int64_t(1) << 31)) return fail(RUS_ERR_UNSUPPORTED, "%s: too many tokens", fn);
+  ExpandArgs xa{static_cast<const f16*>(d_mid_q), static_cast<const f16*>(d_mid_v),
+                static_cast<const f16*>(a_t_q), static_cast<const f16*>(a_t_v), n_tokens, d,
+                static_cast<f16*>(dx), stride_dx, bits_q, bits_v, (d + 31) / 32,
+                bits_q ? 1.0f / (1.0f - p_q) : 1.0f, bits_v ? 1.0f / (1.0f - p_v) : 1.0f};
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const dim3 grid(static_cast<uint32_t>(blocks)), blk(64 * kWWaves);
+  const int nb = static_cast<int>(n_blk), nc = static_cast<int>(n_chunk),
+            xc = static_cast<int>(x_col_blocks);
+#define RUS_BXW(RR)                                                                          \
+  case RR:                                                                                   \
+    if (bits_q)                                                                              \
+      hipLaunchKernelGGL((lora_bwd_xw_kernel<RR, true>), grid, blk, 0, st, a, xa, nb, nc, xc); \
+    else                                                                                     \
+      hipLaunchKernelGGL((lora_bwd_xw_kernel<RR, false>), grid, blk, 0, st, a, xa, nb, nc, xc); \
+    break;
+  switch (r) { RUS_BXW(4) RUS_BXW(8) RUS_BXW(16) RUS_BXW(32) }
+#undef RUS_BXW
   return check_launch(fn);
 }

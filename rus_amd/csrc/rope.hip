@@ -268,6 +268,170 @@ __global__ __launch_bounds__(kThreads) void rope_bwd_kernel(RopeBwdArgs<T> a) {
   }
 }
 
+// rope_bwd_kernel<f16, true> that also forms the rank-R LoRA products of its outputs:
+// d_mid_q = fp16(dq_lora B_q) [N, R] and d_mid_v = fp16(dv_lora B_v) (solution/ops.py:975-992,
+// d_mid = dq @ B), with B given rank-major (bt = B^T [R, d]). A block holds whole tokens (every
+// slot of a token), so the reductions over a token's columns stay in the block: each thread
+// forms R partial sums over its 16 elements, a 16-lane transpose reduction leaves one rank per
+// lane, and the per-token merge of the 16-lane groups (all of one kind: the slot ranges of the
+// q, k and v heads are multiples of 16) runs in group order through LDS.
+struct RopeBwdMidArgs {
+  RopeBwdArgs<f16> b;
+  const f16* bt_q;  // [R, h_q * head_dim]
+  const f16* bt_v;  // [R, h_kv * head_dim]
+  f16* dmid_q;      // [N, R]
+  f16* dmid_v;
+};
+
+constexpr int kMidR = 16;  // rank of the fused d_mid products
+
+// p (16 values per lane) -> lane l holds the sum of p[l % 16] over its 16-lane group.
+__device__ __forceinline__ float group16_transpose_sum(const float (&p)[16], int lane) {
+  float v8[8], v4[4], v2[2];
+  const bool b3 = lane & 8, b2 = lane & 4, b1 = lane & 2, b0 = lane & 1;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float send = b3 ? p[i] : p[i + 8];
+    v8[i] = (b3 ? p[i + 8] : p[i]) + __shfl_xor(send, 8);
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float send = b2 ? v8[i] : v8[i + 4];
+    v4[i] = (b2 ? v8[i + 4] : v8[i]) + __shfl_xor(send, 4);
+  }
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const float send = b1 ? v4[i] : v4[i + 2];
+    v2[i] = (b1 ? v4[i + 2] : v4[i]) + __shfl_xor(send, 2);
+  }
+  const float send = b0 ? v2[0] : v2[1];
+  return (b0 ? v2[1] : v2[0]) + __shfl_xor(send, 1);
+}
+
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+
+// The B^T fragments a thread needs: rows r of bt (length d) at columns c .. c + 7 and
+// c + half .. c + half + 7, kept packed (4 registers per 8 values).
+struct MidFrags {
+  f16x8_t lo[kMidR], hi[kMidR];
+};
+
+__device__ __forceinline__ void load_mid_frags(MidFrags& f, const f16* __restrict__ bt, int64_t d,
+                                               int64_t c, int half) {
+#pragma unroll
+  for (int r = 0; r < kMidR; ++r) {
+    f.lo[r] = *reinterpret_cast<const f16x8_t*>(bt + r * d + c);
+    f.hi[r] = *reinterpret_cast<const f16x8_t*>(bt + r * d + c + half);
+  }
+}
+
+// p[r] += sum_i lo[i] bt[r][c + i] + hi[i] bt[r][c + half + i].
+__device__ __forceinline__ void mid_partial(float (&p)[kMidR], const float (&lo)[kSpan],
+                                            const float (&hi)[kSpan], const MidFrags& f) {
+#pragma unroll
+  for (int r = 0; r < kMidR; ++r)
+#pragma unroll
+    for (int i = 0; i < kSpan; ++i)
+      p[r] += lo[i] * static_cast<float>(f.lo[r][i]) + hi[i] * static_cast<float>(f.hi[r][i]);
+}
+
+__global__ __launch_bounds__(kThreads) void rope_bwd_mid_kernel(RopeBwdMidArgs m) {
+  const RopeBwdArgs<f16>& a = m.b;
+  const int half = a.head_dim / 2;
+  const int per_head = half / kSpan;
+  const int heads = a.h_q + 2 * a.h_kv;
+  const int slots = heads * per_head;  // divides kThreads, multiple of 16 (host-checked)
+  const int tpb = kThreads / slots;
+  const int tb = threadIdx.x / slots;
+  const int slot = threadIdx.x - tb * slots;
+  const int64_t t0 = static_cast<int64_t>(blockIdx.x) * tpb;
+  const int64_t t = t0 + tb;
+  const int hd = slot / per_head;
+  const int j = (slot - hd * per_head) * kSpan;
+  const int lane = threadIdx.x & 63;
+  const int64_t d_q = static_cast<int64_t>(a.h_q) * a.head_dim;
+  const int64_t d_v = static_cast<int64_t>(a.h_kv) * a.head_dim;
+
+  float p[kMidR];
+#pragma unroll
+  for (int r = 0; r < kMidR; ++r) p[r] = 0.0f;
+  // The B fragments first: their loads do not wait for the gradient loads and stores below.
+  const bool is_q = hd < a.h_q, is_v = hd >= a.h_q + a.h_kv;
+  MidFrags f;
+  if (t < a.n_tokens && (is_q || is_v))
+    load_mid_frags(f, is_q ? m.bt_q : m.bt_v, is_q ? d_q : d_v,
+                   static_cast<int64_t>(is_q ? hd : hd - a.h_q - a.h_kv) * a.head_dim + j, half);
+  if (t < a.n_tokens) {
+    f16* out = a.dqkv + t * a.stride_dqkv + static_cast<int64_t>(hd) * a.head_dim;
+    float lo[kSpan], hi[kSpan];
+    if (is_v) {  // dV: copy, scale into dv_lora, d_mid_v partials
+      const int kv = hd - a.h_q - a.h_kv;
+      const f16* src = a.dv + (t * a.h_kv + kv) * a.head_dim;
+      load_f32<f16, kSpan>(src + j, lo);
+      load_f32<f16, kSpan>(src + j + half, hi);
+      store_from_f32<f16, kSpan>(out + j, lo);
+      store_from_f32<f16, kSpan>(out + j + half, hi);
+#pragma unroll
+      for (int i = 0; i < kSpan; ++i) {
+        lo[i] = round_to<f16>(lo[i] * a.scale_v);  // the stored dv_lora values
+        hi[i] = round_to<f16>(hi[i] * a.scale_v);
+      }
+      f16* l = a.dv_lora + (t * a.h_kv + kv) * a.head_dim;
+      store_from_f32<f16, kSpan>(l + j, lo);
+      store_from_f32<f16, kSpan>(l + j + half, hi);
+      mid_partial(p, lo, hi, f);
+    } else {
+      const f16* src = hd < a.h_q ? a.dq + (t * a.h_q + hd) * a.head_dim
+                                  : a.dk + (t * a.h_kv + (hd - a.h_q)) * a.head_dim;
+      load_f32<f16, kSpan>(src + j, lo);
+      load_f32<f16, kSpan>(src + j + half, hi);
+      const int64_t ps = clamp_pos(a.pos, t, a.n_pos, a.err_flag);
+      float cl[kSpan], ch[kSpan], sl[kSpan], sh[kSpan];
+      const f16* cr = a.cos + ps * a.stride_cos;
+      const f16* sr = a.sin + ps * a.stride_cos;
+      load_f32<f16, kSpan>(cr + j, cl);
+      load_f32<f16, kSpan>(cr + j + half, ch);
+      load_f32<f16, kSpan>(sr + j, sl);
+      load_f32<f16, kSpan>(sr + j + half, sh);
+      float ol[kSpan], oh[kSpan];
+#pragma unroll
+      for (int i = 0; i < kSpan; ++i) {
+        ol[i] = round_to<f16>(lo[i] * cl[i] + hi[i] * sh[i]);
+        oh[i] = round_to<f16>(hi[i] * ch[i] - lo[i] * sl[i]);
+      }
+      store_from_f32<f16, kSpan>(out + j, ol);
+      store_from_f32<f16, kSpan>(out + j + half, oh);
+      if (is_q) {
+#pragma unroll
+        for (int i = 0; i < kSpan; ++i) {
+          ol[i] = round_to<f16>(ol[i] * a.scale_q);  // the stored dq_lora values
+          oh[i] = round_to<f16>(oh[i] * a.scale_q);
+        }
+        f16* l = a.dq_lora + (t * a.h_q + hd) * a.head_dim;
+        store_from_f32<f16, kSpan>(l + j, ol);
+        store_from_f32<f16, kSpan>(l + j + half, oh);
+        mid_partial(p, ol, oh, f);
+      }
+    }
+  }
+  __shared__ float red[kThreads / 16][kMidR];
+  red[threadIdx.x >> 4][threadIdx.x & 15] = group16_transpose_sum(p, lane);
+  __syncthreads();
+  const int groups = slots / 16;
+  const int gq = a.h_q * per_head / 16, gv0 = (a.h_q + a.h_kv) * per_head / 16;
+  if (threadIdx.x < tpb * 2 * kMidR) {
+    const int tk = threadIdx.x / (2 * kMidR), rr = threadIdx.x % (2 * kMidR);
+    const int64_t tt = t0 + tk;
+    if (tt < a.n_tokens) {
+      const bool out_q = rr < kMidR;
+      const int r = out_q ? rr : rr - kMidR;
+      float acc = 0.0f;
+      for (int g = out_q ? 0 : gv0; g < (out_q ? gq : groups); ++g) acc += red[tk * groups + g][r];
+      (out_q ? m.dmid_q : m.dmid_v)[tt * kMidR + r] = static_cast<f16>(acc);
+    }
+  }
+}
+
 int check_heads(const char* fn, int64_t n_tokens, int32_t h_q, int32_t h_kv, int32_t head_dim,
                 int64_t n_pos, int64_t stride_cos, int32_t dtype) {
   if (dtype != RUS_DTYPE_F16 && dtype != RUS_DTYPE_F32)
@@ -344,6 +508,26 @@ int bwd_typed(const RopeBwdArgs<T>& a, hipStream_t st) {
   else
     hipLaunchKernelGGL((rope_bwd_kernel<T, false>), grid, dim3(kThreads), 0, st, a);
   return check_launch("rus_qkv_rope_bwd");
+}
+
+int bwd_mid(const RopeBwdMidArgs& m, hipStream_t st) {
+  const char* fn = "rus_qkv_rope_bwd_mid";
+  const RopeBwdArgs<f16>& a = m.b;
+  const int per_head = a.head_dim / 2 / kSpan;
+  const int slots = (a.h_q + 2 * a.h_kv) * per_head;
+  if (kThreads % slots || slots % 16 || (a.h_q * per_head) % 16 || (a.h_kv * per_head) % 16)
+    return fail(RUS_ERR_UNSUPPORTED,
+                "%s: h_q=%d h_kv=%d head_dim=%d: a token's slots must divide %d and each head "
+                "kind's slots be a multiple of 16", fn, a.h_q, a.h_kv, a.head_dim, kThreads);
+  if (!aligned(a.dq, 16) || !aligned(a.dk, 16) || !aligned(a.dv, 16) ||
+      !aligned8<f16>(a.cos, a.stride_cos) || !aligned8<f16>(a.sin, a.stride_cos) ||
+      !aligned8<f16>(a.dqkv, a.stride_dqkv) || !aligned(a.dq_lora, 16) ||
+      !aligned(a.dv_lora, 16) || !aligned(m.bt_q, 16) || !aligned(m.bt_v, 16))
+    return fail(RUS_ERR_INVALID, "%s: pointers/strides must be 16-byte aligned", fn);
+  const int64_t tpb = kThreads / slots;
+  const dim3 grid(static_cast<unsigned>((a.n_tokens + tpb - 1) / tpb));
+  hipLaunchKernelGGL(rope_bwd_mid_kernel, grid, dim3(kThreads), 0, st, m);
+  return check_launch(fn);
 }
 
 }  // namespace
@@ -464,4 +648,41 @@ extern "C" int rus_qkv_lora_rope_fwd_mid(const void* qkv, const void* mid_q, con
   a.b_q = static_cast<const f16*>(b_q);
   a.b_v = static_cast<const f16*>(b_v);
   return fwd_mid(a, r, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int rus_qkv_rope_bwd_mid(const void* dq_rot, const void* dk_rot, const void* dv,
+                                    const void* cos, const void* sin, const int64_t* pos_ids,
+                                    void* dqkv, void* dq_lora, void* dv_lora, const void* bt_q,
+                                    const void* bt_v, int32_t r, void* d_mid_q, void* d_mid_v,
+                                    int64_t n_tokens, int64_t stride_dqkv, int64_t stride_cos,
+                                    int64_t n_pos, float scale_q, float scale_v, int32_t h_q,
+                                    int32_t h_kv, int32_t head_dim, int32_t* err_flag,
+                                    void* stream) {
+  using namespace rus;
+  const char* fn = "rus_qkv_rope_bwd_mid";
+  if (int e = check_heads(fn, n_tokens, h_q, h_kv, head_dim, n_pos, stride_cos, RUS_DTYPE_F16))
+    return e;
+  if (r != kMidR) return fail(RUS_ERR_UNSUPPORTED, "%s: rank %d (only %d)", fn, r, kMidR);
+  if (n_tokens == 0) return RUS_OK;
+  if (!dq_rot || !dk_rot || !dv || !cos || !sin || !pos_ids || !dqkv || !dq_lora || !dv_lora ||
+      !bt_q || !bt_v || !d_mid_q || !d_mid_v)
+    return fail(RUS_ERR_INVALID, "%s: null pointer argument", fn);
+  if (stride_dqkv < static_cast<int64_t>(h_q + 2 * h_kv) * head_dim)
+    return fail(RUS_ERR_INVALID, "%s: stride_dqkv smaller than a row", fn);
+  RopeBwdMidArgs m{};
+  m.b = RopeBwdArgs<f16>{static_cast<const f16*>(dq_rot), static_cast<const f16*>(dk_rot),
+                         static_cast<const f16*>(dv),     static_cast<const f16*>(cos),
+                         static_cast<const f16*>(sin),    pos_ids,
+                         static_cast<f16*>(dqkv),         static_cast<f16*>(dq_lora),
+                         static_cast<f16*>(dv_lora),      n_tokens,
+                         stride_dqkv,                     stride_cos,
+                         n_pos,                           scale_q,
+                         scale_v,                         h_q,
+                         h_kv,                            head_dim,
+                         err_flag};
+  m.bt_q = static_cast<const f16*>(bt_q);
+  m.bt_v = static_cast<const f16*>(bt_v);
+  m.dmid_q = static_cast<f16*>(d_mid_q);
+  m.dmid_v = static_cast<f16*>(d_mid_v);
+  return bwd_mid(m, static_cast<hipStream_t>(stream));
 }

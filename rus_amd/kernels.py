@@ -30,6 +30,8 @@ __all__ = [
     "qkv_rope_fwd",
     "qkv_rope_bwd",
     "qkv_rope_bwd_lora",
+    "qkv_rope_bwd_lora_mid",
+    "rope_bwd_mid_supported",
     "lora_dropout_fwd",
     "lora_dropout_bwd_add",
     "dropout_keep_bits",
@@ -580,7 +582,7 @@ def qkv_rope_fwd(
 
 
 def _rope_bwd(fn, dq_rot, dk_rot, dv_out, cos, sin, pos_ids, h_q, h_kv, head_dim, scale_q,
-              scale_v, with_lora):
+              scale_v, with_lora, mid=None):
     _require_device(fn, dq_rot, dk_rot, dv_out, cos, sin, pos_ids)
     dt = _dtype_code(fn, dq_rot.dtype)
     n_tokens = dq_rot.shape[0]
@@ -605,6 +607,20 @@ def _rope_bwd(fn, dq_rot, dk_rot, dv_out, cos, sin, pos_ids, h_q, h_kv, head_dim
         dvl = torch.empty((n_tokens, kv_dim), dtype=dq_c.dtype, device=dq_c.device)
     es = dq_c.element_size()
     width = q_dim + 2 * kv_dim
+    if mid is not None:
+        bt_q, bt_v = mid
+        r = bt_q.shape[0]
+        dmq = torch.empty((n_tokens, r), dtype=dq_c.dtype, device=dq_c.device)
+        dmv = torch.empty((n_tokens, r), dtype=dq_c.dtype, device=dq_c.device)
+        _launch(
+            "rope_bwd", n_tokens * (es * (2 * width + 2 * head_dim + q_dim + kv_dim + 2 * r) + 8)
+            + es * r * (q_dim + kv_dim), 2 * n_tokens * r * (q_dim + kv_dim),
+            "rus_qkv_rope_bwd_mid", dq_c.data_ptr(), dk_c.data_ptr(), dv_c.data_ptr(),
+            cos.data_ptr(), sin.data_ptr(), pos.data_ptr(), dqkv.data_ptr(), dql.data_ptr(),
+            dvl.data_ptr(), bt_q.data_ptr(), bt_v.data_ptr(), r, dmq.data_ptr(), dmv.data_ptr(),
+            n_tokens, dqkv.stride(0), cos.stride(0), cos.shape[0], float(scale_q),
+            float(scale_v), h_q, h_kv, head_dim, None, _stream(dq_c))
+        return dqkv, dql, dvl, dmq, dmv
     _launch(
         "rope_bwd", n_tokens * (es * (2 * width + 2 * head_dim + (q_dim + kv_dim if with_lora else 0)) + 8),
         0, "rus_qkv_rope_bwd",
@@ -614,6 +630,39 @@ def _rope_bwd(fn, dq_rot, dk_rot, dv_out, cos, sin, pos_ids, h_q, h_kv, head_dim
         dt, _stream(dq_c),
     )
     return dqkv, dql, dvl
+
+
+def rope_bwd_mid_supported(h_q: int, h_kv: int, head_dim: int, r: int) -> bool:
+    """Whether ``qkv_rope_bwd_lora_mid`` covers this head layout and rank: rank 16, and a
+    token's (h_q + 2 h_kv) * head_dim / 16 thread slots divide 256 with each head kind's slots a
+    multiple of 16 (so one block holds whole tokens and every 16-lane group one head kind)."""
+    if r != 16 or head_dim % 16:
+        return False
+    per_head = head_dim // 16
+    slots = (h_q + 2 * h_kv) * per_head
+    return 256 % slots == 0 and slots % 16 == 0 and (h_q * per_head) % 16 == 0 and \
+        (h_kv * per_head) % 16 == 0
+
+
+def qkv_rope_bwd_lora_mid(dq_rot, dk_rot, dv_out, cos, sin, pos_ids, scale_q: float,
+                          scale_v: float, bt_q: torch.Tensor, bt_v: torch.Tensor, h_q: int = 12,
+                          h_kv: int = 2, head_dim: int = 128):
+    """``qkv_rope_bwd_lora`` that also returns the LoRA products d_mid_q = fp16(dq_lora B_q) and
+    d_mid_v = fp16(dv_lora B_v) [n_tokens, 16] from the same launch (solution/ops.py:975-992,
+    d_mid = dq @ B). bt_q / bt_v are B^T [16, h * head_dim]. fp16 only. Returns
+    (dqkv, dq_lora, dv_lora, d_mid_q, d_mid_v)."""
+    fn = "qkv_rope_bwd_lora_mid"
+    _require_device(fn, dq_rot, dk_rot, dv_out, cos, sin, pos_ids, bt_q, bt_v)
+    if dq_rot.dtype != torch.float16:
+        raise ValueError(f"{fn}: fp16 gradients only")
+    r = bt_q.shape[0]
+    if not rope_bwd_mid_supported(h_q, h_kv, head_dim, r):
+        raise ValueError(f"{fn}: unsupported layout h_q={h_q} h_kv={h_kv} head_dim={head_dim} "
+                         f"rank={r}")
+    _lora_operand(fn, bt_q, (r, h_q * head_dim), "bt_q")
+    _lora_operand(fn, bt_v, (r, h_kv * head_dim), "bt_v")
+    return _rope_bwd(fn, dq_rot, dk_rot, dv_out, cos, sin, pos_ids, h_q, h_kv, head_dim, scale_q,
+                     scale_v, True, mid=(bt_q, bt_v))
 
 
 def qkv_rope_bwd(
@@ -986,11 +1035,14 @@ def lora_bwd_w(x: torch.Tensor, dq_lora: torch.Tensor, dv_lora: torch.Tensor,
                mid_q: torch.Tensor, mid_v: torch.Tensor, d_mid_q: torch.Tensor,
                d_mid_v: torch.Tensor, g_a_q: torch.Tensor, g_b_q: torch.Tensor,
                g_a_v: torch.Tensor, g_b_v: torch.Tensor, bits_q: torch.Tensor | None = None,
-               bits_v: torch.Tensor | None = None, p_q: float = 0.0, p_v: float = 0.0) -> None:
+               bits_v: torch.Tensor | None = None, p_q: float = 0.0, p_v: float = 0.0,
+               expand=None) -> None:
     """g_a = d_mid^T drop(x) [r, d], g_b = dq^T mid [d_q, r] for both branches (the dropped
     inputs formed from x and the forward's keep bits), fp16 outputs written in place (e.g. views
-    of a flat gradient buffer)."""
-    fn = "lora_bwd_w"
+    of a flat gradient buffer). With ``expand = (a_t_q, a_t_v, dx)`` the same launch also adds
+    the input gradients drop_q(d_mid_q A_q), then drop_v(d_mid_v A_v), into dx in place
+    (``lora_bwd_x`` without its d_mid products; a_t = A^T [d, r])."""
+    fn = "lora_bwd_w" if expand is None else "lora_bwd_xw"
     _require_device(fn, x, dq_lora, dv_lora, mid_q, mid_v, d_mid_q, d_mid_v, g_a_q, g_b_q,
                     g_a_v, g_b_v)
     n, r = mid_q.shape
@@ -1010,12 +1062,26 @@ def lora_bwd_w(x: torch.Tensor, dq_lora: torch.Tensor, dv_lora: torch.Tensor,
     bq = _bits(fn, bits_q, n, d, "bits_q")
     bv = _bits(fn, bits_v, n, d, "bits_v")
     ws, cnt = _lora_scratch(LORA_BWD_W, n, d, d_q, d_v, r, x.device)
-    _launch("lora_bwd_w", 2 * n * (d + d_q + d_v + 4 * r) + n * d // 4,
-            2 * n * r * (2 * d + d_q + d_v), "rus_lora_bwd_w", x2.data_ptr(), x2.stride(0), bq,
-            bv, float(p_q), float(p_v), dq_lora.data_ptr(), dv_lora.data_ptr(),
-            mid_q.data_ptr(), mid_v.data_ptr(), d_mid_q.data_ptr(), d_mid_v.data_ptr(), n, d,
-            d_q, d_v, r, g_a_q.data_ptr(), g_b_q.data_ptr(), g_a_v.data_ptr(), g_b_v.data_ptr(),
-            ws.data_ptr(), ws.numel(), cnt.data_ptr(), cnt.numel(), _stream(mid_q))
+    args = (x2.data_ptr(), x2.stride(0), bq, bv, float(p_q), float(p_v), dq_lora.data_ptr(),
+            dv_lora.data_ptr(), mid_q.data_ptr(), mid_v.data_ptr(), d_mid_q.data_ptr(),
+            d_mid_v.data_ptr(), n, d, d_q, d_v, r, g_a_q.data_ptr(), g_b_q.data_ptr(),
+            g_a_v.data_ptr(), g_b_v.data_ptr())
+    scratch = (ws.data_ptr(), ws.numel(), cnt.data_ptr(), cnt.numel(), _stream(mid_q))
+    nbytes = 2 * n * (d + d_q + d_v + 4 * r) + n * d // 4
+    flops = 2 * n * r * (2 * d + d_q + d_v)
+    if expand is None:
+        _launch("lora_bwd_w", nbytes, flops, "rus_lora_bwd_w", *args, *scratch)
+        return
+    a_t_q, a_t_v, dx = expand
+    _require_device(fn, a_t_q, a_t_v, dx)
+    _lora_operand(fn, a_t_q, (d, r), "a_t_q")
+    _lora_operand(fn, a_t_v, (d, r), "a_t_v")
+    dx2 = _rows(fn, dx, d, "dx")
+    if dx2.data_ptr() != dx.data_ptr() or dx2.dtype != torch.float16 or dx2.shape[0] != n:
+        raise ValueError(f"{fn}: dx must be fp16 [{n}, {d}] with unit column stride")
+    _launch("lora_bwd_w", nbytes + 4 * n * d + 4 * r * d, flops + 4 * n * r * d,
+            "rus_lora_bwd_xw", *args, a_t_q.data_ptr(), a_t_v.data_ptr(), dx2.data_ptr(),
+            dx2.stride(0), *scratch)
 
 
 # ---------------------------------------------------------------------------------------------

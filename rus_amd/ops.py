@@ -804,9 +804,18 @@ def stack_backward(engine, st: StackState, d_final_norm, grad16) -> torch.Tensor
             dq, dk, dv = torch.autograd.grad(attn, (q_req, k_req, v_req), d_attn)
             del q_req, k_req, v_req
         del attn, attn2d, d_attn, q_rot, k_rot, v_out
-        dqkv, dq_scaled, dv_scaled = K.qkv_rope_bwd_lora(dq, dk, dv, cos, sin, pos_ids,
-                                                         meta["scale_q"], meta["scale_v"],
-                                                         h_q=hq, h_kv=hkv, head_dim=hd)
+        # Fused LoRA at rank 16: d_mid from the RoPE backward's launch; the input-gradient
+        # expansion beside the weight gradients in one launch.
+        mid_fused = fused and K.rope_bwd_mid_supported(hq, hkv, hd, qA.shape[0])
+        if mid_fused:
+            qBt, vBt = st.lora16t[4 * l + 1], st.lora16t[4 * l + 3]
+            dqkv, dq_scaled, dv_scaled, d_mid_q, d_mid_v = K.qkv_rope_bwd_lora_mid(
+                dq, dk, dv, cos, sin, pos_ids, meta["scale_q"], meta["scale_v"], qBt, vBt,
+                h_q=hq, h_kv=hkv, head_dim=hd)
+        else:
+            dqkv, dq_scaled, dv_scaled = K.qkv_rope_bwd_lora(dq, dk, dv, cos, sin, pos_ids,
+                                                             meta["scale_q"], meta["scale_v"],
+                                                             h_q=hq, h_kv=hkv, head_dim=hd)
         del dq, dk, dv
 
         # LoRA gradients (solution/ops.py:975-992): weight gradients into the flat buffer, input
@@ -816,7 +825,11 @@ def stack_backward(engine, st: StackState, d_final_norm, grad16) -> torch.Tensor
         del dqkv
         if fused_gemm:
             ws.release_slot(l)  # the layer's last read of the packed slot is enqueued
-        if fused:  # d_mid, the expansion, masks and both adds; then all four weight gradients
+        if mid_fused:  # the expansion into d_norm1 and all four weight gradients, one launch
+            qAt, vAt = st.lora16t[4 * l], st.lora16t[4 * l + 2]
+            K.lora_bwd_w(norm1, dq_scaled, dv_scaled, mid_q, mid_v, d_mid_q, d_mid_v, g_qA, g_qB,
+                         g_vA, g_vB, *bits, expand=(qAt, vAt, d_norm1))
+        elif fused:  # d_mid, the expansion, masks and both adds; then all four weight gradients
             qAt, qBt, vAt, vBt = st.lora16t[4 * l: 4 * l + 4]
             d_mid_q, d_mid_v = K.lora_bwd_x(dq_scaled, dv_scaled, qAt, vAt, qBt, vBt, d_norm1,
                                             *bits)

@@ -91,6 +91,18 @@ def test_header_compiles_as_c():
         ("rus_rmsnorm_bwd_parts", (16, 0, 16, 16, 0, 16, None, 16, 4, 64, 64, None), "n_parts"),
         ("rus_rmsnorm_bwd_parts", (16, 2, 16, 16, 0, 16, None, 16, 4, 60, 60, None),
          "multiples of 8"),
+        # LoRA weight gradients + expansion: width not a multiple of 32, missing dx
+        ("rus_lora_bwd_xw", (16, 40, None, None, 0.0, 0.0, 16, 16, 16, 16, 16, 16, 4, 40, 16, 16,
+                             16, 16, 16, 16, 16, 16, 16, 16, 40, 16, 4096, 16, 4, None),
+         "need d"),
+        ("rus_lora_bwd_xw", (16, 64, None, None, 0.0, 0.0, 16, 16, 16, 16, 16, 16, 4, 64, 16, 16,
+                             16, 16, 16, 16, 16, 16, 16, None, 64, 16, 8192, 16, 4, None),
+         "null pointer"),
+        # RoPE backward with d_mid: rank other than 16, a head layout a block cannot hold
+        ("rus_qkv_rope_bwd_mid", (16, 16, 16, 16, 16, 16, 16, 16, 16, 16, 16, 8, 16, 16, 4, 2048,
+                                  128, 8, 1.0, 1.0, 12, 2, 128, None, None), "rank"),
+        ("rus_qkv_rope_bwd_mid", (16, 16, 16, 16, 16, 16, 16, 16, 16, 16, 16, 16, 16, 16, 4, 2304,
+                                  128, 8, 1.0, 1.0, 12, 3, 128, None, None), "slots"),
     ],
 )
 def test_invalid_arguments_are_rejected_on_the_host(name, args, msg):

@@ -208,3 +208,62 @@ def test_lora_kernels_reject_bad_rank_and_layout():
     bad = torch.zeros(8, 3, dtype=torch.int32, device=DEV)  # 64 columns need 2 words per row
     with pytest.raises(ValueError, match="bits_q"):
         K.lora_down_fwd(x, a4, a4, bad, None, 0.1, 0.0)
+
+
+@pytest.mark.parametrize("n", [1, 3, 300, 707])
+def test_rope_bwd_mid_matches_rope_bwd_and_oracle_products(n):
+    # The RoPE backward with the rank-16 products: its packed and scaled outputs equal the plain
+    # kernel's bit for bit; d_mid = fp16(dq_lora B) within one ulp (different fp32 sum order).
+    hq, hkv, hd, r = 12, 2, 128, 16
+    g = torch.Generator().manual_seed(300 + n)
+    dq = torch.randn(n, hq, hd, generator=g).half()
+    dk = torch.randn(n, hkv, hd, generator=g).half()
+    dv = torch.randn(n, hkv, hd, generator=g).half()
+    n_pos = 600
+    ang = torch.rand(n_pos, hd, generator=g) * 6.3
+    cos, sin = ang.cos().half(), ang.sin().half()
+    pos = torch.randint(0, n_pos, (n,), generator=g)
+    bq = (torch.randn(hq * hd, r, generator=g) * 0.05).half()
+    bv = (torch.randn(hkv * hd, r, generator=g) * 0.05).half()
+    args = tuple(t.to(DEV) for t in (dq, dk, dv, cos, sin, pos)) + (2.0, 0.5)
+    assert K.rope_bwd_mid_supported(hq, hkv, hd, r)
+    got = K.qkv_rope_bwd_lora_mid(*args, bq.t().contiguous().to(DEV), bv.t().contiguous().to(DEV),
+                                  h_q=hq, h_kv=hkv, head_dim=hd)
+    want = K.qkv_rope_bwd_lora(*args, h_q=hq, h_kv=hkv, head_dim=hd)
+    torch.cuda.synchronize()
+    for a, b in zip(got[:3], want):
+        assert torch.equal(a, b)
+    for gm, x, b in ((got[3], want[1].cpu(), bq), (got[4], want[2].cpu(), bv)):
+        ok, err = _close(gm, ref._mm16(x, b), a=x, b=b)
+        assert ok, err
+
+
+@pytest.mark.parametrize("r", [8, 16])
+@pytest.mark.parametrize("drop", [False, True])
+@pytest.mark.parametrize("n", [1, 37, 707])
+def test_lora_bwd_xw_equals_bwd_x_then_bwd_w(r, drop, n):
+    # The expansion beside the weight gradients in one launch runs the same per-wave and
+    # per-block code as the two separate launches: dx and all four gradients are bit-identical.
+    d, dq_dim, dv_dim = 1536, 1536, 256
+    g, x, aq, av, bq, bv = _inputs(n, d, dq_dim, dv_dim, r, seed=900 + r + n)
+    dq = torch.randn(n, dq_dim, generator=g).half()
+    dv = torch.randn(n, dv_dim, generator=g).half()
+    dx = torch.randn(n, d, generator=g).half().to(DEV)
+    mq = (torch.randn(n, r, generator=g) * 0.5).half().to(DEV)
+    mv = (torch.randn(n, r, generator=g) * 0.5).half().to(DEV)
+    bits = _bits(77, 6, n, d, 0.05, 0.1) if drop else (None, None)
+    ts = [t.t().contiguous().to(DEV) for t in (aq, av, bq, bv)]
+    xd, dqd, dvd = x.to(DEV), dq.to(DEV), dv.to(DEV)
+    dx_a = dx.clone()
+    dmq, dmv = K.lora_bwd_x(dqd, dvd, *ts, dx_a, *bits, 0.05, 0.1)
+    shapes = ((r, d), (dq_dim, r), (r, d), (dv_dim, r))
+    outs_a = [torch.full(sh, 7.0, dtype=torch.float16, device=DEV) for sh in shapes]
+    outs_b = [torch.full(sh, 7.0, dtype=torch.float16, device=DEV) for sh in shapes]
+    K.lora_bwd_w(xd, dqd, dvd, mq, mv, dmq, dmv, *outs_a, *bits, 0.05, 0.1)
+    dx_b = dx.clone()
+    K.lora_bwd_w(xd, dqd, dvd, mq, mv, dmq, dmv, *outs_b, *bits, 0.05, 0.1,
+                 expand=(ts[0], ts[1], dx_b))
+    torch.cuda.synchronize()
+    assert torch.equal(dx_a, dx_b)
+    for a, b in zip(outs_a, outs_b):
+        assert torch.equal(a, b)
