@@ -177,7 +177,8 @@ def lmhead_probe(reps: int = 5) -> None:
 
 def kernel_probe(reps: int = 5) -> None:
     """Fixed launches for hardware-counter runs: a plain 128 MiB device copy (the calibration for
-    the FETCH_SIZE / WRITE_SIZE counters) and one config-5 layer's four-segment NF4 dequant."""
+    the FETCH_SIZE / WRITE_SIZE counters) and one config-5 layer's four-segment NF4 dequant
+    carrying a residual + RMSNorm forward of a 707-token batch, as in the train step."""
     import torch
 
     from rus_amd import model as M
@@ -195,10 +196,16 @@ def kernel_probe(reps: int = 5) -> None:
         dst.copy_(src)
     torch.cuda.synchronize()
     print(f"probe: {reps} copies of {src.numel() * 2} bytes", flush=True)
+    from rus_amd import kernels as K
+
+    x = torch.randn(707, cfg.hidden_size, device=dev).half()
+    res = torch.randn_like(x)
+    lnw = torch.ones(cfg.hidden_size, device=dev)
     for _ in range(reps):
-        ws.dequant_layer(0)
+        *_, pend = K.rms_norm_fwd(x, lnw, 1e-6, residual=res, defer=True)
+        ws.dequant_layer(0, norm=pend)
     torch.cuda.synchronize()
-    print(f"probe: {reps} four-segment dequants of layer 0", flush=True)
+    print(f"probe: {reps} four-segment dequants of layer 0 with a riding norm", flush=True)
 
 
 def measured_traffic(kernel: str):

@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define RUS_ABI_VERSION 7
+#define RUS_ABI_VERSION 8
 
 #define RUS_DTYPE_F16 0
 #define RUS_DTYPE_F32 1
@@ -96,6 +96,41 @@ typedef struct rus_nf4_job {
  */
 int rus_nf4_dequant_multi(const rus_nf4_job* jobs, int32_t n_jobs, const float* code2,
                           int32_t blocksize, int32_t super_blocksize, void* stream);
+
+#define RUS_NORM_FWD 1
+#define RUS_NORM_BWD 2
+
+/*
+ * One RMSNorm (fp16 activations, weight fp16 or fp32) for rus_nf4_dequant_multi_norm:
+ *   RUS_NORM_FWD: as rus_rmsnorm_fwd with x, residual (or NULL), weight, sum_out, y = out, rstd;
+ *   RUS_NORM_BWD: as rus_rmsnorm_bwd with dy = x, h, weight, rstd, dresidual = residual (or
+ *                 NULL), dx = out.
+ */
+typedef struct rus_norm_side {
+  int32_t kind;
+  int32_t w_dtype;
+  int64_t n_rows, n_cols, stride_row;
+  float eps;
+  const void* x;
+  const void* residual;
+  const void* h;
+  const void* weight;
+  float* rstd;
+  void* sum_out;
+  void* out;
+} rus_norm_side;
+
+/*
+ * rus_nf4_dequant_multi and one independent RMSNorm in a single launch (the norm's rows run in
+ * blocks of their own beside the decode): a layer's weight dequant with that layer's input norm
+ * (solution/ops.py:760-766 before 768-771) or with the norm backward of the layer above
+ * (ops.py:994-996, then the next layer's dequant, ops.py:855-860). Same results as the two
+ * separate calls. The norm must satisfy n_cols <= 2048, n_cols and stride_row multiples of 8,
+ * 16-byte aligned rows; otherwise RUS_ERR_UNSUPPORTED (nothing launched).
+ */
+int rus_nf4_dequant_multi_norm(const rus_nf4_job* jobs, int32_t n_jobs, const float* code2,
+                               int32_t blocksize, int32_t super_blocksize,
+                               const rus_norm_side* side, void* stream);
 
 /*
  * Product with an NF4 double-quant weight W [w_rows, w_cols] (one job of up to three row

@@ -11,7 +11,7 @@ import threading
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "librus_amd.so"
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 DTYPE_F16 = 0
 DTYPE_F32 = 1
@@ -35,11 +35,27 @@ class Nf4Job(ctypes.Structure):
     ]
 
 
+class NormSide(ctypes.Structure):
+    """struct rus_norm_side of include/rus_amd.h."""
+
+    _fields_ = [
+        ("kind", ctypes.c_int32), ("w_dtype", ctypes.c_int32), ("n_rows", ctypes.c_int64),
+        ("n_cols", ctypes.c_int64), ("stride_row", ctypes.c_int64), ("eps", ctypes.c_float),
+        ("x", ctypes.c_void_p), ("residual", ctypes.c_void_p), ("h", ctypes.c_void_p),
+        ("weight", ctypes.c_void_p), ("rstd", ctypes.c_void_p), ("sum_out", ctypes.c_void_p),
+        ("out", ctypes.c_void_p),
+    ]
+
+
+NORM_FWD, NORM_BWD = 1, 2
+
 # name -> argtypes, in the order of include/rus_amd.h. Every entry point returns int.
 SIGNATURES: dict[str, list] = {
     "rus_nf4_dequant": [_vp, _vp, _vp, _vp, _f32, _f32, _f32, _i64, _i64, _i64, _i64, _i64, _i64,
                         _i64, _i32, _i32, _vp, _vp],
     "rus_nf4_dequant_multi": [ctypes.POINTER(Nf4Job), _i32, _vp, _i32, _i32, _vp],
+    "rus_nf4_dequant_multi_norm": [ctypes.POINTER(Nf4Job), _i32, _vp, _i32, _i32,
+                                   ctypes.POINTER(NormSide), _vp],
     "rus_nf4_gemm_plan": [_i64, _i64, _i64, _i32, ctypes.POINTER(_i32), ctypes.POINTER(_i64),
                           ctypes.POINTER(_i64)],
     "rus_nf4_gemm": [_vp, _i64, _i64, ctypes.POINTER(Nf4Job), _vp, _i64, _i64, _i32, _i32, _i32,

@@ -14,7 +14,10 @@
 //     roundings, matching an eager mul-then-add (bitsandbytes dequantize_blockwise + offset);
 //   * the super-block (absmax2) index is taken relative to each segment's first block, so fused
 //     segments whose block counts are not multiples of super_blocksize stay correct.
+#include <type_traits>
+
 #include "common.h"
+#include "rmsnorm_rows.h"
 
 namespace rus {
 namespace {
@@ -276,6 +279,65 @@ __global__ __launch_bounds__(kThreads) void nf4_dequant_multi_kernel(Nf4Multi m)
   }
 }
 
+// A layer's dequant with one RMSNorm (forward or backward, fp16 activations) in the same launch:
+// blocks [0, norm_blocks) run the norm, four rows each (one per wave), the rest the segment
+// jobs as nf4_dequant_multi_kernel. The norm's rows do not depend on the weights, so the
+// latency-bound norm blocks run beside the bandwidth-bound decode instead of in a launch of
+// their own. Each block's role is uniform (the decode's barriers involve only its blocks).
+struct NormSide {
+  const f16* x;    // forward: x; backward: dy
+  const f16* res;  // forward: residual; backward: dresidual (either may be null)
+  const f16* h;    // backward: the norm input
+  const void* w;
+  float* rstd;     // forward: written; backward: read
+  f16* sum_out;    // forward with residual
+  f16* out;        // forward: y; backward: dx
+  int n_rows, n_cols;
+  int64_t stride;
+  float eps;
+  uint32_t blocks;
+};
+
+template <int UNROLL, bool BWD, typename W, int NIT>
+__global__ __launch_bounds__(kThreads) void nf4_dequant_norm_kernel(Nf4Multi m, NormSide s) {
+  __shared__ float s_code2[256];
+  __shared__ float s_nf4[16];
+  __shared__ float s_scale[kTabMaxBlocks + 1];
+  __shared__ float s_tab[(kTabMaxBlocks + 1) * 16];
+  if (blockIdx.x < s.blocks) {
+    const int row = blockIdx.x * (kThreads / kWave) + threadIdx.x / kWave;
+    const W* w = static_cast<const W*>(s.w);
+    if constexpr (BWD) {
+      if (s.res)
+        rmsnorm_bwd_row<f16, W, NIT, true>(s.x, s.h, w, s.rstd, s.res, s.out, row, s.n_rows,
+                                           s.n_cols, s.stride);
+      else
+        rmsnorm_bwd_row<f16, W, NIT, false>(s.x, s.h, w, s.rstd, s.res, s.out, row, s.n_rows,
+                                            s.n_cols, s.stride);
+    } else {
+      if (s.res)
+        rmsnorm_fwd_row<f16, W, NIT, true>(s.x, s.res, w, s.sum_out, s.out, s.rstd, row,
+                                           s.n_rows, s.n_cols, s.stride, s.eps);
+      else
+        rmsnorm_fwd_row<f16, W, NIT, false>(s.x, s.res, w, s.sum_out, s.out, s.rstd, row,
+                                            s.n_rows, s.n_cols, s.stride, s.eps);
+    }
+    return;
+  }
+  const uint32_t b = blockIdx.x - s.blocks;
+  int j = 0;
+#pragma unroll
+  for (int k = 1; k < kMaxJobs; ++k) j += (k < m.n_jobs && b >= m.start[k]) ? 1 : 0;
+  if (m.job[j].wide) {
+    dequant_block_tab<UNROLL>(m.job[j], b - m.start[j], m.start[j + 1] - m.start[j], s_code2,
+                              s_nf4, s_scale, s_tab);
+  } else {
+    load_tables(m.job[0].code2, s_code2, s_nf4);
+    dequant_block<UNROLL>(m.job[j], b - m.start[j], m.start[j + 1] - m.start[j], s_code2,
+                          s_nf4);
+  }
+}
+
 bool is_pow2(int64_t v) { return v > 0 && (v & (v - 1)) == 0; }
 
 int ilog2(int64_t v) {
@@ -410,5 +472,87 @@ extern "C" int rus_nf4_dequant_multi(const rus_nf4_job* jobs, int32_t n_jobs, co
   for (int j = n_jobs; j <= kMaxJobs; ++j) m.start[j] = total;
   hipLaunchKernelGGL(nf4_dequant_multi_kernel<kUnrollMain>, dim3(total), dim3(kThreads), 0,
                      static_cast<hipStream_t>(stream), m);
+  return check_launch(fn);
+}
+
+extern "C" int rus_nf4_dequant_multi_norm(const rus_nf4_job* jobs, int32_t n_jobs,
+                                          const float* code2, int32_t blocksize,
+                                          int32_t super_blocksize, const rus_norm_side* side,
+                                          void* stream) {
+  using namespace rus;
+  const char* fn = "rus_nf4_dequant_multi_norm";
+  if (n_jobs <= 0 || n_jobs > kMaxJobs || !jobs || !side)
+    return fail(RUS_ERR_INVALID, "%s: n_jobs=%d outside [1, %d] or no norm", fn, n_jobs,
+                kMaxJobs);
+  const rus_norm_side& q = *side;
+  const bool bwd = q.kind == RUS_NORM_BWD;
+  if (q.kind != RUS_NORM_FWD && !bwd) return fail(RUS_ERR_INVALID, "%s: kind %d", fn, q.kind);
+  if (q.w_dtype != RUS_DTYPE_F16 && q.w_dtype != RUS_DTYPE_F32)
+    return fail(RUS_ERR_INVALID, "%s: w_dtype %d", fn, q.w_dtype);
+  if (q.n_rows <= 0 || q.n_rows >= (int64_t(1) << 31) || q.n_cols <= 0 || q.stride_row < q.n_cols)
+    return fail(RUS_ERR_INVALID, "%s: bad norm shape", fn);
+  if (!q.x || !q.weight || !q.rstd || !q.out || (bwd && !q.h) || (!bwd && q.residual && !q.sum_out))
+    return fail(RUS_ERR_INVALID, "%s: null norm operand", fn);
+  const int nit = q.n_cols <= 512 ? 1 : q.n_cols <= 1024 ? 2 : q.n_cols <= 1536 ? 3
+                  : q.n_cols <= 2048 ? 4 : 0;
+  if (nit == 0 || q.n_cols % 8 || q.stride_row % 8 || !aligned(q.x, 16) || !aligned(q.out, 16) ||
+      !aligned(q.weight, 16) || (q.residual && !aligned(q.residual, 16)) ||
+      (q.h && !aligned(q.h, 16)) || (q.sum_out && !aligned(q.sum_out, 16)))
+    return fail(RUS_ERR_UNSUPPORTED,
+                "%s: the norm needs n_cols <= 2048, n_cols and stride multiples of 8 and "
+                "16-byte aligned rows", fn);
+  Nf4Multi m{};
+  m.n_jobs = n_jobs;
+  uint32_t total = 0;
+  for (int j = 0; j < n_jobs; ++j) {
+    const rus_nf4_job& jb = jobs[j];
+    if (int e = make_job(fn, jb.packed, jb.absmax, code2, jb.absmax2, jb.off0, jb.off1, jb.off2,
+                         jb.split_byte_1, jb.split_byte_2, jb.absmax2_base_1, jb.absmax2_base_2,
+                         jb.n_bytes, jb.n_absmax, jb.n_absmax2, blocksize, super_blocksize,
+                         jb.out_u32, m.job[j]))
+      return e;
+    m.start[j] = total;
+    total += blocks_for(m.job[j]);
+  }
+  for (int j = n_jobs; j <= kMaxJobs; ++j) m.start[j] = total;
+  NormSide ns{static_cast<const f16*>(q.x),
+              static_cast<const f16*>(q.residual),
+              static_cast<const f16*>(q.h),
+              q.weight,
+              q.rstd,
+              static_cast<f16*>(q.sum_out),
+              static_cast<f16*>(q.out),
+              static_cast<int>(q.n_rows),
+              static_cast<int>(q.n_cols),
+              q.stride_row,
+              q.eps,
+              static_cast<uint32_t>((q.n_rows + kThreads / kWave - 1) / (kThreads / kWave))};
+  const dim3 grid(total + ns.blocks);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  auto launch = [&](auto bwd_c, auto wtag, auto nit_c) {
+    constexpr bool B = decltype(bwd_c)::value;
+    constexpr int N = decltype(nit_c)::value;
+    using WT = decltype(wtag);
+    hipLaunchKernelGGL((nf4_dequant_norm_kernel<kUnrollMain, B, WT, N>), grid, dim3(kThreads), 0,
+                       st, m, ns);
+  };
+  auto by_nit = [&](auto bwd_c, auto wtag) {
+    switch (nit) {
+      case 1: launch(bwd_c, wtag, std::integral_constant<int, 1>{}); break;
+      case 2: launch(bwd_c, wtag, std::integral_constant<int, 2>{}); break;
+      case 3: launch(bwd_c, wtag, std::integral_constant<int, 3>{}); break;
+      default: launch(bwd_c, wtag, std::integral_constant<int, 4>{}); break;
+    }
+  };
+  auto by_w = [&](auto bwd_c) {
+    if (q.w_dtype == RUS_DTYPE_F16)
+      by_nit(bwd_c, f16{});
+    else
+      by_nit(bwd_c, float{});
+  };
+  if (bwd)
+    by_w(std::true_type{});
+  else
+    by_w(std::false_type{});
   return check_launch(fn);
 }

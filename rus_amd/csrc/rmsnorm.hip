@@ -15,28 +15,10 @@
 #include <type_traits>
 
 #include "common.h"
+#include "rmsnorm_rows.h"
 
 namespace rus {
 namespace {
-
-// Loads a pack of N weights as 16-byte chunks (fp32 weights for 8 fp16 activations: two 16-byte
-// loads) or as one narrower access (fp16 weights for 4 fp32 activations: one 8-byte load).
-template <typename T, int N>
-__device__ __forceinline__ void load16(const T* __restrict__ p, float (&out)[N]) {
-  constexpr int per = 16 / sizeof(T);
-  if constexpr (N >= per) {
-    static_assert(N % per == 0, "pack must be whole 16-byte chunks");
-#pragma unroll
-    for (int k = 0; k < N / per; ++k) {
-      float tmp[per];
-      load_f32<T, per>(p + k * per, tmp);
-#pragma unroll
-      for (int i = 0; i < per; ++i) out[k * per + i] = tmp[i];
-    }
-  } else {
-    load_f32<T, N>(p, out);
-  }
-}
 
 template <typename T, typename W, int NIT, bool HAS_RES>
 __global__ __launch_bounds__(256) void rmsnorm_fwd_vec(const T* __restrict__ x,
@@ -45,44 +27,9 @@ __global__ __launch_bounds__(256) void rmsnorm_fwd_vec(const T* __restrict__ x,
                                                       T* __restrict__ sum_out, T* __restrict__ y,
                                                       float* __restrict__ rstd, int n_rows,
                                                       int n_cols, int64_t stride, float eps) {
-  constexpr int V = 16 / sizeof(T);
-  const int lane = threadIdx.x & (kWave - 1);
-  const int row = blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave;
-  if (row >= n_rows) return;
-  const int64_t off = static_cast<int64_t>(row) * stride;
-
-  float h[NIT][V];
-  float ss = 0.0f;
-#pragma unroll
-  for (int it = 0; it < NIT; ++it) {
-    const int c = (it * kWave + lane) * V;
-    if (c < n_cols) {
-      load_f32<T, V>(x + off + c, h[it]);
-      if (HAS_RES) {
-        float r[V];
-        load_f32<T, V>(res + off + c, r);
-#pragma unroll
-        for (int i = 0; i < V; ++i) h[it][i] = round_to<T>(h[it][i] + r[i]);
-        store_from_f32<T, V>(sum_out + off + c, h[it]);
-      }
-#pragma unroll
-      for (int i = 0; i < V; ++i) ss += h[it][i] * h[it][i];
-    }
-  }
-  ss = wave_sum(ss);
-  const float r = 1.0f / sqrtf(ss / static_cast<float>(n_cols) + eps);
-  if (lane == 0) rstd[row] = r;
-#pragma unroll
-  for (int it = 0; it < NIT; ++it) {
-    const int c = (it * kWave + lane) * V;
-    if (c < n_cols) {
-      float wv[V], o[V];
-      load16<W, V>(w + c, wv);
-#pragma unroll
-      for (int i = 0; i < V; ++i) o[i] = round_to<T>(h[it][i] * r) * wv[i];
-      store_from_f32<T, V>(y + off + c, o);
-    }
-  }
+  rmsnorm_fwd_row<T, W, NIT, HAS_RES>(x, res, w, sum_out, y, rstd,
+                                      blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave,
+                                      n_rows, n_cols, stride, eps);
 }
 
 // Scalar two-pass fallback for any width.
@@ -124,48 +71,9 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_vec(const T* __restrict__ dy,
                                                       const T* __restrict__ dres,
                                                       T* __restrict__ dx, int n_rows, int n_cols,
                                                       int64_t stride) {
-  constexpr int V = 16 / sizeof(T);
-  const int lane = threadIdx.x & (kWave - 1);
-  const int row = blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave;
-  if (row >= n_rows) return;
-  const int64_t off = static_cast<int64_t>(row) * stride;
-  const float r = rstd[row];
-
-  float xh[NIT][V], g[NIT][V];
-  float acc = 0.0f;
-#pragma unroll
-  for (int it = 0; it < NIT; ++it) {
-    const int c = (it * kWave + lane) * V;
-    if (c < n_cols) {
-      float dv[V], wv[V];
-      load_f32<T, V>(h + off + c, xh[it]);
-      load_f32<T, V>(dy + off + c, dv);
-      load16<W, V>(w + c, wv);
-#pragma unroll
-      for (int i = 0; i < V; ++i) {
-        xh[it][i] = xh[it][i] * r;
-        g[it][i] = wv[i] * dv[i];
-        acc += xh[it][i] * g[it][i];
-      }
-    }
-  }
-  const float cm = wave_sum(acc) / static_cast<float>(n_cols);
-#pragma unroll
-  for (int it = 0; it < NIT; ++it) {
-    const int c = (it * kWave + lane) * V;
-    if (c < n_cols) {
-      float o[V];
-#pragma unroll
-      for (int i = 0; i < V; ++i) o[i] = (g[it][i] - xh[it][i] * cm) * r;
-      if (HAS_DRES) {
-        float d[V];
-        load_f32<T, V>(dres + off + c, d);
-#pragma unroll
-        for (int i = 0; i < V; ++i) o[i] = o[i] + d[i];
-      }
-      store_from_f32<T, V>(dx + off + c, o);
-    }
-  }
+  rmsnorm_bwd_row<T, W, NIT, HAS_DRES>(dy, h, w, rstd, dres, dx,
+                                       blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave,
+                                       n_rows, n_cols, stride);
 }
 
 // rmsnorm_bwd_vec whose dy is the fp16 rounding of the sum of n_parts fp32 partial products

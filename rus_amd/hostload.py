@@ -281,9 +281,10 @@ class WeightStream:
             blocksize=seg.blocksize, super_blocksize=seg.super_blocksize,
             absmax2_bases=seg.absmax2_bases)
 
-    def dequant_layer(self, layer_idx: int, workspaces=None) -> dict[str, torch.Tensor]:
+    def dequant_layer(self, layer_idx: int, workspaces=None, norm=None) -> dict[str, torch.Tensor]:
         """All four segments of a layer in one dequant launch: {"qkv", "o", "gu", "down"} ->
-        fp16 weights (views of the per-segment workspaces, or of ``workspaces``)."""
+        fp16 weights (views of the per-segment workspaces, or of ``workspaces``). ``norm``: a
+        deferred RMSNorm (``K.DeferredNorm``) that runs in the same launch."""
         packed, absmax, absmax2 = self._arrays(layer_idx)
         segs = self.layer_segments[layer_idx]
         first = segs[SEGMENTS[0]]
@@ -293,7 +294,8 @@ class WeightStream:
                  "out_shape": (sg.out_features, sg.in_features), "out_buf": wsp[name],
                  "split_bytes": sg.split_bytes, "absmax2_bases": sg.absmax2_bases}
                 for name, sg in ((n, segs[n]) for n in SEGMENTS)]
-        outs = K.dequant_nf4_segments(jobs, self.code2_gpu, first.blocksize, first.super_blocksize)
+        outs = K.dequant_nf4_segments(jobs, self.code2_gpu, first.blocksize, first.super_blocksize,
+                                      norm=norm)
         return dict(zip(SEGMENTS, outs))
 
     def nf4_layer(self, layer_idx: int) -> dict[str, "K.NF4Operand"]:

@@ -26,6 +26,7 @@ __all__ = [
     "nf4_absmax2_bases",
     "rms_norm_fwd",
     "rms_norm_bwd",
+    "DeferredNorm",
     "rms_norm_bwd_parts",
     "qkv_rope_fwd",
     "qkv_rope_bwd",
@@ -225,12 +226,15 @@ def dequant_nf4_tensor(
 
 
 def dequant_nf4_segments(segments: list[dict], code2: torch.Tensor, blocksize: int = 64,
-                         super_blocksize: int = 256) -> list[torch.Tensor]:
+                         super_blocksize: int = 256,
+                         norm: DeferredNorm | None = None) -> list[torch.Tensor]:
     """Dequantise 1..4 NF4 segments in one launch (one layer's [q|k|v], o, [gate|up], down).
 
     Each entry: packed, absmax, absmax2 (device tensors), offset (float or 3-tuple), out_shape,
     out_buf (fp16, optional), split_bytes and absmax2_bases (optional), as for
-    ``dequant_nf4_tensor``. Returns the fp16 weights in order."""
+    ``dequant_nf4_tensor``. ``norm``: a deferred RMSNorm run inside the same launch (or just
+    before it, when its shape does not fit the combined kernel). Returns the fp16 weights in
+    order."""
     fn = "dequant_nf4_segments"
     if not 1 <= len(segments) <= 4:
         raise ValueError(f"{fn}: 1..4 segments")
@@ -276,6 +280,14 @@ def dequant_nf4_segments(segments: list[dict], code2: torch.Tensor, blocksize: i
         jb.out_u32 = out.data_ptr()
         outs.append(out)
         total_bytes += nb + absmax.numel() + 4 * absmax2.numel() + 2 * n_el
+    if norm is not None and not norm.done and norm.side is not None:
+        _launch("nf4_dequant", total_bytes + norm.nbytes, 0, "rus_nf4_dequant_multi_norm", jobs,
+                len(segments), code2.data_ptr(), int(blocksize), int(super_blocksize),
+                ctypes.byref(norm.side), _stream(code2))
+        norm.done = True
+        return outs
+    if norm is not None:
+        norm.run()
     _launch("nf4_dequant", total_bytes, 0, "rus_nf4_dequant_multi", jobs, len(segments),
             code2.data_ptr(), int(blocksize), int(super_blocksize), _stream(code2))
     return outs
@@ -402,13 +414,49 @@ def _counter_buffer(cache: dict, dev: torch.device, need: int) -> torch.Tensor:
 # ---------------------------------------------------------------------------------------------
 
 
+class DeferredNorm:
+    """An RMSNorm launch held back (``rms_norm_fwd`` / ``rms_norm_bwd`` with ``defer=True``): its
+    outputs exist, its kernel runs either inside the next layer dequant launch
+    (``dequant_nf4_segments(..., norm=...)``, when ``side`` is set) or alone (``run``). Nothing
+    may read the outputs before one of the two has been enqueued. Holds its operands alive."""
+
+    __slots__ = ("kernel", "nbytes", "fn", "args", "side", "keep", "done")
+
+    def __init__(self, kernel, nbytes, fn, args, side, keep):
+        self.kernel, self.nbytes, self.fn, self.args = kernel, nbytes, fn, args
+        self.side, self.keep, self.done = side, keep, False
+
+    def run(self) -> None:
+        """Launches the norm on its own (no-op once it has been enqueued)."""
+        if not self.done:
+            _launch(self.kernel, self.nbytes, 0, self.fn, *self.args)
+            self.done = True
+
+
+def _norm_side(kind, n_rows, n_cols, stride, eps, wdt, x, res, h, w, rstd, sum_out, out):
+    """The rus_norm_side of a norm the dequant launch can carry (None when it cannot: fp16
+    rows of at most 2048 columns, widths and strides multiples of 8, 16-byte aligned)."""
+    ptrs = [t for t in (x, res, h, w, sum_out, out) if t is not None]
+    if n_rows == 0 or n_cols > 2048 or n_cols % 8 or stride % 8 or \
+            any(t.data_ptr() % 16 for t in ptrs) or x.dtype != torch.float16:
+        return None
+    sd = _lib.NormSide()
+    sd.kind, sd.w_dtype = kind, wdt
+    sd.n_rows, sd.n_cols, sd.stride_row, sd.eps = n_rows, n_cols, stride, float(eps)
+    sd.x, sd.residual, sd.h, sd.weight = (_ptr(t) for t in (x, res, h, w))
+    sd.rstd, sd.sum_out, sd.out = _ptr(rstd), _ptr(sum_out), _ptr(out)
+    return sd
+
+
 def rms_norm_fwd(
     x: torch.Tensor,
     weight: torch.Tensor,
     eps: float = 1e-6,
     residual: torch.Tensor | None = None,
-) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
-    """Fused residual add + RMSNorm forward. Returns (norm_out, sum_out_or_x, rstd)."""
+    defer: bool = False,
+):
+    """Fused residual add + RMSNorm forward. Returns (norm_out, sum_out_or_x, rstd), plus a
+    ``DeferredNorm`` (not yet launched) when ``defer``."""
     fn = "rms_norm_fwd"
     _require_device(fn, x, weight, residual)
     dt = _dtype_code(fn, x.dtype)
@@ -427,16 +475,20 @@ def rms_norm_fwd(
             raise ValueError(f"{fn}: residual must match x in shape and dtype")
         res_2d = residual.contiguous().view(-1, n_cols)
         sum_out = torch.empty_like(x_2d)
-        _launch("rmsnorm_fwd", 4 * n_rows * n_cols * x_2d.element_size() + w.numel() * w.element_size()
-                + 4 * n_rows, 0, "rus_rmsnorm_fwd", x_2d.data_ptr(), res_2d.data_ptr(), w.data_ptr(), wdt,
-                  sum_out.data_ptr(), norm_out.data_ptr(), rstd.data_ptr(), n_rows, n_cols,
-                  x_2d.stride(0), float(eps), dt, _stream(x))
-        return norm_out.view(orig_shape), sum_out.view(orig_shape), rstd
-    _launch("rmsnorm_fwd", 2 * n_rows * n_cols * x_2d.element_size() + w.numel() * w.element_size()
-            + 4 * n_rows, 0, "rus_rmsnorm_fwd", x_2d.data_ptr(), None, w.data_ptr(), wdt, None,
-              norm_out.data_ptr(), rstd.data_ptr(), n_rows, n_cols, x_2d.stride(0), float(eps), dt,
-              _stream(x))
-    return norm_out.view(orig_shape), x, rstd
+    else:
+        res_2d = sum_out = None
+    nbytes = (4 if res_2d is not None else 2) * n_rows * n_cols * x_2d.element_size() + \
+        w.numel() * w.element_size() + 4 * n_rows
+    args = (x_2d.data_ptr(), _ptr(res_2d), w.data_ptr(), wdt, _ptr(sum_out), norm_out.data_ptr(),
+            rstd.data_ptr(), n_rows, n_cols, x_2d.stride(0), float(eps), dt, _stream(x))
+    outs = (norm_out.view(orig_shape), x if sum_out is None else sum_out.view(orig_shape), rstd)
+    if defer:
+        side = _norm_side(_lib.NORM_FWD, n_rows, n_cols, x_2d.stride(0), eps, wdt, x_2d, res_2d,
+                          None, w, rstd, sum_out, norm_out)
+        return outs + (DeferredNorm("rmsnorm_fwd", nbytes, "rus_rmsnorm_fwd", args, side,
+                                    (x_2d, res_2d, w, sum_out, norm_out, rstd)),)
+    _launch("rmsnorm_fwd", nbytes, 0, "rus_rmsnorm_fwd", *args)
+    return outs
 
 
 def rms_norm_bwd(
@@ -445,8 +497,10 @@ def rms_norm_bwd(
     weight: torch.Tensor,
     rstd: torch.Tensor,
     dresidual: torch.Tensor | None = None,
-) -> torch.Tensor:
-    """RMSNorm backward with optional residual-gradient accumulation (no weight gradient)."""
+    defer: bool = False,
+):
+    """RMSNorm backward with optional residual-gradient accumulation (no weight gradient).
+    Returns dx, or (dx, ``DeferredNorm``) when ``defer`` (not yet launched)."""
     fn = "rms_norm_bwd"
     _require_device(fn, dy, h, weight, rstd, dresidual)
     dt = _dtype_code(fn, h.dtype)
@@ -463,17 +517,25 @@ def rms_norm_bwd(
     if rs.dtype != torch.float32 or rs.numel() != n_rows:
         raise ValueError(f"{fn}: rstd must be float32 with {n_rows} entries")
     dx = torch.empty_like(h_2d)
-    dres_ptr = None
+    dres_ptr = dres_2d = None
     if dresidual is not None:
         dres_2d = dresidual.contiguous().view(-1, n_cols)
         if dres_2d.dtype != h_2d.dtype or dres_2d.shape != h_2d.shape:
             raise ValueError(f"{fn}: dresidual must match h in shape and dtype")
         dres_ptr = dres_2d.data_ptr()
-    _launch("rmsnorm_bwd", (4 if dres_ptr is not None else 3) * n_rows * n_cols * h_2d.element_size()
-            + w.numel() * w.element_size() + 4 * n_rows, 0,
-            "rus_rmsnorm_bwd", dy_2d.data_ptr(), h_2d.data_ptr(), w.data_ptr(), wdt,
-              rs.data_ptr(), dres_ptr, dx.data_ptr(), n_rows, n_cols, dy_2d.stride(0), dt,
-              _stream(dy))
+    nbytes = (4 if dres_ptr is not None else 3) * n_rows * n_cols * h_2d.element_size() + \
+        w.numel() * w.element_size() + 4 * n_rows
+    args = (dy_2d.data_ptr(), h_2d.data_ptr(), w.data_ptr(), wdt, rs.data_ptr(), dres_ptr,
+            dx.data_ptr(), n_rows, n_cols, dy_2d.stride(0), dt, _stream(dy))
+    if defer:
+        side = None
+        if dy_2d.stride(0) == h_2d.stride(0) == dx.stride(0) and \
+                (dres_2d is None or dres_2d.stride(0) == dx.stride(0)):
+            side = _norm_side(_lib.NORM_BWD, n_rows, n_cols, dx.stride(0), 0.0, wdt, dy_2d,
+                              dres_2d, h_2d, w, rs, None, dx)
+        return dx.view(orig_shape), DeferredNorm("rmsnorm_bwd", nbytes, "rus_rmsnorm_bwd", args,
+                                                 side, (dy_2d, h_2d, w, rs, dres_2d, dx))
+    _launch("rmsnorm_bwd", nbytes, 0, "rus_rmsnorm_bwd", *args)
     return dx.view(orig_shape)
 
 

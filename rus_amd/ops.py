@@ -602,6 +602,14 @@ def _layer_front(engine, l, norm1, w_qkv, lora16, training, seed, masks, pos_ids
     return q_rot, k_rot, v_out, (mid_q, mid_v, x_q, x_v, bits)
 
 
+def _norm_rides_dequant(engine) -> bool:
+    """Whether a layer's RMSNorm can be deferred into the next dequant launch: the dequant runs
+    on the current stream (not ahead on its own stream, not inside the fused products) and layer
+    inputs stay in HBM (an offloaded input's slot is recycled once the layer releases it)."""
+    return engine.gemm != "fused" and not engine.weight_stream.dequant_ahead and \
+        not engine.input_stream.offload
+
+
 def stack_forward(engine, h_packed, pos_ids, row_lengths, training, lora16, seed, vm=None,
                   save=False):
     """All decoder layers over packed tokens (solution/ops.py:736-830) -> (final_norm, state).
@@ -636,13 +644,16 @@ def stack_forward(engine, h_packed, pos_ids, row_lengths, training, lora16, seed
             ws.prefetch(l + 1)
         if ahead and l + 1 < L:
             ws.issue_dequant(l + 1)  # beside this layer's compute
-        if carry is None:
-            norm1, _, rstd1 = K.rms_norm_fwd(h, engine.ln1_weights[l], eps=eps)
-        else:
-            norm1, h, rstd1 = K.rms_norm_fwd(carry[1], engine.ln1_weights[l], eps=eps,
-                                             residual=carry[0])
-        ins.save(l, h)
+        # The input norm rides in the layer's dequant launch when that launch is on this stream.
         fused_gemm = engine.gemm == "fused"
+        defer = _norm_rides_dequant(engine)
+        if carry is None:
+            norm1, _, rstd1, *pend = K.rms_norm_fwd(h, engine.ln1_weights[l], eps=eps,
+                                                    defer=defer)
+        else:
+            norm1, h, rstd1, *pend = K.rms_norm_fwd(carry[1], engine.ln1_weights[l], eps=eps,
+                                                    residual=carry[0], defer=defer)
+        pend = pend[0] if pend else None
         if fused_gemm:  # NF4 operands: the products decode the packed bytes themselves
             ws.wait_slot(l)
             W = ws.nf4_layer(l)
@@ -650,8 +661,12 @@ def stack_forward(engine, h_packed, pos_ids, row_lengths, training, lora16, seed
             W = ws.take_dequant(l)
         else:
             ws.wait_slot(l)
-            W = ws.dequant_layer(l)  # one launch for [q|k|v], o, [gate|up], down
+            W = ws.dequant_layer(l, norm=pend)  # one launch: [q|k|v], o, [gate|up], down, norm
             ws.release_slot(l)
+        if pend is not None:
+            pend.run()  # no-op when the dequant launch carried it
+        del pend
+        ins.save(l, h)
         q_rot, k_rot, v_out, lora = _layer_front(engine, l, norm1, W["qkv"], lora16, training,
                                                  seed, masks, pos_ids)
         if vm is not None:
@@ -702,8 +717,12 @@ def stack_backward(engine, st: StackState, d_final_norm, grad16) -> torch.Tensor
     q_dim = hq * hd
     gviews = engine.lora_views(grad16)
 
-    dh = K.rms_norm_bwd(d_final_norm.contiguous(), st.h_last, engine.final_norm_weight,
-                        st.final_rstd)
+    # Each norm backward (the final norm's, then every layer's attention norm) is deferred into
+    # the next layer's dequant launch when that launch runs on this stream.
+    defer = _norm_rides_dequant(engine)
+    got = K.rms_norm_bwd(d_final_norm.contiguous(), st.h_last, engine.final_norm_weight,
+                         st.final_rstd, defer=defer)
+    dh, pend = got if defer else (got, None)
     st.lora16t = engine.lora_fp16_t(st.lora16)  # rank-major factors of the fused LoRA backward
     ws.use_buffer(st.buf)
     ahead = ws.dequant_ahead
@@ -726,8 +745,11 @@ def stack_backward(engine, st: StackState, d_final_norm, grad16) -> torch.Tensor
             W = ws.take_dequant(l)
         else:
             ws.wait_slot(l)
-            W = ws.dequant_layer(l)
+            W = ws.dequant_layer(l, norm=pend)
             ws.release_slot(l)  # every read of the packed slot is enqueued
+        if pend is not None:
+            pend.run()  # no-op when the dequant launch carried it
+        pend = None
         w_qkv, w_o, w_gu, w_down = W["qkv"], W["o"], W["gu"], W["down"]
         meta = engine.layer_lora_meta[l]
         qA, qB, vA, vB = st.lora16[4 * l: 4 * l + 4]
@@ -851,9 +873,14 @@ def stack_backward(engine, st: StackState, d_final_norm, grad16) -> torch.Tensor
                 d_norm1.add_(dx_q).add_(dx_v)
             del dx_q, dx_v
         del mid_q, mid_v, x_q, x_v, d_mid_q, d_mid_v, dq_scaled, dv_scaled, norm1
-        dh = K.rms_norm_bwd(d_norm1, h_in, engine.ln1_weights[l], rstd1, dresidual=dh_mid)
+        got = K.rms_norm_bwd(d_norm1, h_in, engine.ln1_weights[l], rstd1, dresidual=dh_mid,
+                             defer=defer)
+        dh, pend = got if defer else (got, None)
+        del got
         ins.release(l)
         del d_norm1, h_in, rstd1, dh_mid
+    if pend is not None:
+        pend.run()
     return dh
 
 

@@ -122,6 +122,23 @@ def test_multi_dequant_validates_every_job():
         _lib.call("rus_nf4_dequant_multi", jobs, 2, 16, 64, 256, None)
 
 
+@pytest.mark.parametrize("field,value,msg", [("kind", 3, "kind"), ("n_cols", 4096, "the norm needs"),
+                                             ("n_cols", 1500, "the norm needs"),
+                                             ("out", None, "null norm operand")])
+def test_dequant_with_norm_validates_the_norm_first(field, value, msg):
+    # The norm side of the combined launch is checked before any job; nothing is launched.
+    jobs = (_lib.Nf4Job * 1)()
+    side = _lib.NormSide()
+    side.kind, side.w_dtype = _lib.NORM_FWD, 1
+    side.n_rows, side.n_cols, side.stride_row, side.eps = 8, 1536, 1536, 1e-6
+    side.x = side.weight = side.rstd = side.out = 16
+    setattr(side, field, value)
+    if field == "n_cols":
+        side.stride_row = value
+    with pytest.raises(RuntimeError, match=msg):
+        _lib.call("rus_nf4_dequant_multi_norm", jobs, 1, 16, 64, 256, side, None)
+
+
 def test_lora_workspace_sizes_follow_the_block_decomposition():
     from rus_amd import kernels as K
 

@@ -114,6 +114,43 @@ def test_nf4_dequant_segments_one_launch_bit_exact():
             assert torch.all(buf[n:] == 7.0)
 
 
+@pytest.mark.parametrize("kind", ["fwd", "fwd_res", "bwd", "bwd_dres"])
+@pytest.mark.parametrize("wdtype", [torch.float16, torch.float32])
+@pytest.mark.parametrize("shape", [(707, 1536), (5, 896), (130, 2048), (33, 512)])
+def test_dequant_with_riding_norm_equals_separate_launches(kind, wdtype, shape):
+    # A deferred RMSNorm carried by the dequant launch writes exactly what its own launch writes,
+    # and the weights are unchanged (bit-exact; the rows and the decode run the same code).
+    g = torch.Generator().manual_seed(shape[0] + len(kind))
+    n, d = shape
+    q = quant.quantize_nf4((torch.randn(384, 256, generator=g) * 0.02).half())
+    job = lambda buf: {"packed": q.packed.to(DEV), "absmax": q.absmax.to(DEV),
+                       "absmax2": q.absmax2.to(DEV), "offset": q.offset, "out_shape": q.shape,
+                       "out_buf": buf}
+    x = torch.randn(shape, generator=g).half().to(DEV)
+    other = torch.randn(shape, generator=g).half().to(DEV)
+    w = (1 + 0.05 * torch.randn(d, generator=g)).to(wdtype).to(DEV)
+    code2 = q.code2.to(DEV)
+    if kind.startswith("fwd"):
+        res = other if kind == "fwd_res" else None
+        want = K.rms_norm_fwd(x, w, 1e-6, residual=res)
+        *got, pend = K.rms_norm_fwd(x, w, 1e-6, residual=res, defer=True)
+    else:
+        _, h, rstd = K.rms_norm_fwd(other, w, 1e-6)
+        dres = torch.randn(shape, generator=g).half().to(DEV) if kind == "bwd_dres" else None
+        want = [K.rms_norm_bwd(x, h, w, rstd, dresidual=dres)]
+        dx, pend = K.rms_norm_bwd(x, h, w, rstd, dresidual=dres, defer=True)
+        got = [dx]
+    assert pend.side is not None and not pend.done
+    w_buf = torch.empty(q.shape[0] * q.shape[1], dtype=torch.float16, device=DEV)
+    (w_out,) = K.dequant_nf4_segments([job(w_buf)], code2, norm=pend)
+    assert pend.done
+    pend.run()  # already enqueued: no second launch
+    torch.cuda.synchronize()
+    for a, b in zip(got, want):
+        assert torch.equal(a, b)
+    assert _bits_equal(w_out, _dequant_ref(q))
+
+
 def test_nf4_dequant_rejects_short_absmax():
     q = quant.quantize_nf4(torch.randn(64, 64).half())
     with pytest.raises(RuntimeError, match="absmax"):
