@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define RUS_ABI_VERSION 8
+#define RUS_ABI_VERSION 9
 
 #define RUS_DTYPE_F16 0
 #define RUS_DTYPE_F32 1
@@ -38,6 +38,15 @@ const char* rus_last_error(void);
 
 /* RUS_ABI_VERSION of the loaded library. */
 int rus_abi_version(void);
+
+/*
+ * Copies n_bytes (a multiple of 16; 16-byte aligned pointers) from page-locked, device-mapped
+ * host memory into device memory with a kernel on `stream` (no copy-engine transfer), so that a
+ * captured step graph can start by reading its batch from a host staging image. Replaces: the
+ * per-step transfer of the packed batch to the device (the reference packs device tensors,
+ * solution/ops.py:1103-1127). RUS_ERR_INVALID when host_src is not pinned and mapped.
+ */
+int rus_copy_from_host(void* dst, const void* host_src, int64_t n_bytes, void* stream);
 
 /*
  * Diagnostic (no counterpart in the reference): node census of a captured hipGraph_t.

@@ -66,3 +66,39 @@ extern "C" int rus_graph_node_counts(void* graph, int64_t* counts, int32_t n_cou
   delete[] nodes;
   return rc;
 }
+
+namespace rus {
+namespace {
+
+// dst[i] = src[i] over 16-byte words, grid-stride; src may be pinned host memory (read over the
+// bus by the kernel).
+__global__ __launch_bounds__(256) void copy16_kernel(const uint4* __restrict__ src,
+                                                     uint4* __restrict__ dst, int64_t n) {
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n;
+       i += static_cast<int64_t>(gridDim.x) * 256)
+    dst[i] = src[i];
+}
+
+}  // namespace
+}  // namespace rus
+
+extern "C" int rus_copy_from_host(void* dst, const void* host_src, int64_t n_bytes,
+                                  void* stream) {
+  using namespace rus;
+  const char* fn = "rus_copy_from_host";
+  if (n_bytes < 0 || n_bytes % 16) return fail(RUS_ERR_INVALID, "%s: n_bytes %% 16 != 0", fn);
+  if (n_bytes == 0) return RUS_OK;
+  if (!dst || !host_src || !aligned(dst, 16) || !aligned(host_src, 16))
+    return fail(RUS_ERR_INVALID, "%s: null or misaligned pointer", fn);
+  // Only page-locked host memory mapped for the device may be read by the kernel.
+  void* dev_src = nullptr;
+  const hipError_t e = hipHostGetDevicePointer(&dev_src, const_cast<void*>(host_src), 0);
+  if (e != hipSuccess || !dev_src)
+    return fail(RUS_ERR_INVALID, "%s: source is not page-locked, device-mapped host memory (%s)",
+                fn, hipGetErrorString(e));
+  const int64_t n = n_bytes / 16;
+  const unsigned blocks = static_cast<unsigned>(n < 256 * 64 ? (n + 255) / 256 : 64);
+  hipLaunchKernelGGL(copy16_kernel, dim3(blocks), dim3(256), 0, static_cast<hipStream_t>(stream),
+                     static_cast<const uint4*>(dev_src), static_cast<uint4*>(dst), n);
+  return check_launch(fn);
+}

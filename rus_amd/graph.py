@@ -13,8 +13,13 @@ nothing to the loss or to any gradient. A graph is keyed by (Np, number of rows,
 rounded up to a power of two); the first batch of a key captures it.
 
 Semantics of ``step``: it overwrites (does not accumulate) each LoRA parameter's ``.grad``, which
-are views of one fp32 buffer; the loss is the reference's sum(nll) / denom; dropout masks change
-every replay (the graph advances the engine's device seed).
+are views of one fp32 buffer (also the ``.grad`` of ``engine.flat_lora_parameter()`` when that
+exists); the loss is the reference's sum(nll) / denom; dropout masks change every replay (the
+graph advances the engine's device seed). The first batch fixes where inputs are packed: host
+(CPU) batches on the host, into the next of a ring of pinned images that one kernel copies into
+the bucket's device image right before the replay (no copy-engine transfer for the step to wait
+on, and the host waits only when the ring wraps onto a copy that has not run); device batches on
+the device.
 """
 
 from __future__ import annotations
@@ -48,36 +53,82 @@ def _pow2_at_least(x: int) -> int:
     return p
 
 
-class _Captured:
-    """Static buffers and the graph of one bucket."""
+HOST_RING = 4  # pinned host images per bucket, used in turn
+
+
+class _Stage:
+    """One device image of a bucket's inputs: ids | positions | labels (int64, n_pad each) |
+    cu_seqlens (int32), and the views a captured graph reads."""
 
     def __init__(self, n_pad: int, n_rows: int, max_len: int, device):
+        cu_words = (n_rows + 2) // 2
+        words = 3 * n_pad + cu_words
+        words += words % 2  # whole 16-byte units for the host-image copy kernel
+        self.buf = torch.zeros(words, dtype=torch.int64, device=device)
+        self.ids = self.buf[:n_pad]
+        self.pos = self.buf[n_pad: 2 * n_pad]
+        self.labels = self.buf[2 * n_pad: 3 * n_pad]
+        self.labels.fill_(-100)
+        self.cu = self.buf[3 * n_pad:].view(torch.int32)[: n_rows + 1]
+        self.vm = VarlenMeta.from_device(self.cu, max_len)
+
+
+class _Captured:
+    """Static buffers and graphs of one bucket: one input image and one graph per whole-model
+    weight buffer (otherwise one of each), and a ring of pinned host images."""
+
+    def __init__(self, n_pad: int, n_rows: int, max_len: int, device, host: bool,
+                 n_images: int):
         self.n_pad, self.n_rows, self.max_len = n_pad, n_rows, max_len
-        self.ids = torch.zeros(n_pad, dtype=torch.int64, device=device)
-        self.pos = torch.zeros(n_pad, dtype=torch.int64, device=device)
-        self.labels = torch.full((n_pad,), -100, dtype=torch.int64, device=device)
-        self.cu = torch.zeros(n_rows + 1, dtype=torch.int32, device=device)
+        self.stages = [_Stage(n_pad, n_rows, max_len, device) for _ in range(n_images)]
         self.cu_host = torch.zeros(n_rows + 1, dtype=torch.int32).pin_memory()
         self.pad_pos = torch.arange(n_pad, dtype=torch.int64, device=device)
-        self.vm = VarlenMeta.from_device(self.cu, max_len)
+        n_words = self.stages[0].buf.numel()
+        self.ring = [torch.zeros(n_words, dtype=torch.int64).pin_memory()
+                     for _ in range(HOST_RING if host else 0)]
+        self.ring_done: list[torch.cuda.Event | None] = [None] * len(self.ring)
+        self.ring_turn = 0
         self.graphs: dict[int, torch.cuda.CUDAGraph] = {}  # per whole-model weight buffer
         self.outputs: dict[int, tuple] = {}  # (loss, nll, entropy, argmax) static tensors
         self.node_counts: dict[int, dict] = {}
 
-    def load(self, pb, lens: list[int]) -> None:
-        n = pb.input_ids.numel()
-        self.ids[:n].copy_(pb.input_ids)
-        self.ids[n:].zero_()
-        self.pos[:n].copy_(pb.pos_ids)
-        self.pos[n:].copy_(self.pad_pos[: self.n_pad - n])
-        self.labels[:n].copy_(pb.shift_labels)
-        self.labels[n:].fill_(-100)
+    def load(self, pb, lens: list[int], j: int) -> None:
+        """Batch -> device image ``j``, enqueued on the current stream: a host batch through the
+        next pinned image of the ring and one copy kernel (waiting on the host only if that
+        image's previous copy has not run yet); a device batch by device copies."""
+        st = self.stages[j]
         cu = [0]
         for L in lens:
             cu.append(cu[-1] + L)
+        n, P = pb.input_ids.numel(), self.n_pad
+        if pb.input_ids.device.type == "cpu":
+            r = self.ring_turn
+            self.ring_turn = (r + 1) % len(self.ring)
+            done = self.ring_done[r]
+            if done is not None and not done.query():
+                done.synchronize()
+            hb = self.ring[r]
+            hb[:n] = pb.input_ids
+            hb[n:P] = 0
+            hb[P: P + n] = pb.pos_ids
+            hb[P + n: 2 * P] = torch.arange(P - n, dtype=torch.int64)
+            hb[2 * P: 2 * P + n] = pb.shift_labels
+            hb[2 * P + n: 3 * P] = -100
+            hb[3 * P:].view(torch.int32)[: len(cu)] = torch.tensor(cu, dtype=torch.int32)
+            K.copy_from_host(st.buf, hb)
+            ev = torch.cuda.Event()
+            ev.record(torch.cuda.current_stream(st.buf.device))
+            self.ring_done[r] = ev
+            return
+        st.ids[:n].copy_(pb.input_ids)
+        st.ids[n:].zero_()
+        st.pos[:n].copy_(pb.pos_ids)
+        st.pos[n:].copy_(self.pad_pos[: P - n])
+        st.labels[:n].copy_(pb.shift_labels)
+        st.labels[n:].fill_(-100)
         # The previous replay's copy from cu_host is complete: pack_varlen synchronised.
         self.cu_host.copy_(torch.tensor(cu, dtype=torch.int32))
-        self.cu.copy_(self.cu_host, non_blocking=True)
+        st.cu.copy_(self.cu_host, non_blocking=True)
 
 
 class GraphedTrainStep:
@@ -105,20 +156,21 @@ class GraphedTrainStep:
         self.grad_views = engine.lora_views(self.grad32)
         self.last = None
         self.census = census  # count each captured graph's node types (node_counts per bucket)
+        self.host_inputs: bool | None = None  # fixed by the first batch: host or device tensors
 
     # -- the captured body -----------------------------------------------------------------------
-    def _body(self, cap: _Captured):
+    def _body(self, img: _Stage):
         eng = self.engine
         seed = eng.dropout_seed
         if self.training:
             seed.add_(1)
-        h = eng.host_head.embed(cap.ids)
+        h = eng.host_head.embed(img.ids)
         lora16 = eng.lora_fp16()
-        final, st = stack_forward(eng, h, cap.pos, None, self.training, lora16, seed, vm=cap.vm,
+        final, st = stack_forward(eng, h, img.pos, None, self.training, lora16, seed, vm=img.vm,
                                   save=not eng.recompute)
         head = eng.host_head
         nll, _lse, ent, amax, _denom, d_final, loss = K.lm_head_ce(
-            final, head.gpu_weight, cap.labels, num_items_in_batch=self.num_items,
+            final, head.gpu_weight, img.labels, num_items_in_batch=self.num_items,
             need_grad=True, weight_t=head.gpu_weight_t, dh_scale=1.0 / PRESCALE_GRAD,
             dh_dtype=final.dtype)
         del final
@@ -132,22 +184,40 @@ class GraphedTrainStep:
         lens = [int(L) for L in pb.row_lengths if L > 0] + [n_pad - n]
         return (n_pad, len(lens), _pow2_at_least(max(max(lens), 16))), lens
 
+    def _images(self) -> tuple[int, ...]:
+        """Input images (and graphs) per bucket: one per whole-model weight buffer, else one."""
+        return tuple(range(self.engine.weight_stream.n_buffers))
+
+    def _pack(self, input_ids, attention_mask, labels):
+        """Packs a batch where this step's inputs live (fixed by the first batch): host tensors
+        are packed on the host, device tensors on the device."""
+        if self.host_inputs is None:
+            self.host_inputs = input_ids.device.type == "cpu"
+        dev = self.engine.device
+        if self.host_inputs:
+            ts = [None if t is None else t.cpu() for t in (input_ids, attention_mask, labels)]
+        else:
+            ts = [None if t is None else t.to(dev) for t in (input_ids, attention_mask, labels)]
+        return pack_varlen(*ts)
+
     def _capture(self, key, pb, lens) -> _Captured:
         cap = self.graphs.get(key)
         if cap is None:
-            cap = _Captured(*key, self.engine.device)
+            cap = _Captured(*key, self.engine.device, bool(self.host_inputs),
+                            len(self._images()))
             self.graphs[key] = cap
-        ws = self.engine.weight_stream
-        for buf in ((0, 1) if ws.unit == "model" else (0,)):
+        for buf in self._images():
             if buf not in cap.graphs:
                 self._capture_one(cap, buf, pb, lens)
         return cap
 
     def _capture_one(self, cap: _Captured, buf: int, pb, lens) -> None:
-        """Warm-up and capture of the step reading whole-model weight buffer ``buf``."""
+        """Warm-up and capture of the step reading input image ``buf`` (and, with whole-model
+        streaming, weight buffer ``buf``)."""
         eng = self.engine
         ws = eng.weight_stream
-        cap.load(pb, lens)
+        img = cap.stages[buf]
+        cap.load(pb, lens, buf)
         if ws.unit == "model":  # the buffer's contents must be valid for the warm-up run
             ws.stage(buf)
             torch.cuda.current_stream(eng.device).wait_event(ws.ready_events[buf])
@@ -159,7 +229,7 @@ class GraphedTrainStep:
         side.wait_stream(torch.cuda.current_stream(eng.device))
         with torch.cuda.stream(side):
             eng.weight_stream.after_replay()
-            self._body(cap)
+            self._body(img)
             eng.weight_stream.after_replay()
         torch.cuda.current_stream(eng.device).wait_stream(side)
         torch.cuda.synchronize(eng.device)
@@ -167,7 +237,7 @@ class GraphedTrainStep:
         g = torch.cuda.CUDAGraph(keep_graph=self.census)
         with torch.cuda.graph(g, pool=self.pool):
             ws.begin_capture()
-            cap.outputs[buf] = self._body(cap)
+            cap.outputs[buf] = self._body(img)
         ws.after_replay()
         ws.end_step(buf)
         if self.census:
@@ -177,17 +247,18 @@ class GraphedTrainStep:
 
     def prepare(self, input_ids, attention_mask=None, labels=None) -> None:
         """Captures the graph for this batch's bucket if it does not exist yet (no step taken)."""
-        pb = pack_varlen(input_ids, attention_mask, labels)
+        pb = self._pack(input_ids, attention_mask, labels)
         key, lens = self._key(pb)
         self._capture(key, pb, lens)
 
     def step(self, input_ids, attention_mask=None, labels=None) -> torch.Tensor:
         self.engine.sync_lora_storage()  # the graphs read the parameters' flat buffer
-        pb = pack_varlen(input_ids, attention_mask, labels)
+        pb = self._pack(input_ids, attention_mask, labels)
         key, lens = self._key(pb)
         cap = self._capture(key, pb, lens)
-        cap.load(pb, lens)
         ws = self.engine.weight_stream
+        j = ws.next_buffer if ws.unit == "model" else 0  # the image paired with the weights
+        cap.load(pb, lens, j)
         buf = ws.begin_step()  # waits for this step's whole-model copy (unit="model")
         cap.graphs[buf].replay()
         ws.after_replay()
@@ -195,6 +266,9 @@ class GraphedTrainStep:
         for p, v in zip(self.engine.lora_params, self.grad_views):
             if p.grad is None or p.grad.data_ptr() != v.data_ptr():
                 p.grad = v
+        flat = self.engine.flat_param
+        if flat is not None and (flat.grad is None or flat.grad.data_ptr() != self.grad32.data_ptr()):
+            flat.grad = self.grad32
         self.last = (cap, buf, pb)
         return cap.outputs[buf][0][0]
 

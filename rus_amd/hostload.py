@@ -63,16 +63,22 @@ class WeightStream:
     ``unit`` (when not resident) sets what is streamed from pinned host memory:
       * "layer": two one-layer device slots refilled per layer per pass (the reference's policy,
         hostload.py:286-323; 2 x 28 layer copies per step);
-      * "model": two whole-model device buffers; each step copies the packed model once (one
-        645 MiB H2D copy at Qwen2.5-1.5B) into the buffer the previous step did not use, on the
-        copy stream, overlapping the previous step. The step waits for its copy, uses that
-        buffer for forward and backward and then releases it (``begin_step`` / ``end_step``).
-        Copies that overlap a reader of the same buffer write identical bytes (the base weights
-        are frozen)."""
+      * "model": ``model_buffers`` (default 2) whole-model device buffers used in turn; each
+        step copies the packed model once (one 645 MiB H2D copy at Qwen2.5-1.5B) into the
+        buffer of the next step, on the copy stream, overlapping the current step; the step
+        waits for its own copy (``begin_step``), uses that buffer for forward and backward and
+        releases it (``end_step``). A copy does not wait for the last reader of its buffer: the
+        base weights are frozen, so it rewrites the bytes that reader sees. (A copy stream
+        holding a wait on a running step delays, on this runtime, the completion of the copies
+        ahead of it, which idles the start of the next step.)"""
 
-    def __init__(self, layers, device, resident: bool = False, unit: str = "layer"):
+    def __init__(self, layers, device, resident: bool = False, unit: str = "layer",
+                 model_buffers: int = 2):
         if unit not in ("layer", "model"):
             raise ValueError("unit must be 'layer' or 'model'")
+        if model_buffers < 2:
+            raise ValueError("model_buffers must be at least 2")
+        self.n_buffers = model_buffers if (unit == "model" and not resident) else 1
         self.device = torch.device(device)
         self.num_layers = len(layers)
         self.resident = resident
@@ -135,7 +141,7 @@ class WeightStream:
 
     def _init_model_buffers(self, packed_l, absmax_l, absmax2_l) -> None:
         """One pinned host blob holding every layer (packed | absmax | absmax2, each 256-byte
-        aligned) and two device blobs of the same layout."""
+        aligned) and n_buffers device blobs of the same layout."""
         def up(x):
             return (x + 255) // 256 * 256
 
@@ -153,7 +159,9 @@ class WeightStream:
             blob[ao: ao + a.numel()] = a
             blob[a2o: a2o + 4 * a2.numel()] = a2.contiguous().view(torch.uint8)
         self.host_blob = _pinned(blob)
-        self.dev_blobs = [torch.empty(cur, dtype=torch.uint8, device=self.device) for _ in range(2)]
+        nb = self.n_buffers
+        self.dev_blobs = [torch.empty(cur, dtype=torch.uint8, device=self.device)
+                          for _ in range(nb)]
         self.blob_views = []
         for b in self.dev_blobs:
             views = []
@@ -162,18 +170,17 @@ class WeightStream:
                               b[a2o: a2o + 4 * a2.numel()].view(torch.float32)))
             self.blob_views.append(views)
         self.stream = torch.cuda.Stream(device=self.device)
-        self.ready_events = [torch.cuda.Event() for _ in range(2)]
-        self.free_events = [torch.cuda.Event() for _ in range(2)]
-        self.staged = [False, False]
+        self.ready_events = [torch.cuda.Event() for _ in range(nb)]
+        self.staged = [False] * nb
         self.active = 0
         self.next_buffer = 0
 
     # -- whole-model streaming (unit="model") --------------------------------------------------
     def stage(self, buf: int) -> None:
-        """Copies the packed model into device buffer ``buf`` on the copy stream, after the last
-        step that used ``buf`` released it."""
+        """Copies the packed model into device buffer ``buf`` on the copy stream. Only a buffer's
+        first copy precedes every read of it; later copies rewrite identical bytes, so they do
+        not wait for the buffer's readers."""
         with torch.cuda.stream(self.stream):
-            self.stream.wait_event(self.free_events[buf])
             self.dev_blobs[buf].copy_(self.host_blob, non_blocking=True)
             self.ready_events[buf].record(self.stream)
         self.staged[buf] = True
@@ -190,7 +197,7 @@ class WeightStream:
         torch.cuda.current_stream(self.device).wait_event(self.ready_events[buf])
         self.staged[buf] = False
         self.active = buf
-        self.next_buffer = 1 - buf
+        self.next_buffer = (buf + 1) % self.n_buffers
         self.stage(self.next_buffer)
         return buf
 
@@ -201,9 +208,9 @@ class WeightStream:
             self.active = buf
 
     def end_step(self, buf: int) -> None:
-        """Releases ``buf`` after the work enqueued so far on the current stream."""
-        if self.unit == "model":
-            self.free_events[buf].record(torch.cuda.current_stream(self.device))
+        """Ends a step's use of ``buf``. Nothing to record: the next copy into ``buf`` rewrites
+        the bytes its readers see, so it does not wait for them."""
+        del buf
 
     # -- streaming protocol (hostload.py:297-323) ------------------------------------------------
     def prefetch(self, layer_idx: int) -> None:

@@ -27,6 +27,7 @@ __all__ = [
     "rms_norm_fwd",
     "rms_norm_bwd",
     "DeferredNorm",
+    "copy_from_host",
     "rms_norm_bwd_parts",
     "qkv_rope_fwd",
     "qkv_rope_bwd",
@@ -412,6 +413,22 @@ def _counter_buffer(cache: dict, dev: torch.device, need: int) -> torch.Tensor:
 # ---------------------------------------------------------------------------------------------
 # Residual + RMSNorm (reference: kernels.py:125-199, launchers kernels.py:622-714)
 # ---------------------------------------------------------------------------------------------
+
+
+def copy_from_host(dst: torch.Tensor, host_src: torch.Tensor) -> None:
+    """dst <- host_src, where host_src is a pinned CPU tensor of the same byte size (a multiple of
+    16): read by a kernel on the current stream (no copy-engine transfer), so a captured graph can
+    take its inputs from a host staging image."""
+    fn = "copy_from_host"
+    _require_device(fn, dst)
+    if host_src.device.type != "cpu" or not host_src.is_pinned():
+        raise ValueError(f"{fn}: the source must be a pinned CPU tensor")
+    nb = dst.numel() * dst.element_size()
+    if not dst.is_contiguous() or not host_src.is_contiguous() or \
+            host_src.numel() * host_src.element_size() != nb:
+        raise ValueError(f"{fn}: contiguous tensors of equal byte size required")
+    _launch("copy_from_host", 2 * nb, 0, "rus_copy_from_host", dst.data_ptr(),
+            host_src.data_ptr(), nb, _stream(dst))
 
 
 class DeferredNorm:

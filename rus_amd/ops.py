@@ -349,6 +349,21 @@ class Qwen2FusedEngine:
         self._lora_flat = flat
         self._lora_ptrs = [p.data_ptr() for p in params]
 
+    @property
+    def flat_param(self):
+        """The Parameter of ``flat_lora_parameter`` if it has been made, else None."""
+        return getattr(self, "_flat_param", None)
+
+    def flat_lora_parameter(self) -> torch.nn.Parameter:
+        """One fp32 Parameter over the flat buffer that holds every LoRA factor (the LoRA
+        parameters are views of it), so that an optimizer over it updates all factors with one
+        fused launch; elementwise optimizers (AdamW) give the same values as over the separate
+        factors. A captured step sets its ``.grad`` to the step's flat gradient."""
+        if self.flat_param is None:
+            self.sync_lora_storage()
+            self._flat_param = torch.nn.Parameter(self._lora_flat, requires_grad=True)
+        return self._flat_param
+
     def sync_lora_storage(self) -> None:
         """Re-points the LoRA parameters at the flat buffer if any was re-assigned (values kept)."""
         if [p.data_ptr() for p in self.lora_params] != self._lora_ptrs:

@@ -162,7 +162,9 @@ def test_graph_replays_repeatable_across_buckets(unit):
             assert torch.equal(g0, g1), it
     assert len(gs.graphs) == 2
     for cap in gs.graphs.values():
-        assert len(cap.node_counts) == (2 if unit == "model" else 1)  # one graph per buffer
+        # one graph per whole-model weight buffer
+        assert len(cap.node_counts) == engine.weight_stream.n_buffers
+        assert engine.weight_stream.n_buffers == (2 if unit == "model" else 1)
         for c in cap.node_counts.values():
             print("graph nodes", unit, c)
             assert c["memset"] == 0 and c["kernel"] > 50
@@ -204,3 +206,54 @@ def test_graph_saved_activations_match_recompute_bitwise():
             else:
                 for g0, g1 in zip(x, y):
                     assert torch.equal(g0, g1)
+
+
+@pytest.mark.parametrize("resident", [True, False])
+def test_host_packed_batches_match_device_packed_bitwise(resident):
+    # Host (CPU) batches are packed on the host into a pinned image that the graph's first kernel
+    # copies; the replays must give the device-packed steps' loss and gradients bit for bit, also
+    # when the two images alternate and another bucket runs in between (whole-model streaming
+    # pairs each image with a weight buffer; resident weights alternate the images per step).
+    cfg = small_config()
+    model = M.build_random_qlora_qwen2(cfg, DEV, seed=9, std=0.05)
+    engine = ops.Qwen2FusedEngine(model, DEV, resident_weights=resident,
+                                  stream_unit="layer" if resident else "model")
+    gs_dev = GraphedTrainStep(engine, bucket=64, training=False)
+    gs_host = GraphedTrainStep(engine, bucket=64, training=False)
+    a = _batch(cfg, [37, 64, 21], seed=3)
+    b = _batch(cfg, [100, 9], seed=4)
+    want = {}
+    for name, bt in (("a", a), ("b", b)):
+        want[name] = (float(gs_dev.step(*bt)), _grads(engine))
+    host = {"a": [t.cpu().pin_memory() for t in a], "b": [t.cpu().pin_memory() for t in b]}
+    for name in ("a", "b", "a", "a", "b", "b", "a"):
+        loss = float(gs_host.step(*host[name]))
+        torch.cuda.synchronize()
+        assert loss == want[name][0], name
+        for x, y in zip(_grads(engine), want[name][1]):
+            assert torch.equal(x, y), name
+    assert gs_host.host_inputs and not gs_dev.host_inputs
+
+
+def test_flat_lora_parameter_adamw_equals_per_factor_adamw():
+    # The flat Parameter holds every factor (the LoRA parameters are its views) and receives the
+    # step's flat gradient; AdamW over it gives the per-factor AdamW's values (elementwise).
+    cfg = small_config()
+    model = M.build_random_qlora_qwen2(cfg, DEV, seed=11, std=0.05)
+    engine = ops.Qwen2FusedEngine(model, DEV, resident_weights=True)
+    gs = GraphedTrainStep(engine, bucket=64, training=False)
+    flat = engine.flat_lora_parameter()
+    batch = _batch(cfg, [50, 30], seed=5)
+    start = [p.detach().clone() for p in engine.lora_params]
+    gs.step(*batch)
+    assert flat.grad is not None and flat.grad.data_ptr() == gs.grad32.data_ptr()
+    torch.optim.AdamW(engine.lora_params, lr=1e-2, foreach=False).step()
+    torch.cuda.synchronize()
+    per_factor = [p.detach().clone() for p in engine.lora_params]
+    with torch.no_grad():
+        for p, s in zip(engine.lora_params, start):
+            p.copy_(s)
+    torch.optim.AdamW([flat], lr=1e-2, foreach=False).step()
+    torch.cuda.synchronize()
+    for p, want in zip(engine.lora_params, per_factor):
+        assert torch.equal(p.detach(), want)
