@@ -38,6 +38,7 @@ constexpr int kHD = 128;       // head_dim
 constexpr int kBlk = 32;       // tokens per block
 constexpr int kTS = kBlk + 4;  // transposed-tile row stride (halfs): 72 B, conflict-free reads
 constexpr int kW = 4;          // waves per block (one 32x32 head-dim tile each in the merges)
+constexpr int kMaxGroup = 8;   // query heads per KV head (GQA group) the backward supports
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 constexpr float kLazy = 8.0f;  // lazy-rescale threshold (log2 units)
@@ -557,20 +558,27 @@ __global__ __launch_bounds__(64 * kW) void attn_bwd_dkdv_kernel(AttnArgs a) {
   for (int pass = 0; pass < 2; ++pass) {
     const float* src = pass == 0 ? a.dk_part : a.dv_part;
     f16* out = pass == 0 ? a.dk : a.dv;
-    float acc[16];
+    // Every head's 16 loads are issued together (the partials are read device-coherently, from
+    // beyond this XCD's L2: one latency instead of one per head), then added in head order;
+    // slots past the group re-read its last head and are not added.
+    float v[kMaxGroup][16];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
-    // One head per round: its 16 loads are issued together, then added in head order.
-    for (int j = 0; j < grp; ++j) {
-      const float* hsrc = src + static_cast<int64_t>(g * grp + j) * a.n_tok * kHD + wave * 32 + col;
-      float v[16];
+    for (int j = 0; j < kMaxGroup; ++j) {
+      const int jj = min(j, grp - 1);
+      const float* hsrc = src + static_cast<int64_t>(g * grp + jj) * a.n_tok * kHD + wave * 32 + col;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int key = min(k0 + acc_row(r, h), end - 1);  // rows past the end: read, not stored
-        v[r] = load_partial(hsrc + static_cast<int64_t>(key) * kHD);
+        v[j][r] = load_partial(hsrc + static_cast<int64_t>(key) * kHD);
       }
+    }
+    float acc[16];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) acc[r] += v[r];
+    for (int r = 0; r < 16; ++r) {
+      acc[r] = v[0][r];
+#pragma unroll
+      for (int j = 1; j < kMaxGroup; ++j)
+        if (j < grp) acc[r] += v[j][r];
     }
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
@@ -646,6 +654,9 @@ extern "C" int rus_attn_varlen_bwd(const void* q, const void* k, const void* v, 
       !aligned(dout, 16) || !aligned(dq, 16) || !aligned(dk, 16) || !aligned(dv, 16) ||
       !aligned(workspace, 16) || !counters || !aligned(counters, 4))
     return fail(RUS_ERR_INVALID, "%s: null or misaligned argument", fn);
+  if (h_q / h_kv > kMaxGroup)
+    return fail(RUS_ERR_UNSUPPORTED, "%s: %d query heads per KV head (at most %d)", fn,
+                h_q / h_kv, kMaxGroup);
   if (n_counters < static_cast<int64_t>(max_blocks) * h_kv)
     return fail(RUS_ERR_INVALID, "%s: %lld counters, need max_blocks * h_kv = %lld", fn,
                 static_cast<long long>(n_counters),
