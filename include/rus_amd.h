@@ -507,7 +507,9 @@ int rus_attn_varlen_fwd(const void* q, const void* k, const void* v, const int32
 /*
  * Backward of rus_attn_varlen_fwd: dq like q, dk / dv like k / v (fp16; dk and dv sum the h_q /
  * h_kv query heads of each group in fp32 and are rounded once). out and lse are the forward's.
- * workspace: fp32, at least round_up(h_q * n_tokens, 64) + 2 * h_q * n_tokens * 128 elements.
+ * workspace: fp32, at least round_up(h_q * n_tokens, 64) + 2 * h_q * n_tokens * 128 elements
+ * (the first part is reserved; then per-head dK and dV partials). Both passes (dQ, and dK / dV
+ * with the sum over each group's heads) run as one launch; max_blocks at most 32767.
  * counters: int32, at least max_blocks * h_kv, zero before the first call and left zero (calls
  * sharing them must not run concurrently).
  * Replaces: the autograd backward of solution/ops.py:669-696 (torch SDPA backward plus the

@@ -52,7 +52,6 @@ struct AttnArgs {
   const int32_t* cu;
   f16* out;        // forward: O; backward kernel 1: dQ
   float* lse;      // [h_q, n_tok], natural log
-  float* dsum;     // [h_q, n_tok], D = rowsum(dO o O)
   float* dk_part;  // [h_q, n_tok, 128]
   float* dv_part;
   f16* dk;         // [n_tok, h_kv, 128]
@@ -60,6 +59,7 @@ struct AttnArgs {
   int* counters;   // [max_blocks, h_kv] arrival counters (zero on entry, left zero)
   int64_t n_tok;
   int n_seq, h_q, h_kv;
+  int max_blocks;  // backward: blocks per pass (grid y of each pass)
   float scale, scale_log2;
 };
 
@@ -352,11 +352,11 @@ __global__ __launch_bounds__(64 * kW) void attn_fwd_kernel(AttnArgs a) {
 // Backward 1: D = rowsum(dO o O) and dQ = scale * dS K. Block = (row, query block, head); the
 // kW waves split the key blocks and their dQ partials are summed at the end.
 // ---------------------------------------------------------------------------------------------
-__global__ __launch_bounds__(64 * kW) void attn_bwd_dq_kernel(AttnArgs a) {
-  constexpr int kBytes = kMax(kW * kStageHalfs * 2, kParkBytes);
-  __shared__ __attribute__((aligned(16))) char smem[kBytes];
+constexpr int kBwdBytes = kMax(2 * kW * kStageHalfs * 2, kParkBytes);  // LDS of a backward block
+
+__device__ __forceinline__ void attn_bwd_dq_block(const AttnArgs& a, int blk, char* smem) {
   int start, end, q0;
-  if (!find_block<true>(a.cu, a.n_seq, static_cast<int>(a.n_tok), blockIdx.y, start, end, q0)) return;
+  if (!find_block<true>(a.cu, a.n_seq, static_cast<int>(a.n_tok), blk, start, end, q0)) return;
   const int head = blockIdx.x, g = head / (a.h_q / a.h_kv);
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, h = lane >> 5, col = lane & 31;
   const int64_t sq = static_cast<int64_t>(a.h_q) * kHD, skv = static_cast<int64_t>(a.h_kv) * kHD;
@@ -379,7 +379,6 @@ __global__ __launch_bounds__(64 * kW) void attn_bwd_dq_kernel(AttnArgs a) {
   }
   dsum += __shfl_xor(dsum, 32, 64);
   const float lse2 = a.lse[head * a.n_tok + qr] * kLog2e;
-  if (wave == 0 && qi < end && h == 0) a.dsum[head * a.n_tok + qi] = dsum;
 
   f32x16 dq[4];
 #pragma unroll
@@ -448,11 +447,9 @@ __global__ __launch_bounds__(64 * kW) void attn_bwd_dq_kernel(AttnArgs a) {
 // KV group store fp32 partials; the last of them to finish sums the group in head order and
 // writes dK and dV once (no atomics on data, no separate reduce launch).
 // ---------------------------------------------------------------------------------------------
-__global__ __launch_bounds__(64 * kW) void attn_bwd_dkdv_kernel(AttnArgs a) {
-  constexpr int kBytes = kMax(2 * kW * kStageHalfs * 2, kParkBytes);
-  __shared__ __attribute__((aligned(16))) char smem[kBytes];
+__device__ __forceinline__ void attn_bwd_dkdv_block(const AttnArgs& a, int blk, char* smem) {
   int start, end, k0;
-  if (!find_block<false>(a.cu, a.n_seq, static_cast<int>(a.n_tok), blockIdx.y, start, end, k0)) return;
+  if (!find_block<false>(a.cu, a.n_seq, static_cast<int>(a.n_tok), blk, start, end, k0)) return;
   const int head = blockIdx.x, g = head / (a.h_q / a.h_kv);
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, h = lane >> 5, col = lane & 31;
   const int64_t sq = static_cast<int64_t>(a.h_q) * kHD, skv = static_cast<int64_t>(a.h_kv) * kHD;
@@ -463,7 +460,7 @@ __global__ __launch_bounds__(64 * kW) void attn_bwd_dkdv_kernel(AttnArgs a) {
   f16* qt = reinterpret_cast<f16*>(smem) + 2 * wave * kStageHalfs;
   f16* dt = qt + kStageHalfs;
   const float* lse = a.lse + head * a.n_tok;
-  const float* dsum = a.dsum + head * a.n_tok;
+  const f16* oh = a.o + head * kHD;
 
   const int kj = k0 + col;  // this lane's key (column of S = Q K^T)
   f16x8 kf[8], vf[8];
@@ -476,22 +473,31 @@ __global__ __launch_bounds__(64 * kW) void attn_bwd_dkdv_kernel(AttnArgs a) {
     dv[d] = f32x16{};
   }
   const int nq = (end - k0 + kBlk - 1) / kBlk;  // query blocks from the diagonal to the row end
-  f16x8 qa[8], da[8], qs[8], ds[8];
+  f16x8 qa[8], da[8], qs[8], ds[8], oa[8];
   if (wave < nq) {
     const int q0 = k0 + wave * kBlk, qrow = min(q0 + col, end - 1);
     load_frags(qa, qh, qrow, sq, h);
     load_frags(da, doh, qrow, sq, h);
+    load_frags(oa, oh, qrow, sq, h);
     load_rows4(qs, qh, sq, q0, start, end);
     load_rows4(ds, doh, sq, q0, start, end);
   }
   for (int qb = wave; qb < nq; qb += kW) {
     const int q0 = k0 + qb * kBlk;
+    // D = rowsum(dO o O) of query row q0 + col from this lane's half of the head dims and its
+    // partner's, then the 16 rows of this lane's accumulator registers by lane exchange.
+    float dcol = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) dcol += static_cast<float>(da[k][i]) * static_cast<float>(oa[k][i]);
+    dcol += __shfl_xor(dcol, 32, 64);
     float lq[16], dr[16];  // lse (log2 units) and D of this lane's 16 query rows
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int qi = min(q0 + acc_row(r, h), end - 1);
       lq[r] = lse[qi] * kLog2e;
-      dr[r] = dsum[qi];
+      dr[r] = __shfl(dcol, acc_row(r, h), 64);
     }
     f32x16 st = f32x16{}, dp = f32x16{};
 #pragma unroll
@@ -505,6 +511,7 @@ __global__ __launch_bounds__(64 * kW) void attn_bwd_dkdv_kernel(AttnArgs a) {
       const int q1 = q0 + kW * kBlk, qrow = min(q1 + col, end - 1);
       load_frags(qa, qh, qrow, sq, h);
       load_frags(da, doh, qrow, sq, h);
+      load_frags(oa, oh, qrow, sq, h);
       load_rows4(qs, qh, sq, q1, start, end);
       load_rows4(ds, doh, sq, q1, start, end);
     }
@@ -551,7 +558,7 @@ __global__ __launch_bounds__(64 * kW) void attn_bwd_dkdv_kernel(AttnArgs a) {
     }
   }
   const int grp = a.h_q / a.h_kv;
-  if (!arrive_last(a.counters + static_cast<int64_t>(blockIdx.y) * a.h_kv + g, grp)) return;
+  if (!arrive_last(a.counters + static_cast<int64_t>(blk) * a.h_kv + g, grp)) return;
   // Last head of the group: dk[key, g, :] = fp16(sum over the group's heads in head order).
   // Thread (wave, lane) owns head dims wave*32 + col of its 16 keys, as in the partial stores.
 #pragma unroll
@@ -588,6 +595,16 @@ __global__ __launch_bounds__(64 * kW) void attn_bwd_dkdv_kernel(AttnArgs a) {
             static_cast<f16>(acc[r]);
     }
   }
+}
+
+// Both backward passes in one launch: blocks y < max_blocks are dK/dV blocks (the heavier ones,
+// dispatched first), the rest dQ blocks; each forms D = rowsum(dO o O) for its own query rows.
+__global__ __launch_bounds__(64 * kW) void attn_bwd_kernel(AttnArgs a) {
+  __shared__ __attribute__((aligned(16))) char smem[kBwdBytes];
+  if (static_cast<int>(blockIdx.y) < a.max_blocks)
+    attn_bwd_dkdv_block(a, blockIdx.y, smem);
+  else
+    attn_bwd_dq_block(a, blockIdx.y - a.max_blocks, smem);
 }
 
 int check(const char* fn, const void* q, const void* k, const void* v, const int32_t* cu,
@@ -675,17 +692,17 @@ extern "C" int rus_attn_varlen_bwd(const void* q, const void* k, const void* v, 
   a.h_kv = h_kv;
   a.scale = scale;
   a.scale_log2 = scale * kLog2e;
-  // workspace: dsum [h_q, n_tok] | dk_part [h_q, n_tok, 128] | dv_part [h_q, n_tok, 128]
-  a.dsum = workspace;
+  // workspace: [h_q, n_tok] floats reserved | dk_part [h_q, n_tok, 128] | dv_part (alike)
+  if (2 * static_cast<int64_t>(max_blocks) > 65535)
+    return fail(RUS_ERR_UNSUPPORTED, "%s: max_blocks=%d (at most 32767)", fn, max_blocks);
   a.dk_part = workspace + ((static_cast<int64_t>(h_q) * n_tokens + 63) / 64) * 64;
   a.dv_part = a.dk_part + static_cast<int64_t>(h_q) * n_tokens * kHD;
   hipStream_t st = static_cast<hipStream_t>(stream);
   a.out = static_cast<f16*>(dq);
-  hipLaunchKernelGGL(attn_bwd_dq_kernel, dim3(h_q, max_blocks), dim3(64 * kW), 0, st, a);
-  if (int e = check_launch(fn)) return e;
   a.dk = static_cast<f16*>(dk);
   a.dv = static_cast<f16*>(dv);
   a.counters = counters;
-  hipLaunchKernelGGL(attn_bwd_dkdv_kernel, dim3(h_q, max_blocks), dim3(64 * kW), 0, st, a);
+  a.max_blocks = max_blocks;
+  hipLaunchKernelGGL(attn_bwd_kernel, dim3(h_q, 2 * max_blocks), dim3(64 * kW), 0, st, a);
   return check_launch(fn);
 }
