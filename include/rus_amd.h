@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define RUS_ABI_VERSION 9
+#define RUS_ABI_VERSION 10
 
 #define RUS_DTYPE_F16 0
 #define RUS_DTYPE_F32 1
@@ -435,6 +435,20 @@ int rus_lmhead_ce_fwd(const void* hidden, const void* weight, const int64_t* lab
                       int64_t part_base, int64_t part_stride, float* target, void* stream);
 
 /*
+ * rus_lmhead_ce_fwd plus the logits it rounds: logits[t][v - vocab_start] = z (fp16) for columns up
+ * to round_up(n_vocab, 64) (zeros past n_vocab), ld_z >= that, 16-byte aligned. The buffer is the
+ * one rus_lmhead_ce_grad_from_logits later turns into the logit gradient, so a single-pass head
+ * forms the gradient without a second GEMM.
+ * Replaces: lm_head_piece_kernel MODE 0 (solution/kernels.py:480-516) together with the logit
+ *           recompute GEMM of the gradient pass (solution/ops.py:287-319), whose product it keeps.
+ */
+int rus_lmhead_ce_fwd_keep(const void* hidden, const void* weight, const int64_t* labels,
+                           int64_t n_tok, int64_t d, int64_t ld_h, int64_t ld_w, int64_t n_vocab,
+                           int64_t vocab_start, float* part_m, float* part_s, float* part_w,
+                           int32_t* part_idx, int64_t part_base, int64_t part_stride, float* target,
+                           void* logits, int64_t ld_z, void* stream);
+
+/*
  * Merges n_parts partial rows per token and finishes the statistics.
  * Replaces: solution/kernels.py:534-565 (lm_head_finish_kernel) plus the cross-chunk argmax of
  *           kernels.py:494-498. lse = M + ln S, entropy = lse - W/S, nll = lse - target (0 where the
@@ -465,6 +479,17 @@ int rus_lmhead_ce_grad_logits(const void* hidden, const void* weight, const int6
                               const float* lse, const float* denom, int64_t n_tok, int64_t d,
                               int64_t ld_h, int64_t ld_w, int64_t n_vocab, int64_t vocab_start,
                               void* grad_logits, int64_t ld_g, void* stream);
+
+/*
+ * In place: logits_grad[t][c] = fp16((e^{z - lse[t]} - 1[c = label[t] - vocab_start]) * 2^16 /
+ * max(*denom, 1)) with z = logits_grad[t][c] as written by rus_lmhead_ce_fwd_keep, 0 for labels
+ * -100 and for columns n_vocab .. round_up(n_vocab, 64). Element for element the formula of
+ * rus_lmhead_ce_grad_logits on the same fp16 logits, so both give the same bits.
+ * Replaces: lm_head_piece_kernel MODE 1 (solution/kernels.py:517-531) without its recompute GEMM.
+ */
+int rus_lmhead_ce_grad_from_logits(void* logits_grad, int64_t ld_g, const int64_t* labels,
+                                   const float* lse, const float* denom, int64_t n_tok,
+                                   int64_t n_vocab, int64_t vocab_start, void* stream);
 
 /*
  * Hidden-state gradient partials: parts[s] (+)= grad_logits[:, Ks] . (W^T[:, Ks])^T over split s of

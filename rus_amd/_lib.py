@@ -11,7 +11,7 @@ import threading
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "librus_amd.so"
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 DTYPE_F16 = 0
 DTYPE_F32 = 1
@@ -97,6 +97,9 @@ SIGNATURES: dict[str, list] = {
                        _vp],
     "rus_lmhead_ce_fwd": [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _vp,
                           _i64, _i64, _vp, _vp],
+    "rus_lmhead_ce_fwd_keep": [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _vp,
+                               _vp, _i64, _i64, _vp, _vp, _i64, _vp],
+    "rus_lmhead_ce_grad_from_logits": [_vp, _i64, _vp, _vp, _vp, _i64, _i64, _i64, _vp],
     "rus_lmhead_ce_combine": [_vp, _vp, _vp, _vp, _i64, _i64, _vp, _vp, _i64, _vp, _vp, _vp, _vp,
                               _vp],
     "rus_lmhead_ce_grad_logits": [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64,

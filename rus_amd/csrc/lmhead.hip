@@ -206,6 +206,52 @@ __device__ __forceinline__ float round16(float x) {
 
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Writes the block's 256 (vocab) x 256 (token) tile, held in the accumulator layout, as fp16
+// out[token][vocab - tile base]: value(mt, nt, r, row) is the element of accumulator (mt, nt, r),
+// whose vocab row local to A is row; rows >= g.M are written as 0. Staged through the LDS as
+// [token][vocab] with 8-byte quads XOR-swizzled by row (pairs kept adjacent) so every lane stores
+// 16 contiguous bytes of one token's row: out[tok][tl.m0 + c] for tok < g.N, c < kpad.
+template <class F>
+__device__ __forceinline__ void store_tile_tv(char* smem, const GemmArgs& g, const Tile& tl,
+                                              f16* out, int64_t ld, int kpad, F value) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave >> 1, wn = wave & 1, h = lane >> 5;
+  const int vrow0 = tl.m0 + wm * kWM;
+#pragma unroll
+  for (int nt = 0; nt < kNT; ++nt) {
+    const int trow = wn * kWN + nt * 32 + (lane & 31);  // token row within the block tile
+    char* srow = smem + trow * 512;
+#pragma unroll
+    for (int mt = 0; mt < kMT; ++mt)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        f16x4 v;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int row = vrow0 + mt * 32 + 8 * q + 4 * h + e;
+          v[e] = static_cast<_Float16>(row < g.M ? value(mt, nt, q * 4 + e, row) : 0.0f);
+        }
+        const int col = wm * kWM + mt * 32 + 8 * q + 4 * h;  // vocab column within the tile
+        const int pq = (col >> 2) ^ ((trow & 31) << 1);
+        *reinterpret_cast<f16x4*>(srow + pq * 8) = v;
+      }
+  }
+  __syncthreads();
+  const int t = threadIdx.x;
+  const int c = t & 31;
+#pragma unroll 4
+  for (int it = 0; it < kBN / 8; ++it) {
+    const int trow = it * 8 + (t >> 5);
+    const int tok = tl.n0 + trow;
+    const int col = tl.m0 + c * 8;
+    if (tok < g.N && col < kpad) {
+      const int pq = (2 * c) ^ ((trow & 31) << 1);
+      const uint4 v = *reinterpret_cast<const uint4*>(smem + trow * 512 + pq * 8);
+      *reinterpret_cast<uint4*>(out + static_cast<int64_t>(tok) * ld + col) = v;
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------------------------
 // Forward statistics: A = W rows (vocab), B = H rows (tokens).
 // ---------------------------------------------------------------------------------------------
@@ -220,8 +266,12 @@ struct StatsParams {
   int64_t part_stride;  // entries per partial row (>= n_tok)
   int part_base;        // partial row of A's first 256-row tile
   int vocab_start;      // global vocabulary index of A's row 0
+  f16* z;               // KEEP: the fp16 logits [n_tok][ld_z], columns up to kpad (0 past M)
+  int64_t ld_z;
+  int kpad;
 };
 
+template <bool KEEP>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))) void
 lmhead_stats_kernel(GemmArgs g, StatsParams p) {
   __shared__ __attribute__((aligned(16))) char smem[kSmemBytes];
@@ -243,6 +293,9 @@ lmhead_stats_kernel(GemmArgs g, StatsParams p) {
     for (int nt = 0; nt < kNT; ++nt)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[mt][nt][r] = round16(acc[mt][nt][r]);
+  if constexpr (KEEP)
+    store_tile_tv(smem, g, tl, p.z, p.ld_z, p.kpad,
+                  [&](int mt, int nt, int r, int) { return acc[mt][nt][r]; });
   // Accumulator row of (mt, r) for this lane: mt*32 + 8*(r/4) + 4*h + r%4 (local to vrow0).
   const int rows_left = g.M - vrow0;  // rows at or past this are padding (edge tile only)
 #pragma unroll
@@ -327,6 +380,7 @@ lmhead_stats_kernel(GemmArgs g, StatsParams p) {
   }
 
   // Merge the two vocab halves (wm = 0, 1) of the block through LDS; wm = 0 writes the partial.
+  if constexpr (KEEP) __syncthreads();  // the logits' staging reads of the LDS are done
   float* xm = reinterpret_cast<float*>(smem);  // [wn][nt*32 + lane] x (m, s, w, idx)
   if (wm == 1 && h == 0) {
 #pragma unroll
@@ -390,59 +444,75 @@ lmhead_grad_logits_kernel(GemmArgs g, GradParams p) {
   f32x16 acc[kMT][kNT];
   mainloop(g, tl, smem, acc);
 
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int wm = wave >> 1, wn = wave & 1, h = lane >> 5;
   const float scale_all = kPrescale / fmaxf(*p.denom, 1.0f);
-  const int vrow0 = tl.m0 + wm * kWM;
+  const int lane = threadIdx.x & 63, wn = (threadIdx.x >> 6) & 1;
+  int lab[kNT];
+  float scale[kNT], l2[kNT];
 #pragma unroll
   for (int nt = 0; nt < kNT; ++nt) {
-    const int trow = wn * kWN + nt * 32 + (lane & 31);  // token row within the block tile
-    const int tok = tl.n0 + trow;
-    int lab = -1;
-    float scale = 0.0f, l2 = 0.0f;
+    const int tok = tl.n0 + wn * kWN + nt * 32 + (lane & 31);
+    lab[nt] = -1;
+    scale[nt] = 0.0f;
+    l2[nt] = 0.0f;
     if (tok < g.N) {
       const int64_t lg = p.labels[tok];
       if (lg != -100) {
-        scale = scale_all;
+        scale[nt] = scale_all;
         const int64_t l = lg - p.vocab_start;
-        lab = (l >= 0 && l < g.M) ? static_cast<int>(l) : -1;
+        lab[nt] = (l >= 0 && l < g.M) ? static_cast<int>(l) : -1;
       }
-      l2 = p.lse[tok] * kLog2e;
+      l2[nt] = p.lse[tok] * kLog2e;
     }
-    // Stage as [token][vocab] fp16, 8-byte quads XOR-swizzled by row (pairs kept adjacent).
-    char* srow = smem + trow * 512;
-#pragma unroll
-    for (int mt = 0; mt < kMT; ++mt)
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        f16x4 v;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int r = q * 4 + e;
-          const int row = vrow0 + mt * 32 + 8 * q + 4 * h + e;
-          const float z = round16(acc[mt][nt][r]);
-          const float pr = exp2_fast(__builtin_fmaf(z, kLog2e, -l2));
-          const float gv = (pr - (row == lab ? 1.0f : 0.0f)) * scale;
-          v[e] = static_cast<_Float16>(row < g.M ? gv : 0.0f);
-        }
-        const int col = wm * kWM + mt * 32 + 8 * q + 4 * h;  // vocab column within the tile
-        const int pq = (col >> 2) ^ ((trow & 31) << 1);
-        *reinterpret_cast<f16x4*>(srow + pq * 8) = v;
-      }
   }
-  __syncthreads();
-  const int t = threadIdx.x;
-  const int c = t & 31;
-#pragma unroll 4
-  for (int it = 0; it < kBN / 8; ++it) {
-    const int trow = it * 8 + (t >> 5);
-    const int tok = tl.n0 + trow;
-    const int col = tl.m0 + c * 8;
-    if (tok < g.N && col < p.kpad) {
-      const int pq = (2 * c) ^ ((trow & 31) << 1);
-      const uint4 v = *reinterpret_cast<const uint4*>(smem + trow * 512 + pq * 8);
-      *reinterpret_cast<uint4*>(p.g + static_cast<int64_t>(tok) * p.ld_g + col) = v;
+  store_tile_tv(smem, g, tl, p.g, p.ld_g, p.kpad, [&](int mt, int nt, int r, int row) {
+    const float z = round16(acc[mt][nt][r]);
+    const float pr = exp2_fast(__builtin_fmaf(z, kLog2e, -l2[nt]));
+    return (pr - (row == lab[nt] ? 1.0f : 0.0f)) * scale[nt];
+  });
+}
+
+// ---------------------------------------------------------------------------------------------
+// Logit gradient in place from the logits the statistics pass kept: per element the formula of
+// lmhead_grad_logits_kernel's epilogue on the same fp16 logit, so both give the same bits.
+// Block = (token, kZgCols columns); each thread loads its kZgUnroll 16-byte packs before any math.
+// ---------------------------------------------------------------------------------------------
+
+constexpr int kZgThreads = 256, kZgUnroll = 2, kZgCols = kZgThreads * kZgUnroll * 8;
+
+__global__ __launch_bounds__(kZgThreads) void lmhead_grad_from_logits_kernel(
+    f16* zg, int64_t ld, int n_vocab, int kpad, const int64_t* labels, const float* lse,
+    const float* denom, int vocab_start) {
+  const int tok = blockIdx.x;
+  const int64_t lg = labels[tok];
+  float scale = 0.0f;
+  int lab = -1;
+  if (lg != -100) {
+    scale = kPrescale / fmaxf(*denom, 1.0f);
+    const int64_t l = lg - vocab_start;
+    lab = (l >= 0 && l < n_vocab) ? static_cast<int>(l) : -1;
+  }
+  const float l2 = lse[tok] * kLog2e;
+  f16* row = zg + static_cast<int64_t>(tok) * ld;
+  const int c0 = blockIdx.y * kZgCols + threadIdx.x * 8;
+  f16x8 v[kZgUnroll];
+#pragma unroll
+  for (int u = 0; u < kZgUnroll; ++u) {
+    const int c = c0 + u * kZgThreads * 8;
+    if (c < kpad) v[u] = *reinterpret_cast<const f16x8*>(row + c);
+  }
+#pragma unroll
+  for (int u = 0; u < kZgUnroll; ++u) {
+    const int c = c0 + u * kZgThreads * 8;
+    if (c >= kpad) continue;
+    f16x8 o;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float z = static_cast<float>(v[u][e]);
+      const float pr = exp2_fast(__builtin_fmaf(z, kLog2e, -l2));
+      const float gv = (pr - (c + e == lab ? 1.0f : 0.0f)) * scale;
+      o[e] = static_cast<_Float16>(c + e < n_vocab ? gv : 0.0f);
     }
+    *reinterpret_cast<f16x8*>(row + c) = o;
   }
 }
 
@@ -598,13 +668,11 @@ int check_operand(const char* fn, const void* p, int64_t ld, const char* name) {
 
 using namespace rus;
 
-extern "C" int rus_lmhead_ce_fwd(const void* hidden, const void* weight, const int64_t* labels,
-                                 int64_t n_tok, int64_t d, int64_t ld_h, int64_t ld_w,
-                                 int64_t n_vocab, int64_t vocab_start, float* part_m,
-                                 float* part_s, float* part_w, int32_t* part_idx,
-                                 int64_t part_base, int64_t part_stride, float* target,
-                                 void* stream) {
-  const char* fn = "rus_lmhead_ce_fwd";
+static int lmhead_fwd(const char* fn, const void* hidden, const void* weight,
+                      const int64_t* labels, int64_t n_tok, int64_t d, int64_t ld_h, int64_t ld_w,
+                      int64_t n_vocab, int64_t vocab_start, float* part_m, float* part_s,
+                      float* part_w, int32_t* part_idx, int64_t part_base, int64_t part_stride,
+                      float* target, void* logits, int64_t ld_z, void* stream) {
   if (n_tok < 0 || n_tok >= (1 << 30) || n_vocab < 0 || n_vocab >= (1 << 30) || d <= 0 ||
       d % kBK || vocab_start < 0 || vocab_start + n_vocab >= (int64_t(1) << 31))
     return fail(RUS_ERR_INVALID,
@@ -617,6 +685,12 @@ extern "C" int rus_lmhead_ce_fwd(const void* hidden, const void* weight, const i
   if (!labels || !part_m || !part_s || !part_w || !part_idx || !target || part_base < 0 ||
       part_stride < n_tok)
     return fail(RUS_ERR_INVALID, "%s: null output or bad partial layout", fn);
+  if (logits) {
+    const int64_t kpad = (n_vocab + kBK - 1) / kBK * kBK;
+    if (ld_z < kpad)
+      return fail(RUS_ERR_INVALID, "%s: ld_z must be >= %lld", fn, (long long)kpad);
+    if (int e = check_operand(fn, logits, ld_z, "logits")) return e;
+  }
   GemmArgs g;
   g.A = static_cast<const f16*>(weight);
   g.lda = ld_w;
@@ -629,10 +703,67 @@ extern "C" int rus_lmhead_ce_fwd(const void* hidden, const void* weight, const i
   g.splits = 1;
   g.tiles_m = (g.M + kBM - 1) / kBM;
   g.tiles_n = (g.N + kBN - 1) / kBN;
-  StatsParams p{labels,      part_m,      part_s, part_w, part_idx, target, part_stride,
-                static_cast<int>(part_base), static_cast<int>(vocab_start)};
-  hipLaunchKernelGGL(lmhead_stats_kernel, dim3(launch_grid(g)), dim3(kThreads), 0,
-                     static_cast<hipStream_t>(stream), g, p);
+  StatsParams p{labels,      part_m,      part_s, part_w,  part_idx,
+                target,      part_stride, static_cast<int>(part_base),
+                static_cast<int>(vocab_start), static_cast<f16*>(logits), ld_z,
+                static_cast<int>((n_vocab + kBK - 1) / kBK * kBK)};
+  if (logits)
+    hipLaunchKernelGGL(lmhead_stats_kernel<true>, dim3(launch_grid(g)), dim3(kThreads), 0,
+                       static_cast<hipStream_t>(stream), g, p);
+  else
+    hipLaunchKernelGGL(lmhead_stats_kernel<false>, dim3(launch_grid(g)), dim3(kThreads), 0,
+                       static_cast<hipStream_t>(stream), g, p);
+  return check_launch(fn);
+}
+
+extern "C" int rus_lmhead_ce_fwd(const void* hidden, const void* weight, const int64_t* labels,
+                                 int64_t n_tok, int64_t d, int64_t ld_h, int64_t ld_w,
+                                 int64_t n_vocab, int64_t vocab_start, float* part_m,
+                                 float* part_s, float* part_w, int32_t* part_idx,
+                                 int64_t part_base, int64_t part_stride, float* target,
+                                 void* stream) {
+  return lmhead_fwd("rus_lmhead_ce_fwd", hidden, weight, labels, n_tok, d, ld_h, ld_w, n_vocab,
+                    vocab_start, part_m, part_s, part_w, part_idx, part_base, part_stride, target,
+                    nullptr, 0, stream);
+}
+
+extern "C" int rus_lmhead_ce_fwd_keep(const void* hidden, const void* weight,
+                                      const int64_t* labels, int64_t n_tok, int64_t d,
+                                      int64_t ld_h, int64_t ld_w, int64_t n_vocab,
+                                      int64_t vocab_start, float* part_m, float* part_s,
+                                      float* part_w, int32_t* part_idx, int64_t part_base,
+                                      int64_t part_stride, float* target, void* logits,
+                                      int64_t ld_z, void* stream) {
+  const char* fn = "rus_lmhead_ce_fwd_keep";
+  if (!logits) return fail(RUS_ERR_INVALID, "%s: null logits buffer", fn);
+  return lmhead_fwd(fn, hidden, weight, labels, n_tok, d, ld_h, ld_w, n_vocab, vocab_start,
+                    part_m, part_s, part_w, part_idx, part_base, part_stride, target, logits,
+                    ld_z, stream);
+}
+
+extern "C" int rus_lmhead_ce_grad_from_logits(void* logits_grad, int64_t ld_g,
+                                              const int64_t* labels, const float* lse,
+                                              const float* denom, int64_t n_tok,
+                                              int64_t n_vocab, int64_t vocab_start,
+                                              void* stream) {
+  const char* fn = "rus_lmhead_ce_grad_from_logits";
+  if (n_tok < 0 || n_tok >= (1 << 30) || n_vocab < 0 || n_vocab >= (1 << 30) || vocab_start < 0 ||
+      vocab_start + n_vocab >= (int64_t(1) << 31))
+    return fail(RUS_ERR_INVALID, "%s: bad sizes n_tok=%lld n_vocab=%lld", fn, (long long)n_tok,
+                (long long)n_vocab);
+  if (n_tok == 0 || n_vocab == 0) return RUS_OK;
+  const int64_t kpad = (n_vocab + kBK - 1) / kBK * kBK;
+  if (ld_g < kpad)
+    return fail(RUS_ERR_INVALID, "%s: ld_g must be >= %lld", fn, (long long)kpad);
+  if (int e = check_operand(fn, logits_grad, ld_g, "logits_grad")) return e;
+  if (!labels || !lse || !denom) return fail(RUS_ERR_INVALID, "%s: null pointer argument", fn);
+  const int64_t col_blocks = (kpad + kZgCols - 1) / kZgCols;
+  if (col_blocks > 65535) return fail(RUS_ERR_INVALID, "%s: n_vocab too large", fn);
+  hipLaunchKernelGGL(lmhead_grad_from_logits_kernel,
+                     dim3(static_cast<unsigned>(n_tok), static_cast<unsigned>(col_blocks)),
+                     dim3(kZgThreads), 0, static_cast<hipStream_t>(stream),
+                     static_cast<f16*>(logits_grad), ld_g, static_cast<int>(n_vocab),
+                     static_cast<int>(kpad), labels, lse, denom, static_cast<int>(vocab_start));
   return check_launch(fn);
 }
 

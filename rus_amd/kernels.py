@@ -49,6 +49,7 @@ __all__ = [
     "lm_head_ce_fwd_chunk",
     "lm_head_ce_combine",
     "lm_head_ce_grad_logits",
+    "lm_head_ce_grad_from_logits",
     "lm_head_ce_grad_hidden",
     "lm_head_dh_reduce",
     "lm_head_weight_t",
@@ -1217,11 +1218,14 @@ def _lm_operand(fn: str, t: torch.Tensor, d: int, name: str) -> torch.Tensor:
 
 
 def lm_head_ce_fwd_chunk(hidden: torch.Tensor, weight_rows: torch.Tensor, labels: torch.Tensor,
-                         vocab_start: int, parts: LMHeadPartials, target: torch.Tensor) -> None:
+                         vocab_start: int, parts: LMHeadPartials, target: torch.Tensor,
+                         logits_out: torch.Tensor | None = None) -> None:
     """Forward partial statistics of vocabulary rows [vocab_start, vocab_start + len(weight_rows))
-    (replaces one iteration of the reference's forward chunk loop, ops.py:217-251)."""
+    (replaces one iteration of the reference's forward chunk loop, ops.py:217-251). With
+    ``logits_out`` ([n_tok, >= round_up(n, 64)] fp16) the rounded logits are kept there too, for
+    ``lm_head_ce_grad_from_logits``."""
     fn = "lm_head_ce_fwd_chunk"
-    _require_device(fn, hidden, weight_rows, labels, target)
+    _require_device(fn, hidden, weight_rows, labels, target, logits_out)
     if vocab_start % LM_TILE:
         raise ValueError(f"{fn}: vocab_start must be a multiple of {LM_TILE}")
     d = hidden.shape[1]
@@ -1235,12 +1239,23 @@ def lm_head_ce_fwd_chunk(hidden: torch.Tensor, weight_rows: torch.Tensor, labels
     if lab.dtype != torch.int64 or lab.numel() != n_tok:
         raise ValueError(f"{fn}: labels must be int64 with {n_tok} entries")
     lab = lab.contiguous()
-    _launch("lmhead_ce_fwd", (n_tok + n_vocab) * d * 2 + 16 * n_tok * lm_head_num_parts(n_vocab),
-            2.0 * n_tok * d * n_vocab,
-            "rus_lmhead_ce_fwd", h.data_ptr(), w.data_ptr(), lab.data_ptr(), n_tok, d,
-              h.stride(0), w.stride(0), n_vocab, vocab_start, parts.m.data_ptr(),
-              parts.s.data_ptr(), parts.w.data_ptr(), parts.idx.data_ptr(), part_base, n_tok,
-              target.data_ptr(), _stream(h))
+    nbytes = (n_tok + n_vocab) * d * 2 + 16 * n_tok * lm_head_num_parts(n_vocab)
+    args = (h.data_ptr(), w.data_ptr(), lab.data_ptr(), n_tok, d, h.stride(0), w.stride(0),
+            n_vocab, vocab_start, parts.m.data_ptr(), parts.s.data_ptr(), parts.w.data_ptr(),
+            parts.idx.data_ptr(), part_base, n_tok, target.data_ptr())
+    if logits_out is None:
+        _launch("lmhead_ce_fwd", nbytes, 2.0 * n_tok * d * n_vocab, "rus_lmhead_ce_fwd", *args,
+                _stream(h))
+        return
+    kp = _round_up(n_vocab, LM_K)
+    z = logits_out
+    if z.dtype != torch.float16 or z.dim() != 2 or z.shape[0] != n_tok or z.shape[1] < kp \
+            or z.stride(1) != 1:
+        raise ValueError(f"{fn}: logits_out must be fp16 [{n_tok}, >= {kp}] with contiguous rows")
+    if z.shape[0] * z.stride(0) * 2 >= 1 << 32:
+        raise ValueError(f"{fn}: logits_out exceeds the 4 GiB operand limit of the MFMA kernels")
+    _launch("lmhead_ce_fwd_keep", nbytes + n_tok * kp * 2, 2.0 * n_tok * d * n_vocab,
+            "rus_lmhead_ce_fwd_keep", *args, z.data_ptr(), z.stride(0), _stream(h))
 
 
 def lm_head_ce_combine(parts: LMHeadPartials, target: torch.Tensor, labels: torch.Tensor):
@@ -1284,6 +1299,30 @@ def lm_head_ce_grad_logits(hidden: torch.Tensor, weight_rows: torch.Tensor, labe
               lse.data_ptr(), denom.data_ptr(), n_tok, d, h.stride(0), w.stride(0), n_vocab,
               vocab_start, out.data_ptr(), out.stride(0), _stream(h))
     return out
+
+
+def lm_head_ce_grad_from_logits(logits: torch.Tensor, labels: torch.Tensor, lse: torch.Tensor,
+                                denom: torch.Tensor, n_vocab: int, vocab_start: int = 0) -> torch.Tensor:
+    """Turn the fp16 logits kept by ``lm_head_ce_fwd_chunk(..., logits_out=)`` into the logit
+    gradient in place, element for element the value ``lm_head_ce_grad_logits`` computes
+    (replaces lm_head_piece_kernel MODE 1, kernels.py:517-531, without its recompute GEMM)."""
+    fn = "lm_head_ce_grad_from_logits"
+    _require_device(fn, logits, labels, lse, denom)
+    n_tok = logits.shape[0]
+    kp = _round_up(n_vocab, LM_K)
+    if logits.dtype != torch.float16 or logits.dim() != 2 or logits.shape[1] < kp \
+            or logits.stride(1) != 1:
+        raise ValueError(f"{fn}: logits must be fp16 [n_tok, >= {kp}] with contiguous rows")
+    if denom.dtype != torch.float32 or denom.numel() != 1:
+        raise ValueError(f"{fn}: denom must be a one-element float32 device tensor")
+    lab = labels.reshape(-1)
+    if lab.dtype != torch.int64 or lab.numel() != n_tok or lse.numel() != n_tok:
+        raise ValueError(f"{fn}: labels (int64) and lse need {n_tok} entries")
+    lab = lab.contiguous()
+    _launch("lmhead_ce_grad_from_logits", 2 * n_tok * kp * 2 + 12 * n_tok, 0,
+            "rus_lmhead_ce_grad_from_logits", logits.data_ptr(), logits.stride(0), lab.data_ptr(),
+              lse.data_ptr(), denom.data_ptr(), n_tok, n_vocab, vocab_start, _stream(logits))
+    return logits
 
 
 def lm_head_ce_grad_hidden(grad_logits: torch.Tensor, weight_t_cols: torch.Tensor, n_vocab: int,
@@ -1476,20 +1515,29 @@ def lm_head_ce(hidden: torch.Tensor, weight: torch.Tensor, labels: torch.Tensor,
         raise ValueError(f"{fn}: v_chunk must be a positive multiple of {LM_TILE}")
     parts = LMHeadPartials(lm_head_num_parts(V), n_tok, dev)
     target = torch.zeros(n_tok, dtype=torch.float32, device=dev)
+    # One pass over the whole vocabulary keeps its logits in the gradient buffer, which then
+    # becomes the gradient in place (no second logit GEMM); chunked passes recompute them.
+    keep = need_grad and chunk >= V
+    g = None
+    if need_grad:
+        g = torch.empty((n_tok, _round_up(min(chunk, V), LM_K)), dtype=torch.float16, device=dev)
     for start in range(0, V, chunk):
-        lm_head_ce_fwd_chunk(hidden, weight[start:start + chunk], lab, start, parts, target)
+        lm_head_ce_fwd_chunk(hidden, weight[start:start + chunk], lab, start, parts, target,
+                             logits_out=g if keep else None)
     lse, nll, ent, amax = lm_head_ce_combine(parts, target, lab)
     loss, denom = lm_head_ce_loss(nll, lab, num_items_in_batch)
     dh_pre = None
     if need_grad:
         wt = weight_t if weight_t is not None else lm_head_weight_t(weight)
-        g = torch.empty((n_tok, _round_up(min(chunk, V), LM_K)), dtype=torch.float16, device=dev)
         n_split = lm_head_split_count(n_tok, d, min(chunk, V))
         dparts = torch.empty((n_split, n_tok, d), dtype=torch.float32, device=dev)
         first = True
         for start in range(0, V, chunk):
             end = min(start + chunk, V)
-            lm_head_ce_grad_logits(hidden, weight[start:end], lab, lse, denom, start, g)
+            if keep:
+                lm_head_ce_grad_from_logits(g, lab, lse, denom, V)
+            else:
+                lm_head_ce_grad_logits(hidden, weight[start:end], lab, lse, denom, start, g)
             # A shorter last chunk may use fewer splits; it accumulates into the leading ones.
             ns = lm_head_split_count(n_tok, d, end - start)
             lm_head_ce_grad_hidden(g, wt[:, start:], end - start, dparts[:ns], accumulate=not first)

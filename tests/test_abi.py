@@ -154,3 +154,20 @@ def test_lora_workspace_sizes_follow_the_block_decomposition():
     assert K.lora_workspace_size(K.LORA_BWD_W, 0, 1536, 1536, 256, 8) == (76 * 8 * 64, 76)
     with pytest.raises(RuntimeError, match="unknown entry point"):
         K.lora_workspace_size(7, 1, 64, 64, 64, 16)
+
+
+@pytest.mark.parametrize(
+    "name,args,msg",
+    [
+        # kept logits: null buffer, stride below round_up(n_vocab, 64)
+        ("rus_lmhead_ce_fwd_keep", (16, 16, 16, 4, 64, 64, 64, 100, 0, 16, 16, 16, 16, 0, 4, 16,
+                                    None, 128, None), "null logits"),
+        ("rus_lmhead_ce_fwd_keep", (16, 16, 16, 4, 64, 64, 64, 100, 0, 16, 16, 16, 16, 0, 4, 16,
+                                    16, 120, None), "ld_z"),
+        ("rus_lmhead_ce_grad_from_logits", (16, 120, 16, 16, 16, 4, 100, 0, None), "ld_g"),
+        ("rus_lmhead_ce_grad_from_logits", (16, 128, None, 16, 16, 4, 100, 0, None), "null"),
+    ],
+)
+def test_kept_logit_entry_points_validate_on_the_host(name, args, msg):
+    with pytest.raises(RuntimeError, match=msg):
+        _lib.call(name, *args)

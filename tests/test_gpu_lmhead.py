@@ -140,3 +140,46 @@ def test_lmhead_num_items_in_batch_scales_gradient():
     torch.cuda.synchronize()
     assert float(a[4].item()) == N and float(b[4].item()) == 2 * N
     assert torch.allclose(a[5].cpu() * 0.5, b[5].cpu(), rtol=1e-2, atol=1e-3)
+
+
+@pytest.mark.parametrize("n,d,v,start", [(37, 128, 1031, 0), (300, 256, 4099, 0), (64, 64, 700, 256)])
+def test_kept_logits_gradient_equals_recomputed_gradient(n, d, v, start):
+    # Single-pass head: the statistics pass keeps its fp16 logits in the gradient buffer and the
+    # elementwise pass turns them into the gradient; both must give the bits of the recompute
+    # GEMM's epilogue. Ragged vocabulary (v % 64 != 0), masked labels, labels outside the range.
+    g = torch.Generator().manual_seed(n + v)
+    h = torch.randn(n, d, generator=g).half()
+    w = (torch.randn(start + v, d, generator=g) * 0.05).half()
+    lab = torch.randint(0, start + v, (n,), generator=g)
+    lab[torch.rand(n, generator=g) < 0.2] = -100
+    hd, wd, ld = h.to(DEV), w[start:].to(DEV), lab.to(DEV)
+    kp = (v + 63) // 64 * 64
+    parts = K.LMHeadPartials(start // 256 + K.lm_head_num_parts(v), n, DEV)
+    parts.m.fill_(-float("inf"))
+    parts.s.zero_()
+    parts.w.zero_()
+    parts.idx.fill_(0)
+    tgt_a = torch.zeros(n, dtype=torch.float32, device=DEV)
+    tgt_b = torch.zeros(n, dtype=torch.float32, device=DEV)
+    z = torch.full((n, kp + 64), 7.0, dtype=torch.float16, device=DEV)  # stride > kp
+    K.lm_head_ce_fwd_chunk(hd, wd, ld, start, parts, tgt_a, logits_out=z[:, :kp])
+    m_keep = parts.m.clone()
+    K.lm_head_ce_fwd_chunk(hd, wd, ld, start, parts, tgt_b)
+    torch.cuda.synchronize()
+    assert torch.equal(m_keep, parts.m) and torch.equal(tgt_a, tgt_b)
+    zc = z.cpu()
+    assert torch.all(zc[:, v:kp] == 0) and torch.all(zc[:, kp:] == 7.0)
+    # the kept logits are fp16(H.W^T) of an fp32 accumulation: the two fp32 sums differ by at
+    # most d * 2^-24 * sum|h_i w_i| (summation order), then each rounds to fp16 (an ulp apart at
+    # most, taken at the larger binade)
+    want = (h.float() @ w[start:].float().T).half().float()
+    acc_err = d * 2.0 ** -24 * (h.abs().float() @ w[start:].abs().float().T)
+    assert torch.all((zc[:, :v].float() - want).abs() <= 2 * ref.fp16_ulp(want) + acc_err)
+    lse = torch.randn(n, generator=g).abs().to(DEV) + zc[:, :v].float().amax(1).to(DEV)
+    denom = torch.tensor([float((lab != -100).sum())], dtype=torch.float32, device=DEV)
+    g_ref = torch.empty((n, kp), dtype=torch.float16, device=DEV)
+    K.lm_head_ce_grad_logits(hd, wd, ld, lse, denom, start, g_ref)
+    K.lm_head_ce_grad_from_logits(z[:, :kp], ld, lse, denom, v, start)
+    torch.cuda.synchronize()
+    assert torch.equal(z[:, :kp].cpu(), g_ref.cpu())
+    assert torch.all(z[:, kp:].cpu() == 7.0)
