@@ -276,8 +276,8 @@ def main() -> int:
                          "lm_head CE kernels at config 2")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); the "
-              "multi-GPU design is described in DESIGN.md", file=sys.stderr)
+        print(f"bench.py: this build runs and measures one GPU only (asked for --gpus "
+              f"{args.gpus}); a sharded run over several GPUs is not implemented", file=sys.stderr)
         return 2
     if args.probe == "lmhead":
         lmhead_probe()
