@@ -1182,16 +1182,27 @@ def lm_head_num_parts(vocab_size: int) -> int:
     return (vocab_size + LM_TILE - 1) // LM_TILE
 
 
-def lm_head_split_count(n_tok: int, d: int, n_vocab: int, target_blocks: int = 512) -> int:
-    """Split-K count for the hidden-gradient GEMM: enough (token, hidden) tiles x splits for two
-    workgroups per CU, each split a multiple of 64 vocabulary columns (the C ABI's rule)."""
+def lm_head_split_count(n_tok: int, d: int, n_vocab: int, n_cu: int = 256,
+                        max_split: int = 64) -> int:
+    """Split-K count for the hidden-gradient GEMM. One of its workgroups fills a CU (128 KiB of
+    LDS, 512 registers per lane), so the grid runs in rounds of ``n_cu`` blocks: of the split
+    counts the C ABI accepts (each split a multiple of 64 vocabulary columns) up to ``max_split``,
+    take the one whose (token, hidden) tiles x splits fill their last round best (the share of the
+    CUs used when under one round), the smallest on ties (fewer fp32 partials to write and sum)."""
     kpad = _round_up(n_vocab, LM_K)
     if kpad == 0:
         return 1
     tiles = max(1, -(-n_tok // 256) * -(-d // 256))
-    want = max(1, min(64, -(-target_blocks // tiles), kpad // LM_K))
-    per = _round_up(-(-kpad // want), LM_K)
-    return -(-kpad // per)
+    best, best_key = 1, None
+    for want in range(1, max(1, min(64, max_split, kpad // LM_K)) + 1):
+        per = _round_up(-(-kpad // want), LM_K)
+        n_split = -(-kpad // per)
+        blocks = tiles * n_split
+        fill = blocks / (n_cu * -(-blocks // n_cu))
+        key = (fill, -n_split)
+        if best_key is None or key > best_key:
+            best, best_key = n_split, key
+    return best
 
 
 class LMHeadPartials:
@@ -1539,7 +1550,7 @@ def lm_head_ce(hidden: torch.Tensor, weight: torch.Tensor, labels: torch.Tensor,
             else:
                 lm_head_ce_grad_logits(hidden, weight[start:end], lab, lse, denom, start, g)
             # A shorter last chunk may use fewer splits; it accumulates into the leading ones.
-            ns = lm_head_split_count(n_tok, d, end - start)
+            ns = lm_head_split_count(n_tok, d, end - start, max_split=n_split)
             lm_head_ce_grad_hidden(g, wt[:, start:], end - start, dparts[:ns], accumulate=not first)
             first = False
         dh_pre = lm_head_dh_reduce(dparts, dh_scale, dh_dtype)

@@ -141,7 +141,7 @@ def _lm_head_streamed(h_2d, labels, head: HostHead, num_items_in_batch, need_gra
     dh_pre = None
     if need_grad:
         g = torch.empty((n_tok, K._round_up(vc, K.LM_K)), dtype=torch.float16, device=dev)
-        n_split = K.lm_head_split_count(n_tok, d, vc, target_blocks=256)
+        n_split = K.lm_head_split_count(n_tok, d, vc)
         dparts = torch.zeros((n_split, n_tok, d), dtype=torch.float32, device=dev)
         for c in range(len(starts) - 1, -1, -1):
             s = starts[c]
@@ -152,7 +152,7 @@ def _lm_head_streamed(h_2d, labels, head: HostHead, num_items_in_batch, need_gra
             K.lm_head_ce_grad_logits(h_2d, w, labels, lse, denom, s, g)
             wt = torch.zeros((d, K._round_up(e - s, K.LM_K)), dtype=torch.float16, device=dev)
             wt[:, : e - s].copy_(w.t())
-            ns = K.lm_head_split_count(n_tok, d, e - s, target_blocks=256)
+            ns = K.lm_head_split_count(n_tok, d, e - s, max_split=n_split)
             K.lm_head_ce_grad_hidden(g, wt, e - s, dparts[:ns], accumulate=True)
             head.release_chunk(c)
         dh_pre = K.lm_head_dh_reduce(dparts, 1.0, torch.float32)
