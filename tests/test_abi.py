@@ -171,3 +171,24 @@ def test_lora_workspace_sizes_follow_the_block_decomposition():
 def test_kept_logit_entry_points_validate_on_the_host(name, args, msg):
     with pytest.raises(RuntimeError, match=msg):
         _lib.call(name, *args)
+
+
+def test_lm_head_split_count_fills_whole_rounds_of_workgroups():
+    from rus_amd import kernels as K
+
+    def abi_ok(k, s):  # the C ABI's rule: n_split = ceil(K / round_up(ceil(K / n_split), 64))
+        per = -(-k // s)
+        per = -(-per // 64) * 64
+        return s == -(-k // per)
+
+    # config 5 (707 tokens): 3 x 6 tiles; 14 splits = 252 blocks, one round on 256 CUs
+    assert K.lm_head_split_count(707, 1536, 151936) == 14
+    # config 2 (2048 tokens): 8 x 6 tiles; 16 splits = 768 blocks, three full rounds
+    assert K.lm_head_split_count(2048, 1536, 151936) == 16
+    for n, d, v in [(707, 1536, 151936), (17, 256, 700), (300, 256, 1031), (64, 64, 64)]:
+        kp = -(-v // 64) * 64
+        s = K.lm_head_split_count(n, d, v)
+        assert 1 <= s <= 64 and abi_ok(kp, s)
+        for cap in (1, 2, 5):
+            c = K.lm_head_split_count(n, d, v, max_split=cap)
+            assert c <= cap and abi_ok(kp, c)
