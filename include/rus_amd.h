@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define RUS_ABI_VERSION 10
+#define RUS_ABI_VERSION 11
 
 #define RUS_DTYPE_F16 0
 #define RUS_DTYPE_F32 1
@@ -47,6 +47,18 @@ int rus_abi_version(void);
  * solution/ops.py:1103-1127). RUS_ERR_INVALID when host_src is not pinned and mapped.
  */
 int rus_copy_from_host(void* dst, const void* host_src, int64_t n_bytes, void* stream);
+
+/*
+ * Row gather from page-locked, device-mapped host memory: dst[i, :] = host_src[ids[i], :] for
+ * i < n_ids, rows of row_bytes bytes (a multiple of 16; 16-byte aligned pointers), ids an int64
+ * DEVICE array. A kernel on `stream` reads each selected row over the bus, so nothing waits on the
+ * host. An id outside [0, n_src_rows) gives a zero row and sets *err_flag (device int32, optional).
+ * Replaces: HostHead.embed's host index_select + pinned staging + H2D copy
+ * (solution/hostload.py:381-386), which needs the ids on the host (a device synchronisation).
+ */
+int rus_gather_rows_from_host(const void* host_src, int64_t n_src_rows, int64_t row_bytes,
+                              const int64_t* ids, int64_t n_ids, void* dst, int32_t* err_flag,
+                              void* stream);
 
 /*
  * Diagnostic (no counterpart in the reference): node census of a captured hipGraph_t.
@@ -462,7 +474,9 @@ int rus_lmhead_ce_combine(const float* part_m, const float* part_s, const float*
 /*
  * Loss reduction: denom = max(*num_items, 1) when num_items is not NULL, else
  * max(#(labels != -100), 1); loss = sum(nll) / denom. One workgroup; both outputs on the device.
- * Replaces: solution/ops.py:268-277 (loss = nll.sum() / denominator, with its host .item()).
+ * With nll NULL only denom is written (loss may then be NULL too): the denominator the gradient
+ * needs before the per-token losses exist. Replaces: solution/ops.py:268-277 (loss = nll.sum() /
+ * denominator, with its host .item()).
  */
 int rus_lmhead_ce_loss(const float* nll, const int64_t* labels, int64_t n_tok,
                        const float* num_items, float* loss, float* denom, void* stream);
@@ -504,6 +518,52 @@ int rus_lmhead_ce_grad_hidden(const void* grad_logits, int64_t ld_g, const void*
                               float* parts, int32_t n_split, int32_t accumulate, void* stream);
 
 /*
+ * The hidden-gradient GEMM of the single-pass head: as rus_lmhead_ce_grad_hidden with the
+ * chunk's probabilities P (rus_lmhead_ce_chunk_scale) as the first operand, except that with
+ * accumulate != 0 each partial row is rescaled before the sum: parts[s][t][:] =
+ * parts[s][t][:] * alpha[t] + (P . W_chunk)[t][:] over split s. alpha (device, n_tok floats) is
+ * the factor e^{M_old - M_new} that chunk_scale wrote. n_split may exceed the number of 64-wide
+ * K pieces: the splits past them have an empty K range and only rescale their partials (so a
+ * shorter last chunk keeps every split's rows on the same maximum). Replaces: the per-chunk
+ * backward GEMM of
+ * solution/ops.py:300-322 (dH += G . W_chunk), without its logit recompute.
+ */
+int rus_lmhead_ce_grad_hidden_scaled(const void* probs, int64_t ld_p, const void* weight_t,
+                                     int64_t ld_wt, int64_t n_tok, int64_t d, int64_t n_vocab,
+                                     float* parts, int32_t n_split, int32_t accumulate,
+                                     const float* alpha, void* stream);
+
+/*
+ * One vocabulary chunk of the single-pass head, between its statistics GEMM (which kept the
+ * chunk's fp16 logits in `logits`, rus_lmhead_ce_fwd_keep, partial rows from part_base) and its
+ * hidden-gradient GEMM: with the running maximum M_run[t] (ignored when first != 0) and the
+ * chunk's maximum (from its partials), M = max(M_run[t], chunk max); the logits become
+ * P = fp16(e^{z - M}) in place (0 in the padding columns up to round_up(n_vocab, 64)),
+ * M_run[t] = M and alpha[t] = e^{M_run_old - M} (0 when first). Replaces: the logit recompute
+ * and lm_head_piece_kernel MODE 1 of solution/ops.py:287-319 / kernels.py:517-531 (the gradient
+ * is formed from P once lse is known, in rus_lmhead_ce_dh_finish).
+ */
+int rus_lmhead_ce_chunk_scale(void* logits, int64_t ld_z, int64_t n_tok, int64_t n_vocab,
+                              const float* part_m, int64_t part_stride, int64_t part_base,
+                              float* m_run, float* alpha, int32_t first, void* stream);
+
+/*
+ * Hidden gradient of the single-pass head from its accumulated partials:
+ *   out[t][c] = (sum_s parts[s][t][c] * e^{M_run[t] - lse[t]} - W[y_t][c]) * 2^16 / denom * scale
+ *               (* *scale_dev when given)
+ * for tokens with y_t != -100 (the W row only when 0 <= y_t < n_vocab), 0 otherwise; since
+ * sum_s parts = sum_v e^{z_v - M_run} W_v, this is sum_v (softmax - onehot) W_v with the
+ * reference's 2^16 / denom prescale. w_rows [n_vocab, ld_w] fp16 is device memory, or pinned
+ * host memory when w_on_host != 0 (label rows read over the bus). d % 4 == 0; out fp16 or fp32.
+ * Replaces: the backward's fp16 dH accumulation and rescale, solution/ops.py:283, 320, 332-339.
+ */
+int rus_lmhead_ce_dh_finish(const float* parts, int32_t n_parts, int64_t n_tok, int64_t d,
+                            const float* m_run, const float* lse, const int64_t* labels,
+                            const void* w_rows, int64_t ld_w, int64_t n_vocab, int32_t w_on_host,
+                            const float* denom, float scale, const float* scale_dev, void* out,
+                            int32_t out_dtype, void* stream);
+
+/*
  * out[i] = T(scale * (*scale_dev) * sum_p parts[p * n_elem + i]), T = out_dtype (fp16 or fp32);
  * scale_dev is an optional device scalar (NULL = 1), e.g. the incoming loss gradient, so the
  * caller never has to read it back to the host.
@@ -511,6 +571,16 @@ int rus_lmhead_ce_grad_hidden(const void* grad_logits, int64_t ld_g, const void*
  */
 int rus_lmhead_dh_reduce(const float* parts, int32_t n_parts, int64_t n_elem, float scale,
                          const float* scale_dev, void* out, int32_t out_dtype, void* stream);
+
+/*
+ * dst[c][r] = src[r][c] for r < rows, c < cols and dst[c][r] = 0 for rows <= r < rows_pad (fp16,
+ * row strides ld_src >= cols, ld_dst >= rows_pad). Builds the K-contiguous W^T operand of the
+ * hidden-gradient GEMM from W rows on the device (once for a resident head; per chunk for a head
+ * streamed from the host). Replaces: the weight transpose inside the reference's backward GEMM
+ * call (solution/ops.py:320, torch addmm on W^T views).
+ */
+int rus_transpose_f16(const void* src, int64_t rows, int64_t cols, int64_t ld_src, void* dst,
+                      int64_t ld_dst, int64_t rows_pad, void* stream);
 
 /*
  * Varlen causal GQA attention forward over packed tokens (fp16, head_dim 128 only):

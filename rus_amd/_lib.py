@@ -11,7 +11,7 @@ import threading
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "librus_amd.so"
-ABI_VERSION = 10
+ABI_VERSION = 11
 
 DTYPE_F16 = 0
 DTYPE_F32 = 1
@@ -52,6 +52,7 @@ NORM_FWD, NORM_BWD = 1, 2
 # name -> argtypes, in the order of include/rus_amd.h. Every entry point returns int.
 SIGNATURES: dict[str, list] = {
     "rus_copy_from_host": [_vp, _vp, _i64, _vp],
+    "rus_gather_rows_from_host": [_vp, _i64, _i64, _vp, _i64, _vp, _vp, _vp],
     "rus_nf4_dequant": [_vp, _vp, _vp, _vp, _f32, _f32, _f32, _i64, _i64, _i64, _i64, _i64, _i64,
                         _i64, _i32, _i32, _vp, _vp],
     "rus_nf4_dequant_multi": [ctypes.POINTER(Nf4Job), _i32, _vp, _i32, _i32, _vp],
@@ -106,6 +107,12 @@ SIGNATURES: dict[str, list] = {
                                   _vp, _i64, _vp],
     "rus_lmhead_ce_grad_hidden": [_vp, _i64, _vp, _i64, _i64, _i64, _i64, _vp, _i32, _i32, _vp],
     "rus_lmhead_dh_reduce": [_vp, _i32, _i64, _f32, _vp, _vp, _i32, _vp],
+    "rus_transpose_f16": [_vp, _i64, _i64, _i64, _vp, _i64, _i64, _vp],
+    "rus_lmhead_ce_grad_hidden_scaled": [_vp, _i64, _vp, _i64, _i64, _i64, _i64, _vp, _i32, _i32,
+                                         _vp, _vp],
+    "rus_lmhead_ce_chunk_scale": [_vp, _i64, _i64, _i64, _vp, _i64, _i64, _vp, _vp, _i32, _vp],
+    "rus_lmhead_ce_dh_finish": [_vp, _i32, _i64, _i64, _vp, _vp, _vp, _vp, _i64, _i64, _i32, _vp,
+                                _f32, _vp, _vp, _i32, _vp],
 }
 
 _lock = threading.Lock()

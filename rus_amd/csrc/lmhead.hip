@@ -523,6 +523,7 @@ __global__ __launch_bounds__(kZgThreads) void lmhead_grad_from_logits_kernel(
 struct StoreParams {
   float* parts;  // [splits][M][N] fp32
   int accumulate;
+  const float* alpha;  // accumulate: parts = parts * alpha[row] + acc (alpha null: factor 1)
 };
 
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))) void
@@ -547,10 +548,97 @@ lmhead_grad_hidden_kernel(GemmArgs g, StoreParams p) {
         const int row = tl.m0 + wm * kWM + mt * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
         if (row < g.M) {
           float* dst = base + static_cast<int64_t>(row) * g.N + col;
-          *dst = p.accumulate ? *dst + acc[mt][nt][r] : acc[mt][nt][r];
+          if (!p.accumulate)
+            *dst = acc[mt][nt][r];
+          else
+            *dst = (p.alpha ? *dst * p.alpha[row] : *dst) + acc[mt][nt][r];
         }
       }
   }
+}
+
+// ---------------------------------------------------------------------------------------------
+// Online single pass: one vocabulary chunk's kept logits z become P = fp16(e^{z - M}) in place,
+// where M = max(M_run, the chunk's maximum) is the running maximum over the chunks so far; the
+// hidden-gradient GEMM then accumulates P . W_chunk into partials rescaled by
+// alpha = e^{M_run - M}. Block = (token, kZgCols columns). Every block of a token forms M itself
+// from the chunk's partial maxima (max(M_run, chunk max) is the same whether it reads M_run before
+// or after block (token, 0) stores the new value); block (token, 0) writes M_run and alpha.
+// ---------------------------------------------------------------------------------------------
+
+__global__ __launch_bounds__(kZgThreads) void lmhead_chunk_scale_kernel(
+    f16* zg, int64_t ld, int n_vocab, int kpad, const float* __restrict__ part_m,
+    int64_t part_stride, int part_base, int n_parts, float* m_run, float* alpha, int first) {
+  __shared__ float red[kZgThreads / kWave];
+  const int tok = blockIdx.x;
+  float cm = -INFINITY;
+  for (int q = threadIdx.x; q < n_parts; q += kZgThreads)
+    cm = fmaxf(cm, part_m[static_cast<int64_t>(part_base + q) * part_stride + tok]);
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) cm = fmaxf(cm, __shfl_xor(cm, off, kWave));
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = cm;
+  __syncthreads();
+#pragma unroll
+  for (int w = 0; w < kZgThreads / kWave; ++w) cm = fmaxf(cm, red[w]);
+  const float mo = first ? -INFINITY : m_run[tok];
+  const float mn = fmaxf(mo, cm);
+  __syncthreads();  // every thread has read m_run before it is replaced
+  if (blockIdx.y == 0 && threadIdx.x == 0) {
+    m_run[tok] = mn;
+    alpha[tok] = first ? 0.0f : exp2_fast((mo - mn) * kLog2e);
+  }
+  const float mb = mn * kLog2e;
+  f16* row = zg + static_cast<int64_t>(tok) * ld;
+  const int c0 = blockIdx.y * kZgCols + threadIdx.x * 8;
+  f16x8 v[kZgUnroll];
+#pragma unroll
+  for (int u = 0; u < kZgUnroll; ++u) {
+    const int c = c0 + u * kZgThreads * 8;
+    if (c < kpad) v[u] = *reinterpret_cast<const f16x8*>(row + c);
+  }
+#pragma unroll
+  for (int u = 0; u < kZgUnroll; ++u) {
+    const int c = c0 + u * kZgThreads * 8;
+    if (c >= kpad) continue;
+    f16x8 o;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float pr = exp2_fast(__builtin_fmaf(static_cast<float>(v[u][e]), kLog2e, -mb));
+      o[e] = static_cast<_Float16>(c + e < n_vocab ? pr : 0.0f);
+    }
+    *reinterpret_cast<f16x8*>(row + c) = o;
+  }
+}
+
+// dH (times 2^16 / denom, times scale) from the online accumulation:
+//   out[t][c] = (sum_s parts[s][t][c] * e^{M[t] - lse[t]} - W[y_t][c]) * 2^16 / denom * scale
+// for labelled tokens (y_t != -100; the W row term only when y_t indexes the vocabulary), 0 for
+// the others. w_rows may be device memory or device-mapped pinned host memory. Four columns per
+// thread.
+template <typename T>
+__global__ __launch_bounds__(256) void lmhead_dh_finish_kernel(
+    const float* __restrict__ parts, int n_parts, int n_tok, int d, const float* __restrict__ m_run,
+    const float* __restrict__ lse, const int64_t* __restrict__ labels,
+    const f16* __restrict__ w_rows, int64_t ld_w, int64_t n_vocab, const float* __restrict__ denom,
+    float scale_h, const float* __restrict__ scale_d, T* __restrict__ out) {
+  const int64_t n = static_cast<int64_t>(n_tok) * d;
+  const int64_t i = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) * 4;
+  if (i >= n) return;
+  const int t = static_cast<int>(i / d), c = static_cast<int>(i % d);
+  const int64_t y = labels[t];
+  float o[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  if (y != -100) {
+    f32x4 a = *reinterpret_cast<const f32x4*>(parts + i);
+    for (int q = 1; q < n_parts; ++q) a += *reinterpret_cast<const f32x4*>(parts + q * n + i);
+    const float f = exp2_fast((m_run[t] - lse[t]) * kLog2e);
+    float scale = kPrescale / fmaxf(*denom, 1.0f) * scale_h;
+    if (scale_d) scale *= *scale_d;
+    float wy[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (y >= 0 && y < n_vocab) load_f32<f16, 4>(w_rows + y * ld_w + c, wy);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o[e] = (a[e] * f - wy[e]) * scale;
+  }
+  store_from_f32<T, 4>(out + i, o);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -647,6 +735,36 @@ __global__ __launch_bounds__(256) void dh_reduce_kernel(const float* __restrict_
       for (int q = 1; q < n_parts; ++q) s += parts[q * n + j];
       out[j] = static_cast<T>(s * scale);
     }
+  }
+}
+
+// dst[c][r] = src[r][c] for r < rows, c < cols, and dst[c][r] = 0 for rows <= r < rows_pad:
+// 64x64 tiles through LDS (row pitch 66 halves, so the column reads of the write phase spread
+// over the banks); each thread moves 16 elements in and 16 out.
+__global__ __launch_bounds__(256) void transpose_f16_kernel(const f16* __restrict__ src,
+                                                            int64_t rows, int64_t cols,
+                                                            int64_t ld_src, f16* __restrict__ dst,
+                                                            int64_t ld_dst, int64_t rows_pad) {
+  __shared__ f16 tile[64][66];
+  const int64_t r0 = static_cast<int64_t>(blockIdx.x) * 64, c0 = static_cast<int64_t>(blockIdx.y) * 64;
+  const int t = threadIdx.x;
+  {
+    const int rr = t >> 2, cc = (t & 3) * 16;
+    const int64_t r = r0 + rr;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int64_t c = c0 + cc + e;
+      tile[rr][cc + e] = (r < rows && c < cols) ? src[r * ld_src + c] : static_cast<f16>(0.0f);
+    }
+  }
+  __syncthreads();
+  const int cc = t >> 2, rr = (t & 3) * 16;
+  const int64_t c = c0 + cc;
+  if (c >= cols) return;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) {
+    const int64_t r = r0 + rr + e;
+    if (r < rows_pad) dst[c * ld_dst + r] = tile[rr + e][cc];
   }
 }
 
@@ -802,7 +920,7 @@ __global__ __launch_bounds__(1024) void lmhead_loss_kernel(const float* __restri
   __shared__ float s_sum[16], s_cnt[16];
   float sum = 0.0f, cnt = 0.0f;
   for (int i = threadIdx.x; i < n_tok; i += 1024) {
-    sum += nll[i];
+    if (nll) sum += nll[i];
     cnt += labels[i] != -100 ? 1.0f : 0.0f;
   }
   sum = wave_sum(sum);
@@ -821,7 +939,7 @@ __global__ __launch_bounds__(1024) void lmhead_loss_kernel(const float* __restri
     }
     const float d = fmaxf(num_items ? *num_items : c, 1.0f);
     denom[0] = d;
-    loss[0] = t / d;
+    if (loss) loss[0] = t / d;
   }
 }
 
@@ -835,7 +953,7 @@ extern "C" int rus_lmhead_ce_loss(const float* nll, const int64_t* labels, int64
   const char* fn = "rus_lmhead_ce_loss";
   if (n_tok < 0 || n_tok >= (int64_t(1) << 31))
     return fail(RUS_ERR_INVALID, "%s: n_tok=%lld outside [0, 2^31)", fn, (long long)n_tok);
-  if ((n_tok > 0 && (!nll || !labels)) || !loss || !denom)
+  if ((n_tok > 0 && !labels) || (nll && !loss) || !denom)
     return fail(RUS_ERR_INVALID, "%s: null pointer argument", fn);
   hipLaunchKernelGGL(lmhead_loss_kernel, dim3(1), dim3(1024), 0, static_cast<hipStream_t>(stream),
                      nll, labels, static_cast<int>(n_tok), num_items, loss, denom);
@@ -880,11 +998,12 @@ extern "C" int rus_lmhead_ce_grad_logits(const void* hidden, const void* weight,
   return check_launch(fn);
 }
 
-extern "C" int rus_lmhead_ce_grad_hidden(const void* grad_logits, int64_t ld_g,
-                                         const void* weight_t, int64_t ld_wt, int64_t n_tok,
-                                         int64_t d, int64_t n_vocab, float* parts,
-                                         int32_t n_split, int32_t accumulate, void* stream) {
-  const char* fn = "rus_lmhead_ce_grad_hidden";
+// allow_empty: splits past the last non-empty one still run (empty K range, so their epilogue
+// only rescales: parts = parts * alpha + 0).
+static int grad_hidden(const char* fn, const void* grad_logits, int64_t ld_g, const void* weight_t,
+                       int64_t ld_wt, int64_t n_tok, int64_t d, int64_t n_vocab, float* parts,
+                       int32_t n_split, int32_t accumulate, const float* alpha, bool allow_empty,
+                       void* stream) {
   if (n_tok < 0 || n_tok >= (1 << 30) || d <= 0 || d >= (1 << 30) || n_vocab < 0 ||
       n_vocab >= (1 << 30) || n_split <= 0 || n_split > 64)
     return fail(RUS_ERR_INVALID, "%s: bad sizes or n_split=%d (1..64)", fn, n_split);
@@ -909,14 +1028,99 @@ extern "C" int rus_lmhead_ce_grad_hidden(const void* grad_logits, int64_t ld_g,
   const int64_t per = (kpad + n_split - 1) / n_split;
   g.k_per_split = static_cast<int>((per + kBK - 1) / kBK * kBK);
   g.splits = static_cast<int>((kpad + g.k_per_split - 1) / g.k_per_split);
+  if (allow_empty) g.splits = n_split;
   if (g.splits != n_split)
     return fail(RUS_ERR_INVALID, "%s: n_split=%d does not divide K=%lld into 64-wide pieces", fn,
                 n_split, (long long)kpad);
   g.tiles_m = (g.M + kBM - 1) / kBM;
   g.tiles_n = (g.N + kBN - 1) / kBN;
-  StoreParams p{parts, accumulate};
+  StoreParams p{parts, accumulate, alpha};
   hipLaunchKernelGGL(lmhead_grad_hidden_kernel, dim3(launch_grid(g)), dim3(kThreads), 0,
                      static_cast<hipStream_t>(stream), g, p);
+  return check_launch(fn);
+}
+
+extern "C" int rus_lmhead_ce_grad_hidden(const void* grad_logits, int64_t ld_g,
+                                         const void* weight_t, int64_t ld_wt, int64_t n_tok,
+                                         int64_t d, int64_t n_vocab, float* parts,
+                                         int32_t n_split, int32_t accumulate, void* stream) {
+  return grad_hidden("rus_lmhead_ce_grad_hidden", grad_logits, ld_g, weight_t, ld_wt, n_tok, d,
+                     n_vocab, parts, n_split, accumulate, nullptr, false, stream);
+}
+
+extern "C" int rus_lmhead_ce_grad_hidden_scaled(const void* probs, int64_t ld_p,
+                                                const void* weight_t, int64_t ld_wt,
+                                                int64_t n_tok, int64_t d, int64_t n_vocab,
+                                                float* parts, int32_t n_split,
+                                                int32_t accumulate, const float* alpha,
+                                                void* stream) {
+  const char* fn = "rus_lmhead_ce_grad_hidden_scaled";
+  if (accumulate && !alpha) return fail(RUS_ERR_INVALID, "%s: alpha is null", fn);
+  return grad_hidden(fn, probs, ld_p, weight_t, ld_wt, n_tok, d, n_vocab, parts, n_split,
+                     accumulate, alpha, true, stream);
+}
+
+extern "C" int rus_lmhead_ce_chunk_scale(void* logits, int64_t ld_z, int64_t n_tok,
+                                         int64_t n_vocab, const float* part_m,
+                                         int64_t part_stride, int64_t part_base, float* m_run,
+                                         float* alpha, int32_t first, void* stream) {
+  const char* fn = "rus_lmhead_ce_chunk_scale";
+  if (n_tok < 0 || n_tok >= (1 << 30) || n_vocab < 0 || n_vocab >= (1 << 30) || part_base < 0 ||
+      part_base >= (1 << 30) || part_stride < n_tok)
+    return fail(RUS_ERR_INVALID, "%s: bad sizes", fn);
+  if (n_tok == 0 || n_vocab == 0) return RUS_OK;
+  const int64_t kpad = (n_vocab + kBK - 1) / kBK * kBK;
+  if (ld_z < kpad) return fail(RUS_ERR_INVALID, "%s: ld_z must be >= %lld", fn, (long long)kpad);
+  if (int e = check_operand(fn, logits, ld_z, "logits")) return e;
+  if (!part_m || !m_run || !alpha) return fail(RUS_ERR_INVALID, "%s: null pointer argument", fn);
+  const int64_t col_blocks = (kpad + kZgCols - 1) / kZgCols;
+  if (col_blocks > 65535) return fail(RUS_ERR_INVALID, "%s: n_vocab too large", fn);
+  const int n_parts = static_cast<int>((n_vocab + kBM - 1) / kBM);
+  hipLaunchKernelGGL(lmhead_chunk_scale_kernel,
+                     dim3(static_cast<unsigned>(n_tok), static_cast<unsigned>(col_blocks)),
+                     dim3(kZgThreads), 0, static_cast<hipStream_t>(stream),
+                     static_cast<f16*>(logits), ld_z, static_cast<int>(n_vocab),
+                     static_cast<int>(kpad), part_m, part_stride, static_cast<int>(part_base),
+                     n_parts, m_run, alpha, first ? 1 : 0);
+  return check_launch(fn);
+}
+
+extern "C" int rus_lmhead_ce_dh_finish(const float* parts, int32_t n_parts, int64_t n_tok,
+                                       int64_t d, const float* m_run, const float* lse,
+                                       const int64_t* labels, const void* w_rows, int64_t ld_w,
+                                       int64_t n_vocab, int32_t w_on_host, const float* denom,
+                                       float scale, const float* scale_dev, void* out,
+                                       int32_t out_dtype, void* stream) {
+  const char* fn = "rus_lmhead_ce_dh_finish";
+  if (n_parts <= 0 || n_tok < 0 || n_tok >= (1 << 30) || d <= 0 || d % 4 || d >= (1 << 30) ||
+      n_vocab < 0 || ld_w < d || (out_dtype != RUS_DTYPE_F16 && out_dtype != RUS_DTYPE_F32))
+    return fail(RUS_ERR_INVALID, "%s: bad arguments (d must be a multiple of 4)", fn);
+  if (n_tok == 0) return RUS_OK;
+  if (!parts || !m_run || !lse || !labels || !w_rows || !denom || !out || !aligned(parts, 16) ||
+      !aligned(out, 16) || !aligned(w_rows, 8) || ld_w % 4)
+    return fail(RUS_ERR_INVALID, "%s: null or misaligned pointer", fn);
+  const void* w = w_rows;
+  if (w_on_host) {  // pinned host rows are read through their device mapping
+    void* mapped = nullptr;
+    const hipError_t e = hipHostGetDevicePointer(&mapped, const_cast<void*>(w_rows), 0);
+    if (e != hipSuccess || !mapped)
+      return fail(RUS_ERR_INVALID, "%s: w_rows is not page-locked, device-mapped host memory (%s)",
+                  fn, hipGetErrorString(e));
+    w = mapped;
+  }
+  const int64_t n = n_tok * d;
+  const dim3 grid(static_cast<unsigned>((n / 4 + 255) / 256));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (out_dtype == RUS_DTYPE_F16)
+    hipLaunchKernelGGL(lmhead_dh_finish_kernel<f16>, grid, dim3(256), 0, st, parts, n_parts,
+                       static_cast<int>(n_tok), static_cast<int>(d), m_run, lse, labels,
+                       static_cast<const f16*>(w), ld_w, n_vocab, denom, scale, scale_dev,
+                       static_cast<f16*>(out));
+  else
+    hipLaunchKernelGGL(lmhead_dh_finish_kernel<float>, grid, dim3(256), 0, st, parts, n_parts,
+                       static_cast<int>(n_tok), static_cast<int>(d), m_run, lse, labels,
+                       static_cast<const f16*>(w), ld_w, n_vocab, denom, scale, scale_dev,
+                       static_cast<float*>(out));
   return check_launch(fn);
 }
 
@@ -947,5 +1151,21 @@ extern "C" int rus_lmhead_dh_reduce(const float* parts, int32_t n_parts, int64_t
       hipLaunchKernelGGL((dh_reduce_kernel<float, false>), grid, dim3(256), 0, st, parts, n_parts,
                          n_elem, scale, scale_dev, static_cast<float*>(out));
   }
+  return check_launch(fn);
+}
+
+extern "C" int rus_transpose_f16(const void* src, int64_t rows, int64_t cols, int64_t ld_src,
+                                 void* dst, int64_t ld_dst, int64_t rows_pad, void* stream) {
+  const char* fn = "rus_transpose_f16";
+  if (rows < 0 || cols < 0 || rows_pad < rows || ld_src < cols || ld_dst < rows_pad)
+    return fail(RUS_ERR_INVALID, "%s: bad sizes or strides", fn);
+  if (rows_pad == 0 || cols == 0) return RUS_OK;
+  if (!src || !dst) return fail(RUS_ERR_INVALID, "%s: null pointer argument", fn);
+  const int64_t gx = (rows_pad + 63) / 64, gy = (cols + 63) / 64;
+  if (gx >= (int64_t(1) << 31) || gy > 65535)
+    return fail(RUS_ERR_INVALID, "%s: matrix too large", fn);
+  hipLaunchKernelGGL(transpose_f16_kernel, dim3(static_cast<unsigned>(gx), static_cast<unsigned>(gy)),
+                     dim3(256), 0, static_cast<hipStream_t>(stream), static_cast<const f16*>(src),
+                     rows, cols, ld_src, static_cast<f16*>(dst), ld_dst, rows_pad);
   return check_launch(fn);
 }

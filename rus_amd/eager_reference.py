@@ -9,7 +9,7 @@ stack's counter-based ones for a given seed (drawn by the dropout kernel on a te
 applied with plain torch ops under autograd), so both paths drop the same elements.
 
 Used by bench.py for the peak-memory / throughput comparison and by the GPU tests as a second,
-independent GPU reference for dropout replay and the full-size step.
+independent GPU reference (the 28-layer step's loss and LoRA gradients).
 """
 
 from __future__ import annotations
@@ -18,7 +18,29 @@ import torch
 import torch.nn.functional as F
 
 from . import kernels as K
-from .ops import _run_packed_sdpa
+
+
+def _run_packed_sdpa(q_rot, k_rot, v_out, row_lengths, num_heads, num_kv_heads, head_dim):
+    """Causal GQA attention per packed row with K/V expanded per group, as the reference's
+    stack does it (solution/ops.py:669-696): torch SDPA, differentiable."""
+    n_tokens = q_rot.shape[0]
+    out = torch.empty((n_tokens, num_heads * head_dim), dtype=q_rot.dtype, device=q_rot.device)
+    groups = num_heads // num_kv_heads
+    cur = 0
+    for L in row_lengths:
+        if L <= 0:
+            continue
+        nxt = cur + L
+        q = q_rot[cur:nxt].transpose(0, 1).unsqueeze(0)
+        k = k_rot[cur:nxt].transpose(0, 1).unsqueeze(0)
+        v = v_out[cur:nxt].transpose(0, 1).unsqueeze(0)
+        if groups > 1:
+            k = k.unsqueeze(2).expand(1, num_kv_heads, groups, L, head_dim).reshape(1, num_heads, L, head_dim)
+            v = v.unsqueeze(2).expand(1, num_kv_heads, groups, L, head_dim).reshape(1, num_heads, L, head_dim)
+        o = F.scaled_dot_product_attention(q, k, v, is_causal=True)
+        out[cur:nxt] = o.squeeze(0).transpose(0, 1).reshape(L, num_heads * head_dim)
+        cur = nxt
+    return out
 
 
 class _NF4Linear(torch.autograd.Function):

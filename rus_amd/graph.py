@@ -141,9 +141,6 @@ class GraphedTrainStep:
             raise ValueError("GraphedTrainStep needs an HBM-resident lm_head (resident_head=True)")
         if engine.input_stream.offload:
             raise ValueError("GraphedTrainStep keeps layer inputs in HBM (offload_inputs=False)")
-        if engine.attention not in ("varlen", "varlen_aten"):
-            raise ValueError("GraphedTrainStep needs one launch over all packed rows "
-                             "(attention='varlen' or 'varlen_aten')")
         self.engine = engine
         self.bucket = int(bucket)
         self.training = training

@@ -1,38 +1,129 @@
 """Weight, lm_head and activation residency for the fused Qwen2 stack (solution/hostload.py).
 
+Everything that moves between pinned host memory and HBM goes through one mechanism here, a
+``SlotRing``: a few device buffers ("slots") that a copy stream refills from the host while the
+compute stream reads the others, ordered only by events (no host synchronisation). The three
+reference classes keep their public protocol on top of it:
+
 * ``WeightStream`` packs each layer's seven NF4 projections into four fused segments
-  ([q|k|v], o, [gate|up], down; solution/hostload.py:159-258) in one byte buffer per layer and
-  serves fp16 weights through the gfx950 dequant kernel. Two residencies:
-    - ``resident=False`` (the reference's policy): packed layers live in pinned
-      host memory and are copied per step into two device slots on a side stream, ordered by
-      events (prefetch / wait_slot / release_slot, hostload.py:297-323);
-    - ``resident=True`` (MI355X: 28 packed layers are 0.65 GB of 288 GB HBM): packed layers stay in
-      HBM and prefetch / wait_slot / release_slot do nothing.
-  Each segment dequantises into its own fp16 workspace, so the stack dequantises a segment once
-  per layer per pass instead of re-dequantising a single shared workspace (the reference does 17
-  dequants per layer per step, hostload.py:295, 325-342; this layout needs 8).
-* ``HostHead`` holds the tied embedding / lm_head: HBM-resident with its W^T for the gradient GEMM
-  (default), or in pinned host memory streamed in vocabulary chunks through two device slots
-  (hostload.py:345-408).
-* ``InputStream`` keeps each layer's input for the backward recompute: in HBM (default) or
-  offloaded to pinned host memory with a one-ahead reverse prefetch (hostload.py:411-488, whose
-  three-ahead prefetch into a two-slot ring is always overwritten before use).
+  ([q|k|v], o, [gate|up], down; solution/hostload.py:159-258) and lays all layers out in one
+  byte image (per layer: packed | absmax | absmax2, 256-byte aligned). Placements:
+    - ``resident=True``: the image lives in HBM (0.65 GB at Qwen2.5-1.5B; prefetch / wait_slot /
+      release_slot do nothing);
+    - ``unit="layer"`` (the reference's policy, hostload.py:286-323): the image is pinned on the
+      host and a two-slot ring receives one layer at a time (prefetch / wait_slot /
+      release_slot);
+    - ``unit="model"``: the whole image is copied once per step into one of two device buffers
+      while the previous step runs (begin_step / end_step).
+  Each segment dequantises into its own fp16 workspace, so a layer needs one dequant launch per
+  pass instead of the reference's 17 per step (hostload.py:295, 325-342).
+* ``HostHead`` holds the tied embedding / lm_head: HBM-resident with W^T for the gradient GEMM
+  (default), or pinned on the host with vocabulary chunks streamed through a two-slot ring
+  (hostload.py:345-408). Embedding rows of a host head are gathered on the device by a kernel
+  that reads them over the bus (the reference gathers on the host after synchronising).
+* ``InputStream`` keeps each layer's input for the backward recompute: in HBM (default), or
+  offloaded to pinned host memory and brought back one layer ahead through a two-slot ring
+  (hostload.py:411-488, whose three-ahead prefetch into a two-slot ring is always overwritten
+  before use).
 """
 
 from __future__ import annotations
 
+from typing import Callable, Sequence
+
 import torch
 
 from . import kernels as K
-from .quant import NF4Weight, concat_segments
+from .quant import concat_segments
 
 MAX_MLP_TOKENS = 1 << 30  # the reference chunks the MLP at 512 tokens for a 15 GB T4; not needed
 V_CHUNK_DEFAULT = 8192  # vocabulary rows per streamed lm_head chunk (hostload.py:24)
 SEGMENTS = ("qkv", "o", "gu", "down")
+_ALIGN = 256
+
+
+def _align(x: int) -> int:
+    return (x + _ALIGN - 1) // _ALIGN * _ALIGN
+
+
+def _pinned(t: torch.Tensor) -> torch.Tensor:
+    cpu = t.detach().contiguous().cpu()
+    return cpu.pin_memory() if torch.cuda.is_available() else cpu
+
+
+class SlotRing:
+    """Device slots refilled from pinned host memory on a copy stream.
+
+    Item ``i`` always uses slot ``i % len(slots)``. Per slot the ring remembers which tag it
+    holds, an event that completes when its last fill has landed and an event that completes when
+    its last reader is done. ``fill`` enqueues a copy behind that reader event (so a copy never
+    overwrites bytes a kernel still reads) unless the slot already holds the tag; ``take`` fills
+    if needed and makes the current stream wait for the fill; ``give_back`` marks the reader
+    event on the current stream. Copies of one ring run in the order they are enqueued."""
+
+    def __init__(self, device, slots: Sequence):
+        self.device = torch.device(device)
+        self.slots = list(slots)
+        n = len(self.slots)
+        self.copy_stream = torch.cuda.Stream(device=self.device)  # default priority
+        self._holds: list = [None] * n
+        self._landed = [torch.cuda.Event() for _ in range(n)]
+        self._read_done = [torch.cuda.Event() for _ in range(n)]
+        self._read_marked = [False] * n
+
+    def slot(self, item: int) -> int:
+        return item % len(self.slots)
+
+    def holds(self, item: int, tag) -> bool:
+        return self._holds[self.slot(item)] == tag
+
+    def fill(self, item: int, tag, copy: Callable) -> int:
+        """Enqueues ``copy(slot_buffers)`` on the copy stream (after the slot's last reader) unless
+        the slot already holds ``tag``; returns the slot index."""
+        s = self.slot(item)
+        if self._holds[s] == tag:
+            return s
+        cs = self.copy_stream
+        with torch.cuda.stream(cs):
+            if self._read_marked[s]:
+                cs.wait_event(self._read_done[s])
+            copy(self.slots[s])
+            self._landed[s].record(cs)
+        self._holds[s] = tag
+        return s
+
+    def take(self, item: int, tag, copy: Callable):
+        """The slot buffers holding ``tag`` (filled now if they do not), ready for the current
+        stream."""
+        s = self.fill(item, tag, copy)
+        torch.cuda.current_stream(self.device).wait_event(self._landed[s])
+        return self.slots[s]
+
+    def give_back(self, item: int, forget: bool = False) -> None:
+        """The current stream's reads of ``item``'s slot are all enqueued; ``forget`` drops the tag
+        (the next ``fill`` copies again)."""
+        s = self.slot(item)
+        self._read_done[s].record(torch.cuda.current_stream(self.device))
+        self._read_marked[s] = True
+        if forget:
+            self._holds[s] = None
+
+    def restart(self) -> None:
+        """Every slot empty, and idle once the current stream's work so far is done. Used around
+        graph capture and replay: the copy stream's first waits then depend on an event recorded
+        in the same stream as the capture, and a captured step copies every item it reads."""
+        cur = torch.cuda.current_stream(self.device)
+        n = len(self.slots)
+        self._landed = [torch.cuda.Event() for _ in range(n)]
+        self._read_done = [torch.cuda.Event() for _ in range(n)]
+        for ev in self._read_done:
+            ev.record(cur)
+        self._read_marked = [True] * n
+        self._holds = [None] * n
 
 
 class PackedNF4Segment:
-    """One fused segment of a layer's packed buffer (hostload.py:27-62), plus the absmax2 base of
+    """One fused segment of a layer's packed bytes (hostload.py:27-62), plus the absmax2 base of
     each sub-segment (the reference assumes global super-block indexing)."""
 
     __slots__ = ("out_features", "in_features", "packed_slice", "absmax_slice", "absmax2_slice",
@@ -52,25 +143,55 @@ class PackedNF4Segment:
         self.super_blocksize = super_blocksize
 
 
-def _pinned(t: torch.Tensor) -> torch.Tensor:
-    cpu = t.detach().contiguous().cpu()
-    return cpu.pin_memory() if torch.cuda.is_available() else cpu
+class _LayerImage:
+    """Byte layout of the packed model: per layer [packed | absmax | absmax2 (fp32)], each part
+    256-byte aligned, layers back to back. ``views(buf, l, base)`` cuts one layer's three arrays out
+    of a byte buffer holding that layer at byte ``base``."""
+
+    def __init__(self, packed_l, absmax_l, absmax2_l):
+        self.parts = []  # per layer (start, packed_off, absmax_off, absmax2_off, n_p, n_a, n_a2)
+        cur = 0
+        for p, a, a2 in zip(packed_l, absmax_l, absmax2_l):
+            start = cur
+            ao = _align(p.numel())
+            a2o = _align(ao + a.numel())
+            size = _align(a2o + 4 * a2.numel())
+            self.parts.append((start, 0, ao, a2o, p.numel(), a.numel(), a2.numel(), size))
+            cur += size
+        self.total = cur
+        self.max_layer = max((q[-1] for q in self.parts), default=0)
+
+    def build(self, packed_l, absmax_l, absmax2_l) -> torch.Tensor:
+        img = torch.zeros(self.total, dtype=torch.uint8)
+        for (start, po, ao, a2o, *_), p, a, a2 in zip(self.parts, packed_l, absmax_l, absmax2_l):
+            img[start + po: start + po + p.numel()] = p
+            img[start + ao: start + ao + a.numel()] = a
+            img[start + a2o: start + a2o + 4 * a2.numel()] = a2.contiguous().view(torch.uint8)
+        return img
+
+    def layer_range(self, l: int) -> tuple[int, int]:
+        start, *_, size = self.parts[l]
+        return start, start + size
+
+    def views(self, buf: torch.Tensor, l: int, base: int):
+        _, po, ao, a2o, n_p, n_a, n_a2, _ = self.parts[l]
+        return (buf[base + po: base + po + n_p], buf[base + ao: base + ao + n_a],
+                buf[base + a2o: base + a2o + 4 * n_a2].view(torch.float32))
 
 
 class WeightStream:
     """Packed NF4 layers served as fp16 weights through the dequant kernel.
 
-    ``unit`` (when not resident) sets what is streamed from pinned host memory:
-      * "layer": two one-layer device slots refilled per layer per pass (the reference's policy,
-        hostload.py:286-323; 2 x 28 layer copies per step);
-      * "model": ``model_buffers`` (default 2) whole-model device buffers used in turn; each
-        step copies the packed model once (one 645 MiB H2D copy at Qwen2.5-1.5B) into the
-        buffer of the next step, on the copy stream, overlapping the current step; the step
-        waits for its own copy (``begin_step``), uses that buffer for forward and backward and
-        releases it (``end_step``). A copy does not wait for the last reader of its buffer: the
-        base weights are frozen, so it rewrites the bytes that reader sees. (A copy stream
-        holding a wait on a running step delays, on this runtime, the completion of the copies
-        ahead of it, which idles the start of the next step.)"""
+    ``unit`` (when not resident) sets what is streamed from pinned host memory per step:
+      * "layer": a two-slot ring refilled one layer at a time in each pass (the reference's
+        policy, hostload.py:286-323; 2 x 28 layer copies per step);
+      * "model": ``model_buffers`` (default 2) whole-model device buffers used in turn; each step
+        copies the packed model once (645 MiB at Qwen2.5-1.5B) into the buffer of the next step,
+        on the copy stream, while the current step runs. Such a copy does not wait for the
+        buffer's last reader while the host image is unchanged (it rewrites the same bytes; a
+        copy stream holding a wait on a running step delays, on this runtime, the completion of
+        the copies queued before it). After ``host_image_changed()`` the next copy into each
+        buffer waits for that buffer's last step."""
 
     def __init__(self, layers, device, resident: bool = False, unit: str = "layer",
                  model_buffers: int = 2):
@@ -117,72 +238,54 @@ class WeightStream:
             absmax2_l.append(torch.cat([t.reshape(-1).float().cpu() for t in a2b]))
         self.layer_bytes = [int(p.numel() + a.numel() + 4 * a2.numel())
                             for p, a, a2 in zip(packed_l, absmax_l, absmax2_l)]
+        self.image = _LayerImage(packed_l, absmax_l, absmax2_l)
+        self.model_bytes = self.image.total
+        host = self.image.build(packed_l, absmax_l, absmax2_l)
+        del packed_l, absmax_l, absmax2_l
+        self.active = 0
         if resident:
-            self.gpu_layers = [(p.to(self.device), a.to(self.device), a2.to(self.device))
-                               for p, a, a2 in zip(packed_l, absmax_l, absmax2_l)]
-        elif self.unit == "model":
-            self._init_model_buffers(packed_l, absmax_l, absmax2_l)
+            self.dev_blobs = [host.to(self.device)]
         else:
-            self.cpu_packed = [_pinned(p) for p in packed_l]
-            self.cpu_absmax = [_pinned(a) for a in absmax_l]
-            self.cpu_absmax2 = [_pinned(a) for a in absmax2_l]
-            mp = max(p.numel() for p in packed_l)
-            ma = max(a.numel() for a in absmax_l)
-            ma2 = max(a.numel() for a in absmax2_l)
-            self.gpu_packed_slots = [torch.empty(mp, dtype=torch.uint8, device=self.device) for _ in range(2)]
-            self.gpu_absmax_slots = [torch.empty(ma, dtype=torch.uint8, device=self.device) for _ in range(2)]
-            self.gpu_absmax2_slots = [torch.empty(ma2, dtype=torch.float32, device=self.device) for _ in range(2)]
-            self.stream = torch.cuda.Stream(device=self.device)
-            self.slot_events = [torch.cuda.Event() for _ in range(2)]
-            self.compute_done_events = [torch.cuda.Event() for _ in range(2)]
-            self.slot_layer = [-1, -1]
+            self.host_blob = _pinned(host)
+            if self.unit == "model":
+                self._init_model_buffers()
+            else:
+                self._ring = SlotRing(self.device, [
+                    torch.empty(self.image.max_layer, dtype=torch.uint8, device=self.device)
+                    for _ in range(2)])
+        del host
         self.workspaces = {s: torch.empty(n, dtype=torch.float16, device=self.device)
                            for s, n in ws_elems.items()}
 
-    def _init_model_buffers(self, packed_l, absmax_l, absmax2_l) -> None:
-        """One pinned host blob holding every layer (packed | absmax | absmax2, each 256-byte
-        aligned) and n_buffers device blobs of the same layout."""
-        def up(x):
-            return (x + 255) // 256 * 256
-
-        offs, cur = [], 0
-        for p, a, a2 in zip(packed_l, absmax_l, absmax2_l):
-            po = cur
-            ao = up(po + p.numel())
-            a2o = up(ao + a.numel())
-            cur = up(a2o + 4 * a2.numel())
-            offs.append((po, ao, a2o))
-        self.model_bytes = cur
-        blob = torch.zeros(cur, dtype=torch.uint8)
-        for (po, ao, a2o), p, a, a2 in zip(offs, packed_l, absmax_l, absmax2_l):
-            blob[po: po + p.numel()] = p
-            blob[ao: ao + a.numel()] = a
-            blob[a2o: a2o + 4 * a2.numel()] = a2.contiguous().view(torch.uint8)
-        self.host_blob = _pinned(blob)
+    # -- whole-model streaming (unit="model") --------------------------------------------------
+    def _init_model_buffers(self) -> None:
         nb = self.n_buffers
-        self.dev_blobs = [torch.empty(cur, dtype=torch.uint8, device=self.device)
+        self.dev_blobs = [torch.empty(self.image.total, dtype=torch.uint8, device=self.device)
                           for _ in range(nb)]
-        self.blob_views = []
-        for b in self.dev_blobs:
-            views = []
-            for (po, ao, a2o), p, a, a2 in zip(offs, packed_l, absmax_l, absmax2_l):
-                views.append((b[po: po + p.numel()], b[ao: ao + a.numel()],
-                              b[a2o: a2o + 4 * a2.numel()].view(torch.float32)))
-            self.blob_views.append(views)
-        self.stream = torch.cuda.Stream(device=self.device)
+        self.stream = torch.cuda.Stream(device=self.device)  # default priority
         self.ready_events = [torch.cuda.Event() for _ in range(nb)]
+        self._last_step = [torch.cuda.Event() for _ in range(nb)]
+        self._stepped = [False] * nb
+        self._image_version = 0
+        self._buf_version = [-1] * nb
         self.staged = [False] * nb
-        self.active = 0
         self.next_buffer = 0
 
-    # -- whole-model streaming (unit="model") --------------------------------------------------
+    def host_image_changed(self) -> None:
+        """Call after modifying ``host_blob``: the next copy into each device buffer then waits
+        for the last step that read that buffer."""
+        if self.unit == "model":
+            self._image_version += 1
+
     def stage(self, buf: int) -> None:
-        """Copies the packed model into device buffer ``buf`` on the copy stream. Only a buffer's
-        first copy precedes every read of it; later copies rewrite identical bytes, so they do
-        not wait for the buffer's readers."""
+        """Copies the packed model into device buffer ``buf`` on the copy stream."""
         with torch.cuda.stream(self.stream):
+            stale = self._buf_version[buf] not in (-1, self._image_version)
+            if stale and self._stepped[buf]:
+                self.stream.wait_event(self._last_step[buf])
             self.dev_blobs[buf].copy_(self.host_blob, non_blocking=True)
             self.ready_events[buf].record(self.stream)
+        self._buf_version[buf] = self._image_version
         self.staged[buf] = True
 
     def begin_step(self) -> int:
@@ -208,73 +311,56 @@ class WeightStream:
             self.active = buf
 
     def end_step(self, buf: int) -> None:
-        """Ends a step's use of ``buf``. Nothing to record: the next copy into ``buf`` rewrites
-        the bytes its readers see, so it does not wait for them."""
-        del buf
+        """The current stream's reads of ``buf`` for this step are enqueued."""
+        if self.unit == "model":
+            self._last_step[buf].record(torch.cuda.current_stream(self.device))
+            self._stepped[buf] = True
 
-    # -- streaming protocol (hostload.py:297-323) ------------------------------------------------
+    # -- per-layer streaming protocol (hostload.py:297-323) ---------------------------------------
+    def _layer_copy(self, layer_idx: int):
+        lo, hi = self.image.layer_range(layer_idx)
+        src = self.host_blob[lo:hi]
+
+        def copy(slot: torch.Tensor) -> None:
+            slot[: hi - lo].copy_(src, non_blocking=True)
+
+        return copy
+
     def prefetch(self, layer_idx: int) -> None:
-        if self.unit != "layer" or layer_idx < 0 or layer_idx >= self.num_layers:
+        """Starts copying ``layer_idx`` into its slot (unit="layer"; otherwise nothing)."""
+        if self.unit != "layer" or not 0 <= layer_idx < self.num_layers:
             return
-        slot = layer_idx % 2
-        if self.slot_layer[slot] == layer_idx:
-            return
-        with torch.cuda.stream(self.stream):
-            self.stream.wait_event(self.compute_done_events[slot])
-            for dst, src in ((self.gpu_packed_slots, self.cpu_packed),
-                             (self.gpu_absmax_slots, self.cpu_absmax),
-                             (self.gpu_absmax2_slots, self.cpu_absmax2)):
-                s = src[layer_idx]
-                dst[slot][: s.numel()].copy_(s, non_blocking=True)
-            self.slot_events[slot].record(self.stream)
-            self.slot_layer[slot] = layer_idx
+        self._ring.fill(layer_idx, layer_idx, self._layer_copy(layer_idx))
 
     def wait_slot(self, layer_idx: int) -> int:
+        """Makes the current stream wait until ``layer_idx`` is in its slot; returns the slot."""
         if self.unit != "layer":
             return 0
-        slot = layer_idx % 2
-        if self.slot_layer[slot] != layer_idx:
-            self.prefetch(layer_idx)
-        torch.cuda.current_stream(self.device).wait_event(self.slot_events[slot])
-        return slot
+        self._ring.take(layer_idx, layer_idx, self._layer_copy(layer_idx))
+        return self._ring.slot(layer_idx)
+
+    def release_slot(self, layer_idx: int) -> None:
+        """Every read of ``layer_idx``'s slot is enqueued on the current stream."""
+        if self.unit == "layer":
+            self._ring.give_back(layer_idx)
 
     def begin_capture(self) -> None:
-        """Before capturing a step into a HIP graph: the side stream's first waits depend on an
-        event recorded in the capturing stream, and the slots are taken as empty so that the
-        graph copies every layer it uses (unit="layer"; nothing to do otherwise)."""
-        if self.unit != "layer":
-            return
-        cur = torch.cuda.current_stream(self.device)
-        self.compute_done_events = [torch.cuda.Event() for _ in range(2)]
-        for ev in self.compute_done_events:
-            ev.record(cur)
-        self.slot_events = [torch.cuda.Event() for _ in range(2)]
-        self.slot_layer = [-1, -1]
+        """Before capturing a step into a HIP graph (unit="layer"): the ring restarts empty, so
+        the graph copies every layer it reads, behind an event of the capturing stream."""
+        if self.unit == "layer":
+            self._ring.restart()
 
     def after_replay(self) -> None:
         """After a graph replay (or capture) on the current stream: later eager prefetches wait
-        for it before overwriting the slots, and take the slots as empty (unit="layer")."""
-        if self.unit != "layer":
-            return
-        cur = torch.cuda.current_stream(self.device)
-        self.compute_done_events = [torch.cuda.Event() for _ in range(2)]
-        for ev in self.compute_done_events:
-            ev.record(cur)
-        self.slot_events = [torch.cuda.Event() for _ in range(2)]
-        self.slot_layer = [-1, -1]
-
-    def release_slot(self, layer_idx: int) -> None:
-        if self.unit != "layer":
-            return
-        self.compute_done_events[layer_idx % 2].record(torch.cuda.current_stream(self.device))
+        for it, and take the slots as empty (unit="layer")."""
+        if self.unit == "layer":
+            self._ring.restart()
 
     def _arrays(self, layer_idx: int):
-        if self.unit == "resident":
-            return self.gpu_layers[layer_idx]
-        if self.unit == "model":
-            return self.blob_views[self.active][layer_idx]
-        slot = layer_idx % 2
-        return self.gpu_packed_slots[slot], self.gpu_absmax_slots[slot], self.gpu_absmax2_slots[slot]
+        if self.unit == "layer":
+            return self.image.views(self._ring.slots[self._ring.slot(layer_idx)], layer_idx, 0)
+        buf = self.dev_blobs[self.active if self.unit == "model" else 0]
+        return self.image.views(buf, layer_idx, self.image.layer_range(layer_idx)[0])
 
     def dequant(self, layer_idx: int, seg_name: str) -> torch.Tensor:
         """fp16 [out, in] weight of one segment (a view of that segment's workspace, valid until
@@ -310,7 +396,8 @@ class WeightStream:
         no dequantisation; the kernels read the packed bytes where they lie (slot, whole-model
         buffer or resident copy), so a streamed slot must stay unreleased until the layer's last
         product is enqueued. Operands are cached per (buffer, layer)."""
-        key = (self.unit, getattr(self, "active", 0) if self.unit == "model" else 0, layer_idx)
+        where = self._ring.slot(layer_idx) if self.unit == "layer" else self.active
+        key = (self.unit, where, layer_idx)
         cache = self.__dict__.setdefault("_nf4_ops", {})
         got = cache.get(key)
         if got is None:
@@ -366,59 +453,83 @@ class WeightStream:
 
 
 class HostHead:
-    """Tied embedding / lm_head: HBM-resident (with W^T for the gradient GEMM) or streamed from
-    pinned host memory in ``v_chunk``-row chunks through two device slots."""
+    """Tied embedding / lm_head: HBM-resident (with W^T for the gradient GEMM) or pinned on the
+    host and streamed in ``v_chunk``-row vocabulary chunks through a two-slot ring. A chunk slot
+    holds the rows [start, end) and, for the gradient GEMM, their transpose (built on the device
+    from the rows just copied, so the host is read once per chunk and pass)."""
 
     def __init__(self, weight: torch.Tensor, device, v_chunk: int = V_CHUNK_DEFAULT,
                  resident: bool = True):
         self.device = torch.device(device)
-        self.v_chunk = v_chunk
+        self.v_chunk = int(v_chunk)
         self.resident = resident
         self.vocab_size, self.hidden_size = weight.shape
+        if self.v_chunk <= 0 or self.v_chunk % K.LM_TILE:
+            raise ValueError(f"v_chunk must be a positive multiple of {K.LM_TILE}")
         if resident:
             self.gpu_weight = weight.detach().to(self.device, torch.float16).contiguous()
             self.gpu_weight_t = K.lm_head_weight_t(self.gpu_weight)
         else:
             self.cpu_weight = _pinned(weight.detach().to(torch.float16))
-            self.stream = torch.cuda.Stream(device=self.device)
-            self.slot_events = [torch.cuda.Event() for _ in range(2)]
-            self.compute_done_events = [torch.cuda.Event() for _ in range(2)]
-            self.slot_chunk = [-1, -1]
-            self.gpu_slots = [torch.empty((v_chunk, self.hidden_size), dtype=torch.float16,
-                                          device=self.device) for _ in range(2)]
+            rows = min(self.v_chunk, self.vocab_size)
+            self._ring = SlotRing(self.device, [
+                (torch.empty((rows, self.hidden_size), dtype=torch.float16, device=self.device),
+                 torch.zeros((self.hidden_size, K._round_up(rows, K.LM_K)), dtype=torch.float16,
+                             device=self.device))
+                for _ in range(2)])
+            self.embed_error = torch.zeros(1, dtype=torch.int32, device=self.device)
 
     def embed(self, input_ids: torch.Tensor) -> torch.Tensor:
+        """Embedding rows of ``input_ids`` (any shape) as fp16 [*shape, hidden] on the device."""
         ids = input_ids.reshape(-1)
         if self.resident:
             out = torch.nn.functional.embedding(ids.to(self.device), self.gpu_weight)
-        else:  # host gather + async copy, as hostload.py:381-386
-            emb = self.cpu_weight.index_select(0, ids.cpu())
-            out = emb.pin_memory().to(self.device, non_blocking=True)
+        else:
+            out = K.gather_rows_from_host(self.cpu_weight, ids.to(self.device, torch.int64),
+                                          err_flag=self.embed_error)
         return out.view(*input_ids.shape, self.hidden_size)
 
+    def _chunk_copy(self, start_v: int, end_v: int):
+        src = self.cpu_weight[start_v:end_v]
+
+        def copy(slot) -> None:
+            rows, rows_t = slot
+            rows[: end_v - start_v].copy_(src, non_blocking=True)
+
+        return copy
+
     def prefetch_chunk(self, chunk_idx: int, start_v: int, end_v: int) -> None:
-        slot = chunk_idx % 2
-        if self.slot_chunk[slot] == start_v:
-            return
-        with torch.cuda.stream(self.stream):
-            self.stream.wait_event(self.compute_done_events[slot])
-            self.gpu_slots[slot][: end_v - start_v].copy_(self.cpu_weight[start_v:end_v], non_blocking=True)
-            self.slot_events[slot].record(self.stream)
-            self.slot_chunk[slot] = start_v
+        """Starts copying vocabulary rows [start_v, end_v) into chunk ``chunk_idx``'s slot."""
+        self._ring.fill(chunk_idx, (start_v, end_v), self._chunk_copy(start_v, end_v))
 
     def get_chunk(self, chunk_idx: int, start_v: int, end_v: int) -> torch.Tensor:
-        slot = chunk_idx % 2
-        if self.slot_chunk[slot] != start_v:
-            self.prefetch_chunk(chunk_idx, start_v, end_v)
-        torch.cuda.current_stream(self.device).wait_event(self.slot_events[slot])
-        return self.gpu_slots[slot][: end_v - start_v]
+        """W[start_v:end_v] on the device, ready for the current stream."""
+        rows, _ = self._ring.take(chunk_idx, (start_v, end_v), self._chunk_copy(start_v, end_v))
+        return rows[: end_v - start_v]
+
+    def get_chunk_t(self, chunk_idx: int, start_v: int, end_v: int) -> torch.Tensor:
+        """W[start_v:end_v]^T [hidden, round_up(rows, 64)] (zero padding columns), formed on the
+        current stream from the chunk's rows (which must be in the slot: ``get_chunk`` first)."""
+        s = self._ring.slot(chunk_idx)
+        if not self._ring.holds(chunk_idx, (start_v, end_v)):
+            raise RuntimeError("get_chunk_t: the chunk is not in its slot")
+        rows, rows_t = self._ring.slots[s]
+        n = end_v - start_v
+        K.transpose_rows(rows[:n], rows_t)
+        return rows_t
 
     def release_chunk(self, chunk_idx: int) -> None:
-        self.compute_done_events[chunk_idx % 2].record(torch.cuda.current_stream(self.device))
+        """Every read of chunk ``chunk_idx``'s slot is enqueued on the current stream."""
+        self._ring.give_back(chunk_idx)
 
 
 class InputStream:
-    """Per-layer inputs kept for the backward recompute (solution/hostload.py:411-488)."""
+    """Per-layer inputs kept for the backward recompute (solution/hostload.py:411-488).
+
+    In HBM by default. With ``offload=True`` every layer but the last two goes to pinned host
+    memory on the ring's copy stream (after the producing stream's work), and ``prefetch`` /
+    ``load`` bring it back through a two-slot ring one layer ahead; a layer's host copy and its
+    return trip run on the same copy stream, so the return waits for the copy by stream order."""
 
     def __init__(self, num_layers: int, hidden_size: int, max_tokens: int, device,
                  offload: bool = False):
@@ -429,60 +540,60 @@ class InputStream:
         self.offload = offload
         self.gpu_saved: dict[int, torch.Tensor] = {}
         if offload:
-            self.stream = torch.cuda.Stream(device=self.device)
-            self.d2h_events = [torch.cuda.Event() for _ in range(num_layers)]
-            self.h2d_events = [torch.cuda.Event() for _ in range(2)]
-            self.slot_ready_events = [torch.cuda.Event() for _ in range(2)]
-            self.slot_layer = [-1, -1]
             self._alloc(max_tokens)
 
     def _alloc(self, n: int) -> None:
         self.max_tokens = n
         self.cpu_buffers = [torch.empty((n, self.hidden_size), dtype=torch.float16, pin_memory=True)
                             for _ in range(self.num_layers)]
-        self.gpu_slots = [torch.empty((n, self.hidden_size), dtype=torch.float16, device=self.device)
-                          for _ in range(2)]
+        self._ring = SlotRing(self.device, [
+            torch.empty((n, self.hidden_size), dtype=torch.float16, device=self.device)
+            for _ in range(2)])
+        self._saved_n = [0] * self.num_layers
+
+    def _on_host(self, layer_idx: int) -> bool:
+        return self.offload and layer_idx < self.num_layers - 2
 
     def save(self, layer_idx: int, x: torch.Tensor) -> None:
-        if not self.offload or layer_idx >= self.num_layers - 2:
-            self.gpu_saved[layer_idx] = x.detach()  # the stack never modifies a layer input
+        """Keeps layer ``layer_idx``'s input (the stack never modifies it afterwards)."""
+        if not self._on_host(layer_idx):
+            self.gpu_saved[layer_idx] = x.detach()
             return
         n = x.shape[0]
         if n > self.max_tokens:
             torch.cuda.current_stream(self.device).synchronize()
+            self._ring.copy_stream.synchronize()
             self._alloc(max(n, 2 * self.max_tokens))
-            self.slot_layer = [-1, -1]
-        ev = torch.cuda.Event()
-        ev.record(torch.cuda.current_stream(self.device))
-        with torch.cuda.stream(self.stream):
-            self.stream.wait_event(ev)
+        cur = torch.cuda.current_stream(self.device)
+        cs = self._ring.copy_stream
+        cs.wait_stream(cur)
+        with torch.cuda.stream(cs):
             self.cpu_buffers[layer_idx][:n].copy_(x.detach(), non_blocking=True)
-            self.d2h_events[layer_idx].record(self.stream)
+        x.record_stream(cs)
+        self._saved_n[layer_idx] = n
+
+    def _copy_back(self, layer_idx: int, n: int):
+        src = self.cpu_buffers[layer_idx][:n]
+
+        def copy(slot: torch.Tensor) -> None:
+            slot[:n].copy_(src, non_blocking=True)
+
+        return copy
 
     def prefetch(self, layer_idx: int, n_tokens: int) -> None:
-        if not self.offload or layer_idx < 0 or layer_idx in self.gpu_saved:
+        """Starts bringing layer ``layer_idx``'s input back into its slot."""
+        if not self._on_host(layer_idx) or layer_idx < 0:
             return
-        slot = layer_idx % 2
-        if self.slot_layer[slot] == layer_idx:
-            return
-        with torch.cuda.stream(self.stream):
-            self.stream.wait_event(self.d2h_events[layer_idx])
-            self.stream.wait_event(self.slot_ready_events[slot])
-            self.gpu_slots[slot][:n_tokens].copy_(self.cpu_buffers[layer_idx][:n_tokens], non_blocking=True)
-            self.h2d_events[slot].record(self.stream)
-            self.slot_layer[slot] = layer_idx
+        self._ring.fill(layer_idx, layer_idx, self._copy_back(layer_idx, n_tokens))
 
     def load(self, layer_idx: int, n_tokens: int) -> torch.Tensor:
+        """Layer ``layer_idx``'s input [n_tokens, hidden], ready for the current stream."""
         if layer_idx in self.gpu_saved:
             return self.gpu_saved.pop(layer_idx)
-        slot = layer_idx % 2
-        if self.slot_layer[slot] != layer_idx:
-            self.prefetch(layer_idx, n_tokens)
-        torch.cuda.current_stream(self.device).wait_event(self.h2d_events[slot])
-        return self.gpu_slots[slot][:n_tokens]
+        slot = self._ring.take(layer_idx, layer_idx, self._copy_back(layer_idx, n_tokens))
+        return slot[:n_tokens]
 
     def release(self, layer_idx: int) -> None:
-        if self.offload and layer_idx < self.num_layers - 2:
-            slot = layer_idx % 2
-            self.slot_ready_events[slot].record(torch.cuda.current_stream(self.device))
-            self.slot_layer[slot] = -1
+        """The current stream's reads of layer ``layer_idx``'s input are enqueued."""
+        if self._on_host(layer_idx):
+            self._ring.give_back(layer_idx, forget=True)

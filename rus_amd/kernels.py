@@ -28,6 +28,7 @@ __all__ = [
     "rms_norm_bwd",
     "DeferredNorm",
     "copy_from_host",
+    "gather_rows_from_host",
     "rms_norm_bwd_parts",
     "qkv_rope_fwd",
     "qkv_rope_bwd",
@@ -46,6 +47,13 @@ __all__ = [
     "mlp_glu_bwd",
     "lm_head_ce",
     "lm_head_ce_loss",
+    "lm_head_ce_chunk_scale",
+    "lm_head_ce_grad_hidden_scaled",
+    "lm_head_ce_dh_finish",
+    "lm_head_chunk_cols",
+    "lm_head_token_blocks",
+    "lm_head_ce_denom",
+    "LMHeadPass",
     "lm_head_ce_fwd_chunk",
     "lm_head_ce_combine",
     "lm_head_ce_grad_logits",
@@ -53,6 +61,7 @@ __all__ = [
     "lm_head_ce_grad_hidden",
     "lm_head_dh_reduce",
     "lm_head_weight_t",
+    "transpose_rows",
     "attn_varlen_fwd",
     "attn_varlen_bwd",
 ]
@@ -430,6 +439,33 @@ def copy_from_host(dst: torch.Tensor, host_src: torch.Tensor) -> None:
         raise ValueError(f"{fn}: contiguous tensors of equal byte size required")
     _launch("copy_from_host", 2 * nb, 0, "rus_copy_from_host", dst.data_ptr(),
             host_src.data_ptr(), nb, _stream(dst))
+
+
+def gather_rows_from_host(host_rows: torch.Tensor, ids: torch.Tensor,
+                          err_flag: torch.Tensor | None = None) -> torch.Tensor:
+    """host_rows[ids] as a new device tensor, where host_rows is a pinned 2-D CPU tensor and ids
+    an int64 device tensor: a kernel on the current stream reads the selected rows over the bus
+    (no host synchronisation). Ids out of range give zero rows and set ``err_flag`` (a device
+    int32 tensor) when one is passed."""
+    fn = "gather_rows_from_host"
+    _require_device(fn, ids, err_flag)
+    if host_rows.device.type != "cpu" or not host_rows.is_pinned() or host_rows.dim() != 2 \
+            or not host_rows.is_contiguous():
+        raise ValueError(f"{fn}: the source must be a contiguous pinned 2-D CPU tensor")
+    row_bytes = host_rows.shape[1] * host_rows.element_size()
+    if row_bytes % 16:
+        raise ValueError(f"{fn}: rows must be a multiple of 16 bytes")
+    flat = ids.reshape(-1)
+    if flat.dtype != torch.int64:
+        raise TypeError(f"{fn}: ids must be int64")
+    flat = flat.contiguous()
+    out = torch.empty((flat.numel(), host_rows.shape[1]), dtype=host_rows.dtype, device=ids.device)
+    if err_flag is not None and (err_flag.dtype != torch.int32 or err_flag.numel() < 1):
+        raise ValueError(f"{fn}: err_flag must be a device int32 tensor")
+    _launch("gather_rows_from_host", 2 * out.numel() * out.element_size() + 8 * flat.numel(), 0,
+            "rus_gather_rows_from_host", host_rows.data_ptr(), host_rows.shape[0], row_bytes,
+            flat.data_ptr(), flat.numel(), out.data_ptr(), _ptr(err_flag), _stream(out))
+    return out
 
 
 class DeferredNorm:
@@ -1182,6 +1218,29 @@ def lm_head_num_parts(vocab_size: int) -> int:
     return (vocab_size + LM_TILE - 1) // LM_TILE
 
 
+_CU_COUNT: dict = {}
+
+
+def cu_count(device=None) -> int:
+    """Compute units of ``device`` (256 on MI355X; also the value used without a GPU)."""
+    if device is None or not torch.cuda.is_available():
+        return 256
+    dev = torch.device(device)
+    if dev.type != "cuda":
+        return 256
+    idx = dev.index if dev.index is not None else torch.cuda.current_device()
+    if idx not in _CU_COUNT:
+        _CU_COUNT[idx] = int(torch.cuda.get_device_properties(idx).multi_processor_count)
+    return _CU_COUNT[idx]
+
+
+def _round_fill(blocks: int, n_cu: int) -> float:
+    """Share of the CU slots used by a grid of ``blocks`` one-per-CU workgroups, with the grid
+    rounded up to a multiple of 8 as the GEMM launches do (whole rounds of n_cu blocks)."""
+    launched = -(-blocks // 8) * 8
+    return blocks / (n_cu * -(-launched // n_cu))
+
+
 def lm_head_split_count(n_tok: int, d: int, n_vocab: int, n_cu: int = 256,
                         max_split: int = 64) -> int:
     """Split-K count for the hidden-gradient GEMM. One of its workgroups fills a CU (128 KiB of
@@ -1197,12 +1256,36 @@ def lm_head_split_count(n_tok: int, d: int, n_vocab: int, n_cu: int = 256,
     for want in range(1, max(1, min(64, max_split, kpad // LM_K)) + 1):
         per = _round_up(-(-kpad // want), LM_K)
         n_split = -(-kpad // per)
-        blocks = tiles * n_split
-        fill = blocks / (n_cu * -(-blocks // n_cu))
-        key = (fill, -n_split)
+        key = (_round_fill(tiles * n_split, n_cu), -n_split)
         if best_key is None or key > best_key:
             best, best_key = n_split, key
     return best
+
+
+LM_CHUNK_BUDGET = 64 << 20  # bytes of fp16 logits one chunk of the single-pass head may hold
+
+
+def lm_head_chunk_cols(n_tok: int, n_vocab: int, n_cu: int = 256,
+                       budget: int = LM_CHUNK_BUDGET) -> int:
+    """Vocabulary rows per chunk of the single-pass head: a multiple of 256 whose fp16 logits
+    [n_tok, cols] fit ``budget``, chosen to minimise an estimate of the statistics GEMM time
+    (whole rounds of one-per-CU 256x256 tiles, ~50 us each) plus a per-chunk cost for the three
+    launches of a chunk (~15 us)."""
+    tiles_v = -(-n_vocab // LM_TILE)
+    if tiles_v <= 1 or n_tok <= 0:
+        return max(LM_TILE, tiles_v * LM_TILE)
+    tt = -(-n_tok // 256)
+    cap = max(1, min(tiles_v, budget // (2 * LM_TILE * n_tok)))
+    best, best_cost = 1, None
+    for k in range(1, cap + 1):
+        full, rest = divmod(tiles_v, k)
+        rounds = full * -(-(-(-k * tt // 8) * 8) // n_cu)
+        if rest:
+            rounds += -(-(-(-rest * tt // 8) * 8) // n_cu)
+        cost = 50.0 * rounds + 15.0 * (full + (1 if rest else 0))
+        if best_cost is None or cost < best_cost or (cost == best_cost and k > best):
+            best, best_cost = k, cost
+    return best * LM_TILE
 
 
 class LMHeadPartials:
@@ -1362,16 +1445,21 @@ def lm_head_ce_grad_hidden(grad_logits: torch.Tensor, weight_t_cols: torch.Tenso
 
 def lm_head_dh_reduce(parts: torch.Tensor, scale: float, out_dtype=torch.float16,
                       scale_dev: torch.Tensor | None = None,
-                      _tag: str = "lmhead_dh_reduce") -> torch.Tensor:
+                      _tag: str = "lmhead_dh_reduce", out: torch.Tensor | None = None) -> torch.Tensor:
     """out = out_dtype(scale * scale_dev * sum over the leading split dimension of ``parts``);
-    ``scale_dev`` is an optional one-element float32 device tensor (read on the device)."""
+    ``scale_dev`` is an optional one-element float32 device tensor (read on the device); ``out``
+    (contiguous, ``parts.shape[1:]``, 16-byte aligned) receives the result when given."""
     fn = "lm_head_dh_reduce"
-    _require_device(fn, parts, scale_dev)
+    _require_device(fn, parts, scale_dev, out)
     if parts.dtype != torch.float32 or not parts.is_contiguous():
         raise ValueError(f"{fn}: parts must be contiguous float32")
     if scale_dev is not None and (scale_dev.dtype != torch.float32 or scale_dev.numel() != 1):
         raise ValueError(f"{fn}: scale_dev must be a one-element float32 tensor")
-    out = torch.empty(parts.shape[1:], dtype=out_dtype, device=parts.device)
+    if out is None:
+        out = torch.empty(parts.shape[1:], dtype=out_dtype, device=parts.device)
+    elif out.shape != parts.shape[1:] or not out.is_contiguous():
+        raise ValueError(f"{fn}: out must be contiguous {tuple(parts.shape[1:])}")
+    out_dtype = out.dtype
     _launch(_tag, parts.numel() * 4 + out.numel() * out.element_size(), 0,
             "rus_lmhead_dh_reduce", parts.data_ptr(), parts.shape[0], out.numel(), float(scale),
               _ptr(scale_dev), out.data_ptr(), _dtype_code(fn, out_dtype), _stream(parts))
@@ -1469,6 +1557,23 @@ def attn_varlen_bwd(dout: torch.Tensor, q: torch.Tensor, k: torch.Tensor, v: tor
     return dq, dk, dv
 
 
+def transpose_rows(rows: torch.Tensor, out: torch.Tensor) -> torch.Tensor:
+    """out[:, :n] = rows^T and out[:, n:] = 0 for fp16 rows [n, d] and out [d, >= n] (both with
+    contiguous rows): the K-contiguous W^T operand of the hidden-gradient GEMM, on the device."""
+    fn = "transpose_rows"
+    _require_device(fn, rows, out)
+    if rows.dtype != torch.float16 or out.dtype != torch.float16 or rows.dim() != 2 \
+            or out.dim() != 2 or rows.stride(1) != 1 or out.stride(1) != 1:
+        raise ValueError(f"{fn}: fp16 2-D tensors with contiguous rows expected")
+    n, d = rows.shape
+    if out.shape[0] != d or out.shape[1] < n:
+        raise ValueError(f"{fn}: out must be [{d}, >= {n}]")
+    _launch("transpose_f16", 2 * (n * d + out.shape[0] * out.shape[1]), 0, "rus_transpose_f16",
+            rows.data_ptr(), n, d, rows.stride(0), out.data_ptr(), out.stride(0), out.shape[1],
+            _stream(rows))
+    return out
+
+
 def lm_head_weight_t(weight: torch.Tensor) -> torch.Tensor:
     """W^T [d, round_up(V, 64)] fp16 with zero padding columns, cached on the weight tensor (the
     lm_head is frozen in QLoRA, so this is built once; rebuilt if the weight is modified)."""
@@ -1476,8 +1581,8 @@ def lm_head_weight_t(weight: torch.Tensor) -> torch.Tensor:
     if hit is not None and hit[0] == weight._version and hit[1].device == weight.device:
         return hit[1]
     V, d = weight.shape
-    wt = torch.zeros((d, _round_up(V, LM_K)), dtype=torch.float16, device=weight.device)
-    wt[:, :V].copy_(weight.detach().t())
+    wt = torch.empty((d, _round_up(V, LM_K)), dtype=torch.float16, device=weight.device)
+    transpose_rows(weight.detach(), wt)
     weight._rus_weight_t = (weight._version, wt)
     return wt
 
@@ -1503,17 +1608,232 @@ def lm_head_ce_loss(nll: torch.Tensor, labels: torch.Tensor, num_items_in_batch=
     return out[0:1], out[1:2]
 
 
+def lm_head_ce_chunk_scale(logits: torch.Tensor, n_vocab: int, parts: LMHeadPartials,
+                           part_base: int, m_run: torch.Tensor, alpha: torch.Tensor,
+                           first: bool) -> torch.Tensor:
+    """In place over one chunk's kept fp16 logits [n_tok, >= round_up(n_vocab, 64)]: P =
+    fp16(e^{z - M}) with M = max(running max, the chunk's max from partial rows part_base ...);
+    updates ``m_run`` and writes ``alpha`` = e^{M_old - M} (replaces the logit recompute and
+    lm_head_piece_kernel MODE 1, kernels.py:517-531)."""
+    fn = "lm_head_ce_chunk_scale"
+    _require_device(fn, logits, m_run, alpha)
+    n_tok = logits.shape[0]
+    kp = _round_up(n_vocab, LM_K)
+    if logits.dtype != torch.float16 or logits.dim() != 2 or logits.shape[1] < kp \
+            or logits.stride(1) != 1:
+        raise ValueError(f"{fn}: logits must be fp16 [n_tok, >= {kp}] with contiguous rows")
+    for name, t in (("m_run", m_run), ("alpha", alpha)):
+        if t.dtype != torch.float32 or t.numel() < n_tok or not t.is_contiguous():
+            raise ValueError(f"{fn}: {name} must be contiguous float32 with {n_tok} entries")
+    if part_base < 0 or part_base + lm_head_num_parts(n_vocab) > parts.n_parts \
+            or parts.n_tok != n_tok:
+        raise ValueError(f"{fn}: partial rows out of range")
+    _launch("lmhead_ce_chunk_scale", 2 * n_tok * kp * 2 + 4 * n_tok * lm_head_num_parts(n_vocab),
+            0, "rus_lmhead_ce_chunk_scale", logits.data_ptr(), logits.stride(0), n_tok, n_vocab,
+            parts.m.data_ptr(), parts.m.stride(0), part_base, m_run.data_ptr(), alpha.data_ptr(),
+            1 if first else 0, _stream(logits))
+    return logits
+
+
+def lm_head_ce_grad_hidden_scaled(probs: torch.Tensor, weight_t_cols: torch.Tensor, n_vocab: int,
+                                  parts: torch.Tensor, accumulate: bool,
+                                  alpha: torch.Tensor) -> None:
+    """parts[s] = parts[s] * alpha[row] + (P . W_chunk)[split s] (or = without ``accumulate``):
+    the hidden-gradient GEMM of one chunk of the single-pass head (replaces the per-chunk
+    ``addmm_`` of ops.py:320). Every split of ``parts`` is written, empty ones only rescaled."""
+    fn = "lm_head_ce_grad_hidden_scaled"
+    _require_device(fn, probs, weight_t_cols, parts, alpha)
+    n_tok = probs.shape[0]
+    d = weight_t_cols.shape[0]
+    n_split = parts.shape[0]
+    if parts.dtype != torch.float32 or tuple(parts.shape[1:]) != (n_tok, d) or not parts.is_contiguous():
+        raise ValueError(f"{fn}: parts must be contiguous float32 [n_split, {n_tok}, {d}]")
+    if alpha.dtype != torch.float32 or alpha.numel() < n_tok:
+        raise ValueError(f"{fn}: alpha must be float32 with {n_tok} entries")
+    for name, t in (("probs", probs), ("weight_t", weight_t_cols)):
+        if t.dtype != torch.float16 or t.stride(1) != 1:
+            raise ValueError(f"{fn}: {name} must be fp16 with contiguous rows")
+        if t.shape[0] * t.stride(0) * 2 >= 1 << 32:
+            raise ValueError(f"{fn}: {name} exceeds the 4 GiB operand limit of the MFMA kernels")
+    kp = _round_up(n_vocab, LM_K)
+    _launch("lmhead_ce_grad_hidden", (n_tok + d) * kp * 2 + 4 * n_split * n_tok * d * (2 if accumulate else 1),
+            2.0 * n_tok * d * n_vocab, "rus_lmhead_ce_grad_hidden_scaled", probs.data_ptr(),
+            probs.stride(0), weight_t_cols.data_ptr(), weight_t_cols.stride(0), n_tok, d,
+            n_vocab, parts.data_ptr(), n_split, 1 if accumulate else 0, alpha.data_ptr(),
+            _stream(probs))
+
+
+def lm_head_ce_dh_finish(parts: torch.Tensor, m_run: torch.Tensor, lse: torch.Tensor,
+                         labels: torch.Tensor, w_rows: torch.Tensor, denom: torch.Tensor,
+                         scale: float = 1.0, scale_dev: torch.Tensor | None = None,
+                         out_dtype=torch.float32) -> torch.Tensor:
+    """Hidden gradient (x 2^16 / denom x scale) of the single-pass head: (sum_s parts[s] *
+    e^{m_run - lse} - W[y]) per labelled token, 0 for label -100. ``w_rows`` is the lm_head
+    weight [V, d] on the device or pinned on the host (its label rows are then read over the
+    bus)."""
+    fn = "lm_head_ce_dh_finish"
+    _require_device(fn, parts, m_run, lse, labels, denom, scale_dev)
+    n_split, n_tok, d = parts.shape
+    if parts.dtype != torch.float32 or not parts.is_contiguous():
+        raise ValueError(f"{fn}: parts must be contiguous float32")
+    on_host = w_rows.device.type == "cpu"
+    if on_host and not w_rows.is_pinned():
+        raise ValueError(f"{fn}: a host weight must be pinned")
+    if not on_host:
+        _require_device(fn, w_rows)
+    if w_rows.dtype != torch.float16 or w_rows.dim() != 2 or w_rows.shape[1] != d \
+            or w_rows.stride(1) != 1:
+        raise ValueError(f"{fn}: w_rows must be fp16 [V, {d}] with contiguous rows")
+    lab = labels.reshape(-1)
+    if lab.dtype != torch.int64 or lab.numel() != n_tok:
+        raise ValueError(f"{fn}: labels must be int64 with {n_tok} entries")
+    out = torch.empty((n_tok, d), dtype=out_dtype, device=parts.device)
+    _launch("lmhead_ce_dh_finish", parts.numel() * 4 + out.numel() * out.element_size(), 0,
+            "rus_lmhead_ce_dh_finish", parts.data_ptr(), n_split, n_tok, d, m_run.data_ptr(),
+            lse.data_ptr(), lab.contiguous().data_ptr(), w_rows.data_ptr(), w_rows.stride(0),
+            w_rows.shape[0], 1 if on_host else 0, denom.data_ptr(), float(scale),
+            _ptr(scale_dev), out.data_ptr(), _dtype_code(fn, out_dtype), _stream(parts))
+    return out
+
+
+class LMHeadPass:
+    """One single pass of the lm_head cross-entropy over vocabulary chunks (in order).
+
+    Per chunk: the statistics GEMM (partial m, s, w, argmax and the target logit per 256 rows)
+    and, when the hidden gradient is wanted, its fp16 logits kept in a [n_tok, chunk] buffer,
+    turned in place into P = e^{z - M} (M the running maximum) and accumulated as P . W_chunk into
+    fp32 split-K partials rescaled whenever M grows. ``finish`` combines the statistics (lse,
+    nll, entropy, argmax, loss) and forms dH = sum_v (softmax - onehot) W_v x 2^16 / denom. W is
+    read once, and no [n_tok, V] array exists (the reference reads W twice and recomputes the
+    logits, solution/ops.py:217-322)."""
+
+    def __init__(self, n_tok: int, d: int, n_vocab: int, chunk: int, device, need_grad: bool):
+        self.n_tok, self.d, self.n_vocab, self.chunk = n_tok, d, n_vocab, int(chunk)
+        self.need_grad = need_grad
+        self.parts = LMHeadPartials(lm_head_num_parts(n_vocab), n_tok, device)
+        self.target = torch.zeros(n_tok, dtype=torch.float32, device=device)
+        self.first = True
+        if need_grad:
+            self.z = torch.empty((n_tok, _round_up(min(self.chunk, n_vocab), LM_K)),
+                                 dtype=torch.float16, device=device)
+            self.m_run = torch.empty(n_tok, dtype=torch.float32, device=device)
+            self.alpha = torch.empty(n_tok, dtype=torch.float32, device=device)
+            self.n_split = lm_head_split_count(n_tok, d, min(self.chunk, n_vocab), cu_count(device))
+            self.dparts = torch.empty((self.n_split, n_tok, d), dtype=torch.float32, device=device)
+
+    def add_chunk(self, hidden: torch.Tensor, w_rows: torch.Tensor, w_t: torch.Tensor | None,
+                  start: int, labels: torch.Tensor) -> None:
+        """Vocabulary rows [start, start + len(w_rows)) with their transpose ``w_t`` [d, >= rows]
+        (needed with the gradient only)."""
+        n = w_rows.shape[0]
+        if not self.need_grad:
+            lm_head_ce_fwd_chunk(hidden, w_rows, labels, start, self.parts, self.target)
+            return
+        lm_head_ce_fwd_chunk(hidden, w_rows, labels, start, self.parts, self.target,
+                             logits_out=self.z)
+        lm_head_ce_chunk_scale(self.z, n, self.parts, start // LM_TILE, self.m_run, self.alpha,
+                               self.first)
+        lm_head_ce_grad_hidden_scaled(self.z, w_t, n, self.dparts, not self.first, self.alpha)
+        self.first = False
+
+    def finish(self, labels: torch.Tensor, num_items_in_batch, w_rows_all: torch.Tensor,
+               dh_scale: float = 1.0, dh_dtype=torch.float32, scale_dev=None):
+        """(nll, lse, entropy, argmax, denom, dh, loss); dh None without the gradient."""
+        lse, nll, ent, amax = lm_head_ce_combine(self.parts, self.target, labels)
+        loss, denom = lm_head_ce_loss(nll, labels, num_items_in_batch)
+        dh = None
+        if self.need_grad:
+            dh = lm_head_ce_dh_finish(self.dparts, self.m_run, lse, labels, w_rows_all, denom,
+                                      dh_scale, scale_dev, dh_dtype)
+        return nll, lse, ent, amax, denom, dh, loss
+
+
+def lm_head_ce_denom(labels: torch.Tensor, num_items_in_batch=None) -> torch.Tensor:
+    """The loss denominator alone, as a one-element float32 device tensor (what ``lm_head_ce_loss``
+    will use): max(num_items_in_batch, 1) if given, else max(#(labels != -100), 1)."""
+    fn = "lm_head_ce_denom"
+    _require_device(fn, labels)
+    dev = labels.device
+    lab = labels.reshape(-1)
+    if lab.dtype != torch.int64:
+        raise ValueError(f"{fn}: labels must be int64")
+    ni = None
+    if isinstance(num_items_in_batch, torch.Tensor):
+        ni = num_items_in_batch.detach().to(device=dev, dtype=torch.float32).reshape(1)
+    elif num_items_in_batch is not None:
+        ni = torch.full((1,), float(num_items_in_batch), dtype=torch.float32, device=dev)
+    denom = torch.empty(1, dtype=torch.float32, device=dev)
+    _launch("lmhead_ce_loss", lab.numel() * 8, 0, "rus_lmhead_ce_loss", None,
+            lab.contiguous().data_ptr(), lab.numel(), _ptr(ni), None, denom.data_ptr(),
+            _stream(lab))
+    return denom
+
+
+def lm_head_token_blocks(n_tok: int, max_block: int = LM_TILE) -> list[tuple[int, int]]:
+    """Token ranges [t0, t1) of at most ``max_block`` tokens, balanced (sizes differ by <= 1)."""
+    if n_tok <= 0:
+        return []
+    nb = -(-n_tok // max_block)
+    base, extra = divmod(n_tok, nb)
+    out, t = [], 0
+    for b in range(nb):
+        n = base + (1 if b < extra else 0)
+        out.append((t, t + n))
+        t += n
+    return out
+
+
+def _fwd_rows(hidden, weight, labels, parts: LMHeadPartials, target, t0: int, t1: int,
+              logits: torch.Tensor | None) -> None:
+    """Statistics (and kept logits) of tokens [t0, t1) over the whole vocabulary: the token
+    columns t0 .. of the partial arrays."""
+    n, d = t1 - t0, hidden.shape[1]
+    V = weight.shape[0]
+    h = hidden[t0:t1]
+    args = (h.data_ptr(), weight.data_ptr(), labels.data_ptr() + 8 * t0, n, d, h.stride(0),
+            weight.stride(0), V, 0, parts.m.data_ptr() + 4 * t0, parts.s.data_ptr() + 4 * t0,
+            parts.w.data_ptr() + 4 * t0, parts.idx.data_ptr() + 4 * t0, 0, parts.n_tok,
+            target.data_ptr() + 4 * t0)
+    nbytes = (n + V) * d * 2 + 16 * n * parts.n_parts
+    if logits is None:
+        _launch("lmhead_ce_fwd", nbytes, 2.0 * n * d * V, "rus_lmhead_ce_fwd", *args, _stream(h))
+    else:
+        _launch("lmhead_ce_fwd_keep", nbytes + n * logits.shape[1] * 2, 2.0 * n * d * V,
+                "rus_lmhead_ce_fwd_keep", *args, logits.data_ptr(), logits.stride(0), _stream(h))
+
+
+def _combine_rows(parts: LMHeadPartials, target, labels, t0: int, t1: int, lse, nll, ent,
+                  amax) -> None:
+    n = t1 - t0
+    _launch("lmhead_ce_combine", 16 * n * parts.n_parts + 32 * n, 0, "rus_lmhead_ce_combine",
+            parts.m.data_ptr() + 4 * t0, parts.s.data_ptr() + 4 * t0,
+            parts.w.data_ptr() + 4 * t0, parts.idx.data_ptr() + 4 * t0, parts.n_parts,
+            parts.n_tok, target.data_ptr() + 4 * t0, labels.data_ptr() + 8 * t0, n,
+            lse.data_ptr() + 4 * t0, nll.data_ptr() + 4 * t0, ent.data_ptr() + 4 * t0,
+            amax.data_ptr() + 8 * t0, _stream(lse))
+
+
 def lm_head_ce(hidden: torch.Tensor, weight: torch.Tensor, labels: torch.Tensor,
                num_items_in_batch=None, v_chunk: int | None = None, need_grad: bool = True,
                weight_t: torch.Tensor | None = None, dh_scale: float = 1.0,
                dh_dtype: torch.dtype = torch.float32):
-    """Whole vocab-tiled CE on a device-resident fp16 lm_head weight [V, d].
+    """Whole cross-entropy head on a device-resident fp16 lm_head weight [V, d].
 
     Returns (nll, lse, entropy, argmax, denom, dh, loss) where denom is a float32 device scalar
     (num_items_in_batch, else the count of labels != -100, clamped to >= 1), loss = sum(nll) /
     denom (device scalar) and dh the hidden gradient of loss times 2^16, scaled by ``dh_scale``
-    and stored as ``dh_dtype`` (None without need_grad). ``v_chunk`` bounds the fp16
-    logit-gradient buffer to [n_tok, v_chunk] (default: the whole vocabulary in one pass).
+    and stored as ``dh_dtype`` (None without need_grad).
+
+    With the gradient, the tokens go in blocks of at most 256 (one MFMA token tile). For each
+    block one statistics GEMM over the whole vocabulary keeps its fp16 logits in a [256, V]
+    buffer; the block's statistics are combined; its logits become the reference's fp16 gradient
+    G = fp16((softmax - onehot) 2^16 / denom) in place (the denominator is known up front); and
+    a split-K GEMM G . W writes the block's dH partials, summed once. W is read once per block;
+    no [N, V] array exists and no logit is recomputed (the reference holds [N, 8192] chunks and
+    recomputes every logit, solution/ops.py:209-322). ``v_chunk`` (a multiple of 256) selects
+    the single pass over vocabulary chunks instead (``LMHeadPass``: W read once in total, an
+    [N, v_chunk] buffer), the layout of a head streamed from the host. ``weight_t`` is W^T
+    [d, >= round_up(V, 64)] (built and cached on the weight when not given).
     """
     fn = "lm_head_ce"
     _require_device(fn, hidden, weight, labels)
@@ -1521,37 +1841,59 @@ def lm_head_ce(hidden: torch.Tensor, weight: torch.Tensor, labels: torch.Tensor,
     V = weight.shape[0]
     dev = hidden.device
     lab = labels.reshape(-1).to(torch.int64).contiguous()
-    chunk = V if v_chunk is None else int(v_chunk)
-    if chunk <= 0 or (chunk < V and chunk % LM_TILE):
-        raise ValueError(f"{fn}: v_chunk must be a positive multiple of {LM_TILE}")
-    parts = LMHeadPartials(lm_head_num_parts(V), n_tok, dev)
-    target = torch.zeros(n_tok, dtype=torch.float32, device=dev)
-    # One pass over the whole vocabulary keeps its logits in the gradient buffer, which then
-    # becomes the gradient in place (no second logit GEMM); chunked passes recompute them.
-    keep = need_grad and chunk >= V
-    g = None
-    if need_grad:
-        g = torch.empty((n_tok, _round_up(min(chunk, V), LM_K)), dtype=torch.float16, device=dev)
-    for start in range(0, V, chunk):
-        lm_head_ce_fwd_chunk(hidden, weight[start:start + chunk], lab, start, parts, target,
-                             logits_out=g if keep else None)
-    lse, nll, ent, amax = lm_head_ce_combine(parts, target, lab)
-    loss, denom = lm_head_ce_loss(nll, lab, num_items_in_batch)
-    dh_pre = None
-    if need_grad:
-        wt = weight_t if weight_t is not None else lm_head_weight_t(weight)
-        n_split = lm_head_split_count(n_tok, d, min(chunk, V))
-        dparts = torch.empty((n_split, n_tok, d), dtype=torch.float32, device=dev)
-        first = True
+    h = _lm_operand(fn, hidden, d, "hidden")
+    w = _lm_operand(fn, weight, d, "weight")
+    if lab.numel() != n_tok:
+        raise ValueError(f"{fn}: labels must have {n_tok} entries")
+    if v_chunk is not None:
+        chunk = int(v_chunk)
+        if chunk <= 0 or (chunk < V and chunk % LM_TILE):
+            raise ValueError(f"{fn}: v_chunk must be a positive multiple of {LM_TILE}")
+        wt = None
+        if need_grad:
+            wt = weight_t if weight_t is not None else lm_head_weight_t(weight)
+        hp = LMHeadPass(n_tok, d, V, chunk, dev, need_grad)
         for start in range(0, V, chunk):
             end = min(start + chunk, V)
-            if keep:
-                lm_head_ce_grad_from_logits(g, lab, lse, denom, V)
-            else:
-                lm_head_ce_grad_logits(hidden, weight[start:end], lab, lse, denom, start, g)
-            # A shorter last chunk may use fewer splits; it accumulates into the leading ones.
-            ns = lm_head_split_count(n_tok, d, end - start, max_split=n_split)
-            lm_head_ce_grad_hidden(g, wt[:, start:], end - start, dparts[:ns], accumulate=not first)
-            first = False
-        dh_pre = lm_head_dh_reduce(dparts, dh_scale, dh_dtype)
-    return nll, lse, ent, amax, denom, dh_pre, loss
+            hp.add_chunk(h, w[start:end], None if wt is None else wt[:, start:], start, lab)
+        return hp.finish(lab, num_items_in_batch, w, dh_scale, dh_dtype)
+
+    parts = LMHeadPartials(lm_head_num_parts(V), n_tok, dev)
+    target = torch.zeros(n_tok, dtype=torch.float32, device=dev)
+    if not need_grad or n_tok == 0:
+        if n_tok:
+            _fwd_rows(h, w, lab, parts, target, 0, n_tok, None)
+        lse, nll, ent, amax = lm_head_ce_combine(parts, target, lab)
+        loss, denom = lm_head_ce_loss(nll, lab, num_items_in_batch)
+        dh = torch.zeros((n_tok, d), dtype=dh_dtype, device=dev) if need_grad else None
+        return nll, lse, ent, amax, denom, dh, loss
+    wt = weight_t if weight_t is not None else lm_head_weight_t(weight)
+    kp = _round_up(V, LM_K)
+    if wt.dtype != torch.float16 or wt.shape[0] != d or wt.shape[1] < kp or wt.stride(1) != 1:
+        raise ValueError(f"{fn}: weight_t must be fp16 [{d}, >= {kp}] with contiguous rows")
+    blocks = lm_head_token_blocks(n_tok)
+    nb_max = max(t1 - t0 for t0, t1 in blocks)
+    ncu = cu_count(dev)
+    splits = {nb: lm_head_split_count(nb, d, V, ncu) for nb in {t1 - t0 for t0, t1 in blocks}}
+    z = torch.empty((nb_max, kp), dtype=torch.float16, device=dev)
+    if z.numel() * 2 >= 1 << 32:
+        raise ValueError(f"{fn}: a {nb_max}-token block of logits exceeds the 4 GiB operand limit")
+    dflat = torch.empty(max(splits.values()) * nb_max * d, dtype=torch.float32, device=dev)
+    denom = lm_head_ce_denom(lab, num_items_in_batch)
+    lse = torch.empty(n_tok, dtype=torch.float32, device=dev)
+    nll = torch.empty(n_tok, dtype=torch.float32, device=dev)
+    ent = torch.empty(n_tok, dtype=torch.float32, device=dev)
+    amax = torch.empty(n_tok, dtype=torch.int64, device=dev)
+    dh = torch.empty((n_tok, d), dtype=dh_dtype, device=dev)
+    for t0, t1 in blocks:
+        nb = t1 - t0
+        zb = z[:nb]
+        _fwd_rows(h, w, lab, parts, target, t0, t1, zb)
+        _combine_rows(parts, target, lab, t0, t1, lse, nll, ent, amax)
+        lm_head_ce_grad_from_logits(zb, lab[t0:t1], lse[t0:t1], denom, V)
+        s = splits[nb]
+        dparts = dflat[: s * nb * d].view(s, nb, d)
+        lm_head_ce_grad_hidden(zb, wt, V, dparts, accumulate=False)
+        lm_head_dh_reduce(dparts, dh_scale, dh_dtype, out=dh[t0:t1])
+    loss, _ = lm_head_ce_loss(nll, lab, num_items_in_batch)
+    return nll, lse, ent, amax, denom, dh, loss

@@ -169,7 +169,8 @@ def test_graph_replays_repeatable_across_buckets(unit):
             print("graph nodes", unit, c)
             assert c["memset"] == 0 and c["kernel"] > 50
             if unit == "layer":
-                assert c["memcpy"] >= 3 * cfg.num_hidden_layers  # the layers' H2D copies
+                # each layer's packed image is one H2D copy into its slot, at least once
+                assert c["memcpy"] >= cfg.num_hidden_layers
     # resident and streamed weights give the same bits
     if not resident:
         eng_r = ops.Qwen2FusedEngine(model, DEV, resident_weights=True)

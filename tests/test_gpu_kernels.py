@@ -380,3 +380,31 @@ def test_nf4_dequant_table_and_direct_paths_bit_exact(blocksize, offset_bytes, s
                                super_blocksize=q.super_blocksize)
     torch.cuda.synchronize()
     assert _bits_equal(out, _dequant_ref(q))
+
+
+def test_gather_rows_from_host_and_transpose():
+    # Embedding rows read over the bus by a kernel (ids on the device; no host synchronisation):
+    # exact copies, zero rows and the error flag for ids out of range.
+    g = torch.Generator().manual_seed(11)
+    w = torch.randn(1000, 264, generator=g).half().pin_memory()
+    ids = torch.randint(0, 1000, (77,), generator=g)
+    flag = torch.zeros(1, dtype=torch.int32, device="cuda")
+    out = K.gather_rows_from_host(w, ids.to("cuda"), err_flag=flag)
+    torch.cuda.synchronize()
+    assert torch.equal(out.cpu(), w[ids]) and int(flag.item()) == 0
+    bad = ids.clone()
+    bad[5], bad[9] = -1, 1000
+    out = K.gather_rows_from_host(w, bad.to("cuda"), err_flag=flag)
+    torch.cuda.synchronize()
+    want = w[ids].clone()
+    want[5] = 0
+    want[9] = 0
+    assert torch.equal(out.cpu(), want) and int(flag.item()) == 1
+    # W^T on the device: exact transpose, zero padding columns
+    for n, d in ((1000, 264), (64, 128), (4099, 256)):
+        src = torch.randn(n, d, generator=g).half().cuda()
+        dst = torch.full((d, n + 70), 3.0, dtype=torch.float16, device="cuda")
+        K.transpose_rows(src, dst)
+        torch.cuda.synchronize()
+        assert torch.equal(dst[:, :n].cpu(), src.cpu().t())
+        assert torch.all(dst[:, n:].cpu() == 0)

@@ -183,3 +183,58 @@ def test_kept_logits_gradient_equals_recomputed_gradient(n, d, v, start):
     torch.cuda.synchronize()
     assert torch.equal(z[:, :kp].cpu(), g_ref.cpu())
     assert torch.all(z[:, kp:].cpu() == 7.0)
+
+
+@pytest.mark.parametrize("n,d,v,chunk", [(300, 256, 5000, 1024), (700, 1536, 20000, 8192)])
+def test_single_pass_head_chunking_and_streaming(n, d, v, chunk):
+    # The single-pass head over different vocabulary chunkings: statistics bit-identical (the
+    # per-256-row partials do not depend on the chunking), hidden gradient within rtol 1e-2 of the
+    # oracle. A HostHead streamed from pinned host memory with the same chunk gives the resident
+    # head's bits, including the gradient; back-to-back calls without the gradient (which leave a
+    # streamed slot's last reader to the next call's prefetch) and with it, on fresh inputs.
+    from rus_amd import ops
+    from rus_amd.hostload import HostHead
+
+    g = torch.Generator().manual_seed(n + v)
+    w = (torch.randn(v, d, generator=g) * 0.03).half()
+    lab = torch.randint(0, v, (n,), generator=g)
+    lab[torch.rand(n, generator=g) < 0.1] = -100
+    lab[0] = v - 1  # a label in the last (partial) chunk
+    labd = lab.to(DEV)
+    streamed = HostHead(w, DEV, v_chunk=chunk, resident=False)
+    resident = HostHead(w, DEV, v_chunk=chunk, resident=True)
+    for step, need_grad in enumerate((False, False, True, True, False)):
+        h = torch.randn(n, d, generator=g).half()
+        outs = []
+        for head in (streamed, resident):
+            hd = h.to(DEV).requires_grad_(need_grad)
+            with torch.set_grad_enabled(need_grad):
+                loss, nll, ent, amax = ops.chunked_lm_head(hd, labd, head, v_chunk=chunk)
+            if need_grad:
+                loss.backward()
+            torch.cuda.synchronize()
+            outs.append((loss.detach().cpu(), nll.cpu(), ent.cpu(), amax.cpu(),
+                         hd.grad.cpu() if need_grad else None))
+        for a, b in zip(outs[0][:4], outs[1][:4]):
+            assert torch.equal(a, b), step
+        if need_grad:
+            assert torch.equal(outs[0][4], outs[1][4]), step
+    # the last gradient against the oracle; other chunkings agree on the statistics bitwise
+    out = K.lm_head_ce(h.to(DEV), w.to(DEV), labd, v_chunk=chunk)
+    auto = K.lm_head_ce(h.to(DEV), w.to(DEV), labd)
+    torch.cuda.synchronize()
+    for i in (0, 1, 2, 3, 6):
+        assert torch.equal(out[i].cpu(), auto[i].cpu()), i
+    rows = torch.arange(0, min(n, 40))
+    _check_against_oracle(h, w, lab, out, rows=rows, denom=float(out[4].item()))
+    _check_against_oracle(h, w, lab, auto, rows=rows, denom=float(auto[4].item()))
+
+
+def test_chunk_choice_bounds_the_logit_buffer():
+    # The default chunk keeps the per-chunk fp16 logits within the 64 MiB budget at any token
+    # count (the [N, V] logits are never held), and covers a small vocabulary in one chunk.
+    for n in (1, 707, 2048, 8192, 65536):
+        c = K.lm_head_chunk_cols(n, 151936)
+        assert c % 256 == 0 and c >= 256
+        assert n * c * 2 <= max(K.LM_CHUNK_BUDGET, n * 256 * 2)
+    assert K.lm_head_chunk_cols(64, 4099) >= 4099

@@ -3,7 +3,8 @@
 * Against the CPU oracle (oracle/stack.py, pinned to transformers' Qwen2ForCausalLM) on a small
   model with dropout off: loss within 2e-3 relative, every LoRA gradient tensor within 1e-2 in
   relative Frobenius norm (||g - g_ref|| <= 1e-2 ||g_ref||; fp16 activations against fp32).
-* Streamed (pinned host, two slots) and HBM-resident weights give bit-identical results.
+* Streamed (pinned host, two slots) and HBM-resident weights give bit-identical results, and so
+  do the host-streamed lm_head / embedding and the host-offloaded layer inputs.
 * With dropout on, the fused stack (forward masks re-drawn in the backward recompute) matches a
   plain autograd eager step using the same counter-based masks (rus_amd.eager_reference) and the
   CPU oracle given the oracle's own Philox masks: same tolerances.
@@ -58,13 +59,15 @@ def _rel(a, b):
     return float((a.float() - b.float()).norm() / (b.float().norm() + 1e-30))
 
 
-@pytest.mark.parametrize("resident,attention", [(False, "varlen"), (True, "varlen"),
-                                                (True, "varlen_aten"),
-                                                (True, "sdpa_rows")])
-def test_fused_stack_matches_cpu_oracle(resident, attention):
+@pytest.mark.parametrize("resident,head,offload", [(False, True, False), (True, True, False),
+                                                 (False, False, True), (True, False, False)])
+def test_fused_stack_matches_cpu_oracle(resident, head, offload):
+    # head=False: the lm_head / embedding streamed from pinned host memory (HostHead); offload:
+    # layer inputs kept in pinned host memory for the backward recompute (InputStream).
     cfg = small_config()
     model = M.build_random_qlora_qwen2(cfg, DEV, seed=1, std=0.05)
-    engine = ops.Qwen2FusedEngine(model, DEV, resident_weights=resident, attention=attention)
+    engine = ops.Qwen2FusedEngine(model, DEV, resident_weights=resident, resident_head=head,
+                                  offload_inputs=offload, v_chunk=256)
     ids, mask, labels = _batch(cfg, [37, 64, 21])
     pb = ops.pack_varlen(ids, mask, labels)
     loss, grads = _fused_step(engine, pb, training=False)
@@ -209,8 +212,86 @@ def test_saved_activations_match_recompute_bitwise(dropout, lora_kernels):
             assert torch.equal(a, b)
 
 
-def test_recompute_off_needs_varlen_attention():
+def test_engine_has_one_attention_path():
     cfg = small_config()
     model = M.build_random_qlora_qwen2(cfg, DEV, seed=4, std=0.05)
-    with pytest.raises(ValueError, match="recompute=False"):
-        ops.Qwen2FusedEngine(model, DEV, attention="sdpa_rows", recompute=False)
+    for other in ("varlen_aten", "sdpa_rows"):
+        with pytest.raises(ValueError, match="only attention path"):
+            ops.Qwen2FusedEngine(model, DEV, attention=other)
+
+
+@pytest.mark.parametrize("recompute", [True, False])
+def test_host_streams_agree_bitwise_with_hbm_residency(recompute):
+    # Streamed head (embedding rows gathered on the device from pinned host memory, vocabulary
+    # chunks through the two-slot ring) and inputs offloaded to the host: the same bits as the
+    # HBM-resident head and inputs, given the same vocabulary chunk; two steps in a row.
+    cfg = small_config(dropout=0.1)
+    model = M.build_random_qlora_qwen2(cfg, DEV, seed=7, std=0.05)
+    ids, mask, labels = _batch(cfg, [33, 58, 27], seed=5)
+    pb = ops.pack_varlen(ids, mask, labels)
+    out = []
+    for head, offload in ((True, False), (False, True), (False, False), (True, True)):
+        engine = ops.Qwen2FusedEngine(model, DEV, resident_head=head, offload_inputs=offload,
+                                      v_chunk=256, dropout_seed=77, recompute=recompute)
+        for _ in range(2):
+            for p in engine.lora_params:
+                p.grad = None
+            h = engine.host_head.embed(pb.input_ids.to(DEV))
+            final = ops.FusedQwen2StackFn.apply(h, pb.pos_ids.to(DEV), pb.row_lengths, engine,
+                                                True, *engine.lora_params)
+            loss, nll, ent, amax = ops.chunked_lm_head(final, pb.shift_labels.to(DEV),
+                                                       engine.host_head, v_chunk=256)
+            loss.backward()
+            torch.cuda.synchronize()
+            out.append((loss.detach().cpu(), nll.cpu(), ent.cpu(), amax.cpu(),
+                        [p.grad.detach().cpu().clone() for p in engine.lora_params]))
+    for i in range(0, len(out), 2):  # the engines' second steps draw the same masks
+        for a, b in zip(out[0][:4], out[i][:4]):
+            assert torch.equal(a, b), i
+        for a, b in zip(out[0][4], out[i][4]):
+            assert torch.equal(a, b), i
+        assert torch.equal(out[1][0], out[i + 1][0])
+    if not engine.host_head.resident:
+        assert int(engine.host_head.embed_error.item()) == 0
+
+
+def test_patched_qwen2_forward_returns_loss_and_logits_proxy():
+    # transformers' Qwen2ForCausalLM.forward, patched, on the attribute layout of a PEFT +
+    # bitsandbytes model: the fused engine's loss and a ChunkedLogitsProxy whose statistics are
+    # the fused head's (padding positions: nll 0, the batch-mean entropy).
+    pytest.importorskip("transformers")
+    from duck_hf import duck_causal_lm
+    from transformers.models.qwen2 import modeling_qwen2
+
+    import torch.nn.functional as F
+
+    cfg = small_config(layers=1)
+    model = M.build_random_qlora_qwen2(cfg, DEV, seed=8, std=0.05)
+    duck = duck_causal_lm(model, dropout_p=0.0, training=False)
+    ids, mask, labels = _batch(cfg, [17, 29], seed=6)
+    ids, mask, labels = ids.to(DEV), mask.to(DEV), labels.to(DEV)
+    unpatched = modeling_qwen2.Qwen2ForCausalLM.forward
+    try:
+        assert ops.install_runtime_patches()["transformers_qwen2"]
+        out = modeling_qwen2.Qwen2ForCausalLM.forward(duck, input_ids=ids, attention_mask=mask,
+                                                      labels=labels)
+    finally:
+        modeling_qwen2.Qwen2ForCausalLM.forward = unpatched
+    engine = duck.__dict__["_rus_fused_engine"]
+    loss_f, nll, ent, amax = ops.fused_causal_lm_forward(engine, ids, mask, labels,
+                                                         training=False)
+    torch.cuda.synchronize()
+    assert torch.equal(out.loss.detach().cpu(), loss_f.detach().cpu())
+    proxy = out.logits
+    assert isinstance(proxy, ops.ChunkedLogitsProxy) and proxy.shape == (2, 29, cfg.vocab_size)
+    assert torch.equal(proxy.argmax(-1).cpu(), amax.cpu())
+    assert torch.all(proxy.per_token_nll[0, 17:].cpu() == 0)
+    mean_ent = ent[mask.bool()].mean()
+    assert torch.allclose(ent[0, 17:], mean_ent.expand(12))
+    # the trainer's shifted loss from the proxy equals the fused loss
+    V = cfg.vocab_size
+    ce = F.cross_entropy(proxy[:, :-1].reshape(-1, V), labels[:, 1:].reshape(-1),
+                         ignore_index=-100)
+    assert torch.allclose(ce.cpu(), out.loss.detach().float().cpu(), rtol=1e-5, atol=1e-6)
+    out.loss.backward()
+    assert all(p.grad is not None for p in engine.lora_params)

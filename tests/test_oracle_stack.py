@@ -3,7 +3,6 @@ host-side packing (rus_amd.ops.pack_varlen) and model adapter on the CPU."""
 
 from __future__ import annotations
 
-from types import SimpleNamespace
 
 import torch
 
@@ -168,39 +167,14 @@ def _att64(q, k, v, row_lengths):
 
 def test_model_from_duck_typed_causal_lm():
     """The adapter reads the attribute layout of a PEFT + bitsandbytes Qwen2 (no libraries)."""
+    from duck_hf import duck_causal_lm
+
     from rus_amd.adapters import model_from_causal_lm
 
     cfg = tiny_config(layers=1)
     m = M.build_random_qlora_qwen2(cfg, "cpu", seed=4)
     L = m.layers[0]
-
-    def lin(w, bias=None, lora=None):
-        qs = SimpleNamespace(absmax=w.absmax, offset=torch.tensor(w.offset), shape=w.shape,
-                             blocksize=w.blocksize,
-                             state2=SimpleNamespace(absmax=w.absmax2, code=w.code2,
-                                                    blocksize=w.super_blocksize))
-        weight = SimpleNamespace(data=w.packed.view(-1, 1), quant_state=qs)
-        base = SimpleNamespace(weight=weight, bias=bias)
-        mod = SimpleNamespace(base_layer=base)
-        if lora is not None:
-            A, B = lora
-            mod.lora_A = {"default": SimpleNamespace(weight=A)}
-            mod.lora_B = {"default": SimpleNamespace(weight=B)}
-            mod.scaling = {"default": cfg.lora_scaling}
-            mod.lora_dropout = {"default": SimpleNamespace(p=0.05)}
-        return mod
-
-    attn = SimpleNamespace(q_proj=lin(L.q, L.q_bias, (L.q_A, L.q_B)), k_proj=lin(L.k, L.k_bias),
-                           v_proj=lin(L.v, L.v_bias, (L.v_A, L.v_B)), o_proj=lin(L.o))
-    mlp = SimpleNamespace(gate_proj=lin(L.gate), up_proj=lin(L.up), down_proj=lin(L.down))
-    layer = SimpleNamespace(self_attn=attn, mlp=mlp, input_layernorm=SimpleNamespace(weight=L.ln1),
-                            post_attention_layernorm=SimpleNamespace(weight=L.ln2))
-    hf_cfg = SimpleNamespace(hidden_size=64, intermediate_size=128, num_attention_heads=4,
-                             num_key_value_heads=2, vocab_size=300, rms_norm_eps=1e-6,
-                             rope_theta=1e6)
-    causal = SimpleNamespace(config=hf_cfg, model=SimpleNamespace(
-        layers=[layer], embed_tokens=SimpleNamespace(weight=m.embed),
-        norm=SimpleNamespace(weight=m.final_norm)))
+    causal = duck_causal_lm(m)
     got = model_from_causal_lm(causal)
     assert got.config.lora_r == 4 and abs(got.config.lora_scaling - cfg.lora_scaling) < 1e-12
     G = got.layers[0]
