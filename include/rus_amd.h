@@ -339,6 +339,22 @@ int rus_lora_down_fwd(const void* x, int64_t n_tokens, int64_t d, int64_t stride
                       int64_t n_counters, void* stream);
 
 /*
+ * rus_lora_down_fwd without the workspace and counters arguments, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). No counterpart in the reference. The scratch is a file-scope device array of this
+ * library: 4,194,304 fp32 partials (16 MiB) and 4,096 int32 counters per device, held until the
+ * process ends; its address is taken with hipGetSymbolAddress on the first call on each device,
+ * which also clears the counters on `stream` (every launch leaves them zero). Shapes whose scratch
+ * (rus_lora_workspace_size(RUS_LORA_DOWN, ...)) exceeds that are rejected with RUS_ERR_UNSUPPORTED
+ * (d = 1536: up to 10,912 tokens at r <= 16, 5,440 at r = 32). The call itself allocates nothing.
+ * All calls on one device share the array: calls that overlap in time on one device race.
+ */
+int rus_lora_down_fwd_noalloc(const void* x, int64_t n_tokens, int64_t d, int64_t stride_x,
+                              const void* a_q, const void* a_v, int32_t r, void* mid_q,
+                              void* mid_v, const uint32_t* bits_q, const uint32_t* bits_v,
+                              float p_q, float p_v, void* stream);
+
+/*
  * rus_qkv_lora_rope_fwd with the LoRA deltas formed in-kernel from the rank-r factors (fp16):
  *   q_lora[t, c] = fp16(mid_q[t, :] . b_q[c, :]), v_lora likewise (b_q [h_q*head_dim, r],
  *   b_v [h_kv*head_dim, r], mid [n_tokens, r], all contiguous), then exactly the RoPE forward.

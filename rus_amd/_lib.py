@@ -70,6 +70,8 @@ SIGNATURES: dict[str, list] = {
                                 ctypes.POINTER(_i64)],
     "rus_lora_down_fwd": [_vp, _i64, _i64, _i64, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _f32, _f32,
                           _vp, _i64, _vp, _i64, _vp],
+    "rus_lora_down_fwd_noalloc": [_vp, _i64, _i64, _i64, _vp, _vp, _i32, _vp, _vp, _vp, _vp,
+                                  _f32, _f32, _vp],
     "rus_qkv_lora_rope_fwd_mid": [_vp, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp,
                                   _i64, _i64, _i64, _i64, _f32, _f32, _i32, _i32, _i32, _vp, _vp],
     "rus_lora_bwd_x": [_vp, _vp, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _i32, _i64, _vp, _vp, _vp,

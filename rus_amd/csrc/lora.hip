@@ -31,6 +31,8 @@
 // Workspace: fp32 partials (rus_lora_workspace_size) and int32 arrival counters that are zero
 // when a launch starts and are left zero by it. Launches that share counters must not overlap.
 
+#include <mutex>
+
 #include "common.h"
 
 namespace rus {
@@ -639,13 +641,12 @@ static int check_scratch(const char* fn, int which, int64_t n, int64_t d, int64_
   return RUS_OK;
 }
 
-extern "C" int rus_lora_down_fwd(const void* x, int64_t n_tokens, int64_t d, int64_t stride_x,
-                                 const void* a_q, const void* a_v, int32_t r, void* mid_q,
-                                 void* mid_v, const uint32_t* bits_q, const uint32_t* bits_v,
-                                 float p_q, float p_v, float* workspace, int64_t workspace_floats,
-                                 int32_t* counters, int64_t n_counters, void* stream) {
+static int lora_down(const char* fn, const void* x, int64_t n_tokens, int64_t d,
+                     int64_t stride_x, const void* a_q, const void* a_v, int32_t r, void* mid_q,
+                     void* mid_v, const uint32_t* bits_q, const uint32_t* bits_v, float p_q,
+                     float p_v, float* workspace, int64_t workspace_floats, int32_t* counters,
+                     int64_t n_counters, void* stream) {
   using namespace rus;
-  const char* fn = "rus_lora_down_fwd";
   if ((bits_q == nullptr) != (bits_v == nullptr))
     return fail(RUS_ERR_INVALID, "%s: give the keep bits of both branches or of neither", fn);
   if (!rank_ok(r)) return fail(RUS_ERR_UNSUPPORTED, "%s: rank %d not in {4,8,16,32}", fn, r);
@@ -682,6 +683,101 @@ extern "C" int rus_lora_down_fwd(const void* x, int64_t n_tokens, int64_t d, int
   switch (r) { RUS_DOWN(4) RUS_DOWN(8) RUS_DOWN(16) RUS_DOWN(32) }
 #undef RUS_DOWN
   return check_launch(fn);
+}
+
+extern "C" int rus_lora_down_fwd(const void* x, int64_t n_tokens, int64_t d, int64_t stride_x,
+                                 const void* a_q, const void* a_v, int32_t r, void* mid_q,
+                                 void* mid_v, const uint32_t* bits_q, const uint32_t* bits_v,
+                                 float p_q, float p_v, float* workspace, int64_t workspace_floats,
+                                 int32_t* counters, int64_t n_counters, void* stream) {
+  return lora_down("rus_lora_down_fwd", x, n_tokens, d, stride_x, a_q, a_v, r, mid_q, mid_v,
+                   bits_q, bits_v, p_q, p_v, workspace, workspace_floats, counters, n_counters,
+                   stream);
+}
+
+// ---------------------------------------------------------------------------------------------
+// rus_lora_down_fwd_noalloc: the same launch with its workspace and counters in a file-scope
+// device array, for callers that cannot allocate. Each device holds its own copy of the array
+// (16 MiB of fp32 partials + 16 KiB of counters) until the process ends; its address on a device
+// is taken once with hipGetSymbolAddress and kept, and the counters are cleared then (every launch
+// leaves them zero). All calls on one device share the array: calls that overlap on one device
+// race.
+// ---------------------------------------------------------------------------------------------
+
+namespace rus {
+namespace {
+constexpr int64_t kNoAllocFloats = int64_t(1) << 22;
+constexpr int64_t kNoAllocCounters = 4096;
+constexpr int kMaxDevices = 64;
+}  // namespace
+}  // namespace rus
+
+static __device__ __align__(256) float scratch[rus::kNoAllocFloats + rus::kNoAllocCounters];
+
+namespace rus {
+namespace {
+
+__global__ __launch_bounds__(256) void zero_words_kernel(int32_t* p, int64_t n) {
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n;
+       i += static_cast<int64_t>(gridDim.x) * 256)
+    p[i] = 0;
+}
+
+std::mutex g_noalloc_mutex;
+float* g_noalloc_base[kMaxDevices] = {};
+
+// The current device's copy of `scratch` (address taken on the first call on that device, when
+// its counters are also cleared on `stream`).
+int noalloc_scratch(const char* fn, void* stream, float** base) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return fail(RUS_ERR_LAUNCH, "%s: no current device (%s)", fn, hipGetErrorString(e));
+  std::lock_guard<std::mutex> lock(g_noalloc_mutex);
+  if (!g_noalloc_base[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail(RUS_ERR_LAUNCH, "%s: hipGetSymbolAddress(scratch) failed on device %d: %s", fn,
+                  dev, hipGetErrorString(e));
+    float* f = static_cast<float*>(p);
+    hipLaunchKernelGGL(zero_words_kernel, dim3(16), dim3(256), 0,
+                       static_cast<hipStream_t>(stream),
+                       reinterpret_cast<int32_t*>(f + kNoAllocFloats), kNoAllocCounters);
+    if (int rc = check_launch(fn)) return rc;
+    g_noalloc_base[dev] = f;
+  }
+  *base = g_noalloc_base[dev];
+  return RUS_OK;
+}
+
+}  // namespace
+}  // namespace rus
+
+extern "C" int rus_lora_down_fwd_noalloc(const void* x, int64_t n_tokens, int64_t d,
+                                         int64_t stride_x, const void* a_q, const void* a_v,
+                                         int32_t r, void* mid_q, void* mid_v,
+                                         const uint32_t* bits_q, const uint32_t* bits_v,
+                                         float p_q, float p_v, void* stream) {
+  using namespace rus;
+  const char* fn = "rus_lora_down_fwd_noalloc";
+  if (!rank_ok(r)) return fail(RUS_ERR_UNSUPPORTED, "%s: rank %d not in {4,8,16,32}", fn, r);
+  if (n_tokens < 0 || d <= 0 || d % 16)
+    return fail(RUS_ERR_INVALID, "%s: need n_tokens >= 0 and d %% 16 == 0", fn);
+  int64_t need_f = 0, need_c = 0;
+  scratch_need(RUS_LORA_DOWN, n_tokens, d, 16, 16, r, need_f, need_c);
+  if (need_f > kNoAllocFloats || need_c > kNoAllocCounters)
+    return fail(RUS_ERR_UNSUPPORTED,
+                "%s: n_tokens=%lld, d=%lld, r=%d need %lld scratch floats and %lld counters; the "
+                "static scratch holds %lld and %lld (use rus_lora_down_fwd with a workspace)",
+                fn, static_cast<long long>(n_tokens), static_cast<long long>(d), r,
+                static_cast<long long>(need_f), static_cast<long long>(need_c),
+                static_cast<long long>(kNoAllocFloats), static_cast<long long>(kNoAllocCounters));
+  float* base = nullptr;
+  if (int e = noalloc_scratch(fn, stream, &base)) return e;
+  return lora_down(fn, x, n_tokens, d, stride_x, a_q, a_v, r, mid_q, mid_v, bits_q, bits_v, p_q,
+                   p_v, base, kNoAllocFloats, reinterpret_cast<int32_t*>(base + kNoAllocFloats),
+                   kNoAllocCounters, stream);
 }
 
 extern "C" int rus_lora_bwd_x(const void* dq_lora, const void* dv_lora, int64_t n_tokens,
