@@ -33,7 +33,7 @@ if REPO not in sys.path:
 METRIC = "train tokens/s (packed 1.5B NF4 QLoRA); lm_head-CE & NF4-dequant HBM GB/s"
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E
 FP16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA
-MFMA_KERNELS = ("lmhead_ce_fwd", "lmhead_ce_fwd_keep", "lmhead_ce_grad_logits",
+MFMA_KERNELS = ("lmhead_ce_fwd", "lmhead_ce_fwd_keep", "lmhead_ce_logits", "lmhead_ce_grad_logits",
                 "lmhead_ce_grad_hidden")
 
 

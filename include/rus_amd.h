@@ -477,6 +477,29 @@ int rus_lmhead_ce_fwd_keep(const void* hidden, const void* weight, const int64_t
                            void* logits, int64_t ld_z, void* stream);
 
 /*
+ * Logits only: logits[t][v] = fp16(hidden[t] . weight[v]) (fp32 accumulation) for t < n_tok,
+ * v < n_vocab, 0 in the columns n_vocab .. round_up(n_vocab, 64) (ld_z >= that). The statistics
+ * GEMM without its statistics epilogue; rus_lmhead_ce_rows forms them from the stored rows.
+ * Replaces: the chunk GEMM of solution/ops.py:231-237 (the logits of lm_head_piece_kernel's input).
+ */
+int rus_lmhead_ce_logits(const void* hidden, const void* weight, int64_t n_tok, int64_t d,
+                         int64_t ld_h, int64_t ld_w, int64_t n_vocab, void* logits, int64_t ld_z,
+                         void* stream);
+
+/*
+ * Per-token statistics of kept logit rows [n_tok, n_vocab] (row stride ld_z): lse, entropy,
+ * nll (lse - logits[t][labels[t]], 0 for label -100; lse where the label is outside the
+ * vocabulary), argmax (first index of the maximum); then, when denom (device scalar) is not NULL,
+ * each row becomes its fp16 logit gradient in place: G = fp16((e^{z - lse} - 1[v = label]) *
+ * 2^16 / max(denom, 1)) (0 for label -100 and in the padding columns up to round_up(n_vocab, 64)).
+ * Replaces: lm_head_piece_kernel MODE 0 and MODE 1 plus lm_head_finish_kernel over one whole row
+ * (solution/kernels.py:453-565), for a row the caller holds whole.
+ */
+int rus_lmhead_ce_rows(void* logits, int64_t ld_z, int64_t n_tok, int64_t n_vocab,
+                       const int64_t* labels, const float* denom, float* lse, float* nll,
+                       float* entropy, int64_t* argmax, void* stream);
+
+/*
  * Merges n_parts partial rows per token and finishes the statistics.
  * Replaces: solution/kernels.py:534-565 (lm_head_finish_kernel) plus the cross-chunk argmax of
  *           kernels.py:494-498. lse = M + ln S, entropy = lse - W/S, nll = lse - target (0 where the

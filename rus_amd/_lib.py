@@ -110,6 +110,8 @@ SIGNATURES: dict[str, list] = {
     "rus_lmhead_ce_grad_hidden": [_vp, _i64, _vp, _i64, _i64, _i64, _i64, _vp, _i32, _i32, _vp],
     "rus_lmhead_dh_reduce": [_vp, _i32, _i64, _f32, _vp, _vp, _i32, _vp],
     "rus_transpose_f16": [_vp, _i64, _i64, _i64, _vp, _i64, _i64, _vp],
+    "rus_lmhead_ce_logits": [_vp, _vp, _i64, _i64, _i64, _i64, _i64, _vp, _i64, _vp],
+    "rus_lmhead_ce_rows": [_vp, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp],
     "rus_lmhead_ce_grad_hidden_scaled": [_vp, _i64, _vp, _i64, _i64, _i64, _i64, _vp, _i32, _i32,
                                          _vp, _vp],
     "rus_lmhead_ce_chunk_scale": [_vp, _i64, _i64, _i64, _vp, _i64, _i64, _vp, _vp, _i32, _vp],

@@ -423,6 +423,29 @@ lmhead_stats_kernel(GemmArgs g, StatsParams p) {
 }
 
 // ---------------------------------------------------------------------------------------------
+// Logits only: A = W rows (vocab), B = H rows (tokens) -> z[token][vocab] = fp16(H.W^T), the
+// mainloop followed by the tile's store (no statistics in the epilogue: lmhead_rows_kernel forms
+// them from the stored row, at full occupancy, beside other rows' HBM traffic).
+// ---------------------------------------------------------------------------------------------
+
+struct LogitsParams {
+  f16* z;  // [n_tok][ld_z], columns up to kpad (0 past M)
+  int64_t ld_z;
+  int kpad;
+};
+
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))) void
+lmhead_logits_kernel(GemmArgs g, LogitsParams p) {
+  __shared__ __attribute__((aligned(16))) char smem[kSmemBytes];
+  Tile tl;
+  if (!tile_of(g, tl)) return;
+  f32x16 acc[kMT][kNT];
+  mainloop(g, tl, smem, acc);
+  store_tile_tv(smem, g, tl, p.z, p.ld_z, p.kpad,
+                [&](int mt, int nt, int r, int) { return acc[mt][nt][r]; });
+}
+
+// ---------------------------------------------------------------------------------------------
 // Logit gradient: A = W rows (vocab chunk), B = H rows (tokens) -> G[token][vocab] fp16.
 // ---------------------------------------------------------------------------------------------
 
@@ -639,6 +662,152 @@ __global__ __launch_bounds__(256) void lmhead_dh_finish_kernel(
     for (int e = 0; e < 4; ++e) o[e] = (a[e] * f - wy[e]) * scale;
   }
   store_from_f32<T, 4>(out + i, o);
+}
+
+// ---------------------------------------------------------------------------------------------
+// One token's row of kept logits z[0 .. n_vocab): its statistics (first-index argmax, max m,
+// s = sum e^{z-m}, w = sum e^{z-m} z, the label's logit) in one pass, lse = m + ln s,
+// entropy = lse - w/s, nll = lse - z[label]; then, when a denominator is given, the logit
+// gradient G = fp16((e^{z-lse} - 1[v=label]) 2^16 / denom) in place (the formula of
+// lmhead_grad_logits_kernel's epilogue; 0 in the padding columns up to kpad, and for label -100).
+// Block = one row, kRowThreads threads, each taking 16-byte packs kRowThreads * 8 apart and
+// keeping kRowDepth of them in flight.
+// ---------------------------------------------------------------------------------------------
+
+constexpr int kRowThreads = 512, kRowDepth = 4;
+
+__device__ __forceinline__ void merge_row(float& m, float& s, float& w, float& bv, int& bi, float m2,
+                                          float s2, float w2, float bv2, int bi2) {
+  const float M = fmaxf(m, m2);
+  if (M > -INFINITY) {
+    const float c1 = exp2_fast((m - M) * kLog2e), c2 = exp2_fast((m2 - M) * kLog2e);
+    s = s * c1 + s2 * c2;
+    w = w * c1 + w2 * c2;
+  }
+  m = M;
+  if (bv2 > bv || (bv2 == bv && bi2 < bi)) {
+    bv = bv2;
+    bi = bi2;
+  }
+}
+
+__global__ __launch_bounds__(kRowThreads) void lmhead_rows_kernel(
+    f16* zg, int64_t ld, int n_vocab, int kpad, const int64_t* __restrict__ labels,
+    const float* __restrict__ denom, float* __restrict__ lse_out, float* __restrict__ nll_out,
+    float* __restrict__ ent_out, int64_t* __restrict__ amax_out) {
+  __shared__ float red[5][kRowThreads / kWave];
+  const int tok = blockIdx.x, tid = threadIdx.x;
+  f16* row = zg + static_cast<int64_t>(tok) * ld;
+  float m = -INFINITY, s = 0.0f, w = 0.0f, bv = -INFINITY;
+  int bi = 0x7fffffff;
+  const int n_packs = (n_vocab + 7) / 8;
+  for (int p0 = tid; p0 < n_packs; p0 += kRowThreads * kRowDepth) {
+    f16x8 v[kRowDepth];
+#pragma unroll
+    for (int u = 0; u < kRowDepth; ++u) {
+      const int p = p0 + u * kRowThreads;
+      if (p < n_packs) v[u] = *reinterpret_cast<const f16x8*>(row + 8 * p);
+    }
+#pragma unroll
+    for (int u = 0; u < kRowDepth; ++u) {
+      const int p = p0 + u * kRowThreads;
+      if (p >= n_packs) break;
+      float z[8];
+      float mc = -INFINITY;
+      int ic = 0;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        z[e] = 8 * p + e < n_vocab ? static_cast<float>(v[u][e]) : -INFINITY;
+        if (z[e] > mc) {  // strict: the first index of the pack's maximum
+          mc = z[e];
+          ic = e;
+        }
+      }
+      if (mc > bv) {  // packs ascend within a thread: strict keeps the first index
+        bv = mc;
+        bi = 8 * p + ic;
+      }
+      if (mc > m) {
+        const float c = exp2_fast((m - mc) * kLog2e);
+        s *= c;
+        w *= c;
+        m = mc;
+      }
+      if (mc == -INFINITY) continue;  // only padding in this pack
+      const float mb = m * kLog2e;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        if (8 * p + e < n_vocab) {  // the padding's -inf would make 0 * -inf in w
+          const float t = exp2_fast(__builtin_fmaf(z[e], kLog2e, -mb));
+          s += t;
+          w = __builtin_fmaf(t, z[e], w);
+        }
+      }
+    }
+  }
+  // wave, then block: merge (m, s, w) and the argmax (ties: the smaller index)
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    const float m2 = __shfl_xor(m, off, kWave), s2 = __shfl_xor(s, off, kWave);
+    const float w2 = __shfl_xor(w, off, kWave), bv2 = __shfl_xor(bv, off, kWave);
+    const int bi2 = __shfl_xor(bi, off, kWave);
+    merge_row(m, s, w, bv, bi, m2, s2, w2, bv2, bi2);
+  }
+  const int wave = tid >> 6;
+  if ((tid & 63) == 0) {
+    red[0][wave] = m;
+    red[1][wave] = s;
+    red[2][wave] = w;
+    red[3][wave] = bv;
+    red[4][wave] = __int_as_float(bi);
+  }
+  __syncthreads();
+  m = red[0][0];
+  s = red[1][0];
+  w = red[2][0];
+  bv = red[3][0];
+  bi = __float_as_int(red[4][0]);
+  for (int k = 1; k < kRowThreads / kWave; ++k)
+    merge_row(m, s, w, bv, bi, red[0][k], red[1][k], red[2][k], red[3][k],
+              __float_as_int(red[4][k]));
+  const float L = m + logf(s);
+  const int64_t y = labels[tok];
+  const bool in_range = y >= 0 && y < n_vocab;
+  if (tid == 0) {
+    const float tgt = in_range ? static_cast<float>(row[y]) : 0.0f;
+    lse_out[tok] = L;
+    ent_out[tok] = L - w / s;
+    nll_out[tok] = y != -100 ? L - tgt : 0.0f;
+    amax_out[tok] = bi;
+  }
+  if (!denom) return;
+  __syncthreads();  // the label's logit is read before it is overwritten
+  const float scale = y != -100 ? kPrescale / fmaxf(*denom, 1.0f) : 0.0f;
+  const int lab = in_range ? static_cast<int>(y) : -1;
+  const float l2 = L * kLog2e;
+  const int k_packs = kpad / 8;
+  for (int p0 = tid; p0 < k_packs; p0 += kRowThreads * kRowDepth) {
+    f16x8 v[kRowDepth];
+#pragma unroll
+    for (int u = 0; u < kRowDepth; ++u) {
+      const int p = p0 + u * kRowThreads;
+      if (p < k_packs) v[u] = *reinterpret_cast<const f16x8*>(row + 8 * p);
+    }
+#pragma unroll
+    for (int u = 0; u < kRowDepth; ++u) {
+      const int p = p0 + u * kRowThreads;
+      if (p >= k_packs) break;
+      f16x8 o;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int c = 8 * p + e;
+        const float pr = exp2_fast(__builtin_fmaf(static_cast<float>(v[u][e]), kLog2e, -l2));
+        const float gv = (pr - (c == lab ? 1.0f : 0.0f)) * scale;
+        o[e] = static_cast<_Float16>(c < n_vocab ? gv : 0.0f);
+      }
+      *reinterpret_cast<f16x8*>(row + 8 * p) = o;
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -1167,5 +1336,57 @@ extern "C" int rus_transpose_f16(const void* src, int64_t rows, int64_t cols, in
   hipLaunchKernelGGL(transpose_f16_kernel, dim3(static_cast<unsigned>(gx), static_cast<unsigned>(gy)),
                      dim3(256), 0, static_cast<hipStream_t>(stream), static_cast<const f16*>(src),
                      rows, cols, ld_src, static_cast<f16*>(dst), ld_dst, rows_pad);
+  return check_launch(fn);
+}
+
+extern "C" int rus_lmhead_ce_logits(const void* hidden, const void* weight, int64_t n_tok,
+                                    int64_t d, int64_t ld_h, int64_t ld_w, int64_t n_vocab,
+                                    void* logits, int64_t ld_z, void* stream) {
+  const char* fn = "rus_lmhead_ce_logits";
+  if (n_tok < 0 || n_tok >= (1 << 30) || n_vocab < 0 || n_vocab >= (1 << 30) || d <= 0 ||
+      d % kBK)
+    return fail(RUS_ERR_INVALID, "%s: bad sizes (d must be a multiple of %d)", fn, kBK);
+  if (n_tok == 0 || n_vocab == 0) return RUS_OK;
+  const int64_t kpad = (n_vocab + kBK - 1) / kBK * kBK;
+  if (ld_h < d || ld_w < d || ld_z < kpad)
+    return fail(RUS_ERR_INVALID, "%s: row strides too small (ld_z must be >= %lld)", fn,
+                (long long)kpad);
+  if (int e = check_operand(fn, hidden, ld_h, "hidden")) return e;
+  if (int e = check_operand(fn, weight, ld_w, "weight")) return e;
+  if (int e = check_operand(fn, logits, ld_z, "logits")) return e;
+  GemmArgs g;
+  g.A = static_cast<const f16*>(weight);
+  g.lda = ld_w;
+  g.M = static_cast<int>(n_vocab);
+  g.B = static_cast<const f16*>(hidden);
+  g.ldb = ld_h;
+  g.N = static_cast<int>(n_tok);
+  g.K = static_cast<int>(d);
+  g.k_per_split = g.K;
+  g.splits = 1;
+  g.tiles_m = (g.M + kBM - 1) / kBM;
+  g.tiles_n = (g.N + kBN - 1) / kBN;
+  LogitsParams p{static_cast<f16*>(logits), ld_z, static_cast<int>(kpad)};
+  hipLaunchKernelGGL(lmhead_logits_kernel, dim3(launch_grid(g)), dim3(kThreads), 0,
+                     static_cast<hipStream_t>(stream), g, p);
+  return check_launch(fn);
+}
+
+extern "C" int rus_lmhead_ce_rows(void* logits, int64_t ld_z, int64_t n_tok, int64_t n_vocab,
+                                  const int64_t* labels, const float* denom, float* lse,
+                                  float* nll, float* entropy, int64_t* argmax, void* stream) {
+  const char* fn = "rus_lmhead_ce_rows";
+  if (n_tok < 0 || n_tok >= (1 << 30) || n_vocab <= 0 || n_vocab >= (1 << 30))
+    return fail(RUS_ERR_INVALID, "%s: bad sizes", fn);
+  if (n_tok == 0) return RUS_OK;
+  const int64_t kpad = (n_vocab + kBK - 1) / kBK * kBK;
+  if (ld_z < kpad) return fail(RUS_ERR_INVALID, "%s: ld_z must be >= %lld", fn, (long long)kpad);
+  if (int e = check_operand(fn, logits, ld_z, "logits")) return e;
+  if (!labels || !lse || !nll || !entropy || !argmax)
+    return fail(RUS_ERR_INVALID, "%s: null pointer argument", fn);
+  hipLaunchKernelGGL(lmhead_rows_kernel, dim3(static_cast<unsigned>(n_tok)), dim3(kRowThreads), 0,
+                     static_cast<hipStream_t>(stream), static_cast<f16*>(logits), ld_z,
+                     static_cast<int>(n_vocab), static_cast<int>(kpad), labels, denom, lse, nll,
+                     entropy, argmax);
   return check_launch(fn);
 }

@@ -53,6 +53,8 @@ __all__ = [
     "lm_head_chunk_cols",
     "lm_head_token_blocks",
     "lm_head_ce_denom",
+    "lm_head_ce_logits",
+    "lm_head_ce_rows",
     "LMHeadPass",
     "lm_head_ce_fwd_chunk",
     "lm_head_ce_combine",
@@ -1748,6 +1750,56 @@ class LMHeadPass:
         return nll, lse, ent, amax, denom, dh, loss
 
 
+def lm_head_ce_logits(hidden: torch.Tensor, weight: torch.Tensor, out: torch.Tensor) -> torch.Tensor:
+    """out[t, v] = fp16(hidden[t] . weight[v]) for the vocabulary rows of ``weight``, zeros in
+    ``out``'s columns up to round_up(V, 64) (out [n_tok, >= that] fp16, contiguous rows)."""
+    fn = "lm_head_ce_logits"
+    _require_device(fn, hidden, weight, out)
+    d = hidden.shape[1]
+    h = _lm_operand(fn, hidden, d, "hidden")
+    w = _lm_operand(fn, weight, d, "weight")
+    n_tok, V = h.shape[0], w.shape[0]
+    kp = _round_up(V, LM_K)
+    if out.dtype != torch.float16 or out.dim() != 2 or out.shape[0] != n_tok \
+            or out.shape[1] < kp or out.stride(1) != 1:
+        raise ValueError(f"{fn}: out must be fp16 [{n_tok}, >= {kp}] with contiguous rows")
+    if out.shape[0] * out.stride(0) * 2 >= 1 << 32:
+        raise ValueError(f"{fn}: out exceeds the 4 GiB operand limit of the MFMA kernels")
+    _launch("lmhead_ce_logits", (n_tok + V) * d * 2 + n_tok * kp * 2, 2.0 * n_tok * d * V,
+            "rus_lmhead_ce_logits", h.data_ptr(), w.data_ptr(), n_tok, d, h.stride(0),
+            w.stride(0), V, out.data_ptr(), out.stride(0), _stream(h))
+    return out
+
+
+def lm_head_ce_rows(logits: torch.Tensor, n_vocab: int, labels: torch.Tensor,
+                    denom: torch.Tensor | None, lse: torch.Tensor, nll: torch.Tensor,
+                    ent: torch.Tensor, amax: torch.Tensor) -> None:
+    """Per-token lse / nll / entropy / argmax of kept logit rows into the given tensors (one
+    entry per row) and, with ``denom``, the rows turned into the fp16 logit gradient in place
+    (replaces lm_head_piece_kernel MODE 0 / 1 and lm_head_finish_kernel, kernels.py:453-565)."""
+    fn = "lm_head_ce_rows"
+    _require_device(fn, logits, labels, denom, lse, nll, ent, amax)
+    n_tok = logits.shape[0]
+    kp = _round_up(n_vocab, LM_K)
+    if logits.dtype != torch.float16 or logits.dim() != 2 or logits.shape[1] < kp \
+            or logits.stride(1) != 1:
+        raise ValueError(f"{fn}: logits must be fp16 [n_tok, >= {kp}] with contiguous rows")
+    lab = labels.reshape(-1)
+    if lab.dtype != torch.int64 or lab.numel() != n_tok or not lab.is_contiguous():
+        raise ValueError(f"{fn}: labels must be contiguous int64 with {n_tok} entries")
+    for name, t, dt in (("lse", lse, torch.float32), ("nll", nll, torch.float32),
+                        ("entropy", ent, torch.float32), ("argmax", amax, torch.int64)):
+        if t.dtype != dt or t.numel() != n_tok or not t.is_contiguous():
+            raise ValueError(f"{fn}: {name} must be contiguous {dt} with {n_tok} entries")
+    if denom is not None and (denom.dtype != torch.float32 or denom.numel() != 1):
+        raise ValueError(f"{fn}: denom must be a one-element float32 device tensor")
+    grad = denom is not None
+    _launch("lmhead_ce_rows", n_tok * kp * 2 * (3 if grad else 1) + 28 * n_tok, 0,
+            "rus_lmhead_ce_rows", logits.data_ptr(), logits.stride(0), n_tok, n_vocab,
+            lab.data_ptr(), _ptr(denom), lse.data_ptr(), nll.data_ptr(), ent.data_ptr(),
+            amax.data_ptr(), _stream(logits))
+
+
 def lm_head_ce_denom(labels: torch.Tensor, num_items_in_batch=None) -> torch.Tensor:
     """The loss denominator alone, as a one-element float32 device tensor (what ``lm_head_ce_loss``
     will use): max(num_items_in_batch, 1) if given, else max(#(labels != -100), 1)."""
@@ -1802,17 +1854,6 @@ def _fwd_rows(hidden, weight, labels, parts: LMHeadPartials, target, t0: int, t1
                 "rus_lmhead_ce_fwd_keep", *args, logits.data_ptr(), logits.stride(0), _stream(h))
 
 
-def _combine_rows(parts: LMHeadPartials, target, labels, t0: int, t1: int, lse, nll, ent,
-                  amax) -> None:
-    n = t1 - t0
-    _launch("lmhead_ce_combine", 16 * n * parts.n_parts + 32 * n, 0, "rus_lmhead_ce_combine",
-            parts.m.data_ptr() + 4 * t0, parts.s.data_ptr() + 4 * t0,
-            parts.w.data_ptr() + 4 * t0, parts.idx.data_ptr() + 4 * t0, parts.n_parts,
-            parts.n_tok, target.data_ptr() + 4 * t0, labels.data_ptr() + 8 * t0, n,
-            lse.data_ptr() + 4 * t0, nll.data_ptr() + 4 * t0, ent.data_ptr() + 4 * t0,
-            amax.data_ptr() + 8 * t0, _stream(lse))
-
-
 def lm_head_ce(hidden: torch.Tensor, weight: torch.Tensor, labels: torch.Tensor,
                num_items_in_batch=None, v_chunk: int | None = None, need_grad: bool = True,
                weight_t: torch.Tensor | None = None, dh_scale: float = 1.0,
@@ -1825,10 +1866,11 @@ def lm_head_ce(hidden: torch.Tensor, weight: torch.Tensor, labels: torch.Tensor,
     and stored as ``dh_dtype`` (None without need_grad).
 
     With the gradient, the tokens go in blocks of at most 256 (one MFMA token tile). For each
-    block one statistics GEMM over the whole vocabulary keeps its fp16 logits in a [256, V]
-    buffer; the block's statistics are combined; its logits become the reference's fp16 gradient
-    G = fp16((softmax - onehot) 2^16 / denom) in place (the denominator is known up front); and
-    a split-K GEMM G . W writes the block's dH partials, summed once. W is read once per block;
+    block one GEMM over the whole vocabulary stores its fp16 logits in a [256, V] buffer; one
+    kernel per token row forms the statistics and turns the row into the reference's fp16
+    gradient G = fp16((softmax - onehot) 2^16 / denom) in place (the denominator is known up
+    front); and a split-K GEMM G . W writes the block's dH partials, summed once. W is read once
+    per block;
     no [N, V] array exists and no logit is recomputed (the reference holds [N, 8192] chunks and
     recomputes every logit, solution/ops.py:209-322). ``v_chunk`` (a multiple of 256) selects
     the single pass over vocabulary chunks instead (``LMHeadPass``: W read once in total, an
@@ -1858,9 +1900,9 @@ def lm_head_ce(hidden: torch.Tensor, weight: torch.Tensor, labels: torch.Tensor,
             hp.add_chunk(h, w[start:end], None if wt is None else wt[:, start:], start, lab)
         return hp.finish(lab, num_items_in_batch, w, dh_scale, dh_dtype)
 
-    parts = LMHeadPartials(lm_head_num_parts(V), n_tok, dev)
-    target = torch.zeros(n_tok, dtype=torch.float32, device=dev)
     if not need_grad or n_tok == 0:
+        parts = LMHeadPartials(lm_head_num_parts(V), n_tok, dev)
+        target = torch.zeros(n_tok, dtype=torch.float32, device=dev)
         if n_tok:
             _fwd_rows(h, w, lab, parts, target, 0, n_tok, None)
         lse, nll, ent, amax = lm_head_ce_combine(parts, target, lab)
@@ -1888,9 +1930,9 @@ def lm_head_ce(hidden: torch.Tensor, weight: torch.Tensor, labels: torch.Tensor,
     for t0, t1 in blocks:
         nb = t1 - t0
         zb = z[:nb]
-        _fwd_rows(h, w, lab, parts, target, t0, t1, zb)
-        _combine_rows(parts, target, lab, t0, t1, lse, nll, ent, amax)
-        lm_head_ce_grad_from_logits(zb, lab[t0:t1], lse[t0:t1], denom, V)
+        lm_head_ce_logits(h[t0:t1], w, zb)
+        lm_head_ce_rows(zb, V, lab[t0:t1], denom, lse[t0:t1], nll[t0:t1], ent[t0:t1],
+                        amax[t0:t1])
         s = splits[nb]
         dparts = dflat[: s * nb * d].view(s, nb, d)
         lm_head_ce_grad_hidden(zb, wt, V, dparts, accumulate=False)
