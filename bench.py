@@ -142,7 +142,10 @@ def cpu_baseline(seed=0):
     from oracle import stack as ostack
     from rus_amd import model as M
 
-    threads = max(1, min(len(os.sched_getaffinity(0)), 16))
+    # the host cores of this GPU's share of the box (its OMP_NUM_THREADS, 16 per GPU), at most
+    # the affinity mask
+    share = int(os.environ.get("OMP_NUM_THREADS", "16") or 16)
+    threads = max(1, min(len(os.sched_getaffinity(0)), share))
     torch.set_num_threads(threads)
     cfg = M.qwen2_1p5b()
     cfg1 = M.Qwen2Config(**{**cfg.__dict__, "num_hidden_layers": 1, "lora_dropout": 0.0})
@@ -171,6 +174,330 @@ def cpu_baseline(seed=0):
             "sample": (f"oracle (eager fp32 torch + numpy NF4 dequant) on 1 of 28 config-5 layers "
                        f"+ lm_head, one packed row of {n} tokens, fwd+bwd; per-step estimate "
                        f"28*{t_layer:.3f}s + {t_head:.3f}s (lm_head)")}
+
+
+# ---------------------------------------------------------------------------------------------
+# Per-configuration kernel records on cold inputs
+# ---------------------------------------------------------------------------------------------
+
+COLD_BYTES = 640 << 20  # input sets rotated per launch: > 2x the 256 MB last-level cache
+
+
+def _n_sets(set_bytes: int, cap: int = 64) -> int:
+    return max(2, min(cap, -(-COLD_BYTES // max(set_bytes, 1))))
+
+
+def _time_rotating(launch, n_sets: int, reps: int) -> float:
+    """Average µs per launch of ``launch(i)``, i cycling over the input sets: ``reps`` launches
+    captured into one HIP graph (so the host's per-call cost is out of the measurement, as in
+    the replayed training step), the graph replayed three times between one pair of HIP events
+    on the current stream. Each launch reads a set the previous n_sets - 1 launches did not."""
+    import torch
+
+    for i in range(min(n_sets, 4)):
+        launch(i)  # warm-up outside the graph
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for i in range(reps):
+            launch(i % n_sets)
+    graph.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(3):
+        graph.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    del graph
+    return e0.elapsed_time(e1) * 1e3 / (3 * reps)
+
+
+def _hbm(name, shape, us, nbytes, **extra):
+    gbps = nbytes / (us * 1e-6) / 1e9
+    return {"kernel": name, "shape": shape, "gpu_us": us, "bytes": nbytes, "gbps": gbps,
+            "bound": "hbm", "frac": gbps / HBM_PEAK_GBS, **extra}
+
+
+def _mfma(name, shape, us, flops, **extra):
+    tf = flops / (us * 1e-6) / 1e12
+    return {"kernel": name, "shape": shape, "gpu_us": us, "flops": flops, "tflops": tf,
+            "bound": "mfma", "frac": tf / FP16_PEAK_TFLOPS, **extra}
+
+
+def _nf4_bytes(n: int, n_absmax2: int) -> int:
+    return n // 2 + n // 64 + 4 * n_absmax2 + 1024 + 2 * n
+
+
+def config_batch_lengths(seed: int = 0):
+    from rus_amd.model import lengths_lognormal
+
+    return lengths_lognormal(4, seed=seed)
+
+
+def config_records(seed: int = 0, reps: int = 40) -> dict:
+    """GPU time per kernel of BASELINE configs 1-4 at their shapes, each launch reading inputs
+    not touched by the previous launches (rotating input sets of > 2x the last-level cache):
+    averages over back-to-back launches between one event pair, with the algorithmic bytes or
+    FLOPs and the fraction of the roofline."""
+    import torch
+
+    from rus_amd import kernels as K
+    from rus_amd import ops as O
+    from rus_amd import quant
+
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(seed)
+    out = {}
+
+    def nf4_job(shapes):
+        parts = [quant.quantize_nf4((torch.randn(r, c, device=dev, generator=g) * 0.02).half())
+                 for r, c in shapes]
+        fused, splits, offs, bases = quant.concat_segments(parts)
+        return fused, splits, offs, bases
+
+    def dequant_record(name, shapes):
+        fused, splits, offs, bases = nf4_job(shapes)
+        n = fused.shape[0] * fused.shape[1]
+        nb = _nf4_bytes(n, fused.absmax2.numel())
+        ns = _n_sets(nb)
+        sets = [(fused.packed.clone(), fused.absmax.clone(), fused.absmax2.clone(),
+                 torch.empty(n, dtype=torch.float16, device=dev)) for _ in range(ns)]
+        code2 = fused.code2.to(dev)
+
+        def launch(i):
+            p, a, a2, o = sets[i]
+            K.dequant_nf4_tensor(p, a, code2, a2, offs, fused.shape, out_buf=o,
+                                 split_bytes=splits, absmax2_bases=bases)
+        us = _time_rotating(launch, ns, reps)
+        return _hbm(name, list(fused.shape), us, nb, input_sets=ns)
+
+    # config 1: fused q|k|v dequant; residual + RMSNorm forward and backward [880, 1536]
+    c1 = [dequant_record("nf4_dequant qkv", [(1536, 1536), (256, 1536), (256, 1536)])]
+    N, D = 880, 1536
+    w = (1 + 0.05 * torch.randn(D, device=dev, generator=g)).half()
+    nbytes = 4 * N * D * 2 + 2 * D + 4 * N
+    ns = _n_sets(nbytes)
+    xs = [(torch.randn(N, D, device=dev, generator=g).half(),
+           torch.randn(N, D, device=dev, generator=g).half()) for _ in range(ns)]
+    fw = [K.rms_norm_fwd(x, w, 1e-6, residual=r) for x, r in xs]  # eager: the backward's inputs
+
+    def norm_fwd(i):
+        K.rms_norm_fwd(xs[i][0], w, 1e-6, residual=xs[i][1])
+    c1.append(_hbm("rmsnorm_fwd residual", [N, D], _time_rotating(norm_fwd, ns, reps), nbytes,
+                   input_sets=ns))
+
+    def norm_bwd(i):
+        y, h, rstd = fw[i]
+        K.rms_norm_bwd(xs[i][0], h, w, rstd, dresidual=xs[i][1])
+    c1.append(_hbm("rmsnorm_bwd dresidual", [N, D], _time_rotating(norm_bwd, ns, reps),
+                   5 * N * D * 2 + 2 * D + 4 * N, input_sets=ns))
+    out["1"] = c1
+    del xs, fw
+
+    # config 2: the lm_head CE forward + backward at N=2048, V=151936, chunk [256, V] logits
+    n2, V = 2048, 151936
+    h = torch.randn(n2, D, device=dev, generator=g).half()
+    W = (torch.randn(V, D, device=dev, generator=g) * 0.02).half()
+    lab = torch.randint(0, V, (n2,), device=dev, generator=g)
+    lab[torch.rand(n2, device=dev, generator=g) < 0.1] = -100
+    wt = K.lm_head_weight_t(W)
+    for _ in range(2):
+        K.lm_head_ce(h, W, lab, weight_t=wt)
+    torch.cuda.synchronize()
+    timer = K.KernelTimer()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(3):
+        K.lm_head_ce(h, W, lab, weight_t=wt)
+    e1.record()
+    torch.cuda.synchronize()
+    head_us = e0.elapsed_time(e1) * 1e3 / 3
+    with timer:
+        for _ in range(3):
+            K.lm_head_ce(h, W, lab, weight_t=wt)
+    summ = timer.summary()
+    flops = 2.0 * n2 * D * V
+    c2 = [_mfma("lm_head_ce fwd+bwd (whole head)", [n2, D, V], head_us, 2 * flops,
+                note="4*N*D*V over the whole head's time (logits GEMM, row statistics and "
+                     "gradient, hidden-gradient GEMM, split-K reduce)")]
+    for k in ("lmhead_ce_logits", "lmhead_ce_grad_hidden"):
+        r = summ[k]
+        us = r["ms"] * 1e3 / r["launches"]
+        c2.append(_mfma(k, [r["launches"] // 3, "launches per head"], us,
+                        r["flops"] / r["launches"], note="per launch (one token block)"))
+    for k in ("lmhead_ce_rows", "lmhead_dh_reduce"):
+        r = summ[k]
+        us = r["ms"] * 1e3 / r["launches"]
+        c2.append(_hbm(k, [r["launches"] // 3, "launches per head"], us, r["bytes"] / r["launches"]))
+    out["2"] = c2
+    del h, W, wt, lab
+
+    # config 3: attention prologue / epilogue on a lognormal 4-row batch
+    lens = config_batch_lengths(seed)
+    n3 = sum(lens)
+    cos, sin = O.rope_cache(2048, 128, 1e6, dev)
+    pos = torch.cat([torch.arange(L, device=dev) for L in lens])
+    per_tok_f, per_tok_b = 12296, 8712
+    ns = _n_sets(n3 * per_tok_f)
+    rs = [(torch.randn(n3, 2048, device=dev, generator=g).half(),
+           torch.randn(n3, 1536, device=dev, generator=g).half(),
+           torch.randn(n3, 256, device=dev, generator=g).half()) for _ in range(ns)]
+    qkv_out = [K.qkv_rope_fwd(q, cos, sin, pos, ql, vl) for q, ql, vl in rs]  # eager
+
+    def rope_f(i):
+        qkv, ql, vl = rs[i]
+        K.qkv_rope_fwd(qkv, cos, sin, pos, ql, vl)
+    c3 = [_hbm("rope_fwd lora", [n3, 12, 2, 128], _time_rotating(rope_f, ns, reps),
+               n3 * per_tok_f, input_sets=ns)]
+
+    def rope_b(i):
+        K.qkv_rope_bwd(*qkv_out[i], cos, sin, pos)
+    c3.append(_hbm("rope_bwd", [n3, 12, 2, 128], _time_rotating(rope_b, ns, reps),
+                   n3 * per_tok_b, input_sets=ns))
+    cu = torch.tensor([0] + list(torch.tensor(lens).cumsum(0).tolist()), dtype=torch.int32,
+                      device=dev)
+    att_flops = float(sum(2 * L * (L + 1) * 128 * 12 for L in lens))
+    att = [K.attn_varlen_fwd(*qkv_out[i], cu) for i in range(ns)]  # eager: the backward's inputs
+
+    def attn_f(i):
+        q, k, v = qkv_out[i]
+        K.attn_varlen_fwd(q, k, v, cu)
+    c3.append(_mfma("attn_varlen_fwd", [n3, 12, 2, 128], _time_rotating(attn_f, ns, reps),
+                    att_flops, note="causal FLOPs 4*h*d*sum L(L+1)/2"))
+
+    def attn_b(i):
+        q, k, v = qkv_out[i]
+        o, lse = att[i]
+        K.attn_varlen_bwd(o, q, k, v, o, lse, cu)
+    c3.append(_mfma("attn_varlen_bwd", [n3, 12, 2, 128], _time_rotating(attn_b, ns, reps),
+                    2.5 * att_flops))
+    out["3"] = c3
+    del rs, qkv_out, att
+
+    # config 4: MLP block: [gate|up] and down dequant, SwiGLU forward / backward [880, 17920]
+    c4 = [dequant_record("nf4_dequant gate|up", [(8960, 1536), (8960, 1536)]),
+          dequant_record("nf4_dequant down", [(1536, 8960)])]
+    I = 8960
+    nbf, nbb = N * 3 * I * 2, N * 5 * I * 2
+    ns = _n_sets(nbf)
+    gus = [torch.randn(N, 2 * I, device=dev, generator=g).half() for _ in range(ns)]
+    douts = [torch.randn(N, I, device=dev, generator=g).half() for _ in range(ns)]
+    c4.append(_hbm("swiglu_fwd", [N, 2 * I], _time_rotating(lambda i: K.mlp_glu_fwd(gus[i]), ns, reps),
+                   nbf, input_sets=ns))
+    c4.append(_hbm("swiglu_bwd in place", [N, 2 * I],
+                   _time_rotating(lambda i: K.mlp_glu_bwd(douts[i], gus[i]), ns, reps), nbb,
+                   input_sets=ns))
+    out["4"] = c4
+    return out
+
+
+def config_cpu_times(seed: int = 0) -> dict:
+    """CPU oracle times for the configuration records (bench.py's CPU-baseline leg): the same
+    operations on the host cores (fp32 torch / numpy restatement of the reference's arithmetic),
+    median of 3, bounded samples where the full shape would take minutes."""
+    import numpy as np
+    import torch
+
+    from oracle import ops as ref
+    from rus_amd import quant
+
+    g = torch.Generator().manual_seed(seed)
+    out = {}
+
+    def med(fn, n=3):
+        ts = []
+        for _ in range(n):
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+        return statistics.median(ts) * 1e6
+
+    def nf4(shapes):
+        parts = [quant.quantize_nf4((torch.randn(r, c, generator=g) * 0.02).half()) for r, c in shapes]
+        fused, splits, offs, bases = quant.concat_segments(parts)
+        args = (fused.packed.numpy(), fused.absmax.numpy(), fused.code2.numpy(),
+                fused.absmax2.numpy(), offs, fused.shape)
+        return lambda: ref.nf4_dequant(*args, split_bytes=splits, absmax2_bases=bases)
+
+    N, D, I = 880, 1536, 8960
+    x, res = torch.randn(N, D, generator=g).half(), torch.randn(N, D, generator=g).half()
+    w = (1 + 0.05 * torch.randn(D, generator=g)).half()
+    y, h, rstd = ref.rms_norm_fwd(x, w, 1e-6, residual=res)
+    out["1"] = {"nf4_dequant qkv": med(nf4([(1536, 1536), (256, 1536), (256, 1536)])),
+                "rmsnorm_fwd residual": med(lambda: ref.rms_norm_fwd(x, w, 1e-6, residual=res)),
+                "rmsnorm_bwd dresidual": med(lambda: ref.rms_norm_bwd(x, h, w, rstd, dresidual=res))}
+    # config 2 on 256 of the 2048 tokens (per-token work; scaled by 8)
+    V, n2 = 151936, 256
+    hh = torch.randn(n2, D, generator=g).half()
+    W = (torch.randn(V, D, generator=g) * 0.02).half()
+    lab = torch.randint(0, V, (n2,), generator=g)
+    t = med(lambda: ref.lm_head_ce(hh, W, lab, need_grad=True), n=1)
+    out["2"] = {"lm_head_ce fwd+bwd (whole head)": t * (2048 / n2)}
+    lens = config_batch_lengths(seed)
+    n3 = sum(lens)
+    cos, sin = ref.rope_tables(2048, 128, 1e6)
+    pos = torch.cat([torch.arange(L) for L in lens])
+    qkv = torch.randn(n3, 2048, generator=g).half()
+    ql, vl = torch.randn(n3, 1536, generator=g).half(), torch.randn(n3, 256, generator=g).half()
+    q, k, v = ref.qkv_rope_fwd(qkv, cos, sin, pos, ql, vl)
+    cu = [0] + list(np.cumsum(lens))
+    out["3"] = {"rope_fwd lora": med(lambda: ref.qkv_rope_fwd(qkv, cos, sin, pos, ql, vl)),
+                "rope_bwd": med(lambda: ref.qkv_rope_bwd(q, k, v, cos, sin, pos)),
+                "attn_varlen_fwd": med(lambda: ref.attention_varlen_fwd(q, k, v, cu), n=1),
+                "attn_varlen_bwd": med(lambda: ref.attention_varlen_bwd(q, q, k, v, cu), n=1)}
+    gg, uu = torch.randn(N, I, generator=g).half(), torch.randn(N, I, generator=g).half()
+    do = torch.randn(N, I, generator=g).half()
+    out["4"] = {"nf4_dequant gate|up": med(nf4([(8960, 1536), (8960, 1536)]), n=1),
+                "nf4_dequant down": med(nf4([(1536, 8960)]), n=1),
+                "swiglu_fwd": med(lambda: ref.swiglu_fwd(gg, uu)),
+                "swiglu_bwd in place": med(lambda: ref.swiglu_bwd(do, gg, uu))}
+    return out
+
+
+def elementwise_probe(reps: int = 5) -> None:
+    """Fixed launches for counter runs of the bandwidth-bound kernels at their BASELINE shapes,
+    each launch on input sets no earlier launch touched (so HBM, not the last-level cache,
+    serves them): RMSNorm forward / backward [880, 1536], RoPE forward (LoRA) / backward on the
+    config-3 batch, SwiGLU forward / backward [880, 17920]; plus 5 plain 128 MiB device copies
+    (the counters' calibration)."""
+    import torch
+
+    from rus_amd import kernels as K
+    from rus_amd import ops as O
+
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(0)
+    src = torch.empty(64 << 20, dtype=torch.float16, device=dev).normal_()
+    dst = torch.empty_like(src)
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+    N, D, I = 880, 1536, 8960
+    w = (1 + 0.05 * torch.randn(D, device=dev, generator=g)).half()
+    xs = [(torch.randn(N, D, device=dev, generator=g).half(),
+           torch.randn(N, D, device=dev, generator=g).half()) for _ in range(reps)]
+    fw = [K.rms_norm_fwd(x, w, 1e-6, residual=r) for x, r in xs]
+    for (x, r), (y, h, rstd) in zip(xs, fw):
+        K.rms_norm_bwd(x, h, w, rstd, dresidual=r)
+    lens = config_batch_lengths(0)
+    n3 = sum(lens)
+    cos, sin = O.rope_cache(2048, 128, 1e6, dev)
+    pos = torch.cat([torch.arange(L, device=dev) for L in lens])
+    rs = [(torch.randn(n3, 2048, device=dev, generator=g).half(),
+           torch.randn(n3, 1536, device=dev, generator=g).half(),
+           torch.randn(n3, 256, device=dev, generator=g).half()) for _ in range(reps)]
+    qkvs = [K.qkv_rope_fwd(q, cos, sin, pos, ql, vl) for q, ql, vl in rs]
+    for q, k, v in qkvs:
+        K.qkv_rope_bwd(q, k, v, cos, sin, pos)
+    gus = [torch.randn(N, 2 * I, device=dev, generator=g).half() for _ in range(reps)]
+    outs = [K.mlp_glu_fwd(gu) for gu in gus]
+    for gu, o in zip(gus, outs):
+        K.mlp_glu_bwd(o, gu)
+    torch.cuda.synchronize()
+    print(f"probe: {reps} launches each of rmsnorm fwd/bwd [{N},{D}], rope fwd/bwd "
+          f"[{n3} tokens], swiglu fwd/bwd [{N},{2 * I}] on distinct inputs", flush=True)
 
 
 def lmhead_probe(reps: int = 5) -> None:
@@ -226,7 +553,13 @@ def kernel_probe(reps: int = 5) -> None:
         *_, pend = K.rms_norm_fwd(x, lnw, 1e-6, residual=res, defer=True)
         ws.dequant_layer(0, norm=pend)
     torch.cuda.synchronize()
-    print(f"probe: {reps} four-segment dequants of layer 0 with a riding norm", flush=True)
+    print(f"probe: {reps} four-segment dequants of layer 0 with a riding norm forward", flush=True)
+    y, h, rstd = K.rms_norm_fwd(x, lnw, 1e-6, residual=res)
+    for _ in range(reps):
+        _, pend = K.rms_norm_bwd(x, h, lnw, rstd, dresidual=res, defer=True)
+        ws.dequant_layer(0, norm=pend)
+    torch.cuda.synchronize()
+    print(f"probe: {reps} four-segment dequants of layer 0 with a riding norm backward", flush=True)
 
 
 def measured_traffic(kernel: str):
@@ -241,6 +574,18 @@ def measured_traffic(kernel: str):
     return None
 
 
+def _graph_run(engine, model_opt, batches, steps, warmup):
+    """Captures the step's graphs for every batch bucket and times ``steps`` replays + AdamW."""
+    from rus_amd.graph import GraphedTrainStep
+
+    g = GraphedTrainStep(engine)
+    for b in batches:
+        g.prepare(b[0], b[1], b[2])
+    opt = flat_adamw(engine)[0]
+    secs, tokens, _, _ = timed_run(engine, opt, batches, steps, warmup, graph=g)
+    return tokens / secs, g
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -252,12 +597,15 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-eager", action="store_true")
     ap.add_argument("--no-resident", action="store_true")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip the per-configuration kernel records (BASELINE configs 1-4)")
     ap.add_argument("--no-graph", action="store_true",
                     help="time eager autograd steps instead of captured-graph replays")
     ap.add_argument("--roofline-steps", type=int, default=8)
     ap.add_argument("--stream-unit", choices=("model", "layer"), default="model",
                     help="per step, copy the packed model once (model) or each layer per pass "
-                         "through two one-layer slots (layer, the reference's policy)")
+                         "through two one-layer slots (layer, the reference's policy); the other "
+                         "is timed as an ablation")
     ap.add_argument("--recompute", choices=("off", "on"), default="off",
                     help="off: the forward keeps every layer's activations for the backward; on: "
                          "the backward recomputes them from the saved layer inputs (the "
@@ -270,10 +618,12 @@ def main() -> int:
                     help="dequant: NF4 -> fp16 workspace, then the library GEMM; fused: the "
                          "products decode NF4 inside their MFMA loop (rus_nf4_gemm)")
     ap.add_argument("--no-ablation", action="store_true",
-                    help="skip the timing of the other --recompute setting")
-    ap.add_argument("--probe", nargs="?", const="dequant", choices=("dequant", "lmhead"),
-                    help="only fixed launches for counter runs: copy + dequant (default) or the "
-                         "lm_head CE kernels at config 2")
+                    help="skip the timing of the other --recompute and --stream-unit settings")
+    ap.add_argument("--probe", nargs="?", const="dequant",
+                    choices=("dequant", "lmhead", "elementwise"),
+                    help="only fixed launches for counter runs: copy + dequant (default), the "
+                         "lm_head CE kernels at config 2, or the elementwise kernels on cold "
+                         "inputs")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs and measures one GPU only (asked for --gpus "
@@ -281,6 +631,9 @@ def main() -> int:
         return 2
     if args.probe == "lmhead":
         lmhead_probe()
+        return 0
+    if args.probe == "elementwise":
+        elementwise_probe()
         return 0
     if args.probe:
         kernel_probe()
@@ -290,6 +643,7 @@ def main() -> int:
 
     from rus_amd import model as M
     from rus_amd.eager_reference import eager_step_loss
+    from rus_amd.kernels import KernelTimer
     from rus_amd.ops import Qwen2FusedEngine, pack_varlen
 
     dev = torch.device("cuda:0")
@@ -299,6 +653,7 @@ def main() -> int:
     batches = make_batches(cfg, 8, args.rows, args.max_len, args.seed, dev)
     params = model.lora_parameters()
     opt = torch.optim.AdamW(params, lr=2e-4)
+    model_mib = torch.cuda.memory_allocated(dev) / 2**20  # the random model's device tensors
 
     # Configured engine: NF4 layers streamed per step from pinned host memory.
     recompute = args.recompute == "on"
@@ -310,7 +665,7 @@ def main() -> int:
     dominant = max(calib, key=lambda k: calib[k]["ms"])
     # Roofline pass (eager, same steps): the dominant kernel's launches bracketed by HIP events on
     # the stream they run on (events cannot time single kernels inside a replayed graph). Its
-    # peak allocation is the step's working set.
+    # peak allocation above the engine's resident buffers is the step's working set.
     torch.cuda.reset_peak_memory_stats(dev)
     base_alloc = torch.cuda.memory_allocated(dev)
     r_secs, r_tokens, _, summary = timed_run(engine, opt, batches, args.roofline_steps, 0,
@@ -327,8 +682,16 @@ def main() -> int:
             graph.prepare(b[0], b[1], b[2])
     graph_pool_mib = (torch.cuda.memory_reserved(dev) - reserved0) / 2**20
     opt_t, opt_kind = (opt, "foreach") if graph is None else flat_adamw(engine)
+    torch.cuda.synchronize()
+    torch.cuda.reset_peak_memory_stats(dev)
     secs, tokens, per_step, _ = timed_run(engine, opt_t, batches, args.steps, args.warmup,
                                           graph=graph)
+    device_peak = {"max_allocated_mib": torch.cuda.max_memory_allocated(dev) / 2**20,
+                   "max_reserved_mib": torch.cuda.max_memory_reserved(dev) / 2**20,
+                   "model_tensors_mib": model_mib,
+                   "note": "whole process during the timed replays: the random model's device "
+                           "tensors, the engine's two whole-model NF4 buffers, workspaces, "
+                           "the embedding / lm_head and its transpose, graph pools"}
     value = tokens / secs
     d = summary[dominant]
     avg_ms = d["ms"] / d["launches"]
@@ -339,9 +702,10 @@ def main() -> int:
     else:
         achieved = d["bytes"] / (d["ms"] / 1e3) / 1e9
         roof = {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": achieved / HBM_PEAK_GBS, "traffic": measured_traffic(dominant)}
-    from rus_amd.kernels import KernelTimer
-
+                "frac": achieved / HBM_PEAK_GBS, "traffic": measured_traffic(dominant),
+                "traffic_source": f"profiles/{dominant}_traffic_config5.txt (FETCH_SIZE / "
+                                  "WRITE_SIZE counter runs of bench.py --probe, both launch "
+                                  "variants, scaled by a plain copy's counters)"}
     roof.update({"kernel": dominant, "avg_launch_ms": avg_ms, "launches": d["launches"],
                  "event_pair_overhead_ms": KernelTimer.pair_overhead_ms(),
                  "per_launch": d["flops"] / d["launches"] if dominant in MFMA_KERNELS
@@ -359,11 +723,14 @@ def main() -> int:
                    "tokens_per_step": tokens / args.steps, "lora": "r16 alpha32 dropout0.05 q,v",
                    "stream_unit": args.stream_unit, "recompute": args.recompute,
                    "overlap": "on" if overlap else "off", "gemm": args.gemm,
+                   "lm_head": "token blocks of <= 256, [block, V] logits buffer, no [N, V]",
                    "optimizer": f"AdamW lr 2e-4 ({opt_kind}"
                                 + (", one flat LoRA buffer)" if graph is not None else ")")},
         "roofline": roof,
         "median_step_tokens_per_s": statistics.median(n / sec for sec, n in per_step),
         "peak_hbm_mib": (peak - base_alloc) / 2**20,
+        "peak_hbm_mib_note": "working set of one step above the resident buffers (eager pass)",
+        "device_peak": device_peak,
         "kernels_calibration": kernel_rates(calib, 2),
         "step_mode": "hip_graph" if graph is not None else "eager",
         "eager_fused_tokens_per_s": r_tokens / r_secs,
@@ -372,54 +739,50 @@ def main() -> int:
     }
     lm = [calib[k] for k in MFMA_KERNELS if k in calib]
     if lm:
-        # rate of the head's MFMA launches; and 4*N*D*V (one forward and one backward product)
-        # over the whole head's kernel time, the in-place gradient pass included
         out["lm_head_ce_tflops"] = sum(r["flops"] for r in lm) / (sum(r["ms"] for r in lm) / 1e3) / 1e12
-        fwd = sum(calib[k]["flops"] for k in ("lmhead_ce_fwd", "lmhead_ce_fwd_keep") if k in calib)
-        head_ms = sum(r["ms"] for r in lm) + sum(
-            calib[k]["ms"] for k in ("lmhead_ce_grad_from_logits",) if k in calib)
-        out["lm_head_ce_tflops_credited_4NDV"] = 2.0 * fwd / (head_ms / 1e3) / 1e12
     if "nf4_dequant" in calib:
         r = calib["nf4_dequant"]
         out["nf4_dequant_gbps"] = r["bytes"] / (r["ms"] / 1e3) / 1e9
+    del graph
+    torch.cuda.empty_cache()
 
-    if not args.no_ablation:
-        # The other activation policy: same streamed weights, graphs, batches; its throughput
-        # and its working set (peak allocation of one eager step, as for the headline engine).
+    if not args.no_ablation and not args.no_graph:
+        # The other activation policy and the other streaming unit: same batches, graphs.
+        other = "on" if not recompute else "off"
         eng_a = Qwen2FusedEngine(model, dev, resident_weights=False, stream_unit=args.stream_unit,
                                  recompute=not recompute, overlap=overlap, gemm=args.gemm)
         torch.cuda.synchronize()
         torch.cuda.reset_peak_memory_stats(dev)
         base_a = torch.cuda.memory_allocated(dev)
         timed_run(eng_a, opt, batches, 1, 0)
-        peak_a = (torch.cuda.max_memory_allocated(dev) - base_a) / 2**20
-        g_a = None
-        if graph is not None:
-            g_a = GraphedTrainStep(eng_a)
-            for b in batches:
-                g_a.prepare(b[0], b[1], b[2])
-        opt_a = opt if g_a is None else flat_adamw(eng_a)[0]
-        s_a, t_a, _, _ = timed_run(eng_a, opt_a, batches, min(args.steps, 16), 1, graph=g_a)
-        other = "on" if not recompute else "off"
-        out[f"recompute_{other}_tokens_per_s"] = t_a / s_a
-        out[f"recompute_{other}_peak_hbm_mib"] = peak_a
+        out[f"recompute_{other}_peak_hbm_mib"] = (torch.cuda.max_memory_allocated(dev) - base_a) / 2**20
+        out[f"recompute_{other}_tokens_per_s"], g_a = _graph_run(eng_a, None, batches,
+                                                                 min(args.steps, 16), 1)
         del eng_a, g_a
+        unit = "layer" if args.stream_unit == "model" else "model"
+        eng_u = Qwen2FusedEngine(model, dev, resident_weights=False, stream_unit=unit,
+                                 recompute=recompute, overlap=False, gemm=args.gemm)
+        out[f"stream_unit_{unit}_tokens_per_s"], g_u = _graph_run(eng_u, None, batches,
+                                                                   min(args.steps, 16), 1)
+        del eng_u, g_u
+        torch.cuda.empty_cache()
 
-    if not args.no_resident:
+    if not args.no_resident and not args.no_graph:
         eng_r = Qwen2FusedEngine(model, dev, resident_weights=True, recompute=recompute,
                                  overlap=overlap, gemm=args.gemm)
-        g_r = None
-        if graph is not None:
-            g_r = GraphedTrainStep(eng_r)
-            for b in batches:
-                g_r.prepare(b[0], b[1], b[2])
-        opt_r = opt if g_r is None else flat_adamw(eng_r)[0]
-        s_r, t_r, _, _ = timed_run(eng_r, opt_r, batches, min(args.steps, 16), 1, graph=g_r)
-        out["resident_weights_tokens_per_s"] = t_r / s_r
-        del eng_r
+        out["resident_weights_tokens_per_s"], g_r = _graph_run(eng_r, None, batches,
+                                                                min(args.steps, 16), 1)
+        del eng_r, g_r
+        torch.cuda.empty_cache()
 
     if not args.no_eager:
-        eng_e = Qwen2FusedEngine(model, dev, resident_weights=False)
+        # Unfused eager autograd step (transformers-style stack, fp16 [N, V] logits): with every
+        # fused engine and graph of this run freed, its device peak is comparable with the timed
+        # run's (both include the random model's own tensors).
+        del engine
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+        eng_e = Qwen2FusedEngine(model, dev, resident_weights=True)
         b = batches[0]
         pb = pack_varlen(*(t.to(dev) for t in b[:3]))
         torch.cuda.synchronize()
@@ -436,12 +799,30 @@ def main() -> int:
         out["eager_ms_per_step"] = (time.perf_counter() - t0) / 2 * 1e3
         out["eager_tokens_per_s"] = b[3] / (out["eager_ms_per_step"] / 1e3)
         out["eager_peak_hbm_mib"] = (torch.cuda.max_memory_allocated(dev) - base_e) / 2**20
+        out["eager_device_peak_mib"] = torch.cuda.max_memory_allocated(dev) / 2**20
         del eng_e
+        torch.cuda.empty_cache()
+
+    records = None
+    if not args.no_configs:
+        records = config_records(args.seed)
+        torch.cuda.empty_cache()
 
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(args.seed)
+        if records is not None:
+            cpu = config_cpu_times(args.seed)
+            for c, recs in records.items():
+                for r in recs:
+                    t = cpu.get(c, {}).get(r["kernel"])
+                    if t is not None:
+                        r["cpu_us"] = t
+                        r["cpu_cores"] = out["cpu_baseline"]["cores"]
+                        r["speedup"] = t / r["gpu_us"]
     else:
         out["cpu_baseline"] = None
+    if records is not None:
+        out["configs"] = records
     print(json.dumps(out), flush=True)
     return 0
 
