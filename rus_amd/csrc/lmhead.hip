@@ -38,8 +38,8 @@ constexpr int kBM = 256, kBN = 256, kBK = 64;
 constexpr int kThreads = 256;
 constexpr int kWM = 128, kWN = 128;
 constexpr int kMT = kWM / 32, kNT = kWN / 32;
-constexpr int kTileBytes = kBM * kBK * 2;  // one operand, one stage: 32 KiB
-constexpr int kSmemBytes = 4 * kTileBytes;  // 2 stages x (A, B) = 128 KiB
+constexpr int kTileBytes = kBM * kBK * 2;  // 32 KiB
+constexpr int kSmemBytes = 4 * kTileBytes;  // 128 KiB: the mainloop's four stages, the epilogues' staging
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kPrescale = 65536.0f;  // solution/ops.py:171
 
@@ -58,11 +58,6 @@ struct Tile {
   int m0, n0, split;
 };
 
-// Byte offset of 16-byte chunk `chunk` (0..7) of row `row` in a [256][64] fp16 LDS tile.
-__device__ __forceinline__ uint32_t lds_off(int row, int chunk) {
-  return row * (kBK * 2) + ((chunk ^ (row & 7) ^ ((row >> 3) & 1)) << 4);
-}
-
 __device__ __forceinline__ bool tile_of(const GemmArgs& g, Tile& t) {
   const int total = g.tiles_m * g.tiles_n * g.splits;
   const int per_xcd = (total + 7) >> 3;
@@ -77,126 +72,157 @@ __device__ __forceinline__ bool tile_of(const GemmArgs& g, Tile& t) {
   return true;
 }
 
-// The 16-byte operand fragments of MFMA step kk (16 of K) for this wave's 128x128 tile.
-__device__ __forceinline__ void load_frags(const char* sa, int arow, int brow, int half, int asw,
-                                           int bsw, int kk, f16x8 (&fa)[kMT], f16x8 (&fb)[kNT]) {
-  const char* sb = sa + kTileBytes;
-  const int ch = kk * 2 + half;
-  const char* pa = sa + arow * (kBK * 2) + ((ch ^ asw) << 4);
-  const char* pb = sb + brow * (kBK * 2) + ((ch ^ bsw) << 4);
-#pragma unroll
-  for (int mt = 0; mt < kMT; ++mt) fa[mt] = *reinterpret_cast<const f16x8*>(pa + mt * 32 * (kBK * 2));
-#pragma unroll
-  for (int nt = 0; nt < kNT; ++nt) fb[nt] = *reinterpret_cast<const f16x8*>(pb + nt * 32 * (kBK * 2));
-}
-
-// One LDS stage (kBK of K) of MFMAs for this wave's 128x128 tile. The fragments of step kk+1
-// are read from LDS while step kk's 16 MFMAs issue (two register sets), so each read's latency
-// is covered by a block of MFMAs instead of stalling the first MFMA that needs it.
-__device__ __forceinline__ void mma_stage(const char* sa, int arow, int brow, int half, int asw,
-                                          int bsw, f32x16 (&acc)[kMT][kNT]) {
-  f16x8 fa[2][kMT], fb[2][kNT];
-  load_frags(sa, arow, brow, half, asw, bsw, 0, fa[0], fb[0]);
-#pragma unroll
-  for (int kk = 0; kk < kBK / 16; ++kk) {
-    const int cur = kk & 1;
-    if (kk + 1 < kBK / 16)
-      load_frags(sa, arow, brow, half, asw, bsw, kk + 1, fa[cur ^ 1], fb[cur ^ 1]);
-#pragma unroll
-    for (int mt = 0; mt < kMT; ++mt)
-#pragma unroll
-      for (int nt = 0; nt < kNT; ++nt)
-        acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[cur][mt], fb[cur][nt],
-                                                             acc[mt][nt], 0, 0, 0);
-  }
-  // Issue order: reads of steps 0 and 1, MFMAs of step 0, reads of step 2, MFMAs of step 1,
-  // reads of step 3, MFMAs of steps 2 and 3.
-  static_assert(kBK / 16 == 4 && kMT * kNT == 16 && kMT + kNT == 8, "schedule assumes 4x4 tiles");
-  __builtin_amdgcn_sched_group_barrier(0x100, 16, 0);
-  __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);
-  __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
-  __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);
-  __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
-  __builtin_amdgcn_sched_group_barrier(0x008, 32, 0);
-}
-
 // acc[mt][nt] += A[m0 + wm*128 + mt*32 .. +32, k] . B[n0 + wn*128 + nt*32 .. +32, k]^T over the
 // split's K range. Accumulator layout (v_mfma_f32_32x32x16_f16): register r of lane l holds
 // row 8*(r/4) + 4*(l/32) + r%4, column l%32 of the 32x32 tile.
 //
-// Register budget (one wave per SIMD, 512 registers): 256 accumulators, 64 for the next stage's
-// global loads, 32 for MFMA operands; addresses are kept small: global loads use a uniform base
-// plus a 32-bit byte offset per row (the host checks that every operand is < 4 GiB), and LDS
-// addresses are one per-lane base plus immediate offsets, because the swizzle only depends on
-// row bits 0..3, which the 32-row steps between i / mt do not change.
+// Pipeline: K is staged 32 at a time through four LDS buffers of 32 KiB (A then B, 256 rows x
+// 64 bytes each). Global memory is copied straight into LDS (global_load_lds_dwordx4: each lane's
+// 16 bytes land at buffer + lane * 16), three stages ahead of the MFMAs, so no register holds a
+// tile in flight and the 256 accumulators stay in AGPRs. The 16-byte chunk c of row r is stored
+// at chunk c ^ ((r >> 2) & 3) of its 64-byte row, which a lane realises by loading the chunk
+// that belongs at its position; the MFMAs' 16-byte fragment reads (16 consecutive rows per quarter
+// wave, one chunk) then hit all 64 banks once. The fragment reads are explicit ds_read_b128 with
+// explicit lgkmcnt waits (the compiler would otherwise wait for every LDS-bound global load before
+// any LDS read); vmcnt waits and the one barrier per stage sit inside the stage's second K step,
+// so the MFMA pipe keeps busy across stages.
+typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void* lds_void_ptr;
+
+constexpr int kDK = 32;                  // K per LDS stage
+constexpr int kStageBytes = 2 * kBM * kDK * 2;  // A + B: 32 KiB
+constexpr int kNStages = 4;
+static_assert(kNStages * kStageBytes == kSmemBytes, "stages fill the kernel's LDS");
+
+template <int OFF>
+__device__ __forceinline__ u32x4v lds_read16(uint32_t addr) {
+  u32x4v v;
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF));
+  return v;
+}
+
+// The 8 fragments (4 A rows-groups, 4 B row-groups) of one K step of 16 from LDS addresses a / b.
+__device__ __forceinline__ void read_frags(uint32_t a, uint32_t b, u32x4v (&fa)[kMT],
+                                           u32x4v (&fb)[kNT]) {
+  fa[0] = lds_read16<0>(a);
+  fa[1] = lds_read16<2048>(a);
+  fa[2] = lds_read16<4096>(a);
+  fa[3] = lds_read16<6144>(a);
+  fb[0] = lds_read16<0>(b);
+  fb[1] = lds_read16<2048>(b);
+  fb[2] = lds_read16<4096>(b);
+  fb[3] = lds_read16<6144>(b);
+}
+
+// Every LDS read issued so far has returned; ties the fragments so that no MFMA using them is
+// scheduled before the wait.
+__device__ __forceinline__ void wait_frags(u32x4v (&fa)[kMT], u32x4v (&fb)[kNT]) {
+  asm volatile("s_waitcnt lgkmcnt(0)"
+               : "+v"(fa[0]), "+v"(fa[1]), "+v"(fa[2]), "+v"(fa[3]), "+v"(fb[0]), "+v"(fb[1]),
+                 "+v"(fb[2]), "+v"(fb[3]));
+}
+
+__device__ __forceinline__ void mma16(const u32x4v (&fa)[kMT], const u32x4v (&fb)[kNT],
+                                      f32x16 (&acc)[kMT][kNT]) {
+#pragma unroll
+  for (int mt = 0; mt < kMT; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < kNT; ++nt)
+      acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+          __builtin_bit_cast(f16x8, fa[mt]), __builtin_bit_cast(f16x8, fb[nt]), acc[mt][nt], 0,
+          0, 0);
+}
+
+// s_waitcnt vmcnt(n) for n in {0, 8, 16, 24} (expcnt and lgkmcnt not waited on).
+__device__ __forceinline__ void wait_vm(int n) {
+  if (n >= 24)
+    __builtin_amdgcn_s_waitcnt((24 & 15) | ((24 >> 4) << 14) | (7 << 4) | (15 << 8));
+  else if (n >= 16)
+    __builtin_amdgcn_s_waitcnt((16 & 15) | ((16 >> 4) << 14) | (7 << 4) | (15 << 8));
+  else if (n >= 8)
+    __builtin_amdgcn_s_waitcnt(8 | (7 << 4) | (15 << 8));
+  else
+    __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8));
+}
+
 __device__ __forceinline__ void mainloop(const GemmArgs& g, const Tile& tl, char* smem,
                                          f32x16 (&acc)[kMT][kNT]) {
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int wm = wave >> 1, wn = wave & 1;
   const int kb = tl.split * g.k_per_split;
   const int ke = min(kb + g.k_per_split, g.K);
-  const int KT = ke > kb ? (ke - kb) / kBK : 0;
-
-  const int lrow = t >> 3, lch = t & 7;
-  uint32_t oa[8], ob[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    // Rows past the matrix edge re-read the last row: finite values the epilogues discard.
-    const int ra_ = min(tl.m0 + lrow + 32 * i, g.M - 1);
-    const int rb_ = min(tl.n0 + lrow + 32 * i, g.N - 1);
-    oa[i] = static_cast<uint32_t>((ra_ * g.lda + kb + lch * 8) * 2);
-    ob[i] = static_cast<uint32_t>((rb_ * g.ldb + kb + lch * 8) * 2);
-  }
-  const char* gA = reinterpret_cast<const char*>(g.A);
-  const char* gB = reinterpret_cast<const char*>(g.B);
-  const uint32_t so = lds_off(lrow, lch);  // store offset of row lrow; row lrow + 32i adds 4096*i
+  const int KT = ke > kb ? (ke - kb) / kDK : 0;
 #pragma unroll
   for (int mt = 0; mt < kMT; ++mt)
 #pragma unroll
     for (int nt = 0; nt < kNT; ++nt) acc[mt][nt] = f32x16{};
-
-  u32x4 ra[8], rb[8];
-  if (KT > 0) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      ra[i] = *reinterpret_cast<const u32x4*>(gA + oa[i]);
-      rb[i] = *reinterpret_cast<const u32x4*>(gB + ob[i]);
-    }
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      *reinterpret_cast<u32x4*>(smem + so + 4096 * i) = ra[i];
-      *reinterpret_cast<u32x4*>(smem + kTileBytes + so + 4096 * i) = rb[i];
-    }
-  }
-  __syncthreads();
-
-  const int arow = wm * kWM + (lane & 31);
-  const int brow = wn * kWN + (lane & 31);
-  const int half = lane >> 5;
-  const int asw = (arow & 7) ^ ((arow >> 3) & 1);
-  const int bsw = (brow & 7) ^ ((brow >> 3) & 1);
-  // Steady state: load stage kt+1 into registers, compute stage kt, store stage kt+1, barrier.
-  for (int kt = 0; kt + 1 < KT; ++kt) {
-    const char* nA = gA + (kt + 1) * (kBK * 2);
-    const char* nB = gB + (kt + 1) * (kBK * 2);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      ra[i] = *reinterpret_cast<const u32x4*>(nA + oa[i]);
-      rb[i] = *reinterpret_cast<const u32x4*>(nB + ob[i]);
-    }
-    // Keep the next stage's loads ahead of this stage's MFMAs so their latency is hidden.
-    __builtin_amdgcn_sched_barrier(0);
-    mma_stage(smem + (kt & 1) * 2 * kTileBytes, arow, brow, half, asw, bsw, acc);
-    __builtin_amdgcn_sched_barrier(0);
-    char* da = smem + ((kt + 1) & 1) * 2 * kTileBytes;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      *reinterpret_cast<u32x4*>(da + so + 4096 * i) = ra[i];
-      *reinterpret_cast<u32x4*>(da + kTileBytes + so + 4096 * i) = rb[i];
-    }
+  if (KT == 0) {
     __syncthreads();
+    return;
   }
-  if (KT > 0) mma_stage(smem + ((KT - 1) & 1) * 2 * kTileBytes, arow, brow, half, asw, bsw, acc);
+  // Loads: instruction i of wave w fills rows 64i + 16w .. +16 of A (and of B), 64 bytes each;
+  // lane l covers row 64i + 16w + l/4 at position l%4, i.e. the chunk (l%4) ^ ((l/16) & 3).
+  const int lrow = 16 * wave + (lane >> 2);
+  const int lchunk = (lane & 3) ^ ((lane >> 4) & 3);
+  const char* gA = reinterpret_cast<const char*>(g.A);
+  const char* gB = reinterpret_cast<const char*>(g.B);
+  uint32_t oa[4], ob[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    // Rows past the matrix edge re-read the last row: finite values the epilogues discard.
+    const int ra_ = min(tl.m0 + lrow + 64 * i, g.M - 1);
+    const int rb_ = min(tl.n0 + lrow + 64 * i, g.N - 1);
+    oa[i] = static_cast<uint32_t>((ra_ * g.lda + kb + lchunk * 8) * 2);
+    ob[i] = static_cast<uint32_t>((rb_ * g.ldb + kb + lchunk * 8) * 2);
+  }
+  auto issue = [&](int k) {  // stage k's 8 copies into buffer k % 4
+    char* st = smem + (k & (kNStages - 1)) * kStageBytes;
+    const int kbytes = k * (kDK * 2);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      __builtin_amdgcn_global_load_lds(gA + oa[i] + kbytes,
+                                       (lds_void_ptr)(st + (64 * i + 16 * wave) * 64), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(gB + ob[i] + kbytes,
+                                       (lds_void_ptr)(st + kBM * 64 + (64 * i + 16 * wave) * 64),
+                                       16, 0, 0);
+    }
+  };
+  const int pre = min(kNStages, KT);
+  for (int k = 0; k < pre; ++k) issue(k);
+  wait_vm(8 * (pre - 1));  // stage 0 landed (this wave's copies)
+  __builtin_amdgcn_s_barrier();  // ... and every wave's
+  // Fragment addresses: row wm*128 + (l & 31) (+ 32 mt, immediate), chunk 2 kk + l/32 stored at
+  // chunk ^ ((l >> 2) & 3).
+  const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void_ptr)smem));
+  const int sw = (lane >> 2) & 3, half = lane >> 5;
+  const uint32_t a0 = lds0 + (wm * kWM + (lane & 31)) * 64 + (((0 + half) ^ sw) << 4);
+  const uint32_t a1 = lds0 + (wm * kWM + (lane & 31)) * 64 + (((2 + half) ^ sw) << 4);
+  const uint32_t b0 = a0 - wm * kWM * 64 + kBM * 64 + wn * kWN * 64;
+  const uint32_t b1 = a1 - wm * kWM * 64 + kBM * 64 + wn * kWN * 64;
+  u32x4v fa0[kMT], fb0[kNT], fa1[kMT], fb1[kNT];
+  read_frags(a0, b0, fa0, fb0);
+  wait_frags(fa0, fb0);
+  for (int k = 0; k < KT; ++k) {
+    const uint32_t sb = (k & (kNStages - 1)) * kStageBytes;
+    read_frags(a1 + sb, b1 + sb, fa1, fb1);  // step 1 of stage k
+    __builtin_amdgcn_sched_barrier(0);
+    mma16(fa0, fb0, acc);  // step 0 of stage k
+    __builtin_amdgcn_sched_barrier(0);
+    wait_frags(fa1, fb1);
+    if (k + 1 < KT) {
+      // Stage k + 1 has landed for every wave, and every wave has read stage k: its buffer takes
+      // stage k + 4.
+      wait_vm(8 * min(2, KT - 2 - k));
+      __builtin_amdgcn_s_barrier();
+      if (k + kNStages < KT) issue(k + kNStages);
+      const uint32_t nb = ((k + 1) & (kNStages - 1)) * kStageBytes;
+      read_frags(a0 + nb, b0 + nb, fa0, fb0);  // step 0 of stage k + 1
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    mma16(fa1, fb1, acc);  // step 1 of stage k
+    __builtin_amdgcn_sched_barrier(0);
+    if (k + 1 < KT) wait_frags(fa0, fb0);
+  }
   __syncthreads();  // the epilogues reuse the LDS
 }
 
