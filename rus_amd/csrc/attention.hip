@@ -185,7 +185,7 @@ __device__ __forceinline__ f16x8 frag_t(const f16* t, int row, int s, int h) {
 __device__ __forceinline__ f16x8 frag_acc(const f32x16& c, int s) {
   f16x8 r;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) r[i] = static_cast<_Float16>(c[8 * s + i]);
+  for (int i = 0; i < 8; ++i) r[i] = from_f32<f16>(c[8 * s + i]);
   return r;
 }
 
@@ -213,7 +213,7 @@ __device__ __forceinline__ void store_tile_row(f16* row, const float (&x)[16], i
   for (int r4 = 0; r4 < 4; ++r4) {
     f16x4 w;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) w[i] = static_cast<_Float16>(x[4 * r4 + i]);
+    for (int i = 0; i < 4; ++i) w[i] = from_f32<f16>(x[4 * r4 + i]);
     *reinterpret_cast<f16x4*>(row + d * 32 + 8 * r4 + 4 * h) = w;
   }
 }
@@ -592,7 +592,7 @@ __device__ __forceinline__ void attn_bwd_dkdv_block(const AttnArgs& a, int blk, 
       const int key = k0 + acc_row(r, h);
       if (key < end)
         out[(static_cast<int64_t>(key) * a.h_kv + g) * kHD + wave * 32 + col] =
-            static_cast<f16>(acc[r]);
+            from_f32<f16>(acc[r]);
     }
   }
 }

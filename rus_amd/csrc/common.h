@@ -41,18 +41,28 @@ __device__ __forceinline__ void load_f32(const T* __restrict__ p, float (&out)[N
   for (int i = 0; i < N; ++i) out[i] = static_cast<float>(t.v[i]);
 }
 
+// fp32 -> T (round to nearest even) of the fp32 value x as it stands. The empty asm makes x
+// opaque: without it the compiler may fold a preceding fp32 product into the conversion as a
+// mixed-precision FMA (v_fma_mixlo_f16), which rounds the exact product once to fp16 instead of
+// first to fp32 and then to fp16 — a different result in rare halfway cases.
+template <typename T>
+__device__ __forceinline__ T from_f32(float x) {
+  if constexpr (sizeof(T) < sizeof(float)) asm("" : "+v"(x));
+  return static_cast<T>(x);
+}
+
 template <typename T, int N>
 __device__ __forceinline__ void store_from_f32(T* __restrict__ p, const float (&in)[N]) {
   Pack<T, N> t;
 #pragma unroll
-  for (int i = 0; i < N; ++i) t.v[i] = static_cast<T>(in[i]);
+  for (int i = 0; i < N; ++i) t.v[i] = from_f32<T>(in[i]);
   *reinterpret_cast<Pack<T, N>*>(p) = t;
 }
 
 // Round through the storage type (fp32 -> T -> fp32), i.e. what a T-typed intermediate holds.
 template <typename T>
 __device__ __forceinline__ float round_to(float x) {
-  return static_cast<float>(static_cast<T>(x));
+  return static_cast<float>(from_f32<T>(x));
 }
 
 // Sum over the 64 lanes of a wavefront; every lane receives the total.

@@ -103,8 +103,8 @@ __global__ __launch_bounds__(kThreads) void dropout_fwd_kernel(const T* __restri
     if (e >= total) break;
     const int64_t row = e / s.n_cols, col = e - row * s.n_cols;
     const float v = static_cast<float>(x[row * s.stride_x + col]);
-    out_a[row * s.stride_a + col] = static_cast<T>((ma >> j) & 1u ? v * s.scale_a : 0.0f);
-    out_b[row * s.stride_b + col] = static_cast<T>((mb >> j) & 1u ? v * s.scale_b : 0.0f);
+    out_a[row * s.stride_a + col] = from_f32<T>((ma >> j) & 1u ? v * s.scale_a : 0.0f);
+    out_b[row * s.stride_b + col] = from_f32<T>((mb >> j) & 1u ? v * s.scale_b : 0.0f);
   }
 }
 
@@ -146,7 +146,7 @@ __global__ __launch_bounds__(kThreads) void dropout_bwd_add_kernel(T* __restrict
     const float ta = round_to<T>((ma >> j) & 1u ? static_cast<float>(ga[row * s.stride_a + col]) * s.scale_a : 0.0f);
     const float tb = round_to<T>((mb >> j) & 1u ? static_cast<float>(gb[row * s.stride_b + col]) * s.scale_b : 0.0f);
     T* p = acc + row * s.stride_x + col;
-    *p = static_cast<T>(round_to<T>(static_cast<float>(*p) + ta) + tb);
+    *p = from_f32<T>(round_to<T>(static_cast<float>(*p) + ta) + tb);
   }
 }
 

@@ -227,7 +227,7 @@ __device__ __forceinline__ void mainloop(const GemmArgs& g, const Tile& tl, char
 }
 
 __device__ __forceinline__ float round16(float x) {
-  return static_cast<float>(static_cast<_Float16>(x));
+  return static_cast<float>(from_f32<f16>(x));
 }
 
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
@@ -255,7 +255,7 @@ __device__ __forceinline__ void store_tile_tv(char* smem, const GemmArgs& g, con
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int row = vrow0 + mt * 32 + 8 * q + 4 * h + e;
-          v[e] = static_cast<_Float16>(row < g.M ? value(mt, nt, q * 4 + e, row) : 0.0f);
+          v[e] = from_f32<f16>(row < g.M ? value(mt, nt, q * 4 + e, row) : 0.0f);
         }
         const int col = wm * kWM + mt * 32 + 8 * q + 4 * h;  // vocab column within the tile
         const int pq = (col >> 2) ^ ((trow & 31) << 1);
@@ -559,7 +559,7 @@ __global__ __launch_bounds__(kZgThreads) void lmhead_grad_from_logits_kernel(
       const float z = static_cast<float>(v[u][e]);
       const float pr = exp2_fast(__builtin_fmaf(z, kLog2e, -l2));
       const float gv = (pr - (c + e == lab ? 1.0f : 0.0f)) * scale;
-      o[e] = static_cast<_Float16>(c + e < n_vocab ? gv : 0.0f);
+      o[e] = from_f32<f16>(c + e < n_vocab ? gv : 0.0f);
     }
     *reinterpret_cast<f16x8*>(row + c) = o;
   }
@@ -653,7 +653,7 @@ __global__ __launch_bounds__(kZgThreads) void lmhead_chunk_scale_kernel(
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const float pr = exp2_fast(__builtin_fmaf(static_cast<float>(v[u][e]), kLog2e, -mb));
-      o[e] = static_cast<_Float16>(c + e < n_vocab ? pr : 0.0f);
+      o[e] = from_f32<f16>(c + e < n_vocab ? pr : 0.0f);
     }
     *reinterpret_cast<f16x8*>(row + c) = o;
   }
@@ -829,7 +829,7 @@ __global__ __launch_bounds__(kRowThreads) void lmhead_rows_kernel(
         const int c = 8 * p + e;
         const float pr = exp2_fast(__builtin_fmaf(static_cast<float>(v[u][e]), kLog2e, -l2));
         const float gv = (pr - (c == lab ? 1.0f : 0.0f)) * scale;
-        o[e] = static_cast<_Float16>(c < n_vocab ? gv : 0.0f);
+        o[e] = from_f32<f16>(c < n_vocab ? gv : 0.0f);
       }
       *reinterpret_cast<f16x8*>(row + 8 * p) = o;
     }
@@ -928,7 +928,7 @@ __global__ __launch_bounds__(256) void dh_reduce_kernel(const float* __restrict_
     for (int64_t j = i; j < n && j < i + 4; ++j) {
       float s = parts[j];
       for (int q = 1; q < n_parts; ++q) s += parts[q * n + j];
-      out[j] = static_cast<T>(s * scale);
+      out[j] = from_f32<T>(s * scale);
     }
   }
 }

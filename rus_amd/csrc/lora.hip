@@ -56,7 +56,7 @@ __device__ __forceinline__ f16x8 zero8() { return f16x8{0, 0, 0, 0, 0, 0, 0, 0};
 // Accumulator row of register r for lane half h (v_mfma_f32_32x32x16: lane l holds column l % 32).
 __device__ __forceinline__ int acc_row(int r, int h) { return 8 * (r >> 2) + 4 * h + (r & 3); }
 
-__device__ __forceinline__ float round16(float x) { return static_cast<float>(static_cast<f16>(x)); }
+__device__ __forceinline__ float round16(float x) { return static_cast<float>(from_f32<f16>(x)); }
 
 // Ranks k0 .. k0+7 (k0 in {0, 8, 16, 24}) of a row of R fp16 values, zero past R.
 template <int R>
@@ -77,7 +77,7 @@ __device__ __forceinline__ f16x8 drop8(f16x8 x, uint32_t w, int sh, float scale)
   f16x8 r;
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    const f16 v = static_cast<f16>(static_cast<float>(x[i]) * scale);
+    const f16 v = from_f32<f16>(static_cast<float>(x[i]) * scale);
     r[i] = (w >> (sh + i)) & 1u ? v : static_cast<f16>(0.0f);
   }
   return r;
@@ -162,7 +162,7 @@ __device__ __forceinline__ void store_ranks(const float (&tot)[Cfg<R>::NACC * 4]
     int br, rank;
     col_owner<R>(j, ln & 31, br, rank);
     const int64_t tt = t0 + acc_row(r, ln >> 5);
-    if (br >= 0 && tt < n_tok) (br ? out_v : out_q)[tt * R + rank] = static_cast<f16>(tot[k]);
+    if (br >= 0 && tt < n_tok) (br ? out_v : out_q)[tt * R + rank] = from_f32<f16>(tot[k]);
   }
 }
 
@@ -368,7 +368,7 @@ __device__ __forceinline__ void expand_wave(const ExpandArgs& a, int dt, int64_t
       const float hq = round16(oq[r]), hv = round16(ov[r]);  // fp16 dx_q, dx_v
       const float tq = round16((wq >> bit) & 1u ? hq * a.scale_q : 0.0f);
       const float tv = round16((wv >> bit) & 1u ? hv * a.scale_v : 0.0f);
-      c[k] = static_cast<f16>(round16(static_cast<float>(c[k]) + tq) + tv);
+      c[k] = from_f32<f16>(round16(static_cast<float>(c[k]) + tq) + tv);
     }
     *reinterpret_cast<f16x4*>(p + off) = c;
   }
@@ -522,7 +522,7 @@ __device__ __forceinline__ void bwd_w_block(const BwdWArgs& a, int blk, int chun
     const int j = o / kWCols;
     const int64_t col = c0 + o % kWCols;
     if (o >= kPart || col >= a.cols[p]) continue;
-    const f16 hs = static_cast<f16>(tot[i]);
+    const f16 hs = from_f32<f16>(tot[i]);
     if (a.transposed[p])
       a.g[p][j * a.cols[p] + col] = hs;
     else

@@ -93,8 +93,8 @@ __device__ __forceinline__ uint32_t decode_byte(uint32_t b, float scale,
   const float vh = s_nf4[(b >> 4) & 15u] * scale;
   const float vl = s_nf4[b & 15u] * scale;
   h2 r;
-  r.x = static_cast<_Float16>(vh);
-  r.y = static_cast<_Float16>(vl);
+  r.x = from_f32<f16>(vh);
+  r.y = from_f32<f16>(vl);
   return __builtin_bit_cast(uint32_t, r);
 }
 

@@ -257,8 +257,8 @@ __global__ __launch_bounds__(kThreads) void nf4_gemm_kernel(GemmArgs a) {
       f16 v[EPT];
 #pragma unroll
       for (int q = 0; q < EPT / 2; ++q) {  // byte q: high nibble = even element
-        v[2 * q] = static_cast<f16>(lv[q].x * scale);
-        v[2 * q + 1] = static_cast<f16>(lv[q].y * scale);
+        v[2 * q] = from_f32<f16>(lv[q].x * scale);
+        v[2 * q + 1] = from_f32<f16>(lv[q].y * scale);
       }
       if constexpr (!TRANS) {
         f16* db = sB[buf] + wr * kLd + 16 * (wr / EPT) + wq * EPT;
@@ -354,7 +354,7 @@ __global__ __launch_bounds__(kThreads) void nf4_gemm_kernel(GemmArgs a) {
         f16x4 o;
 #pragma unroll
         for (int k = 0; k < 4; ++k)
-          o[k] = static_cast<f16>(acc[i][j][4 * r4 + k] + static_cast<float>(bv[k]));
+          o[k] = from_f32<f16>(acc[i][j][4 * r4 + k] + static_cast<float>(bv[k]));
         *reinterpret_cast<f16x4*>(yrow + i * 32 + 8 * r4) = o;
       }
   }

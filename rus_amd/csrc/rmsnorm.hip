@@ -49,7 +49,7 @@ __global__ __launch_bounds__(256) void rmsnorm_fwd_any(const T* __restrict__ x,
     float h = static_cast<float>(x[off + c]);
     if (HAS_RES) {
       h = round_to<T>(h + static_cast<float>(res[off + c]));
-      sum_out[off + c] = static_cast<T>(h);
+      sum_out[off + c] = from_f32<T>(h);
     }
     ss += h * h;
   }
@@ -59,7 +59,7 @@ __global__ __launch_bounds__(256) void rmsnorm_fwd_any(const T* __restrict__ x,
   const T* hsrc = HAS_RES ? sum_out : x;  // this lane wrote these sum_out elements itself
   for (int c = lane; c < n_cols; c += kWave) {
     const float h = static_cast<float>(hsrc[off + c]);
-    y[off + c] = static_cast<T>(round_to<T>(h * r) * static_cast<float>(w[c]));
+    y[off + c] = from_f32<T>(round_to<T>(h * r) * static_cast<float>(w[c]));
   }
 }
 
@@ -163,7 +163,7 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_any(const T* __restrict__ dy,
     const float g = static_cast<float>(w[c]) * static_cast<float>(dy[off + c]);
     float o = (g - xh * cm) * r;
     if (HAS_DRES) o = o + static_cast<float>(dres[off + c]);
-    dx[off + c] = static_cast<T>(o);
+    dx[off + c] = from_f32<T>(o);
   }
 }
 

@@ -427,7 +427,7 @@ __global__ __launch_bounds__(kThreads) void rope_bwd_mid_kernel(RopeBwdMidArgs m
       const int r = out_q ? rr : rr - kMidR;
       float acc = 0.0f;
       for (int g = out_q ? 0 : gv0; g < (out_q ? gq : groups); ++g) acc += red[tk * groups + g][r];
-      (out_q ? m.dmid_q : m.dmid_v)[tt * kMidR + r] = static_cast<f16>(acc);
+      (out_q ? m.dmid_q : m.dmid_v)[tt * kMidR + r] = from_f32<f16>(acc);
     }
   }
 }
