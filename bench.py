@@ -562,6 +562,166 @@ def kernel_probe(reps: int = 5) -> None:
     print(f"probe: {reps} four-segment dequants of layer 0 with a riding norm backward", flush=True)
 
 
+def _print_record(rec: dict) -> None:
+    print(json.dumps({k: (round(v, 3) if isinstance(v, float) else v) for k, v in rec.items()}),
+          flush=True)
+
+
+def ceilings_probe(reps: int = 40) -> None:
+    """Streaming rates of this GPU at the per-layer dequant's traffic (config 5: 23.5 MB of
+    packed codes read, 94 MB of fp16 written), each launch on buffers the previous launches did
+    not touch: torch ``fill_`` (write only), ``copy_`` (1 byte read per byte written), a 1:4
+    broadcast copy (the dequant's read:write ratio) and the dequant launch itself (four segments
+    of one layer, no riding norm). Prints one JSON record per measurement."""
+    import torch
+
+    from rus_amd import model as M
+    from rus_amd.hostload import WeightStream
+
+    dev = torch.device("cuda:0")
+    cfg = M.qwen2_1p5b()
+    out_bytes = 94_175_232  # one layer's fp16 weights: 2 x 47,087,616 parameters
+    n_out = out_bytes // 2
+    sets = _n_sets(out_bytes + out_bytes // 4)
+    outs = [torch.empty(n_out, dtype=torch.float16, device=dev) for _ in range(sets)]
+    ins = [torch.randn(n_out // 4, device=dev).half() for _ in range(sets)]
+    recs = [
+        _hbm("torch fill_ (write only)", [n_out], _time_rotating(
+            lambda i: outs[i].fill_(1.0), sets, reps), out_bytes),
+        _hbm("torch copy_ (1:1)", [n_out // 4], _time_rotating(
+            lambda i: outs[i][: n_out // 4].copy_(ins[i]), sets, reps), out_bytes // 2),
+        _hbm("torch broadcast copy (1:4 read:write)", [n_out // 4, 4], _time_rotating(
+            lambda i: outs[i].view(-1, 4).copy_(ins[i].view(-1, 1).expand(-1, 4)), sets, reps),
+            out_bytes + out_bytes // 4),
+    ]
+    del outs, ins
+    torch.cuda.empty_cache()
+    cfg_n = M.Qwen2Config(**{**cfg.__dict__, "num_hidden_layers": sets})
+    model = M.build_random_qlora_qwen2(cfg_n, dev, seed=0)
+    ws = WeightStream(model.layers, dev, resident=True)
+    spaces = [{k: torch.empty_like(v) for k, v in ws.workspaces.items()} for _ in range(sets)]
+    n_abs2 = sum(sg.absmax2_slice.stop - sg.absmax2_slice.start
+                 for sg in ws.layer_segments[0].values())
+    dq_bytes = _nf4_bytes(n_out, n_abs2)
+    recs.append(_hbm("rus nf4 dequant, 4 segments", [n_out], _time_rotating(
+        lambda i: ws.dequant_layer(i, workspaces=spaces[i]), sets, reps), dq_bytes))
+    for r in recs:
+        r["sets"] = sets
+        _print_record(r)
+
+
+def gemm_probe(reps: int = 20) -> None:
+    """Per-product GPU time of one config-5 layer at the bench batch's token count (the eight
+    projections: F.linear / the input-gradient torch.mm on dequantised fp16 weights, i.e.
+    hipBLASLt, against the fused NF4 products rus_nf4_gemm), the layer's dequant launch, and the
+    lm_head's two GEMMs of one 256-token block against hipBLASLt on the same operands. Weights
+    rotate over several layers so each launch reads them from HBM. Prints JSON records."""
+    import torch
+    import torch.nn.functional as F
+
+    from rus_amd import kernels as K
+    from rus_amd import model as M
+    from rus_amd import ops as O
+    from rus_amd.hostload import SEGMENTS, WeightStream
+
+    dev = torch.device("cuda:0")
+    cfg = M.qwen2_1p5b()
+    n_tok = sum(config_batch_lengths(0))
+    sets = 4
+    cfg_n = M.Qwen2Config(**{**cfg.__dict__, "num_hidden_layers": sets})
+    model = M.build_random_qlora_qwen2(cfg_n, dev, seed=0)
+    ws = WeightStream(model.layers, dev, resident=True)
+    w16 = []
+    for i in range(sets):
+        spaces = {k: torch.empty_like(v) for k, v in ws.workspaces.items()}
+        w16.append(ws.dequant_layer(i, workspaces=spaces))
+    nf4 = [ws.nf4_layer(i) for i in range(sets)]
+    g = torch.Generator(device=dev).manual_seed(0)
+    tot = {"hipblaslt": 0.0, "fused": 0.0}
+    for name in SEGMENTS:
+        rows, cols = w16[0][name].shape
+        for trans in (False, True):
+            k_in, n_out = (rows, cols) if trans else (cols, rows)
+            x = torch.randn(n_tok, k_in, device=dev, generator=g).half()
+            if trans:
+                lib = lambda i: O._mm_w(x, w16[i][name])
+                fused = lambda i: K.nf4_gemm(x, nf4[i][name], trans=True)
+            else:
+                lib = lambda i: F.linear(x, w16[i][name])
+                fused = lambda i: K.nf4_gemm(x, nf4[i][name])
+            flops = 2.0 * n_tok * k_in * n_out
+            shape = [n_tok, k_in, n_out]
+            for kind, fn in (("hipblaslt", lib), ("fused", fused)):
+                us = _time_rotating(fn, sets, reps)
+                tot[kind] += us
+                _print_record(_mfma(f"{name} {'input-grad' if trans else 'forward'} {kind}",
+                                    shape, us, flops))
+    dq = _time_rotating(lambda i: ws.dequant_layer(i), sets, reps)
+    _print_record({"kernel": "layer dequant (4 segments)", "gpu_us": dq})
+    _print_record({"kernel": "layer total", "dequant_plus_hipblaslt_us": tot["hipblaslt"] + 2 * dq,
+                   "fused_us": tot["fused"], "note": "dequant once per pass (forward, backward)"})
+    del w16, nf4, ws, model
+    torch.cuda.empty_cache()
+    # lm_head: one 256-token block against the whole vocabulary
+    nb, d, V = 256, cfg.hidden_size, cfg.vocab_size
+    h = torch.randn(nb, d, device=dev, generator=g).half()
+    w = (torch.randn(V, d, device=dev, generator=g) * 0.02).half()
+    wt = K.lm_head_weight_t(w)
+    kp = _round_up(V, 64)
+    z = torch.empty((nb, kp), dtype=torch.float16, device=dev)
+    zl = torch.empty((nb, V), dtype=torch.float16, device=dev)
+    splits = K.lm_head_split_count(nb, d, V, K.cu_count(dev))
+    parts = torch.empty((splits, nb, d), dtype=torch.float32, device=dev)
+    dh = torch.empty((nb, d), dtype=torch.float16, device=dev)
+    fl = 2.0 * nb * d * V
+    for kind, fn in (("rus lmhead_ce_logits", lambda i: K.lm_head_ce_logits(h, w, z)),
+                     ("hipblaslt h W^T", lambda i: torch.mm(h, w.t(), out=zl))):
+        _print_record(_mfma(f"lm_head logits {kind}", [nb, d, V], _time_rotating(fn, 1, reps), fl))
+    for kind, fn in (("rus lmhead_ce_grad_hidden", lambda i: K.lm_head_ce_grad_hidden(
+                         z, wt, V, parts, accumulate=False)),
+                     ("hipblaslt G W", lambda i: torch.mm(zl, w, out=dh))):
+        _print_record(_mfma(f"lm_head hidden grad {kind}", [nb, V, d],
+                            _time_rotating(fn, 1, reps), fl, splits=splits))
+
+
+def trace_summary(path: str, steps: int) -> None:
+    """Per-step kernel time of the last ``steps`` graph replays in a ``rocprofv3 --kernel-trace``
+    CSV of a bench run: the replays are the kernels between the last steps + 1 launches of the
+    once-per-step dropout-bits kernel. hipBLASLt kernels are summed as one line."""
+    import csv
+    import re
+
+    with open(path) as f:
+        rows = sorted(csv.DictReader(f), key=lambda r: int(r["Start_Timestamp"]))
+    marks = [i for i, r in enumerate(rows) if "keep_bits_kernel" in r["Kernel_Name"]]
+    if len(marks) < steps + 1:
+        raise SystemExit(f"{path}: {len(marks)} step markers, need {steps + 1}")
+    sel = rows[marks[-steps - 1] + 1: marks[-1] + 1]
+    dur = [int(r["End_Timestamp"]) - int(r["Start_Timestamp"]) for r in sel]
+    wall = int(sel[-1]["End_Timestamp"]) - int(sel[0]["Start_Timestamp"])
+    print(f"{steps} replayed steps: {len(sel) / steps:.0f} kernels/step, "
+          f"{wall / 1e6 / steps:.2f} ms/step from first start to last end, "
+          f"{sum(dur) / 1e6 / steps:.2f} ms/step of kernels")
+    agg: dict = {}
+    for r, d in zip(sel, dur):
+        n = r["Kernel_Name"]
+        if n.startswith(("Cijk", "Custom_Cijk")):
+            k = "hipBLASLt GEMMs"
+        else:
+            k = re.sub(r"^void |rus::\(anonymous namespace\)::|_ZN3rus12_GLOBAL__N_1\d+", "", n)
+            k = k.split("(")[0].split("<")[0][:48]
+        a = agg.setdefault(k, [0, 0])
+        a[0] += d
+        a[1] += 1
+    print(" ms/step  launches/step  us/launch  kernel")
+    for k, (t, c) in sorted(agg.items(), key=lambda kv: -kv[1][0]):
+        print(f"{t / 1e6 / steps:8.3f}  {c / steps:13.1f}  {t / c / 1e3:9.2f}  {k}")
+
+
+def _round_up(x: int, m: int) -> int:
+    return -(-x // m) * m
+
+
 def measured_traffic(kernel: str):
     """HBM bytes per launch of ``kernel`` from the committed counter summary, if there is one."""
     path = os.path.join(REPO, "profiles", f"{kernel}_traffic_config5.txt")
@@ -619,21 +779,34 @@ def main() -> int:
                          "products decode NF4 inside their MFMA loop (rus_nf4_gemm)")
     ap.add_argument("--no-ablation", action="store_true",
                     help="skip the timing of the other --recompute and --stream-unit settings")
+    ap.add_argument("--trace-summary", metavar="KERNEL_TRACE_CSV",
+                    help="print the per-step kernel time of the last --steps replays in a "
+                         "rocprofv3 --kernel-trace CSV of a bench run, and exit")
     ap.add_argument("--probe", nargs="?", const="dequant",
-                    choices=("dequant", "lmhead", "elementwise"),
+                    choices=("dequant", "lmhead", "elementwise", "ceilings", "gemm"),
                     help="only fixed launches for counter runs: copy + dequant (default), the "
                          "lm_head CE kernels at config 2, or the elementwise kernels on cold "
-                         "inputs")
+                         "inputs; or printed timings: streaming ceilings at the dequant's "
+                         "traffic (ceilings), per-product GEMM times (gemm)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs and measures one GPU only (asked for --gpus "
               f"{args.gpus}); a sharded run over several GPUs is not implemented", file=sys.stderr)
         return 2
+    if args.trace_summary:
+        trace_summary(args.trace_summary, args.steps)
+        return 0
     if args.probe == "lmhead":
         lmhead_probe()
         return 0
     if args.probe == "elementwise":
         elementwise_probe()
+        return 0
+    if args.probe == "ceilings":
+        ceilings_probe()
+        return 0
+    if args.probe == "gemm":
+        gemm_probe()
         return 0
     if args.probe:
         kernel_probe()
