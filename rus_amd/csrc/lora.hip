@@ -531,7 +531,8 @@ __device__ __forceinline__ void bwd_w_block(const BwdWArgs& a, int blk, int chun
 }
 
 template <int R>
-__global__ __launch_bounds__(64 * kWWaves) void lora_bwd_w_kernel(BwdWArgs a) {
+__global__ __launch_bounds__(64 * kWWaves) __attribute__((amdgpu_waves_per_eu(4)))
+void lora_bwd_w_kernel(BwdWArgs a) {
   bwd_w_block<R>(a, blockIdx.x, blockIdx.y, gridDim.x, gridDim.y);
 }
 
@@ -540,7 +541,8 @@ __global__ __launch_bounds__(64 * kWWaves) void lora_bwd_w_kernel(BwdWArgs a) {
 // expansion blocks of kWWaves column tiles of one 32-token tile each. Each block's role is
 // uniform, so the weight-gradient blocks' barriers and arrival counters involve only them.
 template <int R, bool DROP>
-__global__ __launch_bounds__(64 * kWWaves) void lora_bwd_xw_kernel(BwdWArgs a, ExpandArgs x,
+__global__ __launch_bounds__(64 * kWWaves) __attribute__((amdgpu_waves_per_eu(4)))
+void lora_bwd_xw_kernel(BwdWArgs a, ExpandArgs x,
                                                                   int n_blk, int n_chunk,
                                                                   int x_col_blocks) {
   const int b = blockIdx.x;
