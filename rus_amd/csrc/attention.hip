@@ -226,7 +226,10 @@ constexpr int kMax(int x, int y) { return x > y ? x : y; }
 // Forward: O = softmax(Q K^T * scale, causal) V and LSE. Block = (row, query block, head); its
 // kW waves take key blocks w, w + kW, ... with their own running max / sum, merged at the end.
 // ---------------------------------------------------------------------------------------------
-__global__ __launch_bounds__(64 * kW) void attn_fwd_kernel(AttnArgs a) {
+// At most 256 registers per lane (no spills): two blocks share a CU, so the grid of (query
+// block, head) blocks fits the chip in one round and one block's loads overlap another's MFMAs.
+__global__ __launch_bounds__(64 * kW) __attribute__((amdgpu_waves_per_eu(2, 2))) void
+attn_fwd_kernel(AttnArgs a) {
   constexpr int kBytes = kMax(kW * kStageHalfs * 2, kParkBytes + kW * 64 * 4);
   __shared__ __attribute__((aligned(16))) char smem[kBytes];
   int start, end, q0;
