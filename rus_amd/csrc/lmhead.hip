@@ -101,129 +101,166 @@ __device__ __forceinline__ u32x4v lds_read16(uint32_t addr) {
   return v;
 }
 
-// The 8 fragments (4 A rows-groups, 4 B row-groups) of one K step of 16 from LDS addresses a / b.
+// The fragments of one K step of 16 from LDS addresses a (4 A row groups) / b (NT B row groups).
+template <int NT>
 __device__ __forceinline__ void read_frags(uint32_t a, uint32_t b, u32x4v (&fa)[kMT],
-                                           u32x4v (&fb)[kNT]) {
+                                           u32x4v (&fb)[NT]) {
   fa[0] = lds_read16<0>(a);
   fa[1] = lds_read16<2048>(a);
   fa[2] = lds_read16<4096>(a);
   fa[3] = lds_read16<6144>(a);
   fb[0] = lds_read16<0>(b);
   fb[1] = lds_read16<2048>(b);
-  fb[2] = lds_read16<4096>(b);
-  fb[3] = lds_read16<6144>(b);
+  if constexpr (NT == 4) {
+    fb[2] = lds_read16<4096>(b);
+    fb[3] = lds_read16<6144>(b);
+  }
 }
 
 // Every LDS read issued so far has returned; ties the fragments so that no MFMA using them is
 // scheduled before the wait.
-__device__ __forceinline__ void wait_frags(u32x4v (&fa)[kMT], u32x4v (&fb)[kNT]) {
-  asm volatile("s_waitcnt lgkmcnt(0)"
-               : "+v"(fa[0]), "+v"(fa[1]), "+v"(fa[2]), "+v"(fa[3]), "+v"(fb[0]), "+v"(fb[1]),
-                 "+v"(fb[2]), "+v"(fb[3]));
+template <int NT>
+__device__ __forceinline__ void wait_frags(u32x4v (&fa)[kMT], u32x4v (&fb)[NT]) {
+  if constexpr (NT == 4)
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(fa[0]), "+v"(fa[1]), "+v"(fa[2]), "+v"(fa[3]), "+v"(fb[0]), "+v"(fb[1]),
+                   "+v"(fb[2]), "+v"(fb[3]));
+  else
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(fa[0]), "+v"(fa[1]), "+v"(fa[2]), "+v"(fa[3]), "+v"(fb[0]), "+v"(fb[1]));
 }
 
-__device__ __forceinline__ void mma16(const u32x4v (&fa)[kMT], const u32x4v (&fb)[kNT],
-                                      f32x16 (&acc)[kMT][kNT]) {
+template <int NT>
+__device__ __forceinline__ void mma16(const u32x4v (&fa)[kMT], const u32x4v (&fb)[NT],
+                                      f32x16 (&acc)[kMT][NT]) {
 #pragma unroll
   for (int mt = 0; mt < kMT; ++mt)
 #pragma unroll
-    for (int nt = 0; nt < kNT; ++nt)
+    for (int nt = 0; nt < NT; ++nt)
       acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
           __builtin_bit_cast(f16x8, fa[mt]), __builtin_bit_cast(f16x8, fb[nt]), acc[mt][nt], 0,
           0, 0);
 }
 
-// s_waitcnt vmcnt(n) for n in {0, 8, 16, 24} (expcnt and lgkmcnt not waited on).
-__device__ __forceinline__ void wait_vm(int n) {
-  if (n >= 24)
-    __builtin_amdgcn_s_waitcnt((24 & 15) | ((24 >> 4) << 14) | (7 << 4) | (15 << 8));
-  else if (n >= 16)
-    __builtin_amdgcn_s_waitcnt((16 & 15) | ((16 >> 4) << 14) | (7 << 4) | (15 << 8));
-  else if (n >= 8)
-    __builtin_amdgcn_s_waitcnt(8 | (7 << 4) | (15 << 8));
-  else
-    __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8));
+// s_waitcnt vmcnt(N) (expcnt and lgkmcnt not waited on).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-__device__ __forceinline__ void mainloop(const GemmArgs& g, const Tile& tl, char* smem,
-                                         f32x16 (&acc)[kMT][kNT]) {
+// Waits until at most `stages` (0..3) stages of PER copies each are still in flight.
+template <int PER>
+__device__ __forceinline__ void wait_stages(int stages) {
+  if (stages >= 3)
+    wait_vmcnt<3 * PER>();
+  else if (stages == 2)
+    wait_vmcnt<2 * PER>();
+  else if (stages == 1)
+    wait_vmcnt<PER>();
+  else
+    wait_vmcnt<0>();
+}
+
+// NW = 4: waves 2 (vocab halves) x 2 (token halves) of 128 x 128 (acc[4][4], one wave per
+// SIMD); NW = 8: 2 x 4 waves of 128 x 64 (acc[4][2], two waves per SIMD, so one wave's fragment
+// reads and copy waits overlap the other's MFMAs). Same LDS stages and swizzle either way.
+template <int NW>
+__device__ __forceinline__ void mainloop_t(const GemmArgs& g, const Tile& tl, char* smem,
+                                           f32x16 (&acc)[kMT][16 / NW]) {
+  constexpr int NT = 16 / NW;        // 32-token MFMA tiles per wave
+  constexpr int RW = kBN / (NW / 2);  // token rows per wave: 128 or 64
+  constexpr int CP = 16 / NW;        // copies per thread per operand and stage: 4 or 2
+  constexpr int PER = 2 * CP;
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / (NW / 2), wn = wave % (NW / 2);
   const int kb = tl.split * g.k_per_split;
   const int ke = min(kb + g.k_per_split, g.K);
   const int KT = ke > kb ? (ke - kb) / kDK : 0;
 #pragma unroll
   for (int mt = 0; mt < kMT; ++mt)
 #pragma unroll
-    for (int nt = 0; nt < kNT; ++nt) acc[mt][nt] = f32x16{};
+    for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = f32x16{};
   if (KT == 0) {
     __syncthreads();
     return;
   }
-  // Loads: instruction i of wave w fills rows 64i + 16w .. +16 of A (and of B), 64 bytes each;
-  // lane l covers row 64i + 16w + l/4 at position l%4, i.e. the chunk (l%4) ^ ((l/16) & 3).
+  // Copies: instruction i of wave w fills rows 16 NW i + 16 w .. +16 of A and of B, 64 bytes
+  // each; lane l covers row 16 NW i + 16 w + l/4 at position l%4, i.e. the chunk
+  // (l%4) ^ ((l/16) & 3).
   const int lrow = 16 * wave + (lane >> 2);
   const int lchunk = (lane & 3) ^ ((lane >> 4) & 3);
   const char* gA = reinterpret_cast<const char*>(g.A);
   const char* gB = reinterpret_cast<const char*>(g.B);
-  uint32_t oa[4], ob[4];
+  uint32_t oa[CP], ob[CP];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < CP; ++i) {
     // Rows past the matrix edge re-read the last row: finite values the epilogues discard.
-    const int ra_ = min(tl.m0 + lrow + 64 * i, g.M - 1);
-    const int rb_ = min(tl.n0 + lrow + 64 * i, g.N - 1);
+    const int ra_ = min(tl.m0 + lrow + 16 * NW * i, g.M - 1);
+    const int rb_ = min(tl.n0 + lrow + 16 * NW * i, g.N - 1);
     oa[i] = static_cast<uint32_t>((ra_ * g.lda + kb + lchunk * 8) * 2);
     ob[i] = static_cast<uint32_t>((rb_ * g.ldb + kb + lchunk * 8) * 2);
   }
-  auto issue = [&](int k) {  // stage k's 8 copies into buffer k % 4
+  auto issue = [&](int k) {  // stage k's copies into buffer k % 4
     char* st = smem + (k & (kNStages - 1)) * kStageBytes;
     const int kbytes = k * (kDK * 2);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < CP; ++i) {
       __builtin_amdgcn_global_load_lds(gA + oa[i] + kbytes,
-                                       (lds_void_ptr)(st + (64 * i + 16 * wave) * 64), 16, 0, 0);
-      __builtin_amdgcn_global_load_lds(gB + ob[i] + kbytes,
-                                       (lds_void_ptr)(st + kBM * 64 + (64 * i + 16 * wave) * 64),
-                                       16, 0, 0);
+                                       (lds_void_ptr)(st + (16 * NW * i + 16 * wave) * 64), 16, 0,
+                                       0);
+      __builtin_amdgcn_global_load_lds(
+          gB + ob[i] + kbytes, (lds_void_ptr)(st + kBM * 64 + (16 * NW * i + 16 * wave) * 64), 16,
+          0, 0);
     }
   };
   const int pre = min(kNStages, KT);
   for (int k = 0; k < pre; ++k) issue(k);
-  wait_vm(8 * (pre - 1));  // stage 0 landed (this wave's copies)
+  wait_stages<PER>(pre - 1);  // stage 0 landed (this wave's copies)
   __builtin_amdgcn_s_barrier();  // ... and every wave's
-  // Fragment addresses: row wm*128 + (l & 31) (+ 32 mt, immediate), chunk 2 kk + l/32 stored at
-  // chunk ^ ((l >> 2) & 3).
+  // Fragment addresses: A row wm*128 + (l & 31), B row wn*RW + (l & 31) (+ 32 per MFMA tile,
+  // immediate), chunk 2 kk + l/32 stored at chunk ^ ((l >> 2) & 3).
   const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void_ptr)smem));
   const int sw = (lane >> 2) & 3, half = lane >> 5;
-  const uint32_t a0 = lds0 + (wm * kWM + (lane & 31)) * 64 + (((0 + half) ^ sw) << 4);
-  const uint32_t a1 = lds0 + (wm * kWM + (lane & 31)) * 64 + (((2 + half) ^ sw) << 4);
-  const uint32_t b0 = a0 - wm * kWM * 64 + kBM * 64 + wn * kWN * 64;
-  const uint32_t b1 = a1 - wm * kWM * 64 + kBM * 64 + wn * kWN * 64;
-  u32x4v fa0[kMT], fb0[kNT], fa1[kMT], fb1[kNT];
-  read_frags(a0, b0, fa0, fb0);
-  wait_frags(fa0, fb0);
+  const uint32_t c0 = ((0 + half) ^ sw) << 4, c1 = ((2 + half) ^ sw) << 4;
+  const uint32_t arow = lds0 + (wm * kWM + (lane & 31)) * 64;
+  const uint32_t brow = lds0 + kBM * 64 + (wn * RW + (lane & 31)) * 64;
+  const uint32_t a0 = arow + c0, a1 = arow + c1, b0 = brow + c0, b1 = brow + c1;
+  u32x4v fa0[kMT], fb0[NT], fa1[kMT], fb1[NT];
+  read_frags<NT>(a0, b0, fa0, fb0);
+  wait_frags<NT>(fa0, fb0);
   for (int k = 0; k < KT; ++k) {
     const uint32_t sb = (k & (kNStages - 1)) * kStageBytes;
-    read_frags(a1 + sb, b1 + sb, fa1, fb1);  // step 1 of stage k
+    read_frags<NT>(a1 + sb, b1 + sb, fa1, fb1);  // step 1 of stage k
     __builtin_amdgcn_sched_barrier(0);
-    mma16(fa0, fb0, acc);  // step 0 of stage k
+    mma16<NT>(fa0, fb0, acc);  // step 0 of stage k
     __builtin_amdgcn_sched_barrier(0);
-    wait_frags(fa1, fb1);
+    wait_frags<NT>(fa1, fb1);
     if (k + 1 < KT) {
       // Stage k + 1 has landed for every wave, and every wave has read stage k: its buffer takes
       // stage k + 4.
-      wait_vm(8 * min(2, KT - 2 - k));
+      wait_stages<PER>(min(2, KT - 2 - k));
       __builtin_amdgcn_s_barrier();
       if (k + kNStages < KT) issue(k + kNStages);
       const uint32_t nb = ((k + 1) & (kNStages - 1)) * kStageBytes;
-      read_frags(a0 + nb, b0 + nb, fa0, fb0);  // step 0 of stage k + 1
+      read_frags<NT>(a0 + nb, b0 + nb, fa0, fb0);  // step 0 of stage k + 1
     }
     __builtin_amdgcn_sched_barrier(0);
-    mma16(fa1, fb1, acc);  // step 1 of stage k
+    mma16<NT>(fa1, fb1, acc);  // step 1 of stage k
     __builtin_amdgcn_sched_barrier(0);
-    if (k + 1 < KT) wait_frags(fa0, fb0);
+    if (k + 1 < KT) wait_frags<NT>(fa0, fb0);
   }
   __syncthreads();  // the epilogues reuse the LDS
+}
+
+__device__ __forceinline__ void mainloop(const GemmArgs& g, const Tile& tl, char* smem,
+                                         f32x16 (&acc)[kMT][4]) {
+  mainloop_t<4>(g, tl, smem, acc);
+}
+
+__device__ __forceinline__ void mainloop(const GemmArgs& g, const Tile& tl, char* smem,
+                                         f32x16 (&acc)[kMT][2]) {
+  mainloop_t<8>(g, tl, smem, acc);
 }
 
 __device__ __forceinline__ float round16(float x) {
@@ -237,15 +274,17 @@ __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_ex
 // whose vocab row local to A is row; rows >= g.M are written as 0. Staged through the LDS as
 // [token][vocab] with 8-byte quads XOR-swizzled by row (pairs kept adjacent) so every lane stores
 // 16 contiguous bytes of one token's row: out[tok][tl.m0 + c] for tok < g.N, c < kpad.
-template <class F>
+// NW waves in the mainloop's layout (4: 128 x 128 each, 8: 128 x 64).
+template <int NW = 4, class F>
 __device__ __forceinline__ void store_tile_tv(char* smem, const GemmArgs& g, const Tile& tl,
                                               f16* out, int64_t ld, int kpad, F value) {
+  constexpr int NT = 16 / NW, RW = kBN / (NW / 2);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int wm = wave >> 1, wn = wave & 1, h = lane >> 5;
+  const int wm = wave / (NW / 2), wn = wave % (NW / 2), h = lane >> 5;
   const int vrow0 = tl.m0 + wm * kWM;
 #pragma unroll
-  for (int nt = 0; nt < kNT; ++nt) {
-    const int trow = wn * kWN + nt * 32 + (lane & 31);  // token row within the block tile
+  for (int nt = 0; nt < NT; ++nt) {
+    const int trow = wn * RW + nt * 32 + (lane & 31);  // token row within the block tile
     char* srow = smem + trow * 512;
 #pragma unroll
     for (int mt = 0; mt < kMT; ++mt)
@@ -266,8 +305,8 @@ __device__ __forceinline__ void store_tile_tv(char* smem, const GemmArgs& g, con
   const int t = threadIdx.x;
   const int c = t & 31;
 #pragma unroll 4
-  for (int it = 0; it < kBN / 8; ++it) {
-    const int trow = it * 8 + (t >> 5);
+  for (int it = 0; it < kBN / (2 * NW); ++it) {
+    const int trow = it * 2 * NW + (t >> 5);
     const int tok = tl.n0 + trow;
     const int col = tl.m0 + c * 8;
     if (tok < g.N && col < kpad) {
@@ -460,15 +499,19 @@ struct LogitsParams {
   int kpad;
 };
 
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))) void
+// Eight waves (two per SIMD): the accumulators of a 128 x 64 wave tile leave room for a second
+// wave per SIMD, whose MFMAs run while the first waits on its fragment reads and copies.
+constexpr int kThreads8 = 512;
+
+__global__ __launch_bounds__(kThreads8) __attribute__((amdgpu_waves_per_eu(2, 2))) void
 lmhead_logits_kernel(GemmArgs g, LogitsParams p) {
   __shared__ __attribute__((aligned(16))) char smem[kSmemBytes];
   Tile tl;
   if (!tile_of(g, tl)) return;
-  f32x16 acc[kMT][kNT];
+  f32x16 acc[kMT][2];
   mainloop(g, tl, smem, acc);
-  store_tile_tv(smem, g, tl, p.z, p.ld_z, p.kpad,
-                [&](int mt, int nt, int r, int) { return acc[mt][nt][r]; });
+  store_tile_tv<8>(smem, g, tl, p.z, p.ld_z, p.kpad,
+                   [&](int mt, int nt, int r, int) { return acc[mt][nt][r]; });
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -575,20 +618,20 @@ struct StoreParams {
   const float* alpha;  // accumulate: parts = parts * alpha[row] + acc (alpha null: factor 1)
 };
 
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))) void
+__global__ __launch_bounds__(kThreads8) __attribute__((amdgpu_waves_per_eu(2, 2))) void
 lmhead_grad_hidden_kernel(GemmArgs g, StoreParams p) {
   __shared__ __attribute__((aligned(16))) char smem[kSmemBytes];
   Tile tl;
   if (!tile_of(g, tl)) return;
-  f32x16 acc[kMT][kNT];
+  f32x16 acc[kMT][2];
   mainloop(g, tl, smem, acc);
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int wm = wave >> 1, wn = wave & 1, h = lane >> 5;
+  const int wm = wave >> 2, wn = wave & 3, h = lane >> 5;
   float* base = p.parts + static_cast<int64_t>(tl.split) * g.M * g.N;
 #pragma unroll
-  for (int nt = 0; nt < kNT; ++nt) {
-    const int col = tl.n0 + wn * kWN + nt * 32 + (lane & 31);
+  for (int nt = 0; nt < 2; ++nt) {
+    const int col = tl.n0 + wn * 64 + nt * 32 + (lane & 31);
     if (col >= g.N) continue;
 #pragma unroll
     for (int mt = 0; mt < kMT; ++mt)
@@ -1230,7 +1273,7 @@ static int grad_hidden(const char* fn, const void* grad_logits, int64_t ld_g, co
   g.tiles_m = (g.M + kBM - 1) / kBM;
   g.tiles_n = (g.N + kBN - 1) / kBN;
   StoreParams p{parts, accumulate, alpha};
-  hipLaunchKernelGGL(lmhead_grad_hidden_kernel, dim3(launch_grid(g)), dim3(kThreads), 0,
+  hipLaunchKernelGGL(lmhead_grad_hidden_kernel, dim3(launch_grid(g)), dim3(kThreads8), 0,
                      static_cast<hipStream_t>(stream), g, p);
   return check_launch(fn);
 }
@@ -1393,7 +1436,7 @@ extern "C" int rus_lmhead_ce_logits(const void* hidden, const void* weight, int6
   g.tiles_m = (g.M + kBM - 1) / kBM;
   g.tiles_n = (g.N + kBN - 1) / kBN;
   LogitsParams p{static_cast<f16*>(logits), ld_z, static_cast<int>(kpad)};
-  hipLaunchKernelGGL(lmhead_logits_kernel, dim3(launch_grid(g)), dim3(kThreads), 0,
+  hipLaunchKernelGGL(lmhead_logits_kernel, dim3(launch_grid(g)), dim3(kThreads8), 0,
                      static_cast<hipStream_t>(stream), g, p);
   return check_launch(fn);
 }
