@@ -637,28 +637,51 @@ def gemm_probe(reps: int = 20) -> None:
         w16.append(ws.dequant_layer(i, workspaces=spaces))
     nf4 = [ws.nf4_layer(i) for i in range(sets)]
     g = torch.Generator(device=dev).manual_seed(0)
-    tot = {"hipblaslt": 0.0, "fused": 0.0}
+    tot = {"hipblaslt": 0.0, "engine": 0.0, "fused": 0.0}
     for name in SEGMENTS:
         rows, cols = w16[0][name].shape
         for trans in (False, True):
             k_in, n_out = (rows, cols) if trans else (cols, rows)
             x = torch.randn(n_tok, k_in, device=dev, generator=g).half()
             if trans:
-                lib = lambda i: O._mm_w(x, w16[i][name])
+                lib = lambda i: torch.mm(x, w16[i][name])
+                eng = lambda i: O._mm_w(x, w16[i][name])
                 fused = lambda i: K.nf4_gemm(x, nf4[i][name], trans=True)
             else:
                 lib = lambda i: F.linear(x, w16[i][name])
+                eng = lambda i: O._lin(x, w16[i][name])
                 fused = lambda i: K.nf4_gemm(x, nf4[i][name])
             flops = 2.0 * n_tok * k_in * n_out
             shape = [n_tok, k_in, n_out]
-            for kind, fn in (("hipblaslt", lib), ("fused", fused)):
+            label = f"{name} {'input-grad' if trans else 'forward'}"
+            split = k_in >= O.SPLIT_K_MIN
+            kinds = [("hipblaslt", lib), ("fused", fused)]
+            if split:
+                kinds.insert(1, ("engine", eng))
+            for kind, fn in kinds:
                 us = _time_rotating(fn, sets, reps)
                 tot[kind] += us
-                _print_record(_mfma(f"{name} {'input-grad' if trans else 'forward'} {kind}",
-                                    shape, us, flops))
+                if kind == "hipblaslt" and not split:
+                    tot["engine"] += us  # the engine calls the library GEMM as is
+                _print_record(_mfma(f"{label} {kind}", shape, us, flops))
+            for sp in (2, 4, 7) if split else ():  # the batched GEMM of sp slices + its reduce
+                if k_in % sp:
+                    continue
+                if trans:
+                    part = lambda i: O._split_k_parts(x, w16[i][name], sp)
+                else:  # x [M, K] @ W[D, K]^T over K slices
+                    wk = lambda i: w16[i][name].view(n_out, sp, k_in // sp).permute(1, 2, 0)
+                    part = lambda i: torch.bmm(x.view(n_tok, sp, k_in // sp).permute(1, 0, 2),
+                                               wk(i), out_dtype=torch.float32)
+                us_p = _time_rotating(part, sets, reps)
+                pr = part(0)
+                us_r = _time_rotating(lambda i: K.sum_splits(pr, x.dtype), sets, reps)
+                _print_record(_mfma(f"{label} split-K {sp}", shape, us_p + us_r, flops,
+                                    batched_gemm_us=us_p, reduce_us=us_r))
     dq = _time_rotating(lambda i: ws.dequant_layer(i), sets, reps)
     _print_record({"kernel": "layer dequant (4 segments)", "gpu_us": dq})
     _print_record({"kernel": "layer total", "dequant_plus_hipblaslt_us": tot["hipblaslt"] + 2 * dq,
+                   "dequant_plus_engine_products_us": tot["engine"] + 2 * dq,
                    "fused_us": tot["fused"], "note": "dequant once per pass (forward, backward)"})
     del w16, nf4, ws, model
     torch.cuda.empty_cache()
