@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define RUS_ABI_VERSION 11
+#define RUS_ABI_VERSION 12
 
 #define RUS_DTYPE_F16 0
 #define RUS_DTYPE_F32 1
@@ -178,6 +178,19 @@ int rus_nf4_gemm(const void* x, int64_t m, int64_t stride_x, const rus_nf4_job* 
                  int32_t super_blocksize, int32_t trans, const void* bias, void* y,
                  int64_t stride_y, int32_t split, float* workspace, int64_t workspace_floats,
                  int32_t* counters, int64_t n_counters, void* stream);
+
+/*
+ * Split-K fp16 product into fp32 partials: parts[s] = A[:, Ks] . op(B)[Ks, :] for s = 0..n_split-1,
+ * parts = [n_split][m][n] fp32 (contiguous), Ks the s-th of the n_split pieces of round_up(
+ * ceil(k / n_split), 64) columns (n_split must equal the number of such pieces). A is [m, lda]
+ * fp16 (K-contiguous); B is [n, ldb] (b_kn = 0: op(B) = B^T, K-contiguous) or [k, ldb] (b_kn = 1:
+ * op(B) = B, N-contiguous, the weight as dequantised). k > 0 a multiple of 64, n a multiple of 8,
+ * strides multiples of 8, operands 16-byte aligned, each operand under 4 GiB. The partials feed
+ * rus_rmsnorm_bwd_parts, which sums them in part order.
+ * Replaces: d_norm2 = torch.mm(d_gu_c, w_gu) (solution/ops.py:939), an fp16 product there.
+ */
+int rus_gemm_parts(const void* a, int64_t lda, const void* b, int64_t ldb, int32_t b_kn,
+                   int64_t m, int64_t n, int64_t k, float* parts, int32_t n_split, void* stream);
 
 /*
  * Fused residual add + RMSNorm forward, one row per wavefront.

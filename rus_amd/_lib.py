@@ -11,7 +11,7 @@ import threading
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "librus_amd.so"
-ABI_VERSION = 11
+ABI_VERSION = 12
 
 DTYPE_F16 = 0
 DTYPE_F32 = 1
@@ -62,6 +62,7 @@ SIGNATURES: dict[str, list] = {
                           ctypes.POINTER(_i64)],
     "rus_nf4_gemm": [_vp, _i64, _i64, ctypes.POINTER(Nf4Job), _vp, _i64, _i64, _i32, _i32, _i32,
                      _vp, _vp, _i64, _i32, _vp, _i64, _vp, _i64, _vp],
+    "rus_gemm_parts": [_vp, _i64, _vp, _i64, _i32, _i64, _i64, _i64, _vp, _i32, _vp],
     "rus_lora_dropout_fwd": [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _vp, _u64, _u64, _f32, _f32, _i32, _vp],
     "rus_lora_dropout_bwd_add": [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _vp, _u64, _u64, _f32, _f32, _i32, _vp],
     "rus_graph_node_counts": [_vp, _vp, _i32],

@@ -1,7 +1,12 @@
 // Row functions of the vectorised RMSNorm forward and backward (one wavefront per row, 16-byte
-// packs held in registers between the reduction and the output pass), shared by the norm
-// kernels and by launches that run a norm beside other work (the NF4 dequant). No barriers:
+// packs held in registers between the reduction and the output pass), used by launches that run
+// a norm beside other work (the NF4 dequant) and by the norm kernels for wide rows. No barriers:
 // a wave whose row is past the end returns.
+//
+// Row sums follow one fixed order, which the multi-wave norm kernels (rmsnorm.hip) reproduce:
+// each 16-byte pack's terms are summed in element order, lane l adds its packs l, 64 + l,
+// 128 + l, ... in that order (a pack past the row contributes nothing), and a 64-lane butterfly
+// adds the lanes. The standalone and the riding norm therefore give the same bits.
 #pragma once
 
 #include "common.h"
@@ -53,8 +58,10 @@ __device__ __forceinline__ void rmsnorm_fwd_row(const T* __restrict__ x, const T
         for (int i = 0; i < V; ++i) h[it][i] = round_to<T>(h[it][i] + r[i]);
         store_from_f32<T, V>(sum_out + off + c, h[it]);
       }
+      float sp = 0.0f;
 #pragma unroll
-      for (int i = 0; i < V; ++i) ss += h[it][i] * h[it][i];
+      for (int i = 0; i < V; ++i) sp += h[it][i] * h[it][i];
+      ss += sp;
     }
   }
   ss = wave_sum(ss);
@@ -97,12 +104,14 @@ __device__ __forceinline__ void rmsnorm_bwd_row(const T* __restrict__ dy, const 
       load_f32<T, V>(h + off + c, xh[it]);
       load_f32<T, V>(dy + off + c, dv);
       load16<W, V>(w + c, wv);
+      float ap = 0.0f;
 #pragma unroll
       for (int i = 0; i < V; ++i) {
         xh[it][i] = xh[it][i] * r;
         g[it][i] = wv[i] * dv[i];
-        acc += xh[it][i] * g[it][i];
+        ap += xh[it][i] * g[it][i];
       }
+      acc += ap;
     }
   }
   const float cm = wave_sum(acc) / static_cast<float>(n_cols);

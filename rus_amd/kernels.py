@@ -595,6 +595,38 @@ def rms_norm_bwd(
     return dx.view(orig_shape)
 
 
+def gemm_parts_count(k: int, n_split: int) -> int:
+    """Number of pieces rus_gemm_parts cuts a K-long reduction into when asked for ``n_split``:
+    pieces of round_up(ceil(k / n_split), 64) columns."""
+    per = _round_up(-(-k // n_split), LM_K)
+    return -(-k // per)
+
+
+def gemm_parts(a: torch.Tensor, b: torch.Tensor, b_kn: bool, n_split: int,
+               out: torch.Tensor | None = None) -> torch.Tensor:
+    """fp32 split-K partials [S, M, N] of a . b (``b_kn``: b is [K, N]) or a . b^T (b is [N, K]),
+    S = gemm_parts_count(K, n_split); the split-K form of torch.mm(d_gu, W_gu)
+    (solution/ops.py:939) whose partials rms_norm_bwd_parts consumes."""
+    fn = "gemm_parts"
+    _require_device(fn, a, b, out)
+    for name, t in (("a", a), ("b", b)):
+        if t.dtype != torch.float16 or t.dim() != 2 or t.stride(1) != 1:
+            raise ValueError(f"{fn}: {name} must be a 2-D fp16 tensor with contiguous rows")
+    m, k = a.shape
+    n = b.shape[1] if b_kn else b.shape[0]
+    if (b.shape[0] if b_kn else b.shape[1]) != k:
+        raise ValueError(f"{fn}: inner dimensions differ: a {tuple(a.shape)}, b {tuple(b.shape)}")
+    sp = gemm_parts_count(k, n_split)
+    if out is None:
+        out = torch.empty(sp, m, n, dtype=torch.float32, device=a.device)
+    elif out.dtype != torch.float32 or tuple(out.shape) != (sp, m, n) or not out.is_contiguous():
+        raise ValueError(f"{fn}: out must be contiguous float32 [{sp}, {m}, {n}]")
+    _launch("gemm_parts", (m * k + k * n) * 2 + 4 * sp * m * n, 2.0 * m * n * k,
+            "rus_gemm_parts", a.data_ptr(), a.stride(0), b.data_ptr(), b.stride(0),
+            1 if b_kn else 0, m, n, k, out.data_ptr(), sp, _stream(a))
+    return out
+
+
 def rms_norm_bwd_parts(dy_parts: torch.Tensor, h: torch.Tensor, weight: torch.Tensor,
                        rstd: torch.Tensor, dresidual: torch.Tensor | None = None) -> torch.Tensor:
     """``rms_norm_bwd`` whose dy is fp16(sum over the leading axis of the fp32 partials
@@ -610,8 +642,8 @@ def rms_norm_bwd_parts(dy_parts: torch.Tensor, h: torch.Tensor, weight: torch.Te
     if dy_parts.dtype != torch.float32 or dy_parts.dim() != 3 or \
             tuple(dy_parts.shape[1:]) != (n_rows, n_cols) or not dy_parts.is_contiguous():
         raise ValueError(f"{fn}: dy_parts must be contiguous float32 [S, {n_rows}, {n_cols}]")
-    if not 1 <= dy_parts.shape[0] <= 8:
-        raise ValueError(f"{fn}: 1 to 8 partials, got {dy_parts.shape[0]}")
+    if not 1 <= dy_parts.shape[0] <= 64:
+        raise ValueError(f"{fn}: 1 to 64 partials, got {dy_parts.shape[0]}")
     wdt = _dtype_code(fn, weight.dtype)
     w = weight.contiguous()
     rs = rstd.contiguous()

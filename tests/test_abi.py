@@ -89,6 +89,14 @@ def test_header_compiles_as_c():
                                  16, 16, 16, 3, None), "counters"),
         # split-partial norm backward: n_parts out of range, width not a multiple of 8
         ("rus_rmsnorm_bwd_parts", (16, 0, 16, 16, 0, 16, None, 16, 4, 64, 64, None), "n_parts"),
+        ("rus_rmsnorm_bwd_parts", (16, 65, 16, 16, 0, 16, None, 16, 4, 64, 64, None), "n_parts"),
+        # split-K product: K not a multiple of 64, N not a multiple of 8, a split count that does
+        # not cut K into 64-wide pieces, a misaligned operand, an unknown B layout
+        ("rus_gemm_parts", (16, 96, 16, 96, 1, 4, 8, 96, 16, 1, None), "not a multiple of 64"),
+        ("rus_gemm_parts", (16, 64, 16, 16, 1, 4, 12, 64, 16, 1, None), "not a multiple of 8"),
+        ("rus_gemm_parts", (16, 128, 16, 16, 1, 4, 16, 128, 16, 3, None), "does not divide"),
+        ("rus_gemm_parts", (8, 64, 16, 16, 1, 4, 16, 64, 16, 1, None), "16-byte aligned"),
+        ("rus_gemm_parts", (16, 64, 16, 16, 2, 4, 16, 64, 16, 1, None), "bad sizes"),
         ("rus_rmsnorm_bwd_parts", (16, 2, 16, 16, 0, 16, None, 16, 4, 60, 60, None),
          "multiples of 8"),
         # LoRA weight gradients + expansion: width not a multiple of 32, missing dx

@@ -166,7 +166,8 @@ def test_nf4_dequant_rejects_short_absmax():
 @pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
 @pytest.mark.parametrize("wdtype", [torch.float16, torch.float32])
 @pytest.mark.parametrize("has_residual", [False, True])
-@pytest.mark.parametrize("shape", [(4, 128, 1536), (273, 1536), (880, 1536), (7, 1001), (5000, 896)])
+@pytest.mark.parametrize("shape", [(4, 128, 1536), (273, 1536), (880, 1536), (7, 1001), (5000, 896),
+                                   (3, 8960)])
 def test_rmsnorm_fwd_bwd(dtype, wdtype, has_residual, shape):
     g = torch.Generator().manual_seed(0)
     x = torch.randn(shape, generator=g).to(dtype)
@@ -204,7 +205,7 @@ def test_rmsnorm_fwd_bwd(dtype, wdtype, has_residual, shape):
 
 
 @pytest.mark.parametrize("wdtype", [torch.float16, torch.float32])
-@pytest.mark.parametrize("n_parts", [1, 3, 4])
+@pytest.mark.parametrize("n_parts", [1, 3, 4, 8, 11, 35])
 @pytest.mark.parametrize("has_residual", [False, True])
 @pytest.mark.parametrize("shape", [(707, 1536), (5, 896)])
 def test_rmsnorm_bwd_over_split_partials_equals_reduce_then_bwd(wdtype, n_parts, has_residual,
