@@ -52,6 +52,7 @@ struct AttnArgs {
   const int32_t* cu;
   f16* out;        // forward: O; backward kernel 1: dQ
   float* lse;      // [h_q, n_tok], natural log
+  float* dsum;     // backward: D = rowsum(dO o O) [h_q, n_tok]
   float* dk_part;  // [h_q, n_tok, 128]
   float* dv_part;
   f16* dk;         // [n_tok, h_kv, 128]
@@ -352,62 +353,172 @@ attn_fwd_kernel(AttnArgs a) {
 }
 
 // ---------------------------------------------------------------------------------------------
-// Backward 1: D = rowsum(dO o O) and dQ = scale * dS K. Block = (row, query block, head); the
-// kW waves split the key blocks and their dQ partials are summed at the end.
+// Backward. Every operand tile (32 tokens x 128 head dims of Q, dO, K or V) is copied straight
+// from global memory into LDS (global_load_lds_dwordx4: 4 rows x 256 contiguous bytes per wave
+// instruction, no registers in flight) and read from there both ways: 16-byte row fragments
+// (ds_read_b128) for S = Q K^T and dP = dO V^T, and transposed fragments (ds_read_b64_tr_b16) for
+// dV += P^T dO, dK += dS^T Q and dQ^T += K^T dS^T, so each tile is loaded once per use.
+// D = rowsum(dO o O) is formed once per (head, query) by a small kernel before the main launch.
 // ---------------------------------------------------------------------------------------------
-constexpr int kBwdBytes = kMax(2 * kW * kStageHalfs * 2, kParkBytes);  // LDS of a backward block
+typedef __attribute__((address_space(3))) void* lds_void_ptr;
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
 
+// Waves per backward block: 4 (80 KiB of LDS and at most 256 registers, so two blocks share a
+// CU and one block's waits overlap the other's work; 8 waves in one block per CU ran 13% slower).
+constexpr int kWB = 4;
+static_assert(kWB == 4 || kWB == 8, "4 or 8 waves per backward block");
+constexpr int kCopiesPerWave = 8 / kWB;  // a shared tile's 8 copies over the block's waves
+constexpr int kRegsPerWave = 64 / kWB;   // accumulator registers each wave sums in the merge
+constexpr int kTile = kBlk * kHD * 2;    // one 32 x 128 fp16 tile: 8 KiB
+// LDS of a backward block: 2 shared tiles + 2 per wave; the merge reuses it as a buffer of every
+// wave's four 32x32 fp32 accumulator tiles.
+constexpr int kBwdBytes = (2 + 2 * kWB) * kTile;
+static_assert(kWB * 64 * 64 * 4 <= kBwdBytes, "the merge buffer fits the tiles' LDS");
+
+// Tiles are row-major, 256 bytes per token row, with the 16-byte chunk c of row r stored at chunk
+// c ^ swz(r): a quarter wave's 16-byte fragment reads (16 consecutive rows, one chunk) and a
+// half wave's transposing reads (4 consecutive rows x 64 bytes) each cover the 64 banks once.
+__device__ __forceinline__ int swz(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
+
+// Issues copies i0 .. i0 + n - 1 of the 8 that fill a tile with token rows r0 .. r0 + 31 of a
+// [*, stride] head slice (rows clamped into [lo, hi): rows past a row's end repeat its last token,
+// finite values that the masks discard). Copy i fills tile rows 4 i .. 4 i + 3; lane l lands at
+// row 4 i + l / 16, position l % 16, so it loads the chunk (l % 16) ^ swz(row).
+__device__ __forceinline__ void tile_copy(char* tile, const f16* x, int64_t stride, int r0,
+                                          int lo, int hi, int i0, int n) {
+  const int lane = threadIdx.x & 63;
+  for (int i = i0; i < i0 + n; ++i) {
+    const int r = 4 * i + (lane >> 4);
+    int t = r0 + r;
+    t = t < hi ? t : hi - 1;
+    t = t < lo ? lo : t;
+    const int c = (lane & 15) ^ swz(r);
+    __builtin_amdgcn_global_load_lds(x + static_cast<int64_t>(t) * stride + c * 8,
+                                     (lds_void_ptr)(tile + i * 1024), 16, 0, 0);
+  }
+}
+
+// s_waitcnt vmcnt(0): this wave's tile copies have landed (expcnt / lgkmcnt not waited on).
+__device__ __forceinline__ void wait_copies() {
+  __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
+}
+
+// This wave's LDS reads have returned: a copy may now overwrite the tiles they read.
+__device__ __forceinline__ void wait_tile_reads() {
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0), vmcnt / expcnt not waited on
+  asm volatile("" ::: "memory");
+}
+
+// 16-byte fragment: head dims 8 c .. 8 c + 7 of tile row r.
+__device__ __forceinline__ f16x8 tile_frag(const char* tile, int r, int c) {
+  return *reinterpret_cast<const f16x8*>(tile + r * 256 + ((c ^ swz(r)) << 4));
+}
+
+// Transposed fragment of k-step s in the accumulator order k(h, i) = 16 s + 8 (i / 4) + 4 h +
+// i % 4, head-dim tile d: lane l holds x[k(h, i)][32 d + l % 32], i = 0..7. ds_read_b64_tr_b16
+// gives lane i of each 16-lane group element i % 4 of the 8 bytes read by lanes i / 4 + 4 e of
+// the group, so lane j of a group reads row k0 + j / 4, head dims n0 + 4 (j % 4) .. +4, and lane i
+// receives x[k0 + e][n0 + i], e = 0..3 (k0 = 16 s + 4 h, then + 8).
+__device__ __forceinline__ f16x8 tile_frag_t(const char* tile, int s, int d) {
+  const int lane = threadIdx.x & 63, j = lane & 15;
+  const int col = 32 * d + (lane & 16) + 4 * (j & 3);
+  const int r0 = 16 * s + 4 * (lane >> 5) + (j >> 2), r1 = r0 + 8;
+  const int cb = (col & 7) * 2;
+  const v4i16 x0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (lds_v4i16*)(tile + r0 * 256 + (((col >> 3) ^ swz(r0)) << 4) + cb));
+  const v4i16 x1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (lds_v4i16*)(tile + r1 * 256 + (((col >> 3) ^ swz(r1)) << 4) + cb));
+  const f16x4 a = __builtin_bit_cast(f16x4, x0), b = __builtin_bit_cast(f16x4, x1);
+  return f16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+}
+
+// Every wave's four 32x32 fp32 tiles into the merge buffer (the accumulator layout,
+// lane-contiguous); thread (wave w, lane) then sums tile w % 4, registers kRegsPerWave (w / 4)
+// .. + kRegsPerWave, over the waves in wave order.
+__device__ __forceinline__ void park_b(float* buf, const f32x16 (&acc)[4], int wave, int lane) {
+#pragma unroll
+  for (int d = 0; d < 4; ++d)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) buf[(wave * 64 + d * 16 + r) * 64 + lane] = acc[d][r];
+}
+
+__device__ __forceinline__ void merge_b(const float* buf, int wave, int lane,
+                                        float (&x)[kRegsPerWave]) {
+  const int tile = wave & 3, r0 = kRegsPerWave * (wave >> 2);
+#pragma unroll
+  for (int r = 0; r < kRegsPerWave; ++r) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kWB; ++w) acc += buf[(w * 64 + tile * 16 + r0 + r) * 64 + lane];
+    x[r] = acc;
+  }
+}
+
+// D[head][t] = rowsum(dO o O) over the head's 128 dims: 16 lanes per (token, head), 8 fp32
+// products of fp16 values per lane, summed in dim order, then over the lanes by a butterfly.
+__global__ __launch_bounds__(256) void attn_bwd_prep_kernel(const f16* __restrict__ o,
+                                                            const f16* __restrict__ dout,
+                                                            float* __restrict__ dsum,
+                                                            int64_t n_tok, int h_q) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  const int64_t pair = i >> 4;  // token * h_q + head
+  const int c = static_cast<int>(i & 15);
+  float acc = 0.0f;
+  if (pair < n_tok * h_q) {
+    const f16x8 x = *reinterpret_cast<const f16x8*>(o + pair * kHD + 8 * c);
+    const f16x8 y = *reinterpret_cast<const f16x8*>(dout + pair * kHD + 8 * c);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc += static_cast<float>(x[e]) * static_cast<float>(y[e]);
+  }
+#pragma unroll
+  for (int off = 8; off >= 1; off >>= 1) acc += __shfl_xor(acc, off, 16);
+  if (pair < n_tok * h_q && c == 0) {
+    const int64_t t = pair / h_q;
+    const int head = static_cast<int>(pair - t * h_q);
+    dsum[head * n_tok + t] = acc;
+  }
+}
+
+// dQ = scale * dS K. Block = (row, query block, head): the Q and dO tiles of its 32 queries are
+// shared; the kWB waves take key blocks w, w + kWB, ... (K and V tiles of their own) and their
+// dQ partials are summed in wave order at the end.
 __device__ __forceinline__ void attn_bwd_dq_block(const AttnArgs& a, int blk, char* smem) {
   int start, end, q0;
   if (!find_block<true>(a.cu, a.n_seq, static_cast<int>(a.n_tok), blk, start, end, q0)) return;
   const int head = blockIdx.x, g = head / (a.h_q / a.h_kv);
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, h = lane >> 5, col = lane & 31;
   const int64_t sq = static_cast<int64_t>(a.h_q) * kHD, skv = static_cast<int64_t>(a.h_kv) * kHD;
-  const f16* qh = a.q + head * kHD;
   const f16* kh = a.k + g * kHD;
   const f16* vh = a.v + g * kHD;
-  f16* kt = reinterpret_cast<f16*>(smem) + wave * kStageHalfs;
-
-  const int qi = q0 + col;
-  const int qr = qi < end ? qi : end - 1;
-  f16x8 qf[8], df[8];
-  load_frags(qf, qh, qr, sq, h);
-  load_frags(df, a.dout + head * kHD, qr, sq, h);
-  float dsum = 0.0f;
-#pragma unroll
-  for (int s = 0; s < 8; ++s) {
-    const f16x8 of = ld8(a.o + head * kHD, qr, sq, 16 * s + 8 * h);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) dsum += static_cast<float>(df[s][i]) * static_cast<float>(of[i]);
+  char* qt = smem;
+  char* dt = smem + kTile;
+  char* kt = smem + (2 + 2 * wave) * kTile;
+  char* vt = kt + kTile;
+  const int nk = (q0 - start) / kBlk + 1;
+  tile_copy(qt, a.q + head * kHD, sq, q0, start, end, kCopiesPerWave * wave, kCopiesPerWave);
+  tile_copy(dt, a.dout + head * kHD, sq, q0, start, end, kCopiesPerWave * wave, kCopiesPerWave);
+  if (wave < nk) {
+    const int k0 = start + wave * kBlk;
+    tile_copy(kt, kh, skv, k0, start, end, 0, 8);
+    tile_copy(vt, vh, skv, k0, start, end, 0, 8);
   }
-  dsum += __shfl_xor(dsum, 32, 64);
+  const int qi = q0 + col, qr = qi < end ? qi : end - 1;
+  const float dsum = a.dsum[head * a.n_tok + qr];
   const float lse2 = a.lse[head * a.n_tok + qr] * kLog2e;
+  wait_copies();
+  __syncthreads();  // every wave's share of the Q and dO tiles has landed
 
   f32x16 dq[4];
 #pragma unroll
   for (int d = 0; d < 4; ++d) dq[d] = f32x16{};
-  const int nk = (q0 - start) / kBlk + 1;
-  f16x8 kf[8], vf[8], kk[8];
-  if (wave < nk) {
-    const int k0 = start + wave * kBlk, kr = min(k0 + col, end - 1);
-    load_frags(kf, kh, kr, skv, h);
-    load_frags(vf, vh, kr, skv, h);
-    load_rows4(kk, kh, skv, k0, start, end);
-  }
-  for (int kb = wave; kb < nk; kb += kW) {
+  for (int kb = wave; kb < nk; kb += kWB) {
     const int k0 = start + kb * kBlk;
     f32x16 st = f32x16{}, dp = f32x16{};
 #pragma unroll
     for (int s = 0; s < 8; ++s) {
-      st = mfma(kf[s], qf[s], st);  // S^T = K Q^T
-      dp = mfma(vf[s], df[s], dp);  // dP^T = V dO^T
-    }
-    write_t4(kt, kk);
-    if (kb + kW < nk) {
-      const int k1 = k0 + kW * kBlk, kr = min(k1 + col, end - 1);
-      load_frags(kf, kh, kr, skv, h);
-      load_frags(vf, vh, kr, skv, h);
-      load_rows4(kk, kh, skv, k1, start, end);
+      st = mfma(tile_frag(kt, col, 2 * s + h), tile_frag(qt, col, 2 * s + h), st);  // S^T = K Q^T
+      dp = mfma(tile_frag(vt, col, 2 * s + h), tile_frag(dt, col, 2 * s + h), dp);  // dP^T = V dO^T
     }
     if (kb == nk - 1) {  // diagonal block: causal and row-end mask
 #pragma unroll
@@ -423,33 +534,42 @@ __device__ __forceinline__ void attn_bwd_dq_block(const AttnArgs& a, int blk, ch
     const f16x8 s0 = frag_acc(st, 0), s1 = frag_acc(st, 1);
 #pragma unroll
     for (int d = 0; d < 4; ++d) {
-      dq[d] = mfma(frag_t(kt, d * 32 + col, 0, h), s0, dq[d]);  // dQ^T += K^T dS^T
-      dq[d] = mfma(frag_t(kt, d * 32 + col, 1, h), s1, dq[d]);
+      dq[d] = mfma(tile_frag_t(kt, 0, d), s0, dq[d]);  // dQ^T += K^T dS^T
+      dq[d] = mfma(tile_frag_t(kt, 1, d), s1, dq[d]);
+    }
+    if (kb + kWB < nk) {  // the wave's next key block into its tiles
+      wait_tile_reads();
+      const int k1 = k0 + kWB * kBlk;
+      tile_copy(kt, kh, skv, k1, start, end, 0, 8);
+      tile_copy(vt, vh, skv, k1, start, end, 0, 8);
+      wait_copies();
     }
   }
-  __syncthreads();
+  __syncthreads();  // every wave is done with the tiles; the space becomes the merge buffer
   float* buf = reinterpret_cast<float*>(smem);
-  park(buf, dq, wave, lane);
+  park_b(buf, dq, wave, lane);
   __syncthreads();
   if (qi < end) {
-    float x[16];
+    float x[kRegsPerWave];
+    merge_b(buf, wave, lane, x);
+    // Register 4 r4 + i of tile d holds head dim 32 d + 8 r4 + 4 h + i.
+    const int d = wave & 3, r4b = (kRegsPerWave / 4) * (wave >> 2);
+    f16* row = a.out + qi * sq + head * kHD;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      float acc = 0.0f;
+    for (int r4 = 0; r4 < kRegsPerWave / 4; ++r4) {
+      f16x4 w;
 #pragma unroll
-      for (int w = 0; w < kW; ++w) acc += parked(buf, w, wave, r, lane);
-      x[r] = acc * a.scale;
+      for (int i = 0; i < 4; ++i) w[i] = from_f32<f16>(x[4 * r4 + i] * a.scale);
+      *reinterpret_cast<f16x4*>(row + d * 32 + 8 * (r4b + r4) + 4 * h) = w;
     }
-    store_tile_row(a.out + qi * sq + head * kHD, x, wave, h);
   }
 }
 
-// ---------------------------------------------------------------------------------------------
-// Backward 2: this query head's dK = scale * dS^T Q and dV = P^T dO for one 32-key block, fp32.
-// Block = (row, key block, head); the kW waves split the query blocks. The h_q / h_kv heads of a
-// KV group store fp32 partials; the last of them to finish sums the group in head order and
-// writes dK and dV once (no atomics on data, no separate reduce launch).
-// ---------------------------------------------------------------------------------------------
+// This query head's dK = scale * dS^T Q and dV = P^T dO for one 32-key block, fp32. Block = (row,
+// key block, head): the K and V tiles are shared; the kWB waves take query blocks (Q and dO tiles
+// of their own). The h_q / h_kv heads of a KV group store fp32 partials; the last of them to
+// finish sums the group in head order and writes dK and dV once (no atomics on data, no separate
+// reduce launch).
 __device__ __forceinline__ void attn_bwd_dkdv_block(const AttnArgs& a, int blk, char* smem) {
   int start, end, k0;
   if (!find_block<false>(a.cu, a.n_seq, static_cast<int>(a.n_tok), blk, start, end, k0)) return;
@@ -458,65 +578,37 @@ __device__ __forceinline__ void attn_bwd_dkdv_block(const AttnArgs& a, int blk, 
   const int64_t sq = static_cast<int64_t>(a.h_q) * kHD, skv = static_cast<int64_t>(a.h_kv) * kHD;
   const f16* qh = a.q + head * kHD;
   const f16* doh = a.dout + head * kHD;
-  const f16* kh = a.k + g * kHD;
-  const f16* vh = a.v + g * kHD;
-  f16* qt = reinterpret_cast<f16*>(smem) + 2 * wave * kStageHalfs;
-  f16* dt = qt + kStageHalfs;
   const float* lse = a.lse + head * a.n_tok;
-  const f16* oh = a.o + head * kHD;
-
+  const float* dsum = a.dsum + head * a.n_tok;
+  char* kt = smem;
+  char* vt = smem + kTile;
+  char* qt = smem + (2 + 2 * wave) * kTile;
+  char* dt = qt + kTile;
+  const int nq = (end - k0 + kBlk - 1) / kBlk;  // query blocks from the diagonal to the row end
+  tile_copy(kt, a.k + g * kHD, skv, k0, start, end, kCopiesPerWave * wave, kCopiesPerWave);
+  tile_copy(vt, a.v + g * kHD, skv, k0, start, end, kCopiesPerWave * wave, kCopiesPerWave);
+  if (wave < nq) {
+    const int q0 = k0 + wave * kBlk;
+    tile_copy(qt, qh, sq, q0, start, end, 0, 8);
+    tile_copy(dt, doh, sq, q0, start, end, 0, 8);
+  }
   const int kj = k0 + col;  // this lane's key (column of S = Q K^T)
-  f16x8 kf[8], vf[8];
-  load_frags(kf, kh, kj < end ? kj : end - 1, skv, h);
-  load_frags(vf, vh, kj < end ? kj : end - 1, skv, h);
+  wait_copies();
+  __syncthreads();  // every wave's share of the K and V tiles has landed
+
   f32x16 dk[4], dv[4];
 #pragma unroll
   for (int d = 0; d < 4; ++d) {
     dk[d] = f32x16{};
     dv[d] = f32x16{};
   }
-  const int nq = (end - k0 + kBlk - 1) / kBlk;  // query blocks from the diagonal to the row end
-  f16x8 qa[8], da[8], qs[8], ds[8], oa[8];
-  if (wave < nq) {
-    const int q0 = k0 + wave * kBlk, qrow = min(q0 + col, end - 1);
-    load_frags(qa, qh, qrow, sq, h);
-    load_frags(da, doh, qrow, sq, h);
-    load_frags(oa, oh, qrow, sq, h);
-    load_rows4(qs, qh, sq, q0, start, end);
-    load_rows4(ds, doh, sq, q0, start, end);
-  }
-  for (int qb = wave; qb < nq; qb += kW) {
+  for (int qb = wave; qb < nq; qb += kWB) {
     const int q0 = k0 + qb * kBlk;
-    // D = rowsum(dO o O) of query row q0 + col from this lane's half of the head dims and its
-    // partner's, then the 16 rows of this lane's accumulator registers by lane exchange.
-    float dcol = 0.0f;
-#pragma unroll
-    for (int k = 0; k < 8; ++k)
-#pragma unroll
-      for (int i = 0; i < 8; ++i) dcol += static_cast<float>(da[k][i]) * static_cast<float>(oa[k][i]);
-    dcol += __shfl_xor(dcol, 32, 64);
-    float lq[16], dr[16];  // lse (log2 units) and D of this lane's 16 query rows
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int qi = min(q0 + acc_row(r, h), end - 1);
-      lq[r] = lse[qi] * kLog2e;
-      dr[r] = __shfl(dcol, acc_row(r, h), 64);
-    }
     f32x16 st = f32x16{}, dp = f32x16{};
 #pragma unroll
     for (int s = 0; s < 8; ++s) {
-      st = mfma(qa[s], kf[s], st);  // S = Q K^T
-      dp = mfma(da[s], vf[s], dp);  // dP = dO V^T
-    }
-    write_t4(qt, qs);
-    write_t4(dt, ds);
-    if (qb + kW < nq) {
-      const int q1 = q0 + kW * kBlk, qrow = min(q1 + col, end - 1);
-      load_frags(qa, qh, qrow, sq, h);
-      load_frags(da, doh, qrow, sq, h);
-      load_frags(oa, oh, qrow, sq, h);
-      load_rows4(qs, qh, sq, q1, start, end);
-      load_rows4(ds, doh, sq, q1, start, end);
+      st = mfma(tile_frag(qt, col, 2 * s + h), tile_frag(kt, col, 2 * s + h), st);  // S = Q K^T
+      dp = mfma(tile_frag(dt, col, 2 * s + h), tile_frag(vt, col, 2 * s + h), dp);  // dP = dO V^T
     }
     // Query rows past the row's end (last block) and before the key (diagonal block) are
     // masked; key columns past the row's end only feed dK / dV rows that are not written.
@@ -524,85 +616,95 @@ __device__ __forceinline__ void attn_bwd_dkdv_block(const AttnArgs& a, int blk, 
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int qi = q0 + acc_row(r, h);
-      float p = exp2_raw(st[r] * a.scale_log2 - lq[r]);
+      const int qc = qi < end ? qi : end - 1;
+      float p = exp2_raw(st[r] * a.scale_log2 - lse[qc] * kLog2e);
       if (edge) p = (kj <= qi && qi < end) ? p : 0.0f;
-      st[r] = p;                    // P
-      dp[r] = p * (dp[r] - dr[r]);  // dS
+      st[r] = p;                         // P
+      dp[r] = p * (dp[r] - dsum[qc]);    // dS
     }
     const f16x8 p0 = frag_acc(st, 0), p1 = frag_acc(st, 1);
     const f16x8 s0 = frag_acc(dp, 0), s1 = frag_acc(dp, 1);
 #pragma unroll
     for (int d = 0; d < 4; ++d) {
-      dv[d] = mfma(p0, frag_t(dt, d * 32 + col, 0, h), dv[d]);  // dV += P^T dO
-      dv[d] = mfma(p1, frag_t(dt, d * 32 + col, 1, h), dv[d]);
-      dk[d] = mfma(s0, frag_t(qt, d * 32 + col, 0, h), dk[d]);  // dK += dS^T Q
-      dk[d] = mfma(s1, frag_t(qt, d * 32 + col, 1, h), dk[d]);
+      dv[d] = mfma(p0, tile_frag_t(dt, 0, d), dv[d]);  // dV += P^T dO
+      dv[d] = mfma(p1, tile_frag_t(dt, 1, d), dv[d]);
+      dk[d] = mfma(s0, tile_frag_t(qt, 0, d), dk[d]);  // dK += dS^T Q
+      dk[d] = mfma(s1, tile_frag_t(qt, 1, d), dk[d]);
+    }
+    if (qb + kWB < nq) {  // the wave's next query block into its tiles
+      wait_tile_reads();
+      const int q1 = q0 + kWB * kBlk;
+      tile_copy(qt, qh, sq, q1, start, end, 0, 8);
+      tile_copy(dt, doh, sq, q1, start, end, 0, 8);
+      wait_copies();
     }
   }
-  // Sum the waves' partials (dK, then dV through the same buffer). Rows are keys (accumulator
-  // rows), columns head dims (lanes); thread (wave w, lane) writes head-dim tile w.
+  // Sum the waves' partials (dK, then dV through the same buffer) and store this head's fp32
+  // partial. Rows are keys (accumulator rows), columns head dims (lanes); thread (wave w, lane)
+  // writes head-dim tile w % 4, key rows of registers kRegsPerWave (w / 4) .. + kRegsPerWave.
   float* buf = reinterpret_cast<float*>(smem);
+  const int dt4 = wave & 3, rb = kRegsPerWave * (wave >> 2);
 #pragma unroll
   for (int pass = 0; pass < 2; ++pass) {
     __syncthreads();
-    park(buf, pass == 0 ? dk : dv, wave, lane);
+    park_b(buf, pass == 0 ? dk : dv, wave, lane);
     __syncthreads();
+    float x[kRegsPerWave];
+    merge_b(buf, wave, lane, x);
     float* dst = pass == 0 ? a.dk_part : a.dv_part;
     const float sc = pass == 0 ? a.scale : 1.0f;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int key = k0 + acc_row(r, h);
-      float acc = 0.0f;
-#pragma unroll
-      for (int w = 0; w < kW; ++w) acc += parked(buf, w, wave, r, lane);
+    for (int r = 0; r < kRegsPerWave; ++r) {
+      const int key = k0 + acc_row(rb + r, h);
       if (key < end)
-        store_partial(dst + (static_cast<int64_t>(head) * a.n_tok + key) * kHD + wave * 32 + col,
-                      acc * sc);
+        store_partial(dst + (static_cast<int64_t>(head) * a.n_tok + key) * kHD + dt4 * 32 + col,
+                      x[r] * sc);
     }
   }
   const int grp = a.h_q / a.h_kv;
-  if (!arrive_last(a.counters + static_cast<int64_t>(blk) * a.h_kv + g, grp)) return;
+  // The verdict goes through the first word of the merge buffer, which every thread is done
+  // reading once arrive_last_at's first barrier has passed.
+  if (!arrive_last_at(a.counters + static_cast<int64_t>(blk) * a.h_kv + g, grp,
+                      reinterpret_cast<int*>(smem)))
+    return;
   // Last head of the group: dk[key, g, :] = fp16(sum over the group's heads in head order).
-  // Thread (wave, lane) owns head dims wave*32 + col of its 16 keys, as in the partial stores.
+  // Thread (wave, lane) owns head dims (wave % 4) * 32 + col of its keys, as in the stores.
 #pragma unroll
   for (int pass = 0; pass < 2; ++pass) {
     const float* src = pass == 0 ? a.dk_part : a.dv_part;
     f16* out = pass == 0 ? a.dk : a.dv;
-    // Every head's 16 loads are issued together (the partials are read device-coherently, from
+    // Every head's loads are issued together (the partials are read device-coherently, from
     // beyond this XCD's L2: one latency instead of one per head), then added in head order;
     // slots past the group re-read its last head and are not added.
-    float v[kMaxGroup][16];
+    float v[kMaxGroup][kRegsPerWave];
 #pragma unroll
     for (int j = 0; j < kMaxGroup; ++j) {
       const int jj = min(j, grp - 1);
-      const float* hsrc = src + static_cast<int64_t>(g * grp + jj) * a.n_tok * kHD + wave * 32 + col;
+      const float* hsrc =
+          src + static_cast<int64_t>(g * grp + jj) * a.n_tok * kHD + dt4 * 32 + col;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int key = min(k0 + acc_row(r, h), end - 1);  // rows past the end: read, not stored
+      for (int r = 0; r < kRegsPerWave; ++r) {
+        const int key = min(k0 + acc_row(rb + r, h), end - 1);  // past the end: read, not stored
         v[j][r] = load_partial(hsrc + static_cast<int64_t>(key) * kHD);
       }
     }
-    float acc[16];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      acc[r] = v[0][r];
+    for (int r = 0; r < kRegsPerWave; ++r) {
+      float acc = v[0][r];
 #pragma unroll
       for (int j = 1; j < kMaxGroup; ++j)
-        if (j < grp) acc[r] += v[j][r];
-    }
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int key = k0 + acc_row(r, h);
+        if (j < grp) acc += v[j][r];
+      const int key = k0 + acc_row(rb + r, h);
       if (key < end)
-        out[(static_cast<int64_t>(key) * a.h_kv + g) * kHD + wave * 32 + col] =
-            from_f32<f16>(acc[r]);
+        out[(static_cast<int64_t>(key) * a.h_kv + g) * kHD + dt4 * 32 + col] = from_f32<f16>(acc);
     }
   }
 }
 
 // Both backward passes in one launch: blocks y < max_blocks are dK/dV blocks (the heavier ones,
-// dispatched first), the rest dQ blocks; each forms D = rowsum(dO o O) for its own query rows.
-__global__ __launch_bounds__(64 * kW) void attn_bwd_kernel(AttnArgs a) {
+// dispatched first), the rest dQ blocks.
+__global__ __launch_bounds__(64 * kWB) __attribute__((amdgpu_waves_per_eu(2, 2))) void
+attn_bwd_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) char smem[kBwdBytes];
   if (static_cast<int>(blockIdx.y) < a.max_blocks)
     attn_bwd_dkdv_block(a, blockIdx.y, smem);
@@ -695,9 +797,10 @@ extern "C" int rus_attn_varlen_bwd(const void* q, const void* k, const void* v, 
   a.h_kv = h_kv;
   a.scale = scale;
   a.scale_log2 = scale * kLog2e;
-  // workspace: [h_q, n_tok] floats reserved | dk_part [h_q, n_tok, 128] | dv_part (alike)
+  // workspace: D [h_q, n_tok] (padded to 64 floats) | dk_part [h_q, n_tok, 128] | dv_part (alike)
   if (2 * static_cast<int64_t>(max_blocks) > 65535)
     return fail(RUS_ERR_UNSUPPORTED, "%s: max_blocks=%d (at most 32767)", fn, max_blocks);
+  a.dsum = workspace;
   a.dk_part = workspace + ((static_cast<int64_t>(h_q) * n_tokens + 63) / 64) * 64;
   a.dv_part = a.dk_part + static_cast<int64_t>(h_q) * n_tokens * kHD;
   hipStream_t st = static_cast<hipStream_t>(stream);
@@ -706,6 +809,9 @@ extern "C" int rus_attn_varlen_bwd(const void* q, const void* k, const void* v, 
   a.dv = static_cast<f16*>(dv);
   a.counters = counters;
   a.max_blocks = max_blocks;
-  hipLaunchKernelGGL(attn_bwd_kernel, dim3(h_q, 2 * max_blocks), dim3(64 * kW), 0, st, a);
+  const int64_t prep_threads = n_tokens * h_q * 16;
+  hipLaunchKernelGGL(attn_bwd_prep_kernel, dim3(static_cast<unsigned>((prep_threads + 255) / 256)),
+                     dim3(256), 0, st, a.o, a.dout, a.dsum, n_tokens, h_q);
+  hipLaunchKernelGGL(attn_bwd_kernel, dim3(h_q, 2 * max_blocks), dim3(64 * kWB), 0, st, a);
   return check_launch(fn);
 }

@@ -91,8 +91,9 @@ __device__ __forceinline__ float load_partial(const float* p) {
 // in the last of the n blocks sharing `counter` to arrive. Each thread waits for its own memory
 // accesses to complete before the block arrives; the last block puts the counter back to 0
 // (counters are zero when a launch starts and are left zero). No block waits for another.
-__device__ __forceinline__ bool arrive_last(int* counter, int n) {
-  __shared__ int s_last;
+// The block's verdict travels through `flag`, an int of LDS that no thread touches from the call
+// until it returns (callers whose LDS is full pass a word of memory they are done with).
+__device__ __forceinline__ bool arrive_last_at(int* counter, int n, int* flag) {
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
   __builtin_amdgcn_s_waitcnt(0);  // every memory access of this thread has completed
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
@@ -101,10 +102,15 @@ __device__ __forceinline__ bool arrive_last(int* counter, int n) {
     const int old = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const bool last = old == n - 1;
     if (last) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    s_last = last ? 1 : 0;
+    *flag = last ? 1 : 0;
   }
   __syncthreads();
-  return s_last != 0;
+  return *flag != 0;
+}
+
+__device__ __forceinline__ bool arrive_last(int* counter, int n) {
+  __shared__ int s_last;
+  return arrive_last_at(counter, n, &s_last);
 }
 
 }  // namespace rus
