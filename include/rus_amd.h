@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define RUS_ABI_VERSION 12
+#define RUS_ABI_VERSION 13
 
 #define RUS_DTYPE_F16 0
 #define RUS_DTYPE_F32 1
@@ -281,6 +281,23 @@ int rus_qkv_rope_bwd_mid(const void* dq_rot, const void* dk_rot, const void* dv,
                          int64_t stride_cos, int64_t n_pos, float scale_q, float scale_v,
                          int32_t h_q, int32_t h_kv, int32_t head_dim, int32_t* err_flag,
                          void* stream);
+
+/*
+ * rus_qkv_rope_bwd_mid with dK and dV given as the per-query-head fp32 partials that
+ * rus_attn_varlen_bwd_parts leaves ([h_q, n_tokens, head_dim] each, dK already scaled): each KV
+ * head's values are the sum of its h_q / h_kv query heads' partials in head order, rounded to
+ * fp16 once -- the dk / dv rus_attn_varlen_bwd writes -- so the packed outputs are the same.
+ * At most 8 query heads per KV head.
+ * Replaces: as rus_qkv_rope_bwd_mid, fed by the attention backward's sum over the expanded K/V
+ * heads (solution/ops.py:669-696, 903-928).
+ */
+int rus_qkv_rope_bwd_mid_parts(const void* dq_rot, const float* dk_part, const float* dv_part,
+                               const void* cos, const void* sin, const int64_t* pos_ids,
+                               void* dqkv, void* dq_lora, void* dv_lora, const void* bt_q,
+                               const void* bt_v, int32_t r, void* d_mid_q, void* d_mid_v,
+                               int64_t n_tokens, int64_t stride_dqkv, int64_t stride_cos,
+                               int64_t n_pos, float scale_q, float scale_v, int32_t h_q,
+                               int32_t h_kv, int32_t head_dim, int32_t* err_flag, void* stream);
 
 /*
  * LoRA-input dropout, both branches in one pass: out_a = dropout(x; stream_a, p_a),
@@ -655,8 +672,9 @@ int rus_attn_varlen_fwd(const void* q, const void* k, const void* v, const int32
  * Backward of rus_attn_varlen_fwd: dq like q, dk / dv like k / v (fp16; dk and dv sum the h_q /
  * h_kv query heads of each group in fp32 and are rounded once). out and lse are the forward's.
  * workspace: fp32, at least round_up(h_q * n_tokens, 64) + 2 * h_q * n_tokens * 128 elements
- * (the first part is reserved; then per-head dK and dV partials). Both passes (dQ, and dK / dV
- * with the sum over each group's heads) run as one launch; max_blocks at most 32767.
+ * (D = rowsum(dO o O) [h_q, n_tokens], padded to 64; then per-query-head dK and dV partials
+ * [h_q, n_tokens, 128] each, dK scaled). A small kernel forms D, then both passes (dQ, and
+ * dK / dV with the sum over each group's heads) run as one launch; max_blocks at most 32767.
  * counters: int32, at least max_blocks * h_kv, zero before the first call and left zero (calls
  * sharing them must not run concurrently).
  * Replaces: the autograd backward of solution/ops.py:669-696 (torch SDPA backward plus the
@@ -668,6 +686,18 @@ int rus_attn_varlen_bwd(const void* q, const void* k, const void* v, const void*
                         int32_t h_kv, int32_t head_dim, float scale, void* dq, void* dk,
                         void* dv, float* workspace, int32_t* counters, int64_t n_counters,
                         void* stream);
+
+/*
+ * rus_attn_varlen_bwd without the sum over each KV group's query heads: dq as there; dK and dV
+ * stay in the workspace as the per-query-head fp32 partials (layout above), for
+ * rus_qkv_rope_bwd_mid_parts to sum while it packs them (no counters, no dk / dv outputs).
+ * Replaces: as rus_attn_varlen_bwd.
+ */
+int rus_attn_varlen_bwd_parts(const void* q, const void* k, const void* v, const void* out,
+                              const void* dout, const float* lse, const int32_t* cu_seqlens,
+                              int32_t n_seq, int64_t n_tokens, int32_t max_blocks, int32_t h_q,
+                              int32_t h_kv, int32_t head_dim, float scale, void* dq,
+                              float* workspace, void* stream);
 
 #ifdef __cplusplus
 }

@@ -11,7 +11,7 @@ import threading
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "librus_amd.so"
-ABI_VERSION = 12
+ABI_VERSION = 13
 
 DTYPE_F16 = 0
 DTYPE_F32 = 1
@@ -87,11 +87,16 @@ SIGNATURES: dict[str, list] = {
                             _vp],
     "rus_attn_varlen_bwd": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i64, _i32, _i32, _i32, _i32,
                             _f32, _vp, _vp, _vp, _vp, _vp, _i64, _vp],
+    "rus_attn_varlen_bwd_parts": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i64, _i32, _i32,
+                                  _i32, _i32, _f32, _vp, _vp, _vp],
     "rus_rmsnorm_fwd": [_vp, _vp, _vp, _i32, _vp, _vp, _vp, _i64, _i64, _i64, _f32, _i32, _vp],
     "rus_rmsnorm_bwd": [_vp, _vp, _vp, _i32, _vp, _vp, _vp, _i64, _i64, _i64, _i32, _vp],
     "rus_rmsnorm_bwd_parts": [_vp, _i32, _vp, _vp, _i32, _vp, _vp, _vp, _i64, _i64, _i64, _vp],
     "rus_qkv_rope_bwd_mid": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _vp,
                              _i64, _i64, _i64, _i64, _f32, _f32, _i32, _i32, _i32, _vp, _vp],
+    "rus_qkv_rope_bwd_mid_parts": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                                   _i32, _vp, _vp, _i64, _i64, _i64, _i64, _f32, _f32,
+                                   _i32, _i32, _i32, _vp, _vp],
     "rus_qkv_lora_rope_fwd": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64,
                               _i64, _i64, _f32, _f32, _i32, _i32, _i32, _vp, _i32, _vp],
     "rus_qkv_rope_bwd": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _f32,

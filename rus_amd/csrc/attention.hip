@@ -61,6 +61,7 @@ struct AttnArgs {
   int64_t n_tok;
   int n_seq, h_q, h_kv;
   int max_blocks;  // backward: blocks per pass (grid y of each pass)
+  int group_sum;   // backward: 1 = sum each KV group's dK / dV partials into dk / dv
   float scale, scale_log2;
 };
 
@@ -661,6 +662,7 @@ __device__ __forceinline__ void attn_bwd_dkdv_block(const AttnArgs& a, int blk, 
                       x[r] * sc);
     }
   }
+  if (!a.group_sum) return;  // the partials are the output (summed by the RoPE backward)
   const int grp = a.h_q / a.h_kv;
   // The verdict goes through the first word of the merge buffer, which every thread is done
   // reading once arrive_last_at's first barrier has passed.
@@ -761,28 +763,29 @@ extern "C" int rus_attn_varlen_fwd(const void* q, const void* k, const void* v,
   return check_launch(fn);
 }
 
-extern "C" int rus_attn_varlen_bwd(const void* q, const void* k, const void* v, const void* out,
-                                   const void* dout, const float* lse,
-                                   const int32_t* cu_seqlens, int32_t n_seq, int64_t n_tokens,
-                                   int32_t max_blocks, int32_t h_q, int32_t h_kv,
-                                   int32_t head_dim, float scale, void* dq, void* dk, void* dv,
-                                   float* workspace, int32_t* counters, int64_t n_counters,
-                                   void* stream) {
+static int attn_bwd(const char* fn, const void* q, const void* k, const void* v,
+                    const void* out, const void* dout, const float* lse,
+                    const int32_t* cu_seqlens, int32_t n_seq, int64_t n_tokens,
+                    int32_t max_blocks, int32_t h_q, int32_t h_kv, int32_t head_dim, float scale,
+                    void* dq, void* dk, void* dv, float* workspace, int32_t* counters,
+                    int64_t n_counters, bool group_sum, void* stream) {
   using namespace rus;
-  const char* fn = "rus_attn_varlen_bwd";
   if (int e = check(fn, q, k, v, cu_seqlens, n_tokens, n_seq, h_q, h_kv, head_dim, max_blocks))
     return e;
-  if (!out || !dout || !lse || !dq || !dk || !dv || !workspace || !aligned(out, 16) ||
-      !aligned(dout, 16) || !aligned(dq, 16) || !aligned(dk, 16) || !aligned(dv, 16) ||
-      !aligned(workspace, 16) || !counters || !aligned(counters, 4))
+  if (!out || !dout || !lse || !dq || !workspace || !aligned(out, 16) || !aligned(dout, 16) ||
+      !aligned(dq, 16) || !aligned(workspace, 16))
     return fail(RUS_ERR_INVALID, "%s: null or misaligned argument", fn);
-  if (h_q / h_kv > kMaxGroup)
-    return fail(RUS_ERR_UNSUPPORTED, "%s: %d query heads per KV head (at most %d)", fn,
-                h_q / h_kv, kMaxGroup);
-  if (n_counters < static_cast<int64_t>(max_blocks) * h_kv)
-    return fail(RUS_ERR_INVALID, "%s: %lld counters, need max_blocks * h_kv = %lld", fn,
-                static_cast<long long>(n_counters),
-                static_cast<long long>(max_blocks) * h_kv);
+  if (group_sum) {
+    if (!dk || !dv || !aligned(dk, 16) || !aligned(dv, 16) || !counters || !aligned(counters, 4))
+      return fail(RUS_ERR_INVALID, "%s: null or misaligned argument", fn);
+    if (h_q / h_kv > kMaxGroup)
+      return fail(RUS_ERR_UNSUPPORTED, "%s: %d query heads per KV head (at most %d)", fn,
+                  h_q / h_kv, kMaxGroup);
+    if (n_counters < static_cast<int64_t>(max_blocks) * h_kv)
+      return fail(RUS_ERR_INVALID, "%s: %lld counters, need max_blocks * h_kv = %lld", fn,
+                  static_cast<long long>(n_counters),
+                  static_cast<long long>(max_blocks) * h_kv);
+  }
   AttnArgs a{};
   a.q = static_cast<const f16*>(q);
   a.k = static_cast<const f16*>(k);
@@ -809,9 +812,33 @@ extern "C" int rus_attn_varlen_bwd(const void* q, const void* k, const void* v, 
   a.dv = static_cast<f16*>(dv);
   a.counters = counters;
   a.max_blocks = max_blocks;
+  a.group_sum = group_sum ? 1 : 0;
   const int64_t prep_threads = n_tokens * h_q * 16;
   hipLaunchKernelGGL(attn_bwd_prep_kernel, dim3(static_cast<unsigned>((prep_threads + 255) / 256)),
                      dim3(256), 0, st, a.o, a.dout, a.dsum, n_tokens, h_q);
   hipLaunchKernelGGL(attn_bwd_kernel, dim3(h_q, 2 * max_blocks), dim3(64 * kWB), 0, st, a);
   return check_launch(fn);
+}
+
+extern "C" int rus_attn_varlen_bwd(const void* q, const void* k, const void* v, const void* out,
+                                   const void* dout, const float* lse,
+                                   const int32_t* cu_seqlens, int32_t n_seq, int64_t n_tokens,
+                                   int32_t max_blocks, int32_t h_q, int32_t h_kv,
+                                   int32_t head_dim, float scale, void* dq, void* dk, void* dv,
+                                   float* workspace, int32_t* counters, int64_t n_counters,
+                                   void* stream) {
+  return attn_bwd("rus_attn_varlen_bwd", q, k, v, out, dout, lse, cu_seqlens, n_seq, n_tokens,
+                  max_blocks, h_q, h_kv, head_dim, scale, dq, dk, dv, workspace, counters,
+                  n_counters, true, stream);
+}
+
+extern "C" int rus_attn_varlen_bwd_parts(const void* q, const void* k, const void* v,
+                                         const void* out, const void* dout, const float* lse,
+                                         const int32_t* cu_seqlens, int32_t n_seq,
+                                         int64_t n_tokens, int32_t max_blocks, int32_t h_q,
+                                         int32_t h_kv, int32_t head_dim, float scale, void* dq,
+                                         float* workspace, void* stream) {
+  return attn_bwd("rus_attn_varlen_bwd_parts", q, k, v, out, dout, lse, cu_seqlens, n_seq,
+                  n_tokens, max_blocks, h_q, h_kv, head_dim, scale, dq, nullptr, nullptr,
+                  workspace, nullptr, 0, false, stream);
 }

@@ -281,7 +281,35 @@ struct RopeBwdMidArgs {
   const f16* bt_v;  // [R, h_kv * head_dim]
   f16* dmid_q;      // [N, R]
   f16* dmid_v;
+  // Non-null: dK and dV come as the attention backward's fp32 per-query-head partials
+  // [h_q, N, head_dim] (b.dk / b.dv unused), each KV group's heads summed here.
+  const float* dk_part;
+  const float* dv_part;
 };
+
+constexpr int kMaxGroupSum = 8;  // query heads per KV head the partial sums support
+
+// dK or dV values c .. c + kSpan of KV head kv, token t, from the per-query-head partials: the
+// group's h_q / h_kv heads added in head order in fp32, rounded to fp16 once (the values the
+// attention backward's own group sum writes).
+__device__ __forceinline__ void load_group_sum(const float* __restrict__ part, int kv, int grp,
+                                               int64_t n_tok, int64_t t, int c, int head_dim,
+                                               float (&out)[kSpan]) {
+  const float* p = part + (static_cast<int64_t>(kv) * grp * n_tok + t) * head_dim + c;
+  const int64_t hs = n_tok * head_dim;
+  float v[kMaxGroupSum][kSpan];
+#pragma unroll
+  for (int j = 0; j < kMaxGroupSum; ++j)
+    if (j < grp) load_f32<float, kSpan>(p + j * hs, v[j]);
+#pragma unroll
+  for (int i = 0; i < kSpan; ++i) {
+    float acc = v[0][i];
+#pragma unroll
+    for (int j = 1; j < kMaxGroupSum; ++j)
+      if (j < grp) acc += v[j][i];
+    out[i] = round_to<f16>(acc);
+  }
+}
 
 constexpr int kMidR = 16;  // rank of the fused d_mid products
 
@@ -366,9 +394,15 @@ __global__ __launch_bounds__(kThreads) void rope_bwd_mid_kernel(RopeBwdMidArgs m
     float lo[kSpan], hi[kSpan];
     if (is_v) {  // dV: copy, scale into dv_lora, d_mid_v partials
       const int kv = hd - a.h_q - a.h_kv;
-      const f16* src = a.dv + (t * a.h_kv + kv) * a.head_dim;
-      load_f32<f16, kSpan>(src + j, lo);
-      load_f32<f16, kSpan>(src + j + half, hi);
+      if (m.dv_part) {
+        const int grp = a.h_q / a.h_kv;
+        load_group_sum(m.dv_part, kv, grp, a.n_tokens, t, j, a.head_dim, lo);
+        load_group_sum(m.dv_part, kv, grp, a.n_tokens, t, j + half, a.head_dim, hi);
+      } else {
+        const f16* src = a.dv + (t * a.h_kv + kv) * a.head_dim;
+        load_f32<f16, kSpan>(src + j, lo);
+        load_f32<f16, kSpan>(src + j + half, hi);
+      }
       store_from_f32<f16, kSpan>(out + j, lo);
       store_from_f32<f16, kSpan>(out + j + half, hi);
 #pragma unroll
@@ -381,10 +415,16 @@ __global__ __launch_bounds__(kThreads) void rope_bwd_mid_kernel(RopeBwdMidArgs m
       store_from_f32<f16, kSpan>(l + j + half, hi);
       mid_partial(p, lo, hi, f);
     } else {
-      const f16* src = hd < a.h_q ? a.dq + (t * a.h_q + hd) * a.head_dim
-                                  : a.dk + (t * a.h_kv + (hd - a.h_q)) * a.head_dim;
-      load_f32<f16, kSpan>(src + j, lo);
-      load_f32<f16, kSpan>(src + j + half, hi);
+      if (!is_q && m.dk_part) {
+        const int grp = a.h_q / a.h_kv;
+        load_group_sum(m.dk_part, hd - a.h_q, grp, a.n_tokens, t, j, a.head_dim, lo);
+        load_group_sum(m.dk_part, hd - a.h_q, grp, a.n_tokens, t, j + half, a.head_dim, hi);
+      } else {
+        const f16* src = is_q ? a.dq + (t * a.h_q + hd) * a.head_dim
+                              : a.dk + (t * a.h_kv + (hd - a.h_q)) * a.head_dim;
+        load_f32<f16, kSpan>(src + j, lo);
+        load_f32<f16, kSpan>(src + j + half, hi);
+      }
       const int64_t ps = clamp_pos(a.pos, t, a.n_pos, a.err_flag);
       float cl[kSpan], ch[kSpan], sl[kSpan], sh[kSpan];
       const f16* cr = a.cos + ps * a.stride_cos;
@@ -510,8 +550,7 @@ int bwd_typed(const RopeBwdArgs<T>& a, hipStream_t st) {
   return check_launch("rus_qkv_rope_bwd");
 }
 
-int bwd_mid(const RopeBwdMidArgs& m, hipStream_t st) {
-  const char* fn = "rus_qkv_rope_bwd_mid";
+int bwd_mid(const char* fn, const RopeBwdMidArgs& m, hipStream_t st) {
   const RopeBwdArgs<f16>& a = m.b;
   const int per_head = a.head_dim / 2 / kSpan;
   const int slots = (a.h_q + 2 * a.h_kv) * per_head;
@@ -519,11 +558,16 @@ int bwd_mid(const RopeBwdMidArgs& m, hipStream_t st) {
     return fail(RUS_ERR_UNSUPPORTED,
                 "%s: h_q=%d h_kv=%d head_dim=%d: a token's slots must divide %d and each head "
                 "kind's slots be a multiple of 16", fn, a.h_q, a.h_kv, a.head_dim, kThreads);
-  if (!aligned(a.dq, 16) || !aligned(a.dk, 16) || !aligned(a.dv, 16) ||
+  const bool parts = m.dk_part != nullptr;
+  if (!aligned(a.dq, 16) || (parts ? !aligned(m.dk_part, 16) : !aligned(a.dk, 16)) ||
+      (parts ? !aligned(m.dv_part, 16) : !aligned(a.dv, 16)) ||
       !aligned8<f16>(a.cos, a.stride_cos) || !aligned8<f16>(a.sin, a.stride_cos) ||
       !aligned8<f16>(a.dqkv, a.stride_dqkv) || !aligned(a.dq_lora, 16) ||
       !aligned(a.dv_lora, 16) || !aligned(m.bt_q, 16) || !aligned(m.bt_v, 16))
     return fail(RUS_ERR_INVALID, "%s: pointers/strides must be 16-byte aligned", fn);
+  if (parts && a.h_q / a.h_kv > kMaxGroupSum)
+    return fail(RUS_ERR_UNSUPPORTED, "%s: %d query heads per KV head (at most %d)", fn,
+                a.h_q / a.h_kv, kMaxGroupSum);
   const int64_t tpb = kThreads / slots;
   const dim3 grid(static_cast<unsigned>((a.n_tokens + tpb - 1) / tpb));
   hipLaunchKernelGGL(rope_bwd_mid_kernel, grid, dim3(kThreads), 0, st, m);
@@ -650,22 +694,21 @@ extern "C" int rus_qkv_lora_rope_fwd_mid(const void* qkv, const void* mid_q, con
   return fwd_mid(a, r, static_cast<hipStream_t>(stream));
 }
 
-extern "C" int rus_qkv_rope_bwd_mid(const void* dq_rot, const void* dk_rot, const void* dv,
-                                    const void* cos, const void* sin, const int64_t* pos_ids,
-                                    void* dqkv, void* dq_lora, void* dv_lora, const void* bt_q,
-                                    const void* bt_v, int32_t r, void* d_mid_q, void* d_mid_v,
-                                    int64_t n_tokens, int64_t stride_dqkv, int64_t stride_cos,
-                                    int64_t n_pos, float scale_q, float scale_v, int32_t h_q,
-                                    int32_t h_kv, int32_t head_dim, int32_t* err_flag,
-                                    void* stream) {
+static int rope_bwd_mid_entry(const char* fn, const void* dq_rot, const void* dk_rot,
+                              const void* dv, const float* dk_part, const float* dv_part,
+                              const void* cos, const void* sin, const int64_t* pos_ids,
+                              void* dqkv, void* dq_lora, void* dv_lora, const void* bt_q,
+                              const void* bt_v, int32_t r, void* d_mid_q, void* d_mid_v,
+                              int64_t n_tokens, int64_t stride_dqkv, int64_t stride_cos,
+                              int64_t n_pos, float scale_q, float scale_v, int32_t h_q,
+                              int32_t h_kv, int32_t head_dim, int32_t* err_flag, void* stream) {
   using namespace rus;
-  const char* fn = "rus_qkv_rope_bwd_mid";
   if (int e = check_heads(fn, n_tokens, h_q, h_kv, head_dim, n_pos, stride_cos, RUS_DTYPE_F16))
     return e;
   if (r != kMidR) return fail(RUS_ERR_UNSUPPORTED, "%s: rank %d (only %d)", fn, r, kMidR);
   if (n_tokens == 0) return RUS_OK;
-  if (!dq_rot || !dk_rot || !dv || !cos || !sin || !pos_ids || !dqkv || !dq_lora || !dv_lora ||
-      !bt_q || !bt_v || !d_mid_q || !d_mid_v)
+  if (!dq_rot || !(dk_rot || dk_part) || !(dv || dv_part) || !cos || !sin || !pos_ids || !dqkv ||
+      !dq_lora || !dv_lora || !bt_q || !bt_v || !d_mid_q || !d_mid_v)
     return fail(RUS_ERR_INVALID, "%s: null pointer argument", fn);
   if (stride_dqkv < static_cast<int64_t>(h_q + 2 * h_kv) * head_dim)
     return fail(RUS_ERR_INVALID, "%s: stride_dqkv smaller than a row", fn);
@@ -684,5 +727,39 @@ extern "C" int rus_qkv_rope_bwd_mid(const void* dq_rot, const void* dk_rot, cons
   m.bt_v = static_cast<const f16*>(bt_v);
   m.dmid_q = static_cast<f16*>(d_mid_q);
   m.dmid_v = static_cast<f16*>(d_mid_v);
-  return bwd_mid(m, static_cast<hipStream_t>(stream));
+  m.dk_part = dk_part;
+  m.dv_part = dv_part;
+  return bwd_mid(fn, m, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int rus_qkv_rope_bwd_mid(const void* dq_rot, const void* dk_rot, const void* dv,
+                                    const void* cos, const void* sin, const int64_t* pos_ids,
+                                    void* dqkv, void* dq_lora, void* dv_lora, const void* bt_q,
+                                    const void* bt_v, int32_t r, void* d_mid_q, void* d_mid_v,
+                                    int64_t n_tokens, int64_t stride_dqkv, int64_t stride_cos,
+                                    int64_t n_pos, float scale_q, float scale_v, int32_t h_q,
+                                    int32_t h_kv, int32_t head_dim, int32_t* err_flag,
+                                    void* stream) {
+  if (!dk_rot || !dv) return rus::fail(RUS_ERR_INVALID, "rus_qkv_rope_bwd_mid: null pointer argument");
+  return rope_bwd_mid_entry("rus_qkv_rope_bwd_mid", dq_rot, dk_rot, dv, nullptr, nullptr, cos,
+                            sin, pos_ids, dqkv, dq_lora, dv_lora, bt_q, bt_v, r, d_mid_q,
+                            d_mid_v, n_tokens, stride_dqkv, stride_cos, n_pos, scale_q, scale_v,
+                            h_q, h_kv, head_dim, err_flag, stream);
+}
+
+extern "C" int rus_qkv_rope_bwd_mid_parts(const void* dq_rot, const float* dk_part,
+                                          const float* dv_part, const void* cos, const void* sin,
+                                          const int64_t* pos_ids, void* dqkv, void* dq_lora,
+                                          void* dv_lora, const void* bt_q, const void* bt_v,
+                                          int32_t r, void* d_mid_q, void* d_mid_v,
+                                          int64_t n_tokens, int64_t stride_dqkv,
+                                          int64_t stride_cos, int64_t n_pos, float scale_q,
+                                          float scale_v, int32_t h_q, int32_t h_kv,
+                                          int32_t head_dim, int32_t* err_flag, void* stream) {
+  if (!dk_part || !dv_part)
+    return rus::fail(RUS_ERR_INVALID, "rus_qkv_rope_bwd_mid_parts: null pointer argument");
+  return rope_bwd_mid_entry("rus_qkv_rope_bwd_mid_parts", dq_rot, nullptr, nullptr, dk_part,
+                            dv_part, cos, sin, pos_ids, dqkv, dq_lora, dv_lora, bt_q, bt_v, r,
+                            d_mid_q, d_mid_v, n_tokens, stride_dqkv, stride_cos, n_pos, scale_q,
+                            scale_v, h_q, h_kv, head_dim, err_flag, stream);
 }

@@ -34,6 +34,7 @@ __all__ = [
     "qkv_rope_bwd",
     "qkv_rope_bwd_lora",
     "qkv_rope_bwd_lora_mid",
+    "qkv_rope_bwd_lora_mid_parts",
     "rope_bwd_mid_supported",
     "lora_dropout_fwd",
     "lora_dropout_bwd_add",
@@ -66,6 +67,9 @@ __all__ = [
     "transpose_rows",
     "attn_varlen_fwd",
     "attn_varlen_bwd",
+    "attn_varlen_bwd_parts",
+    "gemm_parts",
+    "gemm_parts_count",
 ]
 
 
@@ -732,7 +736,7 @@ def qkv_rope_fwd(
 
 
 def _rope_bwd(fn, dq_rot, dk_rot, dv_out, cos, sin, pos_ids, h_q, h_kv, head_dim, scale_q,
-              scale_v, with_lora, mid=None):
+              scale_v, with_lora, mid=None, parts=False):
     _require_device(fn, dq_rot, dk_rot, dv_out, cos, sin, pos_ids)
     dt = _dtype_code(fn, dq_rot.dtype)
     n_tokens = dq_rot.shape[0]
@@ -740,9 +744,14 @@ def _rope_bwd(fn, dq_rot, dk_rot, dv_out, cos, sin, pos_ids, h_q, h_kv, head_dim
     dq_c = dq_rot.contiguous()
     dk_c = dk_rot.contiguous()
     dv_c = dv_out.contiguous()
-    for name, t, width in (("dq_rot", dq_c, q_dim), ("dk_rot", dk_c, kv_dim), ("dv_out", dv_c, kv_dim)):
-        if t.numel() != n_tokens * width or t.dtype != dq_c.dtype:
-            raise ValueError(f"{fn}: {name} must hold [{n_tokens}, {width}] of {dq_c.dtype}")
+    checks = [("dq_rot", dq_c, q_dim, dq_c.dtype)]
+    if parts:  # per-query-head fp32 partials [h_q, n_tokens, head_dim]
+        checks += [("dk_part", dk_c, q_dim, torch.float32), ("dv_part", dv_c, q_dim, torch.float32)]
+    else:
+        checks += [("dk_rot", dk_c, kv_dim, dq_c.dtype), ("dv_out", dv_c, kv_dim, dq_c.dtype)]
+    for name, t, width, dtype in checks:
+        if t.numel() != n_tokens * width or t.dtype != dtype:
+            raise ValueError(f"{fn}: {name} must hold [{n_tokens}, {width}] of {dtype}")
     cos = _rows(fn, cos, head_dim, "cos")
     sin = _rows(fn, sin, head_dim, "sin")
     if cos.dtype != dq_c.dtype or sin.dtype != dq_c.dtype or sin.stride(0) != cos.stride(0):
@@ -762,10 +771,12 @@ def _rope_bwd(fn, dq_rot, dk_rot, dv_out, cos, sin, pos_ids, h_q, h_kv, head_dim
         r = bt_q.shape[0]
         dmq = torch.empty((n_tokens, r), dtype=dq_c.dtype, device=dq_c.device)
         dmv = torch.empty((n_tokens, r), dtype=dq_c.dtype, device=dq_c.device)
+        extra = n_tokens * (8 * q_dim - 4 * kv_dim) if parts else 0  # fp32 partials read
         _launch(
             "rope_bwd", n_tokens * (es * (2 * width + 2 * head_dim + q_dim + kv_dim + 2 * r) + 8)
-            + es * r * (q_dim + kv_dim), 2 * n_tokens * r * (q_dim + kv_dim),
-            "rus_qkv_rope_bwd_mid", dq_c.data_ptr(), dk_c.data_ptr(), dv_c.data_ptr(),
+            + es * r * (q_dim + kv_dim) + extra, 2 * n_tokens * r * (q_dim + kv_dim),
+            "rus_qkv_rope_bwd_mid_parts" if parts else "rus_qkv_rope_bwd_mid",
+            dq_c.data_ptr(), dk_c.data_ptr(), dv_c.data_ptr(),
             cos.data_ptr(), sin.data_ptr(), pos.data_ptr(), dqkv.data_ptr(), dql.data_ptr(),
             dvl.data_ptr(), bt_q.data_ptr(), bt_v.data_ptr(), r, dmq.data_ptr(), dmv.data_ptr(),
             n_tokens, dqkv.stride(0), cos.stride(0), cos.shape[0], float(scale_q),
@@ -813,6 +824,26 @@ def qkv_rope_bwd_lora_mid(dq_rot, dk_rot, dv_out, cos, sin, pos_ids, scale_q: fl
     _lora_operand(fn, bt_v, (r, h_kv * head_dim), "bt_v")
     return _rope_bwd(fn, dq_rot, dk_rot, dv_out, cos, sin, pos_ids, h_q, h_kv, head_dim, scale_q,
                      scale_v, True, mid=(bt_q, bt_v))
+
+
+def qkv_rope_bwd_lora_mid_parts(dq_rot, dk_part, dv_part, cos, sin, pos_ids, scale_q: float,
+                                scale_v: float, bt_q: torch.Tensor, bt_v: torch.Tensor,
+                                h_q: int = 12, h_kv: int = 2, head_dim: int = 128):
+    """``qkv_rope_bwd_lora_mid`` fed by ``attn_varlen_bwd_parts``: dK and dV are the fp32
+    per-query-head partials [h_q, N, head_dim], summed over each KV group in head order and
+    rounded once inside the launch (the same values as the attention's own group sum)."""
+    fn = "qkv_rope_bwd_lora_mid_parts"
+    _require_device(fn, dq_rot, dk_part, dv_part, cos, sin, pos_ids, bt_q, bt_v)
+    if dq_rot.dtype != torch.float16:
+        raise ValueError(f"{fn}: fp16 gradients only")
+    r = bt_q.shape[0]
+    if not rope_bwd_mid_supported(h_q, h_kv, head_dim, r) or h_q // h_kv > 8:
+        raise ValueError(f"{fn}: unsupported layout h_q={h_q} h_kv={h_kv} head_dim={head_dim} "
+                         f"rank={r}")
+    _lora_operand(fn, bt_q, (r, h_q * head_dim), "bt_q")
+    _lora_operand(fn, bt_v, (r, h_kv * head_dim), "bt_v")
+    return _rope_bwd(fn, dq_rot, dk_part, dv_part, cos, sin, pos_ids, h_q, h_kv, head_dim,
+                     scale_q, scale_v, True, mid=(bt_q, bt_v), parts=True)
 
 
 def qkv_rope_bwd(
@@ -1589,6 +1620,37 @@ def attn_varlen_bwd(dout: torch.Tensor, q: torch.Tensor, k: torch.Tensor, v: tor
             dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), ws.data_ptr(), cnt.data_ptr(),
             cnt.numel(), _stream(q))
     return dq, dk, dv
+
+
+def attn_varlen_bwd_parts(dout: torch.Tensor, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                          out: torch.Tensor, lse: torch.Tensor, cu_seqlens: torch.Tensor,
+                          max_blocks: int | None = None, scale: float | None = None, lens=None):
+    """``attn_varlen_bwd`` without the sum over each KV group's query heads: (dq, dk_part,
+    dv_part), the partials fp32 [h_q, N, 128] (dk_part scaled), for
+    ``qkv_rope_bwd_lora_mid_parts`` to sum."""
+    fn = "attn_varlen_bwd_parts"
+    _attn_operands(fn, q, k, v, cu_seqlens)
+    n, hq, d = q.shape
+    for name, t in (("dout", dout), ("out", out)):
+        if t.shape != q.shape or t.dtype != torch.float16 or not t.is_contiguous():
+            raise ValueError(f"{fn}: {name} must be contiguous fp16 like q")
+    if lse.shape != (hq, n) or lse.dtype != torch.float32 or not lse.is_contiguous():
+        raise ValueError(f"{fn}: lse must be contiguous fp32 [h_q, N]")
+    _require_device(fn, dout, out, lse)
+    n_rows = cu_seqlens.numel() - 1
+    mb = attn_max_blocks(n, n_rows) if max_blocks is None else int(max_blocks)
+    scale = 1.0 / math.sqrt(d) if scale is None else float(scale)
+    dq = torch.empty_like(q)
+    off = _round_up(hq * n, 64)
+    ws = torch.empty(off + 2 * hq * n * d, dtype=torch.float32, device=q.device)
+    nbytes = 2 * (4 * q.numel() + 2 * k.numel()) + 4 * 2 * hq * n * d + lse.numel() * 8
+    _launch("attn_bwd", nbytes, 2.5 * _attn_flops(lens, hq), "rus_attn_varlen_bwd_parts",
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), dout.data_ptr(),
+            lse.data_ptr(), cu_seqlens.data_ptr(), n_rows, n, mb, hq, k.shape[1], d, scale,
+            dq.data_ptr(), ws.data_ptr(), _stream(q))
+    dk_part = ws[off: off + hq * n * d].view(hq, n, d)
+    dv_part = ws[off + hq * n * d:].view(hq, n, d)
+    return dq, dk_part, dv_part
 
 
 def transpose_rows(rows: torch.Tensor, out: torch.Tensor) -> torch.Tensor:

@@ -111,6 +111,12 @@ def test_header_compiles_as_c():
                                   128, 8, 1.0, 1.0, 12, 2, 128, None, None), "rank"),
         ("rus_qkv_rope_bwd_mid", (16, 16, 16, 16, 16, 16, 16, 16, 16, 16, 16, 16, 16, 16, 4, 2304,
                                   128, 8, 1.0, 1.0, 12, 3, 128, None, None), "slots"),
+        # the partial-sum variants: a missing partial buffer, a missing workspace
+        ("rus_qkv_rope_bwd_mid_parts", (16, None, 16, 16, 16, 16, 16, 16, 16, 16, 16, 16, 16, 16,
+                                        4, 2304, 128, 8, 1.0, 1.0, 12, 2, 128, None, None),
+         "null pointer"),
+        ("rus_attn_varlen_bwd_parts", (16, 16, 16, 16, 16, 16, 16, 1, 32, 2, 12, 2, 128, 0.1, 16,
+                                       None, None), "null or misaligned"),
     ],
 )
 def test_invalid_arguments_are_rejected_on_the_host(name, args, msg):

@@ -180,3 +180,50 @@ def test_attention_matches_torch_flash_on_device():
                                                   True, False)[0]
     torch.cuda.synchronize()
     assert (out.float() - o_t.float()).abs().max().item() < 4e-3
+
+
+@pytest.mark.parametrize("lens,hq,hkv", [([33, 90, 1, 200], 12, 2), ([40, 7], 4, 4), ([70, 5], 8, 1)])
+def test_attention_partials_equal_group_sum(lens, hq, hkv):
+    # The partial-output backward: dq is the group-summing backward's bit for bit, and each KV
+    # head's per-query-head partials summed in head order and rounded once are its dk / dv.
+    q, k, v, dout, cu = _inputs(lens, hq, hkv, seed=sum(lens))
+    qd, kd, vd, dd = _dev(q, k, v, dout)
+    cud = torch.tensor(cu, dtype=torch.int32, device=DEV)
+    out, lse = K.attn_varlen_fwd(qd, kd, vd, cud)
+    dq, dk, dv = K.attn_varlen_bwd(dd, qd, kd, vd, out, lse, cud)
+    dq_p, dk_p, dv_p = K.attn_varlen_bwd_parts(dd, qd, kd, vd, out, lse, cud)
+    torch.cuda.synchronize()
+    assert torch.equal(dq_p, dq)
+    grp = hq // hkv
+    for part, full in ((dk_p, dk), (dv_p, dv)):
+        acc = part.view(hkv, grp, -1, 128)[:, 0].clone()
+        for j in range(1, grp):
+            acc += part.view(hkv, grp, -1, 128)[:, j]
+        assert torch.equal(acc.half().permute(1, 0, 2).contiguous(), full)
+
+
+def test_rope_mid_over_attention_partials_equals_group_sum_path():
+    # Attention partials -> RoPE backward that sums them equals attention group sum -> RoPE
+    # backward, for all five outputs, bit for bit (bench-shaped heads, rank 16).
+    lens = [100, 37, 250]
+    hq, hkv, hd, r = 12, 2, 128, 16
+    q, k, v, dout, cu = _inputs(lens, hq, hkv, seed=21)
+    qd, kd, vd, dd = _dev(q, k, v, dout)
+    cud = torch.tensor(cu, dtype=torch.int32, device=DEV)
+    n = sum(lens)
+    g = torch.Generator().manual_seed(5)
+    ang = torch.rand(600, hd, generator=g) * 6.3
+    cos, sin = ang.cos().half().to(DEV), ang.sin().half().to(DEV)
+    pos = torch.randint(0, 600, (n,), generator=g).to(DEV)
+    bqt = (torch.randn(r, hq * hd, generator=g) * 0.05).half().to(DEV)
+    bvt = (torch.randn(r, hkv * hd, generator=g) * 0.05).half().to(DEV)
+    out, lse = K.attn_varlen_fwd(qd, kd, vd, cud)
+    dq, dk, dv = K.attn_varlen_bwd(dd, qd, kd, vd, out, lse, cud)
+    want = K.qkv_rope_bwd_lora_mid(dq, dk, dv, cos, sin, pos, 2.0, 0.5, bqt, bvt,
+                                   h_q=hq, h_kv=hkv, head_dim=hd)
+    dq_p, dk_p, dv_p = K.attn_varlen_bwd_parts(dd, qd, kd, vd, out, lse, cud)
+    got = K.qkv_rope_bwd_lora_mid_parts(dq_p, dk_p, dv_p, cos, sin, pos, 2.0, 0.5, bqt, bvt,
+                                        h_q=hq, h_kv=hkv, head_dim=hd)
+    torch.cuda.synchronize()
+    for a, b in zip(got, want):
+        assert torch.equal(a, b)
