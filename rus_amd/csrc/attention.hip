@@ -5,24 +5,29 @@
 // heads; its backward is torch's. Layout here: q [N, h_q, 128], k / v [N, h_kv, 128] token-major
 // (the RoPE kernel's outputs), rows delimited by cu_seqlens [n_seq + 1] (int32, on the device).
 //
-// Design (CDNA4, v_mfma_f32_32x32x16_f16; operand / accumulator lane layouts as in lmhead.hip):
+// Design (CDNA4, v_mfma_f32_32x32x16_f16; operand / accumulator lane layouts as in mfma_gemm.h):
 //   * one block of 4 waves per (row, 32-token block, query head); the waves split the loop over
-//     the other operand's 32-token blocks (prefetching each next block into registers), stage
-//     their transposed tiles in LDS of their own, and merge their partials through LDS at the
-//     end in a fixed order (softmax partials rescaled by their running maxima);
+//     the other operand's 32-token blocks and merge their partials through LDS at the end in a
+//     fixed order (softmax partials rescaled by their running maxima);
+//   * every operand tile (32 tokens x 128 dims) is copied straight into LDS by
+//     global_load_lds_dwordx4 (whole 256-byte rows per 16 lanes; the block's own query tile
+//     once, the waves' key / value tiles per loop step) and read from there as 16-byte row
+//     fragments or, through ds_read_b64_tr_b16, as transposed fragments: no tile is held in
+//     registers in flight, no transposed copy is written, and blocks fit two per CU;
 //   * forward computes S^T = K Q^T, so a lane owns one query (column) and 16 of the block's 32
 //     keys: the running max / sum and the O rescale are per-lane scalars, and P^T feeds the
 //     O^T += V^T P^T product straight from the accumulator registers. An accumulator tile used
 //     as an MFMA operand carries its reduction index in the order
 //         k(h, i) = 16 s + 8 (i / 4) + 4 h + i % 4      (lane half h, slot i of step s),
-//     so the other operand is read in the same order from a transposed LDS copy (two 8-byte
-//     reads per fragment);
+//     which the transposed reads produce (two reads of 4 consecutive tokens per fragment);
 //   * P and dS are rounded to fp16 for their MFMAs, as flash attention does; O, LSE, dQ, dK, dV
 //     accumulate in fp32;
-//   * backward: kernel 1 per (row, query block, head) forms D = rowsum(dO o O) and dQ;
-//     kernel 2 per (row, key block, query head) forms that head's dK and dV contributions in fp32;
-//     the last of a KV group's h_q / h_kv heads to finish a key block sums the group's fp32
-//     partials in head order and rounds once (arrival counter; no atomics on data).
+//   * backward: a small kernel forms D = rowsum(dO o O); one launch then runs the dK / dV blocks
+//     (row, key block, query head; fp32 dK / dV partials per query head) and the dQ blocks
+//     (row, query block, head). The h_q / h_kv partials of a KV group are summed in head order
+//     and rounded once, either by the last of the group's blocks to finish a key block (arrival
+//     counter; no atomics on data) or, in the engine's path, by the RoPE backward that packs
+//     them (rus_qkv_rope_bwd_mid_parts).
 #include <math.h>
 
 #include "common.h"
@@ -36,7 +41,6 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kHD = 128;       // head_dim
 constexpr int kBlk = 32;       // tokens per block
-constexpr int kTS = kBlk + 4;  // transposed-tile row stride (halfs): 72 B, conflict-free reads
 constexpr int kW = 4;          // waves per block (one 32x32 head-dim tile each in the merges)
 constexpr int kMaxGroup = 8;   // query heads per KV head (GQA group) the backward supports
 constexpr float kLog2e = 1.4426950408889634f;
@@ -131,58 +135,6 @@ __device__ __forceinline__ bool find_block(const int32_t* cu, int n_seq, int n_t
   return false;
 }
 
-// 8 consecutive halfs of row `row`, column `col` (16-byte load).
-__device__ __forceinline__ f16x8 ld8(const f16* base, int64_t row, int64_t stride, int col) {
-  return *reinterpret_cast<const f16x8*>(base + row * stride + col);
-}
-
-// Rows r0 .. r0+31 (clamped to [lo, hi)) of a [*, stride] head slice, loaded for a transposed
-// LDS copy: lane (rq = lane % 8, cc = lane / 8 + 8 G) holds rows 4 rq .. 4 rq + 3, columns
-// 8 cc .. 8 cc + 7 in v[4 G + i].
-__device__ __forceinline__ void load_rows4(f16x8 (&v)[8], const f16* x, int64_t stride, int r0,
-                                           int lo, int hi) {
-  const int lane = threadIdx.x & 63, rq = lane & 7, cc = lane >> 3;
-#pragma unroll
-  for (int G = 0; G < 2; ++G)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      int r = r0 + 4 * rq + i;
-      r = r < hi ? r : hi - 1;
-      r = r < lo ? lo : r;
-      v[4 * G + i] = ld8(x, r, stride, (cc + 8 * G) * 8);
-    }
-}
-
-// t[d * kTS + j] = X[r0 + j][d] from load_rows4's registers: one 8-byte write per column and
-// row quad. Lanes 0..31 cover all 64 LDS banks (row stride 18 words, quads 2 words apart).
-__device__ __forceinline__ void write_t4(f16* t, const f16x8 (&v)[8]) {
-  const int lane = threadIdx.x & 63, rq = lane & 7, cc = lane >> 3;
-#pragma unroll
-  for (int G = 0; G < 2; ++G)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const f16x4 w{v[4 * G][e], v[4 * G + 1][e], v[4 * G + 2][e], v[4 * G + 3][e]};
-      *reinterpret_cast<f16x4*>(t + ((cc + 8 * G) * 8 + e) * kTS + 4 * rq) = w;
-    }
-}
-
-// MFMA operand fragments of row `row` (lane % 32) for the 8 k-steps over head_dim:
-// f[s] = x[row][16 s + 8 h .. +7].
-__device__ __forceinline__ void load_frags(f16x8 (&f)[8], const f16* x, int64_t row,
-                                           int64_t stride, int h) {
-#pragma unroll
-  for (int s = 0; s < 8; ++s) f[s] = ld8(x, row, stride, 16 * s + 8 * h);
-}
-
-// Operand fragment of k-step s (reduction index in the accumulator order k(h, i)) for row `row`
-// of a transposed LDS tile.
-__device__ __forceinline__ f16x8 frag_t(const f16* t, int row, int s, int h) {
-  const f16* p = t + row * kTS + 16 * s + 4 * h;
-  const f16x4 a = *reinterpret_cast<const f16x4*>(p);
-  const f16x4 b = *reinterpret_cast<const f16x4*>(p + 8);
-  return f16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
-}
-
 // fp16 operand of k-step s from accumulator registers 8s .. 8s+7.
 __device__ __forceinline__ f16x8 frag_acc(const f32x16& c, int s) {
   f16x8 r;
@@ -220,162 +172,19 @@ __device__ __forceinline__ void store_tile_row(f16* row, const float (&x)[16], i
   }
 }
 
-constexpr int kStageHalfs = kHD * kTS;                   // one transposed 32 x 128 tile
 constexpr int kParkBytes = kW * 64 * 64 * 4;             // 64 KiB
 constexpr int kMax(int x, int y) { return x > y ? x : y; }
 
 // ---------------------------------------------------------------------------------------------
-// Forward: O = softmax(Q K^T * scale, causal) V and LSE. Block = (row, query block, head); its
-// kW waves take key blocks w, w + kW, ... with their own running max / sum, merged at the end.
+// Operand tiles (32 tokens x 128 head dims of Q, dO, K or V) are copied straight from global
+// memory into LDS (global_load_lds_dwordx4: 4 rows x 256 contiguous bytes per wave instruction,
+// no registers in flight) and read from there both ways: 16-byte row fragments (ds_read_b128)
+// and transposed fragments (ds_read_b64_tr_b16), so each tile is loaded once per use.
 // ---------------------------------------------------------------------------------------------
-// At most 256 registers per lane (no spills): two blocks share a CU, so the grid of (query
-// block, head) blocks fits the chip in one round and one block's loads overlap another's MFMAs.
-__global__ __launch_bounds__(64 * kW) __attribute__((amdgpu_waves_per_eu(2, 2))) void
-attn_fwd_kernel(AttnArgs a) {
-  constexpr int kBytes = kMax(kW * kStageHalfs * 2, kParkBytes + kW * 64 * 4);
-  __shared__ __attribute__((aligned(16))) char smem[kBytes];
-  int start, end, q0;
-  if (!find_block<true>(a.cu, a.n_seq, static_cast<int>(a.n_tok), blockIdx.y, start, end, q0)) return;
-  const int head = blockIdx.x, g = head / (a.h_q / a.h_kv);
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, h = lane >> 5, col = lane & 31;
-  const int64_t sq = static_cast<int64_t>(a.h_q) * kHD, skv = static_cast<int64_t>(a.h_kv) * kHD;
-  const f16* qh = a.q + head * kHD;
-  const f16* kh = a.k + g * kHD;
-  const f16* vh = a.v + g * kHD;
-  f16* vt = reinterpret_cast<f16*>(smem) + wave * kStageHalfs;
-
-  const int qi = q0 + col;  // this lane's query
-  f16x8 qf[8];
-  load_frags(qf, qh, qi < end ? qi : end - 1, sq, h);
-  f32x16 o[4];
-#pragma unroll
-  for (int d = 0; d < 4; ++d) o[d] = f32x16{};
-  float m = -INFINITY, l = 0.0f;
-  const int nk = (q0 - start) / kBlk + 1;  // key blocks up to and including the diagonal
-  f16x8 kf[8], vv[8];
-  if (wave < nk) {
-    const int k0 = start + wave * kBlk;
-    load_frags(kf, kh, min(k0 + col, end - 1), skv, h);
-    load_rows4(vv, vh, skv, k0, start, end);
-  }
-  for (int kb = wave; kb < nk; kb += kW) {
-    const int k0 = start + kb * kBlk;
-    f32x16 st = f32x16{};  // S^T = K Q^T: rows keys, columns queries
-#pragma unroll
-    for (int s = 0; s < 8; ++s) st = mfma(kf[s], qf[s], st);
-    write_t4(vt, vv);
-    if (kb + kW < nk) {  // prefetch the wave's next key block
-      const int k1 = k0 + kW * kBlk;
-      load_frags(kf, kh, min(k1 + col, end - 1), skv, h);
-      load_rows4(vv, vh, skv, k1, start, end);
-    }
-    // Only the diagonal block holds keys past the query or past the row's end.
-    float mx = -INFINITY;
-    if (kb == nk - 1) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int key = k0 + acc_row(r, h);
-        st[r] = (key <= qi && key < end) ? st[r] * a.scale_log2 : -INFINITY;
-        mx = fmaxf(mx, st[r]);
-      }
-    } else {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        st[r] *= a.scale_log2;
-        mx = fmaxf(mx, st[r]);
-      }
-    }
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));  // finite: key k0 <= q0 <= qi is always allowed
-    // Lazy rescaling: the reference point m moves only when a block's maximum exceeds it by
-    // more than 8 (log2 units), so p = 2^(s - m) <= 256 (exact in range for fp16) and O and l
-    // share one reference, leaving O / l unchanged; the rescale of O is a wave-uniform branch
-    // that is rarely taken after the first block.
-    const bool bump = mx > m + kLazy;
-    if (__ballot(bump)) {
-      const float mn = bump ? mx : m;
-      const float alpha = exp2_raw(m - mn);  // 0 on the first block (m = -inf)
-      l *= alpha;
-      m = mn;
-#pragma unroll
-      for (int d = 0; d < 4; ++d)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) o[d][r] *= alpha;
-    }
-    float rs = 0.0f;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const float p = exp2_raw(st[r] - m);
-      st[r] = p;
-      rs += p;
-    }
-    rs += __shfl_xor(rs, 32, 64);
-    l += rs;
-    // The wave's own LDS writes above are visible to its reads below (LDS executes a wave's
-    // instructions in order); the next iteration's writes follow these reads likewise.
-    const f16x8 p0 = frag_acc(st, 0), p1 = frag_acc(st, 1);
-#pragma unroll
-    for (int d = 0; d < 4; ++d) {
-      o[d] = mfma(frag_t(vt, d * 32 + col, 0, h), p0, o[d]);
-      o[d] = mfma(frag_t(vt, d * 32 + col, 1, h), p1, o[d]);
-    }
-  }
-  __syncthreads();  // all waves are done with their V^T tiles; the space is reused below
-  float* buf = reinterpret_cast<float*>(smem);
-  float* ml = buf + kW * 64 * 64;  // per wave: m of columns 0..31, then l
-  park(buf, o, wave, lane);
-  if (h == 0) {
-    ml[wave * 64 + col] = m;
-    ml[wave * 64 + 32 + col] = l;
-  }
-  __syncthreads();
-  float M = -INFINITY;
-#pragma unroll
-  for (int w = 0; w < kW; ++w) M = fmaxf(M, ml[w * 64 + col]);
-  float f[kW], L = 0.0f;
-#pragma unroll
-  for (int w = 0; w < kW; ++w) {
-    const float mw = ml[w * 64 + col];
-    f[w] = exp2_raw(mw - M);  // 0 for a wave without key blocks (mw = -inf)
-    L += ml[w * 64 + 32 + col] * f[w];
-  }
-  if (qi < end) {
-    const float inv = 1.0f / L;
-    float x[16];
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      float acc = 0.0f;
-#pragma unroll
-      for (int w = 0; w < kW; ++w) acc += parked(buf, w, wave, r, lane) * f[w];
-      x[r] = acc * inv;
-    }
-    store_tile_row(a.out + qi * sq + head * kHD, x, wave, h);
-    if (wave == 0 && h == 0) a.lse[head * a.n_tok + qi] = (M + log2f(L)) * kLn2;
-  }
-}
-
-// ---------------------------------------------------------------------------------------------
-// Backward. Every operand tile (32 tokens x 128 head dims of Q, dO, K or V) is copied straight
-// from global memory into LDS (global_load_lds_dwordx4: 4 rows x 256 contiguous bytes per wave
-// instruction, no registers in flight) and read from there both ways: 16-byte row fragments
-// (ds_read_b128) for S = Q K^T and dP = dO V^T, and transposed fragments (ds_read_b64_tr_b16) for
-// dV += P^T dO, dK += dS^T Q and dQ^T += K^T dS^T, so each tile is loaded once per use.
-// D = rowsum(dO o O) is formed once per (head, query) by a small kernel before the main launch.
-// ---------------------------------------------------------------------------------------------
+constexpr int kTile = kBlk * kHD * 2;  // one 32 x 128 fp16 tile: 8 KiB
 typedef __attribute__((address_space(3))) void* lds_void_ptr;
 typedef short v4i16 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
-
-// Waves per backward block: 4 (80 KiB of LDS and at most 256 registers, so two blocks share a
-// CU and one block's waits overlap the other's work; 8 waves in one block per CU ran 13% slower).
-constexpr int kWB = 4;
-static_assert(kWB == 4 || kWB == 8, "4 or 8 waves per backward block");
-constexpr int kCopiesPerWave = 8 / kWB;  // a shared tile's 8 copies over the block's waves
-constexpr int kRegsPerWave = 64 / kWB;   // accumulator registers each wave sums in the merge
-constexpr int kTile = kBlk * kHD * 2;    // one 32 x 128 fp16 tile: 8 KiB
-// LDS of a backward block: 2 shared tiles + 2 per wave; the merge reuses it as a buffer of every
-// wave's four 32x32 fp32 accumulator tiles.
-constexpr int kBwdBytes = (2 + 2 * kWB) * kTile;
-static_assert(kWB * 64 * 64 * 4 <= kBwdBytes, "the merge buffer fits the tiles' LDS");
 
 // Tiles are row-major, 256 bytes per token row, with the 16-byte chunk c of row r stored at chunk
 // c ^ swz(r): a quarter wave's 16-byte fragment reads (16 consecutive rows, one chunk) and a
@@ -433,6 +242,156 @@ __device__ __forceinline__ f16x8 tile_frag_t(const char* tile, int s, int d) {
   const f16x4 a = __builtin_bit_cast(f16x4, x0), b = __builtin_bit_cast(f16x4, x1);
   return f16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
 }
+
+
+// ---------------------------------------------------------------------------------------------
+// Forward: O = softmax(Q K^T * scale, causal) V and LSE. Block = (row, query block, head); its
+// kW waves take key blocks w, w + kW, ... with their own running max / sum, merged at the end.
+// ---------------------------------------------------------------------------------------------
+// At most 256 registers per lane (no spills) and 72 KiB of LDS (the block's Q tile, each wave's
+// K and V tiles): two blocks share a CU, so the grid of (query block, head) blocks fits the chip
+// in one round and one block's loads overlap another's MFMAs.
+__global__ __launch_bounds__(64 * kW) __attribute__((amdgpu_waves_per_eu(2, 2))) void
+attn_fwd_kernel(AttnArgs a) {
+  constexpr int kBytes = kMax((1 + 2 * kW) * kTile, kParkBytes + kW * 64 * 4);
+  __shared__ __attribute__((aligned(16))) char smem[kBytes];
+  int start, end, q0;
+  if (!find_block<true>(a.cu, a.n_seq, static_cast<int>(a.n_tok), blockIdx.y, start, end, q0)) return;
+  const int head = blockIdx.x, g = head / (a.h_q / a.h_kv);
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, h = lane >> 5, col = lane & 31;
+  const int64_t sq = static_cast<int64_t>(a.h_q) * kHD, skv = static_cast<int64_t>(a.h_kv) * kHD;
+  const f16* kh = a.k + g * kHD;
+  const f16* vh = a.v + g * kHD;
+  char* qt = smem;
+  char* kt = smem + (1 + 2 * wave) * kTile;
+  char* vt = kt + kTile;
+
+  const int qi = q0 + col;  // this lane's query
+  const int nk = (q0 - start) / kBlk + 1;  // key blocks up to and including the diagonal
+  tile_copy(qt, a.q + head * kHD, sq, q0, start, end, 2 * wave, 2);  // the 8 copies, 2 per wave
+  if (wave < nk) {
+    const int k0 = start + wave * kBlk;
+    tile_copy(kt, kh, skv, k0, start, end, 0, 8);
+    tile_copy(vt, vh, skv, k0, start, end, 0, 8);
+  }
+  wait_copies();
+  __syncthreads();  // every wave's share of the Q tile has landed
+  f16x8 qf[8];
+#pragma unroll
+  for (int s = 0; s < 8; ++s) qf[s] = tile_frag(qt, col, 2 * s + h);
+  f32x16 o[4];
+#pragma unroll
+  for (int d = 0; d < 4; ++d) o[d] = f32x16{};
+  float m = -INFINITY, l = 0.0f;
+  for (int kb = wave; kb < nk; kb += kW) {
+    const int k0 = start + kb * kBlk;
+    f32x16 st = f32x16{};  // S^T = K Q^T: rows keys, columns queries
+#pragma unroll
+    for (int s = 0; s < 8; ++s) st = mfma(tile_frag(kt, col, 2 * s + h), qf[s], st);
+    // Only the diagonal block holds keys past the query or past the row's end.
+    float mx = -INFINITY;
+    if (kb == nk - 1) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int key = k0 + acc_row(r, h);
+        st[r] = (key <= qi && key < end) ? st[r] * a.scale_log2 : -INFINITY;
+        mx = fmaxf(mx, st[r]);
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        st[r] *= a.scale_log2;
+        mx = fmaxf(mx, st[r]);
+      }
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));  // finite: key k0 <= q0 <= qi is always allowed
+    // Lazy rescaling: the reference point m moves only when a block's maximum exceeds it by
+    // more than 8 (log2 units), so p = 2^(s - m) <= 256 (exact in range for fp16) and O and l
+    // share one reference, leaving O / l unchanged; the rescale of O is a wave-uniform branch
+    // that is rarely taken after the first block.
+    const bool bump = mx > m + kLazy;
+    if (__ballot(bump)) {
+      const float mn = bump ? mx : m;
+      const float alpha = exp2_raw(m - mn);  // 0 on the first block (m = -inf)
+      l *= alpha;
+      m = mn;
+#pragma unroll
+      for (int d = 0; d < 4; ++d)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[d][r] *= alpha;
+    }
+    float rs = 0.0f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const float p = exp2_raw(st[r] - m);
+      st[r] = p;
+      rs += p;
+    }
+    rs += __shfl_xor(rs, 32, 64);
+    l += rs;
+    const f16x8 p0 = frag_acc(st, 0), p1 = frag_acc(st, 1);
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      o[d] = mfma(tile_frag_t(vt, 0, d), p0, o[d]);  // O^T += V^T P^T
+      o[d] = mfma(tile_frag_t(vt, 1, d), p1, o[d]);
+    }
+    if (kb + kW < nk) {  // the wave's next key block into its tiles
+      wait_tile_reads();
+      const int k1 = k0 + kW * kBlk;
+      tile_copy(kt, kh, skv, k1, start, end, 0, 8);
+      tile_copy(vt, vh, skv, k1, start, end, 0, 8);
+      wait_copies();
+    }
+  }
+  __syncthreads();  // all waves are done with their V^T tiles; the space is reused below
+  float* buf = reinterpret_cast<float*>(smem);
+  float* ml = buf + kW * 64 * 64;  // per wave: m of columns 0..31, then l
+  park(buf, o, wave, lane);
+  if (h == 0) {
+    ml[wave * 64 + col] = m;
+    ml[wave * 64 + 32 + col] = l;
+  }
+  __syncthreads();
+  float M = -INFINITY;
+#pragma unroll
+  for (int w = 0; w < kW; ++w) M = fmaxf(M, ml[w * 64 + col]);
+  float f[kW], L = 0.0f;
+#pragma unroll
+  for (int w = 0; w < kW; ++w) {
+    const float mw = ml[w * 64 + col];
+    f[w] = exp2_raw(mw - M);  // 0 for a wave without key blocks (mw = -inf)
+    L += ml[w * 64 + 32 + col] * f[w];
+  }
+  if (qi < end) {
+    const float inv = 1.0f / L;
+    float x[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      float acc = 0.0f;
+#pragma unroll
+      for (int w = 0; w < kW; ++w) acc += parked(buf, w, wave, r, lane) * f[w];
+      x[r] = acc * inv;
+    }
+    store_tile_row(a.out + qi * sq + head * kHD, x, wave, h);
+    if (wave == 0 && h == 0) a.lse[head * a.n_tok + qi] = (M + log2f(L)) * kLn2;
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// Backward, on the LDS tiles: row fragments for S = Q K^T and dP = dO V^T, transposed fragments
+// for dV += P^T dO, dK += dS^T Q and dQ^T += K^T dS^T. D = rowsum(dO o O) is formed once per
+// (head, query) by a small kernel before the main launch.
+// ---------------------------------------------------------------------------------------------
+// Waves per backward block: 4 (80 KiB of LDS and at most 256 registers, so two blocks share a
+// CU and one block's waits overlap the other's work; 8 waves in one block per CU ran 13% slower).
+constexpr int kWB = 4;
+static_assert(kWB == 4 || kWB == 8, "4 or 8 waves per backward block");
+constexpr int kCopiesPerWave = 8 / kWB;  // a shared tile's 8 copies over the block's waves
+constexpr int kRegsPerWave = 64 / kWB;   // accumulator registers each wave sums in the merge
+// LDS of a backward block: 2 shared tiles + 2 per wave; the merge reuses it as a buffer of every
+// wave's four 32x32 fp32 accumulator tiles.
+constexpr int kBwdBytes = (2 + 2 * kWB) * kTile;
+static_assert(kWB * 64 * 64 * 4 <= kBwdBytes, "the merge buffer fits the tiles' LDS");
 
 // Every wave's four 32x32 fp32 tiles into the merge buffer (the accumulator layout,
 // lane-contiguous); thread (wave w, lane) then sums tile w % 4, registers kRegsPerWave (w / 4)
