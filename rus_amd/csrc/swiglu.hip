@@ -11,6 +11,7 @@
 //   * rows whose width is not a multiple of the pack (e.g. 1001) use the same kernel with
 //     single-element packs.
 #include "common.h"
+#include "swiglu_math.h"
 
 namespace rus {
 namespace {
@@ -18,9 +19,6 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kUnroll = 2;
 
-__device__ __forceinline__ float sigmoid(float g) {
-  return __builtin_amdgcn_rcpf(1.0f + __expf(-g));
-}
 
 struct GluShape {
   uint32_t n_vec;    // total packs = n_rows * vec_per_row
@@ -58,7 +56,7 @@ __global__ __launch_bounds__(kThreads) void swiglu_fwd_kernel(const T* __restric
     if (idx < s.n_vec) {
       float o[V];
 #pragma unroll
-      for (int i = 0; i < V; ++i) o[i] = (gv[k][i] * sigmoid(gv[k][i])) * uv[k][i];
+      for (int i = 0; i < V; ++i) o[i] = (gv[k][i] * glu_sigmoid(gv[k][i])) * uv[k][i];
       store_from_f32<T, V>(out + oo[k], o);
     }
   }
@@ -89,13 +87,7 @@ __global__ __launch_bounds__(kThreads) void swiglu_bwd_kernel(const T* __restric
     if (idx < s.n_vec) {
       float og[V], ou[V];
 #pragma unroll
-      for (int i = 0; i < V; ++i) {
-        const float sg = sigmoid(gv[k][i]);
-        const float silu = gv[k][i] * sg;
-        ou[i] = dv[k][i] * silu;
-        const float dsilu = sg + silu * (1.0f - sg);
-        og[i] = (dv[k][i] * uv[k][i]) * dsilu;
-      }
+      for (int i = 0; i < V; ++i) glu_bwd(dv[k][i], gv[k][i], uv[k][i], og[i], ou[i]);
       store_from_f32<T, V>(dg + rows[k] * s.stride_d + cols[k], og);
       store_from_f32<T, V>(du + rows[k] * s.stride_e + cols[k], ou);
     }
