@@ -33,8 +33,10 @@ if REPO not in sys.path:
 METRIC = "train tokens/s (packed 1.5B NF4 QLoRA); lm_head-CE & NF4-dequant HBM GB/s"
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E
 FP16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA
-MFMA_KERNELS = ("lmhead_ce_fwd", "lmhead_ce_fwd_keep", "lmhead_ce_logits", "lmhead_ce_grad_logits",
-                "lmhead_ce_grad_hidden")
+LMHEAD_KERNELS = ("lmhead_ce_fwd", "lmhead_ce_fwd_keep", "lmhead_ce_logits",
+                  "lmhead_ce_grad_logits", "lmhead_ce_grad_hidden")
+# kernels whose roofline is the fp16 MFMA peak (the rest are bound by HBM bandwidth)
+MFMA_KERNELS = LMHEAD_KERNELS + ("gemm_parts", "nf4_gemm", "attn_fwd", "attn_bwd")
 
 
 def make_batches(cfg, n_batches, rows, max_len, seed, device):
@@ -562,6 +564,38 @@ def kernel_probe(reps: int = 5) -> None:
     print(f"probe: {reps} four-segment dequants of layer 0 with a riding norm backward", flush=True)
 
 
+def gemm_parts_probe(reps: int = 5, n_tok: int = 707) -> None:
+    """Fixed launches for hardware-counter runs: the plain 128 MiB device copy (the counters'
+    calibration), then the step's split-K MLP input gradient at the bench's mean batch,
+    d_gu [707, 17920] x W_gu [17920, 1536] into fp32 partials with the engine's split count,
+    each launch reading one of 4 weight sets (cold, as in the step)."""
+    import torch
+
+    from rus_amd import ops as O
+
+    dev = torch.device("cuda:0")
+    src = torch.empty(64 << 20, dtype=torch.float16, device=dev).normal_()
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(f"probe: {reps} copies of {src.numel() * 2} bytes", flush=True)
+    del src, dst
+    g = torch.Generator(device=dev).manual_seed(0)
+    ws = [(torch.randn(17920, 1536, device=dev, generator=g) * 0.02).half() for _ in range(4)]
+    x = torch.randn(n_tok, 17920, device=dev, generator=g).half()
+    parts = None
+    for i in range(reps):
+        parts = O._input_grad_parts(x, ws[i % 4])
+    torch.cuda.synchronize()
+    sp = parts.shape[0]
+    nbytes = (n_tok * 17920 + 17920 * 1536) * 2 + 4 * sp * n_tok * 1536
+    print(f"probe: {reps} split-K products [{n_tok}, 17920] x [17920, 1536], {sp} partials, "
+          f"{nbytes} algorithmic bytes per launch", flush=True)
+    del ws, x, parts
+
+
 def _print_record(rec: dict) -> None:
     print(json.dumps({k: (round(v, 3) if isinstance(v, float) else v) for k, v in rec.items()}),
           flush=True)
@@ -800,17 +834,24 @@ def main() -> int:
     ap.add_argument("--gemm", choices=("dequant", "fused"), default="dequant",
                     help="dequant: NF4 -> fp16 workspace, then the library GEMM; fused: the "
                          "products decode NF4 inside their MFMA loop (rus_nf4_gemm)")
+    ap.add_argument("--dequant-once", choices=("on", "off"), default="on",
+                    help="on: each layer is dequantised once per step, into fp16 weights of its "
+                         "own that the backward reads (2.6 GB); off: again in the backward, as "
+                         "the reference does; the other setting is timed as an ablation")
     ap.add_argument("--no-ablation", action="store_true",
-                    help="skip the timing of the other --recompute and --stream-unit settings")
+                    help="skip the timing of the other --recompute, --dequant-once and "
+                         "--stream-unit settings")
     ap.add_argument("--trace-summary", metavar="KERNEL_TRACE_CSV",
                     help="print the per-step kernel time of the last --steps replays in a "
                          "rocprofv3 --kernel-trace CSV of a bench run, and exit")
     ap.add_argument("--probe", nargs="?", const="dequant",
-                    choices=("dequant", "lmhead", "elementwise", "ceilings", "gemm"),
+                    choices=("dequant", "lmhead", "elementwise", "ceilings", "gemm",
+                             "gemm_parts"),
                     help="only fixed launches for counter runs: copy + dequant (default), the "
-                         "lm_head CE kernels at config 2, or the elementwise kernels on cold "
-                         "inputs; or printed timings: streaming ceilings at the dequant's "
-                         "traffic (ceilings), per-product GEMM times (gemm)")
+                         "lm_head CE kernels at config 2, the elementwise kernels on cold "
+                         "inputs, or the split-K MLP input gradient (gemm_parts); or printed "
+                         "timings: streaming ceilings at the dequant's traffic (ceilings), "
+                         "per-product GEMM times (gemm)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs and measures one GPU only (asked for --gpus "
@@ -830,6 +871,9 @@ def main() -> int:
         return 0
     if args.probe == "gemm":
         gemm_probe()
+        return 0
+    if args.probe == "gemm_parts":
+        gemm_parts_probe()
         return 0
     if args.probe:
         kernel_probe()
@@ -854,8 +898,11 @@ def main() -> int:
     # Configured engine: NF4 layers streamed per step from pinned host memory.
     recompute = args.recompute == "on"
     overlap = args.overlap == "on" and args.stream_unit == "model" and args.gemm == "dequant"
+    once = (args.dequant_once == "on" and args.stream_unit == "model" and args.gemm == "dequant"
+            and not overlap)
     engine = Qwen2FusedEngine(model, dev, resident_weights=False, stream_unit=args.stream_unit,
-                              recompute=recompute, overlap=overlap, gemm=args.gemm)
+                              recompute=recompute, overlap=overlap, gemm=args.gemm,
+                              dequant_once=once)
     # Calibration pass (eager): every kernel timed, to name the dominant one.
     _, _, _, calib = timed_run(engine, opt, batches, 2, args.warmup, kernel_filter=None)
     dominant = max(calib, key=lambda k: calib[k]["ms"])
@@ -886,26 +933,37 @@ def main() -> int:
                    "max_reserved_mib": torch.cuda.max_memory_reserved(dev) / 2**20,
                    "model_tensors_mib": model_mib,
                    "note": "whole process during the timed replays: the random model's device "
-                           "tensors, the engine's two whole-model NF4 buffers, workspaces, "
-                           "the embedding / lm_head and its transpose, graph pools"}
+                           "tensors, the engine's two whole-model NF4 buffers, workspaces "
+                           "(with dequant-once: every layer's fp16 weights), the embedding / "
+                           "lm_head and its transpose, graph pools"}
     value = tokens / secs
     d = summary[dominant]
     avg_ms = d["ms"] / d["launches"]
-    if dominant in MFMA_KERNELS:
+    # The roofline that bounds the kernel: MFMA kernels whose algorithmic bytes take longer at
+    # 8 TB/s than their flops at the fp16 peak (a split-K product's fp32 partials) are HBM-bound.
+    mfma_frac = d["flops"] / (d["ms"] / 1e3) / 1e12 / FP16_PEAK_TFLOPS
+    hbm_frac = d["bytes"] / (d["ms"] / 1e3) / 1e9 / HBM_PEAK_GBS
+    mfma_bound = dominant in MFMA_KERNELS and mfma_frac >= hbm_frac
+    if mfma_bound:
         achieved = d["flops"] / (d["ms"] / 1e3) / 1e12
         roof = {"bound": "mfma", "achieved": achieved, "peak": FP16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                "frac": achieved / FP16_PEAK_TFLOPS, "traffic": None}
+                "frac": mfma_frac, "traffic": measured_traffic(dominant)}
     else:
         achieved = d["bytes"] / (d["ms"] / 1e3) / 1e9
         roof = {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": achieved / HBM_PEAK_GBS, "traffic": measured_traffic(dominant),
-                "traffic_source": f"profiles/{dominant}_traffic_config5.txt (FETCH_SIZE / "
-                                  "WRITE_SIZE counter runs of bench.py --probe, both launch "
-                                  "variants, scaled by a plain copy's counters)"}
+                "frac": hbm_frac, "traffic": measured_traffic(dominant)}
+    if dominant in MFMA_KERNELS:
+        roof["mfma_frac"] = mfma_frac
+        roof["tflops"] = mfma_frac * FP16_PEAK_TFLOPS
+    roof["traffic_source"] = (f"profiles/{dominant}_traffic_config5.txt (FETCH_SIZE / WRITE_SIZE "
+                              "counter runs of bench.py --probe, scaled by a plain copy's "
+                              "counters)")
     roof.update({"kernel": dominant, "avg_launch_ms": avg_ms, "launches": d["launches"],
                  "event_pair_overhead_ms": KernelTimer.pair_overhead_ms(),
-                 "per_launch": d["flops"] / d["launches"] if dominant in MFMA_KERNELS
+                 "per_launch": d["flops"] / d["launches"] if mfma_bound
                  else d["bytes"] / d["launches"],
+                 "per_launch_bytes": d["bytes"] / d["launches"],
+                 "per_launch_flops": d["flops"] / d["launches"],
                  "timed_in": f"eager pass of {args.roofline_steps} steps of the same workload"})
 
     out = {
@@ -919,6 +977,7 @@ def main() -> int:
                    "tokens_per_step": tokens / args.steps, "lora": "r16 alpha32 dropout0.05 q,v",
                    "stream_unit": args.stream_unit, "recompute": args.recompute,
                    "overlap": "on" if overlap else "off", "gemm": args.gemm,
+                   "dequant_once": "on" if once else "off",
                    "lm_head": "token blocks of <= 256, [block, V] logits buffer, no [N, V]",
                    "optimizer": f"AdamW lr 2e-4 ({opt_kind}"
                                 + (", one flat LoRA buffer)" if graph is not None else ")")},
@@ -933,7 +992,7 @@ def main() -> int:
         "graph_pool_reserved_mib": graph_pool_mib,
         "graph_buckets": len(graph.graphs) if graph is not None else 0,
     }
-    lm = [calib[k] for k in MFMA_KERNELS if k in calib]
+    lm = [calib[k] for k in LMHEAD_KERNELS if k in calib]
     if lm:
         out["lm_head_ce_tflops"] = sum(r["flops"] for r in lm) / (sum(r["ms"] for r in lm) / 1e3) / 1e12
     if "nf4_dequant" in calib:
@@ -946,7 +1005,8 @@ def main() -> int:
         # The other activation policy and the other streaming unit: same batches, graphs.
         other = "on" if not recompute else "off"
         eng_a = Qwen2FusedEngine(model, dev, resident_weights=False, stream_unit=args.stream_unit,
-                                 recompute=not recompute, overlap=overlap, gemm=args.gemm)
+                                 recompute=not recompute, overlap=overlap, gemm=args.gemm,
+                                 dequant_once=once)
         torch.cuda.synchronize()
         torch.cuda.reset_peak_memory_stats(dev)
         base_a = torch.cuda.memory_allocated(dev)
@@ -955,6 +1015,13 @@ def main() -> int:
         out[f"recompute_{other}_tokens_per_s"], g_a = _graph_run(eng_a, None, batches,
                                                                  min(args.steps, 16), 1)
         del eng_a, g_a
+        if args.stream_unit == "model" and args.gemm == "dequant" and not overlap:
+            eng_d = Qwen2FusedEngine(model, dev, resident_weights=False, stream_unit="model",
+                                     recompute=recompute, gemm=args.gemm, dequant_once=not once)
+            out[f"dequant_once_{'off' if once else 'on'}_tokens_per_s"], g_d = _graph_run(
+                eng_d, None, batches, min(args.steps, 16), 1)
+            del eng_d, g_d
+            torch.cuda.empty_cache()
         unit = "layer" if args.stream_unit == "model" else "model"
         eng_u = Qwen2FusedEngine(model, dev, resident_weights=False, stream_unit=unit,
                                  recompute=recompute, overlap=False, gemm=args.gemm)
@@ -965,7 +1032,7 @@ def main() -> int:
 
     if not args.no_resident and not args.no_graph:
         eng_r = Qwen2FusedEngine(model, dev, resident_weights=True, recompute=recompute,
-                                 overlap=overlap, gemm=args.gemm)
+                                 overlap=overlap, gemm=args.gemm, dequant_once=once)
         out["resident_weights_tokens_per_s"], g_r = _graph_run(eng_r, None, batches,
                                                                 min(args.steps, 16), 1)
         del eng_r, g_r

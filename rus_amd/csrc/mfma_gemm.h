@@ -55,10 +55,10 @@ __device__ __forceinline__ bool tile_of(const GemmArgs& g, Tile& t) {
 // split's K range. Accumulator layout (v_mfma_f32_32x32x16_f16): register r of lane l holds
 // row 8*(r/4) + 4*(l/32) + r%4, column l%32 of the 32x32 tile.
 //
-// Pipeline: K is staged 32 at a time through four LDS buffers of 32 KiB (A then B, 256 rows x
-// 64 bytes each). Global memory is copied straight into LDS (global_load_lds_dwordx4: each lane's
-// 16 bytes land at buffer + lane * 16), three stages ahead of the MFMAs, so no register holds a
-// tile in flight and the 256 accumulators stay in AGPRs. The 16-byte chunk c of row r is stored
+// Pipeline: K is staged 32 at a time through NS LDS buffers of 32 KiB (A then B, 256 rows x
+// 64 bytes each; NS = 4, or 5 for the N-contiguous B). Global memory is copied straight into LDS
+// (global_load_lds_dwordx4: each lane's 16 bytes land at buffer + lane * 16), NS - 1 stages ahead
+// of the MFMAs, so no register holds a tile in flight and the 256 accumulators stay in AGPRs. The 16-byte chunk c of row r is stored
 // at chunk c ^ ((r >> 2) & 3) of its 64-byte row, which a lane realises by loading the chunk
 // that belongs at its position; the MFMAs' 16-byte fragment reads (16 consecutive rows per quarter
 // wave, one chunk) then hit all 64 banks once. The fragment reads are explicit ds_read_b128 with
@@ -72,6 +72,11 @@ constexpr int kDK = 32;                  // K per LDS stage
 constexpr int kStageBytes = 2 * kBM * kDK * 2;  // A + B: 32 KiB
 constexpr int kNStages = 4;
 static_assert(kNStages * kStageBytes == kSmemBytes, "stages fill the kernel's LDS");
+// The N-contiguous mainloop keeps five stages (all 160 KiB of the CU's LDS): four stages in
+// flight instead of three took the split-K product at 707 tokens from 65 to 57 us (isolated); the
+// K-contiguous kernels gained nothing from it.
+constexpr int kNStagesKN = 5;
+constexpr int kSmemBytesKN = kNStagesKN * kStageBytes;
 
 template <int OFF>
 __device__ __forceinline__ u32x4v lds_read16(uint32_t addr) {
@@ -190,10 +195,12 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-// Waits until at most `stages` (0..3) stages of PER copies each are still in flight.
+// Waits until at most `stages` (0..4) stages of PER copies each are still in flight.
 template <int PER>
 __device__ __forceinline__ void wait_stages(int stages) {
-  if (stages >= 3)
+  if (stages >= 4)
+    wait_vmcnt<4 * PER>();
+  else if (stages == 3)
     wait_vmcnt<3 * PER>();
   else if (stages == 2)
     wait_vmcnt<2 * PER>();
@@ -207,7 +214,7 @@ __device__ __forceinline__ void wait_stages(int stages) {
 // NW = 8: 2 x 4 waves of 128 x 64 (acc[4][2], two waves per SIMD, so one wave's fragment reads
 // and copy waits overlap the other's MFMAs). Same LDS stages and A swizzle either way. KN: B is
 // [K, ldb] N-contiguous (NW = 8 only), staged as 32 K rows of 512 bytes per stage.
-template <int NW, bool KN = false>
+template <int NW, bool KN = false, int NS = kNStages>
 __device__ __forceinline__ void mainloop_t(const GemmArgs& g, const Tile& tl, char* smem,
                                            f32x16 (&acc)[kMT][16 / NW]) {
   static_assert(!KN || NW == 8, "the N-contiguous B layout runs on eight waves");
@@ -254,8 +261,8 @@ __device__ __forceinline__ void mainloop_t(const GemmArgs& g, const Tile& tl, ch
     }
   }
   const uint32_t bstep = KN ? static_cast<uint32_t>(kDK * g.ldb * 2) : kDK * 2;
-  auto issue = [&](int k) {  // stage k's copies into buffer k % 4
-    char* st = smem + (k & (kNStages - 1)) * kStageBytes;
+  auto issue = [&](int k) {  // stage k's copies into buffer k % NS
+    char* st = smem + (k % NS) * kStageBytes;
     const uint32_t abytes = k * (kDK * 2), bbytes = k * bstep;
 #pragma unroll
     for (int i = 0; i < CP; ++i) {
@@ -266,7 +273,7 @@ __device__ __forceinline__ void mainloop_t(const GemmArgs& g, const Tile& tl, ch
                                        0, 0);
     }
   };
-  const int pre = min(kNStages, KT);
+  const int pre = min(NS, KT);
   for (int k = 0; k < pre; ++k) issue(k);
   wait_stages<PER>(pre - 1);  // stage 0 landed (this wave's copies)
   __builtin_amdgcn_s_barrier();  // ... and every wave's
@@ -293,17 +300,17 @@ __device__ __forceinline__ void mainloop_t(const GemmArgs& g, const Tile& tl, ch
     read_frags_kn<NT, 0>(a0, bk, 0, fa0, lo0, hi0);
     wait_frags_kn<NT>(fa0, lo0, hi0);
     for (int k = 0; k < KT; ++k) {
-      const uint32_t sb = (k & (kNStages - 1)) * kStageBytes;
+      const uint32_t sb = (k % NS) * kStageBytes;
       read_frags_kn<NT, 1>(a1 + sb, bk, sb, fa1, lo1, hi1);  // step 1 of stage k
       __builtin_amdgcn_sched_barrier(0);
       mma16_kn<NT>(fa0, lo0, hi0, acc);  // step 0 of stage k
       __builtin_amdgcn_sched_barrier(0);
       wait_frags_kn<NT>(fa1, lo1, hi1);
       if (k + 1 < KT) {
-        wait_stages<PER>(min(2, KT - 2 - k));
+        wait_stages<PER>(min(NS - 2, KT - 2 - k));
         __builtin_amdgcn_s_barrier();
-        if (k + kNStages < KT) issue(k + kNStages);
-        const uint32_t nb = ((k + 1) & (kNStages - 1)) * kStageBytes;
+        if (k + NS < KT) issue(k + NS);
+        const uint32_t nb = ((k + 1) % NS) * kStageBytes;
         read_frags_kn<NT, 0>(a0 + nb, bk, nb, fa0, lo0, hi0);  // step 0 of stage k + 1
       }
       __builtin_amdgcn_sched_barrier(0);
@@ -318,7 +325,7 @@ __device__ __forceinline__ void mainloop_t(const GemmArgs& g, const Tile& tl, ch
     read_frags<NT>(a0, b0, fa0, fb0);
     wait_frags<NT>(fa0, fb0);
     for (int k = 0; k < KT; ++k) {
-      const uint32_t sb = (k & (kNStages - 1)) * kStageBytes;
+      const uint32_t sb = (k % NS) * kStageBytes;
       read_frags<NT>(a1 + sb, b1 + sb, fa1, fb1);  // step 1 of stage k
       __builtin_amdgcn_sched_barrier(0);
       mma16<NT>(fa0, fb0, acc);  // step 0 of stage k
@@ -327,10 +334,10 @@ __device__ __forceinline__ void mainloop_t(const GemmArgs& g, const Tile& tl, ch
       if (k + 1 < KT) {
         // Stage k + 1 has landed for every wave, and every wave has read stage k: its buffer
         // takes stage k + 4.
-        wait_stages<PER>(min(2, KT - 2 - k));
+        wait_stages<PER>(min(NS - 2, KT - 2 - k));
         __builtin_amdgcn_s_barrier();
-        if (k + kNStages < KT) issue(k + kNStages);
-        const uint32_t nb = ((k + 1) & (kNStages - 1)) * kStageBytes;
+        if (k + NS < KT) issue(k + NS);
+        const uint32_t nb = ((k + 1) % NS) * kStageBytes;
         read_frags<NT>(a0 + nb, b0 + nb, fa0, fb0);  // step 0 of stage k + 1
       }
       __builtin_amdgcn_sched_barrier(0);
@@ -352,10 +359,10 @@ __device__ __forceinline__ void mainloop(const GemmArgs& g, const Tile& tl, char
   mainloop_t<8>(g, tl, smem, acc);
 }
 
-// The eight-wave mainloop with B stored [K, ldb] N-contiguous.
+// The eight-wave mainloop with B stored [K, ldb] N-contiguous; smem holds kSmemBytesKN.
 __device__ __forceinline__ void mainloop_kn(const GemmArgs& g, const Tile& tl, char* smem,
                                             f32x16 (&acc)[kMT][2]) {
-  mainloop_t<8, true>(g, tl, smem, acc);
+  mainloop_t<8, true, kNStagesKN>(g, tl, smem, acc);
 }
 
 // Eight waves (two per SIMD): the accumulators of a 128 x 64 wave tile leave room for a second

@@ -412,6 +412,47 @@ class WeightStream:
             cache[key] = got
         return got
 
+    # -- one dequant per layer and step: the backward reads the forward's fp16 weights ------------
+    @property
+    def dequant_once(self) -> bool:
+        return getattr(self, "_once", False)
+
+    def enable_dequant_once(self) -> None:
+        """Gives every layer fp16 weights of its own (one device allocation holding all layers'
+        segments, 2 x the model's weight count in bytes: 2.6 GB for Qwen2.5-1.5B). The forward
+        dequantises each layer into its own set and the backward reads that set instead of
+        dequantising again. The base weights are frozen, so the set holds the values a second
+        dequant of the same packed bytes would write. Whole-model and resident units only."""
+        if self.unit == "layer":
+            raise ValueError("dequant-once needs stream_unit='model' or resident weights")
+        if self.dequant_once:
+            return
+        sizes = [{n: sg.out_features * sg.in_features for n, sg in segs.items()}
+                 for segs in self.layer_segments]
+        store = torch.empty(sum(sum(s.values()) for s in sizes), dtype=torch.float16,
+                            device=self.device)
+        sets, off = [], 0
+        for s in sizes:
+            d = {}
+            for name in SEGMENTS:
+                d[name] = store[off: off + s[name]]
+                off += s[name]
+            sets.append(d)
+        self.layer_store, self.layer_sets = store, sets
+        self._once = True
+
+    def forward_weights(self, layer_idx: int, norm=None) -> dict[str, torch.Tensor]:
+        """The forward's dequant of ``layer_idx`` (with ``norm`` riding in its launch), into the
+        layer's own set when dequant-once is on."""
+        sets = self.layer_sets[layer_idx] if self.dequant_once else None
+        return self.dequant_layer(layer_idx, workspaces=sets, norm=norm)
+
+    def stored_weights(self, layer_idx: int) -> dict[str, torch.Tensor]:
+        """The fp16 weights the forward left in ``layer_idx``'s set (dequant-once)."""
+        segs = self.layer_segments[layer_idx]
+        return {n: self.layer_sets[layer_idx][n].view(sg.out_features, sg.in_features)
+                for n, sg in segs.items()}
+
     # -- dequantisation one layer ahead on a second stream ---------------------------------------
     @property
     def dequant_ahead(self) -> bool:

@@ -8,7 +8,8 @@
   loss within 2e-3 relative, every LoRA gradient within 1e-2 relative Frobenius norm.
 * The 28-layer model on a 4-row lognormal batch, by properties that hold at any size:
   activations kept vs recomputed give the same bits; replays are repeatable; whole-model,
-  per-layer and resident weights give the same bits; the loss is finite and near ln V at random
+  per-layer and resident weights, and one dequant per step instead of one per pass, give the
+  same bits; the loss is finite and near ln V at random
   init; one step's loss is within 1e-3 (relative) of the plain autograd eager step
   (rus_amd.eager_reference) on the same weights and masks.
 * The 28-layer model on a short batch, dropout off, against the fp32 CPU oracle: loss within
@@ -103,7 +104,11 @@ def test_full_model_step_properties(full_model):
     cfg, model, batch = full_model
     results = {}
     for name, kw in (("model_keep", dict(stream_unit="model", recompute=False)),
+                     ("model_keep_once", dict(stream_unit="model", recompute=False,
+                                              dequant_once=True)),
                      ("model_recompute", dict(stream_unit="model", recompute=True)),
+                     ("model_recompute_once", dict(stream_unit="model", recompute=True,
+                                                   dequant_once=True)),
                      ("layer_keep", dict(stream_unit="layer", recompute=False)),
                      ("resident_keep", dict(resident_weights=True, recompute=False))):
         kw.setdefault("resident_weights", False)

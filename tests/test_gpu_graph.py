@@ -183,16 +183,19 @@ def test_graph_replays_repeatable_across_buckets(unit):
 
 def test_graph_saved_activations_match_recompute_bitwise():
     # The captured step with activations kept from the forward (and with the second stream:
-    # dequant ahead, LoRA-down beside the q/k/v GEMM) gives the recompute's bits, dropout
-    # included, on two buckets and repeated replays.
+    # dequant ahead, LoRA-down beside the q/k/v GEMM; or with one dequant per step, the backward
+    # reading the forward's fp16 weights) gives the recompute's bits, dropout included, on two
+    # buckets and repeated replays.
     cfg = small_config(dropout=0.1)
     model = M.build_random_qlora_qwen2(cfg, DEV, seed=6, std=0.05)
     a = _batch(cfg, [30, 50], seed=1)
     b = _batch(cfg, [90, 70, 12], seed=2)
     res = []
-    for recompute, ov in ((True, False), (False, False), (False, True)):
+    for recompute, ov, once in ((True, False, False), (False, False, False), (False, True, False),
+                                (False, False, True), (True, False, True)):
         engine = ops.Qwen2FusedEngine(model, DEV, resident_weights=False, stream_unit="model",
-                                      dropout_seed=77, recompute=recompute, overlap=ov)
+                                      dropout_seed=77, recompute=recompute, overlap=ov,
+                                      dequant_once=once)
         gs = GraphedTrainStep(engine, bucket=64, training=True)
         out = []
         for batch in (a, b, a):
@@ -207,6 +210,12 @@ def test_graph_saved_activations_match_recompute_bitwise():
             else:
                 for g0, g1 in zip(x, y):
                     assert torch.equal(g0, g1)
+    # one dequant per step needs the packed weights on the device for the whole step and the
+    # dequant on the step's own stream
+    with pytest.raises(ValueError, match="dequant"):
+        ops.Qwen2FusedEngine(model, DEV, stream_unit="layer", dequant_once=True)
+    with pytest.raises(ValueError, match="dequant_once"):
+        ops.Qwen2FusedEngine(model, DEV, stream_unit="model", overlap=True, dequant_once=True)
 
 
 @pytest.mark.parametrize("resident", [True, False])
