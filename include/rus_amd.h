@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define RUS_ABI_VERSION 13
+#define RUS_ABI_VERSION 14
 
 #define RUS_DTYPE_F16 0
 #define RUS_DTYPE_F32 1
@@ -142,16 +142,46 @@ typedef struct rus_norm_side {
 } rus_norm_side;
 
 /*
+ * LoRA-down of rank r over token rows, by blocks of four tokens:
+ *   mid_q = fp16(drop_q(x) A_q^T), mid_v = fp16(drop_v(x) A_v^T)
+ * x [n_tokens, stride_x] fp16 (d a multiple of 64, stride_x a multiple of 8, 16-byte aligned),
+ * A_q, A_v [r, d] fp16 (16-byte aligned), r in {4, 8, 16}, mid_q / mid_v [n_tokens, r] fp16.
+ * Dropout: keep bits of both branches ([n_tokens, ceil(d / 32)] words, bit c % 32 of word c / 32
+ * keeps element c) with scale 1 / (1 - p), or both NULL (no dropout). fp32 sums: each of the
+ * block's four waves reduces a quarter of d on MFMA, the quarters added in order, one fp16
+ * rounding; the same bits as the product carried by rus_nf4_dequant_multi_norm.
+ * Replaces: mid_q = F.linear(lora_dropout(norm1), A_q) (and v) in solution/ops.py:775-778.
+ */
+typedef struct rus_lora_rows {
+  const void* x;
+  int64_t stride_x, n_tokens, d;
+  int32_t r;
+  const void* a_q;
+  const void* a_v;
+  const uint32_t* bits_q;
+  const uint32_t* bits_v;
+  float p_q, p_v;
+  void* mid_q;
+  void* mid_v;
+} rus_lora_rows;
+
+int rus_lora_down_rows(const rus_lora_rows* args, void* stream);
+
+/*
  * rus_nf4_dequant_multi and one independent RMSNorm in a single launch (the norm's rows run in
  * blocks of their own beside the decode): a layer's weight dequant with that layer's input norm
  * (solution/ops.py:760-766 before 768-771) or with the norm backward of the layer above
  * (ops.py:994-996, then the next layer's dequant, ops.py:855-860). Same results as the two
  * separate calls. The norm must satisfy n_cols <= 2048, n_cols and stride_row multiples of 8,
  * 16-byte aligned rows; otherwise RUS_ERR_UNSUPPORTED (nothing launched).
+ * down (forward norm only, or NULL): the LoRA-down of the norm's output, formed by the same
+ * blocks right after their rows (down->x is the norm's out, with its rows, width and stride):
+ * the bits of rus_lora_down_rows on that output.
  */
 int rus_nf4_dequant_multi_norm(const rus_nf4_job* jobs, int32_t n_jobs, const float* code2,
                                int32_t blocksize, int32_t super_blocksize,
-                               const rus_norm_side* side, void* stream);
+                               const rus_norm_side* side, const rus_lora_rows* down,
+                               void* stream);
 
 /*
  * Product with an NF4 double-quant weight W [w_rows, w_cols] (one job of up to three row

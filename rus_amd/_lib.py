@@ -11,7 +11,7 @@ import threading
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "librus_amd.so"
-ABI_VERSION = 13
+ABI_VERSION = 14
 
 DTYPE_F16 = 0
 DTYPE_F32 = 1
@@ -49,6 +49,18 @@ class NormSide(ctypes.Structure):
 
 NORM_FWD, NORM_BWD = 1, 2
 
+
+class LoraRows(ctypes.Structure):
+    """struct rus_lora_rows of include/rus_amd.h."""
+
+    _fields_ = [
+        ("x", ctypes.c_void_p), ("stride_x", ctypes.c_int64), ("n_tokens", ctypes.c_int64),
+        ("d", ctypes.c_int64), ("r", ctypes.c_int32), ("a_q", ctypes.c_void_p),
+        ("a_v", ctypes.c_void_p), ("bits_q", ctypes.c_void_p), ("bits_v", ctypes.c_void_p),
+        ("p_q", ctypes.c_float), ("p_v", ctypes.c_float), ("mid_q", ctypes.c_void_p),
+        ("mid_v", ctypes.c_void_p),
+    ]
+
 # name -> argtypes, in the order of include/rus_amd.h. Every entry point returns int.
 SIGNATURES: dict[str, list] = {
     "rus_copy_from_host": [_vp, _vp, _i64, _vp],
@@ -56,8 +68,9 @@ SIGNATURES: dict[str, list] = {
     "rus_nf4_dequant": [_vp, _vp, _vp, _vp, _f32, _f32, _f32, _i64, _i64, _i64, _i64, _i64, _i64,
                         _i64, _i32, _i32, _vp, _vp],
     "rus_nf4_dequant_multi": [ctypes.POINTER(Nf4Job), _i32, _vp, _i32, _i32, _vp],
+    "rus_lora_down_rows": [ctypes.POINTER(LoraRows), _vp],
     "rus_nf4_dequant_multi_norm": [ctypes.POINTER(Nf4Job), _i32, _vp, _i32, _i32,
-                                   ctypes.POINTER(NormSide), _vp],
+                                   ctypes.POINTER(NormSide), ctypes.POINTER(LoraRows), _vp],
     "rus_nf4_gemm_plan": [_i64, _i64, _i64, _i32, ctypes.POINTER(_i32), ctypes.POINTER(_i64),
                           ctypes.POINTER(_i64)],
     "rus_nf4_gemm": [_vp, _i64, _i64, ctypes.POINTER(Nf4Job), _vp, _i64, _i64, _i32, _i32, _i32,

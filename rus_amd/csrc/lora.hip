@@ -34,24 +34,13 @@
 #include <mutex>
 
 #include "common.h"
+#include "lora_rows.h"
 
 namespace rus {
 namespace {
 
-typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
-typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
-typedef float f32x16 __attribute__((ext_vector_type(16)));
-
 constexpr int kTok = 32;  // tokens per tile (down, d_mid, expansion)
 constexpr int kSW = 4;    // waves per block (down, d_mid, expansion)
-
-__device__ __forceinline__ f32x16 mfma(f16x8 a, f16x8 b, f32x16 c) {
-  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
-}
-
-__device__ __forceinline__ f16x8 ld8(const f16* p) { return *reinterpret_cast<const f16x8*>(p); }
-
-__device__ __forceinline__ f16x8 zero8() { return f16x8{0, 0, 0, 0, 0, 0, 0, 0}; }
 
 // Accumulator row of register r for lane half h (v_mfma_f32_32x32x16: lane l holds column l % 32).
 __device__ __forceinline__ int acc_row(int r, int h) { return 8 * (r >> 2) + 4 * h + (r & 3); }
@@ -70,17 +59,6 @@ __device__ __forceinline__ f16x8 frag_rank(const f16* row, int k0) {
     const f16x4 v = *reinterpret_cast<const f16x4*>(row);
     return f16x8{v[0], v[1], v[2], v[3], 0, 0, 0, 0};
   }
-}
-
-// The reference's fp16 dropout of 8 values (keep bit sh + i of word w for value i).
-__device__ __forceinline__ f16x8 drop8(f16x8 x, uint32_t w, int sh, float scale) {
-  f16x8 r;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const f16 v = from_f32<f16>(static_cast<float>(x[i]) * scale);
-    r[i] = (w >> (sh + i)) & 1u ? v : static_cast<f16>(0.0f);
-  }
-  return r;
 }
 
 // Accumulator layout of the tokens x ranks products: for R <= 16 the q and v results share one
@@ -556,6 +534,12 @@ void lora_bwd_xw_kernel(BwdWArgs a, ExpandArgs x,
                        static_cast<int64_t>(e / x_col_blocks) * kTok);
 }
 
+// LoRA-down by row blocks (lora_rows.h): block b forms mid_q / mid_v of tokens 4b .. 4b + 3.
+__global__ __launch_bounds__(256) void lora_down_rows_kernel(DownRows a) {
+  __shared__ float park[kDownParkFloats];
+  lora_down_rows4(a, static_cast<int64_t>(blockIdx.x) * kDownRows, park);
+}
+
 bool rank_ok(int r) { return r == 4 || r == 8 || r == 16 || r == 32; }
 
 int check_p(const char* fn, float pq, float pv) {
@@ -968,5 +952,23 @@ extern "C" int rus_lora_bwd_xw(const void* x, int64_t stride_x, const uint32_t* 
     break;
   switch (r) { RUS_BXW(4) RUS_BXW(8) RUS_BXW(16) RUS_BXW(32) }
 #undef RUS_BXW
+  return check_launch(fn);
+}
+
+// ---------------------------------------------------------------------------------------------
+// rus_lora_down_rows: LoRA-down by blocks of four token rows (no workspace), the arithmetic the
+// per-layer dequant launch uses when it carries the input norm and this product.
+// ---------------------------------------------------------------------------------------------
+
+extern "C" int rus_lora_down_rows(const rus_lora_rows* q, void* stream) {
+  using namespace rus;
+  const char* fn = "rus_lora_down_rows";
+  if (!q) return fail(RUS_ERR_INVALID, "%s: null argument", fn);
+  DownRows a;
+  if (int e = lora_rows_args(fn, *q, a)) return e;
+  if (q->n_tokens == 0) return RUS_OK;
+  const dim3 grid(static_cast<uint32_t>((q->n_tokens + kDownRows - 1) / kDownRows));
+  hipLaunchKernelGGL(lora_down_rows_kernel, grid, dim3(256), 0, static_cast<hipStream_t>(stream),
+                     a);
   return check_launch(fn);
 }

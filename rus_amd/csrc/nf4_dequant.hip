@@ -18,6 +18,7 @@
 
 #include "common.h"
 #include "rmsnorm_rows.h"
+#include "lora_rows.h"
 
 namespace rus {
 namespace {
@@ -296,7 +297,11 @@ struct NormSide {
   int64_t stride;
   float eps;
   uint32_t blocks;
+  int has_down;   // forward: the same blocks then form the LoRA-down of their rows' output
+  DownRows down;
 };
+
+static_assert((kTabMaxBlocks + 1) * 16 >= kDownParkFloats, "the LoRA-down sums fit in s_tab");
 
 template <int UNROLL, bool BWD, typename W, int NIT>
 __global__ __launch_bounds__(kThreads) void nf4_dequant_norm_kernel(Nf4Multi m, NormSide s) {
@@ -321,6 +326,10 @@ __global__ __launch_bounds__(kThreads) void nf4_dequant_norm_kernel(Nf4Multi m, 
       else
         rmsnorm_fwd_row<f16, W, NIT, false>(s.x, s.res, w, s.sum_out, s.out, s.rstd, row,
                                             s.n_rows, s.n_cols, s.stride, s.eps);
+      if (s.has_down) {  // uniform; the block's four output rows are its LoRA-down tokens
+        __syncthreads();  // every wave's row is stored
+        lora_down_rows4(s.down, static_cast<int64_t>(blockIdx.x) * kDownRows, s_tab);
+      }
     }
     return;
   }
@@ -478,7 +487,7 @@ extern "C" int rus_nf4_dequant_multi(const rus_nf4_job* jobs, int32_t n_jobs, co
 extern "C" int rus_nf4_dequant_multi_norm(const rus_nf4_job* jobs, int32_t n_jobs,
                                           const float* code2, int32_t blocksize,
                                           int32_t super_blocksize, const rus_norm_side* side,
-                                          void* stream) {
+                                          const rus_lora_rows* down, void* stream) {
   using namespace rus;
   const char* fn = "rus_nf4_dequant_multi_norm";
   if (n_jobs <= 0 || n_jobs > kMaxJobs || !jobs || !side)
@@ -501,6 +510,14 @@ extern "C" int rus_nf4_dequant_multi_norm(const rus_nf4_job* jobs, int32_t n_job
     return fail(RUS_ERR_UNSUPPORTED,
                 "%s: the norm needs n_cols <= 2048, n_cols and stride multiples of 8 and "
                 "16-byte aligned rows", fn);
+  DownRows dn{};
+  if (down) {
+    if (bwd || down->x != q.out || down->n_tokens != q.n_rows || down->d != q.n_cols ||
+        down->stride_x != q.stride_row)
+      return fail(RUS_ERR_INVALID,
+                  "%s: the carried LoRA-down must read the forward norm's output rows", fn);
+    if (int e = lora_rows_args(fn, *down, dn)) return e;
+  }
   Nf4Multi m{};
   m.n_jobs = n_jobs;
   uint32_t total = 0;
@@ -526,7 +543,9 @@ extern "C" int rus_nf4_dequant_multi_norm(const rus_nf4_job* jobs, int32_t n_job
               static_cast<int>(q.n_cols),
               q.stride_row,
               q.eps,
-              static_cast<uint32_t>((q.n_rows + kThreads / kWave - 1) / (kThreads / kWave))};
+              static_cast<uint32_t>((q.n_rows + kThreads / kWave - 1) / (kThreads / kWave)),
+              down ? 1 : 0,
+              dn};
   const dim3 grid(total + ns.blocks);
   hipStream_t st = static_cast<hipStream_t>(stream);
   auto launch = [&](auto bwd_c, auto wtag, auto nit_c) {

@@ -40,6 +40,8 @@ __all__ = [
     "lora_dropout_bwd_add",
     "dropout_keep_bits",
     "lora_workspace_size",
+    "lora_down_rows",
+    "LORA_ROWS_RANKS",
     "lora_down_fwd",
     "qkv_rope_fwd_mid",
     "lora_bwd_x",
@@ -298,9 +300,11 @@ def dequant_nf4_segments(segments: list[dict], code2: torch.Tensor, blocksize: i
         outs.append(out)
         total_bytes += nb + absmax.numel() + 4 * absmax2.numel() + 2 * n_el
     if norm is not None and not norm.done and norm.side is not None:
-        _launch("nf4_dequant", total_bytes + norm.nbytes, 0, "rus_nf4_dequant_multi_norm", jobs,
-                len(segments), code2.data_ptr(), int(blocksize), int(super_blocksize),
-                ctypes.byref(norm.side), _stream(code2))
+        down = None if norm.down is None else ctypes.byref(norm.down)
+        extra = 0 if norm.down is None else _down_rows_bytes(norm.down)
+        _launch("nf4_dequant", total_bytes + norm.nbytes + extra, 0, "rus_nf4_dequant_multi_norm",
+                jobs, len(segments), code2.data_ptr(), int(blocksize), int(super_blocksize),
+                ctypes.byref(norm.side), down, _stream(code2))
         norm.done = True
         return outs
     if norm is not None:
@@ -480,16 +484,32 @@ class DeferredNorm:
     (``dequant_nf4_segments(..., norm=...)``, when ``side`` is set) or alone (``run``). Nothing
     may read the outputs before one of the two has been enqueued. Holds its operands alive."""
 
-    __slots__ = ("kernel", "nbytes", "fn", "args", "side", "keep", "done")
+    __slots__ = ("kernel", "nbytes", "fn", "args", "side", "keep", "done", "out", "down",
+                 "down_keep")
 
-    def __init__(self, kernel, nbytes, fn, args, side, keep):
+    def __init__(self, kernel, nbytes, fn, args, side, keep, out=None):
         self.kernel, self.nbytes, self.fn, self.args = kernel, nbytes, fn, args
-        self.side, self.keep, self.done = side, keep, False
+        self.side, self.keep, self.done, self.out = side, keep, False, out
+        self.down = self.down_keep = None
+
+    def carry_lora_down(self, a_q: torch.Tensor, a_v: torch.Tensor,
+                        bits_q: torch.Tensor | None = None, bits_v: torch.Tensor | None = None,
+                        p_q: float = 0.0, p_v: float = 0.0):
+        """Attaches the LoRA-down of this (forward) norm's output, ``lora_down_rows`` on it, to
+        the norm's launch: the dequant launch that carries the norm forms it in the same blocks,
+        ``run`` right after the norm. Returns (mid_q, mid_v), valid once the norm is enqueued."""
+        if self.out is None or self.done or self.down is not None:
+            raise RuntimeError("carry_lora_down: needs a forward norm not yet enqueued")
+        mid_q, mid_v, args, keep = _lora_rows(self.out, a_q, a_v, bits_q, bits_v, p_q, p_v)
+        self.down, self.down_keep = args, keep
+        return mid_q, mid_v
 
     def run(self) -> None:
-        """Launches the norm on its own (no-op once it has been enqueued)."""
+        """Launches the norm (and a carried LoRA-down) on its own (no-op once enqueued)."""
         if not self.done:
             _launch(self.kernel, self.nbytes, 0, self.fn, *self.args)
+            if self.down is not None:
+                _launch_down_rows(self.down, self.out)
             self.done = True
 
 
@@ -546,7 +566,7 @@ def rms_norm_fwd(
         side = _norm_side(_lib.NORM_FWD, n_rows, n_cols, x_2d.stride(0), eps, wdt, x_2d, res_2d,
                           None, w, rstd, sum_out, norm_out)
         return outs + (DeferredNorm("rmsnorm_fwd", nbytes, "rus_rmsnorm_fwd", args, side,
-                                    (x_2d, res_2d, w, sum_out, norm_out, rstd)),)
+                                    (x_2d, res_2d, w, sum_out, norm_out, rstd), out=norm_out),)
     _launch("rmsnorm_fwd", nbytes, 0, "rus_rmsnorm_fwd", *args)
     return outs
 
@@ -1137,6 +1157,62 @@ def lora_down_fwd(x: torch.Tensor, a_q: torch.Tensor, a_v: torch.Tensor,
             "rus_lora_down_fwd", x2.data_ptr(), n, d, x2.stride(0), a_q.data_ptr(),
             a_v.data_ptr(), r, mid_q.data_ptr(), mid_v.data_ptr(), bq, bv, float(p_q), float(p_v),
             ws.data_ptr(), ws.numel(), cnt.data_ptr(), cnt.numel(), _stream(x2))
+    return mid_q, mid_v
+
+
+LORA_ROWS_RANKS = (4, 8, 16)  # ranks of rus_lora_down_rows
+
+
+def _lora_rows(x: torch.Tensor, a_q, a_v, bits_q, bits_v, p_q, p_v, out=None):
+    """(mid_q, mid_v, rus_lora_rows, tensors it points at) of lora_down_rows."""
+    fn = "lora_down_rows"
+    _require_device(fn, x, a_q, a_v, bits_q, bits_v)
+    r, d = a_q.shape
+    if r not in LORA_ROWS_RANKS or d % 64:
+        raise ValueError(f"{fn}: rank {r} not in {LORA_ROWS_RANKS} or d = {d} not a multiple "
+                         f"of 64")
+    x2 = _rows(fn, x, d, "x")
+    if x2.dtype != torch.float16:
+        raise ValueError(f"{fn}: fp16 activations only")
+    _lora_operand(fn, a_q, (r, d), "a_q")
+    _lora_operand(fn, a_v, (r, d), "a_v")
+    n = x2.shape[0]
+    bq = _bits(fn, bits_q, n, d, "bits_q")
+    bv = _bits(fn, bits_v, n, d, "bits_v")
+    if out is None:
+        mid_q = torch.empty((n, r), dtype=torch.float16, device=x.device)
+        mid_v = torch.empty((n, r), dtype=torch.float16, device=x.device)
+    else:
+        mid_q, mid_v = out
+        _lora_operand(fn, mid_q, (n, r), "mid_q")
+        _lora_operand(fn, mid_v, (n, r), "mid_v")
+    a = _lib.LoraRows()
+    a.x, a.stride_x, a.n_tokens, a.d, a.r = x2.data_ptr(), x2.stride(0), n, d, r
+    a.a_q, a.a_v, a.bits_q, a.bits_v = a_q.data_ptr(), a_v.data_ptr(), bq, bv
+    a.p_q, a.p_v = float(p_q), float(p_v)
+    a.mid_q, a.mid_v = mid_q.data_ptr(), mid_v.data_ptr()
+    return mid_q, mid_v, a, (x2, a_q, a_v, bits_q, bits_v, mid_q, mid_v)
+
+
+def _down_rows_bytes(a) -> int:
+    n, d, r = a.n_tokens, a.d, a.r
+    return n * d * 2 + 4 * r * d + 4 * n * r + (n * d // 4 if a.bits_q else 0)
+
+
+def _launch_down_rows(a, like: torch.Tensor) -> None:
+    _launch("lora_down", _down_rows_bytes(a), 4 * a.n_tokens * a.d * a.r, "rus_lora_down_rows",
+            ctypes.byref(a), _stream(like))
+
+
+def lora_down_rows(x: torch.Tensor, a_q: torch.Tensor, a_v: torch.Tensor,
+                   bits_q: torch.Tensor | None = None, bits_v: torch.Tensor | None = None,
+                   p_q: float = 0.0, p_v: float = 0.0, out=None):
+    """(mid_q, mid_v) = (drop_q(x) A_q^T, drop_v(x) A_v^T) in fp16 as ``lora_down_fwd``, by
+    blocks of four token rows without workspace (ranks 4, 8, 16, d a multiple of 64): the
+    arithmetic of the LoRA-down a dequant launch carries beside the input norm
+    (``DeferredNorm.carry_lora_down``), so both give the same bits."""
+    mid_q, mid_v, a, keep = _lora_rows(x, a_q, a_v, bits_q, bits_v, p_q, p_v, out)
+    _launch_down_rows(a, keep[0])
     return mid_q, mid_v
 
 

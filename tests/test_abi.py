@@ -150,7 +150,45 @@ def test_dequant_with_norm_validates_the_norm_first(field, value, msg):
     if field == "n_cols":
         side.stride_row = value
     with pytest.raises(RuntimeError, match=msg):
-        _lib.call("rus_nf4_dequant_multi_norm", jobs, 1, 16, 64, 256, side, None)
+        _lib.call("rus_nf4_dequant_multi_norm", jobs, 1, 16, 64, 256, side, None, None)
+
+
+def _rows_args(**kw):
+    a = _lib.LoraRows()
+    a.x, a.stride_x, a.n_tokens, a.d, a.r = 16, 1536, 8, 1536, 16
+    a.a_q = a.a_v = a.mid_q = a.mid_v = 16
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+@pytest.mark.parametrize("kw,msg", [({"r": 32}, "rank 32"), ({"d": 1500, "stride_x": 1500},
+                                    "multiple of 64"), ({"bits_q": 16}, "both branches"),
+                                    ({"p_q": 1.0, "bits_q": 16, "bits_v": 16}, "probabilities"),
+                                    ({"x": None}, "null pointer"), ({"x": 8}, "16-byte aligned")])
+def test_lora_down_rows_validates(kw, msg):
+    with pytest.raises(RuntimeError, match=msg):
+        _lib.call("rus_lora_down_rows", _rows_args(**kw), None)
+
+
+def test_dequant_carried_lora_down_must_read_the_norm_output():
+    # The LoRA-down the combined launch carries reads the forward norm's own output rows; it is
+    # checked with the norm, before any job, so nothing is launched.
+    jobs = (_lib.Nf4Job * 1)()
+    side = _lib.NormSide()
+    side.kind, side.w_dtype = _lib.NORM_FWD, 1
+    side.n_rows, side.n_cols, side.stride_row, side.eps = 8, 1536, 1536, 1e-6
+    side.x = side.weight = side.rstd = 16
+    side.out = 32
+    for kw in ({"x": 48}, {"n_tokens": 9}, {"d": 1024}):
+        with pytest.raises(RuntimeError, match="forward norm's output rows"):
+            _lib.call("rus_nf4_dequant_multi_norm", jobs, 1, 16, 64, 256, side,
+                      _rows_args(**{"x": 32, **kw}), None)
+    side.kind = _lib.NORM_BWD
+    side.h = 16
+    with pytest.raises(RuntimeError, match="forward norm's output rows"):
+        _lib.call("rus_nf4_dequant_multi_norm", jobs, 1, 16, 64, 256, side, _rows_args(x=32),
+                  None)
 
 
 def test_lora_workspace_sizes_follow_the_block_decomposition():

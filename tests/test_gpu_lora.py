@@ -267,3 +267,67 @@ def test_lora_bwd_xw_equals_bwd_x_then_bwd_w(r, drop, n):
     assert torch.equal(dx_a, dx_b)
     for a, b in zip(outs_a, outs_b):
         assert torch.equal(a, b)
+
+
+# ---------------------------------------------------------------------------------------------
+# LoRA-down by blocks of four token rows (rus_lora_down_rows) and the same product carried by the
+# per-layer dequant launch beside the input norm (rus_nf4_dequant_multi_norm with `down`).
+
+@pytest.mark.parametrize("r", [4, 8, 16])
+@pytest.mark.parametrize("drop", [False, True])
+@pytest.mark.parametrize("n,d", [(1, 1536), (37, 1536), (301, 1536), (6, 64), (9, 2048)])
+def test_lora_down_rows_matches_oracle(r, drop, n, d):
+    _, x, aq, av, _, _ = _inputs(n, d, 8, 8, r, seed=7 * r + n + d)
+    seed_v = 515
+    args = (seed_v, 2, 3, 0.05, 0.1) if drop else (None,)
+    mq, mv, xq, xv = ref.lora_down_fwd(x, aq, av, *args)
+    bits = _bits(seed_v, 2, n, d, 0.05, 0.1) if drop else (None, None)
+    out = K.lora_down_rows(x.to(DEV), aq.to(DEV), av.to(DEV), *bits, 0.05, 0.1)
+    torch.cuda.synchronize()
+    for got, want, xx, aa in zip(out, (mq, mv), (xq, xv), (aq, av)):
+        ok, err = _close(got, want, a=xx, b=aa.t())
+        assert ok, err
+    # the split-K kernel of rus_lora_down_fwd gives the same values within one ulp each way
+    old = K.lora_down_fwd(x.to(DEV), aq.to(DEV), av.to(DEV), *bits, 0.05, 0.1)
+    for got, o, xx, aa in zip(out, old, (xq, xv), (aq, av)):
+        ok, err = _close(got, o.cpu(), ulps=2.0, a=xx, b=aa.t())
+        assert ok, err
+
+
+@pytest.mark.parametrize("drop", [False, True])
+@pytest.mark.parametrize("n", [3, 300])
+def test_dequant_launch_carries_norm_and_lora_down_bitwise(drop, n):
+    """The input norm and its LoRA-down carried by a layer's dequant launch give the bits of the
+    standalone norm followed by rus_lora_down_rows, and the weights of the plain dequant."""
+    from rus_amd import model as M
+    from rus_amd.hostload import WeightStream
+
+    cfg = M.Qwen2Config(num_hidden_layers=1, hidden_size=1536, intermediate_size=256,
+                        num_attention_heads=12, num_key_value_heads=2, vocab_size=64)
+    model = M.build_random_qlora_qwen2(cfg, DEV, seed=3)
+    ws = WeightStream(model.layers, DEV, resident=True)
+    g = torch.Generator().manual_seed(n)
+    x = torch.randn(n, 1536, generator=g).half().to(DEV)
+    res = torch.randn(n, 1536, generator=g).half().to(DEV)
+    lnw = (torch.rand(1536, generator=g) + 0.5).to(DEV)
+    aq, av = ((torch.randn(16, 1536, generator=g) * 0.05).half().to(DEV) for _ in range(2))
+    bits = _bits(99, 0, n, 1536, 0.05, 0.1) if drop else (None, None)
+    want_w = [w.clone() for w in ws.dequant_layer(0).values()]
+    y0, h0, r0 = K.rms_norm_fwd(x, lnw, 1e-6, residual=res)
+    m0 = K.lora_down_rows(y0, aq, av, *bits, 0.05, 0.1)
+    torch.cuda.synchronize()
+    y1, h1, r1, pend = K.rms_norm_fwd(x, lnw, 1e-6, residual=res, defer=True)
+    m1 = pend.carry_lora_down(aq, av, *bits, 0.05, 0.1)
+    got_w = ws.dequant_layer(0, norm=pend)
+    assert pend.done
+    torch.cuda.synchronize()
+    for a, b in zip((y1, h1, r1, *m1), (y0, h0, r0, *m0)):
+        assert torch.equal(a, b)
+    for a, b in zip(got_w.values(), want_w):
+        assert torch.equal(a, b)
+    # a norm that runs on its own runs its carried LoRA-down too
+    y2, _, _, pend2 = K.rms_norm_fwd(x, lnw, 1e-6, residual=res, defer=True)
+    m2 = pend2.carry_lora_down(aq, av, *bits, 0.05, 0.1)
+    pend2.run()
+    torch.cuda.synchronize()
+    assert torch.equal(y2, y0) and all(torch.equal(a, b) for a, b in zip(m2, m0))
