@@ -791,11 +791,11 @@ def measured_traffic(kernel: str):
     return None
 
 
-def _graph_run(engine, model_opt, batches, steps, warmup):
+def _graph_run(engine, model_opt, batches, steps, warmup, bucket=64):
     """Captures the step's graphs for every batch bucket and times ``steps`` replays + AdamW."""
     from rus_amd.graph import GraphedTrainStep
 
-    g = GraphedTrainStep(engine)
+    g = GraphedTrainStep(engine, bucket=bucket)
     for b in batches:
         g.prepare(b[0], b[1], b[2])
     opt = flat_adamw(engine)[0]
@@ -838,6 +838,10 @@ def main() -> int:
                     help="on: each layer is dequantised once per step, into fp16 weights of its "
                          "own that the backward reads (2.6 GB); off: again in the backward, as "
                          "the reference does; the other setting is timed as an ablation")
+    ap.add_argument("--bucket", type=int, default=64,
+                    help="captured-graph bucket: each batch's packed token count is padded to a "
+                         "multiple of this (one graph per bucket and weight buffer; 64 pads the "
+                         "bench's 707.5 tokens per step to 744 on average, 256 to 864)")
     ap.add_argument("--no-ablation", action="store_true",
                     help="skip the timing of the other --recompute, --dequant-once and "
                          "--stream-unit settings")
@@ -920,7 +924,7 @@ def main() -> int:
     if not args.no_graph:
         from rus_amd.graph import GraphedTrainStep
 
-        graph = GraphedTrainStep(engine)
+        graph = GraphedTrainStep(engine, bucket=args.bucket)
         for b in batches:
             graph.prepare(b[0], b[1], b[2])
     graph_pool_mib = (torch.cuda.memory_reserved(dev) - reserved0) / 2**20
@@ -977,7 +981,7 @@ def main() -> int:
                    "tokens_per_step": tokens / args.steps, "lora": "r16 alpha32 dropout0.05 q,v",
                    "stream_unit": args.stream_unit, "recompute": args.recompute,
                    "overlap": "on" if overlap else "off", "gemm": args.gemm,
-                   "dequant_once": "on" if once else "off",
+                   "dequant_once": "on" if once else "off", "graph_bucket": args.bucket,
                    "lm_head": "token blocks of <= 256, [block, V] logits buffer, no [N, V]",
                    "optimizer": f"AdamW lr 2e-4 ({opt_kind}"
                                 + (", one flat LoRA buffer)" if graph is not None else ")")},
@@ -1013,20 +1017,22 @@ def main() -> int:
         timed_run(eng_a, opt, batches, 1, 0)
         out[f"recompute_{other}_peak_hbm_mib"] = (torch.cuda.max_memory_allocated(dev) - base_a) / 2**20
         out[f"recompute_{other}_tokens_per_s"], g_a = _graph_run(eng_a, None, batches,
-                                                                 min(args.steps, 16), 1)
+                                                                 min(args.steps, 16), 1,
+                                                                 args.bucket)
         del eng_a, g_a
         if args.stream_unit == "model" and args.gemm == "dequant" and not overlap:
             eng_d = Qwen2FusedEngine(model, dev, resident_weights=False, stream_unit="model",
                                      recompute=recompute, gemm=args.gemm, dequant_once=not once)
             out[f"dequant_once_{'off' if once else 'on'}_tokens_per_s"], g_d = _graph_run(
-                eng_d, None, batches, min(args.steps, 16), 1)
+                eng_d, None, batches, min(args.steps, 16), 1, args.bucket)
             del eng_d, g_d
             torch.cuda.empty_cache()
         unit = "layer" if args.stream_unit == "model" else "model"
         eng_u = Qwen2FusedEngine(model, dev, resident_weights=False, stream_unit=unit,
                                  recompute=recompute, overlap=False, gemm=args.gemm)
         out[f"stream_unit_{unit}_tokens_per_s"], g_u = _graph_run(eng_u, None, batches,
-                                                                   min(args.steps, 16), 1)
+                                                                   min(args.steps, 16), 1,
+                                                                   args.bucket)
         del eng_u, g_u
         torch.cuda.empty_cache()
 
@@ -1034,7 +1040,8 @@ def main() -> int:
         eng_r = Qwen2FusedEngine(model, dev, resident_weights=True, recompute=recompute,
                                  overlap=overlap, gemm=args.gemm, dequant_once=once)
         out["resident_weights_tokens_per_s"], g_r = _graph_run(eng_r, None, batches,
-                                                                min(args.steps, 16), 1)
+                                                                min(args.steps, 16), 1,
+                                                                args.bucket)
         del eng_r, g_r
         torch.cuda.empty_cache()
 

@@ -135,7 +135,7 @@ class GraphedTrainStep:
     """``step(input_ids, attention_mask, labels)`` -> loss (device scalar), with the LoRA
     gradients left in the parameters' ``.grad``. One captured graph per bucket."""
 
-    def __init__(self, engine: Qwen2FusedEngine, bucket: int = 256, training: bool = True,
+    def __init__(self, engine: Qwen2FusedEngine, bucket: int = 64, training: bool = True,
                  num_items_in_batch=None, census: bool = False):
         if not engine.host_head.resident:
             raise ValueError("GraphedTrainStep needs an HBM-resident lm_head (resident_head=True)")
