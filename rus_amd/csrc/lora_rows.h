@@ -83,6 +83,7 @@ constexpr int kDownParkFloats = 4 * 128;  // LDS the block's four wave sums take
 // zero) and tokens as columns (4 .. 31 zero); the waves' sums meet in `park` (kDownParkFloats of
 // LDS) and are added in wave order, then rounded to fp16 once. Every thread of the block must
 // call it (it holds barriers); x's rows must be visible to the whole block.
+template <int U = 4>
 __device__ __forceinline__ void lora_down_rows4(const DownRows& a, int64_t t0, float* park) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, h = lane >> 5, col = lane & 31;
   const bool is_q = col < a.r, is_v = col >= a.r && col < 2 * a.r;
@@ -97,7 +98,8 @@ __device__ __forceinline__ void lora_down_rows4(const DownRows& a, int64_t t0, f
   const int per = a.d / 4;  // a multiple of 16
   const int c_begin = wave * per;
   f32x16 acc = f32x16{};
-  constexpr int U = 4;  // K steps whose loads are issued together
+  // U: K steps whose loads are issued together (register budget vs latency; no effect on the
+  // arithmetic)
   for (int s0 = 0; s0 < per; s0 += 16 * U) {
     f16x8 af[U], xf[U];
     uint32_t wq[U], wv[U];

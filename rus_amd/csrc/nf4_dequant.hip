@@ -298,13 +298,18 @@ struct NormSide {
   float eps;
   uint32_t blocks;
   int has_down;   // forward: the same blocks then form the LoRA-down of their rows' output
+                  // (nf4_dequant_norm_down_kernel)
   DownRows down;
 };
 
 static_assert((kTabMaxBlocks + 1) * 16 >= kDownParkFloats, "the LoRA-down sums fit in s_tab");
 
-template <int UNROLL, bool BWD, typename W, int NIT>
-__global__ __launch_bounds__(kThreads) void nf4_dequant_norm_kernel(Nf4Multi m, NormSide s) {
+// DOWN: the forward norm's blocks then form the LoRA-down of their rows (lora_rows.h). Its MFMA
+// code needs registers the decode does not, so it is a kernel of its own: the plain variant keeps
+// the decode at 8 waves per SIMD; the LoRA-down variant runs at 6, its K steps loaded one at a
+// time so that the decode blocks keep their registers.
+template <int UNROLL, bool BWD, typename W, int NIT, bool DOWN>
+__device__ __forceinline__ void dequant_norm_body(const Nf4Multi& m, const NormSide& s) {
   __shared__ float s_code2[256];
   __shared__ float s_nf4[16];
   __shared__ float s_scale[kTabMaxBlocks + 1];
@@ -326,9 +331,9 @@ __global__ __launch_bounds__(kThreads) void nf4_dequant_norm_kernel(Nf4Multi m, 
       else
         rmsnorm_fwd_row<f16, W, NIT, false>(s.x, s.res, w, s.sum_out, s.out, s.rstd, row,
                                             s.n_rows, s.n_cols, s.stride, s.eps);
-      if (s.has_down) {  // uniform; the block's four output rows are its LoRA-down tokens
+      if constexpr (DOWN) {  // the block's four output rows are its LoRA-down tokens
         __syncthreads();  // every wave's row is stored
-        lora_down_rows4(s.down, static_cast<int64_t>(blockIdx.x) * kDownRows, s_tab);
+        lora_down_rows4<1>(s.down, static_cast<int64_t>(blockIdx.x) * kDownRows, s_tab);
       }
     }
     return;
@@ -345,6 +350,17 @@ __global__ __launch_bounds__(kThreads) void nf4_dequant_norm_kernel(Nf4Multi m, 
     dequant_block<UNROLL>(m.job[j], b - m.start[j], m.start[j + 1] - m.start[j], s_code2,
                           s_nf4);
   }
+}
+
+template <int UNROLL, bool BWD, typename W, int NIT>
+__global__ __launch_bounds__(kThreads) void nf4_dequant_norm_kernel(Nf4Multi m, NormSide s) {
+  dequant_norm_body<UNROLL, BWD, W, NIT, false>(m, s);
+}
+
+template <int UNROLL, typename W, int NIT>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(5))) void
+nf4_dequant_norm_down_kernel(Nf4Multi m, NormSide s) {
+  dequant_norm_body<UNROLL, false, W, NIT, true>(m, s);
 }
 
 bool is_pow2(int64_t v) { return v > 0 && (v & (v - 1)) == 0; }
@@ -552,6 +568,13 @@ extern "C" int rus_nf4_dequant_multi_norm(const rus_nf4_job* jobs, int32_t n_job
     constexpr bool B = decltype(bwd_c)::value;
     constexpr int N = decltype(nit_c)::value;
     using WT = decltype(wtag);
+    if constexpr (!B) {
+      if (ns.has_down) {
+        hipLaunchKernelGGL((nf4_dequant_norm_down_kernel<kUnrollMain, WT, N>), grid,
+                           dim3(kThreads), 0, st, m, ns);
+        return;
+      }
+    }
     hipLaunchKernelGGL((nf4_dequant_norm_kernel<kUnrollMain, B, WT, N>), grid, dim3(kThreads), 0,
                        st, m, ns);
   };
