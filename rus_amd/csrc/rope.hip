@@ -338,29 +338,20 @@ __device__ __forceinline__ float group16_transpose_sum(const float (&p)[16], int
 
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 
-// The B^T fragments a thread needs: rows r of bt (length d) at columns c .. c + 7 and
-// c + half .. c + half + 7, kept packed (4 registers per 8 values).
-struct MidFrags {
-  f16x8_t lo[kMidR], hi[kMidR];
-};
-
-__device__ __forceinline__ void load_mid_frags(MidFrags& f, const f16* __restrict__ bt, int64_t d,
-                                               int64_t c, int half) {
+// p[r] += sum_i lo[i] bt[r][c + i] + hi[i] bt[r][c + half + i], the B^T fragments loaded rank by
+// rank (holding all sixteen ranks' fragments at once took 213 VGPRs, two waves per SIMD).
+__device__ __forceinline__ void mid_partial(float (&p)[kMidR], const float (&lo)[kSpan],
+                                                     const float (&hi)[kSpan],
+                                                     const f16* __restrict__ bt, int64_t d,
+                                                     int64_t c, int half) {
 #pragma unroll
   for (int r = 0; r < kMidR; ++r) {
-    f.lo[r] = *reinterpret_cast<const f16x8_t*>(bt + r * d + c);
-    f.hi[r] = *reinterpret_cast<const f16x8_t*>(bt + r * d + c + half);
-  }
-}
-
-// p[r] += sum_i lo[i] bt[r][c + i] + hi[i] bt[r][c + half + i].
-__device__ __forceinline__ void mid_partial(float (&p)[kMidR], const float (&lo)[kSpan],
-                                            const float (&hi)[kSpan], const MidFrags& f) {
-#pragma unroll
-  for (int r = 0; r < kMidR; ++r)
+    const f16x8_t bl = *reinterpret_cast<const f16x8_t*>(bt + r * d + c);
+    const f16x8_t bh = *reinterpret_cast<const f16x8_t*>(bt + r * d + c + half);
 #pragma unroll
     for (int i = 0; i < kSpan; ++i)
-      p[r] += lo[i] * static_cast<float>(f.lo[r][i]) + hi[i] * static_cast<float>(f.hi[r][i]);
+      p[r] += lo[i] * static_cast<float>(bl[i]) + hi[i] * static_cast<float>(bh[i]);
+  }
 }
 
 __global__ __launch_bounds__(kThreads) void rope_bwd_mid_kernel(RopeBwdMidArgs m) {
@@ -383,12 +374,10 @@ __global__ __launch_bounds__(kThreads) void rope_bwd_mid_kernel(RopeBwdMidArgs m
   float p[kMidR];
 #pragma unroll
   for (int r = 0; r < kMidR; ++r) p[r] = 0.0f;
-  // The B fragments first: their loads do not wait for the gradient loads and stores below.
   const bool is_q = hd < a.h_q, is_v = hd >= a.h_q + a.h_kv;
-  MidFrags f;
-  if (t < a.n_tokens && (is_q || is_v))
-    load_mid_frags(f, is_q ? m.bt_q : m.bt_v, is_q ? d_q : d_v,
-                   static_cast<int64_t>(is_q ? hd : hd - a.h_q - a.h_kv) * a.head_dim + j, half);
+  const f16* bt = is_q ? m.bt_q : m.bt_v;
+  const int64_t bd = is_q ? d_q : d_v;
+  const int64_t bc = static_cast<int64_t>(is_q ? hd : hd - a.h_q - a.h_kv) * a.head_dim + j;
   if (t < a.n_tokens) {
     f16* out = a.dqkv + t * a.stride_dqkv + static_cast<int64_t>(hd) * a.head_dim;
     float lo[kSpan], hi[kSpan];
@@ -413,7 +402,7 @@ __global__ __launch_bounds__(kThreads) void rope_bwd_mid_kernel(RopeBwdMidArgs m
       f16* l = a.dv_lora + (t * a.h_kv + kv) * a.head_dim;
       store_from_f32<f16, kSpan>(l + j, lo);
       store_from_f32<f16, kSpan>(l + j + half, hi);
-      mid_partial(p, lo, hi, f);
+      mid_partial(p, lo, hi, bt, bd, bc, half);
     } else {
       if (!is_q && m.dk_part) {
         const int grp = a.h_q / a.h_kv;
@@ -450,7 +439,7 @@ __global__ __launch_bounds__(kThreads) void rope_bwd_mid_kernel(RopeBwdMidArgs m
         f16* l = a.dq_lora + (t * a.h_q + hd) * a.head_dim;
         store_from_f32<f16, kSpan>(l + j, ol);
         store_from_f32<f16, kSpan>(l + j + half, oh);
-        mid_partial(p, ol, oh, f);
+        mid_partial(p, ol, oh, bt, bd, bc, half);
       }
     }
   }
