@@ -842,6 +842,9 @@ def main() -> int:
                     help="captured-graph bucket: each batch's packed token count is padded to a "
                          "multiple of this (one graph per bucket and weight buffer; 64 pads the "
                          "bench's 707.5 tokens per step to 744 on average, 256 to 864)")
+    ap.add_argument("--lm-block", type=int, default=0,
+                    help="most tokens per block of the token-blocked lm_head (whole 256-token "
+                         "tiles; 0: the tiles whose fp16 logits fit 256 MiB, 768 at V=151936)")
     ap.add_argument("--no-ablation", action="store_true",
                     help="skip the timing of the other --recompute, --dequant-once and "
                          "--stream-unit settings")
@@ -887,6 +890,7 @@ def main() -> int:
 
     from rus_amd import model as M
     from rus_amd.eager_reference import eager_step_loss
+    from rus_amd import kernels as K
     from rus_amd.kernels import KernelTimer
     from rus_amd.ops import Qwen2FusedEngine, pack_varlen
 
@@ -907,6 +911,8 @@ def main() -> int:
     engine = Qwen2FusedEngine(model, dev, resident_weights=False, stream_unit=args.stream_unit,
                               recompute=recompute, overlap=overlap, gemm=args.gemm,
                               dequant_once=once)
+    engine.lm_block_tokens = args.lm_block or None
+    lm_block = args.lm_block or K.lm_head_block_tokens(engine.host_head.gpu_weight.shape[0])
     # Calibration pass (eager): every kernel timed, to name the dominant one.
     _, _, _, calib = timed_run(engine, opt, batches, 2, args.warmup, kernel_filter=None)
     dominant = max(calib, key=lambda k: calib[k]["ms"])
@@ -982,7 +988,8 @@ def main() -> int:
                    "stream_unit": args.stream_unit, "recompute": args.recompute,
                    "overlap": "on" if overlap else "off", "gemm": args.gemm,
                    "dequant_once": "on" if once else "off", "graph_bucket": args.bucket,
-                   "lm_head": "token blocks of <= 256, [block, V] logits buffer, no [N, V]",
+                   "lm_head": f"token blocks of <= {lm_block} (whole 256-token tiles), "
+                              "[block, V] logits buffer, no [N, V]",
                    "optimizer": f"AdamW lr 2e-4 ({opt_kind}"
                                 + (", one flat LoRA buffer)" if graph is not None else ")")},
         "roofline": roof,

@@ -169,7 +169,7 @@ class GraphedTrainStep:
         nll, _lse, ent, amax, _denom, d_final, loss = K.lm_head_ce(
             final, head.gpu_weight, img.labels, num_items_in_batch=self.num_items,
             need_grad=True, weight_t=head.gpu_weight_t, dh_scale=1.0 / PRESCALE_GRAD,
-            dh_dtype=final.dtype)
+            dh_dtype=final.dtype, block_tokens=eng.lm_block_tokens)
         del final
         stack_backward(eng, st, d_final, self.grad16)
         self.grad32.copy_(self.grad16)

@@ -55,6 +55,7 @@ __all__ = [
     "lm_head_ce_dh_finish",
     "lm_head_chunk_cols",
     "lm_head_token_blocks",
+    "lm_head_block_tokens",
     "lm_head_ce_denom",
     "lm_head_ce_logits",
     "lm_head_ce_rows",
@@ -1991,17 +1992,31 @@ def lm_head_ce_denom(labels: torch.Tensor, num_items_in_batch=None) -> torch.Ten
     return denom
 
 
+LM_BLOCK_BUDGET = 256 << 20  # bytes of fp16 logits one token block of the blocked head may hold
+
+
+def lm_head_block_tokens(n_vocab: int, budget: int = LM_BLOCK_BUDGET) -> int:
+    """Most tokens one block of the token-blocked head takes: the whole 256-token tiles whose fp16
+    logits [tokens, round_up(V, 64)] fit ``budget`` (at least one tile)."""
+    kp = max(LM_K, _round_up(n_vocab, LM_K))
+    return max(1, budget // (2 * kp * LM_TILE)) * LM_TILE
+
+
 def lm_head_token_blocks(n_tok: int, max_block: int = LM_TILE) -> list[tuple[int, int]]:
-    """Token ranges [t0, t1) of at most ``max_block`` tokens, balanced (sizes differ by <= 1)."""
+    """Token ranges [t0, t1): the ceil(n_tok / 256) MFMA token tiles spread evenly over the fewest
+    blocks of at most ``max_block`` tokens (rounded down to whole tiles, at least one), every block
+    whole tiles but the last, so no block adds a partly filled tile."""
     if n_tok <= 0:
         return []
-    nb = -(-n_tok // max_block)
-    base, extra = divmod(n_tok, nb)
+    max_tiles = max(1, max_block // LM_TILE)
+    tiles = -(-n_tok // LM_TILE)
+    nb = -(-tiles // max_tiles)
+    base, extra = divmod(tiles, nb)
     out, t = [], 0
     for b in range(nb):
-        n = base + (1 if b < extra else 0)
-        out.append((t, t + n))
-        t += n
+        t1 = min(n_tok, t + (base + (1 if b < extra else 0)) * LM_TILE)
+        out.append((t, t1))
+        t = t1
     return out
 
 
@@ -2027,7 +2042,7 @@ def _fwd_rows(hidden, weight, labels, parts: LMHeadPartials, target, t0: int, t1
 def lm_head_ce(hidden: torch.Tensor, weight: torch.Tensor, labels: torch.Tensor,
                num_items_in_batch=None, v_chunk: int | None = None, need_grad: bool = True,
                weight_t: torch.Tensor | None = None, dh_scale: float = 1.0,
-               dh_dtype: torch.dtype = torch.float32):
+               dh_dtype: torch.dtype = torch.float32, block_tokens: int | None = None):
     """Whole cross-entropy head on a device-resident fp16 lm_head weight [V, d].
 
     Returns (nll, lse, entropy, argmax, denom, dh, loss) where denom is a float32 device scalar
@@ -2035,13 +2050,14 @@ def lm_head_ce(hidden: torch.Tensor, weight: torch.Tensor, labels: torch.Tensor,
     denom (device scalar) and dh the hidden gradient of loss times 2^16, scaled by ``dh_scale``
     and stored as ``dh_dtype`` (None without need_grad).
 
-    With the gradient, the tokens go in blocks of at most 256 (one MFMA token tile). For each
-    block one GEMM over the whole vocabulary stores its fp16 logits in a [256, V] buffer; one
-    kernel per token row forms the statistics and turns the row into the reference's fp16
-    gradient G = fp16((softmax - onehot) 2^16 / denom) in place (the denominator is known up
-    front); and a split-K GEMM G . W writes the block's dH partials, summed once. W is read once
-    per block;
-    no [N, V] array exists and no logit is recomputed (the reference holds [N, 8192] chunks and
+    With the gradient, the tokens go in blocks of whole 256-token MFMA tiles, at most
+    ``block_tokens`` each (default: the tiles whose fp16 logits fit 256 MiB, 768 tokens at
+    V = 151936). For each block one GEMM over the whole vocabulary stores its fp16 logits in a
+    [block, V] buffer; one kernel per token row forms the statistics and turns the row into the
+    reference's fp16 gradient G = fp16((softmax - onehot) 2^16 / denom) in place (the denominator
+    is known up front); and a split-K GEMM G . W writes the block's dH partials, summed once. W
+    (and W^T) is read once per block; the logit buffer stays bounded at any token count and no
+    logit is recomputed (the reference holds [N, 8192] chunks and
     recomputes every logit, solution/ops.py:209-322). ``v_chunk`` (a multiple of 256) selects
     the single pass over vocabulary chunks instead (``LMHeadPass``: W read once in total, an
     [N, v_chunk] buffer), the layout of a head streamed from the host. ``weight_t`` is W^T
@@ -2083,7 +2099,7 @@ def lm_head_ce(hidden: torch.Tensor, weight: torch.Tensor, labels: torch.Tensor,
     kp = _round_up(V, LM_K)
     if wt.dtype != torch.float16 or wt.shape[0] != d or wt.shape[1] < kp or wt.stride(1) != 1:
         raise ValueError(f"{fn}: weight_t must be fp16 [{d}, >= {kp}] with contiguous rows")
-    blocks = lm_head_token_blocks(n_tok)
+    blocks = lm_head_token_blocks(n_tok, block_tokens if block_tokens else lm_head_block_tokens(V))
     nb_max = max(t1 - t0 for t0, t1 in blocks)
     ncu = cu_count(dev)
     splits = {nb: lm_head_split_count(nb, d, V, ncu) for nb in {t1 - t0 for t0, t1 in blocks}}

@@ -244,3 +244,26 @@ def test_lm_head_split_count_fills_whole_rounds_of_workgroups():
         for cap in (1, 2, 5):
             c = K.lm_head_split_count(n, d, v, max_split=cap)
             assert c <= cap and abi_ok(kp, c)
+
+
+def test_lm_head_token_blocks_take_whole_tiles_within_the_logit_budget():
+    from rus_amd import kernels as K
+
+    # V = 151936: three 256-token tiles of fp16 logits fit the 256 MiB budget
+    assert K.lm_head_block_tokens(151936) == 768
+    assert K.lm_head_block_tokens(151936) * 151936 * 2 <= K.LM_BLOCK_BUDGET
+    assert K.lm_head_block_tokens(10**9) == 256  # at least one tile
+    assert K.lm_head_token_blocks(0, 768) == []
+    assert K.lm_head_token_blocks(744, 768) == [(0, 744)]
+    assert K.lm_head_token_blocks(1100, 768) == [(0, 768), (768, 1100)]
+    assert K.lm_head_token_blocks(744, 256) == [(0, 256), (256, 512), (512, 744)]
+    for n in (1, 5, 255, 256, 257, 707, 1088, 2048, 5000):
+        for cap in (1, 256, 300, 768, 1792):
+            blocks = K.lm_head_token_blocks(n, cap)
+            # contiguous cover of [0, n); whole tiles but the last; no more tiles than n needs
+            assert blocks[0][0] == 0 and blocks[-1][1] == n
+            assert all(a[1] == b[0] for a, b in zip(blocks, blocks[1:]))
+            assert all((t1 - t0) % 256 == 0 for t0, t1 in blocks[:-1])
+            assert all(0 < t1 - t0 <= max(256, cap // 256 * 256) for t0, t1 in blocks)
+            assert sum(-(-(t1 - t0) // 256) for t0, t1 in blocks) == -(-n // 256)
+            assert len(blocks) == -(-(-(-n // 256)) // max(1, cap // 256))
