@@ -148,5 +148,104 @@ __device__ __forceinline__ void lora_down_rows4(const DownRows& a, int64_t t0, f
   }
 }
 
+// LDS that lora_down_rows4_staged needs beside `park` (kDownParkFloats floats): the block's
+// four x rows (fp16) and both branches' keep-bit words.
+__host__ __device__ constexpr int down_stage_bytes(int d) {
+  return kDownRows * d * 2 + 2 * kDownRows * ((d + 31) / 32) * 4;
+}
+
+// Copies x rows t0 .. t0 + 3 (zero past n_tok) into xs [kDownRows][d] and their keep-bit words
+// into bq / bv [kDownRows][words] (when the branches drop): 16-byte chunks, all loads of a
+// thread issued before its LDS stores. Every thread of the block must call it (it ends with a
+// barrier); x's rows must be visible to the whole block.
+__device__ __forceinline__ void stage_down_rows(const DownRows& a, int64_t t0, f16* xs,
+                                                uint32_t* bq, uint32_t* bv) {
+  const int per_row = a.d / 8;
+  const int chunks = kDownRows * per_row;
+  for (int i = threadIdx.x; i < chunks; i += blockDim.x) {
+    const int tok = i / per_row, c = (i - tok * per_row) * 8;
+    const int64_t t = t0 + tok;
+    const f16x8 v = t < a.n_tok ? ld8(a.x + t * a.sx + c) : zero8();
+    *reinterpret_cast<f16x8*>(xs + tok * a.d + c) = v;
+  }
+  if (a.bits_q != nullptr) {
+    const int nw = kDownRows * static_cast<int>(a.words);
+    for (int i = threadIdx.x; i < nw; i += blockDim.x) {
+      const int tok = i / static_cast<int>(a.words);
+      const int64_t t = t0 + tok, w = i - tok * a.words;
+      const bool live = t < a.n_tok;
+      const uint32_t q = live ? a.bits_q[t * a.words + w] : 0u;
+      const uint32_t v = live ? a.bits_v[t * a.words + w] : 0u;
+      bq[i] = q;
+      bv[i] = v;
+    }
+  }
+  __syncthreads();
+}
+
+// lora_down_rows4 with the block's x rows and keep bits already in LDS (stage_down_rows): the
+// same MFMA sequence on the same operands, so the same bits. Only the A fragments come from
+// global memory, U K steps of them issued together; x and the bits are read from LDS at each
+// step, so a batch holds 4 U registers per lane.
+template <int U>
+__device__ __forceinline__ void lora_down_rows4_staged(const DownRows& a, int64_t t0,
+                                                       const f16* xs, const uint32_t* bq,
+                                                       const uint32_t* bv, float* park) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, h = lane >> 5, col = lane & 31;
+  const bool is_q = col < a.r, is_v = col >= a.r && col < 2 * a.r;
+  const f16* arow = is_q ? a.aq + static_cast<int64_t>(col) * a.d
+                         : a.av + static_cast<int64_t>(is_v ? col - a.r : 0) * a.d;
+  const bool live = col < kDownRows && t0 + col < a.n_tok;
+  const f16* xrow = xs + (col < kDownRows ? col : 0) * a.d;
+  const int words = static_cast<int>(a.words);
+  const uint32_t* mq = bq + (col < kDownRows ? col : 0) * words;
+  const uint32_t* mv = bv + (col < kDownRows ? col : 0) * words;
+  const bool drop = a.bits_q != nullptr;  // uniform
+  const int per = a.d / 4;  // a multiple of 16
+  const int c_begin = wave * per;
+  f32x16 acc = f32x16{};
+  for (int s0 = 0; s0 < per; s0 += 16 * U) {
+    f16x8 af[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int c = c_begin + min(s0 + 16 * u, per - 16) + 8 * h;
+      af[u] = (is_q || is_v) ? ld8(arow + c) : zero8();
+    }
+    __builtin_amdgcn_sched_barrier(0);  // every A load of the batch is issued before any MFMA
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int c = c_begin + min(s0 + 16 * u, per - 16) + 8 * h;
+      // Steps past the wave's range add zero products, as in lora_down_rows4.
+      const f16x8 x = (live && s0 + 16 * u < per) ? ld8(xrow + c) : zero8();
+      if (drop) {
+        const uint32_t wq = live ? mq[c >> 5] : 0u, wv = live ? mv[c >> 5] : 0u;
+        const int sh = c & 31;
+        acc = mfma(is_q ? af[u] : zero8(), drop8(x, wq, sh, a.scale_q), acc);
+        acc = mfma(is_v ? af[u] : zero8(), drop8(x, wv, sh, a.scale_v), acc);
+      } else {
+        acc = mfma(af[u], x, acc);
+      }
+    }
+  }
+  if (col < kDownRows) {
+#pragma unroll
+    for (int j = 0; j < 16; ++j)
+      park[wave * 128 + col * 32 + 8 * (j >> 2) + 4 * h + (j & 3)] = acc[j];
+  }
+  __syncthreads();
+  if (threadIdx.x < 128) {
+    const int tok = threadIdx.x >> 5, row = threadIdx.x & 31;
+    const float s = ((park[threadIdx.x] + park[128 + threadIdx.x]) + park[256 + threadIdx.x]) +
+                    park[384 + threadIdx.x];
+    const int64_t tt = t0 + tok;
+    if (tt < a.n_tok && row < 2 * a.r) {
+      if (row < a.r)
+        a.mid_q[tt * a.r + row] = from_f32<f16>(s);
+      else
+        a.mid_v[tt * a.r + row - a.r] = from_f32<f16>(s);
+    }
+  }
+}
+
 }  // namespace
 }  // namespace rus

@@ -64,10 +64,15 @@ struct Nf4Args {
   int sb_shift;  // log2(super_blocksize): absmax blocks per absmax2 entry
 };
 
-// Per-block scale for the block holding `byte` (all bytes of a 4-byte unit share one block
-// because blocksize/2 >= 4 and segment starts are block aligned).
-__device__ __forceinline__ float block_scale(const Nf4Args& a, uint32_t byte,
-                                             const float* __restrict__ s_code2) {
+// The global inputs of the scale of the absmax block holding `byte`: its absmax code, its
+// absmax2 entry and its segment's offset (all bytes of a 4-byte unit share one block because
+// blocksize/2 >= 4 and segment starts are block aligned).
+struct ScaleIn {
+  uint32_t code;
+  float a2, off;
+};
+
+__device__ __forceinline__ ScaleIn scale_inputs(const Nf4Args& a, uint32_t byte) {
   const uint32_t blk = byte >> a.hb_shift;
   uint32_t sup;
   float off;
@@ -81,9 +86,18 @@ __device__ __forceinline__ float block_scale(const Nf4Args& a, uint32_t byte,
     sup = blk >> a.sb_shift;
     off = a.off0;
   }
-  const float c = s_code2[a.absmax[blk]];
-  const float s = c * a.absmax2[sup];  // rounded product (no contraction in this file)
-  return s + off;
+  return ScaleIn{a.absmax[blk], a.absmax2[sup], off};
+}
+
+// code2[absmax] * absmax2 + offset, two roundings (no contraction in this file).
+__device__ __forceinline__ float finish_scale(const ScaleIn& in, const float* __restrict__ s_code2) {
+  const float s = s_code2[in.code] * in.a2;
+  return s + in.off;
+}
+
+__device__ __forceinline__ float block_scale(const Nf4Args& a, uint32_t byte,
+                                             const float* __restrict__ s_code2) {
+  return finish_scale(scale_inputs(a, byte), s_code2);
 }
 
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
@@ -173,7 +187,9 @@ __device__ __forceinline__ void dequant_block_tab(const Nf4Args& a, uint32_t blk
   static_assert(UNROLL == kUnrollTab, "table sized for kUnrollTab units per thread");
   const uint32_t t = threadIdx.x;
   const uint32_t base = blk * (kThreads * UNROLL) + t;
-  // 1. The block's packed words, issued before the table set-up so that their latency overlaps it.
+  // 1. Every global read of the block issued at once: its packed words, the code2 table and the
+  // absmax / absmax2 entries of its first kThreads absmax blocks (one per thread), so one
+  // memory latency precedes the decode.
   uint32_t p[UNROLL];
 #pragma unroll
   for (int u = 0; u < UNROLL; ++u) {
@@ -187,11 +203,14 @@ __device__ __forceinline__ void dequant_block_tab(const Nf4Args& a, uint32_t blk
       blk == nblk - 1 ? a.n_bytes : min(byte0 + kThreads * UNROLL * 4u, a.n_bytes);
   const uint32_t ab0 = byte0 >> a.hb_shift;
   const uint32_t n_ab = ((byte_end - 1u) >> a.hb_shift) - ab0 + 1u;
+  ScaleIn mine{0u, 0.0f, 0.0f};
+  if (t < n_ab) mine = scale_inputs(a, (ab0 + t) << a.hb_shift);
   // 2. Lookup tables, then one scale per absmax block of the block's range.
   s_code2[t] = a.code2[t];
   if (t < 16) s_nf4[t] = kNF4[t];
   __syncthreads();
-  for (uint32_t i = t; i < n_ab; i += kThreads)
+  if (t < n_ab) s_scale[t] = finish_scale(mine, s_code2);
+  for (uint32_t i = t + kThreads; i < n_ab; i += kThreads)  // blocksize 32 only: 257 blocks
     s_scale[i] = block_scale(a, (ab0 + i) << a.hb_shift, s_code2);
   __syncthreads();
   // 3. The 16 products per absmax block.
@@ -302,18 +321,26 @@ struct NormSide {
   DownRows down;
 };
 
-static_assert((kTabMaxBlocks + 1) * 16 >= kDownParkFloats, "the LoRA-down sums fit in s_tab");
+constexpr int kTabFloats = (kTabMaxBlocks + 1) * 16;
+// The LoRA-down variant's s_tab also holds the down's wave sums and its staged rows (d <= 2048,
+// the carried norm's limit).
+constexpr int kTabFloatsDown = kDownParkFloats + down_stage_bytes(2048) / 4 > kTabFloats
+                                   ? kDownParkFloats + down_stage_bytes(2048) / 4
+                                   : kTabFloats;
+constexpr int kDownStageU = 2;  // A fragments of 2 K steps in flight per lane
 
-// DOWN: the forward norm's blocks then form the LoRA-down of their rows (lora_rows.h). Its MFMA
-// code needs registers the decode does not, so it is a kernel of its own: the plain variant keeps
-// the decode at 8 waves per SIMD; the LoRA-down variant runs at 6, its K steps loaded one at a
-// time so that the decode blocks keep their registers.
+// DOWN: the forward norm's blocks then form the LoRA-down of their rows (lora_rows.h): the four
+// rows and their keep bits are staged in LDS by one coalesced pass, so each wave's K loop waits
+// on global memory once per kDownStageU steps (for the A fragments) instead of at every step.
+// Its MFMA code needs registers the decode does not, so it is a kernel of its own (80 VGPRs,
+// 6 waves per SIMD; the plain variant keeps the decode at 8). Batches of 4 or 6 steps hold
+// 88-96 VGPRs (5 waves) and ran 0.5-0.9 us slower per launch at 744 tokens.
 template <int UNROLL, bool BWD, typename W, int NIT, bool DOWN>
 __device__ __forceinline__ void dequant_norm_body(const Nf4Multi& m, const NormSide& s) {
   __shared__ float s_code2[256];
   __shared__ float s_nf4[16];
   __shared__ float s_scale[kTabMaxBlocks + 1];
-  __shared__ float s_tab[(kTabMaxBlocks + 1) * 16];
+  __shared__ __attribute__((aligned(16))) float s_tab[DOWN ? kTabFloatsDown : kTabFloats];
   if (blockIdx.x < s.blocks) {
     const int row = blockIdx.x * (kThreads / kWave) + threadIdx.x / kWave;
     const W* w = static_cast<const W*>(s.w);
@@ -333,7 +360,12 @@ __device__ __forceinline__ void dequant_norm_body(const Nf4Multi& m, const NormS
                                             s.n_rows, s.n_cols, s.stride, s.eps);
       if constexpr (DOWN) {  // the block's four output rows are its LoRA-down tokens
         __syncthreads();  // every wave's row is stored
-        lora_down_rows4<1>(s.down, static_cast<int64_t>(blockIdx.x) * kDownRows, s_tab);
+        const int64_t t0 = static_cast<int64_t>(blockIdx.x) * kDownRows;
+        f16* xs = reinterpret_cast<f16*>(s_tab + kDownParkFloats);
+        uint32_t* bq = reinterpret_cast<uint32_t*>(xs + kDownRows * s.down.d);
+        uint32_t* bv = bq + kDownRows * s.down.words;
+        stage_down_rows(s.down, t0, xs, bq, bv);
+        lora_down_rows4_staged<kDownStageU>(s.down, t0, xs, bq, bv, s_tab);
       }
     }
     return;
@@ -358,7 +390,7 @@ __global__ __launch_bounds__(kThreads) void nf4_dequant_norm_kernel(Nf4Multi m, 
 }
 
 template <int UNROLL, typename W, int NIT>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(5))) void
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(6))) void
 nf4_dequant_norm_down_kernel(Nf4Multi m, NormSide s) {
   dequant_norm_body<UNROLL, false, W, NIT, true>(m, s);
 }
