@@ -166,10 +166,13 @@ class GraphedTrainStep:
         final, st = stack_forward(eng, h, img.pos, None, self.training, lora16, seed, vm=img.vm,
                                   save=not eng.recompute)
         head = eng.host_head
+        v_chunk = eng.lm_v_chunk
+        if v_chunk is not None and v_chunk < 0:  # chunk chosen for the bucket's token count
+            v_chunk = K.lm_head_chunk_cols(final.shape[0], head.gpu_weight.shape[0])
         nll, _lse, ent, amax, _denom, d_final, loss = K.lm_head_ce(
             final, head.gpu_weight, img.labels, num_items_in_batch=self.num_items,
             need_grad=True, weight_t=head.gpu_weight_t, dh_scale=1.0 / PRESCALE_GRAD,
-            dh_dtype=final.dtype, block_tokens=eng.lm_block_tokens)
+            dh_dtype=final.dtype, block_tokens=eng.lm_block_tokens, v_chunk=v_chunk)
         del final
         stack_backward(eng, st, d_final, self.grad16)
         self.grad32.copy_(self.grad16)

@@ -2003,13 +2003,19 @@ def lm_head_block_tokens(n_vocab: int, budget: int = LM_BLOCK_BUDGET) -> int:
 
 
 def lm_head_token_blocks(n_tok: int, max_block: int = LM_TILE) -> list[tuple[int, int]]:
-    """Token ranges [t0, t1): the ceil(n_tok / 256) MFMA token tiles spread evenly over the fewest
-    blocks of at most ``max_block`` tokens (rounded down to whole tiles, at least one), every block
-    whole tiles but the last, so no block adds a partly filled tile."""
+    """Token ranges [t0, t1) of the token-blocked head. No block holds every token of a batch of
+    two or more, so the logits of all N tokens never exist at once: a batch of more than one
+    256-token MFMA tile goes in at least two blocks of whole tiles (the last one partial), its
+    tiles spread evenly over the fewest blocks of at most ``max_block`` tokens (rounded down to
+    whole tiles, at least one) — no block adds a partly filled tile; a batch within one tile
+    goes in two halves."""
     if n_tok <= 0:
         return []
-    max_tiles = max(1, max_block // LM_TILE)
     tiles = -(-n_tok // LM_TILE)
+    if tiles == 1:
+        half = (n_tok + 1) // 2
+        return [(0, half), (half, n_tok)] if n_tok > 1 else [(0, n_tok)]
+    max_tiles = max(1, min(max_block // LM_TILE, tiles - 1))
     nb = -(-tiles // max_tiles)
     base, extra = divmod(tiles, nb)
     out, t = [], 0
@@ -2050,9 +2056,10 @@ def lm_head_ce(hidden: torch.Tensor, weight: torch.Tensor, labels: torch.Tensor,
     denom (device scalar) and dh the hidden gradient of loss times 2^16, scaled by ``dh_scale``
     and stored as ``dh_dtype`` (None without need_grad).
 
-    With the gradient, the tokens go in blocks of whole 256-token MFMA tiles, at most
-    ``block_tokens`` each (default: the tiles whose fp16 logits fit 256 MiB, 768 tokens at
-    V = 151936). For each block one GEMM over the whole vocabulary stores its fp16 logits in a
+    With the gradient, the tokens go in blocks (``lm_head_token_blocks``: whole 256-token MFMA
+    tiles, at least two blocks for two or more tokens, at most ``block_tokens`` each; default:
+    the tiles whose fp16 logits fit 256 MiB, 768 tokens at V = 151936; 744 tokens go as 512 +
+    232). For each block one GEMM over the whole vocabulary stores its fp16 logits in a
     [block, V] buffer; one kernel per token row forms the statistics and turns the row into the
     reference's fp16 gradient G = fp16((softmax - onehot) 2^16 / denom) in place (the denominator
     is known up front); and a split-K GEMM G . W writes the block's dH partials, summed once. W

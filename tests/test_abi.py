@@ -254,16 +254,23 @@ def test_lm_head_token_blocks_take_whole_tiles_within_the_logit_budget():
     assert K.lm_head_block_tokens(151936) * 151936 * 2 <= K.LM_BLOCK_BUDGET
     assert K.lm_head_block_tokens(10**9) == 256  # at least one tile
     assert K.lm_head_token_blocks(0, 768) == []
-    assert K.lm_head_token_blocks(744, 768) == [(0, 744)]
+    assert K.lm_head_token_blocks(1, 768) == [(0, 1)]
+    assert K.lm_head_token_blocks(5, 768) == [(0, 3), (3, 5)]  # within one tile: two halves
+    assert K.lm_head_token_blocks(744, 768) == [(0, 512), (512, 744)]  # never all N at once
     assert K.lm_head_token_blocks(1100, 768) == [(0, 768), (768, 1100)]
     assert K.lm_head_token_blocks(744, 256) == [(0, 256), (256, 512), (512, 744)]
-    for n in (1, 5, 255, 256, 257, 707, 1088, 2048, 5000):
-        for cap in (1, 256, 300, 768, 1792):
+    for n in (2, 5, 255, 256, 257, 707, 1088, 2048, 5000):
+        tiles = -(-n // 256)
+        for cap in (1, 256, 300, 768, 1792, 10**6):
             blocks = K.lm_head_token_blocks(n, cap)
-            # contiguous cover of [0, n); whole tiles but the last; no more tiles than n needs
-            assert blocks[0][0] == 0 and blocks[-1][1] == n
-            assert all(a[1] == b[0] for a, b in zip(blocks, blocks[1:]))
+            # contiguous cover of [0, n), at least two blocks (no block holds every token)
+            assert blocks[0][0] == 0 and blocks[-1][1] == n and len(blocks) >= 2
+            assert all(a[1] == b[0] and a[0] < a[1] for a, b in zip(blocks, blocks[1:]))
+            if tiles == 1:
+                continue
+            # whole tiles but the last; no more tiles than n needs; fewest blocks within the cap
+            max_tiles = max(1, min(cap // 256, tiles - 1))
             assert all((t1 - t0) % 256 == 0 for t0, t1 in blocks[:-1])
-            assert all(0 < t1 - t0 <= max(256, cap // 256 * 256) for t0, t1 in blocks)
-            assert sum(-(-(t1 - t0) // 256) for t0, t1 in blocks) == -(-n // 256)
-            assert len(blocks) == -(-(-(-n // 256)) // max(1, cap // 256))
+            assert all(0 < t1 - t0 <= max_tiles * 256 for t0, t1 in blocks)
+            assert sum(-(-(t1 - t0) // 256) for t0, t1 in blocks) == tiles
+            assert len(blocks) == -(-tiles // max_tiles)

@@ -115,7 +115,8 @@ def test_lmhead_baseline_config2_sampled_tokens():
 
 
 def test_lmhead_token_block_size_leaves_the_statistics_unchanged():
-    # 1100 tokens in five 256-token blocks and in one block (the default for a small vocabulary):
+    # 1100 tokens in five 256-token blocks and in two (768 + 332, the default for a small
+    # vocabulary, which allows any block size but never one block for all tokens):
     # each token's logits, statistics and argmax are formed from its own row alone, so they are
     # bit-identical; the hidden gradient's split-K sum order follows the block's split count, so
     # it agrees within rtol 1e-3 and both match the oracle on a sample of tokens.
@@ -125,15 +126,15 @@ def test_lmhead_token_block_size_leaves_the_statistics_unchanged():
     w = (torch.randn(V, D, generator=g) * 0.05).half()
     lab = torch.randint(0, V, (N,), generator=g)
     lab[torch.rand(N, generator=g) < 0.1] = -100
-    assert len(K.lm_head_token_blocks(N, K.lm_head_block_tokens(V))) == 1
-    one = K.lm_head_ce(h.to(DEV), w.to(DEV), lab.to(DEV))
+    assert K.lm_head_token_blocks(N, K.lm_head_block_tokens(V)) == [(0, 768), (768, N)]
+    two = K.lm_head_ce(h.to(DEV), w.to(DEV), lab.to(DEV))
     five = K.lm_head_ce(h.to(DEV), w.to(DEV), lab.to(DEV), block_tokens=256)
     torch.cuda.synchronize()
     for i in (0, 1, 2, 3, 4, 6):
-        assert torch.equal(one[i].cpu(), five[i].cpu()), i
-    assert torch.allclose(one[5].cpu(), five[5].cpu(), rtol=1e-3, atol=1e-3 * one[5].abs().max().item())
+        assert torch.equal(two[i].cpu(), five[i].cpu()), i
+    assert torch.allclose(two[5].cpu(), five[5].cpu(), rtol=1e-3, atol=1e-3 * two[5].abs().max().item())
     rows = torch.cat([torch.arange(0, 20), torch.arange(760, 780), torch.arange(1080, 1100)])
-    _check_against_oracle(h, w, lab, one, rows=rows, denom=float(one[4].item()))
+    _check_against_oracle(h, w, lab, two, rows=rows, denom=float(two[4].item()))
     _check_against_oracle(h, w, lab, five, rows=rows, denom=float(five[4].item()))
 
 
