@@ -78,16 +78,13 @@ def train_step(engine, opt, batch, graph=None):
 
 
 def flat_adamw(engine):
-    """AdamW (lr 2e-4) over the engine's flat LoRA parameter (every factor is a view of it): one
-    fused update launch per step instead of a foreach pass over 112 tensors; elementwise, so the
-    same values. Returns (optimizer, implementation)."""
-    import torch
+    """AdamW (lr 2e-4, torch.optim.AdamW's defaults otherwise) over the engine's flat LoRA
+    parameter (every factor is a view of it): one rus_adamw_step launch per step
+    (rus_amd.optim.FlatAdamW) instead of a foreach pass over 112 tensors; elementwise, so the
+    same update. Returns (optimizer, implementation)."""
+    from rus_amd.optim import FlatAdamW
 
-    p = engine.flat_lora_parameter()
-    try:
-        return torch.optim.AdamW([p], lr=2e-4, fused=True), "fused"
-    except (RuntimeError, ValueError):
-        return torch.optim.AdamW([p], lr=2e-4, foreach=True), "foreach"
+    return FlatAdamW([engine.flat_lora_parameter()], lr=2e-4), "rus_adamw_step"
 
 
 def timed_run(engine, opt, batches, steps, warmup, kernel_filter=None, graph=None):

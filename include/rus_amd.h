@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define RUS_ABI_VERSION 14
+#define RUS_ABI_VERSION 15
 
 #define RUS_DTYPE_F16 0
 #define RUS_DTYPE_F32 1
@@ -728,6 +728,21 @@ int rus_attn_varlen_bwd_parts(const void* q, const void* k, const void* v, const
                               int32_t n_seq, int64_t n_tokens, int32_t max_blocks, int32_t h_q,
                               int32_t h_kv, int32_t head_dim, float scale, void* dq,
                               float* workspace, void* stream);
+
+/*
+ * One AdamW step (step number step >= 1) over n fp32 values: param, exp_avg and exp_avg_sq
+ * updated in place from grad with torch.optim.AdamW's update (amsgrad and maximize off), in the
+ * order of torch's single- and multi-tensor paths: param *= 1 - lr weight_decay; exp_avg =
+ * lerp(exp_avg, grad, 1 - beta1); exp_avg_sq = exp_avg_sq beta2 + (1 - beta2) grad grad;
+ * param += -(lr / bc1) exp_avg / (sqrt(exp_avg_sq) / sqrt(bc2) + eps), bc1 = 1 - beta1^step,
+ * bc2 = 1 - beta2^step. The scalars are formed in double and rounded once to fp32. Buffers
+ * 16-byte aligned, not overlapping. One launch.
+ * Replaces: the trainer's torch.optim.AdamW step over the LoRA factors (HF "adamw_torch";
+ * reference harness/_train.py:30 forwards the trainer's optim settings).
+ */
+int rus_adamw_step(float* param, const float* grad, float* exp_avg, float* exp_avg_sq, int64_t n,
+                   double lr, double beta1, double beta2, double eps, double weight_decay,
+                   int64_t step, void* stream);
 
 #ifdef __cplusplus
 }

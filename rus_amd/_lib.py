@@ -11,7 +11,7 @@ import threading
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "librus_amd.so"
-ABI_VERSION = 14
+ABI_VERSION = 15
 
 DTYPE_F16 = 0
 DTYPE_F32 = 1
@@ -20,6 +20,7 @@ _vp = ctypes.c_void_p
 _i64 = ctypes.c_int64
 _i32 = ctypes.c_int32
 _f32 = ctypes.c_float
+_f64 = ctypes.c_double
 _u64 = ctypes.c_uint64
 
 class Nf4Job(ctypes.Structure):
@@ -69,6 +70,7 @@ SIGNATURES: dict[str, list] = {
                         _i64, _i32, _i32, _vp, _vp],
     "rus_nf4_dequant_multi": [ctypes.POINTER(Nf4Job), _i32, _vp, _i32, _i32, _vp],
     "rus_lora_down_rows": [ctypes.POINTER(LoraRows), _vp],
+    "rus_adamw_step": [_vp, _vp, _vp, _vp, _i64, _f64, _f64, _f64, _f64, _f64, _i64, _vp],
     "rus_nf4_dequant_multi_norm": [ctypes.POINTER(Nf4Job), _i32, _vp, _i32, _i32,
                                    ctypes.POINTER(NormSide), ctypes.POINTER(LoraRows), _vp],
     "rus_nf4_gemm_plan": [_i64, _i64, _i64, _i32, ctypes.POINTER(_i32), ctypes.POINTER(_i64),

@@ -18,6 +18,7 @@ from . import _lib
 from ._lib import DTYPE_F16, DTYPE_F32
 
 __all__ = [
+    "adamw_step",
     "dequant_nf4_tensor",
     "dequant_nf4_segments",
     "NF4Operand",
@@ -2132,3 +2133,28 @@ def lm_head_ce(hidden: torch.Tensor, weight: torch.Tensor, labels: torch.Tensor,
         lm_head_dh_reduce(dparts, dh_scale, dh_dtype, out=dh[t0:t1])
     loss, _ = lm_head_ce_loss(nll, lab, num_items_in_batch)
     return nll, lse, ent, amax, denom, dh, loss
+
+
+# ---------------------------------------------------------------------------------------------
+# AdamW over a flat fp32 buffer (the trainer's torch.optim.AdamW, HF "adamw_torch";
+# reference harness/_train.py:30)
+# ---------------------------------------------------------------------------------------------
+
+
+def adamw_step(param: torch.Tensor, grad: torch.Tensor, exp_avg: torch.Tensor,
+               exp_avg_sq: torch.Tensor, lr: float, beta1: float, beta2: float, eps: float,
+               weight_decay: float, step: int) -> None:
+    """One AdamW step (torch.optim.AdamW's update, amsgrad and maximize off) of step number
+    ``step`` (>= 1) over contiguous fp32 device tensors of one size, in place, one launch."""
+    fn = "adamw_step"
+    _require_device(fn, param, grad, exp_avg, exp_avg_sq)
+    n = param.numel()
+    for name, t in (("param", param), ("grad", grad), ("exp_avg", exp_avg),
+                    ("exp_avg_sq", exp_avg_sq)):
+        if t.dtype != torch.float32 or not t.is_contiguous() or t.numel() != n:
+            raise ValueError(f"{fn}: {name} must be contiguous float32 with {n} values")
+    if int(step) < 1:
+        raise ValueError(f"{fn}: step must be >= 1")
+    _launch("adamw", 28 * n, 0, "rus_adamw_step", param.data_ptr(), grad.data_ptr(),
+            exp_avg.data_ptr(), exp_avg_sq.data_ptr(), n, float(lr), float(beta1), float(beta2),
+            float(eps), float(weight_decay), int(step), _stream(param))

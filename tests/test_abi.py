@@ -117,6 +117,15 @@ def test_header_compiles_as_c():
          "null pointer"),
         ("rus_attn_varlen_bwd_parts", (16, 16, 16, 16, 16, 16, 16, 1, 32, 2, 12, 2, 128, 0.1, 16,
                                        None, None), "null or misaligned"),
+        # AdamW: a missing moment, a misaligned buffer, a beta of 1, a negative size, step 0
+        ("rus_adamw_step", (16, 16, 16, None, 5, 1e-3, 0.9, 0.999, 1e-8, 0.01, 1, None),
+         "null pointer"),
+        ("rus_adamw_step", (16, 8, 16, 16, 5, 1e-3, 0.9, 0.999, 1e-8, 0.01, 1, None),
+         "16-byte aligned"),
+        ("rus_adamw_step", (16, 16, 16, 16, 5, 1e-3, 1.0, 0.999, 1e-8, 0.01, 1, None), "betas"),
+        ("rus_adamw_step", (16, 16, 16, 16, -1, 1e-3, 0.9, 0.999, 1e-8, 0.01, 1, None),
+         "bad size"),
+        ("rus_adamw_step", (16, 16, 16, 16, 5, 1e-3, 0.9, 0.999, 1e-8, 0.01, 0, None), "step"),
     ],
 )
 def test_invalid_arguments_are_rejected_on_the_host(name, args, msg):
