@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define RUS_ABI_VERSION 15
+#define RUS_ABI_VERSION 16
 
 #define RUS_DTYPE_F16 0
 #define RUS_DTYPE_F32 1
@@ -728,6 +728,20 @@ int rus_attn_varlen_bwd_parts(const void* q, const void* k, const void* v, const
                               int32_t n_seq, int64_t n_tokens, int32_t max_blocks, int32_t h_q,
                               int32_t h_kv, int32_t head_dim, float scale, void* dq,
                               float* workspace, void* stream);
+
+/*
+ * A step's fp16 LoRA factors in both layouts, one launch. flat: fp32, n_layers x [segment 0 |
+ * ... | segment n_seg-1] (n_seg <= 4), segment j row-major [seg_rows[j], seg_cols[j]]
+ * (host arrays). out: fp16, the same layout (each value rounded to nearest even once); out_t
+ * (optional): fp16, region j = [n_layers, seg_cols[j], seg_rows[j]], each layer's segment
+ * transposed, regions back to back in segment order (region j starts at n_layers times the
+ * per-layer offset of segment j).
+ * Replaces: the per-layer fp16 casts of the LoRA factors (solution/ops.py:776, 778, and the
+ * backward's q_B_fp16 / q_A_fp16 operands, ops.py:979-987); out_t is the rank-major layout the
+ * fused LoRA backward kernels read.
+ */
+int rus_lora_cast_t(const float* flat, int64_t n_layers, int32_t n_seg, const int64_t* seg_rows,
+                    const int64_t* seg_cols, void* out, void* out_t, void* stream);
 
 /*
  * One AdamW step (step number step >= 1) over n fp32 values: param, exp_avg and exp_avg_sq

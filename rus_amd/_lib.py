@@ -11,7 +11,7 @@ import threading
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "librus_amd.so"
-ABI_VERSION = 15
+ABI_VERSION = 16
 
 DTYPE_F16 = 0
 DTYPE_F32 = 1
@@ -70,6 +70,8 @@ SIGNATURES: dict[str, list] = {
                         _i64, _i32, _i32, _vp, _vp],
     "rus_nf4_dequant_multi": [ctypes.POINTER(Nf4Job), _i32, _vp, _i32, _i32, _vp],
     "rus_lora_down_rows": [ctypes.POINTER(LoraRows), _vp],
+    "rus_lora_cast_t": [_vp, _i64, _i32, ctypes.POINTER(_i64), ctypes.POINTER(_i64), _vp, _vp,
+                        _vp],
     "rus_adamw_step": [_vp, _vp, _vp, _vp, _i64, _f64, _f64, _f64, _f64, _f64, _i64, _vp],
     "rus_nf4_dequant_multi_norm": [ctypes.POINTER(Nf4Job), _i32, _vp, _i32, _i32,
                                    ctypes.POINTER(NormSide), ctypes.POINTER(LoraRows), _vp],

@@ -972,3 +972,80 @@ extern "C" int rus_lora_down_rows(const rus_lora_rows* q, void* stream) {
                      a);
   return check_launch(fn);
 }
+
+// ---------------------------------------------------------------------------------------------
+// The step's fp16 LoRA factors in both layouts, one launch: the flat fp32 parameter buffer
+// (n_layers x [segment 0 | segment 1 | ...], segment s row-major [rows_s, cols_s]) cast to fp16
+// in the same layout, and each segment transposed into out_t region s = [n_layers, cols_s,
+// rows_s] (regions back to back). Replaces the reference's per-layer fp16 casts of the factors
+// (solution/ops.py:776, 778, and the backward's q_B_fp16 / q_A_fp16, ops.py:979-987); the
+// transposed copies are the rank-major layout the fused LoRA backward kernels read.
+// ---------------------------------------------------------------------------------------------
+
+namespace rus {
+namespace {
+
+constexpr int kCastSegs = 4;
+
+struct CastSegs {
+  int64_t off[kCastSegs + 1];  // segment starts within a layer (off[n_seg] = per-layer size)
+  int64_t base_t[kCastSegs];   // start of each segment's region in out_t
+  int64_t cols[kCastSegs];
+  int64_t rows[kCastSegs];
+  int n_seg;
+};
+
+__global__ __launch_bounds__(256) void lora_cast_t_kernel(const float* __restrict__ flat,
+                                                          int64_t n, CastSegs s,
+                                                          f16* __restrict__ out,
+                                                          f16* __restrict__ out_t) {
+  const int64_t e = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (e >= n) return;
+  const f16 h = from_f32<f16>(flat[e]);
+  out[e] = h;
+  if (out_t == nullptr) return;
+  const int64_t per = s.off[s.n_seg];
+  const int64_t l = e / per, rem = e - l * per;
+  int j = 0;
+#pragma unroll
+  for (int k = 1; k < kCastSegs; ++k) j += (k < s.n_seg && rem >= s.off[k]) ? 1 : 0;
+  const int64_t in_seg = rem - s.off[j];
+  const int64_t r = in_seg / s.cols[j], c = in_seg - r * s.cols[j];
+  out_t[s.base_t[j] + l * (s.off[j + 1] - s.off[j]) + c * s.rows[j] + r] = h;
+}
+
+}  // namespace
+}  // namespace rus
+
+extern "C" int rus_lora_cast_t(const float* flat, int64_t n_layers, int32_t n_seg,
+                               const int64_t* seg_rows, const int64_t* seg_cols, void* out,
+                               void* out_t, void* stream) {
+  using namespace rus;
+  const char* fn = "rus_lora_cast_t";
+  if (n_seg < 1 || n_seg > kCastSegs || n_layers < 0 || !seg_rows || !seg_cols)
+    return fail(RUS_ERR_INVALID, "%s: n_seg=%d outside [1, %d] or bad shape arguments", fn,
+                n_seg, kCastSegs);
+  if (!flat || !out) return fail(RUS_ERR_INVALID, "%s: null pointer argument", fn);
+  CastSegs s{};
+  s.n_seg = n_seg;
+  int64_t per = 0;
+  for (int j = 0; j < n_seg; ++j) {
+    if (seg_rows[j] <= 0 || seg_cols[j] <= 0 || seg_rows[j] >= (int64_t(1) << 31) ||
+        seg_cols[j] >= (int64_t(1) << 31))
+      return fail(RUS_ERR_INVALID, "%s: segment %d has shape %lld x %lld", fn, j,
+                  (long long)seg_rows[j], (long long)seg_cols[j]);
+    s.off[j] = per;
+    s.rows[j] = seg_rows[j];
+    s.cols[j] = seg_cols[j];
+    per += seg_rows[j] * seg_cols[j];
+  }
+  s.off[n_seg] = per;
+  for (int j = 0; j < n_seg; ++j) s.base_t[j] = n_layers * s.off[j];
+  const int64_t n = n_layers * per;
+  if (n >= (int64_t(1) << 40)) return fail(RUS_ERR_INVALID, "%s: %lld values", fn, (long long)n);
+  if (n == 0) return RUS_OK;
+  hipLaunchKernelGGL(lora_cast_t_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256),
+                     0, static_cast<hipStream_t>(stream), flat, n, s, static_cast<f16*>(out),
+                     static_cast<f16*>(out_t));
+  return check_launch(fn);
+}

@@ -19,6 +19,7 @@ from ._lib import DTYPE_F16, DTYPE_F32
 
 __all__ = [
     "adamw_step",
+    "lora_cast_t",
     "dequant_nf4_tensor",
     "dequant_nf4_segments",
     "NF4Operand",
@@ -2158,3 +2159,26 @@ def adamw_step(param: torch.Tensor, grad: torch.Tensor, exp_avg: torch.Tensor,
     _launch("adamw", 28 * n, 0, "rus_adamw_step", param.data_ptr(), grad.data_ptr(),
             exp_avg.data_ptr(), exp_avg_sq.data_ptr(), n, float(lr), float(beta1), float(beta2),
             float(eps), float(weight_decay), int(step), _stream(param))
+
+
+def lora_cast_t(flat: torch.Tensor, n_layers: int, shapes, out: torch.Tensor,
+                out_t: torch.Tensor | None = None) -> None:
+    """One launch: ``out`` = fp16(flat) (same layout: n_layers x the segments of ``shapes``, each
+    row-major [rows, cols]) and, when given, ``out_t`` = every layer's segments transposed,
+    region j = [n_layers, cols_j, rows_j] (regions back to back in segment order)."""
+    fn = "lora_cast_t"
+    _require_device(fn, flat, out, out_t)
+    shapes = [(int(r), int(c)) for r, c in shapes]
+    if not 1 <= len(shapes) <= 4:
+        raise ValueError(f"{fn}: 1 to 4 segments per layer")
+    n = int(n_layers) * sum(r * c for r, c in shapes)
+    if flat.dtype != torch.float32 or not flat.is_contiguous() or flat.numel() != n:
+        raise ValueError(f"{fn}: flat must be contiguous float32 with {n} values")
+    for name, t in (("out", out), ("out_t", out_t)):
+        if t is not None and (t.dtype != torch.float16 or not t.is_contiguous() or t.numel() != n):
+            raise ValueError(f"{fn}: {name} must be contiguous float16 with {n} values")
+    rows = (ctypes.c_int64 * len(shapes))(*[r for r, _ in shapes])
+    cols = (ctypes.c_int64 * len(shapes))(*[c for _, c in shapes])
+    _launch("lora_cast_t", n * (4 + 2 + (2 if out_t is not None else 0)), 0, "rus_lora_cast_t",
+            flat.data_ptr(), int(n_layers), len(shapes), rows, cols, out.data_ptr(), _ptr(out_t),
+            _stream(flat))

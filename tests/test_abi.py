@@ -3,6 +3,8 @@ include/rus_amd.h declares, and rejects invalid arguments before touching the GP
 
 from __future__ import annotations
 
+import ctypes
+
 import re
 import subprocess
 from pathlib import Path
@@ -117,6 +119,12 @@ def test_header_compiles_as_c():
          "null pointer"),
         ("rus_attn_varlen_bwd_parts", (16, 16, 16, 16, 16, 16, 16, 1, 32, 2, 12, 2, 128, 0.1, 16,
                                        None, None), "null or misaligned"),
+        # LoRA cast: five segments, a null input, an empty segment
+        ("rus_lora_cast_t", (16, 2, 5, None, None, 16, None, None), "n_seg"),
+        ("rus_lora_cast_t", (None, 2, 1, (ctypes.c_int64 * 1)(4), (ctypes.c_int64 * 1)(4), 16,
+                             None, None), "null pointer"),
+        ("rus_lora_cast_t", (16, 2, 1, (ctypes.c_int64 * 1)(0), (ctypes.c_int64 * 1)(4), 16,
+                             None, None), "segment 0"),
         # AdamW: a missing moment, a misaligned buffer, a beta of 1, a negative size, step 0
         ("rus_adamw_step", (16, 16, 16, None, 5, 1e-3, 0.9, 0.999, 1e-8, 0.01, 1, None),
          "null pointer"),

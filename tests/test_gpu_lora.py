@@ -331,3 +331,48 @@ def test_dequant_launch_carries_norm_and_lora_down_bitwise(drop, n):
     pend2.run()
     torch.cuda.synchronize()
     assert torch.equal(y2, y0) and all(torch.equal(a, b) for a, b in zip(m2, m0))
+
+
+@pytest.mark.parametrize("n_layers,shapes", [(3, [(16, 1536), (1536, 16), (16, 1536), (256, 16)]),
+                                             (2, [(3, 5), (7, 2)]), (1, [(1, 1)])])
+def test_lora_cast_t_matches_torch_cast_and_transposes(n_layers, shapes):
+    # rus_lora_cast_t: fp16 of the flat fp32 factors (torch's round-to-nearest-even cast,
+    # bitwise) and every layer's segments transposed into [n_layers, cols, rows] regions.
+    n = n_layers * sum(r * c for r, c in shapes)
+    flat = torch.randn(n, device=DEV) * 3.0
+    flat[::97] = 65520.0  # rounds to inf in fp16, as torch's cast does
+    out = torch.empty(n, dtype=torch.float16, device=DEV)
+    out_t = torch.empty_like(out)
+    K.lora_cast_t(flat, n_layers, shapes, out, out_t)
+    only = torch.empty_like(out)
+    K.lora_cast_t(flat, n_layers, shapes, only)
+    torch.cuda.synchronize()
+    want = flat.half()
+    assert torch.equal(out, want) and torch.equal(only, want)
+    per = sum(r * c for r, c in shapes)
+    off = 0
+    for r, c in shapes:
+        seg = want.view(n_layers, per)[:, off: off + r * c].reshape(n_layers, r, c)
+        region = out_t[n_layers * off: n_layers * (off + r * c)].view(n_layers, c, r)
+        assert torch.equal(region, seg.transpose(1, 2)), (r, c)
+        off += r * c
+
+
+def test_engine_lora_fp16_t_is_the_cast_launch_copy():
+    # The engine's step casts: lora_fp16_t returns the copies written beside lora_fp16's
+    # (no further launch), equal to the transposes of the fp16 factors.
+    from rus_amd import model as M
+    from rus_amd.ops import Qwen2FusedEngine
+
+    cfg = M.Qwen2Config(hidden_size=512, intermediate_size=256, num_hidden_layers=2,
+                        num_attention_heads=4, num_key_value_heads=2, vocab_size=1000, lora_r=16)
+    model = M.build_random_qlora_qwen2(cfg, DEV, seed=1)
+    eng = Qwen2FusedEngine(model, DEV, resident_weights=True)
+    lora16 = eng.lora_fp16()
+    t = eng.lora_fp16_t(lora16)
+    for p, a, b in zip(eng.lora_params, lora16, t):
+        assert torch.equal(a, p.detach().half()) and torch.equal(b, a.t())
+    # factors from elsewhere (views of another flat fp16 buffer): the transposes are formed
+    again = eng.lora_views(torch.cat([x.reshape(-1) for x in lora16]))
+    for a, b in zip(again, eng.lora_fp16_t(again)):
+        assert torch.equal(b, a.t())
