@@ -622,7 +622,11 @@ __global__ __launch_bounds__(kRowThreads) void lmhead_rows_kernel(
   const int lab = in_range ? static_cast<int>(y) : -1;
   const float l2 = L * kLog2e;
   const int k_packs = kpad / 8;
-  for (int p0 = tid; p0 < k_packs; p0 += kRowThreads * kRowDepth) {
+  // Last chunk first: the row's tail, read last by the statistics pass, is the part most likely
+  // still in L2 (every element's G depends only on its own logit, so the order leaves the bits).
+  constexpr int kChunk = kRowThreads * kRowDepth;
+  for (int ch = (k_packs - 1) / kChunk; ch >= 0; --ch) {
+    const int p0 = ch * kChunk + tid;
     f16x8 v[kRowDepth];
 #pragma unroll
     for (int u = 0; u < kRowDepth; ++u) {
