@@ -294,7 +294,8 @@ def config_records(seed: int = 0, reps: int = 40) -> dict:
     out["1"] = c1
     del xs, fw
 
-    # config 2: the lm_head CE forward + backward at N=2048, V=151936, chunk [256, V] logits
+    # config 2: the lm_head CE forward + backward at N=2048, V=151936 (token blocks of 768, 768
+    # and 512: a [768, V] logit buffer)
     n2, V = 2048, 151936
     h = torch.randn(n2, D, device=dev, generator=g).half()
     W = (torch.randn(V, D, device=dev, generator=g) * 0.02).half()
