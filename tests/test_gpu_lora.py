@@ -333,6 +333,44 @@ def test_dequant_launch_carries_norm_and_lora_down_bitwise(drop, n):
     assert torch.equal(y2, y0) and all(torch.equal(a, b) for a, b in zip(m2, m0))
 
 
+@pytest.mark.parametrize("d,r,n", [(2048, 8, 301), (512, 4, 5), (1024, 16, 257)])
+def test_carried_lora_down_widths_ranks_and_ragged_tokens(d, r, n):
+    """The carried LoRA-down's LDS stage at other widths (2048 fills it exactly), ranks 4 / 8 and
+    token counts that leave a partial last block of four: the bits of the norm followed by
+    rus_lora_down_rows, with dropout, and the mids against the oracle's fp16 product."""
+    from rus_amd import model as M
+    from rus_amd.hostload import WeightStream
+
+    cfg = M.Qwen2Config(num_hidden_layers=1, hidden_size=d, intermediate_size=256,
+                        num_attention_heads=d // 128, num_key_value_heads=2, vocab_size=64)
+    model = M.build_random_qlora_qwen2(cfg, DEV, seed=5)
+    ws = WeightStream(model.layers, DEV, resident=True)
+    g = torch.Generator().manual_seed(n + d)
+    x = torch.randn(n, d, generator=g).half().to(DEV)
+    res = torch.randn(n, d, generator=g).half().to(DEV)
+    lnw = (torch.rand(d, generator=g) + 0.5).to(DEV)
+    aq, av = ((torch.randn(r, d, generator=g) * 0.05).half().to(DEV) for _ in range(2))
+    bits = _bits(7, 0, n, d, 0.05, 0.1)
+    y0, _, _ = K.rms_norm_fwd(x, lnw, 1e-6, residual=res)
+    m0 = K.lora_down_rows(y0, aq, av, *bits, 0.05, 0.1)
+    _, _, _, pend = K.rms_norm_fwd(x, lnw, 1e-6, residual=res, defer=True)
+    m1 = pend.carry_lora_down(aq, av, *bits, 0.05, 0.1)
+    ws.dequant_layer(0, norm=pend)
+    assert pend.done
+    torch.cuda.synchronize()
+    for a, b in zip(m1, m0):
+        assert torch.equal(a, b)
+    # against the oracle: fp16(drop(y) A^T) from the same keep bits, within 2 fp16 ulps
+    yc = y0.cpu()
+    for (mid, a_fac, b_bits, p) in ((m1[0], aq, bits[0], 0.05), (m1[1], av, bits[1], 0.1)):
+        keep = torch.from_numpy(np.unpackbits(
+            b_bits.cpu().numpy().view(np.uint8), axis=1, bitorder="little")[:, :d].astype(bool))
+        xd = torch.where(keep, (yc.float() * (1.0 / (1.0 - p))).half(), torch.zeros((), dtype=torch.float16))
+        ok, err = _close(mid.cpu(), (xd.float() @ a_fac.cpu().float().t()).half(), ulps=2.0,
+                         a=xd, b=a_fac.cpu().t())
+        assert ok, err
+
+
 @pytest.mark.parametrize("n_layers,shapes", [(3, [(16, 1536), (1536, 16), (16, 1536), (256, 16)]),
                                              (2, [(3, 5), (7, 2)]), (1, [(1, 1)])])
 def test_lora_cast_t_matches_torch_cast_and_transposes(n_layers, shapes):
