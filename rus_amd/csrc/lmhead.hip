@@ -510,7 +510,7 @@ __global__ __launch_bounds__(256) void lmhead_dh_finish_kernel(
 // keeping kRowDepth of them in flight.
 // ---------------------------------------------------------------------------------------------
 
-constexpr int kRowThreads = 512, kRowDepth = 4;
+constexpr int kRowThreads = 512, kRowDepth = 8;
 
 __device__ __forceinline__ void merge_row(float& m, float& s, float& w, float& bv, int& bi, float m2,
                                           float s2, float w2, float bv2, int bi2) {
