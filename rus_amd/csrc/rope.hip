@@ -56,16 +56,23 @@ struct RopeFwdArgs {
   const T* b_v;
 };
 
-// The LoRA delta of columns col0 .. col0+7 and col0+half .. +7 from mid row m and B [cols, R]:
-// fp16(sum_k m[k] * B[col, k]), the reference's fp16 mid B^T product (ops.py:776-778).
+// Row slot of B row c in the LDS copy: rows permuted within each group of 8 (low three bits
+// XORed with the group's index mod 8). The eight lanes of a wave that read at one step take rows
+// 8 apart (columns col0 + i, col0 = 8 j), which the plain layout puts in the same banks; the
+// permutation spreads them over eight bank groups. A bijection on each group: same values.
+__device__ __forceinline__ int b_slot(int c) { return (c & ~7) | ((c & 7) ^ ((c >> 3) & 7)); }
+
+// The LoRA delta of columns col0 .. col0+7 and col0+half .. +7 from mid row m and B [cols, R]
+// (rows in b_slot order): fp16(sum_k m[k] * B[col, k]), the reference's fp16 mid B^T product
+// (ops.py:776-778).
 template <typename T, int R>
-__device__ __forceinline__ void lora_up(const float (&m)[R], const T* __restrict__ b, int64_t col0,
+__device__ __forceinline__ void lora_up(const float (&m)[R], const T* __restrict__ b, int col0,
                                         int half, float (&dl)[kSpan], float (&dh)[kSpan]) {
 #pragma unroll
   for (int i = 0; i < kSpan; ++i) {
     float bl[R], bh[R];
-    load_f32<T, R>(b + (col0 + i) * R, bl);
-    load_f32<T, R>(b + (col0 + half + i) * R, bh);
+    load_f32<T, R>(b + b_slot(col0 + i) * R, bl);
+    load_f32<T, R>(b + b_slot(col0 + half + i) * R, bh);
     float sl = 0.0f, sh = 0.0f;
 #pragma unroll
     for (int k = 0; k < R; ++k) {
@@ -99,9 +106,12 @@ __global__ __launch_bounds__(kThreads) void rope_fwd_kernel(RopeFwdArgs<T> a) {
     else if (hd >= a.h_q + a.h_kv)
       bsrc = a.b_v + static_cast<int64_t>(hd - a.h_q - a.h_kv) * a.head_dim * R;
     if (bsrc) {
-      const int n4 = a.head_dim * R / 4;  // 8-byte chunks (B is 8-byte aligned)
-      for (int c = threadIdx.x; c < n4; c += kThreads)
-        reinterpret_cast<uint2*>(s_b)[c] = reinterpret_cast<const uint2*>(bsrc)[c];
+      const int n4 = a.head_dim * R / 4;  // 8-byte chunks (B is 8-byte aligned), R / 4 per row
+      for (int c = threadIdx.x; c < n4; c += kThreads) {
+        const int row = c / (R / 4), part = c - row * (R / 4);
+        reinterpret_cast<uint2*>(s_b)[b_slot(row) * (R / 4) + part] =
+            reinterpret_cast<const uint2*>(bsrc)[c];
+      }
     }
     __syncthreads();
   }
