@@ -56,7 +56,9 @@ def make_batches(cfg, n_batches, rows, max_len, seed, device):
         labels = torch.where(mask.bool(), ids, torch.full_like(ids, -100))
         # Host batches (pinned), as a data loader hands them over: the captured step packs them
         # on the host; the eager step moves them to the device first.
-        out.append((ids.pin_memory(), mask.pin_memory(), labels.pin_memory(), sum(lengths)))
+        if device != "cpu":
+            ids, mask, labels = ids.pin_memory(), mask.pin_memory(), labels.pin_memory()
+        out.append((ids, mask, labels, sum(lengths)))
     return out
 
 
@@ -131,48 +133,58 @@ def kernel_rates(summary, steps):
     return out
 
 
-def cpu_baseline(seed=0):
+def cpu_baseline(seed=0, batch=None, reps=5):
     """The CPU oracle on a bounded sample of the same workload: one config-5 layer plus the
-    lm_head over one packed row of 128 tokens, forward + backward including the NF4 dequant of
-    the layer's weights; extrapolated to the 28-layer step as tokens/s."""
+    lm_head over one of the bench's own batches (its packed tokens and row lengths, ~700 tokens),
+    forward + backward including the NF4 dequant of the layer's weights, median of ``reps`` timed
+    repetitions after one warm-up; extrapolated to the 28-layer step as tokens/s."""
+    import statistics
+
     import torch
 
     from oracle import ops as oref
     from oracle import stack as ostack
     from rus_amd import model as M
+    from rus_amd.ops import pack_varlen
 
-    # the host cores of this GPU's share of the box (its OMP_NUM_THREADS, 16 per GPU), at most
-    # the affinity mask
+    # This GPU's share of the box's host cores (its OMP_NUM_THREADS: 16 per GPU on the GPU
+    # boxes, which ask that thread pools stay within it), at most the affinity mask.
+    affinity = len(os.sched_getaffinity(0))
     share = int(os.environ.get("OMP_NUM_THREADS", "16") or 16)
-    threads = max(1, min(len(os.sched_getaffinity(0)), share))
+    threads = max(1, min(affinity, share))
     torch.set_num_threads(threads)
     cfg = M.qwen2_1p5b()
     cfg1 = M.Qwen2Config(**{**cfg.__dict__, "num_hidden_layers": 1, "lora_dropout": 0.0})
     model = M.build_random_qlora_qwen2(cfg1, "cpu", seed=seed)
-    n = 128
+    if batch is None:
+        batch = make_batches(cfg, 1, 4, 512, seed, "cpu")[0]
+    ids, mask, labels = (t.cpu() for t in batch[:3])
+    pb = pack_varlen(ids, mask, labels)
+    n = pb.input_ids.numel()
     g = torch.Generator().manual_seed(seed)
-    ids = torch.randint(0, cfg.vocab_size, (n,), generator=g)
-    pos = torch.arange(n)
-    labels = torch.cat([ids[1:], torch.tensor([-100])])
-    reps = []
-    for _ in range(2):
+    d_final = torch.randn(n, cfg.hidden_size, generator=g)
+    layer, head = [], []
+    for i in range(reps + 1):
         t0 = time.perf_counter()
         deq = ostack.dequant_model(model)
-        t1 = time.perf_counter()
         lora = ostack.lora_leaves(model)
-        loss, final = ostack.step_loss(model, deq, lora, ids, pos, labels, [n])
-        loss.backward()
-        t2 = time.perf_counter()
-        oref.lm_head_ce(final.detach().half(), model.embed, labels, need_grad=True)
-        t3 = time.perf_counter()
-        reps.append((t1 - t0, t2 - t1, t3 - t2))
-    t_deq, t_fb, t_head = (min(r[i] for r in reps) for i in range(3))
-    t_layer = t_deq + max(t_fb - t_head, 0.0)
+        final = ostack.stack_forward(model, deq, lora, pb.input_ids, pb.pos_ids, pb.row_lengths)
+        final.backward(d_final)  # the layer's LoRA gradients
+        t1 = time.perf_counter()
+        layer.append(t1 - t0)
+        if i < 4:  # the head is the slower part: a warm-up and three repetitions
+            oref.lm_head_ce(final.detach().half(), model.embed, pb.shift_labels, need_grad=True)
+            head.append(time.perf_counter() - t1)
+    t_layer, t_head = statistics.median(layer[1:]), statistics.median(head[1:])
     t_step = cfg.num_hidden_layers * t_layer + t_head
-    return {"value": n / t_step, "unit": "tokens/s", "cores": threads, "kind": "port",
+    return {"value": n / t_step, "unit": "tokens/s", "cores": threads, "affinity_cores": affinity,
+            "kind": "port",
             "sample": (f"oracle (eager fp32 torch + numpy NF4 dequant) on 1 of 28 config-5 layers "
-                       f"+ lm_head, one packed row of {n} tokens, fwd+bwd; per-step estimate "
-                       f"28*{t_layer:.3f}s + {t_head:.3f}s (lm_head)")}
+                       f"+ lm_head over the bench's first batch ({n} packed tokens in "
+                       f"{len(pb.row_lengths)} rows), fwd+bwd, medians of {reps} (layer) and 3 "
+                       f"(lm_head) repetitions after a warm-up; "
+                       f"per-step estimate 28*{t_layer:.3f}s + {t_head:.3f}s (lm_head); threads: "
+                       f"this GPU's share of the host ({threads} of {affinity} affinity cores)")}
 
 
 # ---------------------------------------------------------------------------------------------
@@ -289,8 +301,9 @@ def config_records(seed: int = 0, reps: int = 40) -> dict:
     def norm_bwd(i):
         y, h, rstd = fw[i]
         K.rms_norm_bwd(xs[i][0], h, w, rstd, dresidual=xs[i][1])
+    # reads dy, h and dresidual, writes dx: four [N, D] arrays, the weight and rstd
     c1.append(_hbm("rmsnorm_bwd dresidual", [N, D], _time_rotating(norm_bwd, ns, reps),
-                   5 * N * D * 2 + 2 * D + 4 * N, input_sets=ns))
+                   4 * N * D * 2 + 2 * D + 4 * N, input_sets=ns))
     out["1"] = c1
     del xs, fw
 
@@ -1106,7 +1119,7 @@ def main() -> int:
         torch.cuda.empty_cache()
 
     if not args.no_cpu_baseline:
-        out["cpu_baseline"] = cpu_baseline(args.seed)
+        out["cpu_baseline"] = cpu_baseline(args.seed, batches[0])
         if records is not None:
             cpu = config_cpu_times(args.seed)
             for c, recs in records.items():

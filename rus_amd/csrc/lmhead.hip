@@ -6,22 +6,29 @@
 // s = sum e^{z-m}, w = sum e^{z-m} z, the first-index argmax and the target logit, and finishes
 // lse = m + ln s, entropy = lse - w/s, nll = lse - z[label]. The backward forms
 // G = fp16((e^{z-lse} - 1[v=label]) * 2^16/denom) and dH = sum_v G[:, v] W[v, :].
-// The [N, V] logits never exist in memory. Design (CDNA4, wave64, 160 KiB LDS):
-//   * one NT GEMM mainloop (both operands K-contiguous) feeds every kernel: 256x256 block tiles,
-//     4 waves of 128x128 (4x4 v_mfma_f32_32x32x16_f16 tiles, 256 accumulators in AGPRs),
-//     K stepped by 64 through double-buffered LDS (2 x 64 KiB) with one barrier per step;
-//     LDS rows are XOR-swizzled per 16-byte chunk so both the 16-byte stores and the MFMA
-//     operand reads are bank-conflict free;
-//   * blocks are numbered XCD-aware: block b runs on XCD b%8, and each XCD receives a contiguous
-//     range of (vocab tile, token tile) work with token tiles fastest, so the blocks that share a
-//     W tile run on one XCD at the same time and read it from HBM once into that XCD's L2;
-//   * forward statistics: W is the M operand and H the N operand, so each lane's accumulators
-//     hold 64 vocabulary entries of one token: max/argmax/sum-exp are in-register reductions,
-//     one lane-pair exchange and one LDS merge of the two vocab halves; each block writes one
-//     (m, s, w, argmax) partial per token per 256 vocab rows, merged by a small combine kernel;
-//   * backward: a second pass of the same mainloop turns each logit tile into fp16 G, staged
-//     through LDS for 16-byte coalesced stores, then a split-K GEMM G . (W^T) accumulates dH in
-//     fp32 partials that a reduction kernel sums (the reference accumulates in fp16, ops.py:320).
+// Two layouts share these kernels; neither holds the logits of a whole batch (CDNA4, wave64,
+// 160 KiB LDS):
+//   * token-blocked head (the default with a device-resident W): the tokens go in blocks of whole
+//     256-token tiles, at least two per batch; per block lmhead_logits_kernel writes the block's
+//     fp16 logits into a [block, round_up(V, 64)] buffer (at most 256 MiB: 768 tokens at
+//     V = 151,936), lmhead_rows_kernel (one workgroup per token row) forms lse / nll / entropy /
+//     first argmax and rewrites the row in place as G, and lmhead_grad_hidden_kernel forms
+//     G . (W^T)^T split-K over the vocabulary into fp32 partials that dh_reduce_kernel sums;
+//   * single pass over vocabulary chunks (a head streamed from the host, or v_chunk given):
+//     lmhead_stats_kernel<KEEP> keeps per-token online statistics per 256 vocab rows in
+//     registers and the chunk's logits; lmhead_chunk_scale_kernel turns them into
+//     P = e^{z - M} (M the running maximum) and the same split-K GEMM adds P . W_chunk into fp32
+//     partials rescaled when M grows; lmhead_dh_finish_kernel divides by s and subtracts the
+//     label rows.
+// The GEMMs run the mainloop of mfma_gemm.h: 256 x 256 block tiles on v_mfma_f32_32x32x16_f16,
+// K staged 32 at a time through four 32 KiB LDS stages (five for an N-contiguous B) filled by
+// direct global -> LDS copies, one barrier per stage; eight waves of 128 x 64 (two per SIMD) for
+// the logits and hidden-gradient kernels, four waves of 128 x 128 for the statistics kernel, whose
+// epilogue needs each lane to hold 64 vocabulary entries of one token (W is its M operand). Blocks
+// are numbered XCD-aware (block b on XCD b % 8, each XCD a contiguous range of tiles), so blocks
+// that share a W tile share an L2. LDS rows are XOR-swizzled per 16-byte chunk, so the copies and
+// the MFMA fragment reads are bank-conflict free. The hidden gradient accumulates in fp32
+// partials (the reference accumulates in fp16, solution/ops.py:320).
 #include <math.h>
 
 #include "common.h"

@@ -198,7 +198,7 @@ class GraphedTrainStep:
             ts = [None if t is None else t.cpu() for t in (input_ids, attention_mask, labels)]
         else:
             ts = [None if t is None else t.to(dev) for t in (input_ids, attention_mask, labels)]
-        return pack_varlen(*ts)
+        return pack_varlen(*ts, vocab_size=self.engine.host_head.vocab_size)
 
     def _capture(self, key, pb, lens) -> _Captured:
         cap = self.graphs.get(key)

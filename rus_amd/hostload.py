@@ -521,8 +521,17 @@ class HostHead:
             self.embed_error = torch.zeros(1, dtype=torch.int32, device=self.device)
 
     def embed(self, input_ids: torch.Tensor) -> torch.Tensor:
-        """Embedding rows of ``input_ids`` (any shape) as fp16 [*shape, hidden] on the device."""
+        """Embedding rows of ``input_ids`` (any shape) as fp16 [*shape, hidden] on the device.
+
+        An id outside [0, vocab) raises IndexError: on the host for host ids, and for device ids
+        through ``F.embedding`` (resident) or, streamed, through the packing step's check
+        (``ops.pack_varlen(vocab_size=...)``, which every engine path runs first); the streamed
+        gather itself reads nothing out of range (such a row becomes zeros and sets
+        ``embed_error``)."""
         ids = input_ids.reshape(-1)
+        if ids.device.type == "cpu" and ids.numel() and (
+                int(ids.min()) < 0 or int(ids.max()) >= self.vocab_size):
+            raise IndexError(f"embed: a token id lies outside [0, {self.vocab_size})")
         if self.resident:
             out = torch.nn.functional.embedding(ids.to(self.device), self.gpu_weight)
         else:

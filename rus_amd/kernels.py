@@ -2061,7 +2061,8 @@ def lm_head_ce(hidden: torch.Tensor, weight: torch.Tensor, labels: torch.Tensor,
     With the gradient, the tokens go in blocks (``lm_head_token_blocks``: whole 256-token MFMA
     tiles, at least two blocks for two or more tokens, at most ``block_tokens`` each; default:
     the tiles whose fp16 logits fit 256 MiB, 768 tokens at V = 151936; 744 tokens go as 512 +
-    232). For each block one GEMM over the whole vocabulary stores its fp16 logits in a
+    232; a batch within one tile takes the single pass below over at least two vocabulary
+    chunks). For each block one GEMM over the whole vocabulary stores its fp16 logits in a
     [block, V] buffer; one kernel per token row forms the statistics and turns the row into the
     reference's fp16 gradient G = fp16((softmax - onehot) 2^16 / denom) in place (the denominator
     is known up front); and a split-K GEMM G . W writes the block's dH partials, summed once. W
@@ -2082,6 +2083,12 @@ def lm_head_ce(hidden: torch.Tensor, weight: torch.Tensor, labels: torch.Tensor,
     w = _lm_operand(fn, weight, d, "weight")
     if lab.numel() != n_tok:
         raise ValueError(f"{fn}: labels must have {n_tok} entries")
+    if v_chunk is None and need_grad and 1 < n_tok <= LM_TILE:
+        # A batch within one 256-token tile: split into token blocks, each block's GEMMs would
+        # read all of W on a half-empty tile (twice the cost of one pass); the pass over at
+        # least two vocabulary chunks reads W once and still never holds [N, V] logits.
+        v_chunk = min(lm_head_chunk_cols(n_tok, V, cu_count(dev)),
+                      _round_up(-(-V // 2), LM_TILE))
     if v_chunk is not None:
         chunk = int(v_chunk)
         if chunk <= 0 or (chunk < V and chunk % LM_TILE):

@@ -985,9 +985,12 @@ class PackedBatch:
     batch_shape: tuple[int, int]
 
 
-def pack_varlen(input_ids, attention_mask=None, labels=None, position_ids=None) -> PackedBatch:
+def pack_varlen(input_ids, attention_mask=None, labels=None, position_ids=None,
+                vocab_size: int | None = None) -> PackedBatch:
     """keep = attention_mask | (shifted label != -100); positions = cumsum(mask) - 1 per row;
-    the kept tokens of every row, concatenated (solution/ops.py:1103-1127)."""
+    the kept tokens of every row, concatenated (solution/ops.py:1103-1127). With ``vocab_size``,
+    a kept token id outside [0, vocab_size) raises IndexError (checked in the one host
+    synchronisation the row lengths need, so device inputs cost no extra round trip)."""
     B, S = input_ids.shape
     dev = input_ids.device
     if attention_mask is None:
@@ -998,7 +1001,13 @@ def pack_varlen(input_ids, attention_mask=None, labels=None, position_ids=None) 
     keep = attention_mask.bool() | (shift != -100)
     if not keep.any():
         keep[:, 0] = True
-    row_lengths = keep.sum(dim=-1, dtype=torch.int32).tolist()
+    lens = keep.sum(dim=-1, dtype=torch.int64)
+    if vocab_size is not None:
+        bad = (keep & ((input_ids < 0) | (input_ids >= vocab_size))).sum().reshape(1)
+        lens = torch.cat([lens, bad])
+    row_lengths = lens.tolist()
+    if vocab_size is not None and row_lengths.pop():
+        raise IndexError(f"pack_varlen: a token id lies outside [0, {vocab_size})")
     valid_idx = torch.nonzero(keep.reshape(-1), as_tuple=False).squeeze(-1)
     pos_full = (position_ids.to(torch.long) if position_ids is not None
                 else (attention_mask.to(torch.long).cumsum(dim=-1) - 1).clamp_(min=0))
@@ -1020,7 +1029,8 @@ def fused_causal_lm_forward(engine: Qwen2FusedEngine, input_ids, attention_mask=
     """Packed forward of the whole model with the fused lm_head (the body of the reference's
     patched Qwen2ForCausalLM.forward, solution/ops.py:1097-1164). Returns (loss, per-token nll,
     entropy, argmax) scattered back to [B, S]; padding positions get the mean entropy."""
-    pb = pack_varlen(input_ids, attention_mask, labels, position_ids)
+    pb = pack_varlen(input_ids, attention_mask, labels, position_ids,
+                     vocab_size=engine.host_head.vocab_size)
     h = engine.host_head.embed(pb.input_ids)
     final = FusedQwen2StackFn.apply(h, pb.pos_ids, pb.row_lengths, engine, training, *engine.lora_params)
     loss, nll, ent, amax = chunked_lm_head(final, pb.shift_labels, engine.host_head,
@@ -1103,6 +1113,67 @@ def _patch_transformers_qwen2() -> bool:
     return True
 
 
+_KERNEL_DTYPES = (torch.float16, torch.float32)
+
+
+def _patch_qwen2_mlp() -> bool:
+    """``Qwen2MLP.forward`` → down_proj(mlp_glu(gate_proj(x), up_proj(x))) for device tensors of
+    a kernel dtype with the SiLU activation, for the calls the fused stack does not take (eval
+    without labels, generation); anything else keeps transformers' code (solution/ops.py:1029-1033,
+    1186)."""
+    try:
+        from transformers.models.qwen2 import modeling_qwen2
+    except ImportError:
+        return False
+    cls = modeling_qwen2.Qwen2MLP
+    if getattr(cls.forward, "_rus_fused", False):
+        return True
+    unfused = cls.forward
+
+    def forward(self, x):
+        act = getattr(getattr(self, "config", None), "hidden_act", "silu")
+        if act != "silu" or not isinstance(x, torch.Tensor) or not x.is_cuda:
+            return unfused(self, x)
+        gate, up = self.gate_proj(x), self.up_proj(x)
+        if gate.dtype not in _KERNEL_DTYPES or up.dtype != gate.dtype:
+            return self.down_proj(self.act_fn(gate) * up)
+        return self.down_proj(mlp_glu(gate, up))
+
+    forward._rus_fused = True
+    forward.__wrapped__ = unfused
+    cls.forward = forward
+    return True
+
+
+def _patch_qwen2_rmsnorm() -> bool:
+    """``Qwen2RMSNorm.forward`` → ``rms_norm`` (one-pass kernel, output in the input's dtype, the
+    reference's behaviour, solution/ops.py:1035-1039, 1187) for device tensors of a kernel dtype.
+    The kernel's backward forms no weight gradient (the norms are frozen under QLoRA), so a norm
+    whose weight requires grad under autograd keeps transformers' code."""
+    try:
+        from transformers.models.qwen2 import modeling_qwen2
+    except ImportError:
+        return False
+    cls = modeling_qwen2.Qwen2RMSNorm
+    if getattr(cls.forward, "_rus_fused", False):
+        return True
+    unfused = cls.forward
+
+    def forward(self, hidden_states):
+        w = self.weight
+        if (not isinstance(hidden_states, torch.Tensor) or not hidden_states.is_cuda
+                or hidden_states.dtype not in _KERNEL_DTYPES or w.dtype not in _KERNEL_DTYPES
+                or (w.requires_grad and torch.is_grad_enabled())):
+            return unfused(self, hidden_states)
+        eps = float(getattr(self, "variance_epsilon", getattr(self, "eps", 1e-6)))
+        return rms_norm(hidden_states, w, eps=eps)
+
+    forward._rus_fused = True
+    forward.__wrapped__ = unfused
+    cls.forward = forward
+    return True
+
+
 def _patch_trl_entropy() -> bool:
     try:
         import trl.trainer.sft_trainer as sft  # TRL 0.29.1 (solution/ops.py:1223-1238)
@@ -1128,9 +1199,12 @@ def _patch_trl_entropy() -> bool:
 def install_runtime_patches() -> dict[str, bool]:
     """Routes a transformers ``Qwen2ForCausalLM`` training forward with QLoRA (PEFT LoRA on q / v
     over bitsandbytes NF4) and CUDA inputs through the fused engine, returning the loss and a
-    ``ChunkedLogitsProxy``; and makes TRL's ``entropy_from_logits`` read the proxy's entropy
-    (solution/ops.py:1016-1238). Any other call keeps the library's own code. Idempotent;
-    returns which patches are active (a library that is not importable is skipped, where the
-    reference swallows every exception)."""
+    ``ChunkedLogitsProxy``; routes the remaining ``Qwen2MLP`` / ``Qwen2RMSNorm`` calls on device
+    tensors through the SwiGLU and RMSNorm kernels; and makes TRL's ``entropy_from_logits`` read
+    the proxy's entropy (solution/ops.py:1016-1238). Any other call keeps the library's own code.
+    Idempotent; returns which patches are active (a library that is not importable is skipped,
+    where the reference swallows every exception)."""
     return {"transformers_qwen2": _patch_transformers_qwen2(),
+            "qwen2_mlp": _patch_qwen2_mlp(),
+            "qwen2_rmsnorm": _patch_qwen2_rmsnorm(),
             "trl_entropy": _patch_trl_entropy()}

@@ -4,6 +4,7 @@ host-side packing (rus_amd.ops.pack_varlen) and model adapter on the CPU."""
 from __future__ import annotations
 
 
+import pytest
 import torch
 
 from oracle import stack as ostack
@@ -41,6 +42,15 @@ def test_pack_varlen_matches_reference_rules():
     assert pb.shift_labels.tolist() == [6, 7, -100, -100, 3, 4, 9, -100]
     back = scatter_per_token(pb.input_ids, pb, -1)
     assert back.tolist() == [[5, 6, 7, -1, -1], [1, 2, 3, 4, 9]]
+    # the id check looks at kept tokens only: padding may hold anything
+    ids_pad = ids.clone()
+    ids_pad[0, 3:] = 10**6
+    assert pack_varlen(ids_pad, mask, labels, vocab_size=10).row_lengths == [3, 5]
+    for bad in (-1, 10):
+        ids_bad = ids.clone()
+        ids_bad[1, 2] = bad
+        with pytest.raises(IndexError):
+            pack_varlen(ids_bad, mask, labels, vocab_size=10)
 
 
 def test_stack_oracle_matches_transformers_qwen2():

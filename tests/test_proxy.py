@@ -98,13 +98,15 @@ def test_proxy_rejects_what_needs_the_logits():
 
 @pytest.fixture
 def keep_qwen2_forward(monkeypatch):
-    """install_runtime_patches replaces transformers' Qwen2 forward; restore it afterwards."""
+    """install_runtime_patches replaces transformers' Qwen2 causal-LM, MLP and RMSNorm forwards;
+    restore them afterwards."""
     try:
         from transformers.models.qwen2 import modeling_qwen2
     except ImportError:
         return
-    monkeypatch.setattr(modeling_qwen2.Qwen2ForCausalLM, "forward",
-                        modeling_qwen2.Qwen2ForCausalLM.forward)
+    for cls in (modeling_qwen2.Qwen2ForCausalLM, modeling_qwen2.Qwen2MLP,
+                modeling_qwen2.Qwen2RMSNorm):
+        monkeypatch.setattr(cls, "forward", cls.forward)
 
 
 def test_trl_entropy_patch_reads_the_proxy(monkeypatch, keep_qwen2_forward):
@@ -147,3 +149,48 @@ def test_qwen2_patch_keeps_unfused_calls(keep_qwen2_forward):
     torch.testing.assert_close(after.loss, before.loss)
     torch.testing.assert_close(after.logits, before.logits)
     assert not ops._fusable(model, ids, ids)
+
+
+def test_qwen2_mlp_and_rmsnorm_patches_keep_cpu_calls(keep_qwen2_forward):
+    # Qwen2MLP / Qwen2RMSNorm are routed to the kernels only for device tensors: on CPU tensors
+    # (and for a trainable norm weight under autograd) the library's own code runs, bit for bit.
+    transformers = pytest.importorskip("transformers")
+    from transformers.models.qwen2 import modeling_qwen2
+
+    cfg = transformers.Qwen2Config(vocab_size=97, hidden_size=32, intermediate_size=64,
+                                   num_hidden_layers=1, num_attention_heads=4,
+                                   num_key_value_heads=2, max_position_embeddings=64)
+    torch.manual_seed(1)
+    mlp, norm = modeling_qwen2.Qwen2MLP(cfg), modeling_qwen2.Qwen2RMSNorm(32, eps=1e-6)
+    x = torch.randn(3, 5, 32)
+    with torch.no_grad():
+        want_mlp, want_norm = mlp(x), norm(x)
+    got = ops.install_runtime_patches()
+    assert got["qwen2_mlp"] and got["qwen2_rmsnorm"]
+    for cls in (modeling_qwen2.Qwen2MLP, modeling_qwen2.Qwen2RMSNorm):
+        assert getattr(cls.forward, "_rus_fused", False) and cls.forward.__wrapped__ is not None
+    fwd = modeling_qwen2.Qwen2MLP.forward
+    assert ops.install_runtime_patches()["qwen2_mlp"] and modeling_qwen2.Qwen2MLP.forward is fwd
+    with torch.no_grad():
+        assert torch.equal(mlp(x), want_mlp) and torch.equal(norm(x), want_norm)
+    y = norm(x.requires_grad_())  # trainable weight: transformers' code, weight gradient formed
+    y.sum().backward()
+    assert norm.weight.grad is not None
+
+
+def test_apply_is_idempotent(keep_qwen2_forward, monkeypatch):
+    # rus_amd.apply(): loads the library, installs the patches once; a second call changes
+    # nothing and returns the same answer (solution/__init__.py:111-116). No GPU here, so no
+    # warm-up launches.
+    pytest.importorskip("transformers")
+    import rus_amd
+    from transformers.models.qwen2 import modeling_qwen2
+
+    monkeypatch.setattr(rus_amd, "_ACTIVE", None)
+    first = rus_amd.apply()
+    assert first["transformers_qwen2"] and first["qwen2_mlp"] and first["qwen2_rmsnorm"]
+    fwds = [c.forward for c in (modeling_qwen2.Qwen2ForCausalLM, modeling_qwen2.Qwen2MLP,
+                                modeling_qwen2.Qwen2RMSNorm)]
+    assert rus_amd.apply() == first
+    assert fwds == [c.forward for c in (modeling_qwen2.Qwen2ForCausalLM, modeling_qwen2.Qwen2MLP,
+                                        modeling_qwen2.Qwen2RMSNorm)]

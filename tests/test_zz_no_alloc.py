@@ -49,13 +49,16 @@ def test_noalloc_lora_down_equals_workspace_entry_point(r):
 
 
 def test_noalloc_lora_down_rejects_beyond_static_scratch():
-    d, r = 1536, 16
-    x = torch.empty((1, d), dtype=torch.float16, device=DEV)
-    a = torch.empty((r, d), dtype=torch.float16, device=DEV)
-    mid = torch.empty((1, r), dtype=torch.float16, device=DEV)
+    d, r, n = 1536, 16, 10944
+    # buffers of the full size, so that a regression of the host-side check would show as a
+    # missing error rather than as accesses past small allocations
+    x = torch.zeros((n, d), dtype=torch.float16, device=DEV)
+    a = torch.zeros((r, d), dtype=torch.float16, device=DEV)
+    mid_q = torch.zeros((n, r), dtype=torch.float16, device=DEV)
+    mid_v = torch.zeros((n, r), dtype=torch.float16, device=DEV)
     # 10,944 tokens need 342 tiles of 32: one more than the static scratch holds (checked on the
     # host from the sizes alone, before anything is launched)
     with pytest.raises(RuntimeError, match="static scratch"):
-        _lib.call("rus_lora_down_fwd_noalloc", x.data_ptr(), 10944, d, d, a.data_ptr(),
-                  a.data_ptr(), r, mid.data_ptr(), mid.data_ptr(), None, None, 0.0, 0.0,
+        _lib.call("rus_lora_down_fwd_noalloc", x.data_ptr(), n, d, d, a.data_ptr(),
+                  a.data_ptr(), r, mid_q.data_ptr(), mid_v.data_ptr(), None, None, 0.0, 0.0,
                   torch.cuda.current_stream().cuda_stream)
