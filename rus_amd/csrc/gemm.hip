@@ -46,7 +46,7 @@ gemm_parts_nt_kernel(GemmArgs g, float* parts) {
 
 __global__ __launch_bounds__(kThreads8) __attribute__((amdgpu_waves_per_eu(2, 2))) void
 gemm_parts_kn_kernel(GemmArgs g, float* parts) {
-  __shared__ __attribute__((aligned(16))) char smem[kSmemBytesKN];
+  __shared__ __attribute__((aligned(16))) char smem[kSmem64];
   Tile tl;
   if (!tile_of(g, tl)) return;
   f32x16 acc[kMT][2];

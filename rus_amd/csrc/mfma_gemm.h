@@ -55,10 +55,11 @@ __device__ __forceinline__ bool tile_of(const GemmArgs& g, Tile& t) {
 // split's K range. Accumulator layout (v_mfma_f32_32x32x16_f16): register r of lane l holds
 // row 8*(r/4) + 4*(l/32) + r%4, column l%32 of the 32x32 tile.
 //
-// Pipeline: K is staged 32 at a time through NS LDS buffers of 32 KiB (A then B, 256 rows x
-// 64 bytes each; NS = 4, or 5 for the N-contiguous B). Global memory is copied straight into LDS
-// (global_load_lds_dwordx4: each lane's 16 bytes land at buffer + lane * 16), NS - 1 stages ahead
-// of the MFMAs, so no register holds a tile in flight and the 256 accumulators stay in AGPRs. The 16-byte chunk c of row r is stored
+// Two pipelines. mainloop_t (the four-wave kernels: statistics and logit gradient) stages K 32 at
+// a time through NS LDS buffers of 32 KiB (A then B, 256 rows x 64 bytes each; NS = 4);
+// mainloop_k64 (the eight-wave kernels) stages K 64 at a time, below. Global memory is copied
+// straight into LDS (global_load_lds_dwordx4: each lane's 16 bytes land at buffer + lane * 16),
+// NS - 1 stages ahead of the MFMAs, so no register holds a tile in flight. The 16-byte chunk c of row r is stored
 // at chunk c ^ ((r >> 2) & 3) of its 64-byte row, which a lane realises by loading the chunk
 // that belongs at its position; the MFMAs' 16-byte fragment reads (16 consecutive rows per quarter
 // wave, one chunk) then hit all 64 banks once. The fragment reads are explicit ds_read_b128 with
@@ -72,11 +73,6 @@ constexpr int kDK = 32;                  // K per LDS stage
 constexpr int kStageBytes = 2 * kBM * kDK * 2;  // A + B: 32 KiB
 constexpr int kNStages = 4;
 static_assert(kNStages * kStageBytes == kSmemBytes, "stages fill the kernel's LDS");
-// The N-contiguous mainloop keeps five stages (all 160 KiB of the CU's LDS): four stages in
-// flight instead of three took the split-K product at 707 tokens from 65 to 57 us (isolated); the
-// K-contiguous kernels gained nothing from it.
-constexpr int kNStagesKN = 5;
-constexpr int kSmemBytesKN = kNStagesKN * kStageBytes;
 
 template <int OFF>
 __device__ __forceinline__ u32x4v lds_read16(uint32_t addr) {
@@ -210,10 +206,11 @@ __device__ __forceinline__ void wait_stages(int stages) {
     wait_vmcnt<0>();
 }
 
-// NW = 4: waves 2 (M halves) x 2 (N halves) of 128 x 128 (acc[4][4], one wave per SIMD);
-// NW = 8: 2 x 4 waves of 128 x 64 (acc[4][2], two waves per SIMD, so one wave's fragment reads
-// and copy waits overlap the other's MFMAs). Same LDS stages and A swizzle either way. KN: B is
-// [K, ldb] N-contiguous (NW = 8 only), staged as 32 K rows of 512 bytes per stage.
+// NW = 4: waves 2 (M halves) x 2 (N halves) of 128 x 128 (acc[4][4], one wave per SIMD), the
+// layout of the kernels whose epilogues need 4 x 4 accumulator tiles per wave; NW = 8: 2 x 4 waves
+// of 128 x 64 (acc[4][2]). Same LDS stages and A swizzle either way. KN: B is [K, ldb]
+// N-contiguous (NW = 8 only), staged as 32 K rows of 512 bytes per stage. The eight-wave kernels
+// run mainloop_k64 instead: its whole-line copies made them ~10% faster (isolated, same bits).
 template <int NW, bool KN = false, int NS = kNStages>
 __device__ __forceinline__ void mainloop_t(const GemmArgs& g, const Tile& tl, char* smem,
                                            f32x16 (&acc)[kMT][16 / NW]) {
@@ -349,6 +346,198 @@ __device__ __forceinline__ void mainloop_t(const GemmArgs& g, const Tile& tl, ch
   __syncthreads();  // the epilogues reuse the LDS
 }
 
+// Eight waves (2 x 4 of 128 x 64) with K staged 64 at a time through two 64 KiB LDS buffers:
+// every global -> LDS copy instruction then moves 8 whole 128-byte lines (8 rows x 64 K of a
+// K-contiguous operand) instead of 16 half lines, which doubles what the copy path delivers per
+// CU. Rows of 128 bytes, the 16-byte chunk c of row r stored at c ^ ((r >> 1) & 7): the 16 rows a
+// quarter wave reads at one chunk then cover all 64 banks once. N-contiguous B: 64 K rows of 512
+// bytes per stage (the chunk c of row r at c ^ ((r & 3) << 2), as in the 32-deep stages). The
+// copies of stage k + 2 are issued after the barrier that ends the reads of stage k; one barrier
+// per 64 K.
+constexpr int kDK64 = 64;
+constexpr int kStage64 = 2 * kBM * kDK64 * 2;  // 64 KiB
+constexpr int kSmem64 = 2 * kStage64;          // 128 KiB
+
+template <bool KN>
+__device__ __forceinline__ void mainloop_k64(const GemmArgs& g, const Tile& tl, char* smem,
+                                             f32x16 (&acc)[kMT][2]) {
+  constexpr int NT = 2;
+  constexpr int PER = 8;  // copies per wave per stage (4 for A, 4 for B)
+  const int t = threadIdx.x, lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(t >> 6));
+  const int wm = wave >> 2, wn = wave & 3;
+  const int kb = tl.split * g.k_per_split;
+  const int ke = min(kb + g.k_per_split, g.K);
+  const int KT = ke > kb ? (ke - kb) / kDK64 : 0;
+#pragma unroll
+  for (int mt = 0; mt < kMT; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = f32x16{};
+  if (KT == 0) {
+    __syncthreads();
+    return;
+  }
+  // Copies: instruction i of wave w fills bytes 1024 (8 i + w) .. +1024 of the stage's A tile
+  // (rows 8 (8 i + w) .. +8; lane l covers row + l/8 at position l%8, i.e. the chunk
+  // (l%8) ^ ((row >> 1) & 7)) and the same bytes of the B tile (K-contiguous as A; N-contiguous:
+  // K rows 2 (8 i + w) + l/32 of 512 bytes, lane l at position l%32 of its row r, the chunk
+  // (l%32) ^ ((r & 3) << 2), columns n0 + 8 chunk .. +8).
+  const char* gA = reinterpret_cast<const char*>(g.A);
+  const char* gB = reinterpret_cast<const char*>(g.B);
+  uint32_t oa[4], ob[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int row = 8 * (8 * i + wave) + (lane >> 3);
+    const int ch = (lane & 7) ^ ((row >> 1) & 7);
+    // Rows (columns) past the matrix edge re-read the last one: finite values the epilogues
+    // discard.
+    const int ra_ = min(tl.m0 + row, g.M - 1);
+    oa[i] = static_cast<uint32_t>((ra_ * g.lda + kb + ch * 8) * 2);
+    if constexpr (KN) {
+      const int krow = 2 * (8 * i + wave) + (lane >> 5);
+      const int col = min(tl.n0 + 8 * ((lane & 31) ^ ((krow & 3) << 2)), g.N - 8);
+      ob[i] = static_cast<uint32_t>(((kb + krow) * g.ldb + col) * 2);
+    } else {
+      const int rb_ = min(tl.n0 + row, g.N - 1);
+      ob[i] = static_cast<uint32_t>((rb_ * g.ldb + kb + ch * 8) * 2);
+    }
+  }
+  const uint32_t bstep = KN ? static_cast<uint32_t>(kDK64 * g.ldb * 2) : kDK64 * 2;
+  auto issue = [&](int k) {  // stage k's copies into buffer k % 2
+    char* st = smem + (k & 1) * kStage64 + wave * 1024;
+    const uint32_t abytes = k * (kDK64 * 2), bbytes = k * bstep;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      __builtin_amdgcn_global_load_lds(gA + oa[i] + abytes, (lds_void_ptr)(st + i * 8192), 16,
+                                       0, 0);
+      __builtin_amdgcn_global_load_lds(gB + ob[i] + bbytes,
+                                       (lds_void_ptr)(st + kBM * 128 + i * 8192), 16, 0, 0);
+    }
+  };
+  // Fragment addresses. A: row wm*128 + (l & 31) (+ 32 per MFMA tile: immediate 4096), chunk
+  // 2 kk + l/32 at position chunk ^ ((l >> 1) & 7) (the low row bits are those of l). B
+  // K-contiguous likewise; N-contiguous: lane l of group g = l/16 (j = l%16) reads K row
+  // 16 kk + 8 (g/2) + j/4 (+ 4 for the high half), columns wn*64 + 32 nt + 16 (g%2) + 4 (j%4).
+  const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void_ptr)smem));
+  const int sw = (lane >> 1) & 7, half = lane >> 5;
+  uint32_t cpos[4];
+#pragma unroll
+  for (int kk = 0; kk < 4; ++kk) cpos[kk] = static_cast<uint32_t>(((2 * kk + half) ^ sw) << 4);
+  const uint32_t arow = lds0 + (wm * kWM + (lane & 31)) * 128;
+  const uint32_t brow = lds0 + kBM * 128 + (wn * 64 + (lane & 31)) * 128;
+  uint32_t bk[NT];
+  if constexpr (KN) {
+    const int j = lane & 15, nh = (lane >> 4) & 1;
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      const int col = wn * 64 + nt * 32 + 16 * nh + 4 * (j & 3);
+      bk[nt] = lds0 + kBM * 128 + (8 * half + (j >> 2)) * kKNRowBytes +
+               (((col >> 3) ^ ((j >> 2) << 2)) << 4) + (col & 7) * 2;
+    }
+  }
+  u32x4v fa0[kMT], fa1[kMT], fb0[NT], fb1[NT];
+  u32x2v lo0[NT], hi0[NT], lo1[NT], hi1[NT];
+  // Fragments of K step kk (0..3) of the stage at byte offset sb.
+  auto read0 = [&](uint32_t sb, int kk) {
+    const uint32_t a = arow + sb + cpos[kk];
+    fa0[0] = lds_read16<0>(a);
+    fa0[1] = lds_read16<4096>(a);
+    fa0[2] = lds_read16<8192>(a);
+    fa0[3] = lds_read16<12288>(a);
+    if constexpr (KN) {
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        lo0[nt] = lds_read8_tr<0>(bk[nt] + sb + kk * 16 * kKNRowBytes);
+        hi0[nt] = lds_read8_tr<4 * kKNRowBytes>(bk[nt] + sb + kk * 16 * kKNRowBytes);
+      }
+    } else {
+      fb0[0] = lds_read16<0>(brow + sb + cpos[kk]);
+      fb0[1] = lds_read16<4096>(brow + sb + cpos[kk]);
+    }
+  };
+  auto read1 = [&](uint32_t sb, int kk) {
+    const uint32_t a = arow + sb + cpos[kk];
+    fa1[0] = lds_read16<0>(a);
+    fa1[1] = lds_read16<4096>(a);
+    fa1[2] = lds_read16<8192>(a);
+    fa1[3] = lds_read16<12288>(a);
+    if constexpr (KN) {
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        lo1[nt] = lds_read8_tr<0>(bk[nt] + sb + kk * 16 * kKNRowBytes);
+        hi1[nt] = lds_read8_tr<4 * kKNRowBytes>(bk[nt] + sb + kk * 16 * kKNRowBytes);
+      }
+    } else {
+      fb1[0] = lds_read16<0>(brow + sb + cpos[kk]);
+      fb1[1] = lds_read16<4096>(brow + sb + cpos[kk]);
+    }
+  };
+  auto wait0 = [&]() {
+    if constexpr (KN)
+      wait_frags_kn<NT>(fa0, lo0, hi0);
+    else
+      wait_frags<NT>(fa0, fb0);
+  };
+  auto wait1 = [&]() {
+    if constexpr (KN)
+      wait_frags_kn<NT>(fa1, lo1, hi1);
+    else
+      wait_frags<NT>(fa1, fb1);
+  };
+  auto mma0 = [&]() {
+    if constexpr (KN)
+      mma16_kn<NT>(fa0, lo0, hi0, acc);
+    else
+      mma16<NT>(fa0, fb0, acc);
+  };
+  auto mma1 = [&]() {
+    if constexpr (KN)
+      mma16_kn<NT>(fa1, lo1, hi1, acc);
+    else
+      mma16<NT>(fa1, fb1, acc);
+  };
+  issue(0);
+  if (KT > 1) issue(1);
+  if (KT > 1)
+    wait_vmcnt<PER>();  // stage 0 landed (this wave's copies)
+  else
+    wait_vmcnt<0>();
+  __builtin_amdgcn_s_barrier();  // ... and every wave's
+  read0(0, 0);
+  wait0();
+  for (int k = 0; k < KT; ++k) {
+    const uint32_t sb = (k & 1) * kStage64;
+    read1(sb, 1);
+    __builtin_amdgcn_sched_barrier(0);
+    mma0();
+    __builtin_amdgcn_sched_barrier(0);
+    wait1();
+    read0(sb, 2);
+    __builtin_amdgcn_sched_barrier(0);
+    mma1();
+    __builtin_amdgcn_sched_barrier(0);
+    wait0();
+    read1(sb, 3);
+    __builtin_amdgcn_sched_barrier(0);
+    mma0();
+    __builtin_amdgcn_sched_barrier(0);
+    wait1();
+    if (k + 1 < KT) {
+      // Stage k + 1 has landed for every wave, and every wave has read stage k: its buffer
+      // takes stage k + 2.
+      wait_vmcnt<0>();
+      __builtin_amdgcn_s_barrier();
+      if (k + 2 < KT) issue(k + 2);
+      read0((sb ^ kStage64), 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    mma1();
+    __builtin_amdgcn_sched_barrier(0);
+    if (k + 1 < KT) wait0();
+  }
+  __syncthreads();  // the epilogues reuse the LDS
+}
+
 __device__ __forceinline__ void mainloop(const GemmArgs& g, const Tile& tl, char* smem,
                                          f32x16 (&acc)[kMT][4]) {
   mainloop_t<4>(g, tl, smem, acc);
@@ -356,13 +545,13 @@ __device__ __forceinline__ void mainloop(const GemmArgs& g, const Tile& tl, char
 
 __device__ __forceinline__ void mainloop(const GemmArgs& g, const Tile& tl, char* smem,
                                          f32x16 (&acc)[kMT][2]) {
-  mainloop_t<8>(g, tl, smem, acc);
+  mainloop_k64<false>(g, tl, smem, acc);
 }
 
-// The eight-wave mainloop with B stored [K, ldb] N-contiguous; smem holds kSmemBytesKN.
+// The eight-wave mainloop with B stored [K, ldb] N-contiguous.
 __device__ __forceinline__ void mainloop_kn(const GemmArgs& g, const Tile& tl, char* smem,
                                             f32x16 (&acc)[kMT][2]) {
-  mainloop_t<8, true, kNStagesKN>(g, tl, smem, acc);
+  mainloop_k64<true>(g, tl, smem, acc);
 }
 
 // Eight waves (two per SIMD): the accumulators of a 128 x 64 wave tile leave room for a second

@@ -270,6 +270,19 @@ class WeightStream:
         self._buf_version = [-1] * nb
         self.staged = [False] * nb
         self.next_buffer = 0
+        self.copy_marks: list | None = None  # (start, end) timing events per copy, when timing
+
+    def time_copies(self, on: bool = True) -> None:
+        """Starts (or stops) recording a pair of timing events around every whole-model copy."""
+        self.copy_marks = [] if on else None
+
+    def copy_ms(self) -> list[float]:
+        """Durations (ms) of the copies recorded since ``time_copies()`` (synchronises)."""
+        out = []
+        for e0, e1 in self.copy_marks or []:
+            e1.synchronize()
+            out.append(e0.elapsed_time(e1))
+        return out
 
     def host_image_changed(self) -> None:
         """Call after modifying ``host_blob``: the next copy into each device buffer then waits
@@ -283,8 +296,15 @@ class WeightStream:
             stale = self._buf_version[buf] not in (-1, self._image_version)
             if stale and self._stepped[buf]:
                 self.stream.wait_event(self._last_step[buf])
+            if self.copy_marks is not None:
+                e0 = torch.cuda.Event(enable_timing=True)
+                e0.record(self.stream)
             self.dev_blobs[buf].copy_(self.host_blob, non_blocking=True)
             self.ready_events[buf].record(self.stream)
+            if self.copy_marks is not None:
+                e1 = torch.cuda.Event(enable_timing=True)
+                e1.record(self.stream)
+                self.copy_marks.append((e0, e1))
         self._buf_version[buf] = self._image_version
         self.staged[buf] = True
 
