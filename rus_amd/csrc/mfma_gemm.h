@@ -5,6 +5,8 @@
 // out of LDS with gfx950's transposing ds_read_b64_tr_b16.
 #pragma once
 
+#include <type_traits>
+
 #include "common.h"
 
 namespace rus {
@@ -358,14 +360,18 @@ constexpr int kDK64 = 64;
 constexpr int kStage64 = 2 * kBM * kDK64 * 2;  // 64 KiB
 constexpr int kSmem64 = 2 * kStage64;          // 128 KiB
 
-template <bool KN>
+template <int NW, bool KN>
 __device__ __forceinline__ void mainloop_k64(const GemmArgs& g, const Tile& tl, char* smem,
-                                             f32x16 (&acc)[kMT][2]) {
-  constexpr int NT = 2;
-  constexpr int PER = 8;  // copies per wave per stage (4 for A, 4 for B)
+                                             f32x16 (&acc)[kMT][16 / NW]) {
+  static_assert(NW == 4 || NW == 8, "four waves of 128 x 128 or eight of 128 x 64");
+  static_assert(!KN || NW == 8, "the N-contiguous B layout runs on eight waves");
+  constexpr int NT = 16 / NW;         // 32-column MFMA tiles per wave
+  constexpr int RW = kBN / (NW / 2);  // B rows (N) per wave: 128 or 64
+  constexpr int CP = 32 / NW;         // copies per wave per operand and stage: 8 or 4
+  constexpr int PER = 2 * CP;
   const int t = threadIdx.x, lane = t & 63;
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(t >> 6));
-  const int wm = wave >> 2, wn = wave & 3;
+  const int wm = wave / (NW / 2), wn = wave % (NW / 2);
   const int kb = tl.split * g.k_per_split;
   const int ke = min(kb + g.k_per_split, g.K);
   const int KT = ke > kb ? (ke - kb) / kDK64 : 0;
@@ -377,24 +383,24 @@ __device__ __forceinline__ void mainloop_k64(const GemmArgs& g, const Tile& tl, 
     __syncthreads();
     return;
   }
-  // Copies: instruction i of wave w fills bytes 1024 (8 i + w) .. +1024 of the stage's A tile
-  // (rows 8 (8 i + w) .. +8; lane l covers row + l/8 at position l%8, i.e. the chunk
+  // Copies: instruction i of wave w fills bytes 1024 (NW i + w) .. +1024 of the stage's A tile
+  // (rows 8 (NW i + w) .. +8; lane l covers row + l/8 at position l%8, i.e. the chunk
   // (l%8) ^ ((row >> 1) & 7)) and the same bytes of the B tile (K-contiguous as A; N-contiguous:
-  // K rows 2 (8 i + w) + l/32 of 512 bytes, lane l at position l%32 of its row r, the chunk
+  // K rows 2 (NW i + w) + l/32 of 512 bytes, lane l at position l%32 of its row r, the chunk
   // (l%32) ^ ((r & 3) << 2), columns n0 + 8 chunk .. +8).
   const char* gA = reinterpret_cast<const char*>(g.A);
   const char* gB = reinterpret_cast<const char*>(g.B);
-  uint32_t oa[4], ob[4];
+  uint32_t oa[CP], ob[CP];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int row = 8 * (8 * i + wave) + (lane >> 3);
+  for (int i = 0; i < CP; ++i) {
+    const int row = 8 * (NW * i + wave) + (lane >> 3);
     const int ch = (lane & 7) ^ ((row >> 1) & 7);
     // Rows (columns) past the matrix edge re-read the last one: finite values the epilogues
     // discard.
     const int ra_ = min(tl.m0 + row, g.M - 1);
     oa[i] = static_cast<uint32_t>((ra_ * g.lda + kb + ch * 8) * 2);
     if constexpr (KN) {
-      const int krow = 2 * (8 * i + wave) + (lane >> 5);
+      const int krow = 2 * (NW * i + wave) + (lane >> 5);
       const int col = min(tl.n0 + 8 * ((lane & 31) ^ ((krow & 3) << 2)), g.N - 8);
       ob[i] = static_cast<uint32_t>(((kb + krow) * g.ldb + col) * 2);
     } else {
@@ -407,95 +413,77 @@ __device__ __forceinline__ void mainloop_k64(const GemmArgs& g, const Tile& tl, 
     char* st = smem + (k & 1) * kStage64 + wave * 1024;
     const uint32_t abytes = k * (kDK64 * 2), bbytes = k * bstep;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      __builtin_amdgcn_global_load_lds(gA + oa[i] + abytes, (lds_void_ptr)(st + i * 8192), 16,
-                                       0, 0);
+    for (int i = 0; i < CP; ++i) {
+      __builtin_amdgcn_global_load_lds(gA + oa[i] + abytes, (lds_void_ptr)(st + i * NW * 1024),
+                                       16, 0, 0);
       __builtin_amdgcn_global_load_lds(gB + ob[i] + bbytes,
-                                       (lds_void_ptr)(st + kBM * 128 + i * 8192), 16, 0, 0);
+                                       (lds_void_ptr)(st + kBM * 128 + i * NW * 1024), 16, 0, 0);
     }
   };
   // Fragment addresses. A: row wm*128 + (l & 31) (+ 32 per MFMA tile: immediate 4096), chunk
   // 2 kk + l/32 at position chunk ^ ((l >> 1) & 7) (the low row bits are those of l). B
-  // K-contiguous likewise; N-contiguous: lane l of group g = l/16 (j = l%16) reads K row
-  // 16 kk + 8 (g/2) + j/4 (+ 4 for the high half), columns wn*64 + 32 nt + 16 (g%2) + 4 (j%4).
+  // K-contiguous likewise (rows wn*RW + ...); N-contiguous: lane l of group g = l/16 (j = l%16)
+  // reads K row 16 kk + 8 (g/2) + j/4 (+ 4 for the high half), columns wn*64 + 32 nt + 16 (g%2)
+  // + 4 (j%4).
   const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void_ptr)smem));
   const int sw = (lane >> 1) & 7, half = lane >> 5;
   uint32_t cpos[4];
 #pragma unroll
   for (int kk = 0; kk < 4; ++kk) cpos[kk] = static_cast<uint32_t>(((2 * kk + half) ^ sw) << 4);
   const uint32_t arow = lds0 + (wm * kWM + (lane & 31)) * 128;
-  const uint32_t brow = lds0 + kBM * 128 + (wn * 64 + (lane & 31)) * 128;
+  const uint32_t brow = lds0 + kBM * 128 + (wn * RW + (lane & 31)) * 128;
   uint32_t bk[NT];
   if constexpr (KN) {
     const int j = lane & 15, nh = (lane >> 4) & 1;
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
-      const int col = wn * 64 + nt * 32 + 16 * nh + 4 * (j & 3);
+      const int col = wn * RW + nt * 32 + 16 * nh + 4 * (j & 3);
       bk[nt] = lds0 + kBM * 128 + (8 * half + (j >> 2)) * kKNRowBytes +
                (((col >> 3) ^ ((j >> 2) << 2)) << 4) + (col & 7) * 2;
     }
   }
-  u32x4v fa0[kMT], fa1[kMT], fb0[NT], fb1[NT];
-  u32x2v lo0[NT], hi0[NT], lo1[NT], hi1[NT];
-  // Fragments of K step kk (0..3) of the stage at byte offset sb.
-  auto read0 = [&](uint32_t sb, int kk) {
+  u32x4v fa[2][kMT], fb[2][NT];
+  u32x2v lo[2][NT], hi[2][NT];
+  // Fragments of K step kk (0..3) of the stage at byte offset sb into register set S.
+  auto read = [&](auto S, uint32_t sb, int kk) {
+    constexpr int s = decltype(S)::value;
     const uint32_t a = arow + sb + cpos[kk];
-    fa0[0] = lds_read16<0>(a);
-    fa0[1] = lds_read16<4096>(a);
-    fa0[2] = lds_read16<8192>(a);
-    fa0[3] = lds_read16<12288>(a);
+    fa[s][0] = lds_read16<0>(a);
+    fa[s][1] = lds_read16<4096>(a);
+    fa[s][2] = lds_read16<8192>(a);
+    fa[s][3] = lds_read16<12288>(a);
     if constexpr (KN) {
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) {
-        lo0[nt] = lds_read8_tr<0>(bk[nt] + sb + kk * 16 * kKNRowBytes);
-        hi0[nt] = lds_read8_tr<4 * kKNRowBytes>(bk[nt] + sb + kk * 16 * kKNRowBytes);
+        lo[s][nt] = lds_read8_tr<0>(bk[nt] + sb + kk * 16 * kKNRowBytes);
+        hi[s][nt] = lds_read8_tr<4 * kKNRowBytes>(bk[nt] + sb + kk * 16 * kKNRowBytes);
       }
     } else {
-      fb0[0] = lds_read16<0>(brow + sb + cpos[kk]);
-      fb0[1] = lds_read16<4096>(brow + sb + cpos[kk]);
-    }
-  };
-  auto read1 = [&](uint32_t sb, int kk) {
-    const uint32_t a = arow + sb + cpos[kk];
-    fa1[0] = lds_read16<0>(a);
-    fa1[1] = lds_read16<4096>(a);
-    fa1[2] = lds_read16<8192>(a);
-    fa1[3] = lds_read16<12288>(a);
-    if constexpr (KN) {
-#pragma unroll
-      for (int nt = 0; nt < NT; ++nt) {
-        lo1[nt] = lds_read8_tr<0>(bk[nt] + sb + kk * 16 * kKNRowBytes);
-        hi1[nt] = lds_read8_tr<4 * kKNRowBytes>(bk[nt] + sb + kk * 16 * kKNRowBytes);
+      const uint32_t b = brow + sb + cpos[kk];
+      fb[s][0] = lds_read16<0>(b);
+      fb[s][1] = lds_read16<4096>(b);
+      if constexpr (NT == 4) {
+        fb[s][2] = lds_read16<8192>(b);
+        fb[s][3] = lds_read16<12288>(b);
       }
-    } else {
-      fb1[0] = lds_read16<0>(brow + sb + cpos[kk]);
-      fb1[1] = lds_read16<4096>(brow + sb + cpos[kk]);
     }
   };
-  auto wait0 = [&]() {
+  auto wait = [&](auto S) {
+    constexpr int s = decltype(S)::value;
     if constexpr (KN)
-      wait_frags_kn<NT>(fa0, lo0, hi0);
+      wait_frags_kn<NT>(fa[s], lo[s], hi[s]);
     else
-      wait_frags<NT>(fa0, fb0);
+      wait_frags<NT>(fa[s], fb[s]);
   };
-  auto wait1 = [&]() {
+  auto mma = [&](auto S) {
+    constexpr int s = decltype(S)::value;
     if constexpr (KN)
-      wait_frags_kn<NT>(fa1, lo1, hi1);
+      mma16_kn<NT>(fa[s], lo[s], hi[s], acc);
     else
-      wait_frags<NT>(fa1, fb1);
+      mma16<NT>(fa[s], fb[s], acc);
   };
-  auto mma0 = [&]() {
-    if constexpr (KN)
-      mma16_kn<NT>(fa0, lo0, hi0, acc);
-    else
-      mma16<NT>(fa0, fb0, acc);
-  };
-  auto mma1 = [&]() {
-    if constexpr (KN)
-      mma16_kn<NT>(fa1, lo1, hi1, acc);
-    else
-      mma16<NT>(fa1, fb1, acc);
-  };
+  using S0 = std::integral_constant<int, 0>;
+  using S1 = std::integral_constant<int, 1>;
   issue(0);
   if (KT > 1) issue(1);
   if (KT > 1)
@@ -503,37 +491,37 @@ __device__ __forceinline__ void mainloop_k64(const GemmArgs& g, const Tile& tl, 
   else
     wait_vmcnt<0>();
   __builtin_amdgcn_s_barrier();  // ... and every wave's
-  read0(0, 0);
-  wait0();
+  read(S0{}, 0, 0);
+  wait(S0{});
   for (int k = 0; k < KT; ++k) {
     const uint32_t sb = (k & 1) * kStage64;
-    read1(sb, 1);
+    read(S1{}, sb, 1);
     __builtin_amdgcn_sched_barrier(0);
-    mma0();
+    mma(S0{});
     __builtin_amdgcn_sched_barrier(0);
-    wait1();
-    read0(sb, 2);
+    wait(S1{});
+    read(S0{}, sb, 2);
     __builtin_amdgcn_sched_barrier(0);
-    mma1();
+    mma(S1{});
     __builtin_amdgcn_sched_barrier(0);
-    wait0();
-    read1(sb, 3);
+    wait(S0{});
+    read(S1{}, sb, 3);
     __builtin_amdgcn_sched_barrier(0);
-    mma0();
+    mma(S0{});
     __builtin_amdgcn_sched_barrier(0);
-    wait1();
+    wait(S1{});
     if (k + 1 < KT) {
       // Stage k + 1 has landed for every wave, and every wave has read stage k: its buffer
       // takes stage k + 2.
       wait_vmcnt<0>();
       __builtin_amdgcn_s_barrier();
       if (k + 2 < KT) issue(k + 2);
-      read0((sb ^ kStage64), 0);
+      read(S0{}, sb ^ kStage64, 0);
     }
     __builtin_amdgcn_sched_barrier(0);
-    mma1();
+    mma(S1{});
     __builtin_amdgcn_sched_barrier(0);
-    if (k + 1 < KT) wait0();
+    if (k + 1 < KT) wait(S0{});
   }
   __syncthreads();  // the epilogues reuse the LDS
 }
@@ -545,13 +533,13 @@ __device__ __forceinline__ void mainloop(const GemmArgs& g, const Tile& tl, char
 
 __device__ __forceinline__ void mainloop(const GemmArgs& g, const Tile& tl, char* smem,
                                          f32x16 (&acc)[kMT][2]) {
-  mainloop_k64<false>(g, tl, smem, acc);
+  mainloop_k64<8, false>(g, tl, smem, acc);
 }
 
 // The eight-wave mainloop with B stored [K, ldb] N-contiguous.
 __device__ __forceinline__ void mainloop_kn(const GemmArgs& g, const Tile& tl, char* smem,
                                             f32x16 (&acc)[kMT][2]) {
-  mainloop_k64<true>(g, tl, smem, acc);
+  mainloop_k64<8, true>(g, tl, smem, acc);
 }
 
 // Eight waves (two per SIMD): the accumulators of a 128 x 64 wave tile leave room for a second

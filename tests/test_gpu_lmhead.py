@@ -2,8 +2,8 @@
 
 Cases follow solution/test_kernels.py:189-226 (B=2, S=32, D=256, V=4099, chunk 1024, masked
 prompt labels) plus the BASELINE config 2 shape (N=2048, D=1536, V=151936, 10% labels -100),
-whose per-token results are checked against the oracle on a sample of tokens (each token's
-statistics and gradient row depend only on that token and the shared denominator).
+whose per-token results, hidden gradient and loss are checked against the oracle for every
+token.
 
 Tolerances (written per assertion): loss / entropy / lse within 1e-3 absolute; nll within 1e-3
 plus one fp16 ulp of the target logit (the fp32 accumulation order of an MFMA differs from the
@@ -93,8 +93,9 @@ def test_lmhead_unpadded_vocab_chunked(v_chunk):
     _check_against_oracle(h, w, lab, out, rows=rows, denom=denom)
 
 
-def test_lmhead_baseline_config2_sampled_tokens():
-    # H [2048,1536] ~ N(0,1), W [151936,1536] ~ N(0,0.02), 10% labels -100.
+def test_lmhead_baseline_config2_all_tokens():
+    # H [2048,1536] ~ N(0,1), W [151936,1536] ~ N(0,0.02), 10% labels -100:
+    # every token's statistics and hidden-gradient row against the oracle, and the loss.
     g = torch.Generator().manual_seed(0)
     N, D, V = 2048, 1536, 151936
     h = torch.randn(N, D, generator=g).half()
@@ -105,8 +106,8 @@ def test_lmhead_baseline_config2_sampled_tokens():
     torch.cuda.synchronize()
     denom = float(out[4].item())
     assert denom == float((lab != -100).sum())
-    rows = torch.randperm(N, generator=g)[:48]
-    _check_against_oracle(h, w, lab, out, rows=rows, denom=denom)
+    o = _check_against_oracle(h, w, lab, out, denom=denom)
+    assert abs(float(out[6].cpu()) - float(o["loss"])) <= 1e-3
     nll = out[0].cpu()
     assert torch.all(nll[lab == -100] == 0)
     # size-independent invariants over every token: 0 <= H <= ln V, lse >= max logit.
