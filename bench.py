@@ -402,7 +402,106 @@ def config_records(seed: int = 0, reps: int = 40) -> dict:
                    _time_rotating(lambda i: K.mlp_glu_bwd(douts[i], gus[i]), ns, reps), nbb,
                    input_sets=ns))
     out["4"] = c4
+    out["scaling"] = scaling_records(seed, reps)
     return out
+
+
+def scaling_records(seed: int = 0, reps: int = 40) -> list:
+    """The bandwidth-bound kernels at three sizes each: a launch of one row / token / unit (the
+    fixed cost of a launch: dispatch, wave start, first-load latency, drain), the BASELINE
+    configuration's shape, and a large shape whose transfer time dwarfs that fixed cost. Timed
+    like the configuration records (graph-replayed launches over rotating input sets);
+    ``frac_above_floor`` divides the algorithmic bytes by the time above the size-one launch."""
+    import torch
+
+    from rus_amd import kernels as K
+    from rus_amd import ops as O
+    from rus_amd import quant
+
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(seed + 7)
+    recs = []
+
+    def add(name, size, us, nbytes, floor_us, ns):
+        r = _hbm(name, size, us, nbytes, input_sets=ns)
+        if floor_us is not None and us > floor_us:
+            r["floor_us"] = floor_us
+            r["frac_above_floor"] = nbytes / ((us - floor_us) * 1e-6) / 1e9 / HBM_PEAK_GBS
+        recs.append(r)
+        return us
+
+    D = 1536
+    w = (1 + 0.05 * torch.randn(D, device=dev, generator=g)).half()
+    for tag, N in (("floor", 1), ("config", 880), ("large", 16384)):
+        nbytes = 4 * N * D * 2 + 2 * D + 4 * N
+        ns = _n_sets(nbytes)
+        xs = [(torch.randn(N, D, device=dev, generator=g).half(),
+               torch.randn(N, D, device=dev, generator=g).half()) for _ in range(ns)]
+        fw = [K.rms_norm_fwd(x, w, 1e-6, residual=r) for x, r in xs]
+        us_f = _time_rotating(lambda i: K.rms_norm_fwd(xs[i][0], w, 1e-6, residual=xs[i][1]),
+                              ns, reps)
+        us_b = _time_rotating(lambda i: K.rms_norm_bwd(xs[i][0], fw[i][1], w, fw[i][2],
+                                                       dresidual=xs[i][1]), ns, reps)
+        if tag == "floor":
+            floor_nf, floor_nb = us_f, us_b
+        add(f"rmsnorm_fwd residual ({tag})", [N, D], us_f, nbytes,
+            None if tag == "floor" else floor_nf, ns)
+        add(f"rmsnorm_bwd dresidual ({tag})", [N, D], us_b, nbytes,
+            None if tag == "floor" else floor_nb, ns)
+        del xs, fw
+    cos, sin = O.rope_cache(2048, 128, 1e6, dev)
+    for tag, n in (("floor", 1), ("config", 876), ("large", 16384)):
+        pos = (torch.arange(n, device=dev) % 2048)
+        ns = _n_sets(n * 12296)
+        rs = [(torch.randn(n, 2048, device=dev, generator=g).half(),
+               torch.randn(n, 1536, device=dev, generator=g).half(),
+               torch.randn(n, 256, device=dev, generator=g).half()) for _ in range(ns)]
+        outs = [K.qkv_rope_fwd(q, cos, sin, pos, ql, vl) for q, ql, vl in rs]
+        us_f = _time_rotating(lambda i: K.qkv_rope_fwd(rs[i][0], cos, sin, pos, rs[i][1],
+                                                       rs[i][2]), ns, reps)
+        us_b = _time_rotating(lambda i: K.qkv_rope_bwd(*outs[i], cos, sin, pos), ns, reps)
+        if tag == "floor":
+            floor_rf, floor_rb = us_f, us_b
+        add(f"rope_fwd lora ({tag})", [n, 12, 2, 128], us_f, n * 12296,
+            None if tag == "floor" else floor_rf, ns)
+        add(f"rope_bwd ({tag})", [n, 12, 2, 128], us_b, n * 8712,
+            None if tag == "floor" else floor_rb, ns)
+        del rs, outs
+    I = 8960
+    for tag, N in (("floor", 1), ("config", 880), ("large", 8192)):
+        nbf, nbb = N * 3 * I * 2, N * 5 * I * 2
+        ns = _n_sets(nbf)
+        gus = [torch.randn(N, 2 * I, device=dev, generator=g).half() for _ in range(ns)]
+        douts = [torch.randn(N, I, device=dev, generator=g).half() for _ in range(ns)]
+        us_f = _time_rotating(lambda i: K.mlp_glu_fwd(gus[i]), ns, reps)
+        us_b = _time_rotating(lambda i: K.mlp_glu_bwd(douts[i], gus[i]), ns, reps)
+        if tag == "floor":
+            floor_sf, floor_sb = us_f, us_b
+        add(f"swiglu_fwd ({tag})", [N, 2 * I], us_f, nbf,
+            None if tag == "floor" else floor_sf, ns)
+        add(f"swiglu_bwd in place ({tag})", [N, 2 * I], us_b, nbb,
+            None if tag == "floor" else floor_sb, ns)
+        del gus, douts
+    for tag, shape in (("floor", (64, 64)), ("config qkv", (2048, 1536)),
+                       ("large", (8192, 8192))):
+        part = quant.quantize_nf4((torch.randn(*shape, device=dev, generator=g) * 0.02).half())
+        n = shape[0] * shape[1]
+        nb = _nf4_bytes(n, part.absmax2.numel())
+        ns = _n_sets(nb)
+        sets = [(part.packed.clone(), part.absmax.clone(), part.absmax2.clone(),
+                 torch.empty(n, dtype=torch.float16, device=dev)) for _ in range(ns)]
+        code2 = part.code2.to(dev)
+
+        def launch(i):
+            p_, a_, a2_, o_ = sets[i]
+            K.dequant_nf4_tensor(p_, a_, code2, a2_, part.offset, shape, out_buf=o_)
+        us = _time_rotating(launch, ns, reps)
+        if tag == "floor":
+            floor_dq = us
+        add(f"nf4_dequant ({tag})", list(shape), us, nb, None if tag == "floor" else floor_dq, ns)
+        del sets
+    torch.cuda.empty_cache()
+    return recs
 
 
 def config_cpu_times(seed: int = 0) -> dict:
@@ -468,6 +567,20 @@ def config_cpu_times(seed: int = 0) -> dict:
     return out
 
 
+def _calibration_copies(dev, reps: int = 5) -> None:
+    """Five plain 128 MiB device-to-device copies: what FETCH_SIZE / WRITE_SIZE read for a known
+    number of bytes (the first copy kernels of a probe run; ``counter_summary`` scales by them)."""
+    import torch
+
+    src = torch.empty(64 << 20, dtype=torch.float16, device=dev).normal_()
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(f"probe: {reps} copies of {src.numel() * 2} bytes", flush=True)
+
+
 def elementwise_probe(reps: int = 5) -> None:
     """Fixed launches for counter runs of the bandwidth-bound kernels at their BASELINE shapes,
     each launch on input sets no earlier launch touched (so HBM, not the last-level cache,
@@ -511,6 +624,32 @@ def elementwise_probe(reps: int = 5) -> None:
     torch.cuda.synchronize()
     print(f"probe: {reps} launches each of rmsnorm fwd/bwd [{N},{D}], rope fwd/bwd "
           f"[{n3} tokens], swiglu fwd/bwd [{N},{2 * I}] on distinct inputs", flush=True)
+    del xs, fw, rs, qkvs, gus, outs
+    # the same kernels at large shapes (transfer time >> the launch's fixed cost), 3 launches
+    # each over 2 input sets
+    NL = 16384
+    xs = [(torch.randn(NL, D, device=dev, generator=g).half(),
+           torch.randn(NL, D, device=dev, generator=g).half()) for _ in range(2)]
+    fw = [K.rms_norm_fwd(xs[i % 2][0], w, 1e-6, residual=xs[i % 2][1]) for i in range(3)]
+    for i, (y, h, rstd) in enumerate(fw):
+        K.rms_norm_bwd(xs[i % 2][0], h, w, rstd, dresidual=xs[i % 2][1])
+    del xs, fw
+    posl = torch.arange(NL, device=dev) % 2048
+    rs = [(torch.randn(NL, 2048, device=dev, generator=g).half(),
+           torch.randn(NL, 1536, device=dev, generator=g).half(),
+           torch.randn(NL, 256, device=dev, generator=g).half()) for _ in range(2)]
+    qkvs = [K.qkv_rope_fwd(*rs[i % 2][:1], cos, sin, posl, *rs[i % 2][1:]) for i in range(3)]
+    for q, k, v in qkvs:
+        K.qkv_rope_bwd(q, k, v, cos, sin, posl)
+    del rs, qkvs
+    NS = 8192
+    gus = [torch.randn(NS, 2 * I, device=dev, generator=g).half() for _ in range(2)]
+    outs = [K.mlp_glu_fwd(gus[i % 2]) for i in range(3)]
+    for i, o in enumerate(outs):
+        K.mlp_glu_bwd(o, gus[i % 2])
+    torch.cuda.synchronize()
+    print(f"probe: 3 launches each of rmsnorm fwd/bwd [{NL},{D}], rope fwd/bwd [{NL} tokens], "
+          f"swiglu fwd/bwd [{NS},{2 * I}]", flush=True)
 
 
 def lmhead_probe(reps: int = 5) -> None:
@@ -522,6 +661,7 @@ def lmhead_probe(reps: int = 5) -> None:
     from rus_amd import kernels as K
 
     dev = torch.device("cuda:0")
+    _calibration_copies(dev)
     g = torch.Generator(device=dev).manual_seed(0)
     n, d, v = 2048, 1536, 151936
     h = torch.randn(n, d, device=dev, generator=g).half()
@@ -546,17 +686,11 @@ def kernel_probe(reps: int = 5) -> None:
     from rus_amd.hostload import WeightStream
 
     dev = torch.device("cuda:0")
+    _calibration_copies(dev)
     cfg = M.qwen2_1p5b()
     cfg1 = M.Qwen2Config(**{**cfg.__dict__, "num_hidden_layers": 1})
     model = M.build_random_qlora_qwen2(cfg1, dev, seed=0)
     ws = WeightStream(model.layers, dev, resident=True)
-    src = torch.empty(64 << 20, dtype=torch.float16, device=dev).normal_()
-    dst = torch.empty_like(src)
-    torch.cuda.synchronize()
-    for _ in range(reps):
-        dst.copy_(src)
-    torch.cuda.synchronize()
-    print(f"probe: {reps} copies of {src.numel() * 2} bytes", flush=True)
     from rus_amd import kernels as K
 
     x = torch.randn(707, cfg.hidden_size, device=dev).half()
@@ -573,6 +707,19 @@ def kernel_probe(reps: int = 5) -> None:
         ws.dequant_layer(0, norm=pend)
     torch.cuda.synchronize()
     print(f"probe: {reps} four-segment dequants of layer 0 with a riding norm backward", flush=True)
+    # the step's form: the input norm forward and the q / v LoRA-down (rank 16, dropout 0.05
+    # keep bits) ride in the layer's dequant launch
+    L0 = model.layers[0]
+    a_q, a_v = L0.q_A.detach().half().contiguous(), L0.v_A.detach().half().contiguous()
+    seed = torch.tensor([7], dtype=torch.int64, device=dev)
+    bits_q, bits_v = K.dropout_keep_bits(seed, 0, 2, x.shape[0], cfg.hidden_size, 0.05, 0.05)
+    for _ in range(reps):
+        *_, pend = K.rms_norm_fwd(x, lnw, 1e-6, residual=res, defer=True)
+        pend.carry_lora_down(a_q, a_v, bits_q, bits_v, 0.05, 0.05)
+        ws.dequant_layer(0, norm=pend)
+    torch.cuda.synchronize()
+    print(f"probe: {reps} four-segment dequants of layer 0 carrying the norm forward and the "
+          f"LoRA-down", flush=True)
 
 
 def gemm_parts_probe(reps: int = 5, n_tok: int = 707) -> None:
@@ -605,6 +752,101 @@ def gemm_parts_probe(reps: int = 5, n_tok: int = 707) -> None:
     print(f"probe: {reps} split-K products [{n_tok}, 17920] x [17920, 1536], {sp} partials, "
           f"{nbytes} algorithmic bytes per launch", flush=True)
     del ws, x, parts
+
+
+def step_probe(steps: int = 3) -> None:
+    """Fixed work for counter runs of every kernel in its in-step form: 5 plain 128 MiB device
+    copies (the FETCH_SIZE / WRITE_SIZE calibration), then eager training steps (the bench's
+    engine settings, AdamW) on the bench's first batch. One step runs under the per-launch timer
+    first and prints each launcher's launches and algorithmic bytes / FLOPs per step."""
+    import torch
+
+    from rus_amd import model as M
+    from rus_amd.kernels import KernelTimer
+    from rus_amd.ops import Qwen2FusedEngine
+
+    dev = torch.device("cuda:0")
+    src = torch.empty(64 << 20, dtype=torch.float16, device=dev).normal_()
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+    print(f"probe: 5 copies of {128 << 20} bytes", flush=True)
+    cfg = M.qwen2_1p5b()
+    model = M.build_random_qlora_qwen2(cfg, dev, seed=0)
+    batch = make_batches(cfg, 1, 4, 512, 0, dev)[0]
+    engine = Qwen2FusedEngine(model, dev, resident_weights=False, stream_unit="model",
+                              recompute=False, dequant_once=True)
+    opt = flat_adamw(engine)[0]
+    train_step(engine, opt, batch)
+    torch.cuda.synchronize()
+    with KernelTimer() as timer:
+        train_step(engine, opt, batch)
+    for name, r in sorted(timer.summary().items()):
+        print(json.dumps({"launcher": name, "launches_per_step": r["launches"],
+                          "bytes_per_launch": r["bytes"] / r["launches"],
+                          "flops_per_launch": r["flops"] / r["launches"]}), flush=True)
+    for _ in range(steps):
+        train_step(engine, opt, batch)
+    torch.cuda.synchronize()
+    print(f"probe: {steps} eager steps of {batch[3]} tokens after the timed one", flush=True)
+
+
+def counter_summary(paths: list[str]) -> None:
+    """Per-kernel averages of rocprofv3 counter runs (``--pmc ... --output-format csv``
+    counter_collection files): dispatches, mean duration under collection, and each counter per
+    dispatch. FETCH_SIZE / WRITE_SIZE are also given in MB scaled by what they read for the
+    largest plain device copy in the same file (bytes moved / counter), the calibration."""
+    import collections
+    import csv
+    import re
+
+    for path in paths:
+        rows = list(csv.DictReader(open(path)))
+        agg = collections.defaultdict(lambda: collections.defaultdict(list))
+        dur = collections.defaultdict(dict)
+        for r in rows:
+            n = r["Kernel_Name"]
+            if n.startswith(("Cijk", "Custom_Cijk")):
+                k = "hipBLASLt GEMMs"
+            else:
+                k = re.sub(r"^void |rus::\(anonymous namespace\)::|_ZN3rus12_GLOBAL__N_1\d+", "",
+                           n)
+                k = k.split("(")[0][:70]
+            k = (k, int(r["Grid_Size"]))  # one line per launch shape
+            agg[k][r["Counter_Name"]].append(float(r["Counter_Value"]))
+            dur[k][r["Dispatch_Id"]] = int(r["End_Timestamp"]) - int(r["Start_Timestamp"])
+        # calibration: the five plain 128 MiB device copies every probe runs before anything else
+        # (the first five copy kernels of the run; later copy kernels also move host data)
+        fetch_f = write_f = None
+        copies = sorted({int(r["Dispatch_Id"]) for r in rows if "copyBuffer" in r["Kernel_Name"]})
+        early = [r for r in rows if int(r["Dispatch_Id"]) in set(copies[:5])]
+        if early:
+            big = max(int(r["Grid_Size"]) for r in early)
+            cal = [(c, [float(r["Counter_Value"]) for r in early
+                        if r["Counter_Name"] == c and int(r["Grid_Size"]) == big])
+                   for c in ("FETCH_SIZE", "WRITE_SIZE")]
+            for c, vals in cal:
+                if vals:
+                    f = (128 << 20) / 1024 / (sum(vals) / len(vals))
+                    if c == "FETCH_SIZE":
+                        fetch_f = f
+                    else:
+                        write_f = f
+        print(f"## {path}")
+        if fetch_f or write_f:
+            print(f"calibration (128 MiB copy): fetch factor {fetch_f}, write factor {write_f}")
+        print("| kernel | grid | dispatches | mean us | counter | per dispatch | scaled MB |")
+        print("|---|---|---|---|---|---|---|")
+        for k, cs in sorted(agg.items(), key=lambda kv: -sum(dur[kv[0]].values())):
+            us = sum(dur[k].values()) / len(dur[k]) / 1e3
+            for c, v in sorted(cs.items()):
+                m = sum(v) / len(v)
+                f = fetch_f if c == "FETCH_SIZE" else write_f if c == "WRITE_SIZE" else None
+                mb = f"{m * 1024 * f / 1e6:.2f}" if f else ""
+                print(f"| {k[0]} | {k[1]} | {len(dur[k])} | {us:.2f} | {c} | {m:.1f} | {mb} |")
 
 
 def _print_record(rec: dict) -> None:
@@ -864,15 +1106,18 @@ def main() -> int:
     ap.add_argument("--no-ablation", action="store_true",
                     help="skip the timing of the other --recompute, --dequant-once and "
                          "--stream-unit settings")
+    ap.add_argument("--counter-summary", nargs="+", metavar="COUNTER_CSV",
+                    help="summarise rocprofv3 --pmc counter_collection CSVs per kernel")
     ap.add_argument("--trace-summary", metavar="KERNEL_TRACE_CSV",
                     help="print the per-step kernel time of the last --steps replays in a "
                          "rocprofv3 --kernel-trace CSV of a bench run, and exit")
     ap.add_argument("--probe", nargs="?", const="dequant",
                     choices=("dequant", "lmhead", "elementwise", "ceilings", "gemm",
-                             "gemm_parts"),
+                             "gemm_parts", "step"),
                     help="only fixed launches for counter runs: copy + dequant (default), the "
                          "lm_head CE kernels at config 2, the elementwise kernels on cold "
-                         "inputs, or the split-K MLP input gradient (gemm_parts); or printed "
+                         "inputs, the split-K MLP input gradient (gemm_parts), or eager "
+                         "training steps with every kernel in its in-step form (step); or printed "
                          "timings: streaming ceilings at the dequant's traffic (ceilings), "
                          "per-product GEMM times (gemm)")
     args = ap.parse_args()
@@ -897,6 +1142,12 @@ def main() -> int:
         return 0
     if args.probe == "gemm_parts":
         gemm_parts_probe()
+        return 0
+    if args.probe == "step":
+        step_probe()
+        return 0
+    if args.counter_summary:
+        counter_summary(args.counter_summary)
         return 0
     if args.probe:
         kernel_probe()
