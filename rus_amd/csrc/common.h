@@ -59,6 +59,36 @@ __device__ __forceinline__ void store_from_f32(T* __restrict__ p, const float (&
   *reinterpret_cast<Pack<T, N>*>(p) = t;
 }
 
+// 16-byte load with the non-temporal hint (global_load_dwordx4 ... nt), for inputs a launch reads
+// exactly once: their lines are not kept, so they do not displace the lines of the launch's
+// write stream. A SwiGLU forward over [8192, 17920] fp16 streams 0.68 of 8 TB/s with plain loads
+// and 0.79 with the hint on MI355X. Stores stay plain: the next launch reads a launch's outputs,
+// and non-temporal stores, which keep the lines out of the last-level cache, made the training
+// step slower (0.6-1.5%) although they raised isolated streaming rates.
+typedef uint32_t u32x4s __attribute__((ext_vector_type(4)));
+
+template <typename T, int N>
+__device__ __forceinline__ void load_f32_stream(const T* __restrict__ p, float (&out)[N]) {
+  static_assert((sizeof(T) * N) % 16 == 0, "whole 16-byte packs");
+  constexpr int E = 16 / sizeof(T);  // elements per 16-byte pack
+#pragma unroll
+  for (int c = 0; c < N / E; ++c) {
+    const u32x4s w = __builtin_nontemporal_load(reinterpret_cast<const u32x4s*>(p) + c);
+    const Pack<T, E> t = __builtin_bit_cast(Pack<T, E>, w);
+#pragma unroll
+    for (int i = 0; i < E; ++i) out[c * E + i] = static_cast<float>(t.v[i]);
+  }
+}
+
+// load_f32_stream for whole 16-byte packs, load_f32 otherwise (narrower packs of odd widths).
+template <typename T, int N>
+__device__ __forceinline__ void load_f32_once(const T* __restrict__ p, float (&out)[N]) {
+  if constexpr ((sizeof(T) * N) % 16 == 0)
+    load_f32_stream<T, N>(p, out);
+  else
+    load_f32<T, N>(p, out);
+}
+
 // Round through the storage type (fp32 -> T -> fp32), i.e. what a T-typed intermediate holds.
 template <typename T>
 __device__ __forceinline__ float round_to(float x) {
