@@ -34,9 +34,60 @@ struct alignas(sizeof(T) * N > 16 ? 16 : sizeof(T) * N) Pack {
   T v[N];
 };
 
+// Packs of 16 / 8 / 4 bytes move as one vector access of that width (the pack bit-cast to a
+// 32-bit-lane vector): a struct copy is a memcpy to the compiler, which it may split into 2-, 4-
+// and 8-byte pieces where control flow merges two stores of the same pack.
+typedef uint32_t u32x4s __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2s __attribute__((ext_vector_type(2)));
+
+template <int BYTES>
+struct VecOf {
+  typedef Pack<uint16_t, BYTES / 2> type;  // 2-byte packs (single fp16 elements)
+};
+template <>
+struct VecOf<16> {
+  typedef u32x4s type;
+};
+template <>
+struct VecOf<8> {
+  typedef u32x2s type;
+};
+template <>
+struct VecOf<4> {
+  typedef uint32_t type;
+};
+
+template <typename T, int N>
+__device__ __forceinline__ Pack<T, N> load_pack(const T* __restrict__ p) {
+  constexpr int B = sizeof(Pack<T, N>);
+  constexpr int C = B > 16 ? 16 : B;  // bytes per access: packs above 16 bytes go in 16-byte parts
+  typedef typename VecOf<C>::type V;
+  static_assert(sizeof(V) == C && B % C == 0, "whole accesses per pack");
+  const V* src = static_cast<const V*>(__builtin_assume_aligned(p, alignof(Pack<T, N>)));
+  V v[B / C];
+#pragma unroll
+  for (int k = 0; k < B / C; ++k) v[k] = src[k];
+  return __builtin_bit_cast(Pack<T, N>, v);
+}
+
+template <typename T, int N>
+__device__ __forceinline__ void store_pack(T* __restrict__ p, const Pack<T, N>& t) {
+  constexpr int B = sizeof(Pack<T, N>);
+  constexpr int C = B > 16 ? 16 : B;
+  typedef typename VecOf<C>::type V;
+  static_assert(sizeof(V) == C && B % C == 0, "whole accesses per pack");
+  struct Parts {
+    V v[B / C];
+  };
+  const Parts parts = __builtin_bit_cast(Parts, t);
+  V* dst = static_cast<V*>(__builtin_assume_aligned(p, alignof(Pack<T, N>)));
+#pragma unroll
+  for (int k = 0; k < B / C; ++k) dst[k] = parts.v[k];
+}
+
 template <typename T, int N>
 __device__ __forceinline__ void load_f32(const T* __restrict__ p, float (&out)[N]) {
-  const Pack<T, N> t = *reinterpret_cast<const Pack<T, N>*>(p);
+  const Pack<T, N> t = load_pack<T, N>(p);
 #pragma unroll
   for (int i = 0; i < N; ++i) out[i] = static_cast<float>(t.v[i]);
 }
@@ -56,7 +107,7 @@ __device__ __forceinline__ void store_from_f32(T* __restrict__ p, const float (&
   Pack<T, N> t;
 #pragma unroll
   for (int i = 0; i < N; ++i) t.v[i] = from_f32<T>(in[i]);
-  *reinterpret_cast<Pack<T, N>*>(p) = t;
+  store_pack<T, N>(p, t);
 }
 
 // 16-byte load with the non-temporal hint (global_load_dwordx4 ... nt), for inputs a launch reads
@@ -65,7 +116,6 @@ __device__ __forceinline__ void store_from_f32(T* __restrict__ p, const float (&
 // and 0.79 with the hint on MI355X. Stores stay plain: the next launch reads a launch's outputs,
 // and non-temporal stores, which keep the lines out of the last-level cache, made the training
 // step slower (0.6-1.5%) although they raised isolated streaming rates.
-typedef uint32_t u32x4s __attribute__((ext_vector_type(4)));
 
 template <typename T, int N>
 __device__ __forceinline__ void load_f32_stream(const T* __restrict__ p, float (&out)[N]) {

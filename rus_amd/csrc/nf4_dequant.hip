@@ -102,6 +102,11 @@ __device__ __forceinline__ float block_scale(const Nf4Args& a, uint32_t byte,
 
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 
+// One 16-byte store of four decoded words (a vector access, which the compiler keeps whole).
+__device__ __forceinline__ void store16(uint32_t* p, const uint4& w) {
+  *static_cast<u32x4s*>(__builtin_assume_aligned(p, 16)) = u32x4s{w.x, w.y, w.z, w.w};
+}
+
 // Decode one packed byte into the fp16x2 word (even element in the low half).
 __device__ __forceinline__ uint32_t decode_byte(uint32_t b, float scale,
                                                 const float* __restrict__ s_nf4) {
@@ -135,7 +140,7 @@ __device__ __forceinline__ void dequant_block(const Nf4Args& a, uint32_t blk, ui
       w.y = decode_byte((p[u] >> 8) & 0xffu, sc[u], s_nf4);
       w.z = decode_byte((p[u] >> 16) & 0xffu, sc[u], s_nf4);
       w.w = decode_byte(p[u] >> 24, sc[u], s_nf4);
-      reinterpret_cast<uint4*>(a.out)[base + u * kThreads] = w;
+      store16(a.out + 4 * (base + u * kThreads), w);
     }
   } else {
 #pragma unroll
@@ -157,7 +162,7 @@ __device__ __forceinline__ void dequant_block(const Nf4Args& a, uint32_t blk, ui
         w.y = decode_byte((p[u] >> 8) & 0xffu, sc[u], s_nf4);
         w.z = decode_byte((p[u] >> 16) & 0xffu, sc[u], s_nf4);
         w.w = decode_byte(p[u] >> 24, sc[u], s_nf4);
-        reinterpret_cast<uint4*>(a.out)[idx] = w;
+        store16(a.out + 4 * idx, w);
       }
     }
   }
@@ -232,7 +237,7 @@ __device__ __forceinline__ void dequant_block_tab(const Nf4Args& a, uint32_t blk
         r.y = static_cast<_Float16>(row[b & 15u]);
         ww[k] = __builtin_bit_cast(uint32_t, r);
       }
-      reinterpret_cast<uint4*>(a.out)[idx] = w;
+      store16(a.out + 4 * idx, w);
     }
   }
   // Trailing bytes past the last 4-byte unit (n_bytes % 4 != 0): the last block does them.

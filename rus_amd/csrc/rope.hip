@@ -122,7 +122,12 @@ __global__ __launch_bounds__(kThreads) void rope_fwd_kernel(RopeFwdArgs<T> a) {
   load_f32<T, kSpan>(row + j, lo);
   load_f32<T, kSpan>(row + j + half, hi);
 
-  if (hd >= a.h_q + a.h_kv) {  // V head: LoRA delta only
+  // Every head kind ends at the one pair of stores below: with a store site per branch the
+  // compiler merged the branches' stores and split them into 2-, 4- and 8-byte pieces.
+  const bool is_v = hd >= a.h_q + a.h_kv, is_q = hd < a.h_q;
+  float ol[kSpan], oh[kSpan];
+  T* o;
+  if (is_v) {  // V head: LoRA delta only
     const int kv = hd - a.h_q - a.h_kv;
     if constexpr (LORA == 2) {
       float m[R], dl[kSpan], dh[kSpan];
@@ -145,51 +150,52 @@ __global__ __launch_bounds__(kThreads) void rope_fwd_kernel(RopeFwdArgs<T> a) {
         hi[i] = hi[i] + dh[i] * a.scale_v;
       }
     }
-    T* o = a.v_out + (t * a.h_kv + kv) * a.head_dim;
-    store_from_f32<T, kSpan>(o + j, lo);
-    store_from_f32<T, kSpan>(o + j + half, hi);
-    return;
-  }
-
-  if constexpr (LORA == 2) {
-    if (hd < a.h_q) {
-      float m[R], dl[kSpan], dh[kSpan];
-      load_f32<T, R>(a.mid_q + t * R, m);
-      lora_up<T, R>(m, s_b, j, half, dl, dh);
+#pragma unroll
+    for (int i = 0; i < kSpan; ++i) {
+      ol[i] = lo[i];
+      oh[i] = hi[i];
+    }
+    o = a.v_out + (t * a.h_kv + kv) * a.head_dim;
+  } else {
+    if constexpr (LORA == 2) {
+      if (is_q) {
+        float m[R], dl[kSpan], dh[kSpan];
+        load_f32<T, R>(a.mid_q + t * R, m);
+        lora_up<T, R>(m, s_b, j, half, dl, dh);
+#pragma unroll
+        for (int i = 0; i < kSpan; ++i) {
+          lo[i] = lo[i] + dl[i] * a.scale_q;
+          hi[i] = hi[i] + dh[i] * a.scale_q;
+        }
+      }
+    }
+    if (HAS_LORA && is_q) {
+      float dl[kSpan], dh[kSpan];
+      const T* ql = a.q_lora + t * a.stride_ql + static_cast<int64_t>(hd) * a.head_dim;
+      load_f32<T, kSpan>(ql + j, dl);
+      load_f32<T, kSpan>(ql + j + half, dh);
 #pragma unroll
       for (int i = 0; i < kSpan; ++i) {
         lo[i] = lo[i] + dl[i] * a.scale_q;
         hi[i] = hi[i] + dh[i] * a.scale_q;
       }
     }
-  }
-  if (HAS_LORA && hd < a.h_q) {
-    float dl[kSpan], dh[kSpan];
-    const T* ql = a.q_lora + t * a.stride_ql + static_cast<int64_t>(hd) * a.head_dim;
-    load_f32<T, kSpan>(ql + j, dl);
-    load_f32<T, kSpan>(ql + j + half, dh);
+    const int64_t p = clamp_pos(a.pos, t, a.n_pos, a.err_flag);
+    float cl[kSpan], ch[kSpan], sl[kSpan], sh[kSpan];
+    const T* cr = a.cos + p * a.stride_cos;
+    const T* sr = a.sin + p * a.stride_cos;
+    load_f32<T, kSpan>(cr + j, cl);
+    load_f32<T, kSpan>(cr + j + half, ch);
+    load_f32<T, kSpan>(sr + j, sl);
+    load_f32<T, kSpan>(sr + j + half, sh);
 #pragma unroll
     for (int i = 0; i < kSpan; ++i) {
-      lo[i] = lo[i] + dl[i] * a.scale_q;
-      hi[i] = hi[i] + dh[i] * a.scale_q;
+      ol[i] = lo[i] * cl[i] - hi[i] * sl[i];
+      oh[i] = hi[i] * ch[i] + lo[i] * sh[i];
     }
+    o = is_q ? a.q_out + (t * a.h_q + hd) * a.head_dim
+             : a.k_out + (t * a.h_kv + (hd - a.h_q)) * a.head_dim;
   }
-  const int64_t p = clamp_pos(a.pos, t, a.n_pos, a.err_flag);
-  float cl[kSpan], ch[kSpan], sl[kSpan], sh[kSpan];
-  const T* cr = a.cos + p * a.stride_cos;
-  const T* sr = a.sin + p * a.stride_cos;
-  load_f32<T, kSpan>(cr + j, cl);
-  load_f32<T, kSpan>(cr + j + half, ch);
-  load_f32<T, kSpan>(sr + j, sl);
-  load_f32<T, kSpan>(sr + j + half, sh);
-  float ol[kSpan], oh[kSpan];
-#pragma unroll
-  for (int i = 0; i < kSpan; ++i) {
-    ol[i] = lo[i] * cl[i] - hi[i] * sl[i];
-    oh[i] = hi[i] * ch[i] + lo[i] * sh[i];
-  }
-  T* o = hd < a.h_q ? a.q_out + (t * a.h_q + hd) * a.head_dim
-                    : a.k_out + (t * a.h_kv + (hd - a.h_q)) * a.head_dim;
   store_from_f32<T, kSpan>(o + j, ol);
   store_from_f32<T, kSpan>(o + j + half, oh);
 }
@@ -225,54 +231,46 @@ __global__ __launch_bounds__(kThreads) void rope_bwd_kernel(RopeBwdArgs<T> a) {
   const int j = (slot - hd * per_head) * kSpan;
   T* out = a.dqkv + t * a.stride_dqkv + static_cast<int64_t>(hd) * a.head_dim;
 
-  float lo[kSpan], hi[kSpan];
-  if (hd >= a.h_q + a.h_kv) {  // dV: copy (and scale into dv_lora)
-    const int kv = hd - a.h_q - a.h_kv;
-    const T* src = a.dv + (t * a.h_kv + kv) * a.head_dim;
-    load_f32<T, kSpan>(src + j, lo);
-    load_f32<T, kSpan>(src + j + half, hi);
-    store_from_f32<T, kSpan>(out + j, lo);
-    store_from_f32<T, kSpan>(out + j + half, hi);
-    if (LORA_OUT) {
-#pragma unroll
-      for (int i = 0; i < kSpan; ++i) {
-        lo[i] = lo[i] * a.scale_v;
-        hi[i] = hi[i] * a.scale_v;
-      }
-      T* l = a.dv_lora + (t * a.h_kv + kv) * a.head_dim;
-      store_from_f32<T, kSpan>(l + j, lo);
-      store_from_f32<T, kSpan>(l + j + half, hi);
-    }
-    return;
-  }
-
-  const T* src = hd < a.h_q ? a.dq + (t * a.h_q + hd) * a.head_dim
-                            : a.dk + (t * a.h_kv + (hd - a.h_q)) * a.head_dim;
+  // One store site per output for every head kind (see rope_fwd_kernel).
+  const bool is_v = hd >= a.h_q + a.h_kv, is_q = hd < a.h_q;
+  const T* src = is_v ? a.dv + (t * a.h_kv + (hd - a.h_q - a.h_kv)) * a.head_dim
+                 : is_q ? a.dq + (t * a.h_q + hd) * a.head_dim
+                        : a.dk + (t * a.h_kv + (hd - a.h_q)) * a.head_dim;
+  float lo[kSpan], hi[kSpan], ol[kSpan], oh[kSpan];
   load_f32<T, kSpan>(src + j, lo);
   load_f32<T, kSpan>(src + j + half, hi);
-  const int64_t p = clamp_pos(a.pos, t, a.n_pos, a.err_flag);
-  float cl[kSpan], ch[kSpan], sl[kSpan], sh[kSpan];
-  const T* cr = a.cos + p * a.stride_cos;
-  const T* sr = a.sin + p * a.stride_cos;
-  load_f32<T, kSpan>(cr + j, cl);
-  load_f32<T, kSpan>(cr + j + half, ch);
-  load_f32<T, kSpan>(sr + j, sl);
-  load_f32<T, kSpan>(sr + j + half, sh);
-  float ol[kSpan], oh[kSpan];
+  if (is_v) {  // dV: copied (and scaled into dv_lora)
 #pragma unroll
-  for (int i = 0; i < kSpan; ++i) {
-    ol[i] = round_to<T>(lo[i] * cl[i] + hi[i] * sh[i]);
-    oh[i] = round_to<T>(hi[i] * ch[i] - lo[i] * sl[i]);
+    for (int i = 0; i < kSpan; ++i) {
+      ol[i] = lo[i];
+      oh[i] = hi[i];
+    }
+  } else {
+    const int64_t p = clamp_pos(a.pos, t, a.n_pos, a.err_flag);
+    float cl[kSpan], ch[kSpan], sl[kSpan], sh[kSpan];
+    const T* cr = a.cos + p * a.stride_cos;
+    const T* sr = a.sin + p * a.stride_cos;
+    load_f32<T, kSpan>(cr + j, cl);
+    load_f32<T, kSpan>(cr + j + half, ch);
+    load_f32<T, kSpan>(sr + j, sl);
+    load_f32<T, kSpan>(sr + j + half, sh);
+#pragma unroll
+    for (int i = 0; i < kSpan; ++i) {
+      ol[i] = round_to<T>(lo[i] * cl[i] + hi[i] * sh[i]);
+      oh[i] = round_to<T>(hi[i] * ch[i] - lo[i] * sl[i]);
+    }
   }
   store_from_f32<T, kSpan>(out + j, ol);
   store_from_f32<T, kSpan>(out + j + half, oh);
-  if (LORA_OUT && hd < a.h_q) {
+  if (LORA_OUT && (is_v || is_q)) {
+    const float sc = is_v ? a.scale_v : a.scale_q;
 #pragma unroll
     for (int i = 0; i < kSpan; ++i) {
-      ol[i] = ol[i] * a.scale_q;
-      oh[i] = oh[i] * a.scale_q;
+      ol[i] = ol[i] * sc;
+      oh[i] = oh[i] * sc;
     }
-    T* l = a.dq_lora + (t * a.h_q + hd) * a.head_dim;
+    T* l = is_v ? a.dv_lora + (t * a.h_kv + (hd - a.h_q - a.h_kv)) * a.head_dim
+                : a.dq_lora + (t * a.h_q + hd) * a.head_dim;
     store_from_f32<T, kSpan>(l + j, ol);
     store_from_f32<T, kSpan>(l + j + half, oh);
   }
@@ -389,41 +387,29 @@ __global__ __launch_bounds__(kThreads) void rope_bwd_mid_kernel(RopeBwdMidArgs m
   const int64_t bd = is_q ? d_q : d_v;
   const int64_t bc = static_cast<int64_t>(is_q ? hd : hd - a.h_q - a.h_kv) * a.head_dim + j;
   if (t < a.n_tokens) {
+    // One store site per output for every head kind (see rope_fwd_kernel).
     f16* out = a.dqkv + t * a.stride_dqkv + static_cast<int64_t>(hd) * a.head_dim;
-    float lo[kSpan], hi[kSpan];
-    if (is_v) {  // dV: copy, scale into dv_lora, d_mid_v partials
-      const int kv = hd - a.h_q - a.h_kv;
-      if (m.dv_part) {
-        const int grp = a.h_q / a.h_kv;
-        load_group_sum(m.dv_part, kv, grp, a.n_tokens, t, j, a.head_dim, lo);
-        load_group_sum(m.dv_part, kv, grp, a.n_tokens, t, j + half, a.head_dim, hi);
-      } else {
-        const f16* src = a.dv + (t * a.h_kv + kv) * a.head_dim;
-        load_f32<f16, kSpan>(src + j, lo);
-        load_f32<f16, kSpan>(src + j + half, hi);
-      }
-      store_from_f32<f16, kSpan>(out + j, lo);
-      store_from_f32<f16, kSpan>(out + j + half, hi);
+    const int kv = is_v ? hd - a.h_q - a.h_kv : hd - a.h_q;  // KV head of a k / v slot
+    float lo[kSpan], hi[kSpan], ol[kSpan], oh[kSpan];
+    const float* part = is_v ? m.dv_part : is_q ? nullptr : m.dk_part;
+    if (part) {  // dK / dV from the attention backward's per-query-head partials
+      const int grp = a.h_q / a.h_kv;
+      load_group_sum(part, kv, grp, a.n_tokens, t, j, a.head_dim, lo);
+      load_group_sum(part, kv, grp, a.n_tokens, t, j + half, a.head_dim, hi);
+    } else {
+      const f16* src = is_v ? a.dv + (t * a.h_kv + kv) * a.head_dim
+                       : is_q ? a.dq + (t * a.h_q + hd) * a.head_dim
+                              : a.dk + (t * a.h_kv + kv) * a.head_dim;
+      load_f32<f16, kSpan>(src + j, lo);
+      load_f32<f16, kSpan>(src + j + half, hi);
+    }
+    if (is_v) {  // dV: copied
 #pragma unroll
       for (int i = 0; i < kSpan; ++i) {
-        lo[i] = round_to<f16>(lo[i] * a.scale_v);  // the stored dv_lora values
-        hi[i] = round_to<f16>(hi[i] * a.scale_v);
+        ol[i] = lo[i];
+        oh[i] = hi[i];
       }
-      f16* l = a.dv_lora + (t * a.h_kv + kv) * a.head_dim;
-      store_from_f32<f16, kSpan>(l + j, lo);
-      store_from_f32<f16, kSpan>(l + j + half, hi);
-      mid_partial(p, lo, hi, bt, bd, bc, half);
     } else {
-      if (!is_q && m.dk_part) {
-        const int grp = a.h_q / a.h_kv;
-        load_group_sum(m.dk_part, hd - a.h_q, grp, a.n_tokens, t, j, a.head_dim, lo);
-        load_group_sum(m.dk_part, hd - a.h_q, grp, a.n_tokens, t, j + half, a.head_dim, hi);
-      } else {
-        const f16* src = is_q ? a.dq + (t * a.h_q + hd) * a.head_dim
-                              : a.dk + (t * a.h_kv + (hd - a.h_q)) * a.head_dim;
-        load_f32<f16, kSpan>(src + j, lo);
-        load_f32<f16, kSpan>(src + j + half, hi);
-      }
       const int64_t ps = clamp_pos(a.pos, t, a.n_pos, a.err_flag);
       float cl[kSpan], ch[kSpan], sl[kSpan], sh[kSpan];
       const f16* cr = a.cos + ps * a.stride_cos;
@@ -432,25 +418,26 @@ __global__ __launch_bounds__(kThreads) void rope_bwd_mid_kernel(RopeBwdMidArgs m
       load_f32<f16, kSpan>(cr + j + half, ch);
       load_f32<f16, kSpan>(sr + j, sl);
       load_f32<f16, kSpan>(sr + j + half, sh);
-      float ol[kSpan], oh[kSpan];
 #pragma unroll
       for (int i = 0; i < kSpan; ++i) {
         ol[i] = round_to<f16>(lo[i] * cl[i] + hi[i] * sh[i]);
         oh[i] = round_to<f16>(hi[i] * ch[i] - lo[i] * sl[i]);
       }
-      store_from_f32<f16, kSpan>(out + j, ol);
-      store_from_f32<f16, kSpan>(out + j + half, oh);
-      if (is_q) {
+    }
+    store_from_f32<f16, kSpan>(out + j, ol);
+    store_from_f32<f16, kSpan>(out + j + half, oh);
+    if (is_v || is_q) {  // the scaled LoRA gradient rows and their d_mid partials
+      const float sc = is_v ? a.scale_v : a.scale_q;
 #pragma unroll
-        for (int i = 0; i < kSpan; ++i) {
-          ol[i] = round_to<f16>(ol[i] * a.scale_q);  // the stored dq_lora values
-          oh[i] = round_to<f16>(oh[i] * a.scale_q);
-        }
-        f16* l = a.dq_lora + (t * a.h_q + hd) * a.head_dim;
-        store_from_f32<f16, kSpan>(l + j, ol);
-        store_from_f32<f16, kSpan>(l + j + half, oh);
-        mid_partial(p, ol, oh, bt, bd, bc, half);
+      for (int i = 0; i < kSpan; ++i) {
+        ol[i] = round_to<f16>(ol[i] * sc);  // the stored dq_lora / dv_lora values
+        oh[i] = round_to<f16>(oh[i] * sc);
       }
+      f16* l = is_v ? a.dv_lora + (t * a.h_kv + kv) * a.head_dim
+                    : a.dq_lora + (t * a.h_q + hd) * a.head_dim;
+      store_from_f32<f16, kSpan>(l + j, ol);
+      store_from_f32<f16, kSpan>(l + j + half, oh);
+      mid_partial(p, ol, oh, bt, bd, bc, half);
     }
   }
   __shared__ float red[kThreads / 16][kMidR];
