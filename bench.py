@@ -19,6 +19,7 @@ Usage: python bench.py [--gpus 1] [--steps 64] [--warmup 2]
 from __future__ import annotations
 
 import argparse
+import gc
 import json
 import math
 import os
@@ -808,14 +809,7 @@ def counter_summary(paths: list[str]) -> None:
         agg = collections.defaultdict(lambda: collections.defaultdict(list))
         dur = collections.defaultdict(dict)
         for r in rows:
-            n = r["Kernel_Name"]
-            if n.startswith(("Cijk", "Custom_Cijk")):
-                k = "hipBLASLt GEMMs"
-            else:
-                k = re.sub(r"^void |rus::\(anonymous namespace\)::|_ZN3rus12_GLOBAL__N_1\d+", "",
-                           n)
-                k = k.split("(")[0][:70]
-            k = (k, int(r["Grid_Size"]))  # one line per launch shape
+            k = (_kernel_label(r["Kernel_Name"]), int(r["Grid_Size"]))  # one line per launch shape
             agg[k][r["Counter_Name"]].append(float(r["Counter_Value"]))
             dur[k][r["Dispatch_Id"]] = int(r["End_Timestamp"]) - int(r["Start_Timestamp"])
         # calibration: the five plain 128 MiB device copies every probe runs before anything else
@@ -994,6 +988,25 @@ def gemm_probe(reps: int = 20) -> None:
                             _time_rotating(fn, 1, reps), fl, splits=splits))
 
 
+def _kernel_label(name: str) -> str:
+    """Short label of a kernel-trace name: hipBLASLt kernels as one label; demangled names cut at
+    their argument list; mangled ones (the profiler leaves templates over _Float16 mangled) as
+    name<template arguments, still mangled>, so instantiations stay apart."""
+    import re
+
+    if name.startswith(("Cijk", "Custom_Cijk")):
+        return "hipBLASLt GEMMs"
+    m = re.match(r"_ZN3rus12_GLOBAL__N_1(\d+)", name)
+    if m:
+        rest = name[m.end():]
+        ident, rest = rest[:int(m.group(1))], rest[int(m.group(1)):]
+        if rest.startswith("I") and "EE" in rest:
+            return f"{ident}<{rest[1:rest.index('EE')]}>"
+        return ident
+    k = re.sub(r"^void |rus::|\(anonymous namespace\)::", "", name)
+    return k.split("(")[0][:60]
+
+
 def trace_summary(path: str, steps: int) -> None:
     """Per-step kernel time of the last ``steps`` graph replays in a ``rocprofv3 --kernel-trace``
     CSV of a bench run: the replays are the kernels between the last steps + 1 launches of the
@@ -1015,12 +1028,7 @@ def trace_summary(path: str, steps: int) -> None:
     agg: dict = {}
     for r, d in zip(sel, dur):
         n = r["Kernel_Name"]
-        if n.startswith(("Cijk", "Custom_Cijk")):
-            k = "hipBLASLt GEMMs"
-        else:
-            k = re.sub(r"^void |rus::\(anonymous namespace\)::|_ZN3rus12_GLOBAL__N_1\d+", "", n)
-            k = k.split("(")[0].split("<")[0][:48]
-        a = agg.setdefault(k, [0, 0])
+        a = agg.setdefault(_kernel_label(n), [0, 0])
         a[0] += d
         a[1] += 1
     print(" ms/step  launches/step  us/launch  kernel")
@@ -1225,6 +1233,7 @@ def main() -> int:
                            "HBM, copy stream) during the timed steps; tokens/s ceiling = "
                            "tokens per step / copy time. Splitting the copy over 2 or 4 "
                            "streams gives the same 57.5 GB/s (PCIe link bound)"}
+    del ws  # the engine's buffers must go with the engine (the eager step's memory is measured later)
     device_peak = {"max_allocated_mib": torch.cuda.max_memory_allocated(dev) / 2**20,
                    "max_reserved_mib": torch.cuda.max_memory_reserved(dev) / 2**20,
                    "model_tensors_mib": model_mib,
@@ -1360,6 +1369,7 @@ def main() -> int:
         # fused engine and graph of this run freed, its device peak is comparable with the timed
         # run's (both include the random model's own tensors).
         del engine
+        gc.collect()  # the engines and captured graphs above hold reference cycles
         torch.cuda.synchronize()
         torch.cuda.empty_cache()
         eng_e = Qwen2FusedEngine(model, dev, resident_weights=True)
@@ -1380,6 +1390,7 @@ def main() -> int:
         out["eager_tokens_per_s"] = b[3] / (out["eager_ms_per_step"] / 1e3)
         out["eager_peak_hbm_mib"] = (torch.cuda.max_memory_allocated(dev) - base_e) / 2**20
         out["eager_device_peak_mib"] = torch.cuda.max_memory_allocated(dev) / 2**20
+        out["eager_base_mib"] = base_e / 2**20
         del eng_e
         torch.cuda.empty_cache()
 
