@@ -116,7 +116,6 @@ __device__ __forceinline__ void store_from_f32(T* __restrict__ p, const float (&
 // and 0.79 with the hint on MI355X. Stores stay plain: the next launch reads a launch's outputs,
 // and non-temporal stores, which keep the lines out of the last-level cache, made the training
 // step slower (0.6-1.5%) although they raised isolated streaming rates.
-
 template <typename T, int N>
 __device__ __forceinline__ void load_f32_stream(const T* __restrict__ p, float (&out)[N]) {
   static_assert((sizeof(T) * N) % 16 == 0, "whole 16-byte packs");
