@@ -1053,12 +1053,14 @@ def measured_traffic(kernel: str):
 
 
 def _graph_run(engine, model_opt, batches, steps, warmup, bucket=64):
-    """Captures the step's graphs for every batch bucket and times ``steps`` replays + AdamW."""
+    """Captures the step's graphs for every batch bucket and times ``steps`` replays + AdamW
+    (each replay's device time is kept: ``g.replay_ms()[warmup:]``)."""
     from rus_amd.graph import GraphedTrainStep
 
     g = GraphedTrainStep(engine, bucket=bucket)
     for b in batches:
         g.prepare(b[0], b[1], b[2])
+    g.time_replays()
     opt = flat_adamw(engine)[0]
     secs, tokens, _, _ = timed_run(engine, opt, batches, steps, warmup, graph=g)
     return tokens / secs, g
@@ -1216,8 +1218,15 @@ def main() -> int:
     ws = engine.weight_stream
     if ws.unit == "model":
         ws.time_copies()
+    if graph is not None:
+        graph.time_replays()
     secs, tokens, per_step, _ = timed_run(engine, opt_t, batches, args.steps, args.warmup,
                                           graph=graph)
+    replay_ms = None
+    if graph is not None:
+        rms = graph.replay_ms()[args.warmup:]
+        graph.time_replays(False)
+        replay_ms = statistics.fmean(rms) if rms else None
     h2d = None
     if ws.unit == "model":
         # the per-step copy of the packed model over PCIe, timed on the copy stream while the
@@ -1361,6 +1370,18 @@ def main() -> int:
         out["resident_weights_tokens_per_s"], g_r = _graph_run(eng_r, None, batches,
                                                                 min(args.steps, 16), 1,
                                                                 args.bucket)
+        r_ms = g_r.replay_ms()[1:]
+        if replay_ms is not None and r_ms and h2d is not None:
+            # same batches, whole cycles of the 8 in both runs: the replays' mean device time
+            out["step_replay"] = {
+                "streamed_ms": replay_ms, "resident_ms": statistics.fmean(r_ms),
+                "copy_ms": h2d["ms_per_copy"],
+                "note": "mean device time of one captured step's replay (events after its copy "
+                        "wait), streamed weights vs HBM-resident weights, same batches. The "
+                        "replay itself is the same kernels either way; while the next step's "
+                        "model copy saturates the PCIe link, the streamed replay runs longer "
+                        "(small kernels and the gaps between launches grow), so the streamed "
+                        "step is bounded by max(copy, streamed replay)"}
         del eng_r, g_r
         torch.cuda.empty_cache()
 

@@ -153,6 +153,7 @@ class GraphedTrainStep:
         self.grad_views = engine.lora_views(self.grad32)
         self.last = None
         self.census = census  # count each captured graph's node types (node_counts per bucket)
+        self.replay_marks: list | None = None  # (start, end) timing events per replay, when timing
         self.host_inputs: bool | None = None  # fixed by the first batch: host or device tensors
 
     # -- the captured body -----------------------------------------------------------------------
@@ -245,6 +246,18 @@ class GraphedTrainStep:
             g.instantiate()
         cap.graphs[buf] = g
 
+    def time_replays(self, on: bool = True) -> None:
+        """Starts (or stops) recording a pair of timing events around every replay."""
+        self.replay_marks = [] if on else None
+
+    def replay_ms(self) -> list[float]:
+        """Device time (ms) of each replay recorded since ``time_replays()`` (synchronises)."""
+        out = []
+        for e0, e1 in self.replay_marks or []:
+            e1.synchronize()
+            out.append(e0.elapsed_time(e1))
+        return out
+
     def prepare(self, input_ids, attention_mask=None, labels=None) -> None:
         """Captures the graph for this batch's bucket if it does not exist yet (no step taken)."""
         pb = self._pack(input_ids, attention_mask, labels)
@@ -260,7 +273,14 @@ class GraphedTrainStep:
         j = ws.next_buffer if ws.unit == "model" else 0  # the image paired with the weights
         cap.load(pb, lens, j)
         buf = ws.begin_step()  # waits for this step's whole-model copy (unit="model")
+        marks = self.replay_marks
+        if marks is not None:  # recorded after the copy wait: the events bracket the replay only
+            marks.append((torch.cuda.Event(enable_timing=True),
+                          torch.cuda.Event(enable_timing=True)))
+            marks[-1][0].record()
         cap.graphs[buf].replay()
+        if marks is not None:
+            marks[-1][1].record()
         ws.after_replay()
         ws.end_step(buf)
         for p, v in zip(self.engine.lora_params, self.grad_views):

@@ -8,6 +8,7 @@
 * Streamed weights (per-layer slots with the copies captured in the graph, or whole-model
   buffers copied outside it) and resident weights agree bitwise.
 * The captured graphs contain no memset nodes.
+* ``time_replays()`` brackets each replay with one event pair, and only while it is on.
 """
 
 from __future__ import annotations
@@ -150,6 +151,7 @@ def test_graph_replays_repeatable_across_buckets(unit):
     ref_loss = float(gs.step(*a))
     torch.cuda.synchronize()
     ref_grads = _grads(engine)
+    gs.time_replays()  # an event pair around each replay (after its copy wait)
     for it in range(3):
         x = torch.randn(256, 256, device=DEV)  # unrelated eager work between replays
         (x @ x).sum().item()
@@ -160,6 +162,11 @@ def test_graph_replays_repeatable_across_buckets(unit):
         assert loss == ref_loss, it
         for g0, g1 in zip(ref_grads, _grads(engine)):
             assert torch.equal(g0, g1), it
+    ms = gs.replay_ms()
+    assert len(ms) == 6 and all(0 < t < 1e4 for t in ms), ms
+    gs.time_replays(False)
+    gs.step(*a)
+    assert gs.replay_ms() == []
     assert len(gs.graphs) == 2
     for cap in gs.graphs.values():
         # one graph per whole-model weight buffer
