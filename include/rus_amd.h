@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define RUS_ABI_VERSION 16
+#define RUS_ABI_VERSION 17
 
 #define RUS_DTYPE_F16 0
 #define RUS_DTYPE_F32 1
@@ -701,10 +701,10 @@ int rus_attn_varlen_fwd(const void* q, const void* k, const void* v, const int32
 /*
  * Backward of rus_attn_varlen_fwd: dq like q, dk / dv like k / v (fp16; dk and dv sum the h_q /
  * h_kv query heads of each group in fp32 and are rounded once). out and lse are the forward's.
- * workspace: fp32, at least round_up(h_q * n_tokens, 64) + 2 * h_q * n_tokens * 128 elements
- * (D = rowsum(dO o O) [h_q, n_tokens], padded to 64; then per-query-head dK and dV partials
- * [h_q, n_tokens, 128] each, dK scaled). A small kernel forms D, then both passes (dQ, and
- * dK / dV with the sum over each group's heads) run as one launch; max_blocks at most 32767.
+ * workspace: fp32, at least 2 * h_q * n_tokens * 128 elements (per-query-head dK and dV
+ * partials [h_q, n_tokens, 128] each, dK scaled). Both passes (dQ, and dK / dV with the sum over
+ * each group's heads) run as one launch, each block forming D = rowsum(dO o O) of the query rows
+ * it visits; max_blocks at most 32767.
  * counters: int32, at least max_blocks * h_kv, zero before the first call and left zero (calls
  * sharing them must not run concurrently).
  * Replaces: the autograd backward of solution/ops.py:669-696 (torch SDPA backward plus the

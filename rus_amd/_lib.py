@@ -11,7 +11,7 @@ import threading
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "librus_amd.so"
-ABI_VERSION = 16
+ABI_VERSION = 17
 
 DTYPE_F16 = 0
 DTYPE_F32 = 1

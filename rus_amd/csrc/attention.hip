@@ -22,9 +22,10 @@
 //     which the transposed reads produce (two reads of 4 consecutive tokens per fragment);
 //   * P and dS are rounded to fp16 for their MFMAs, as flash attention does; O, LSE, dQ, dK, dV
 //     accumulate in fp32;
-//   * backward: a small kernel forms D = rowsum(dO o O); one launch then runs the dK / dV blocks
-//     (row, key block, query head; fp32 dK / dV partials per query head) and the dQ blocks
-//     (row, query block, head). The h_q / h_kv partials of a KV group are summed in head order
+//   * backward: one launch runs the dK / dV blocks (row, key block, query head; fp32 dK / dV
+//     partials per query head) and the dQ blocks (row, query block, head); each block forms
+//     D = rowsum(dO o O) of the query rows it visits from the dO tile in LDS and O rows loaded
+//     with that tile (no separate launch, no D array). The h_q / h_kv partials of a KV group are summed in head order
 //     and rounded once, either by the last of the group's blocks to finish a key block (arrival
 //     counter; no atomics on data) or, in the engine's path, by the RoPE backward that packs
 //     them (rus_qkv_rope_bwd_mid_parts).
@@ -56,7 +57,6 @@ struct AttnArgs {
   const int32_t* cu;
   f16* out;        // forward: O; backward kernel 1: dQ
   float* lse;      // [h_q, n_tok], natural log
-  float* dsum;     // backward: D = rowsum(dO o O) [h_q, n_tok]
   float* dk_part;  // [h_q, n_tok, 128]
   float* dv_part;
   f16* dk;         // [n_tok, h_kv, 128]
@@ -415,29 +415,78 @@ __device__ __forceinline__ void merge_b(const float* buf, int wave, int lane,
   }
 }
 
-// D[head][t] = rowsum(dO o O) over the head's 128 dims: 16 lanes per (token, head), 8 fp32
-// products of fp16 values per lane, summed in dim order, then over the lanes by a butterfly.
-__global__ __launch_bounds__(256) void attn_bwd_prep_kernel(const f16* __restrict__ o,
-                                                            const f16* __restrict__ dout,
-                                                            float* __restrict__ dsum,
-                                                            int64_t n_tok, int h_q) {
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-  const int64_t pair = i >> 4;  // token * h_q + head
-  const int c = static_cast<int>(i & 15);
+// D = rowsum(dO o O) of the 32 query rows of a block, formed where it is used: the dO tile is in
+// LDS and the O rows come in registers (ORows, loaded with the tiles). Pass p covers rows 4 p ..
+// 4 p + 3: lane l takes row 4 p + l / 16, head dims 8 (l % 16) .. + 8, sums their 8 fp32 products
+// of fp16 values in dim order, then the 16 lanes of a row add by a butterfly (xor 8, 4, 2, 1);
+// every lane of the group then holds the row's D. Rows past the row's end repeat its last token
+// (as the tiles do), so they hold that token's D.
+struct ORows {
+  f16x8 v[8];
+};
+
+__device__ __forceinline__ void load_o_rows(ORows& o, const f16* oh, int64_t stride, int r0,
+                                            int lo, int hi) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int p = 0; p < 8; ++p) {
+    int t = r0 + 4 * p + (lane >> 4);
+    t = t < hi ? t : hi - 1;
+    t = t < lo ? lo : t;
+    o.v[p] = *reinterpret_cast<const f16x8*>(oh + static_cast<int64_t>(t) * stride +
+                                             8 * (lane & 15));
+  }
+}
+
+// x of the lane N places further round its 16-lane row (DPP row_ror: a VALU move, no LDS).
+template <int N>
+__device__ __forceinline__ float row_ror(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x),
+                                                               0x120 + N, 0xF, 0xF, false));
+}
+
+// The butterfly adds lane c's sum to lane c ^ 8's, then c ^ 4's, c ^ 2's, c ^ 1's. After the
+// step with 8 a lane's sum depends on c mod 8 only, so the lane c + 4 (mod 16) holds what c ^ 4
+// holds; likewise for 2 and 1: rotations give the same sums as the xor exchanges.
+__device__ __forceinline__ float row_dsum(const ORows& o, const char* dt, int p) {
+  const int lane = threadIdx.x & 63;
+  const f16x8 y = tile_frag(dt, 4 * p + (lane >> 4), lane & 15);
   float acc = 0.0f;
-  if (pair < n_tok * h_q) {
-    const f16x8 x = *reinterpret_cast<const f16x8*>(o + pair * kHD + 8 * c);
-    const f16x8 y = *reinterpret_cast<const f16x8*>(dout + pair * kHD + 8 * c);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) acc += static_cast<float>(x[e]) * static_cast<float>(y[e]);
-  }
+  for (int e = 0; e < 8; ++e) acc += static_cast<float>(o.v[p][e]) * static_cast<float>(y[e]);
+  acc += row_ror<8>(acc);
+  acc += row_ror<4>(acc);
+  acc += row_ror<2>(acc);
+  acc += row_ror<1>(acc);
+  return acc;
+}
+
+// D of the rows this lane's accumulator registers cover (register r: row acc_row(r, h)).
+__device__ __forceinline__ void dsum_acc_rows(const ORows& o, const char* dt, int h,
+                                              float (&d)[16]) {
 #pragma unroll
-  for (int off = 8; off >= 1; off >>= 1) acc += __shfl_xor(acc, off, 16);
-  if (pair < n_tok * h_q && c == 0) {
-    const int64_t t = pair / h_q;
-    const int head = static_cast<int>(pair - t * h_q);
-    dsum[head * n_tok + t] = acc;
+  for (int p = 0; p < 8; ++p) {
+    const float s = row_dsum(o, dt, p);
+    // rows 4 p + g sit in lanes 16 g .. 16 g + 15; acc_row(4 j + g, h) = 4 (2 j + h) + g, so
+    // the lanes of half h = p % 2 take them as registers 4 (p / 2) + g
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const float v = __builtin_bit_cast(
+          float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, s), 16 * g));
+      if ((p & 1) == h) d[4 * (p >> 1) + g] = v;
+    }
   }
+}
+
+// D of tile row c (this lane's query column in the dQ blocks).
+__device__ __forceinline__ float dsum_row(const ORows& o, const char* dt, int c) {
+  float d = 0.0f;
+#pragma unroll
+  for (int p = 0; p < 8; ++p) {
+    const float s = __shfl(row_dsum(o, dt, p), 16 * (c & 3), 64);
+    if ((c >> 2) == p) d = s;
+  }
+  return d;
 }
 
 // dQ = scale * dS K. Block = (row, query block, head): the Q and dO tiles of its 32 queries are
@@ -463,11 +512,13 @@ __device__ __forceinline__ void attn_bwd_dq_block(const AttnArgs& a, int blk, ch
     tile_copy(kt, kh, skv, k0, start, end, 0, 8);
     tile_copy(vt, vh, skv, k0, start, end, 0, 8);
   }
+  ORows orow;
+  load_o_rows(orow, a.o + head * kHD, sq, q0, start, end);
   const int qi = q0 + col, qr = qi < end ? qi : end - 1;
-  const float dsum = a.dsum[head * a.n_tok + qr];
   const float lse2 = a.lse[head * a.n_tok + qr] * kLog2e;
   wait_copies();
   __syncthreads();  // every wave's share of the Q and dO tiles has landed
+  const float dsum = dsum_row(orow, dt, col);  // D of this lane's query (tile row col)
 
   f32x16 dq[4];
 #pragma unroll
@@ -539,7 +590,7 @@ __device__ __forceinline__ void attn_bwd_dkdv_block(const AttnArgs& a, int blk, 
   const f16* qh = a.q + head * kHD;
   const f16* doh = a.dout + head * kHD;
   const float* lse = a.lse + head * a.n_tok;
-  const float* dsum = a.dsum + head * a.n_tok;
+  const f16* oh = a.o + head * kHD;
   char* kt = smem;
   char* vt = smem + kTile;
   char* qt = smem + (2 + 2 * wave) * kTile;
@@ -547,14 +598,20 @@ __device__ __forceinline__ void attn_bwd_dkdv_block(const AttnArgs& a, int blk, 
   const int nq = (end - k0 + kBlk - 1) / kBlk;  // query blocks from the diagonal to the row end
   tile_copy(kt, a.k + g * kHD, skv, k0, start, end, kCopiesPerWave * wave, kCopiesPerWave);
   tile_copy(vt, a.v + g * kHD, skv, k0, start, end, kCopiesPerWave * wave, kCopiesPerWave);
+  ORows orow;  // the O rows of the wave's next query block, loaded with its tiles
   if (wave < nq) {
     const int q0 = k0 + wave * kBlk;
     tile_copy(qt, qh, sq, q0, start, end, 0, 8);
     tile_copy(dt, doh, sq, q0, start, end, 0, 8);
+    load_o_rows(orow, oh, sq, q0, start, end);
   }
   const int kj = k0 + col;  // this lane's key (column of S = Q K^T)
   wait_copies();
   __syncthreads();  // every wave's share of the K and V tiles has landed
+  // D of the query rows of this lane's registers, for the wave's current query block; formed
+  // once its dO tile and O rows have landed, so the O rows are not held across the products
+  float dsum[16] = {};
+  if (wave < nq) dsum_acc_rows(orow, dt, h, dsum);
 
   f32x16 dk[4], dv[4];
 #pragma unroll
@@ -580,7 +637,7 @@ __device__ __forceinline__ void attn_bwd_dkdv_block(const AttnArgs& a, int blk, 
       float p = exp2_raw(st[r] * a.scale_log2 - lse[qc] * kLog2e);
       if (edge) p = (kj <= qi && qi < end) ? p : 0.0f;
       st[r] = p;                         // P
-      dp[r] = p * (dp[r] - dsum[qc]);    // dS
+      dp[r] = p * (dp[r] - dsum[r]);     // dS
     }
     const f16x8 p0 = frag_acc(st, 0), p1 = frag_acc(st, 1);
     const f16x8 s0 = frag_acc(dp, 0), s1 = frag_acc(dp, 1);
@@ -596,7 +653,9 @@ __device__ __forceinline__ void attn_bwd_dkdv_block(const AttnArgs& a, int blk, 
       const int q1 = q0 + kWB * kBlk;
       tile_copy(qt, qh, sq, q1, start, end, 0, 8);
       tile_copy(dt, doh, sq, q1, start, end, 0, 8);
+      load_o_rows(orow, oh, sq, q1, start, end);
       wait_copies();
+      dsum_acc_rows(orow, dt, h, dsum);
     }
   }
   // Sum the waves' partials (dK, then dV through the same buffer) and store this head's fp32
@@ -759,11 +818,10 @@ static int attn_bwd(const char* fn, const void* q, const void* k, const void* v,
   a.h_kv = h_kv;
   a.scale = scale;
   a.scale_log2 = scale * kLog2e;
-  // workspace: D [h_q, n_tok] (padded to 64 floats) | dk_part [h_q, n_tok, 128] | dv_part (alike)
+  // workspace: dk_part [h_q, n_tok, 128] | dv_part (alike)
   if (2 * static_cast<int64_t>(max_blocks) > 65535)
     return fail(RUS_ERR_UNSUPPORTED, "%s: max_blocks=%d (at most 32767)", fn, max_blocks);
-  a.dsum = workspace;
-  a.dk_part = workspace + ((static_cast<int64_t>(h_q) * n_tokens + 63) / 64) * 64;
+  a.dk_part = workspace;
   a.dv_part = a.dk_part + static_cast<int64_t>(h_q) * n_tokens * kHD;
   hipStream_t st = static_cast<hipStream_t>(stream);
   a.out = static_cast<f16*>(dq);
@@ -772,9 +830,6 @@ static int attn_bwd(const char* fn, const void* q, const void* k, const void* v,
   a.counters = counters;
   a.max_blocks = max_blocks;
   a.group_sum = group_sum ? 1 : 0;
-  const int64_t prep_threads = n_tokens * h_q * 16;
-  hipLaunchKernelGGL(attn_bwd_prep_kernel, dim3(static_cast<unsigned>((prep_threads + 255) / 256)),
-                     dim3(256), 0, st, a.o, a.dout, a.dsum, n_tokens, h_q);
   hipLaunchKernelGGL(attn_bwd_kernel, dim3(h_q, 2 * max_blocks), dim3(64 * kWB), 0, st, a);
   return check_launch(fn);
 }

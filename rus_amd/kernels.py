@@ -1689,9 +1689,9 @@ def attn_varlen_bwd(dout: torch.Tensor, q: torch.Tensor, k: torch.Tensor, v: tor
     dq = torch.empty_like(q)
     dk = torch.empty_like(k)
     dv = torch.empty_like(v)
-    ws = torch.empty(_round_up(hq * n, 64) + 2 * hq * n * d, dtype=torch.float32,
-                     device=q.device)
-    nbytes = 2 * (4 * q.numel() + 4 * k.numel()) + 4 * 2 * hq * n * d * 2 + lse.numel() * 8
+    ws = torch.empty(2 * hq * n * d, dtype=torch.float32, device=q.device)
+    # q, dO, O, dQ; k, v, dK, dV; the partials written and read back; lse
+    nbytes = 2 * (4 * q.numel() + 4 * k.numel()) + 4 * 2 * hq * n * d * 2 + lse.numel() * 4
     cnt = _counter_buffer(_attn_counters, q.device, mb * k.shape[1])
     _launch("attn_bwd", nbytes, 2.5 * _attn_flops(lens, hq), "rus_attn_varlen_bwd",
             q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), dout.data_ptr(),
@@ -1720,15 +1720,15 @@ def attn_varlen_bwd_parts(dout: torch.Tensor, q: torch.Tensor, k: torch.Tensor, 
     mb = attn_max_blocks(n, n_rows) if max_blocks is None else int(max_blocks)
     scale = 1.0 / math.sqrt(d) if scale is None else float(scale)
     dq = torch.empty_like(q)
-    off = _round_up(hq * n, 64)
-    ws = torch.empty(off + 2 * hq * n * d, dtype=torch.float32, device=q.device)
-    nbytes = 2 * (4 * q.numel() + 2 * k.numel()) + 4 * 2 * hq * n * d + lse.numel() * 8
+    ws = torch.empty(2 * hq * n * d, dtype=torch.float32, device=q.device)
+    # q, dO, O, dQ; k, v; the partials written; lse
+    nbytes = 2 * (4 * q.numel() + 2 * k.numel()) + 4 * 2 * hq * n * d + lse.numel() * 4
     _launch("attn_bwd", nbytes, 2.5 * _attn_flops(lens, hq), "rus_attn_varlen_bwd_parts",
             q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), dout.data_ptr(),
             lse.data_ptr(), cu_seqlens.data_ptr(), n_rows, n, mb, hq, k.shape[1], d, scale,
             dq.data_ptr(), ws.data_ptr(), _stream(q))
-    dk_part = ws[off: off + hq * n * d].view(hq, n, d)
-    dv_part = ws[off + hq * n * d:].view(hq, n, d)
+    dk_part = ws[: hq * n * d].view(hq, n, d)
+    dv_part = ws[hq * n * d:].view(hq, n, d)
     return dq, dk_part, dv_part
 
 
