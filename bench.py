@@ -891,6 +891,90 @@ def ceilings_probe(reps: int = 40) -> None:
         _print_record(r)
 
 
+def contention_probe(steps: int = 24, warmup: int = 8) -> None:
+    """Device time of one captured step's replay (events after its copy wait, mean over whole
+    cycles of the bench's 8 batches) for (a) HBM-resident weights; (b) the same resident graph
+    while an unrelated host-to-device copy of the model image's size loops on a side stream;
+    (c) the resident graph with one such copy per step on the side stream and each step waiting
+    (a stream wait) for the previous step's copy; (d) the bench's streamed engine (whose own
+    per-step copy runs beside it and gates the next step). Shows which of a concurrent PCIe
+    copy and a step tied to the copies lengthens the replay. Prints JSON records."""
+    import torch
+
+    from rus_amd import model as M
+    from rus_amd.graph import GraphedTrainStep
+    from rus_amd.ops import Qwen2FusedEngine
+
+    dev = torch.device("cuda:0")
+    torch.manual_seed(0)
+    cfg = M.qwen2_1p5b()
+    model = M.build_random_qlora_qwen2(cfg, dev, seed=0)
+    batches = make_batches(cfg, 8, 4, 512, 0, dev)
+
+    def replays(engine, side_copy=None, tied=False):
+        g = GraphedTrainStep(engine, bucket=64)
+        for b in batches:
+            g.prepare(b[0], b[1], b[2])
+        opt = flat_adamw(engine)[0]
+        if side_copy is not None:
+            side_copy()
+        ws = engine.weight_stream
+        begin = ws.begin_step
+        if tied:  # each step copies once on the side stream and waits for the previous copy
+            done = []
+
+            def begin_tied():
+                buf = begin()
+                if done:
+                    torch.cuda.current_stream(dev).wait_event(done[-1])
+                with torch.cuda.stream(side):
+                    dst.copy_(host, non_blocking=True)
+                    done.append(torch.cuda.Event())
+                    done[-1].record(side)
+                return buf
+
+            ws.begin_step = begin_tied
+        for i in range(warmup):
+            train_step(engine, opt, batches[i % len(batches)], g)
+        g.time_replays()
+        for i in range(steps):
+            train_step(engine, opt, batches[(warmup + i) % len(batches)], g)
+        ms = g.replay_ms()
+        torch.cuda.synchronize()
+        ws.begin_step = begin
+        return statistics.fmean(ms), [round(x, 3) for x in ms[:8]], [round(x, 3) for x in ms[-8:]]
+
+    eng_s = Qwen2FusedEngine(model, dev, resident_weights=False, stream_unit="model",
+                             recompute=False, dequant_once=True)
+    image_bytes = eng_s.weight_stream.model_bytes
+    eng_r = Qwen2FusedEngine(model, dev, resident_weights=True, recompute=False,
+                             dequant_once=True)
+    host = torch.empty(image_bytes, dtype=torch.uint8, pin_memory=True)
+    dst = torch.empty(image_bytes, dtype=torch.uint8, device=dev)
+    side = torch.cuda.Stream(device=dev)  # default priority
+
+    def copy_loop():  # enough copies to outlast the warm-up and timed replays
+        with torch.cuda.stream(side):
+            for _ in range(warmup + steps + 8):
+                dst.copy_(host, non_blocking=True)
+
+    recs = []
+    for label, eng, loop, tied in (
+            ("resident weights", eng_r, None, False),
+            ("resident weights + side-stream H2D copy loop", eng_r, copy_loop, False),
+            ("resident weights + one side-stream H2D copy per step, each step waiting for the "
+             "previous step's copy", eng_r, None, True),
+            ("streamed weights (bench default)", eng_s, None, False)):
+        mean, first, last = replays(eng, loop, tied)
+        side.synchronize()
+        recs.append({"probe": "contention", "case": label, "replay_ms_mean": mean,
+                     "replay_ms_first8": first, "replay_ms_last8": last, "steps": steps,
+                     "warmup": warmup,
+                     "copy_bytes": image_bytes if loop or tied or eng is eng_s else 0})
+    for r in recs:
+        _print_record(r)
+
+
 def gemm_probe(reps: int = 20) -> None:
     """Per-product GPU time of one config-5 layer at the bench batch's token count (the eight
     projections: F.linear / the input-gradient torch.mm on dequantised fp16 weights, i.e.
@@ -1123,13 +1207,14 @@ def main() -> int:
                          "rocprofv3 --kernel-trace CSV of a bench run, and exit")
     ap.add_argument("--probe", nargs="?", const="dequant",
                     choices=("dequant", "lmhead", "elementwise", "ceilings", "gemm",
-                             "gemm_parts", "step"),
+                             "gemm_parts", "step", "contention"),
                     help="only fixed launches for counter runs: copy + dequant (default), the "
                          "lm_head CE kernels at config 2, the elementwise kernels on cold "
                          "inputs, the split-K MLP input gradient (gemm_parts), or eager "
                          "training steps with every kernel in its in-step form (step); or printed "
                          "timings: streaming ceilings at the dequant's traffic (ceilings), "
-                         "per-product GEMM times (gemm)")
+                         "per-product GEMM times (gemm), a step's replay with and without a "
+                         "concurrent host-to-device copy (contention)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs and measures one GPU only (asked for --gpus "
@@ -1155,6 +1240,9 @@ def main() -> int:
         return 0
     if args.probe == "step":
         step_probe()
+        return 0
+    if args.probe == "contention":
+        contention_probe(args.steps, max(args.warmup, 8))
         return 0
     if args.counter_summary:
         counter_summary(args.counter_summary)
