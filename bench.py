@@ -898,7 +898,8 @@ def contention_probe(steps: int = 24, warmup: int = 8) -> None:
     (c) the resident graph with one such copy per step on the side stream and each step waiting
     (a stream wait) for the previous step's copy; (d) the bench's streamed engine (whose own
     per-step copy runs beside it and gates the next step). Shows which of a concurrent PCIe
-    copy and a step tied to the copies lengthens the replay. Prints JSON records."""
+    copy and a step tied to the copies lengthens the replay, and (copy events on the side or
+    copy stream) how long the copies take meanwhile. Prints JSON records."""
     import torch
 
     from rus_amd import model as M
@@ -911,14 +912,26 @@ def contention_probe(steps: int = 24, warmup: int = 8) -> None:
     model = M.build_random_qlora_qwen2(cfg, dev, seed=0)
     batches = make_batches(cfg, 8, 4, 512, 0, dev)
 
+    copy_marks = []
+
+    def timed_copy():  # on the side stream
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(side)
+        dst.copy_(host, non_blocking=True)
+        e1.record(side)
+        copy_marks.append((e0, e1))
+
     def replays(engine, side_copy=None, tied=False):
         g = GraphedTrainStep(engine, bucket=64)
         for b in batches:
             g.prepare(b[0], b[1], b[2])
         opt = flat_adamw(engine)[0]
+        copy_marks.clear()
         if side_copy is not None:
             side_copy()
         ws = engine.weight_stream
+        if ws.unit == "model":
+            ws.time_copies()
         begin = ws.begin_step
         if tied:  # each step copies once on the side stream and waits for the previous copy
             done = []
@@ -928,7 +941,7 @@ def contention_probe(steps: int = 24, warmup: int = 8) -> None:
                 if done:
                     torch.cuda.current_stream(dev).wait_event(done[-1])
                 with torch.cuda.stream(side):
-                    dst.copy_(host, non_blocking=True)
+                    timed_copy()
                     done.append(torch.cuda.Event())
                     done[-1].record(side)
                 return buf
@@ -942,7 +955,15 @@ def contention_probe(steps: int = 24, warmup: int = 8) -> None:
         ms = g.replay_ms()
         torch.cuda.synchronize()
         ws.begin_step = begin
-        return statistics.fmean(ms), [round(x, 3) for x in ms[:8]], [round(x, 3) for x in ms[-8:]]
+        if ws.unit == "model":
+            cms = ws.copy_ms()
+            ws.time_copies(False)
+        else:
+            cms = [a.elapsed_time(b) for a, b in copy_marks]
+        # the copies that ran beside timed replays: drop the warm-up's and the loop's tail
+        cms = cms[warmup:warmup + steps]
+        return (statistics.fmean(ms), [round(x, 3) for x in ms[:8]], [round(x, 3) for x in ms[-8:]],
+                statistics.fmean(cms) if cms else None)
 
     eng_s = Qwen2FusedEngine(model, dev, resident_weights=False, stream_unit="model",
                              recompute=False, dequant_once=True)
@@ -956,7 +977,7 @@ def contention_probe(steps: int = 24, warmup: int = 8) -> None:
     def copy_loop():  # enough copies to outlast the warm-up and timed replays
         with torch.cuda.stream(side):
             for _ in range(warmup + steps + 8):
-                dst.copy_(host, non_blocking=True)
+                timed_copy()
 
     recs = []
     for label, eng, loop, tied in (
@@ -965,12 +986,13 @@ def contention_probe(steps: int = 24, warmup: int = 8) -> None:
             ("resident weights + one side-stream H2D copy per step, each step waiting for the "
              "previous step's copy", eng_r, None, True),
             ("streamed weights (bench default)", eng_s, None, False)):
-        mean, first, last = replays(eng, loop, tied)
+        mean, first, last, copy_ms = replays(eng, loop, tied)
         side.synchronize()
         recs.append({"probe": "contention", "case": label, "replay_ms_mean": mean,
                      "replay_ms_first8": first, "replay_ms_last8": last, "steps": steps,
                      "warmup": warmup,
-                     "copy_bytes": image_bytes if loop or tied or eng is eng_s else 0})
+                     "copy_bytes": image_bytes if loop or tied or eng is eng_s else 0,
+                     "copy_ms_mean": copy_ms})
     for r in recs:
         _print_record(r)
 
