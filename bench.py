@@ -899,7 +899,8 @@ def contention_probe(steps: int = 24, warmup: int = 8) -> None:
     (a stream wait) for the previous step's copy; (d) the bench's streamed engine (whose own
     per-step copy runs beside it and gates the next step). Shows which of a concurrent PCIe
     copy and a step tied to the copies lengthens the replay, and (copy events on the side or
-    copy stream) how long the copies take meanwhile. Prints JSON records."""
+    copy stream) how long the copies take meanwhile and how much of the replays' time a copy ran
+    beside. Prints JSON records."""
     import torch
 
     from rus_amd import model as M
@@ -927,6 +928,9 @@ def contention_probe(steps: int = 24, warmup: int = 8) -> None:
             g.prepare(b[0], b[1], b[2])
         opt = flat_adamw(engine)[0]
         copy_marks.clear()
+        torch.cuda.synchronize()
+        ref = torch.cuda.Event(enable_timing=True)  # time origin of the copy / replay intervals
+        ref.record()
         if side_copy is not None:
             side_copy()
         ws = engine.weight_stream
@@ -952,18 +956,23 @@ def contention_probe(steps: int = 24, warmup: int = 8) -> None:
         g.time_replays()
         for i in range(steps):
             train_step(engine, opt, batches[(warmup + i) % len(batches)], g)
+        rmarks = list(g.replay_marks)
         ms = g.replay_ms()
         torch.cuda.synchronize()
         ws.begin_step = begin
+        cmarks = list(ws.copy_marks or []) if ws.unit == "model" else list(copy_marks)
         if ws.unit == "model":
-            cms = ws.copy_ms()
             ws.time_copies(False)
-        else:
-            cms = [a.elapsed_time(b) for a, b in copy_marks]
+        # how much of the timed replays' device time a copy ran beside (0 when the copies and the
+        # replays were serialised, e.g. by sharing a hardware queue)
+        civ = [(ref.elapsed_time(a), ref.elapsed_time(b)) for a, b in cmarks]
+        riv = [(ref.elapsed_time(a), ref.elapsed_time(b)) for a, b in rmarks]
+        ov = sum(max(0.0, min(r1, c1) - max(r0, c0)) for r0, r1 in riv for c0, c1 in civ)
+        overlap = ov / sum(r1 - r0 for r0, r1 in riv) if civ else None
         # the copies that ran beside timed replays: drop the warm-up's and the loop's tail
-        cms = cms[warmup:warmup + steps]
+        cms = [c1 - c0 for c0, c1 in civ][warmup:warmup + steps]
         return (statistics.fmean(ms), [round(x, 3) for x in ms[:8]], [round(x, 3) for x in ms[-8:]],
-                statistics.fmean(cms) if cms else None)
+                statistics.fmean(cms) if cms else None, overlap)
 
     eng_s = Qwen2FusedEngine(model, dev, resident_weights=False, stream_unit="model",
                              recompute=False, dequant_once=True)
@@ -986,13 +995,13 @@ def contention_probe(steps: int = 24, warmup: int = 8) -> None:
             ("resident weights + one side-stream H2D copy per step, each step waiting for the "
              "previous step's copy", eng_r, None, True),
             ("streamed weights (bench default)", eng_s, None, False)):
-        mean, first, last, copy_ms = replays(eng, loop, tied)
+        mean, first, last, copy_ms, overlap = replays(eng, loop, tied)
         side.synchronize()
         recs.append({"probe": "contention", "case": label, "replay_ms_mean": mean,
                      "replay_ms_first8": first, "replay_ms_last8": last, "steps": steps,
                      "warmup": warmup,
                      "copy_bytes": image_bytes if loop or tied or eng is eng_s else 0,
-                     "copy_ms_mean": copy_ms})
+                     "copy_ms_mean": copy_ms, "copy_overlap_of_replay_time": overlap})
     for r in recs:
         _print_record(r)
 
