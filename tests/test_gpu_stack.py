@@ -295,3 +295,23 @@ def test_patched_qwen2_forward_returns_loss_and_logits_proxy():
     assert torch.allclose(ce.cpu(), out.loss.detach().float().cpu(), rtol=1e-5, atol=1e-6)
     out.loss.backward()
     assert all(p.grad is not None for p in engine.lora_params)
+    # the patched forward against the CPU oracle (fp32, pinned to transformers' Qwen2) on the same
+    # batch: loss within 2e-3 relative, every real token's entropy within 1e-3 absolute, its nll
+    # within 1e-2, its argmax equal wherever the oracle's top two logits differ by more than 1e-2
+    # (measured: loss 2e-5 relative, entropy 3.5e-4, nll 3.3e-3, every argmax equal)
+    pb = ops.pack_varlen(ids.cpu(), mask.cpu(), labels.cpu())
+    with torch.no_grad():
+        loss_ref, final = ostack.step_loss(model, ostack.dequant_model(model),
+                                           ostack.lora_leaves(model), pb.input_ids, pb.pos_ids,
+                                           pb.shift_labels, pb.row_lengths)
+        logits = final @ model.embed.cpu().float().t()
+        logp = torch.log_softmax(logits, -1)
+        ent_ref = -(logp.exp() * logp).sum(-1)
+        nll_ref = F.cross_entropy(logits, pb.shift_labels, ignore_index=-100, reduction="none")
+        top2 = logits.topk(2, -1).values
+    assert abs(float(out.loss.detach()) - float(loss_ref)) <= 2e-3 * abs(float(loss_ref))
+    real = mask.bool().cpu()  # row-major real positions: the packed token order
+    assert float((proxy.per_token_entropy.cpu()[real].float() - ent_ref).abs().max()) <= 1e-3
+    assert float((proxy.per_token_nll.cpu()[real].float() - nll_ref).abs().max()) <= 1e-2
+    clear = (top2[:, 0] - top2[:, 1]) > 1e-2
+    assert torch.equal(proxy.argmax(-1).cpu()[real][clear], logits.argmax(-1)[clear])
