@@ -20,15 +20,16 @@
 //     P = e^{z - M} (M the running maximum) and the same split-K GEMM adds P . W_chunk into fp32
 //     partials rescaled when M grows; lmhead_dh_finish_kernel divides by s and subtracts the
 //     label rows.
-// The GEMMs run the mainloop of mfma_gemm.h: 256 x 256 block tiles on v_mfma_f32_32x32x16_f16,
-// K staged 32 at a time through four 32 KiB LDS stages (five for an N-contiguous B) filled by
-// direct global -> LDS copies, one barrier per stage; eight waves of 128 x 64 (two per SIMD) for
-// the logits and hidden-gradient kernels, four waves of 128 x 128 for the statistics kernel, whose
-// epilogue needs each lane to hold 64 vocabulary entries of one token (W is its M operand). Blocks
-// are numbered XCD-aware (block b on XCD b % 8, each XCD a contiguous range of tiles), so blocks
-// that share a W tile share an L2. LDS rows are XOR-swizzled per 16-byte chunk, so the copies and
-// the MFMA fragment reads are bank-conflict free. The hidden gradient accumulates in fp32
-// partials (the reference accumulates in fp16, solution/ops.py:320).
+// The GEMMs run the mainloops of mfma_gemm.h: 256 x 256 block tiles on v_mfma_f32_32x32x16_f16
+// filled by direct global -> LDS copies. The logits, statistics and hidden-gradient kernels run
+// eight waves of 128 x 64 (two per SIMD) with K staged 64 deep through two 64 KiB buffers; the
+// logit-gradient kernel (the recomputing backward) runs four waves of 128 x 128 with K staged 32
+// deep through four 32 KiB buffers. In the statistics epilogue each lane holds 64 vocabulary
+// entries of one token (W is the M operand) and the two 128-row halves of a tile meet in the LDS.
+// Blocks are numbered XCD-aware (block b on XCD b % 8, each XCD a contiguous range of tiles), so
+// blocks that share a W tile share an L2. LDS rows are XOR-swizzled per 16-byte chunk, so the
+// copies and the MFMA fragment reads are bank-conflict free. The hidden gradient accumulates in
+// fp32 partials (the reference accumulates in fp16, solution/ops.py:320).
 #include <math.h>
 
 #include "common.h"
@@ -113,36 +114,36 @@ struct StatsParams {
   int kpad;
 };
 
-template <bool KEEP>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))) void
-lmhead_stats_kernel(GemmArgs g, StatsParams p) {
-  __shared__ __attribute__((aligned(16))) char smem[kSmemBytes];
-  Tile tl;
-  if (!tile_of(g, tl)) return;
-  f32x16 acc[kMT][kNT];
-  mainloop(g, tl, smem, acc);
-
+// The statistics epilogue of a block's 256 (vocab) x 256 (token) tile of logits, on NW waves in
+// the mainloop's layout (4: 128 x 128 each, 8: 128 x 64): per token, the maximum, the sums of e^{z-m}
+// and e^{z-m} z, the first argmax and the target logit over the tile's vocab rows (the two 128-row
+// halves merged through the LDS); with KEEP the fp16 logits are stored first.
+template <int NW, bool KEEP>
+__device__ __forceinline__ void stats_epilogue(char* smem, const GemmArgs& g, const Tile& tl,
+                                               const StatsParams& p,
+                                               f32x16 (&acc)[kMT][16 / NW]) {
+  constexpr int NT = 16 / NW, RW = kBN / (NW / 2);  // token columns per wave: 128 or 64
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int wm = wave >> 1, wn = wave & 1, h = lane >> 5;
+  const int wm = wave / (NW / 2), wn = wave % (NW / 2), h = lane >> 5;
   const int vrow0 = tl.m0 + wm * kWM;  // local vocab row of this wave's first accumulator row
   const bool full = tl.m0 + kBM <= g.M;
-  float rm[kNT], rs[kNT], rw[kNT];
-  int ri[kNT];
+  float rm[NT], rs[NT], rw[NT];
+  int ri[NT];
   // Logits as the reference's fp16 GEMM output: rounded once, in place.
 #pragma unroll
   for (int mt = 0; mt < kMT; ++mt)
 #pragma unroll
-    for (int nt = 0; nt < kNT; ++nt)
+    for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[mt][nt][r] = round16(acc[mt][nt][r]);
   if constexpr (KEEP)
-    store_tile_tv(smem, g, tl, p.z, p.ld_z, p.kpad,
-                  [&](int mt, int nt, int r, int) { return acc[mt][nt][r]; });
+    store_tile_tv<NW>(smem, g, tl, p.z, p.ld_z, p.kpad,
+                      [&](int mt, int nt, int r, int) { return acc[mt][nt][r]; });
   // Accumulator row of (mt, r) for this lane: mt*32 + 8*(r/4) + 4*h + r%4 (local to vrow0).
   const int rows_left = g.M - vrow0;  // rows at or past this are padding (edge tile only)
 #pragma unroll
-  for (int nt = 0; nt < kNT; ++nt) {
-    const int tok = tl.n0 + wn * kWN + nt * 32 + (lane & 31);
+  for (int nt = 0; nt < NT; ++nt) {
+    const int tok = tl.n0 + wn * RW + nt * 32 + (lane & 31);
     int lab_adj = -1000;  // label row local to vrow0, minus 4h (compared with the r/mt part)
     if (tok < g.N) {
       const int64_t l = p.labels[tok] - p.vocab_start - vrow0;
@@ -223,26 +224,26 @@ lmhead_stats_kernel(GemmArgs g, StatsParams p) {
 
   // Merge the two vocab halves (wm = 0, 1) of the block through LDS; wm = 0 writes the partial.
   if constexpr (KEEP) __syncthreads();  // the logits' staging reads of the LDS are done
-  float* xm = reinterpret_cast<float*>(smem);  // [wn][nt*32 + lane] x (m, s, w, idx)
+  float* xm = reinterpret_cast<float*>(smem);  // [token column of the tile] x (m, s, w, idx)
   if (wm == 1 && h == 0) {
 #pragma unroll
-    for (int nt = 0; nt < kNT; ++nt) {
-      const int o = wn * kWN + nt * 32 + lane;
+    for (int nt = 0; nt < NT; ++nt) {
+      const int o = wn * RW + nt * 32 + lane;
       xm[o] = rm[nt];
-      xm[2 * kWN + o] = rs[nt];
-      xm[4 * kWN + o] = rw[nt];
-      reinterpret_cast<int*>(xm)[6 * kWN + o] = ri[nt];
+      xm[kBN + o] = rs[nt];
+      xm[2 * kBN + o] = rw[nt];
+      reinterpret_cast<int*>(xm)[3 * kBN + o] = ri[nt];
     }
   }
   __syncthreads();
   if (wm == 0 && h == 0) {
     const int part = p.part_base + tl.m0 / kBM;
 #pragma unroll
-    for (int nt = 0; nt < kNT; ++nt) {
-      const int tok = tl.n0 + wn * kWN + nt * 32 + lane;
-      const int o = wn * kWN + nt * 32 + lane;
-      const float mB = xm[o], sB = xm[2 * kWN + o], wB = xm[4 * kWN + o];
-      const int iB = reinterpret_cast<int*>(xm)[6 * kWN + o];
+    for (int nt = 0; nt < NT; ++nt) {
+      const int tok = tl.n0 + wn * RW + nt * 32 + lane;
+      const int o = wn * RW + nt * 32 + lane;
+      const float mB = xm[o], sB = xm[kBN + o], wB = xm[2 * kBN + o];
+      const int iB = reinterpret_cast<int*>(xm)[3 * kBN + o];
       float m = rm[nt], s = rs[nt], w = rw[nt];
       int idx = ri[nt];
       const float M = fmaxf(m, mB);
@@ -262,6 +263,17 @@ lmhead_stats_kernel(GemmArgs g, StatsParams p) {
       }
     }
   }
+}
+
+template <bool KEEP>
+__global__ __launch_bounds__(kThreads8) __attribute__((amdgpu_waves_per_eu(2, 2))) void
+lmhead_stats_kernel(GemmArgs g, StatsParams p) {
+  __shared__ __attribute__((aligned(16))) char smem[kSmemBytes];
+  Tile tl;
+  if (!tile_of(g, tl)) return;
+  f32x16 acc[kMT][2];
+  mainloop(g, tl, smem, acc);
+  stats_epilogue<8, KEEP>(smem, g, tl, p, acc);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -829,10 +841,10 @@ static int lmhead_fwd(const char* fn, const void* hidden, const void* weight,
                 static_cast<int>(vocab_start), static_cast<f16*>(logits), ld_z,
                 static_cast<int>((n_vocab + kBK - 1) / kBK * kBK)};
   if (logits)
-    hipLaunchKernelGGL(lmhead_stats_kernel<true>, dim3(launch_grid(g)), dim3(kThreads), 0,
+    hipLaunchKernelGGL(lmhead_stats_kernel<true>, dim3(launch_grid(g)), dim3(kThreads8), 0,
                        static_cast<hipStream_t>(stream), g, p);
   else
-    hipLaunchKernelGGL(lmhead_stats_kernel<false>, dim3(launch_grid(g)), dim3(kThreads), 0,
+    hipLaunchKernelGGL(lmhead_stats_kernel<false>, dim3(launch_grid(g)), dim3(kThreads8), 0,
                        static_cast<hipStream_t>(stream), g, p);
   return check_launch(fn);
 }

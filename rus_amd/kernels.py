@@ -1893,7 +1893,13 @@ class LMHeadPass:
                                  dtype=torch.float16, device=device)
             self.m_run = torch.empty(n_tok, dtype=torch.float32, device=device)
             self.alpha = torch.empty(n_tok, dtype=torch.float32, device=device)
-            self.n_split = lm_head_split_count(n_tok, d, min(self.chunk, n_vocab), cu_count(device))
+            # every chunk's GEMM reads and rewrites all the fp32 partials (the rescaled
+            # accumulation), so splits beyond one round of CUs cost a partial pass per chunk for
+            # a few percent of mainloop: at most one round
+            n_cu = cu_count(device)
+            tiles = -(-n_tok // 256) * -(-d // 256)
+            self.n_split = lm_head_split_count(n_tok, d, min(self.chunk, n_vocab), n_cu,
+                                               max_split=max(1, n_cu // tiles))
             self.dparts = torch.empty((self.n_split, n_tok, d), dtype=torch.float32, device=device)
 
     def add_chunk(self, hidden: torch.Tensor, w_rows: torch.Tensor, w_t: torch.Tensor | None,
