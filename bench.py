@@ -1223,11 +1223,11 @@ def main() -> int:
     ap.add_argument("--lm-block", type=int, default=0,
                     help="most tokens per block of the token-blocked lm_head (whole 256-token "
                          "tiles; 0: the tiles whose fp16 logits fit 256 MiB, 768 at V=151936)")
-    ap.add_argument("--lm-chunk", type=int, default=0,
-                    help="vocabulary rows per chunk of the single-pass lm_head in the timed "
-                         "step (a multiple of 256; W read once, an [N, chunk] logit buffer); "
-                         "-1: chosen per token count (64 MiB of logits); 0: the token-blocked "
-                         "head")
+    ap.add_argument("--lm-chunk", type=int, default=-1,
+                    help="lm_head layout: vocabulary rows per chunk of the single pass over "
+                         "the vocabulary (a multiple of 256; W read once, an [N, chunk] logit "
+                         "buffer); -1 (default): chunk chosen per token count (128 MiB of "
+                         "logits at most); 0: the token-blocked head ([block, V] logits)")
     ap.add_argument("--no-ablation", action="store_true",
                     help="skip the timing of the other --recompute, --dequant-once and "
                          "--stream-unit settings")
@@ -1308,7 +1308,7 @@ def main() -> int:
                               recompute=recompute, overlap=overlap, gemm=args.gemm,
                               dequant_once=once)
     engine.lm_block_tokens = args.lm_block or None
-    engine.lm_v_chunk = args.lm_chunk or None
+    engine.lm_v_chunk = args.lm_chunk
     lm_block = args.lm_block or K.lm_head_block_tokens(engine.host_head.gpu_weight.shape[0])
     # Calibration pass (eager): every kernel timed, to name the dominant one.
     _, _, _, calib = timed_run(engine, opt, batches, 2, args.warmup, kernel_filter=None)
@@ -1413,7 +1413,8 @@ def main() -> int:
                    "dequant_once": "on" if once else "off", "graph_bucket": args.bucket,
                    "lm_head": (f"vocabulary chunks of {args.lm_chunk} rows, [N, chunk] logits"
                                if args.lm_chunk > 0 else
-                               "vocabulary chunks chosen per token count (64 MiB of logits)"
+                               "one pass over vocabulary chunks chosen per token count (at most "
+                               "128 MiB of logits, never [N, V]; online max / sum-exp)"
                                if args.lm_chunk < 0 else
                                f"token blocks of whole 256-token tiles, <= {lm_block} tokens and "
                                "at least two per batch: a [block, V] logits buffer, never "
@@ -1463,13 +1464,13 @@ def main() -> int:
                 eng_d, None, batches, min(args.steps, 16), 1, args.bucket)
             del eng_d, g_d
             torch.cuda.empty_cache()
-        # The other lm_head: the single pass over vocabulary chunks (the reference's layout, W
-        # read once, an [N, chunk] buffer of at most 64 MiB) against the token-blocked head.
+        # The other lm_head layout: the token-blocked head ([block, V] logit buffers) against
+        # the single pass over vocabulary chunks (W read once, an [N, chunk] buffer).
         eng_c = Qwen2FusedEngine(model, dev, resident_weights=False, stream_unit=args.stream_unit,
                                  recompute=recompute, overlap=overlap, gemm=args.gemm,
                                  dequant_once=once)
         eng_c.lm_block_tokens = engine.lm_block_tokens
-        eng_c.lm_v_chunk = None if args.lm_chunk else -1
+        eng_c.lm_v_chunk = 0 if args.lm_chunk else -1
         out[f"lm_head_{'token_blocked' if args.lm_chunk else 'vocab_chunked'}_tokens_per_s"], \
             g_c = _graph_run(eng_c, None, batches, min(args.steps, 16), 1, args.bucket)
         del eng_c, g_c

@@ -27,8 +27,8 @@ from __future__ import annotations
 import torch
 
 from . import kernels as K
-from .ops import (PRESCALE_GRAD, Qwen2FusedEngine, VarlenMeta, pack_varlen, stack_backward,
-                  stack_forward)
+from .ops import (PRESCALE_GRAD, Qwen2FusedEngine, VarlenMeta, lm_head_layout, pack_varlen,
+                  stack_backward, stack_forward)
 
 
 GRAPH_NODE_TYPES = ("kernel", "memcpy", "memset", "host", "graph", "empty", "wait_event",
@@ -167,9 +167,9 @@ class GraphedTrainStep:
         final, st = stack_forward(eng, h, img.pos, None, self.training, lora16, seed, vm=img.vm,
                                   save=not eng.recompute)
         head = eng.host_head
-        v_chunk = eng.lm_v_chunk
-        if v_chunk is not None and v_chunk < 0:  # chunk chosen for the bucket's token count
-            v_chunk = K.lm_head_chunk_cols(final.shape[0], head.gpu_weight.shape[0])
+        # the engine's head layout; the single pass's chunk chosen for the bucket's token count
+        v_chunk = lm_head_layout(eng.lm_v_chunk, final.shape[0], head.gpu_weight.shape[0],
+                                 final.device)
         nll, _lse, ent, amax, _denom, d_final, loss = K.lm_head_ce(
             final, head.gpu_weight, img.labels, num_items_in_batch=self.num_items,
             need_grad=True, weight_t=head.gpu_weight_t, dh_scale=1.0 / PRESCALE_GRAD,

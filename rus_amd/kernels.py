@@ -1406,7 +1406,7 @@ def lm_head_split_count(n_tok: int, d: int, n_vocab: int, n_cu: int = 256,
     return best
 
 
-LM_CHUNK_BUDGET = 64 << 20  # bytes of fp16 logits one chunk of the single-pass head may hold
+LM_CHUNK_BUDGET = 128 << 20  # bytes of fp16 logits one chunk of the single-pass head may hold
 
 
 def lm_head_chunk_cols(n_tok: int, n_vocab: int, n_cu: int = 256,
@@ -2076,7 +2076,8 @@ def lm_head_ce(hidden: torch.Tensor, weight: torch.Tensor, labels: torch.Tensor,
     logit is recomputed (the reference holds [N, 8192] chunks and
     recomputes every logit, solution/ops.py:209-322). ``v_chunk`` (a multiple of 256) selects
     the single pass over vocabulary chunks instead (``LMHeadPass``: W read once in total, an
-    [N, v_chunk] buffer), the layout of a head streamed from the host. ``weight_t`` is W^T
+    [N, v_chunk] buffer), the engine's default layout (``ops.lm_head_layout``) and that of a
+    head streamed from the host. ``weight_t`` is W^T
     [d, >= round_up(V, 64)] (built and cached on the weight when not given).
     """
     fn = "lm_head_ce"

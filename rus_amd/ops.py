@@ -163,6 +163,7 @@ class FusedChunkedLMHeadFn(torch.autograd.Function):
                 w, wt = weight_or_host_head.gpu_weight, weight_or_host_head.gpu_weight_t
             else:
                 w, wt = weight_or_host_head.detach(), None
+            v_chunk = lm_head_layout(v_chunk, h_2d.shape[0], w.shape[0], h_2d.device)
             nll, lse, ent, amax, denom, dh_pre, loss = K.lm_head_ce(
                 h_2d, w, labels, num_items_in_batch=num_items_in_batch, v_chunk=v_chunk,
                 need_grad=need_grad, weight_t=wt)
@@ -184,11 +185,24 @@ class FusedChunkedLMHeadFn(torch.autograd.Function):
         return d_h.view(ctx.orig_shape), None, None, None, None
 
 
+def lm_head_layout(v_chunk, n_tok: int, n_vocab: int, device):
+    """``v_chunk`` argument of K.lm_head_ce for a head layout choice: None or negative -> the
+    single pass with the chunk chosen for ``n_tok`` tokens (K.lm_head_chunk_cols), and at least
+    two chunks, so that no buffer holds a logit row of the whole vocabulary; a positive multiple
+    of 256 -> that chunk; 0 -> None (the token-blocked head)."""
+    if v_chunk is None or v_chunk < 0:
+        c = K.lm_head_chunk_cols(n_tok, n_vocab, K.cu_count(device))
+        half = -(-(-(-n_vocab // 2)) // K.LM_TILE) * K.LM_TILE
+        return half if c >= n_vocab and n_vocab > K.LM_TILE else c
+    return int(v_chunk) if v_chunk > 0 else None
+
+
 def chunked_lm_head(hidden_states, shift_labels, weight_or_host_head, num_items_in_batch=None,
                     v_chunk=None):
     """(loss, nll, entropy, argmax) of the lm_head cross-entropy (solution/ops.py:342-349).
     ``v_chunk`` sets the vocabulary rows per chunk, i.e. the [N, v_chunk] fp16 logit buffer
-    (default: chosen within 64 MiB; a streamed HostHead uses its own chunk)."""
+    (default: chosen for the token count within K.LM_CHUNK_BUDGET; 0: the token-blocked head; a
+    streamed HostHead uses its own chunk)."""
     return FusedChunkedLMHeadFn.apply(hidden_states, shift_labels, weight_or_host_head,
                                       num_items_in_batch, v_chunk)
 
@@ -305,8 +319,10 @@ class Qwen2FusedEngine:
         # lm_block_tokens: most tokens per block of the token-blocked lm_head (whole 256-token
         # tiles; None: the tiles whose fp16 logits fit K.LM_BLOCK_BUDGET).
         self.lm_block_tokens = None
-        # lm_v_chunk: vocabulary rows per chunk of the single-pass head in the captured step
-        # (K.LMHeadPass: W read once, an [N, chunk] logit buffer); None: the token-blocked head.
+        # lm_v_chunk: the lm_head layout, eager and captured. None (or negative): one pass over
+        # vocabulary chunks (K.LMHeadPass: W read once, an [N, chunk] logit buffer) with the
+        # chunk chosen for the token count within K.LM_CHUNK_BUDGET; a positive multiple of 256:
+        # that chunk; 0: the token-blocked head ([block, V] logit buffers).
         self.lm_v_chunk = None
         # LoRA dropout: the counter-based masks of step k use seed (base + k), held on the device
         # so that a captured graph advances it by itself. The base comes from torch's CPU
@@ -1034,7 +1050,8 @@ def fused_causal_lm_forward(engine: Qwen2FusedEngine, input_ids, attention_mask=
     h = engine.host_head.embed(pb.input_ids)
     final = FusedQwen2StackFn.apply(h, pb.pos_ids, pb.row_lengths, engine, training, *engine.lora_params)
     loss, nll, ent, amax = chunked_lm_head(final, pb.shift_labels, engine.host_head,
-                                           num_items_in_batch=num_items_in_batch)
+                                           num_items_in_batch=num_items_in_batch,
+                                           v_chunk=engine.lm_v_chunk)
     mean_ent = ent.mean() if ent.numel() else torch.zeros((), device=ent.device)
     full_ent = mean_ent.expand(pb.batch_shape[0] * pb.batch_shape[1]).clone()
     full_ent.index_copy_(0, pb.valid_idx, ent)

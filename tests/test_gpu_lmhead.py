@@ -259,12 +259,16 @@ def test_single_pass_head_chunking_and_streaming(n, d, v, chunk):
 
 
 def test_chunk_choice_bounds_the_logit_buffer():
-    # The default chunk keeps the per-chunk fp16 logits within the 64 MiB budget at any token
-    # count (the [N, V] logits are never held), and covers a small vocabulary in one chunk.
+    # The default chunk keeps the per-chunk fp16 logits within the 128 MiB budget at any token
+    # count and, from a few hundred tokens up, below the whole vocabulary (the [N, V] logits are
+    # never held); a small vocabulary fits one chunk.
+    assert K.LM_CHUNK_BUDGET == 128 << 20
     for n in (1, 707, 2048, 8192, 65536):
         c = K.lm_head_chunk_cols(n, 151936)
         assert c % 256 == 0 and c >= 256
         assert n * c * 2 <= max(K.LM_CHUNK_BUDGET, n * 256 * 2)
+        if n >= 512:
+            assert c < 151936
     assert K.lm_head_chunk_cols(64, 4099) >= 4099
 
 
