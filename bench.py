@@ -344,6 +344,23 @@ def config_records(seed: int = 0, reps: int = 40) -> dict:
         r = summ[k]
         us = r["ms"] * 1e3 / r["launches"]
         c2.append(_hbm(k, [r["launches"] // 3, "launches per head"], us, r["bytes"] / r["launches"]))
+    # the engine's default layout: one pass over vocabulary chunks (the chunk chosen for the
+    # token count), and the config's own V_CHUNK of 8192 rows
+    for chunk, what in ((K.lm_head_chunk_cols(n2, V, K.cu_count(dev)), "chosen for N"),
+                        (8192, "the config's V_CHUNK")):
+        for _ in range(2):
+            K.lm_head_ce(h, W, lab, weight_t=wt, v_chunk=chunk)
+        e0.record()
+        for _ in range(3):
+            K.lm_head_ce(h, W, lab, weight_t=wt, v_chunk=chunk)
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / 3
+        c2.append(_mfma(f"lm_head_ce fwd+bwd (single pass, chunks of {chunk} rows: {what})",
+                        [n2, D, V], us, 2 * flops,
+                        note="4*N*D*V over the whole pass (per chunk: statistics GEMM keeping "
+                             "the logits, P = e^{z-M}, hidden-gradient GEMM into rescaled "
+                             "partials; then combine and finish)"))
     out["2"] = c2
     del h, W, wt, lab
 
