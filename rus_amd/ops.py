@@ -192,8 +192,9 @@ def lm_head_layout(v_chunk, n_tok: int, n_vocab: int, device):
     of 256 -> that chunk; 0 -> None (the token-blocked head)."""
     if v_chunk is None or v_chunk < 0:
         c = K.lm_head_chunk_cols(n_tok, n_vocab, K.cu_count(device))
-        half = -(-(-(-n_vocab // 2)) // K.LM_TILE) * K.LM_TILE
-        return half if c >= n_vocab and n_vocab > K.LM_TILE else c
+        if c >= n_vocab and n_vocab > K.LM_TILE:  # two chunks of whole 256-row tiles
+            return K._round_up(-(-n_vocab // 2), K.LM_TILE)
+        return c
     return int(v_chunk) if v_chunk > 0 else None
 
 
