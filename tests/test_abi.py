@@ -291,3 +291,20 @@ def test_lm_head_token_blocks_take_whole_tiles_within_the_logit_budget():
             assert all(0 < t1 - t0 <= max_tiles * 256 for t0, t1 in blocks)
             assert sum(-(-(t1 - t0) // 256) for t0, t1 in blocks) == tiles
             assert len(blocks) == -(-tiles // max_tiles)
+
+
+def test_lm_head_layout_never_holds_a_whole_vocabulary_row_by_default():
+    from rus_amd import kernels as K
+    from rus_amd import ops
+
+    V = 151936
+    for n in (1, 100, 256, 442, 707, 768, 876, 2048, 8192):
+        c = ops.lm_head_layout(None, n, V, "cpu")
+        assert c % K.LM_TILE == 0 and c < V, (n, c)
+        assert ops.lm_head_layout(-1, n, V, "cpu") == c
+        assert n * c * 2 <= max(K.LM_CHUNK_BUDGET, n * K.LM_TILE * 2)
+    # whole-vocabulary choices split into two chunks of whole tiles
+    assert ops.lm_head_layout(None, 64, 4099, "cpu") == 2304
+    assert ops.lm_head_layout(None, 64, 200, "cpu") == 256  # one tile: one chunk
+    assert ops.lm_head_layout(0, 707, V, "cpu") is None  # the token-blocked head
+    assert ops.lm_head_layout(8192, 707, V, "cpu") == 8192
