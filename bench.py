@@ -670,13 +670,17 @@ def elementwise_probe(reps: int = 5) -> None:
           f"swiglu fwd/bwd [{NS},{2 * I}]", flush=True)
 
 
-def lmhead_probe(reps: int = 5) -> None:
+def lmhead_probe(reps: int = 5, single_pass: bool = False) -> None:
     """Fixed launches for counter runs of the lm_head CE kernels at BASELINE config 2: hidden
     [2048, 1536] ~ N(0,1), W [151936, 1536] ~ N(0, 0.02), 10% labels -100, whole vocabulary per
-    pass (forward statistics, logit gradient, hidden gradient)."""
+    pass (forward statistics, logit gradient, hidden gradient): the token-blocked head, or with
+    ``single_pass`` the engine's default one pass over vocabulary chunks (the chunk chosen for
+    N), one pass first under the per-launch timer, which prints each launcher's algorithmic
+    bytes / FLOPs per launch."""
     import torch
 
     from rus_amd import kernels as K
+    from rus_amd.kernels import KernelTimer
 
     dev = torch.device("cuda:0")
     _calibration_copies(dev)
@@ -687,11 +691,22 @@ def lmhead_probe(reps: int = 5) -> None:
     lab = torch.randint(0, v, (n,), device=dev, generator=g)
     lab[torch.rand(n, device=dev, generator=g) < 0.1] = -100
     wt = K.lm_head_weight_t(w)
+    chunk = K.lm_head_chunk_cols(n, v, K.cu_count(dev)) if single_pass else None
     torch.cuda.synchronize()
+    if single_pass:
+        K.lm_head_ce(h, w, lab, weight_t=wt, v_chunk=chunk)
+        torch.cuda.synchronize()
+        with KernelTimer() as timer:
+            K.lm_head_ce(h, w, lab, weight_t=wt, v_chunk=chunk)
+        for name, r in sorted(timer.summary().items()):
+            print(json.dumps({"launcher": name, "launches_per_pass": r["launches"],
+                              "bytes_per_launch": r["bytes"] / r["launches"],
+                              "flops_per_launch": r["flops"] / r["launches"]}), flush=True)
     for _ in range(reps):
-        K.lm_head_ce(h, w, lab, weight_t=wt)
+        K.lm_head_ce(h, w, lab, weight_t=wt, v_chunk=chunk)
     torch.cuda.synchronize()
-    print(f"probe: {reps} lm_head CE forward+gradient passes at N={n}, V={v}, d={d}", flush=True)
+    what = f"single passes over {chunk}-row vocabulary chunks" if single_pass else "passes"
+    print(f"probe: {reps} lm_head CE forward+gradient {what} at N={n}, V={v}, d={d}", flush=True)
 
 
 def kernel_probe(reps: int = 5) -> None:
@@ -1254,10 +1269,11 @@ def main() -> int:
                     help="print the per-step kernel time of the last --steps replays in a "
                          "rocprofv3 --kernel-trace CSV of a bench run, and exit")
     ap.add_argument("--probe", nargs="?", const="dequant",
-                    choices=("dequant", "lmhead", "elementwise", "ceilings", "gemm",
-                             "gemm_parts", "step", "contention"),
+                    choices=("dequant", "lmhead", "lmhead_pass", "elementwise", "ceilings",
+                             "gemm", "gemm_parts", "step", "contention"),
                     help="only fixed launches for counter runs: copy + dequant (default), the "
-                         "lm_head CE kernels at config 2, the elementwise kernels on cold "
+                         "lm_head CE kernels at config 2 (token blocks; lmhead_pass: the single "
+                         "pass over vocabulary chunks), the elementwise kernels on cold "
                          "inputs, the split-K MLP input gradient (gemm_parts), or eager "
                          "training steps with every kernel in its in-step form (step); or printed "
                          "timings: streaming ceilings at the dequant's traffic (ceilings), "
@@ -1271,8 +1287,8 @@ def main() -> int:
     if args.trace_summary:
         trace_summary(args.trace_summary, args.steps)
         return 0
-    if args.probe == "lmhead":
-        lmhead_probe()
+    if args.probe in ("lmhead", "lmhead_pass"):
+        lmhead_probe(single_pass=args.probe == "lmhead_pass")
         return 0
     if args.probe == "elementwise":
         elementwise_probe()
