@@ -315,3 +315,33 @@ def test_patched_qwen2_forward_returns_loss_and_logits_proxy():
     assert float((proxy.per_token_nll.cpu()[real].float() - nll_ref).abs().max()) <= 1e-2
     clear = (top2[:, 0] - top2[:, 1]) > 1e-2
     assert torch.equal(proxy.argmax(-1).cpu()[real][clear], logits.argmax(-1)[clear])
+
+
+def test_lm_head_layouts_agree_through_the_engine():
+    # The engine's default head (one pass over vocabulary chunks) and the token-blocked head
+    # (lm_v_chunk = 0) on the same step: the same statistics up to fp32 summation order.
+    cfg = small_config()
+    model = M.build_random_qlora_qwen2(cfg, DEV, seed=3, std=0.05)
+    engine = ops.Qwen2FusedEngine(model, DEV, resident_weights=True)
+    ids, mask, labels = _batch(cfg, [37, 64, 21], seed=4)
+    ids, mask, labels = ids.to(DEV), mask.to(DEV), labels.to(DEV)
+    out = {}
+    for layout in (None, 0, 256):
+        engine.lm_v_chunk = layout
+        for p in engine.lora_params:
+            p.grad = None
+        loss, nll, ent, amax = ops.fused_causal_lm_forward(engine, ids, mask, labels,
+                                                           training=False)
+        loss.backward()
+        torch.cuda.synchronize()
+        out[layout] = (float(loss.detach()), nll.detach().cpu(), ent.detach().cpu(),
+                       amax.cpu(), [p.grad.detach().cpu().clone() for p in engine.lora_params])
+    base = out[None]
+    for layout in (0, 256):
+        loss, nll, ent, amax, grads = out[layout]
+        assert abs(loss - base[0]) <= 1e-5 * abs(base[0]), (layout, loss, base[0])
+        assert float((nll - base[1]).abs().max()) <= 1e-4
+        assert float((ent - base[2]).abs().max()) <= 1e-4
+        assert torch.equal(amax, base[3])
+        for gi, (a, b) in enumerate(zip(grads, base[4])):
+            assert _rel(a, b) <= 1e-3, (layout, gi, _rel(a, b))
