@@ -947,11 +947,13 @@ def contention_probe(steps: int = 24, warmup: int = 8) -> None:
 
     copy_marks = []
 
-    def timed_copy():  # on the side stream
+    def timed_copy(st=None):  # on a side stream (default: ``side``)
+        st = side if st is None else st
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(side)
-        dst.copy_(host, non_blocking=True)
-        e1.record(side)
+        e0.record(st)
+        with torch.cuda.stream(st):
+            dst.copy_(host, non_blocking=True)
+        e1.record(st)
         copy_marks.append((e0, e1))
 
     def replays(engine, side_copy=None, tied=False):
@@ -1015,20 +1017,25 @@ def contention_probe(steps: int = 24, warmup: int = 8) -> None:
     dst = torch.empty(image_bytes, dtype=torch.uint8, device=dev)
     side = torch.cuda.Stream(device=dev)  # default priority
 
-    def copy_loop():  # enough copies to outlast the warm-up and timed replays
-        with torch.cuda.stream(side):
-            for _ in range(warmup + steps + 8):
-                timed_copy()
+    def copy_loop(st=None):  # enough copies to outlast the warm-up and timed replays
+        for _ in range(warmup + steps + 8):
+            timed_copy(st)
 
+    # four more side streams created together: HIP maps a process's streams onto a few hardware
+    # queues, so one of them may share the replaying stream's queue (copies and replays then
+    # serialise: overlap 0)
+    fresh = [torch.cuda.Stream(device=dev) for _ in range(4)]
+    cases = [("resident weights", eng_r, None, False),
+             ("resident weights + side-stream H2D copy loop", eng_r, copy_loop, False),
+             ("resident weights + one side-stream H2D copy per step, each step waiting for the "
+              "previous step's copy", eng_r, None, True),
+             ("streamed weights (bench default)", eng_s, None, False)]
+    cases += [(f"resident weights + the H2D copy loop on fresh side stream {k} of 4", eng_r,
+               (lambda st=st: copy_loop(st)), False) for k, st in enumerate(fresh)]
     recs = []
-    for label, eng, loop, tied in (
-            ("resident weights", eng_r, None, False),
-            ("resident weights + side-stream H2D copy loop", eng_r, copy_loop, False),
-            ("resident weights + one side-stream H2D copy per step, each step waiting for the "
-             "previous step's copy", eng_r, None, True),
-            ("streamed weights (bench default)", eng_s, None, False)):
+    for label, eng, loop, tied in cases:
         mean, first, last, copy_ms, overlap = replays(eng, loop, tied)
-        side.synchronize()
+        torch.cuda.synchronize()
         recs.append({"probe": "contention", "case": label, "replay_ms_mean": mean,
                      "replay_ms_first8": first, "replay_ms_last8": last, "steps": steps,
                      "warmup": warmup,
